@@ -1,0 +1,74 @@
+// ref_shim.cpp -- TEST INFRASTRUCTURE ONLY.
+//
+// extern "C" entry points over the reference's own CPU kernels, so that tests can
+// check the oracle restatement (oracle.cpp) against the real thing.  Compiled by
+// oracle/Makefile together with the reference sources where they lie under
+// /root/reference/src; the result goes to oracle/_ref/libref.so (never committed).
+#include "rapidllm/kernels/ops.h"
+#include "rapidllm/runtime/thread_pool.h"
+
+#include <cstdint>
+
+namespace rapidllm {
+int32_t greedy_sample(const float* logits, int vocab);  // src/runtime/sampler.cpp:8
+}
+
+using namespace rapidllm;
+
+extern "C" {
+float ref_e4m3_to_f32(uint8_t b) { return ops::e4m3_to_f32(b); }
+float ref_fp16_to_f32(uint16_t h) { return ops::fp16_to_f32(h); }
+void ref_gemv_fp8(const uint8_t* W, const float* s, const float* x, float* y, int m, int n) {
+    ops::gemv_fp8(W, s, x, y, m, n, 128);
+}
+void ref_dequant_q4_k(const uint8_t* p, float* out, int n) { ops::dequant_q4_k(p, out, n); }
+void ref_dequant_q6_k(const uint8_t* p, float* out, int n) { ops::dequant_q6_k(p, out, n); }
+void ref_gemv_q4_k(const uint8_t* p, const float* x, float* y, int m, int n) { ops::gemv_q4_k(p, x, y, m, n); }
+void ref_gemv_q6_k(const uint8_t* p, const float* x, float* y, int m, int n) { ops::gemv_q6_k(p, x, y, m, n); }
+void ref_gemv_bf16(const uint16_t* W, const float* x, float* y, int m, int n) { ops::gemv_bf16(W, x, y, m, n); }
+void ref_qwen3_rmsnorm(const float* x, const float* g, float* y, int n, float eps) {
+    ops::qwen3_rmsnorm(x, g, y, n, eps);
+}
+void ref_gated_rmsnorm(const float* x, const float* z, const float* g, float* y, int n, float eps, int gn) {
+    ops::gated_rmsnorm(x, z, g, y, n, eps, gn);
+}
+void ref_l2norm(const float* x, float* y, int n, float eps) { ops::l2norm(x, y, n, eps); }
+void ref_conv1d_update(const float* x, const float* w, float* st, float* y, int dim, int k) {
+    ops::conv1d_update(x, w, st, y, dim, k);
+}
+void ref_delta_step_scalar(float* S, const float* q, const float* k, const float* v, const float* beta,
+                           const float* gl, float* o, int nv, int dk, int dv, float eps) {
+    ops::delta_recurrent_step_scalar(S, q, k, v, beta, gl, o, nv, dk, dv, eps);
+}
+void ref_delta_step_simd(float* S, const float* q, const float* k, const float* v, const float* beta,
+                         const float* gl, float* o, int nv, int dk, int dv, float eps) {
+    ops::delta_recurrent_step_simd(S, q, k, v, beta, gl, o, nv, dk, dv, eps);
+}
+void ref_rope_partial(float* q, float* k, int nq, int nkv, int hd, int rot, int pos, float theta) {
+    ops::rope_partial(q, k, nq, nkv, hd, rot, pos, theta);
+}
+void ref_attn_decode(const float* q, const float* kc, const float* vc, float* o, int pos, int nq, int nkv, int hd) {
+    ops::attn_decode(q, kc, vc, o, pos, nq, nkv, hd);
+}
+void ref_swiglu(const float* g, const float* u, float* y, int n) { ops::swiglu(g, u, y, n); }
+int ref_greedy(const float* l, int v) { return greedy_sample(l, v); }
+int ref_num_threads() { return num_threads(); }
+const char* ref_simd_name() { return ops::simd_isa_name(); }
+
+// One-token fused layers at full shape (ops_fused.cpp), for the CPU baseline timing.
+void ref_fused_mlp(const float* rms_w, const uint8_t* wg, const float* sg, const uint8_t* wu, const float* su,
+                   const uint8_t* wd, const float* sd, float* x, int hidden, int inter, float eps) {
+    ops::FusedMlpArgs a{};
+    a.x = x;
+    a.x_inout = x;
+    a.rms_w = rms_w;
+    a.Wg = {wg, sg, QuantKind::FP8_E4M3_B128};
+    a.Wu = {wu, su, QuantKind::FP8_E4M3_B128};
+    a.Wd = {wd, sd, QuantKind::FP8_E4M3_B128};
+    a.hidden = hidden;
+    a.intermediate = inter;
+    a.eps = eps;
+    a.use_simd = true;
+    ops::fused_mlp_decode(a);
+}
+}

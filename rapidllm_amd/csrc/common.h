@@ -1,0 +1,102 @@
+// common.h -- shared device/host helpers for the gfx950 decode backend.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+#include <cstdint>
+#include <cstdio>
+#include <stdexcept>
+#include <string>
+
+#include "../../include/rapidllm_hip.h"
+
+namespace rl {
+
+// Status codes: identical values to RapidStatus (include/rapidllm/api.h:11-25 of the
+// reference), so the C API layer can pass them through unchanged.
+struct Error : std::runtime_error {
+    int code;
+    Error(int c, const std::string& m) : std::runtime_error(m), code(c) {}
+};
+
+void set_last_error(const char* msg);
+
+#define RL_HIP(expr)                                                                                 \
+    do {                                                                                             \
+        hipError_t e_ = (expr);                                                                      \
+        if (e_ != hipSuccess)                                                                        \
+            throw ::rl::Error(RL_ERR_DEVICE, std::string(#expr) + ": " + hipGetErrorString(e_));     \
+    } while (0)
+
+#define RL_REQUIRE(cond, code, msg)                                   \
+    do {                                                              \
+        if (!(cond)) throw ::rl::Error((code), std::string(msg));     \
+    } while (0)
+
+// Run `body` and translate exceptions into a status code + thread-local message.
+// No exception ever crosses the C ABI (mirrors rapidllm_c.cpp:46-50, 246-251).
+template <class F>
+int guard(F&& body) {
+    try {
+        body();
+        return RL_OK;
+    } catch (const Error& e) {
+        set_last_error(e.what());
+        return e.code;
+    } catch (const std::bad_alloc&) {
+        set_last_error("out of memory");
+        return RL_ERR_NOMEM;
+    } catch (const std::exception& e) {
+        set_last_error(e.what());
+        return RL_ERR_INTERNAL;
+    }
+}
+
+inline hipStream_t S(void* s) { return static_cast<hipStream_t>(s); }
+
+// After an async launch: surface launch-configuration errors immediately.
+inline void check_launch(const char* what) {
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) throw Error(RL_ERR_DEVICE, std::string(what) + ": " + hipGetErrorString(e));
+}
+
+constexpr int kWave = 64;
+
+}  // namespace rl
+
+// ------------------------------------------------------------------ device side
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+typedef int i32x4 __attribute__((ext_vector_type(4)));
+typedef int i32x2 __attribute__((ext_vector_type(2)));
+
+// Wave-wide sum / max through cross-lane moves (DPP/permute lowered by the compiler).
+__device__ inline float wave_sum(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ inline double wave_sum_d(double v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
+    return v;
+}
+
+__device__ inline float wave_max(float v) {
+#pragma unroll
+    for (int o = 32; o > 0; o >>= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
+    return v;
+}
+
+// Split an fp32 value into two bf16 terms whose sum carries 16 significant bits:
+// hi = x truncated to bf16, mid = (x - hi) truncated to bf16.  x - hi is exact in
+// fp32; the remainder lost is < 2^-16 |x|.  bf16 keeps fp32's exponent range, so
+// no activation can overflow the split.
+__device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& mid) {
+    const uint32_t xb = __float_as_uint(x);
+    hi = static_cast<uint16_t>(xb >> 16);
+    const float r = x - __uint_as_float(xb & 0xffff0000u);
+    mid = static_cast<uint16_t>(__float_as_uint(r) >> 16);
+}

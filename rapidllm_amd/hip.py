@@ -1,0 +1,171 @@
+"""ctypes binding to the gfx950 C ABI (include/rapidllm_hip.h).
+
+The library is loaded from rapidllm_amd/_lib/librapidllm_hip.so, built in-tree by
+rapidllm_amd/build.py.  There is no fallback: if the library is missing or the
+device is not a gfx950, calls raise.
+"""
+from __future__ import annotations
+
+import ctypes as C
+import os
+
+import numpy as np
+
+HERE = os.path.dirname(os.path.abspath(__file__))
+LIB_PATH = os.path.join(HERE, "_lib", "librapidllm_hip.so")
+
+_vp = C.c_void_p
+_sz = C.c_size_t
+_i = C.c_int
+
+# name -> (restype, argtypes); every entry point returns an RlStatus unless noted.
+_SIGS = {
+    "rl_hip_abi_version": (_i, []),
+    "rl_hip_available": (_i, []),
+    "rl_hip_last_error": (C.c_char_p, []),
+    "rl_hip_device_info": (_i, [C.c_char_p, _i, C.POINTER(_i), C.POINTER(_sz)]),
+    "rl_hip_malloc": (_i, [C.POINTER(_vp), _sz]),
+    "rl_hip_free": (_i, [_vp]),
+    "rl_hip_memcpy_h2d": (_i, [_vp, _vp, _sz, _vp]),
+    "rl_hip_memcpy_d2h": (_i, [_vp, _vp, _sz, _vp]),
+    "rl_hip_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
+    "rl_hip_memset": (_i, [_vp, _i, _sz, _vp]),
+    "rl_hip_stream_create": (_i, [C.POINTER(_vp)]),
+    "rl_hip_stream_destroy": (_i, [_vp]),
+    "rl_hip_stream_synchronize": (_i, [_vp]),
+    "rl_hip_device_synchronize": (_i, []),
+    "rl_hip_event_create": (_i, [C.POINTER(_vp)]),
+    "rl_hip_event_destroy": (_i, [_vp]),
+    "rl_hip_event_record": (_i, [_vp, _vp]),
+    "rl_hip_event_elapsed_ms": (_i, [_vp, _vp, C.POINTER(C.c_float)]),
+    "rl_hip_e4m3_to_f32": (_i, [_vp, _vp, _sz, _vp]),
+    "rl_hip_fp8_packed_bytes": (_sz, [_i, _i]),
+    "rl_hip_fp8_tile_scales": (_sz, [_i, _i]),
+    "rl_hip_bf16_packed_bytes": (_sz, [_i, _i]),
+    "rl_hip_act_frag_bytes": (_sz, [_i, _i]),
+    "rl_hip_pack_fp8": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_pack_bf16": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rl_hip_pack_act": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rl_hip_gemm_fp8_frag": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rl_hip_gemm_bf16_frag": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
+    "rl_hip_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
+}
+
+_lib = None
+
+
+class HipError(RuntimeError):
+    def __init__(self, fn: str, code: int, msg: str):
+        super().__init__(f"{fn} failed (status {code}): {msg}")
+        self.code = code
+
+
+def lib() -> C.CDLL:
+    """Load the HIP library; raises if it was not built (no CPU fallback)."""
+    global _lib
+    if _lib is None:
+        if not os.path.exists(LIB_PATH):
+            raise RuntimeError(f"{LIB_PATH} is missing: run rapidllm_amd/build.py (hipcc, gfx950)")
+        L = C.CDLL(LIB_PATH)
+        for name, (res, args) in _SIGS.items():
+            f = getattr(L, name)
+            f.restype = res
+            f.argtypes = args
+        _lib = L
+    return _lib
+
+
+def declared_symbols():
+    return list(_SIGS)
+
+
+def call(name: str, *args) -> None:
+    """Call an RlStatus-returning entry point and raise on failure."""
+    rc = getattr(lib(), name)(*args)
+    if rc != 0:
+        raise HipError(name, rc, lib().rl_hip_last_error().decode(errors="replace"))
+
+
+def require_gpu() -> None:
+    if not lib().rl_hip_available():
+        raise RuntimeError("no gfx950 device visible to the HIP runtime")
+
+
+class DeviceBuffer:
+    """Owning device allocation (rl_hip_malloc / rl_hip_free)."""
+
+    def __init__(self, nbytes: int):
+        p = C.c_void_p()
+        call("rl_hip_malloc", C.byref(p), max(int(nbytes), 1))
+        self.ptr = p.value
+        self.nbytes = int(nbytes)
+
+    @classmethod
+    def from_numpy(cls, a: np.ndarray, stream=None) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(a.nbytes)
+        if a.nbytes:
+            call("rl_hip_memcpy_h2d", b.ptr, a.ctypes.data, a.nbytes, stream)
+            call("rl_hip_stream_synchronize", stream)
+        return b
+
+    def upload(self, a: np.ndarray, stream=None) -> None:
+        a = np.ascontiguousarray(a)
+        assert a.nbytes <= self.nbytes
+        call("rl_hip_memcpy_h2d", self.ptr, a.ctypes.data, a.nbytes, stream)
+        call("rl_hip_stream_synchronize", stream)
+
+    def numpy(self, dtype, shape, stream=None, offset: int = 0) -> np.ndarray:
+        out = np.empty(shape, dtype)
+        assert offset + out.nbytes <= self.nbytes
+        if out.nbytes:
+            call("rl_hip_memcpy_d2h", out.ctypes.data, self.ptr + offset, out.nbytes, stream)
+        return out
+
+    def zero(self, stream=None) -> None:
+        call("rl_hip_memset", self.ptr, 0, self.nbytes, stream)
+
+    def free(self) -> None:
+        if self.ptr:
+            call("rl_hip_free", self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            if self.ptr and _lib is not None:
+                _lib.rl_hip_free(self.ptr)
+                self.ptr = None
+        except Exception:
+            pass
+
+
+def synchronize() -> None:
+    call("rl_hip_device_synchronize")
+
+
+class Timer:
+    """HIP events recorded on `stream` (the stream the kernels run on)."""
+
+    def __init__(self, stream=None):
+        self.stream = stream
+        a, b = C.c_void_p(), C.c_void_p()
+        call("rl_hip_event_create", C.byref(a))
+        call("rl_hip_event_create", C.byref(b))
+        self.a, self.b = a.value, b.value
+
+    def start(self):
+        call("rl_hip_event_record", self.a, self.stream)
+
+    def stop(self) -> float:
+        call("rl_hip_event_record", self.b, self.stream)
+        ms = C.c_float()
+        call("rl_hip_event_elapsed_ms", self.a, self.b, C.byref(ms))
+        return ms.value
+
+    def __del__(self):
+        try:
+            if _lib is not None:
+                _lib.rl_hip_event_destroy(self.a)
+                _lib.rl_hip_event_destroy(self.b)
+        except Exception:
+            pass

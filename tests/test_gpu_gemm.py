@@ -1,0 +1,93 @@
+"""GPU parity: block-FP8 / BF16 skinny GEMM and e4m3 decode vs the CPU oracle.
+
+Tolerances: decode bit-exact; fp32 outputs within 1e-3
+relative L2 of the reference CPU result.
+"""
+import numpy as np
+import pytest
+
+from rapidllm_amd import ops, synth
+
+pytestmark = pytest.mark.gpu
+
+REL_L2 = 1e-3
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def test_e4m3_decode_bitexact(gpu, orc):
+    codes = np.array([c for c in range(256) if c not in (0x7F, 0xFF)], np.uint8)
+    got = ops.e4m3_to_f32(codes)
+    want = np.array([orc.lib().orc_e4m3_to_f32(int(c)) for c in codes], np.float32)
+    assert np.array_equal(got.view(np.uint32), want.view(np.uint32))
+
+
+@pytest.mark.parametrize("m,n", [(64, 512), (300, 1000), (17, 130), (1024, 5120)])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 8])
+def test_gemm_fp8_vs_oracle(gpu, orc, m, n, T):
+    r = synth.rng(100 + m + n + T)
+    W = synth.fp8_weight(r, m, n)
+    s = synth.fp8_scales(r, m, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    lin = ops.Fp8Linear(W, s)
+    Y = ops.linear_T(lin, X)
+    Yo = orc.gemm_fp8(W, s, X)
+    for t in range(T):
+        assert rel_l2(Y[t], Yo[t]) <= REL_L2, (m, n, T, t, rel_l2(Y[t], Yo[t]))
+
+
+def test_gemm_fp8_tokens_independent_of_T(gpu):
+    """Token t's output is bit-identical whether it runs alone (T=1) or inside a
+    T=4 verify batch: the greedy invariant needs T=4 == 4 x T=1 exactly."""
+    r = synth.rng(7)
+    m, n = 2048, 5120
+    W = synth.fp8_weight(r, m, n)
+    s = synth.fp8_scales(r, m, n)
+    X = r.standard_normal((4, n)).astype(np.float32)
+    lin = ops.Fp8Linear(W, s)
+    Y4 = ops.linear_T(lin, X)
+    for t in range(4):
+        Y1 = ops.linear_T(lin, X[t:t + 1])[0]
+        assert np.array_equal(Y1.view(np.uint32), Y4[t].view(np.uint32)), t
+
+
+def test_gemm_fp8_config1_full_shape(gpu, orc):
+    """W[17408x5120] e4m3, log-uniform scales, x ~ N(0,1)."""
+    r = synth.rng(0xC1)
+    m, n = 17408, 5120
+    W = synth.fp8_weight(r, m, n)
+    s = synth.fp8_scales(r, m, n)
+    x = r.standard_normal(n).astype(np.float32)
+    y = ops.gemv_fp8(W, s, x)
+    yo = orc.gemv_fp8(W, s, x)
+    assert rel_l2(y, yo) <= REL_L2, rel_l2(y, yo)
+
+
+def test_gemm_fp8_large_activations(gpu, orc):
+    """Activations far outside fp16 range (the split keeps fp32's exponent range)."""
+    r = synth.rng(8)
+    m, n = 256, 1024
+    W = synth.fp8_weight(r, m, n)
+    s = synth.fp8_scales(r, m, n)
+    X = (r.standard_normal((2, n)) * np.float32(1e6)).astype(np.float32)
+    X[1] *= np.float32(1e-12)
+    Y = ops.linear_T(ops.Fp8Linear(W, s), X)
+    Yo = orc.gemm_fp8(W, s, X)
+    for t in range(2):
+        assert rel_l2(Y[t], Yo[t]) <= REL_L2
+
+
+@pytest.mark.parametrize("m,n,T", [(96, 512, 1), (1000, 384, 4), (5120, 5120, 3)])
+def test_gemm_bf16_vs_oracle(gpu, orc, m, n, T):
+    r = synth.rng(200 + m)
+    Wf = r.standard_normal((m, n)).astype(np.float32)
+    Wb = synth.bf16_bits(Wf)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    Y = ops.linear_T(ops.Bf16Linear(Wb), X)
+    for t in range(T):
+        yo = orc.gemv_bf16(Wb, X[t])
+        assert rel_l2(Y[t], yo) <= REL_L2
