@@ -90,14 +90,43 @@ int rl_hip_pack_fp8(const uint8_t* w_dev_rowmajor, const float* scale_dev, uint8
                     int m, int n, void* stream);
 int rl_hip_pack_bf16(const uint16_t* w_dev_rowmajor, uint16_t* w_tiled, int m, int n, void* stream);
 int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream);
-/* Y[T][m] (=, or += when accumulate) W . X for T in 1..8 using a packed fragment buffer. */
+/* Y[T][m] (=, or += when accumulate) W . X for T in 1..8 using a packed fragment
+ * buffer.  Deterministic: partial sums are combined in a fixed order, and token t's
+ * result does not depend on T. */
 int rl_hip_gemm_fp8_frag(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                          int T, int accumulate, void* stream);
 int rl_hip_gemm_bf16_frag(const uint16_t* w_tiled, const void* frag, float* Y, int m, int n, int T, int accumulate,
                           void* stream);
+/* Tuning hook: force the work split (row-tiles per workgroup, waves per workgroup
+ * along K, load pipeline depth); row_tiles = 0 restores the shape-based choice. */
+int rl_hip_set_gemm_config(int row_tiles, int k_waves, int depth);
 /* Convenience: pack X into `frag_scratch` then GEMM (two launches). */
 int rl_hip_gemm_fp8(const uint8_t* w_tiled, const float* tile_scale, const float* X, float* Y, void* frag_scratch,
                     int m, int n, int T, void* stream);
+
+/* ---- GGUF K-quant linears -------------------------------------------------
+ * Replaces: ops::dequant_q4_k / dequant_q6_k (src/kernels/ops.cpp:255-284, 357-387),
+ * ops::gemv_q4_k / gemv_q6_k (ops.cpp:292-305, 389-402; threaded in
+ * src/kernels/cpu_caps.cpp:200-222), the CUDA K-quant T=1..4 families
+ * (src/kernels/cuda/cuda_engine.cu:2347-2647, gemv_t4_pipe.cu, gemv_t4_q6_t12tile.cu)
+ * and Device::launch("gemv_q4k" / "gemv_q6k", GemvKQuantParams) (params.h:7).
+ * `type` is RL_Q_Q4_K or RL_Q_Q6_K.  Blocks are the GGUF bytes (144 B / 210 B per
+ * 256 weights, rows contiguous); rl_hip_pack_kquant moves them (bytes only) into
+ * the device layout.  X is fp32 [T][n], T in 1..4, n a multiple of 256.
+ * rl_hip_dequant_kquant decodes row-major blocks bit-exactly like the reference. */
+size_t rl_hip_kquant_tiled_bytes(int type, int m, int n);
+size_t rl_hip_kquant_workspace_bytes(int m, int n, int T);
+int rl_hip_pack_kquant(int type, const uint8_t* blocks, uint8_t* tiled, int m, int n, void* stream);
+int rl_hip_gemm_kquant(int type, const uint8_t* tiled, const float* X, float* Y, void* workspace,
+                       size_t workspace_bytes, int m, int n, int T, int accumulate, void* stream);
+int rl_hip_dequant_kquant(int type, const uint8_t* blocks, float* out, size_t n_blocks, void* stream);
+
+/* ---- bandwidth calibration ------------------------------------------------
+ * No counterpart in the reference.  A streaming copy / read of `bytes` (multiple of
+ * 16) that measures the achievable HBM rate and calibrates rocprof's FETCH_SIZE /
+ * WRITE_SIZE counters against bytes known to be moved. */
+int rl_hip_copy_probe(const void* src, void* dst, size_t bytes, void* stream);
+int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
 
 #ifdef __cplusplus
 }

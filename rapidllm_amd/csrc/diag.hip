@@ -1,0 +1,58 @@
+// diag.hip -- bandwidth calibration kernels (no counterpart in the reference).
+//
+// A plain streaming copy and a streaming read of a known number of bytes.  They
+// give the achievable HBM rate on the box and the scale factor between rocprof's
+// FETCH_SIZE / WRITE_SIZE counters and bytes actually moved.
+#include "common.h"
+
+using namespace rl;
+
+namespace {
+
+__global__ void copy_probe_kernel(const i32x4* __restrict__ src, i32x4* __restrict__ dst, size_t n16) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n16; i += stride)
+        __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
+}
+
+// Each thread keeps UNROLL independent 16-byte loads in flight.
+template <int UNROLL>
+__global__ void read_probe_kernel(const i32x4* __restrict__ src, size_t n16, unsigned* __restrict__ out) {
+    const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
+    size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    i32x4 acc = {0, 0, 0, 0};
+    for (; i + (UNROLL - 1) * stride < n16; i += UNROLL * stride) {
+        i32x4 v[UNROLL];
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+#pragma unroll
+        for (int u = 0; u < UNROLL; ++u) acc ^= v[u];
+    }
+    for (; i < n16; i += stride) acc ^= src[i];
+    const unsigned x = static_cast<unsigned>(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
+    if (x == 0x9e3779b9u) out[0] = x;  // practically never taken; keeps the loads live
+}
+
+}  // namespace
+
+extern "C" {
+
+int rl_hip_copy_probe(const void* src, void* dst, size_t bytes, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(bytes % 16 == 0 && src && dst, RL_ERR_RANGE, "copy_probe: bytes must be a multiple of 16");
+        hipLaunchKernelGGL(copy_probe_kernel, dim3(256 * 8), dim3(256), 0, S(stream),
+                           static_cast<const i32x4*>(src), static_cast<i32x4*>(dst), bytes / 16);
+        check_launch("copy_probe_kernel");
+    });
+}
+
+int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(bytes % 16 == 0 && src && out4, RL_ERR_RANGE, "read_probe: bytes must be a multiple of 16");
+        hipLaunchKernelGGL(read_probe_kernel<8>, dim3(256 * 8), dim3(256), 0, S(stream),
+                           static_cast<const i32x4*>(src), bytes / 16, static_cast<unsigned*>(out4));
+        check_launch("read_probe_kernel");
+    });
+}
+
+}  // extern "C"

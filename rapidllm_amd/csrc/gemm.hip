@@ -51,13 +51,17 @@ __device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 
 enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2 };
 
-template <int RT, int KSPLIT, bool kFp8>
+// Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
+// contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
+// weights in flight while one is computed).
+template <int RT, int KSPLIT, int D, bool kFp8>
 __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
                                                                 float* __restrict__ Y, int m, int n_kb, int T,
                                                                 int epilogue) {
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
+    constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
     const int wave = threadIdx.x >> 6;
     const int g = lane >> 4;
@@ -66,6 +70,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     const int rt0 = blockIdx.x * RT;
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
 
+    // contiguous run of column blocks for this wave
     const int per = (n_kb + KSPLIT - 1) / KSPLIT;
     const int kb_begin = min(n_kb, wave * per);
     const int kb_end = min(n_kb, kb_begin + per);
@@ -76,67 +81,65 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 
     const bool has_col = col < NC;
     const i32x4 zero4 = {0, 0, 0, 0};
-
-    auto load_w = [&](int kb, i32x4 (&wv)[RT][kFp8 ? 2 : 4]) {
+    const uint8_t* wbase[RT];
+    const float* sbase[RT];
 #pragma unroll
-        for (int r = 0; r < RT; ++r) {
-            const int rt = min(rt0 + r, m_tiles - 1);
-            const uint8_t* tile = W + (static_cast<size_t>(rt) * n_kb + kb) * kTileBytes;
-#pragma unroll
-            for (int c = 0; c < (kFp8 ? 2 : 4); ++c)
-                wv[r][c] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(tile + c * 1024 + 16 * lane));
-        }
-    };
-    auto load_b = [&](int kb, i32x4 (&bv)[4]) {
-#pragma unroll
-        for (int i = 0; i < 4; ++i)
-            bv[i] = has_col ? frag[((static_cast<size_t>(kb) * 4 + i) * 4 + g) * NC + col] : zero4;
-    };
-
-    i32x4 wcur[RT][kFp8 ? 2 : 4], wnext[RT][kFp8 ? 2 : 4];
-    i32x4 bcur[4], bnext[4];
-    if (kb_begin < kb_end) {
-        load_w(kb_begin, wcur);
-        load_b(kb_begin, bcur);
+    for (int r = 0; r < RT; ++r) {
+        const int rt = min(rt0 + r, m_tiles - 1);
+        wbase[r] = W + static_cast<size_t>(rt) * n_kb * kTileBytes + 16 * lane;
+        sbase[r] = kFp8 ? tscale + static_cast<size_t>(rt) * n_kb : nullptr;
     }
-    for (int kb = kb_begin; kb < kb_end; ++kb) {
-        if (kb + 1 < kb_end) {
-            load_w(kb + 1, wnext);
-            load_b(kb + 1, bnext);
-        }
+    const i32x4* fbase = frag + static_cast<size_t>(g) * NC + col;
+    const size_t fstride = static_cast<size_t>(16) * NC;  // per column block
+
+    i32x4 wbuf[D][RT][NW];
+    i32x4 bbuf[D][4];
+    auto load = [&](int d, int kb) {
+#pragma unroll
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int c = 0; c < NW; ++c)
+                wbuf[d][r][c] = __builtin_nontemporal_load(
+                    reinterpret_cast<const i32x4*>(wbase[r] + static_cast<size_t>(kb) * kTileBytes + c * 1024));
+#pragma unroll
+        for (int i = 0; i < 4; ++i) bbuf[d][i] = has_col ? fbase[kb * fstride + i * 4 * NC] : zero4;
+    };
+    auto compute = [&](int d, int kb) {
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 Frag8 a, b;
-                b.i = bcur[i];
+                b.i = bbuf[d][i];
                 if constexpr (kFp8) {
-                    const i32x4 wv = wcur[r][i >> 1];
+                    const i32x4 wv = wbuf[d][r][i >> 1];
                     const uint32_t d0 = static_cast<uint32_t>((i & 1) ? wv[2] : wv[0]);
                     const uint32_t d1 = static_cast<uint32_t>((i & 1) ? wv[3] : wv[1]);
                     e4m3x4_to_bf16(d0, a.u[0], a.u[1]);
                     e4m3x4_to_bf16(d1, a.u[2], a.u[3]);
                 } else {
-                    a.i = wcur[r][i];
+                    a.i = wbuf[d][r][i];
                 }
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
             }
-            if constexpr (kFp8) {
-                const int rt = min(rt0 + r, m_tiles - 1);
-                const float s = tscale[static_cast<size_t>(rt) * n_kb + kb];
-                tot[r] += s * acc;
-            } else {
+            if constexpr (kFp8)
+                tot[r] += sbase[r][kb] * acc;
+            else
                 tot[r] += acc;
-            }
         }
-        if (kb + 1 < kb_end) {
+    };
+
 #pragma unroll
-            for (int r = 0; r < RT; ++r)
+    for (int d = 0; d < D; ++d)
+        if (kb_begin + d < kb_end) load(d, kb_begin + d);
+    for (int kb = kb_begin; kb < kb_end; kb += D) {
 #pragma unroll
-                for (int c = 0; c < (kFp8 ? 2 : 4); ++c) wcur[r][c] = wnext[r][c];
-#pragma unroll
-            for (int i = 0; i < 4; ++i) bcur[i] = bnext[i];
+        for (int d = 0; d < D; ++d) {
+            if (kb + d < kb_end) {
+                compute(d, kb + d);
+                if (kb + d + D < kb_end) load(d, kb + d + D);
+            }
         }
     }
 
@@ -147,32 +150,36 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     for (int r = 0; r < RT; ++r) red[wave][r][lane] = tot[r];
     __syncthreads();
 
-    const int items = (epilogue == kSwiGLU ? RT / 2 : RT) * T * kTileRows;
-    for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
-        const int row = it % kTileRows;
-        const int t = (it / kTileRows) % T;
-        const int r = it / (kTileRows * T);
+    // items: (r, t, row); value = hi column + mid column, summed over waves
+    const int items = RT * T * kTileRows;
+    auto wg_value = [&](int r, int t, int row) {
         const int src_lane = (row >> 2) * 16;
         const int v = row & 3;
-        auto cval = [&](int rr, int c) {
-            float s = 0.f;
+        float s = 0.f;
 #pragma unroll
-            for (int w = 0; w < KSPLIT; ++w) s += red[w][rr][src_lane + c][v];
-            return s;
-        };
-        if (epilogue == kSwiGLU) {
-            // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs
-            const int rt_g = rt0 + 2 * r;
-            const int orow = (rt_g / 2) * kTileRows + row;
-            if (rt_g + 1 < m_tiles + 1 && orow < m / 2) {
-                const float gv = cval(2 * r, t) + cval(2 * r, T + t);
-                const float uv = cval(2 * r + 1, t) + cval(2 * r + 1, T + t);
+        for (int w = 0; w < KSPLIT; ++w) s += red[w][r][src_lane + t][v] + red[w][r][src_lane + T + t][v];
+        return s;
+    };
+
+    auto final_value = [&](int r, int t, int row) -> float { return wg_value(r, t, row); };
+
+    if (epilogue == kSwiGLU) {
+        // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs
+        for (int it = threadIdx.x; it < (RT / 2) * T * kTileRows; it += 64 * KSPLIT) {
+            const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
+            const int orow = ((rt0 + 2 * r) / 2) * kTileRows + row;
+            if ((rt0 + 2 * r) * kTileRows + row < m) {
+                const float gv = final_value(2 * r, t, row);
+                const float uv = final_value(2 * r + 1, t, row);
                 Y[static_cast<size_t>(t) * (m / 2) + orow] = gv / (1.f + __expf(-gv)) * uv;
             }
-        } else {
+        }
+    } else {
+        for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
+            const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
             const int orow = (rt0 + r) * kTileRows + row;
             if (orow < m) {
-                const float val = cval(r, t) + cval(r, T + t);
+                const float val = final_value(r, t, row);
                 float* dst = Y + static_cast<size_t>(t) * m + orow;
                 if (epilogue == kAdd)
                     *dst += val;
@@ -273,6 +280,24 @@ __global__ void e4m3_decode_kernel(const uint8_t* __restrict__ in, float* __rest
 inline int n_kb_of(int n) { return (n + kBlockCols - 1) / kBlockCols; }
 inline int m_tiles_of(int m) { return (m + kTileRows - 1) / kTileRows; }
 
+// Work split per launch: row-tiles per workgroup (RT), waves per workgroup along K
+// (KS), load pipeline depth (D).  Measured on MI355X (17408x5120 / 5120x17408,
+// T=1..4): RT=2, D=2 with 8 waves is best when there are >= 256 workgroups; short
+// m (fewer workgroups than CUs) does better with 16 waves per workgroup.
+struct GemmCfg {
+    int rt, ks, d;
+};
+static GemmCfg g_force{0, 0, 0};
+
+template <bool kFp8, int RT, int KS, int D>
+void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
+                     int epilogue, hipStream_t s) {
+    const int groups = (m_tiles_of(m) + RT - 1) / RT;
+    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups), dim3(64 * KS), 0, s,
+                       static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
+                       epilogue);
+}
+
 template <bool kFp8>
 void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y, int m, int n, int T, int epilogue,
                  hipStream_t s) {
@@ -282,14 +307,21 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     RL_REQUIRE(!kFp8 || tscale, RL_ERR_RANGE, "gemm: FP8 weights need tile scales");
     const int n_kb = n_kb_of(n);
     const int m_tiles = m_tiles_of(m);
-    constexpr int RT = 2, KS = 4;
     if (epilogue == kSwiGLU)
         RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm swiglu: interleaved rows must be a multiple of 32");
-    const int grid = (m_tiles + RT - 1) / RT;
-    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, kFp8>), dim3(grid), dim3(64 * KS), 0, s,
-                       static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue);
-    check_launch("gemm_frag_kernel");
+    GemmCfg c{2, (m_tiles + 1) / 2 >= 256 ? 8 : 16, 2};
+    if (g_force.rt) c = g_force;
+    if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
+#define RL_GEMM_CASE(R, K, DD)                                                            \
+    if (c.rt == R && c.ks == K && c.d == DD) {                                            \
+        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, s);     \
+        check_launch("gemm_frag_kernel");                                                 \
+        return;                                                                           \
+    }
+    RL_GEMM_CASE(2, 8, 2) RL_GEMM_CASE(2, 16, 2) RL_GEMM_CASE(2, 4, 2) RL_GEMM_CASE(1, 8, 2)
+    RL_GEMM_CASE(1, 16, 2) RL_GEMM_CASE(2, 8, 3)
+#undef RL_GEMM_CASE
+    throw Error(RL_ERR_UNSUPPORTED, "gemm: unsupported work split");
 }
 
 void launch_pack_act(const float* X, void* frag, int n, int T, hipStream_t s) {
@@ -318,6 +350,11 @@ void pack_act(const float* X, void* frag, int n, int T, hipStream_t s) { launch_
 using namespace rl;
 
 extern "C" {
+
+int rl_hip_set_gemm_config(int row_tiles, int k_waves, int depth) {
+    g_force = GemmCfg{row_tiles, k_waves, depth > 0 ? depth : 2};
+    return RL_OK;
+}
 
 size_t rl_hip_fp8_packed_bytes(int m, int n) { return static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 2048; }
 size_t rl_hip_fp8_tile_scales(int m, int n) { return static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n); }

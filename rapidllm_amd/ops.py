@@ -62,7 +62,8 @@ class Bf16Linear:
         raw.free()
 
     def forward_frag(self, frag_ptr, y_ptr, T, accumulate=False, stream=None):
-        call("rl_hip_gemm_bf16_frag", self.w.ptr, frag_ptr, y_ptr, self.m, self.n, T, 1 if accumulate else 0, stream)
+        call("rl_hip_gemm_bf16_frag", self.w.ptr, frag_ptr, y_ptr, self.m, self.n, T, 1 if accumulate else 0,
+             stream)
 
 
 def act_frag_buffer(n: int, T: int) -> DeviceBuffer:
@@ -95,3 +96,73 @@ def e4m3_to_f32(codes: np.ndarray) -> np.ndarray:
     d_out = DeviceBuffer(4 * codes.size)
     call("rl_hip_e4m3_to_f32", d_in.ptr, d_out.ptr, codes.size, None)
     return d_out.numpy(np.float32, codes.shape)
+
+
+Q4_K, Q6_K = 6, 8  # RlQuant / rapidllm::QuantKind values
+
+
+class KQuantLinear:
+    """GGUF Q4_K / Q6_K weight [m][n] resident in HBM in the K-tiled layout
+    (QuantKind::Q4_K / Q6_K consumed by ops::linear, reference ops.cpp:422-429)."""
+
+    def __init__(self, qtype: int, blocks: np.ndarray, m: int, n: int, stream=None):
+        assert qtype in (Q4_K, Q6_K) and n % 256 == 0
+        bb = 144 if qtype == Q4_K else 210
+        blocks = np.ascontiguousarray(blocks, np.uint8).reshape(-1)
+        assert blocks.size == m * (n // 256) * bb
+        self.qtype, self.m, self.n = qtype, m, n
+        L = hip.lib()
+        self.w = DeviceBuffer(L.rl_hip_kquant_tiled_bytes(qtype, m, n))
+        raw = DeviceBuffer.from_numpy(blocks, stream)
+        call("rl_hip_pack_kquant", qtype, raw.ptr, self.w.ptr, m, n, stream)
+        call("rl_hip_stream_synchronize", stream)
+        raw.free()
+        self.weight_bytes = blocks.size
+
+    def forward(self, x_ptr, y_ptr, T, ws, accumulate=False, stream=None):
+        call("rl_hip_gemm_kquant", self.qtype, self.w.ptr, x_ptr, y_ptr, ws.ptr, ws.nbytes, self.m, self.n, T,
+             1 if accumulate else 0, stream)
+
+
+def kquant_workspace(m: int, n: int, T: int) -> DeviceBuffer:
+    return DeviceBuffer(hip.lib().rl_hip_kquant_workspace_bytes(m, n, T))
+
+
+def kquant_linear_T(lin: KQuantLinear, X: np.ndarray, stream=None) -> np.ndarray:
+    X = _f32(X).reshape(-1, lin.n)
+    T = X.shape[0]
+    xd = DeviceBuffer.from_numpy(X, stream)
+    yd = DeviceBuffer(4 * T * lin.m)
+    lin.forward(xd.ptr, yd.ptr, T, kquant_workspace(lin.m, lin.n, T), stream=stream)
+    return yd.numpy(np.float32, (T, lin.m), stream)
+
+
+def gemv_q4_k(packed: np.ndarray, x: np.ndarray, m: int, n: int) -> np.ndarray:
+    """ops::gemv_q4_k(packed, x, y, m, n) (reference src/kernels/ops.h:203)."""
+    return kquant_linear_T(KQuantLinear(Q4_K, packed, m, n), x)[0]
+
+
+def gemv_q6_k(packed: np.ndarray, x: np.ndarray, m: int, n: int) -> np.ndarray:
+    """ops::gemv_q6_k(packed, x, y, m, n) (reference src/kernels/ops.h:214)."""
+    return kquant_linear_T(KQuantLinear(Q6_K, packed, m, n), x)[0]
+
+
+def _dequant(qtype: int, packed: np.ndarray, n: int) -> np.ndarray:
+    bb = 144 if qtype == Q4_K else 210
+    packed = np.ascontiguousarray(packed, np.uint8).reshape(-1)
+    nb = n // 256
+    assert packed.size >= nb * bb
+    src = DeviceBuffer.from_numpy(packed[: nb * bb])
+    out = DeviceBuffer(4 * nb * 256)
+    call("rl_hip_dequant_kquant", qtype, src.ptr, out.ptr, nb, None)
+    return out.numpy(np.float32, (nb * 256,))
+
+
+def dequant_q4_k(packed: np.ndarray, n: int) -> np.ndarray:
+    """ops::dequant_q4_k(packed, out, n) (reference src/kernels/ops.cpp:255)."""
+    return _dequant(Q4_K, packed, n)
+
+
+def dequant_q6_k(packed: np.ndarray, n: int) -> np.ndarray:
+    """ops::dequant_q6_k(packed, out, n) (reference src/kernels/ops.cpp:357)."""
+    return _dequant(Q6_K, packed, n)
