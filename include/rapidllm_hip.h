@@ -121,6 +121,72 @@ int rl_hip_gemm_kquant(int type, const uint8_t* tiled, const float* X, float* Y,
                        size_t workspace_bytes, int m, int n, int T, int accumulate, void* stream);
 int rl_hip_dequant_kquant(int type, const uint8_t* blocks, float* out, size_t n_blocks, void* stream);
 
+/* ---- Gated DeltaNet recurrent decode -----------------------------------------
+ * Replaces: ops::conv1d_update (src/kernels/ops.cpp:458-468), the gate math of
+ * ops::fused_delta_decode (src/kernels/ops_fused.cpp:111-123), ops::l2norm and
+ * ops::delta_recurrent_step{,_simd} (ops.cpp:158-163, 495-540; cpu_caps.cpp:236-265),
+ * the CUDA gdn_decode_t1_k / gdn_decode_tn_k (cuda_engine.cu:5166-5410) and
+ * Device::launch("conv1d_update" / "delta_recurrent", Conv1dParams /
+ * DeltaRecurrentParams) (params.h:17-18).
+ * For T tokens: qkv/a/b are rows t*ld_in of the in_proj output (raw, before conv);
+ * conv state [conv_dim][conv_k] (tap 0 oldest), conv_dim = 2*nk*dk + nv*dv;
+ * S fp32 per v-head TRANSPOSED: S_dev[h][j][i] = S[h][i][j] (i < dk, j < dv).
+ * o = [T][nv*dv] raw recurrent output (before the gated RMSNorm).
+ * dk must be 128, dv a multiple of 32, T <= 8.  S_out may alias S_in;
+ * conv_out must not alias conv_in. */
+int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
+                      const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
+                      const float* S_in, float* S_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k,
+                      int v_tiled, void* stream);
+
+/* ---- norms fused with GEMM input packing; embedding --------------------------
+ * Replaces: ops::qwen3_rmsnorm (src/kernels/ops.cpp:107-127), ops::gated_rmsnorm
+ * (ops.cpp:129-156), the CUDA rmsnorm_k / gated_rms_k families
+ * (cuda_engine.cu:4293-4450), Device::launch("rmsnorm" / "gated_rmsnorm",
+ * RmsNormParams) (params.h:5) and embed_row (src/runtime/session.cpp:122-140).
+ * Either output may be NULL: y = fp32 [T][n]; frag = GEMM fragments for n columns
+ * (rl_hip_act_frag_bytes(n, T) bytes).  gamma NULL = no weight.  rmsnorm uses
+ * (1 + gamma); the gated norm is per head when gamma_n < n, n % gamma_n == 0 and
+ * n >= 256 (the reference rule), with z rows at stride ld_z. */
+int rl_hip_rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
+                        void* stream);
+int rl_hip_gated_rmsnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, int gamma_n, float* y,
+                              void* frag, int n, int T, float eps, void* stream);
+int rl_hip_embed_rows(const void* table, int kind, const int* tokens_dev, float* out, int H, int vocab, int T,
+                      void* stream);
+
+/* ---- gated GQA attention decode over an fp16 KV cache -----------------------
+ * Replaces: the attention half of ops::fused_attn_decode (src/kernels/ops_fused.cpp:
+ * 137-184: q/gate split, q/k head RMSNorm, rope_partial, KV append, attn_decode,
+ * sigmoid gate), ops::attn_decode (ops.cpp:575-605), the CUDA qk_prep_store_k /
+ * qk_attn_decode_gqa_k (cuda_engine.cu:5696-5866) and Device::launch("attn_decode",
+ * AttnDecodeParams) (params.h:16).
+ * Y: rows t*ld_y of the fused projection [q0|gate0|q1|gate1|...| k | v] (per head
+ * q then gate, hd each).  Token t sits at position *pos_dev + t; its K (after RoPE)
+ * and V are stored as fp16 (round to nearest even) and it attends to positions
+ * 0 .. *pos_dev + t.  Caches: k_cache [n_kv][ctx][hd], vt_cache [n_kv][hd][ctx]
+ * (V transposed), ctx a multiple of 256, zero-filled at allocation.  head_dim 256,
+ * (n_q/n_kv)*T <= 32.  Outputs o * sigmoid(gate): fp32 `out` [T][n_q*hd] and/or
+ * o_proj fragments `frag`.  *pos_dev is not modified. */
+size_t rl_hip_attn_workspace_bytes(int n_kv, int ctx);
+int rl_hip_attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* k_cache,
+                             uint16_t* vt_cache, int ctx, const int* pos_dev, int T, int n_q, int n_kv, int head_dim,
+                             int rotary_dim, float theta, float eps, void* workspace, size_t workspace_bytes,
+                             float* out, void* frag, void* stream);
+
+/* ---- greedy argmax and speculative acceptance --------------------------------
+ * Replaces: greedy_sample (src/runtime/sampler.cpp:8-18), the CUDA
+ * argmax_partial_rows_k / argmax_final_rows_k (cuda_engine.cu:9375-9433) and the
+ * host-side prefix compare of spec_verify (cuda_engine.cu:17053-17117;
+ * src/runtime/session.cpp:802-825).  Ties go to the lowest index; NaN never wins.
+ * accept: n = 1 + longest prefix with preds[i] == toks[i+1]; *pos += n;
+ * *next_tok = preds[n-1].  All pointers are device pointers. */
+size_t rl_hip_argmax_workspace_bytes(int rows, int vocab);
+int rl_hip_argmax_rows(const float* logits, int rows, int vocab, int* out_idx, float* out_val, void* workspace,
+                       void* stream);
+int rl_hip_accept_prefix(const int* toks, const int* preds, int T, int* pos, int* n_consumed, int* next_tok,
+                         void* stream);
+
 /* ---- bandwidth calibration ------------------------------------------------
  * No counterpart in the reference.  A streaming copy / read of `bytes` (multiple of
  * 16) that measures the achievable HBM rate and calibrates rocprof's FETCH_SIZE /

@@ -1,0 +1,393 @@
+// attn.hip -- gated GQA attention decode over an fp16 KV cache, T = 1..4 tokens.
+//
+// Reference semantics (CPU, src/kernels/ops_fused.cpp:137-184; src/runtime/
+// session.cpp:271-323): per head [q | gate] split of the q projection (hd >= 64),
+// Qwen RMSNorm with (1 + gamma) on q and k heads (ops.cpp:107-127), partial RoPE
+// rotate-half over the first rotary_dim dims (ops.cpp:470-493), append K/V at
+// pos, softmax(q.k / sqrt(hd)) over positions 0..pos (ops.cpp:575-605), output
+// times sigmoid(gate).  The cache holds K (after RoPE) and V rounded to fp16 with
+// round-to-nearest-even, as the reference's GPU engine keeps it
+// (src/kernels/cuda/cuda_engine.cu:20122-20123).
+//
+// Kernels:
+//  qk_prep     one wave per (head, token): norm + RoPE + fp16 cache write; q is
+//              written as fp16 hi + lo fragments (hi + lo carries ~22 bits).
+//  attn_part   one workgroup per (kv head, 256-position chunk), 4 waves.  Scores
+//              S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with A = K rows straight
+//              from the cache and B = the fragments of all G*T query rows of the
+//              kv group (hi and lo in two column tiles, summed per lane); chunk
+//              softmax; P (fp16) staged in LDS in B-operand order; O^T = V^T . P^T
+//              with V stored transposed ([d][pos]) so A rows are contiguous.  Every
+//              K and V byte of the chunk is read once for all heads and tokens.
+//  attn_comb   merges the chunk partials (max, sum, O) per query row, applies
+//              sigmoid(gate) and writes fp32 and/or the o_proj GEMM fragments.
+//
+// Cache layouts: K [n_kv][ctx][hd] fp16;  V^T [n_kv][hd][ctx] fp16;  ctx % 256 == 0.
+#include "common.h"
+
+using namespace rl;
+
+namespace {
+
+constexpr int kHD = 256;
+constexpr int kChunk = 256;
+constexpr int kMaxPairs = 32;  // G * T query rows per kv head (<= 2 tiles of 16)
+
+typedef _Float16 half4 __attribute__((ext_vector_type(4)));
+
+__device__ inline float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+
+struct AttnArgs {
+    const float* Y;  // fused q(+gate)/k/v projection output, [T][ld_y]
+    int ld_y;
+    const float* q_norm;
+    const float* k_norm;
+    uint16_t* kc;  // [nkv][ctx][hd]
+    uint16_t* vt;  // [nkv][hd][ctx]
+    int ctx;
+    const int* pos;  // device: position of token 0
+    int T, nq, nkv, G, rot;
+    float theta, eps;
+    i32x4* qf;     // [nkv][8 s][4 g][2*PT ct][16 col] x 16 B
+    float* part_o; // [nkv][chunks][kMaxPairs][hd]
+    float* part_m; // [nkv][chunks][kMaxPairs]
+    float* part_l;
+    int max_chunks;
+    float* out;     // optional [T][nq*hd]
+    i32x4* frag;    // optional o_proj fragments (n = nq*hd)
+};
+
+__host__ __device__ inline int pair_tiles(int G, int T) { return (G * T + 15) / 16; }
+
+// grid (nq + 2*nkv, T), 64 threads.  Heads [0,nq): q; [nq, nq+nkv): k; then v.
+__global__ __launch_bounds__(64) void qk_prep_kernel(AttnArgs p) {
+    __shared__ float vec[kHD];
+    const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int pos = *p.pos + t;
+    const float* row = p.Y + static_cast<size_t>(t) * p.ld_y;
+    const int qcols = p.nq * kHD * 2;
+    if (head >= p.nq + p.nkv) {  // v: straight to the transposed cache
+        const int kv = head - p.nq - p.nkv;
+        const float* src = row + qcols + p.nkv * kHD + kv * kHD;
+        for (int d = lane; d < kHD; d += 64)
+            p.vt[(static_cast<size_t>(kv) * kHD + d) * p.ctx + pos] =
+                __builtin_bit_cast(uint16_t, static_cast<_Float16>(src[d]));
+        return;
+    }
+    const bool is_q = head < p.nq;
+    const float* src = is_q ? row + static_cast<size_t>(head) * 2 * kHD : row + qcols + (head - p.nq) * kHD;
+    const float* gam = is_q ? p.q_norm : p.k_norm;
+    double ss = 0.0;
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        x[r] = src[lane + 64 * r];
+        ss += static_cast<double>(x[r]) * x[r];
+    }
+    ss = wave_sum_d(ss);
+    const float inv = 1.f / sqrtf(static_cast<float>(ss / kHD) + p.eps);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vec[lane + 64 * r] = x[r] * inv * (gam ? 1.f + gam[lane + 64 * r] : 1.f);
+    __syncthreads();
+    const int half = p.rot / 2;
+    for (int i = lane; i < half; i += 64) {
+        const float freq = 1.f / powf(p.theta, static_cast<float>(i) / static_cast<float>(half));
+        const float ang = static_cast<float>(pos) * freq;
+        const float c = cosf(ang), s = sinf(ang);
+        const float x0 = vec[i], x1 = vec[i + half];
+        vec[i] = x0 * c - x1 * s;
+        vec[i + half] = x0 * s + x1 * c;
+    }
+    __syncthreads();
+    if (!is_q) {
+        const int kv = head - p.nq;
+        uint16_t* dst = p.kc + (static_cast<size_t>(kv) * p.ctx + pos) * kHD;
+        for (int d = lane; d < kHD; d += 64) dst[d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vec[d]));
+        return;
+    }
+    // q -> fp16 hi/lo fragments: dim d = 32 s + 8 g + e; pair k = t*G + head%G
+    const int kv = head / p.G;
+    const int k = t * p.G + head % p.G;
+    const int PT = pair_tiles(p.G, p.T);
+    const int pt = k >> 4, col = k & 15;
+    _Float16* qf = reinterpret_cast<_Float16*>(p.qf);
+    for (int d = lane; d < kHD; d += 64) {
+        const int s = d >> 5, g = (d >> 3) & 3, e = d & 7;
+        const _Float16 hi = static_cast<_Float16>(vec[d]);
+        const _Float16 lo = static_cast<_Float16>(vec[d] - static_cast<float>(hi));
+        const size_t base = (((static_cast<size_t>(kv) * 8 + s) * 4 + g) * (2 * PT));
+        qf[((base + 2 * pt) * 16 + col) * 8 + e] = hi;
+        qf[((base + 2 * pt + 1) * 16 + col) * 8 + e] = lo;
+    }
+}
+
+union H8 {
+    f16x8 v;
+    i32x4 i;
+    _Float16 h[8];
+};
+
+template <int PT>
+__global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
+    const int chunk = blockIdx.x, kv = blockIdx.y;
+    const int p0 = *p.pos;
+    const int L = p0 + p.T;  // keys 0 .. L-1 exist after this step's writes
+    const int c0 = chunk * kChunk;
+    if (c0 >= L) return;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const int npairs = p.G * p.T;
+    const float scale = 1.f / sqrtf(static_cast<float>(kHD));
+
+    __shared__ i32x4 P_lds[8][PT][4][16];  // [u][pt][g][col] : 8 fp16 of P^T
+    __shared__ float max_s[4][PT][16];
+    __shared__ float sum_s[4][PT][16];
+
+    // ---- scores for positions c0 + 64*wave + 16*ptile + row
+    f32x4 acc[4][2 * PT];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int b = 0; b < 2 * PT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* kbase = p.kc + static_cast<size_t>(kv) * p.ctx * kHD;
+    const i32x4* qbase = p.qf + static_cast<size_t>(kv) * 8 * 4 * (2 * PT) * 16;
+#pragma unroll 2
+    for (int s = 0; s < 8; ++s) {
+        H8 bq[2 * PT];
+#pragma unroll
+        for (int ct = 0; ct < 2 * PT; ++ct) bq[ct].i = qbase[((s * 4 + g) * (2 * PT) + ct) * 16 + col];
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt) {
+            const int prow = min(c0 + 64 * wave + 16 * pt + col, p.ctx - 1);
+            H8 a;
+            a.i = *reinterpret_cast<const i32x4*>(kbase + static_cast<size_t>(prow) * kHD + 32 * s + 8 * g);
+#pragma unroll
+            for (int ct = 0; ct < 2 * PT; ++ct)
+                acc[pt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bq[ct].v, acc[pt][ct], 0, 0, 0);
+        }
+    }
+
+    // ---- masked scores, chunk max (lane: query row `col` of pair tile, 4 rows each)
+    float sc[4][PT][4];
+    float mx[PT];
+#pragma unroll
+    for (int q = 0; q < PT; ++q) mx[q] = -INFINITY;
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+        for (int q = 0; q < PT; ++q) {
+            const int k = q * 16 + col;
+            const int t = k / p.G;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const int pos = c0 + 64 * wave + 16 * pt + 4 * g + v;
+                const bool ok = k < npairs && pos <= p0 + t;
+                const float val = (acc[pt][2 * q][v] + acc[pt][2 * q + 1][v]) * scale;
+                sc[pt][q][v] = ok ? val : -INFINITY;
+                mx[q] = fmaxf(mx[q], sc[pt][q][v]);
+            }
+        }
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+        mx[q] = fmaxf(mx[q], __shfl_xor(mx[q], 16, 64));
+        mx[q] = fmaxf(mx[q], __shfl_xor(mx[q], 32, 64));
+        if (g == 0) max_s[wave][q][col] = mx[q];
+    }
+    __syncthreads();
+    float M[PT], sum[PT];
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+        M[q] = fmaxf(fmaxf(max_s[0][q][col], max_s[1][q][col]), fmaxf(max_s[2][q][col], max_s[3][q][col]));
+        sum[q] = 0.f;
+    }
+    // P = exp(s - M) (0 where masked), staged as fp16 in PV B-operand order:
+    // unit (u, q, g, col) element e <-> chunk position 32u + 16*(e>=4) + 4g + (e&3)
+#pragma unroll
+    for (int pt = 0; pt < 4; ++pt) {
+        const int tile = 4 * wave + pt;
+#pragma unroll
+        for (int q = 0; q < PT; ++q) {
+            _Float16* unit = reinterpret_cast<_Float16*>(&P_lds[tile >> 1][q][g][col]);
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                const float e = M[q] == -INFINITY ? 0.f : expf(sc[pt][q][v] - M[q]);
+                sum[q] += e;
+                unit[(tile & 1) * 4 + v] = static_cast<_Float16>(e);
+            }
+        }
+    }
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+        sum[q] += __shfl_xor(sum[q], 16, 64);
+        sum[q] += __shfl_xor(sum[q], 32, 64);
+        if (g == 0) sum_s[wave][q][col] = sum[q];
+    }
+    __syncthreads();
+
+    // ---- O^T[d][pair] for d in [64*wave, 64*wave+64)
+    f32x4 o[4][PT];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int q = 0; q < PT; ++q) o[a][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;
+#pragma unroll 2
+    for (int u = 0; u < 8; ++u) {
+        H8 bp[PT];
+#pragma unroll
+        for (int q = 0; q < PT; ++q) bp[q].i = P_lds[u][q][g][col];
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d = 64 * wave + 16 * dt + col;
+            const uint16_t* vr = vbase + static_cast<size_t>(d) * p.ctx + c0 + 32 * u + 4 * g;
+            union {
+                f16x8 v;
+                i32x2 q2[2];
+            } a;
+            a.q2[0] = *reinterpret_cast<const i32x2*>(vr);
+            a.q2[1] = *reinterpret_cast<const i32x2*>(vr + 16);
+#pragma unroll
+            for (int q = 0; q < PT; ++q)
+                o[dt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bp[q].v, o[dt][q], 0, 0, 0);
+        }
+    }
+
+    // ---- partials: O^T lane (pair col, g) holds d = 64*wave + 16*dt + 4g + v
+    const size_t cbase = static_cast<size_t>(kv) * p.max_chunks + chunk;
+#pragma unroll
+    for (int q = 0; q < PT; ++q) {
+        const int k = q * 16 + col;
+        if (k >= npairs) continue;
+        float* dst = p.part_o + (cbase * kMaxPairs + k) * kHD;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            *reinterpret_cast<float4*>(dst + 64 * wave + 16 * dt + 4 * g) =
+                make_float4(o[dt][q][0], o[dt][q][1], o[dt][q][2], o[dt][q][3]);
+        if (wave == 0 && g == 0) {
+            p.part_m[cbase * kMaxPairs + k] = M[q];
+            p.part_l[cbase * kMaxPairs + k] = sum_s[0][q][col] + sum_s[1][q][col] + sum_s[2][q][col] + sum_s[3][q][col];
+        }
+    }
+}
+
+// grid (G*T pairs, nkv), 256 threads (one per d).
+__global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
+    const int k = blockIdx.x, kv = blockIdx.y, d = threadIdx.x;
+    const int t = k / p.G;
+    const int h = kv * p.G + k % p.G;
+    const int L = *p.pos + p.T;
+    const int nch = (L + kChunk - 1) / kChunk;
+    const size_t base = static_cast<size_t>(kv) * p.max_chunks;
+    float M = -INFINITY;
+    for (int c = 0; c < nch; ++c) M = fmaxf(M, p.part_m[(base + c) * kMaxPairs + k]);
+    float acc = 0.f, Ls = 0.f;
+    for (int c = 0; c < nch; ++c) {
+        const float m = p.part_m[(base + c) * kMaxPairs + k];
+        if (m == -INFINITY) continue;
+        const float w = expf(m - M);
+        Ls += p.part_l[(base + c) * kMaxPairs + k] * w;
+        acc += p.part_o[((base + c) * kMaxPairs + k) * kHD + d] * w;
+    }
+    const float gate = p.Y[static_cast<size_t>(t) * p.ld_y + static_cast<size_t>(h) * 2 * kHD + kHD + d];
+    const float val = acc / Ls * sigmoid_f(gate);
+    const int n = p.nq * kHD;
+    const int j = h * kHD + d;
+    if (p.out) p.out[static_cast<size_t>(t) * n + j] = val;
+    if (p.frag) {
+        __shared__ float vals[kHD];
+        vals[d] = val;
+        __syncthreads();
+        if (d < kHD / 8) {
+            const int col8 = (h * kHD) / 8 + d;
+            union {
+                uint16_t hh[8];
+                i32x4 q;
+            } hi, mid;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) split_bf16(vals[8 * d + e], hi.hh[e], mid.hh[e]);
+            const int kb = col8 >> 4, jb = (col8 & 15) * 8;
+            const int gg = jb >> 5, i = (jb >> 3) & 3;
+            const size_t u = ((static_cast<size_t>(kb) * 4 + i) * 4 + gg) * (2 * p.T) + t;
+            p.frag[u] = hi.q;
+            p.frag[u + p.T] = mid.q;
+        }
+    }
+}
+
+}  // namespace
+
+namespace rl {
+
+size_t attn_workspace_bytes(int nkv, int ctx) {
+    const size_t chunks = static_cast<size_t>(ctx) / kChunk;
+    const size_t qf = static_cast<size_t>(nkv) * 8 * 4 * 4 * 16 * 16;  // PT <= 2
+    return qf + static_cast<size_t>(nkv) * chunks * kMaxPairs * (kHD + 2) * 4 + 256;
+}
+
+void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,
+                       int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot, float theta, float eps,
+                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s) {
+    RL_REQUIRE(hd == kHD, RL_ERR_UNSUPPORTED, "attn: head_dim must be 256");
+    RL_REQUIRE(nkv > 0 && nq % nkv == 0, RL_ERR_RANGE, "attn: n_q must be a multiple of n_kv");
+    const int G = nq / nkv;
+    RL_REQUIRE(T >= 1 && G * T <= kMaxPairs, RL_ERR_RANGE, "attn: (n_q/n_kv) * T must be <= 32");
+    RL_REQUIRE(ctx > 0 && ctx % kChunk == 0, RL_ERR_RANGE, "attn: cache capacity must be a multiple of 256");
+    RL_REQUIRE(rot >= 2 && rot % 2 == 0 && rot <= hd, RL_ERR_RANGE, "attn: bad rotary dim");
+    RL_REQUIRE(Y && kc && vt && pos_dev && ws && (out || frag), RL_ERR_RANGE, "attn: null pointer");
+    RL_REQUIRE(ws_bytes >= attn_workspace_bytes(nkv, ctx), RL_ERR_RANGE, "attn: workspace too small");
+    const int chunks = ctx / kChunk;
+    char* w = static_cast<char*>(ws);
+    AttnArgs p{};
+    p.Y = Y;
+    p.ld_y = ld_y;
+    p.q_norm = q_norm;
+    p.k_norm = k_norm;
+    p.kc = kc;
+    p.vt = vt;
+    p.ctx = ctx;
+    p.pos = pos_dev;
+    p.T = T;
+    p.nq = nq;
+    p.nkv = nkv;
+    p.G = G;
+    p.rot = rot;
+    p.theta = theta;
+    p.eps = eps;
+    p.qf = reinterpret_cast<i32x4*>(w);
+    w += static_cast<size_t>(nkv) * 8 * 4 * 4 * 16 * 16;
+    p.part_o = reinterpret_cast<float*>(w);
+    w += static_cast<size_t>(nkv) * chunks * kMaxPairs * kHD * 4;
+    p.part_m = reinterpret_cast<float*>(w);
+    w += static_cast<size_t>(nkv) * chunks * kMaxPairs * 4;
+    p.part_l = reinterpret_cast<float*>(w);
+    p.max_chunks = chunks;
+    p.out = out;
+    p.frag = static_cast<i32x4*>(frag);
+    hipLaunchKernelGGL(qk_prep_kernel, dim3(nq + 2 * nkv, T), dim3(64), 0, s, p);
+    check_launch("qk_prep_kernel");
+    if (pair_tiles(G, T) == 1)
+        hipLaunchKernelGGL(attn_part_kernel<1>, dim3(chunks, nkv), dim3(256), 0, s, p);
+    else
+        hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks, nkv), dim3(256), 0, s, p);
+    check_launch("attn_part_kernel");
+    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv), dim3(256), 0, s, p);
+    check_launch("attn_comb_kernel");
+}
+
+}  // namespace rl
+
+extern "C" {
+
+size_t rl_hip_attn_workspace_bytes(int n_kv, int ctx) { return rl::attn_workspace_bytes(n_kv, ctx); }
+
+int rl_hip_attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* k_cache,
+                             uint16_t* vt_cache, int ctx, const int* pos_dev, int T, int n_q, int n_kv, int head_dim,
+                             int rotary_dim, float theta, float eps, void* workspace, size_t workspace_bytes,
+                             float* out, void* frag, void* stream) {
+    return guard([&] {
+        rl::attn_decode_layer(Y, ld_y, q_norm, k_norm, k_cache, vt_cache, ctx, pos_dev, T, n_q, n_kv, head_dim,
+                              rotary_dim, theta, eps, workspace, workspace_bytes, out, frag, S(stream));
+    });
+}
+
+}  // extern "C"

@@ -1,0 +1,253 @@
+// gdn.hip -- Gated DeltaNet recurrent decode for T = 1..8 tokens, fused:
+//   causal conv1d window update (+SiLU), head map, q/k L2 norm (q * 1/sqrt(dk)),
+//   gates beta = sigmoid(b), g = exp(-exp(A_log) * softplus(a + dt_bias)),
+//   delta rule per token on the fp32 state.
+// Arithmetic follows the reference CPU path: conv1d_update (src/kernels/ops.cpp:
+// 458-468), gates (src/kernels/ops_fused.cpp:111-123), l2norm (ops.cpp:158-163),
+// delta_recurrent_step (ops.cpp:495-534).  Output o is the raw recurrent output;
+// the gated RMSNorm is fused into the packing kernel of the next linear (norms.hip).
+//
+// Work split: one workgroup per (v-head h, 32 value columns).  Thread (c, jj)
+// keeps S[h][16c .. 16c+15][32*cg + jj] in registers; column j of S evolves
+// independently given k, q, g, beta and v_j, so the only cross-thread work per
+// token is two 8-lane sums (k^T S and q^T S) done with lane shuffles.
+// The state is read once and written once for all T tokens.
+//
+// State layout in HBM (transposed per head): St[h][j][i] = S[h][i][j], so each
+// thread's 16 values are 64 contiguous bytes and a wave reads 4 KiB contiguously.
+// Conv window layout is the reference's [channel][tap] (tap 0 oldest).
+#include "common.h"
+
+using namespace rl;
+
+namespace {
+
+constexpr int kDK = 128;    // key head dim (rows of S)
+constexpr int kCols = 32;   // value columns per workgroup
+constexpr int kMaxT = 8;
+constexpr int kConvK = 4;   // conv taps (Qwen3.6/3.8: 4)
+
+__device__ inline float silu_f(float x) { return x / (1.f + expf(-x)); }
+__device__ inline float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
+__device__ inline float softplus_f(float x) { return log1pf(expf(-fabsf(x))) + fmaxf(x, 0.f); }
+
+struct GdnArgs {
+    const float* qkv;   // [T][ld_in]: raw in_proj qkv channels at offset 0
+    const float* a;     // [T][ld_in]: a at this pointer (nv values per token)
+    const float* b;     // [T][ld_in]
+    int ld_in;          // row stride (floats) of qkv/a/b
+    const float* A_log; // [nv]
+    const float* dt_bias;
+    const float* conv_w;  // [conv_dim][K]
+    // Direct mode (cur == nullptr): read conv_in / S_in, write the state after the
+    // last token to conv_out / S_out.  S_out may alias S_in (each thread owns its
+    // slice); conv_out must not alias conv_in (q/k windows are read by several
+    // workgroups).
+    // Ring mode (cur != nullptr): R slots of conv_slot / s_slot floats at conv_in /
+    // S_in; read slot *cur, write the state after token t to slot (*cur + 1 + t) % R
+    // (R > T), so a speculative verify can keep any prefix without recomputation.
+    const float* conv_in;
+    float* conv_out;
+    const float* S_in;    // [nv][dv][dk] (transposed)
+    float* S_out;
+    const int* cur;
+    size_t conv_slot, s_slot;
+    int R;
+    float* o;             // [T][nv*dv]
+    int T, nk, nv, dv, K, v_tiled;
+};
+
+__global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
+    const int tid = threadIdx.x;
+    const int c = tid & 7;    // row chunk: rows 16c .. 16c+15
+    const int jj = tid >> 3;  // column within the group
+    const int groups_per_head = p.dv / kCols;
+    const int h = blockIdx.x / groups_per_head;
+    const int cg = blockIdx.x % groups_per_head;
+    const int j = cg * kCols + jj;
+    const int rep = p.nv / p.nk;
+    const int src = p.v_tiled ? (h % p.nk) : (h / rep);
+    const int qdim = p.nk * kDK;
+    const int T = p.T;
+    constexpr int K = kConvK;
+
+    __shared__ float q_s[kMaxT][kDK];
+    __shared__ float k_s[kMaxT][kDK];
+    __shared__ float v_s[kMaxT][kCols];
+    __shared__ float gate_s[kMaxT][2];  // decay g, beta
+    __shared__ double red_s[2][kMaxT][4];
+
+    const int slot0 = p.cur ? *p.cur : 0;
+    const float* S_in = p.cur ? p.S_in + static_cast<size_t>(slot0) * p.s_slot : p.S_in;
+    const float* conv_in = p.cur ? p.conv_in + static_cast<size_t>(slot0) * p.conv_slot : p.conv_in;
+    auto s_dst = [&](int t) -> float* {
+        return p.cur ? const_cast<float*>(p.S_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.s_slot : p.S_out;
+    };
+    auto conv_dst = [&](int t) -> float* {
+        return p.cur ? const_cast<float*>(p.conv_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.conv_slot
+                     : p.conv_out;
+    };
+    const bool per_token = p.cur != nullptr;
+
+    // ---- state: 16 rows of column j, contiguous in the transposed layout
+    const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + 16 * c;
+    float S[16];
+    {
+        const float4* sp = reinterpret_cast<const float4*>(S_in + s_off);
+#pragma unroll
+        for (int r = 0; r < 4; ++r) {
+            const float4 v = sp[r];
+            S[4 * r] = v.x;
+            S[4 * r + 1] = v.y;
+            S[4 * r + 2] = v.z;
+            S[4 * r + 3] = v.w;
+        }
+    }
+
+    // ---- conv1d over T tokens for the 2*128 q/k channels of the source k-head and
+    // the 32 v channels of this workgroup (288 channels, 256 threads).
+    // The q/k window state is written back only by one workgroup per source head.
+    const bool owns_qk = cg == 0 && (p.v_tiled ? (h == src) : (h == src * rep));
+    for (int ch = tid; ch < 2 * kDK + kCols; ch += 256) {
+        int chan;
+        if (ch < kDK)
+            chan = src * kDK + ch;
+        else if (ch < 2 * kDK)
+            chan = qdim + src * kDK + (ch - kDK);
+        else
+            chan = 2 * qdim + h * p.dv + cg * kCols + (ch - 2 * kDK);
+        const bool write_state = ch >= 2 * kDK || owns_qk;
+        float win[K];
+        {
+            const float4 wv = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan) * K);
+            win[0] = wv.x;
+            win[1] = wv.y;
+            win[2] = wv.z;
+            win[3] = wv.w;
+        }
+        const float* w = p.conv_w + static_cast<size_t>(chan) * K;
+        for (int t = 0; t < T; ++t) {
+#pragma unroll
+            for (int q = 0; q + 1 < K; ++q) win[q] = win[q + 1];
+            win[K - 1] = p.qkv[static_cast<size_t>(t) * p.ld_in + chan];
+            double acc = 0.0;
+#pragma unroll
+            for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
+            const float y = silu_f(static_cast<float>(acc));
+            if (ch < kDK)
+                q_s[t][ch] = y;
+            else if (ch < 2 * kDK)
+                k_s[t][ch - kDK] = y;
+            else
+                v_s[t][ch - 2 * kDK] = y;
+            if (write_state && (per_token || t == T - 1)) {
+                *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan) * K) =
+                    make_float4(win[0], win[1], win[2], win[3]);
+            }
+        }
+    }
+    if (tid < T) {
+        const int t = tid;
+        const float beta = sigmoid_f(p.b[static_cast<size_t>(t) * p.ld_in + h]);
+        const float g_log = -expf(p.A_log[h]) * softplus_f(p.a[static_cast<size_t>(t) * p.ld_in + h] + p.dt_bias[h]);
+        gate_s[t][0] = expf(g_log);
+        gate_s[t][1] = beta;
+    }
+    __syncthreads();
+
+    // ---- L2 norms (double sums over 128): waves 0/1 take q/k of every token
+    {
+        const int wave = tid >> 6, lane = tid & 63;
+        if (wave < 2) {
+            float(*vec)[kDK] = wave == 0 ? q_s : k_s;
+            for (int t = 0; t < T; ++t) {
+                const double a0 = vec[t][lane], a1 = vec[t][lane + 64];
+                const double ss = wave_sum_d(a0 * a0 + a1 * a1);
+                if (lane == 0) red_s[wave][t][0] = ss;
+            }
+        }
+    }
+    __syncthreads();
+    const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
+    for (int e = tid; e < T * kDK; e += 256) {
+        const int t = e / kDK, i = e % kDK;
+        const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t][0]) + 1e-6f);
+        const float ik = 1.f / sqrtf(static_cast<float>(red_s[1][t][0]) + 1e-6f);
+        q_s[t][i] = (q_s[t][i] * iq) * qscale;
+        k_s[t][i] = k_s[t][i] * ik;
+    }
+    __syncthreads();
+
+    // ---- delta rule, token by token
+    for (int t = 0; t < T; ++t) {
+        const float g = gate_s[t][0], beta = gate_s[t][1];
+        float kv = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            S[r] *= g;
+            kv += S[r] * k_s[t][16 * c + r];
+        }
+        kv += __shfl_xor(kv, 1, 64);
+        kv += __shfl_xor(kv, 2, 64);
+        kv += __shfl_xor(kv, 4, 64);
+        const float delta = (v_s[t][jj] - kv) * beta;
+        float ov = 0.f;
+#pragma unroll
+        for (int r = 0; r < 16; ++r) {
+            S[r] += k_s[t][16 * c + r] * delta;
+            ov += S[r] * q_s[t][16 * c + r];
+        }
+        ov += __shfl_xor(ov, 1, 64);
+        ov += __shfl_xor(ov, 2, 64);
+        ov += __shfl_xor(ov, 4, 64);
+        if (c == 0) p.o[static_cast<size_t>(t) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
+        if (per_token || t == T - 1) {
+            float4* dp = reinterpret_cast<float4*>(s_dst(t) + s_off);
+#pragma unroll
+            for (int r = 0; r < 4; ++r) dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
+        }
+    }
+}
+
+}  // namespace
+
+namespace rl {
+
+void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log, const float* dt_bias,
+                const float* conv_w, const float* conv_in, float* conv_out, const float* S_in, float* S_out,
+                const int* cur, size_t conv_slot, size_t s_slot, int R, float* o, int T, int nk, int nv, int dk,
+                int dv, int K, int v_tiled, hipStream_t s) {
+    RL_REQUIRE(dk == kDK, RL_ERR_UNSUPPORTED, "gdn_decode: key head dim must be 128");
+    RL_REQUIRE(dv % kCols == 0 && dv > 0, RL_ERR_UNSUPPORTED, "gdn_decode: value head dim must be a multiple of 32");
+    RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode: T must be in 1..8");
+    RL_REQUIRE(K == kConvK, RL_ERR_UNSUPPORTED, "gdn_decode: conv width must be 4");
+    RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode: nv must be a multiple of nk");
+    RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && o, RL_ERR_RANGE,
+               "gdn_decode: null pointer");
+    if (cur) {
+        RL_REQUIRE(R > T, RL_ERR_RANGE, "gdn_decode: ring needs more slots than tokens");
+    } else {
+        RL_REQUIRE(conv_out && S_out, RL_ERR_RANGE, "gdn_decode: null output state");
+        RL_REQUIRE(conv_out != conv_in, RL_ERR_RANGE, "gdn_decode: conv_out must not alias conv_in");
+    }
+    GdnArgs p{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, s_slot, R,
+              o, T, nk, nv, dv, K, v_tiled};
+    hipLaunchKernelGGL(gdn_decode_kernel, dim3(nv * (dv / kCols)), dim3(256), 0, s, p);
+    check_launch("gdn_decode_kernel");
+}
+
+}  // namespace rl
+
+extern "C" {
+
+int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
+                      const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
+                      const float* S_in, float* S_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k,
+                      int v_tiled, void* stream) {
+    return guard([&] {
+        rl::gdn_decode(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0, 0, 0, o,
+                       T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));
+    });
+}
+
+}  // extern "C"

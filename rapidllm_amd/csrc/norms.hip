@@ -1,0 +1,189 @@
+// norms.hip -- normalisations fused with the activation packing of the next linear,
+// and the embedding lookup.
+//
+//   rmsnorm_pack : Qwen3 RMSNorm y = x / sqrt(mean(x^2) + eps) * (1 + gamma)
+//                  (reference src/kernels/ops.cpp:107-127), written as fp32 and/or as
+//                  the bf16 hi/mid fragments the GEMM consumes (gemm.hip).
+//   gnorm_pack   : gated RMSNorm y = gamma * (o / rms(o)) * silu(z), per head when
+//                  gamma_n < n, n % gamma_n == 0, n >= 256, else over the vector
+//                  (ops.cpp:129-156); output to fragments for out_proj.
+//   embed_rows   : token ids -> fp32 rows of an F32 / F16 / BF16 table
+//                  (src/runtime/session.cpp:122-140).
+// Sums of squares are accumulated in double as in the reference scalar path.
+#include "common.h"
+
+using namespace rl;
+
+namespace {
+
+constexpr int kBlockCols = 128;
+
+__device__ inline float silu_f(float x) { return x / (1.f + expf(-x)); }
+
+// Fragment unit (16 B = 8 bf16) holding columns [8u, 8u+8) of token t, hi part.
+// The mid part sits T units later.  Layout matches pack_act_kernel (gemm.hip).
+__device__ inline size_t frag_unit(int col8, int t, int T) {
+    const int kb = col8 >> 4;           // 16 units per 128-column block
+    const int jb = (col8 & 15) * 8;     // first column within the block
+    const int g = jb >> 5, i = (jb >> 3) & 3;
+    return ((static_cast<size_t>(kb) * 4 + i) * 4 + g) * (2 * T) + t;
+}
+
+__device__ inline void write_frag8(i32x4* frag, int col8, int t, int T, const float (&v)[8]) {
+    union {
+        uint16_t h[8];
+        i32x4 q;
+    } hi, mid;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_bf16(v[e], hi.h[e], mid.h[e]);
+    const size_t u = frag_unit(col8, t, T);
+    frag[u] = hi.q;
+    frag[u + T] = mid.q;
+}
+
+__device__ inline double block_sum_d(double v, double* sh) {
+    v = wave_sum_d(v);
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    __syncthreads();
+    if (lane == 0) sh[wave] = v;
+    __syncthreads();
+    double s = 0.0;
+    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += sh[w];
+    return s;
+}
+
+// grid: T workgroups (one per token); n % 8 == 0.  Columns past n up to the next
+// multiple of 128 are written as zeros so the fragment buffer is fully defined.
+__global__ __launch_bounds__(256) void rmsnorm_pack_kernel(const float* __restrict__ x, int ld_x,
+                                                           const float* __restrict__ gamma, float* __restrict__ y,
+                                                           i32x4* __restrict__ frag, int n, int T, float eps) {
+    __shared__ double sh[4];
+    const int t = blockIdx.x;
+    const float* xt = x + static_cast<size_t>(t) * ld_x;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += static_cast<double>(xt[i]) * xt[i];
+    ss = block_sum_d(ss, sh);
+    const float inv = 1.f / sqrtf(static_cast<float>(ss / n) + eps);
+    const int units = ((n + kBlockCols - 1) / kBlockCols) * 16;
+    for (int u = threadIdx.x; u < units; u += blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int i = 8 * u + e;
+            v[e] = i < n ? xt[i] * inv * (gamma ? 1.f + gamma[i] : 1.f) : 0.f;
+            if (y && i < n) y[static_cast<size_t>(t) * n + i] = v[e];
+        }
+        if (frag) write_frag8(frag, u, t, T, v);
+    }
+}
+
+// grid: (segments, T); one workgroup per normalisation segment (a head, or the
+// whole vector).  seg = gamma_n when per_head, else n.
+__global__ __launch_bounds__(256) void gnorm_pack_kernel(const float* __restrict__ o, const float* __restrict__ z,
+                                                         int ld_z, const float* __restrict__ gamma, int gamma_n,
+                                                         int per_head, float* __restrict__ y,
+                                                         i32x4* __restrict__ frag, int n, int T, float eps) {
+    __shared__ double sh[4];
+    const int t = blockIdx.y;
+    const int seg = per_head ? gamma_n : n;
+    const int h0 = blockIdx.x * seg;
+    const float* ot = o + static_cast<size_t>(t) * n;
+    const float* zt = z + static_cast<size_t>(t) * ld_z;
+    double ss = 0.0;
+    for (int i = threadIdx.x; i < seg; i += blockDim.x) ss += static_cast<double>(ot[h0 + i]) * ot[h0 + i];
+    ss = block_sum_d(ss, sh);
+    const float inv = 1.f / sqrtf(static_cast<float>(ss / seg) + eps);
+    // units of 8 columns inside this segment (segments are multiples of 8)
+    for (int u = threadIdx.x; u < seg / 8; u += blockDim.x) {
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int i = h0 + 8 * u + e;
+            const float g = gamma ? gamma[per_head ? (i - h0) : (i % gamma_n)] : 1.f;
+            v[e] = g * (ot[i] * inv) * silu_f(zt[i]);
+            if (y) y[static_cast<size_t>(t) * n + i] = v[e];
+        }
+        if (frag) write_frag8(frag, (h0 >> 3) + u, t, T, v);
+    }
+    // zero the padding columns of the last 128-block once (by the last segment)
+    if (frag && blockIdx.x == gridDim.x - 1) {
+        const int units = ((n + kBlockCols - 1) / kBlockCols) * 16;
+        for (int u = n / 8 + threadIdx.x; u < units; u += blockDim.x) {
+            const float zero8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
+            write_frag8(frag, u, t, T, zero8);
+        }
+    }
+}
+
+// tokens[t] -> out[t][H]; kind: RL_Q_F32 / RL_Q_F16 / RL_Q_BF16 table [vocab][H].
+__global__ void embed_rows_kernel(const void* __restrict__ table, int kind, const int* __restrict__ tokens,
+                                  float* __restrict__ out, int H, int vocab) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= H) return;
+    int id = tokens[t];
+    id = id < 0 ? 0 : (id >= vocab ? vocab - 1 : id);  // ids are validated on the host
+    const size_t k = static_cast<size_t>(id) * H + i;
+    float v;
+    if (kind == RL_Q_F32)
+        v = static_cast<const float*>(table)[k];
+    else if (kind == RL_Q_BF16)
+        v = __uint_as_float(static_cast<uint32_t>(static_cast<const uint16_t*>(table)[k]) << 16);
+    else
+        v = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<const uint16_t*>(table)[k]));
+    out[static_cast<size_t>(t) * H + i] = v;
+}
+
+}  // namespace
+
+namespace rl {
+
+void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
+                  hipStream_t s) {
+    RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "rmsnorm_pack: n % 8 == 0, T in 1..8");
+    RL_REQUIRE(x && (y || frag), RL_ERR_RANGE, "rmsnorm_pack: null pointer");
+    hipLaunchKernelGGL(rmsnorm_pack_kernel, dim3(T), dim3(256), 0, s, x, ld_x, gamma, y, static_cast<i32x4*>(frag),
+                       n, T, eps);
+    check_launch("rmsnorm_pack_kernel");
+}
+
+void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, int gamma_n, float* y, void* frag,
+                int n, int T, float eps, hipStream_t s) {
+    if (gamma_n <= 0) gamma_n = n;
+    const bool per_head = gamma_n < n && n % gamma_n == 0 && n >= 256;
+    const int seg = per_head ? gamma_n : n;
+    RL_REQUIRE(seg % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "gnorm_pack: segment % 8 == 0, T in 1..8");
+    RL_REQUIRE(o && z && (y || frag), RL_ERR_RANGE, "gnorm_pack: null pointer");
+    hipLaunchKernelGGL(gnorm_pack_kernel, dim3(n / seg, T), dim3(seg >= 256 ? 256 : 128), 0, s, o, z, ld_z, gamma,
+                       gamma_n, per_head ? 1 : 0, y, static_cast<i32x4*>(frag), n, T, eps);
+    check_launch("gnorm_pack_kernel");
+}
+
+void embed_rows(const void* table, int kind, const int* tokens, float* out, int H, int vocab, int T, hipStream_t s) {
+    RL_REQUIRE(kind == RL_Q_F32 || kind == RL_Q_F16 || kind == RL_Q_BF16, RL_ERR_UNSUPPORTED,
+               "embed: table must be F32, F16 or BF16");
+    hipLaunchKernelGGL(embed_rows_kernel, dim3((H + 255) / 256, T), dim3(256), 0, s, table, kind, tokens, out, H,
+                       vocab);
+    check_launch("embed_rows_kernel");
+}
+
+}  // namespace rl
+
+extern "C" {
+
+int rl_hip_rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
+                        void* stream) {
+    return guard([&] { rl::rmsnorm_pack(x, ld_x, gamma, y, frag, n, T, eps, S(stream)); });
+}
+
+int rl_hip_gated_rmsnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, int gamma_n, float* y,
+                              void* frag, int n, int T, float eps, void* stream) {
+    return guard([&] { rl::gnorm_pack(o, z, ld_z, gamma, gamma_n, y, frag, n, T, eps, S(stream)); });
+}
+
+int rl_hip_embed_rows(const void* table, int kind, const int* tokens, float* out, int H, int vocab, int T,
+                      void* stream) {
+    return guard([&] { rl::embed_rows(table, kind, tokens, out, H, vocab, T, S(stream)); });
+}
+
+}  // extern "C"

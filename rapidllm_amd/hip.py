@@ -54,6 +54,17 @@ _SIGS = {
     "rl_hip_pack_kquant": (_i, [_i, _vp, _vp, _i, _i, _vp]),
     "rl_hip_gemm_kquant": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "rl_hip_dequant_kquant": (_i, [_i, _vp, _vp, _sz, _vp]),
+    "rl_hip_gdn_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
+                               _i, _vp]),
+    "rl_hip_rmsnorm_pack": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, C.c_float, _vp]),
+    "rl_hip_gated_rmsnorm_pack": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, C.c_float, _vp]),
+    "rl_hip_embed_rows": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),
+    "rl_hip_attn_workspace_bytes": (_sz, [_i, _i]),
+    "rl_hip_attn_decode_layer": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, C.c_float, C.c_float,
+                                      _vp, _sz, _vp, _vp, _vp]),
+    "rl_hip_argmax_workspace_bytes": (_sz, [_i, _i]),
+    "rl_hip_argmax_rows": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
+    "rl_hip_accept_prefix": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp]),
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
     "rl_hip_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),

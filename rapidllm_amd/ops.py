@@ -166,3 +166,138 @@ def dequant_q4_k(packed: np.ndarray, n: int) -> np.ndarray:
 def dequant_q6_k(packed: np.ndarray, n: int) -> np.ndarray:
     """ops::dequant_q6_k(packed, out, n) (reference src/kernels/ops.cpp:357)."""
     return _dequant(Q6_K, packed, n)
+
+
+# ------------------------------------------------------------------ norms
+
+
+def qwen3_rmsnorm(x: np.ndarray, gamma, eps: float = 1e-6) -> np.ndarray:
+    """ops::qwen3_rmsnorm over each row of x [T][n] (reference ops.cpp:107)."""
+    x = _f32(np.atleast_2d(x))
+    T, n = x.shape
+    xd = DeviceBuffer.from_numpy(x)
+    gd = DeviceBuffer.from_numpy(_f32(gamma)) if gamma is not None else None
+    yd = DeviceBuffer(x.nbytes)
+    call("rl_hip_rmsnorm_pack", xd.ptr, n, gd.ptr if gd else None, yd.ptr, None, n, T, eps, None)
+    return yd.numpy(np.float32, (T, n))
+
+
+def gated_rmsnorm(o: np.ndarray, z: np.ndarray, gamma, eps: float = 1e-6, gamma_n: int = 0) -> np.ndarray:
+    """ops::gated_rmsnorm over each row (reference ops.cpp:129)."""
+    o = _f32(np.atleast_2d(o))
+    z = _f32(np.atleast_2d(z))
+    T, n = o.shape
+    od, zd, yd = DeviceBuffer.from_numpy(o), DeviceBuffer.from_numpy(z), DeviceBuffer(o.nbytes)
+    gd = DeviceBuffer.from_numpy(_f32(gamma)) if gamma is not None else None
+    call("rl_hip_gated_rmsnorm_pack", od.ptr, zd.ptr, n, gd.ptr if gd else None, gamma_n, yd.ptr, None, n, T, eps,
+         None)
+    return yd.numpy(np.float32, (T, n))
+
+
+# ------------------------------------------------------------------ DeltaNet
+
+
+def gdn_decode(qkv, a, b, A_log, dt_bias, conv_w, conv_state, S, nk, nv, v_tiled=False):
+    """T-token Gated DeltaNet decode (conv1d_update + gates + delta_recurrent_step,
+    reference ops.cpp:458-534, ops_fused.cpp:105-130).  S in the reference layout
+    [nv][dk][dv]; returns (o [T][nv*dv], S', conv_state')."""
+    qkv = _f32(np.atleast_2d(qkv))
+    T, conv_dim = qkv.shape
+    nv_, dk, dv = S.shape
+    assert nv_ == nv
+    St = np.ascontiguousarray(np.transpose(S, (0, 2, 1)), np.float32)
+    d_qkv = DeviceBuffer.from_numpy(qkv)
+    d_A = DeviceBuffer.from_numpy(_f32(A_log))
+    d_dt = DeviceBuffer.from_numpy(_f32(dt_bias))
+    d_w = DeviceBuffer.from_numpy(_f32(conv_w))
+    d_cin = DeviceBuffer.from_numpy(_f32(conv_state))
+    d_cout = DeviceBuffer(d_cin.nbytes)
+    d_S = DeviceBuffer.from_numpy(St)
+    d_o = DeviceBuffer(4 * T * nv * dv)
+    # a and b arrive as their own [T][nv] arrays here: row stride differs from qkv
+    # (the engine passes one fused buffer); use a packed copy with a common stride.
+    ld = conv_dim + 2 * nv
+    fused = np.zeros((T, ld), np.float32)
+    fused[:, :conv_dim] = qkv
+    fused[:, conv_dim:conv_dim + nv] = np.atleast_2d(a)
+    fused[:, conv_dim + nv:] = np.atleast_2d(b)
+    d_f = DeviceBuffer.from_numpy(fused)
+    call("rl_hip_gdn_decode", d_f.ptr, d_f.ptr + 4 * conv_dim, d_f.ptr + 4 * (conv_dim + nv), ld, d_A.ptr, d_dt.ptr,
+         d_w.ptr, d_cin.ptr, d_cout.ptr, d_S.ptr, d_S.ptr, d_o.ptr, T, nk, nv, dk, dv, conv_w.shape[1],
+         1 if v_tiled else 0, None)
+    o = d_o.numpy(np.float32, (T, nv * dv))
+    S_new = np.transpose(d_S.numpy(np.float32, (nv, dv, dk)), (0, 2, 1)).copy()
+    conv_new = d_cout.numpy(np.float32, conv_state.shape)
+    return o, S_new, conv_new
+
+
+# ------------------------------------------------------------------ attention
+
+
+class AttnCache:
+    """fp16 K [n_kv][ctx][hd] and transposed V [n_kv][hd][ctx] caches in HBM."""
+
+    def __init__(self, n_kv: int, ctx: int, hd: int = 256):
+        assert ctx % 256 == 0
+        self.n_kv, self.ctx, self.hd = n_kv, ctx, hd
+        self.k = DeviceBuffer(2 * n_kv * ctx * hd)
+        self.vt = DeviceBuffer(2 * n_kv * ctx * hd)
+        self.k.zero()
+        self.vt.zero()
+        call("rl_hip_device_synchronize")
+
+    def fill(self, K: np.ndarray, V: np.ndarray):
+        """K, V: [pos][n_kv][hd] float values (rounded to fp16 here)."""
+        L = K.shape[0]
+        kc = np.zeros((self.n_kv, self.ctx, self.hd), np.float16)
+        vt = np.zeros((self.n_kv, self.hd, self.ctx), np.float16)
+        kc[:, :L, :] = np.transpose(K, (1, 0, 2)).astype(np.float16)
+        vt[:, :, :L] = np.transpose(V, (1, 2, 0)).astype(np.float16)
+        self.k.upload(kc)
+        self.vt.upload(vt)
+
+
+def attn_decode_layer(Y, cache: AttnCache, pos: int, q_norm, k_norm, n_q, n_kv, rotary_dim=64, theta=1e7,
+                      eps=1e-6):
+    """Gated attention for T tokens at positions pos..pos+T-1 from the fused
+    projection rows Y [T][2*n_q*hd + 2*n_kv*hd]; returns o*sigmoid(gate) [T][n_q*hd]."""
+    Y = _f32(np.atleast_2d(Y))
+    T, ld = Y.shape
+    hd = cache.hd
+    d_Y = DeviceBuffer.from_numpy(Y)
+    d_qn = DeviceBuffer.from_numpy(_f32(q_norm))
+    d_kn = DeviceBuffer.from_numpy(_f32(k_norm))
+    d_pos = DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    ws = DeviceBuffer(hip.lib().rl_hip_attn_workspace_bytes(n_kv, cache.ctx))
+    ws.zero()
+    d_out = DeviceBuffer(4 * T * n_q * hd)
+    call("rl_hip_attn_decode_layer", d_Y.ptr, ld, d_qn.ptr, d_kn.ptr, cache.k.ptr, cache.vt.ptr, cache.ctx, d_pos.ptr,
+         T, n_q, n_kv, hd, rotary_dim, theta, eps, ws.ptr, ws.nbytes, d_out.ptr, None, None)
+    return d_out.numpy(np.float32, (T, n_q * hd))
+
+
+# ------------------------------------------------------------------ sampling
+
+
+def argmax_rows(logits: np.ndarray):
+    """greedy_sample per row (reference sampler.cpp:8): (indices, values)."""
+    logits = _f32(np.atleast_2d(logits))
+    rows, V = logits.shape
+    d_l = DeviceBuffer.from_numpy(logits)
+    d_i = DeviceBuffer(4 * rows)
+    d_v = DeviceBuffer(4 * rows)
+    ws = DeviceBuffer(hip.lib().rl_hip_argmax_workspace_bytes(rows, V))
+    call("rl_hip_argmax_rows", d_l.ptr, rows, V, d_i.ptr, d_v.ptr, ws.ptr, None)
+    return d_i.numpy(np.int32, (rows,)), d_v.numpy(np.float32, (rows,))
+
+
+def accept_prefix(toks, preds, pos: int):
+    """Device greedy acceptance: returns (n_consumed, new_pos, next_token)."""
+    toks = np.ascontiguousarray(toks, np.int32)
+    preds = np.ascontiguousarray(preds, np.int32)
+    d_t, d_p = DeviceBuffer.from_numpy(toks), DeviceBuffer.from_numpy(preds)
+    d_pos = DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    d_n, d_nx = DeviceBuffer(4), DeviceBuffer(4)
+    call("rl_hip_accept_prefix", d_t.ptr, d_p.ptr, toks.size, d_pos.ptr, d_n.ptr, d_nx.ptr, None)
+    return (int(d_n.numpy(np.int32, (1,))[0]), int(d_pos.numpy(np.int32, (1,))[0]),
+            int(d_nx.numpy(np.int32, (1,))[0]))
