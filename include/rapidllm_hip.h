@@ -187,6 +187,46 @@ int rl_hip_argmax_rows(const float* logits, int rows, int vocab, int* out_idx, f
 int rl_hip_accept_prefix(const int* toks, const int* preds, int T, int* pos, int* n_consumed, int* next_tok,
                          void* stream);
 
+/* ---- decode engine ----------------------------------------------------------
+ * Replaces: cuda_gen::Engine (include/rapidllm/runtime/cuda_engine.h:13-83) and its
+ * CUDA implementation's decode / verify / MTP paths (src/kernels/cuda/cuda_engine.cu:
+ * 17053-17733 spec_verify, 18613-18997 launch_spec_chunk / launch_decode,
+ * 15266-16300 MTP).  Numerics follow the reference CPU Session
+ * (src/runtime/session.cpp:325-411, 531-559, 619-681, 799-829).
+ * Weights: the reference IR names (see rl_model.h).  Linears may be
+ * FP8_E4M3_B128, BF16, Q4_K or Q6_K; norms / A_log / dt_bias / conv1d F32;
+ * embed F32 / F16 / BF16.  Tensor data is copied during create; the caller may free
+ * it afterwards.  Limits: hidden % 128 == 0, DeltaNet k_dim 128 and v_dim % 32 == 0,
+ * conv width 4, attention head_dim 256, (n_q/n_kv)*max_T <= 32, max_T <= 4.
+ * The engine owns one HIP stream; calls on one engine must not overlap. */
+typedef struct RlEngine RlEngine;
+RlEngine* rl_hip_engine_create(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx, int max_T,
+                               int* status);
+/* Random-init weights of cfg's architecture generated on the device (benchmark). */
+RlEngine* rl_hip_engine_create_synthetic(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T, int* status);
+void rl_hip_engine_destroy(RlEngine* e);
+int rl_hip_engine_reset(RlEngine* e);
+int rl_hip_engine_prefill(RlEngine* e, const int32_t* ids, int n);                    /* cuda_engine.h:18 */
+int rl_hip_engine_decode_token(RlEngine* e, int32_t token);                           /* :21 */
+int rl_hip_engine_decode_steps(RlEngine* e, int n);                                   /* :24 */
+int rl_hip_engine_copy_gen_tokens(RlEngine* e, int32_t* host, int n);                 /* :27 */
+int rl_hip_engine_copy_logits(RlEngine* e, float* host);                              /* :31 */
+int rl_hip_engine_copy_last_hidden(RlEngine* e, float* host);                         /* :33 */
+int rl_hip_engine_mtp_draft(RlEngine* e, int32_t first, int n, int32_t* out, int* n_out); /* :36 */
+int rl_hip_engine_spec_verify(RlEngine* e, const int32_t* toks, int T, int32_t* preds, int* n_consumed); /* :72 */
+/* MTP stem draft of T-1 tokens after t0 and the T-token verify, one submission (:40). */
+int rl_hip_engine_mtp_spec(RlEngine* e, int32_t t0, int T, int32_t* toks_out, int32_t* preds, int* n_consumed);
+int rl_hip_engine_greedy(RlEngine* e, int32_t* tok);                                  /* :41 */
+int rl_hip_engine_pos(RlEngine* e, int* pos);                                         /* :42 */
+int rl_hip_engine_info(RlEngine* e, int* vocab, int* hidden, int* ctx_capacity, size_t* device_bytes);
+/* Benchmark support: set the position, or fill the KV cache rows [0, n) with fp16
+ * N(0,1) and the recurrent states with random values, then set pos = n; time
+ * `iters` graph replays of the T-token step (mtp_drafts > 0: of the MTP draft). */
+int rl_hip_engine_set_pos(RlEngine* e, int pos);
+int rl_hip_engine_synthetic_context(RlEngine* e, int n, uint64_t seed);
+int rl_hip_engine_time_steps(RlEngine* e, int T, int iters, int mtp_drafts, float* ms);
+void* rl_hip_engine_stream(RlEngine* e);
+
 /* ---- bandwidth calibration ------------------------------------------------
  * No counterpart in the reference.  A streaming copy / read of `bytes` (multiple of
  * 16) that measures the achievable HBM rate and calibrates rocprof's FETCH_SIZE /

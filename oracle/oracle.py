@@ -250,3 +250,51 @@ def f16_round(a):
     a = f32(a)
     L = lib()
     return np.array([L.orc_fp16_to_f32(L.orc_f32_to_fp16(float(v))) for v in a.ravel()], np.float32).reshape(a.shape)
+
+
+class OracleModel:
+    """CPU decode model (oracle.cpp Model): Session's fused one-token path with
+    DualCache layouts.  kv_fp16 rounds cached K/V to fp16 like the device cache."""
+
+    def __init__(self, spec, weights, ctx=4096, kv_fp16=True, threads=8):
+        self.spec = spec
+        self._cfg = spec.c_config()
+        arr, n = weights.c_array()
+        self._weights = weights
+        self.h = lib().orc_model_create(C.byref(self._cfg), arr, n, ctx, 1 if kv_fp16 else 0, threads)
+        if not self.h:
+            raise RuntimeError("orc_model_create failed")
+
+    def __del__(self):
+        try:
+            if self.h:
+                lib().orc_model_free(self.h)
+        except Exception:
+            pass
+
+    def reset(self):
+        lib().orc_model_reset(self.h)
+
+    def decode(self, token):
+        """One token; returns (greedy, logits, hidden)."""
+        lg = np.empty(self.spec.vocab, np.float32)
+        hd = np.empty(self.spec.hidden, np.float32)
+        g = lib().orc_model_decode(self.h, int(token), P(lg), P(hd))
+        if g < 0:
+            raise RuntimeError("oracle decode failed")
+        return g, lg, hd
+
+    def mtp_draft(self, first, n):
+        out = np.zeros(n, np.int32)
+        k = lib().orc_model_mtp_draft(self.h, int(first), n, out.ctypes.data_as(_i32))
+        return out[:k]
+
+    def generate(self, prompt, max_new, spec_n=0):
+        prompt = np.ascontiguousarray(prompt, np.int32)
+        out = np.zeros(max_new, np.int32)
+        prop, acc = C.c_int(), C.c_int()
+        k = lib().orc_model_generate(self.h, prompt.ctypes.data_as(_i32), prompt.size, max_new, spec_n,
+                                     out.ctypes.data_as(_i32), C.byref(prop), C.byref(acc))
+        if k < 0:
+            raise RuntimeError("oracle generate failed")
+        return out[:k].tolist(), prop.value, acc.value

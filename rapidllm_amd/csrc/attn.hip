@@ -23,7 +23,7 @@
 //              sigmoid(gate) and writes fp32 and/or the o_proj GEMM fragments.
 //
 // Cache layouts: K [n_kv][ctx][hd] fp16;  V^T [n_kv][hd][ctx] fp16;  ctx % 256 == 0.
-#include "common.h"
+#include "internal.h"
 
 using namespace rl;
 

@@ -1,0 +1,1001 @@
+// engine.hip -- the MI355X decode engine: one forward step over T = 1..Tmax tokens of
+// the Qwen3.6/3.8-27B hybrid stack, the MTP stem draft, greedy acceptance and
+// speculative verify, captured as HIP graphs.
+//
+// It implements the surface of the reference's GPU engine seam, cuda_gen::Engine
+// (include/rapidllm/runtime/cuda_engine.h:13-83): prefill, decode_token,
+// decode_steps (self-feeding), copy_gen_tokens, copy_logits, copy_last_hidden,
+// mtp_draft, spec_verify, greedy, pos, vocab, hidden; plus mtp_spec (draft + verify
+// in one submission, the role of mtp_spec4, cuda_engine.h:40).  Numerics follow the
+// reference CPU session (src/runtime/session.cpp:325-411, 531-559, 619-681,
+// 799-829): the oracle for every parity test.
+//
+// Per step (T tokens), per layer:
+//   rmsnorm_pack -> fused in_proj GEMM [qkv;z;a;b] -> gdn_decode -> gnorm_pack ->
+//   out_proj GEMM (+= residual)                                   (DeltaNet layer)
+//   rmsnorm_pack -> fused [q|gate;k;v] GEMM -> attention (qk_prep, chunk partials,
+//   combine+gate+pack) -> o_proj GEMM (+= residual)              (attention layer)
+//   rmsnorm_pack -> interleaved gate/up GEMM with SwiGLU epilogue -> pack ->
+//   down GEMM (+= residual)                                       (MLP)
+// then final norm -> lm_head -> argmax -> accept.  Every dynamic quantity (token
+// ids, position, recurrent-state slot) lives in device memory, so a step is a fixed
+// launch sequence and is captured once per T.
+//
+// Speculative rollback: recurrent states (S and the conv window) live in rings of
+// R = Tmax + 1 slots; the DeltaNet kernel writes the state after every token of a
+// verify step to its own slot and acceptance just advances the slot index by the
+// number of tokens kept.  KV rows of rejected tokens are overwritten later and are
+// never read (attention masks positions past each query).
+#include <cstring>
+#include <map>
+#include <memory>
+#include <string>
+#include <vector>
+
+#include "internal.h"
+
+using namespace rl;
+
+namespace rl {
+
+namespace {
+
+inline int align16(int v) { return (v + 15) / 16 * 16; }
+
+struct DevAlloc {
+    std::vector<void*> ptrs;
+    size_t total = 0;
+    void* get(size_t bytes) {
+        void* p = nullptr;
+        hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
+        if (e == hipErrorOutOfMemory) throw Error(RL_ERR_NOMEM, "engine: out of device memory");
+        RL_HIP(e);
+        RL_HIP(hipMemset(p, 0, bytes ? bytes : 256));
+        ptrs.push_back(p);
+        total += bytes;
+        return p;
+    }
+    template <class T>
+    T* get_n(size_t n) {
+        return static_cast<T*>(get(n * sizeof(T)));
+    }
+    ~DevAlloc() {
+        for (void* p : ptrs) (void)hipFree(p);
+    }
+};
+
+// A linear on the device.  FP8 / BF16: MFMA-tiled (16-row tiles), possibly several
+// source matrices fused along rows.  Q4_K / Q6_K: K-tiled, one matrix.
+struct Lin {
+    int kind = -1;
+    int m = 0;  // rows of the device weight (FP8/BF16: padded to 16-row tiles)
+    int n = 0;
+    uint8_t* w = nullptr;
+    float* ts = nullptr;
+};
+
+struct Layer {
+    int kind = RL_LAYER_DELTA;
+    const float* attn_norm = nullptr;
+    const float* ffn_norm = nullptr;
+    // DeltaNet
+    std::vector<Lin> in_parts;  // fused [qkv|z|a|b] (one Lin) or separate K-quant parts
+    std::vector<int> in_offs;   // output column offset of each part
+    int in_width = 0, off_z = 0, off_a = 0, off_b = 0;
+    Lin out_proj;
+    const float *A_log = nullptr, *dt_bias = nullptr, *conv_w = nullptr, *gnorm = nullptr;
+    int gnorm_n = 0;
+    int dslot = 0;  // index among DeltaNet layers
+    // attention
+    std::vector<Lin> qkv_parts;
+    std::vector<int> qkv_offs;
+    int qkv_width = 0;
+    Lin o_proj;
+    const float *q_norm = nullptr, *k_norm = nullptr;
+    int aslot = 0;
+    // MLP
+    Lin gate_up;  // FP8/BF16: interleaved gate/up tiles, SwiGLU epilogue
+    Lin gate, up; // K-quant: separate
+    Lin down;
+};
+
+}  // namespace
+
+class Engine {
+   public:
+    Engine(const RlModelConfig& cfg, int ctx, int tmax) : c_(cfg), tmax_(tmax) {
+        RL_REQUIRE(tmax >= 1 && tmax <= 4, RL_ERR_RANGE, "engine: max_T must be in 1..4");
+        RL_REQUIRE(c_.n_layers >= 1 && c_.n_layers <= RL_MAX_LAYERS, RL_ERR_RANGE, "engine: bad layer count");
+        RL_REQUIRE(c_.hidden % 128 == 0, RL_ERR_UNSUPPORTED, "engine: hidden must be a multiple of 128");
+        RL_REQUIRE(c_.k_dim == 128 && c_.v_dim % 32 == 0, RL_ERR_UNSUPPORTED, "engine: DeltaNet dims 128 / 32k");
+        RL_REQUIRE(c_.conv_k == 4, RL_ERR_UNSUPPORTED, "engine: conv width must be 4");
+        RL_REQUIRE(c_.head_dim == 256, RL_ERR_UNSUPPORTED, "engine: attention head_dim must be 256");
+        RL_REQUIRE(c_.n_kv > 0 && c_.n_q % c_.n_kv == 0 && (c_.n_q / c_.n_kv) * tmax <= 32, RL_ERR_UNSUPPORTED,
+                   "engine: (n_q/n_kv) * max_T must be <= 32");
+        ctx_ = (ctx + 255) / 256 * 256 + 256;  // room for a verify chunk past the last position
+        R_ = tmax + 1;
+        RL_HIP(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
+    }
+
+    ~Engine() {
+        for (auto& g : graphs_)
+            if (g.second) (void)hipGraphExecDestroy(g.second);
+        if (st_) (void)hipStreamDestroy(st_);
+        if (host_rb_) (void)hipHostFree(host_rb_);
+    }
+
+    // ------------------------------------------------------------ weights
+    void load(const RlTensor* t, int n) {
+        for (int i = 0; i < n; ++i) tab_[t[i].name] = &t[i];
+        build([&](const std::string& name) -> const RlTensor* {
+            auto it = tab_.find(name);
+            return it == tab_.end() ? nullptr : it->second;
+        });
+    }
+
+    // Synthetic random-init weights of the configured architecture, generated on the
+    // device (benchmark configs: e4m3 bytes uniform without NaN codes, 128x128 fp32
+    // scales log-uniform in [1e-3, 1e-1], bf16 embedding / lm_head, small norms).
+    void load_synthetic(uint64_t seed) {
+        synth_seed_ = seed;
+        synthetic_ = true;
+        build([&](const std::string&) -> const RlTensor* { return nullptr; });
+    }
+
+    // ------------------------------------------------------------ API
+    int vocab() const { return c_.vocab; }
+    int hidden() const { return c_.hidden; }
+    int ctx_capacity() const { return ctx_ - 256; }
+    int max_t() const { return tmax_; }
+    size_t device_bytes() const { return mem_.total; }
+
+    void reset() {
+        sync_graph_state();
+        RL_HIP(hipMemsetAsync(scal_, 0, kScalars * sizeof(int), st_));
+        for (size_t l = 0; l < S_.size(); ++l) {
+            RL_HIP(hipMemsetAsync(S_[l], 0, s_slot_ * sizeof(float), st_));
+            RL_HIP(hipMemsetAsync(conv_[l], 0, conv_slot_ * sizeof(float), st_));
+        }
+        RL_HIP(hipMemsetAsync(h_last_, 0, c_.hidden * sizeof(float), st_));
+        RL_HIP(hipMemsetAsync(h_prev_, 0, c_.hidden * sizeof(float), st_));
+        RL_HIP(hipStreamSynchronize(st_));
+        pos_ = 0;
+        greedy_ = 0;
+        n_last_ = 0;
+    }
+
+    void prefill(const int32_t* ids, int n) {
+        RL_REQUIRE(n >= 1 && ids, RL_ERR_RANGE, "prefill: empty prompt");
+        RL_REQUIRE(n <= ctx_capacity(), RL_ERR_RANGE, "prefill: prompt longer than the context");
+        check_ids(ids, n);
+        reset();
+        for (int i = 0; i < n; i += tmax_) {
+            const int T = std::min(tmax_, n - i);
+            RL_HIP(hipMemcpyAsync(tok_, ids + i, T * sizeof(int), hipMemcpyHostToDevice, st_));
+            step(T, /*force_all=*/1, /*feed=*/false);
+        }
+        readback();
+    }
+
+    void decode_token(int32_t token) {
+        check_ids(&token, 1);
+        RL_REQUIRE(pos_ + 1 <= ctx_capacity(), RL_ERR_RANGE, "decode: context full");
+        RL_HIP(hipMemcpyAsync(scal_ + kNextTok, &token, sizeof(int), hipMemcpyHostToDevice, st_));
+        run_graph(1);
+        readback();
+    }
+
+    // n self-fed T=1 steps, one host sync at the end (cuda_engine.h:22-26).
+    void decode_steps(int n) {
+        RL_REQUIRE(n >= 0, RL_ERR_RANGE, "decode_steps: n < 0");
+        RL_REQUIRE(pos_ + n <= ctx_capacity(), RL_ERR_RANGE, "decode_steps: context full");
+        RL_HIP(hipMemsetAsync(scal_ + kGenCount, 0, sizeof(int), st_));
+        for (int i = 0; i < n; ++i) run_graph(1);
+        readback();
+    }
+
+    void copy_gen_tokens(int32_t* host, int n) {
+        RL_REQUIRE(n >= 0 && n <= kGenCap, RL_ERR_RANGE, "copy_gen_tokens: n out of range");
+        RL_HIP(hipMemcpyAsync(host, gen_, n * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+
+    // logits of the last consumed token
+    void copy_logits(float* host) {
+        const int row = n_last_ > 0 ? n_last_ - 1 : 0;
+        RL_HIP(hipMemcpyAsync(host, logits_ + static_cast<size_t>(row) * c_.vocab, c_.vocab * sizeof(float),
+                              hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+
+    void copy_last_hidden(float* host) {
+        RL_HIP(hipMemcpyAsync(host, h_last_, c_.hidden * sizeof(float), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+
+    // Stem draft after the last consumed token (session.cpp:619-681).
+    int mtp_draft(int32_t first, int n, int32_t* out) {
+        if (!has_mtp_ || n <= 0) return 0;
+        RL_REQUIRE(n <= 7, RL_ERR_RANGE, "mtp_draft: at most 7 drafts");
+        check_ids(&first, 1);
+        RL_HIP(hipMemcpyAsync(scal_ + kNextTok, &first, sizeof(int), hipMemcpyHostToDevice, st_));
+        run_mtp(n);
+        RL_HIP(hipMemcpyAsync(out, tok_ + 1, n * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+        return n;
+    }
+
+    // Verify toks[0..T) in one weight pass (cuda_engine.h:69-77).  Returns n consumed.
+    int spec_verify(const int32_t* toks, int T, int32_t* preds) {
+        RL_REQUIRE(T >= 1 && T <= tmax_ && toks, RL_ERR_RANGE, "spec_verify: T out of range");
+        RL_REQUIRE(pos_ + T <= ctx_capacity(), RL_ERR_RANGE, "spec_verify: context full");
+        check_ids(toks, T);
+        if (T == 1)  // the T = 1 step feeds the device's next token
+            RL_HIP(hipMemcpyAsync(scal_ + kNextTok, toks, sizeof(int), hipMemcpyHostToDevice, st_));
+        else
+            RL_HIP(hipMemcpyAsync(tok_, toks, T * sizeof(int), hipMemcpyHostToDevice, st_));
+        run_graph(T, /*from_host=*/true);
+        readback();
+        if (preds) std::memcpy(preds, host_rb_ + kRbPreds, T * sizeof(int));
+        return n_last_;
+    }
+
+    // MTP draft of T-1 tokens after t0, then verify [t0, drafts] at T, one sync.
+    int mtp_spec(int32_t t0, int T, int32_t* toks_out, int32_t* preds) {
+        RL_REQUIRE(has_mtp_, RL_ERR_UNSUPPORTED, "mtp_spec: model has no MTP head");
+        RL_REQUIRE(T >= 2 && T <= tmax_, RL_ERR_RANGE, "mtp_spec: T out of range");
+        RL_REQUIRE(pos_ + T <= ctx_capacity(), RL_ERR_RANGE, "mtp_spec: context full");
+        check_ids(&t0, 1);
+        RL_HIP(hipMemcpyAsync(scal_ + kNextTok, &t0, sizeof(int), hipMemcpyHostToDevice, st_));
+        run_mtp(T - 1);
+        run_graph(T, /*from_host=*/true);
+        readback();
+        if (toks_out) std::memcpy(toks_out, host_rb_ + kRbToks, T * sizeof(int));
+        if (preds) std::memcpy(preds, host_rb_ + kRbPreds, T * sizeof(int));
+        return n_last_;
+    }
+
+    int32_t greedy() const { return greedy_; }
+    int pos() const { return pos_; }
+
+    // Benchmark support: claim `pos` positions of context as already filled (the KV
+    // rows below pos are whatever the cache holds: zeros or synthetic values).
+    void set_pos(int pos) {
+        RL_REQUIRE(pos >= 0 && pos <= ctx_capacity(), RL_ERR_RANGE, "set_pos: out of range");
+        RL_HIP(hipMemcpyAsync(scal_ + kPos, &pos, sizeof(int), hipMemcpyHostToDevice, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+        pos_ = pos;
+    }
+
+    // Fill KV rows [0, n) with fp16 N(0,1) and recurrent states with their benchmark
+    // distributions (S ~ N(0, 0.02), conv window ~ N(0,1)), then set pos = n.
+    void synthetic_context(int n, uint64_t seed) {
+        RL_REQUIRE(n >= 0 && n <= ctx_capacity(), RL_ERR_RANGE, "synthetic_context: out of range");
+        reset();
+        const size_t kv = static_cast<size_t>(c_.n_kv) * ctx_ * c_.head_dim;
+        for (size_t l = 0; l < kc_.size(); ++l) {
+            fill_normal_f16(kc_[l], kv, 1.f, seed + 11 * l + 1, st_);
+            fill_normal_f16(vt_[l], kv, 1.f, seed + 11 * l + 2, st_);
+        }
+        for (size_t l = 0; l < S_.size(); ++l) {
+            fill_normal_f32(S_[l], s_slot_, 0.f, 0.02f, seed + 13 * l + 3, st_);
+            fill_normal_f32(conv_[l], conv_slot_, 0.f, 1.f, seed + 13 * l + 4, st_);
+        }
+        RL_HIP(hipStreamSynchronize(st_));
+        set_pos(n);
+    }
+
+    // Time `iters` replays of the T-token step graph (or of the MTP draft graph when
+    // mtp_drafts > 0) with events on the engine stream; state advances as in decode.
+    float time_steps(int T, int iters, int mtp_drafts) {
+        hipEvent_t a, b;
+        RL_HIP(hipEventCreate(&a));
+        RL_HIP(hipEventCreate(&b));
+        RL_HIP(hipEventRecord(a, st_));
+        for (int i = 0; i < iters; ++i) {
+            if (mtp_drafts > 0)
+                run_mtp(mtp_drafts);
+            else
+                run_graph(T, /*from_host=*/T > 1);
+        }
+        RL_HIP(hipEventRecord(b, st_));
+        RL_HIP(hipEventSynchronize(b));
+        float ms = 0.f;
+        RL_HIP(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        readback();
+        return ms;
+    }
+
+    void* stream() const { return st_; }
+
+   private:
+    // device scalar block
+    enum { kPos = 0, kSlot = 1, kNCons = 2, kNextTok = 3, kGenCount = 4, kScalars = 8 };
+    // host readback block (ints): scalars, then preds, then toks
+    enum { kRbPreds = 8, kRbToks = 16, kRbInts = 24 };
+    static constexpr int kGenCap = 4096;
+
+    RlModelConfig c_;
+    int ctx_ = 0, tmax_ = 4, R_ = 5;
+    hipStream_t st_ = nullptr;
+    DevAlloc mem_;
+    std::map<std::string, const RlTensor*> tab_;
+    bool synthetic_ = false;
+    uint64_t synth_seed_ = 0;
+    uint64_t synth_ctr_ = 0;
+
+    std::vector<Layer> L_;
+    const void* embed_ = nullptr;
+    int embed_kind_ = RL_Q_BF16;
+    Lin lm_head_;
+    const float* final_norm_ = nullptr;
+    bool has_mtp_ = false;
+    Lin mtp_fc_;
+    const float *mtp_nh_ = nullptr, *mtp_ne_ = nullptr, *mtp_norm_ = nullptr;
+
+    // states
+    std::vector<float*> S_, conv_;
+    size_t s_slot_ = 0, conv_slot_ = 0;
+    std::vector<uint16_t*> kc_, vt_;
+    // activations / workspaces
+    int* scal_ = nullptr;
+    int* tok_ = nullptr;    // [Tmax]
+    int* preds_ = nullptr;  // [Tmax]
+    int* gen_ = nullptr;    // [kGenCap]
+    float* x_ = nullptr;    // [Tmax][H] residual stream
+    float* xn_ = nullptr;   // [Tmax][max_in] fp32 copy of the packed activation
+    void* frag_ = nullptr;  // GEMM fragments
+    float* ybuf_ = nullptr; // [Tmax][max_width] fused projection outputs
+    float* o_ = nullptr;    // [Tmax][zdim]
+    float* h_ = nullptr;    // [Tmax][I]
+    float* g_ = nullptr;    // [Tmax][I] (K-quant MLP)
+    float* u_ = nullptr;
+    float* logits_ = nullptr;
+    float* mtp_logits_ = nullptr;  // [V] (keeps the verify logits intact)
+    float* mtp_e_ = nullptr;   // [H]
+    float* mtp_cat_ = nullptr; // [2H]
+    float* mtp_hp_ = nullptr;  // [H]
+    float* h_last_ = nullptr;
+    float* h_prev_ = nullptr;
+    void* attn_ws_ = nullptr;
+    size_t attn_ws_bytes_ = 0;
+    void* arg_ws_ = nullptr;
+    void* kq_ws_ = nullptr;
+    size_t kq_ws_bytes_ = 0;
+    size_t kq_need_ = 0;  // largest K-quant workspace over the loaded linears
+    int max_in_ = 0;
+
+    std::map<int, hipGraphExec_t> graphs_;  // key: T (1..Tmax), 100 + n for MTP drafts
+    int* host_rb_ = nullptr;
+    int pos_ = 0, n_last_ = 0;
+    int32_t greedy_ = 0;
+
+    // ---------------------------------------------------------------- build
+    template <class Find>
+    void build(Find find) {
+        const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dk = c_.k_dim, dv = c_.v_dim;
+        const int conv_dim = 2 * nk * dk + nv * dv, zdim = nv * dv;
+        const int nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim;
+        int I = c_.intermediate;
+
+        // embedding / head / final norm
+        if (synthetic_) {
+            embed_kind_ = RL_Q_BF16;
+            uint16_t* e = mem_.get_n<uint16_t>(static_cast<size_t>(c_.vocab) * H);
+            fill_normal_bf16(e, static_cast<size_t>(c_.vocab) * H, 0.02f, next_seed(), st_);
+            embed_ = e;
+            lm_head_ = synth_lin(RL_Q_BF16, c_.vocab, H);
+            final_norm_ = synth_vec(H, 0.f, 0.1f);
+        } else {
+            const RlTensor* e = need(find, "embed");
+            RL_REQUIRE(e->quant == RL_Q_F32 || e->quant == RL_Q_F16 || e->quant == RL_Q_BF16, RL_ERR_UNSUPPORTED,
+                       "embed must be F32, F16 or BF16");
+            RL_REQUIRE(e->rows == c_.vocab && e->cols == H, RL_ERR_FORMAT, "embed shape");
+            embed_kind_ = e->quant;
+            const size_t eb = static_cast<size_t>(c_.vocab) * H * (e->quant == RL_Q_F32 ? 4 : 2);
+            void* ed = mem_.get(eb);
+            RL_HIP(hipMemcpyAsync(ed, e->data, eb, hipMemcpyHostToDevice, st_));
+            embed_ = ed;
+            lm_head_ = upload_lin({need(find, "lm_head")}, c_.vocab, H);
+            final_norm_ = upload_vec(need(find, "final_norm"), H);
+        }
+
+        int nd = 0, na = 0;
+        L_.resize(c_.n_layers);
+        int max_width = 0;
+        for (int i = 0; i < c_.n_layers; ++i) {
+            Layer& Ly = L_[i];
+            const std::string p = "layers[" + std::to_string(i) + "].";
+            Ly.kind = c_.layer_kind[i];
+            Ly.attn_norm = synthetic_ ? synth_vec(H, 0.f, 0.1f) : upload_vec(need(find, p + "attn_norm"), H);
+            Ly.ffn_norm = synthetic_ ? synth_vec(H, 0.f, 0.1f) : upload_vec(need(find, p + "ffn_norm"), H);
+            if (Ly.kind == RL_LAYER_DELTA) {
+                Ly.dslot = nd++;
+                Ly.off_z = align16(conv_dim);
+                Ly.off_a = Ly.off_z + align16(zdim);
+                Ly.off_b = Ly.off_a + align16(nv);
+                Ly.in_width = Ly.off_b + align16(nv);
+                const std::vector<std::string> names = {p + "delta.gemm.in_proj_qkv", p + "delta.gemm.in_proj_z",
+                                                        p + "delta.leftover.in_proj_a",
+                                                        p + "delta.leftover.in_proj_b"};
+                const std::vector<int> rows = {conv_dim, zdim, nv, nv};
+                const std::vector<int> offs = {0, Ly.off_z, Ly.off_a, Ly.off_b};
+                make_fused(find, names, rows, offs, H, Ly.in_parts, Ly.in_offs);
+                Ly.out_proj = synthetic_ ? synth_lin(RL_Q_FP8_E4M3_B128, H, zdim)
+                                         : upload_lin({need(find, p + "delta.gemm.out_proj")}, H, zdim);
+                if (synthetic_) {
+                    Ly.A_log = synth_vec(nv, 0.f, 0.5f);
+                    Ly.dt_bias = synth_vec(nv, 0.f, 0.5f);
+                    Ly.conv_w = synth_vec(static_cast<size_t>(conv_dim) * c_.conv_k, 0.f, 0.5f);
+                    Ly.gnorm = synth_vec(dv, 1.f, 0.1f);
+                    Ly.gnorm_n = dv;
+                } else {
+                    Ly.A_log = upload_vec(need(find, p + "delta.leftover.a_log"), nv);
+                    Ly.dt_bias = upload_vec(need(find, p + "delta.leftover.dt_bias"), nv);
+                    Ly.conv_w = upload_vec(need(find, p + "delta.leftover.conv1d"),
+                                           static_cast<size_t>(conv_dim) * c_.conv_k);
+                    const RlTensor* gn = need(find, p + "delta.leftover.norm");
+                    Ly.gnorm_n = static_cast<int>(gn->rows * gn->cols);
+                    Ly.gnorm = upload_vec(gn, Ly.gnorm_n);
+                }
+                max_width = std::max(max_width, Ly.in_width);
+            } else {
+                Ly.aslot = na++;
+                Ly.qkv_width = 2 * nq * hd + 2 * nkv * hd;
+                const std::vector<std::string> names = {p + "attn.wq", p + "attn.wk", p + "attn.wv"};
+                const std::vector<int> rows = {2 * nq * hd, nkv * hd, nkv * hd};
+                const std::vector<int> offs = {0, 2 * nq * hd, 2 * nq * hd + nkv * hd};
+                make_fused(find, names, rows, offs, H, Ly.qkv_parts, Ly.qkv_offs);
+                Ly.o_proj = synthetic_ ? synth_lin(RL_Q_FP8_E4M3_B128, H, nq * hd)
+                                       : upload_lin({need(find, p + "attn.wo")}, H, nq * hd);
+                Ly.q_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.q_norm"), hd);
+                Ly.k_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.k_norm"), hd);
+                max_width = std::max(max_width, Ly.qkv_width);
+            }
+            // MLP
+            if (synthetic_) {
+                Ly.gate_up = synth_gate_up(I, H);
+                Ly.down = synth_lin(RL_Q_FP8_E4M3_B128, H, I);
+            } else {
+                const RlTensor* g = need(find, p + "mlp.gate");
+                const RlTensor* u = need(find, p + "mlp.up");
+                const RlTensor* d = need(find, p + "mlp.down");
+                I = static_cast<int>(d->cols);
+                RL_REQUIRE(I == c_.intermediate, RL_ERR_FORMAT, "mlp.down shape disagrees with intermediate");
+                if (g->quant == u->quant && (g->quant == RL_Q_FP8_E4M3_B128 || g->quant == RL_Q_BF16)) {
+                    Ly.gate_up = upload_gate_up(g, u, I, H);
+                } else {
+                    Ly.gate = upload_lin({g}, I, H);
+                    Ly.up = upload_lin({u}, I, H);
+                }
+                Ly.down = upload_lin({d}, H, I);
+            }
+        }
+
+        // MTP stem head
+        if (c_.has_mtp) {
+            has_mtp_ = true;
+            if (synthetic_) {
+                mtp_fc_ = synth_lin(RL_Q_FP8_E4M3_B128, H, 2 * H);
+                mtp_nh_ = synth_vec(H, 0.f, 0.1f);
+                mtp_ne_ = synth_vec(H, 0.f, 0.1f);
+                mtp_norm_ = synth_vec(H, 0.f, 0.1f);
+            } else {
+                mtp_fc_ = upload_lin({need(find, "mtp.fc")}, H, 2 * H);
+                mtp_nh_ = upload_vec(need(find, "mtp.pre_fc_norm_hidden"), H);
+                mtp_ne_ = upload_vec(need(find, "mtp.pre_fc_norm_embedding"), H);
+                mtp_norm_ = upload_vec(need(find, "mtp.norm"), H);
+            }
+        }
+
+        // states
+        s_slot_ = static_cast<size_t>(nv) * dv * dk;
+        conv_slot_ = static_cast<size_t>(conv_dim) * c_.conv_k;
+        for (int l = 0; l < nd; ++l) {
+            S_.push_back(mem_.get_n<float>(s_slot_ * R_));
+            conv_.push_back(mem_.get_n<float>(conv_slot_ * R_));
+        }
+        const size_t kv = static_cast<size_t>(nkv) * ctx_ * hd;
+        for (int l = 0; l < na; ++l) {
+            kc_.push_back(mem_.get_n<uint16_t>(kv));
+            vt_.push_back(mem_.get_n<uint16_t>(kv));
+        }
+
+        // activations
+        const int T = tmax_;
+        max_in_ = std::max({H, zdim, nq * hd, I, 2 * H});
+        scal_ = mem_.get_n<int>(kScalars);
+        tok_ = mem_.get_n<int>(8);
+        preds_ = mem_.get_n<int>(8);
+        gen_ = mem_.get_n<int>(kGenCap);
+        x_ = mem_.get_n<float>(static_cast<size_t>(T) * H);
+        xn_ = mem_.get_n<float>(static_cast<size_t>(T) * max_in_);
+        frag_ = mem_.get(act_frag_bytes(max_in_, T));
+        ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
+        o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
+        h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
+        g_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
+        u_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
+        logits_ = mem_.get_n<float>(static_cast<size_t>(T) * c_.vocab);
+        mtp_logits_ = mem_.get_n<float>(c_.vocab);
+        mtp_e_ = mem_.get_n<float>(H);
+        mtp_cat_ = mem_.get_n<float>(2 * static_cast<size_t>(H));
+        mtp_hp_ = mem_.get_n<float>(H);
+        h_last_ = mem_.get_n<float>(H);
+        h_prev_ = mem_.get_n<float>(H);
+        attn_ws_bytes_ = attn_workspace_bytes(std::max(nkv, 1), ctx_);
+        attn_ws_ = mem_.get(attn_ws_bytes_);
+        arg_ws_ = mem_.get(argmax_workspace_bytes(T, c_.vocab));
+        kq_ws_bytes_ = std::max<size_t>(kq_need_, 256);
+        kq_ws_ = mem_.get(kq_ws_bytes_);
+        RL_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_rb_), kRbInts * sizeof(int), hipHostMallocDefault));
+        RL_HIP(hipStreamSynchronize(st_));
+        tab_.clear();
+    }
+
+    template <class Find>
+    const RlTensor* need(Find& find, const std::string& name) {
+        const RlTensor* t = find(name);
+        if (!t) throw Error(RL_ERR_FORMAT, "missing weight " + name);
+        return t;
+    }
+
+    uint64_t next_seed() { return synth_seed_ * 0x9E3779B97F4A7C15ull + (++synth_ctr_) * 0xD1B54A32D192ED03ull; }
+
+    const float* upload_vec(const RlTensor* t, size_t n) {
+        RL_REQUIRE(t->quant == RL_Q_F32, RL_ERR_UNSUPPORTED, std::string(t->name) + ": expected F32");
+        RL_REQUIRE(static_cast<size_t>(t->rows * t->cols) == n, RL_ERR_FORMAT, std::string(t->name) + ": shape");
+        float* d = mem_.get_n<float>(n);
+        RL_HIP(hipMemcpyAsync(d, t->data, n * sizeof(float), hipMemcpyHostToDevice, st_));
+        return d;
+    }
+
+    const float* synth_vec(size_t n, float mean, float stdv) {
+        float* d = mem_.get_n<float>(n);
+        fill_normal_f32(d, n, mean, stdv, next_seed(), st_);
+        return d;
+    }
+
+    static size_t lin_bytes(int kind, int m_pad, int n) {
+        const size_t nkb = (n + 127) / 128;
+        if (kind == RL_Q_FP8_E4M3_B128) return static_cast<size_t>(m_pad) * nkb * 128;
+        return static_cast<size_t>(m_pad) * nkb * 256;  // BF16
+    }
+
+    // Upload one (or several row-concatenated, 16-row aligned) FP8 / BF16 matrices.
+    void place_dense(Lin& L, const RlTensor* t, int rows, int n, int rt_stride, int rt_offset) {
+        RL_REQUIRE(t->rows == rows && t->cols == n, RL_ERR_FORMAT, std::string(t->name) + ": shape mismatch");
+        if (L.kind == RL_Q_FP8_E4M3_B128) {
+            RL_REQUIRE(t->scale != nullptr, RL_ERR_FORMAT, std::string(t->name) + ": FP8 weight without scale");
+            const size_t wb = static_cast<size_t>(rows) * n;
+            const size_t sb = static_cast<size_t>((rows + 127) / 128) * ((n + 127) / 128) * 4;
+            uint8_t* tmp = nullptr;
+            float* stmp = nullptr;
+            RL_HIP(hipMalloc(&tmp, wb));
+            RL_HIP(hipMalloc(&stmp, sb));
+            RL_HIP(hipMemcpyAsync(tmp, t->data, wb, hipMemcpyHostToDevice, st_));
+            RL_HIP(hipMemcpyAsync(stmp, t->scale, sb, hipMemcpyHostToDevice, st_));
+            pack_fp8_rows(tmp, stmp, L.w, L.ts, rows, n, rt_stride, rt_offset, st_);
+            RL_HIP(hipStreamSynchronize(st_));
+            (void)hipFree(tmp);
+            (void)hipFree(stmp);
+        } else {
+            const size_t wb = static_cast<size_t>(rows) * n * 2;
+            uint16_t* tmp = nullptr;
+            RL_HIP(hipMalloc(&tmp, wb));
+            RL_HIP(hipMemcpyAsync(tmp, t->data, wb, hipMemcpyHostToDevice, st_));
+            pack_bf16_rows(tmp, reinterpret_cast<uint16_t*>(L.w), rows, n, rt_stride, rt_offset, st_);
+            RL_HIP(hipStreamSynchronize(st_));
+            (void)hipFree(tmp);
+        }
+    }
+
+    Lin alloc_dense(int kind, int m_pad, int n) {
+        Lin L;
+        L.kind = kind;
+        L.m = m_pad;
+        L.n = n;
+        L.w = static_cast<uint8_t*>(mem_.get(lin_bytes(kind, m_pad, n)));
+        if (kind == RL_Q_FP8_E4M3_B128) L.ts = mem_.get_n<float>(static_cast<size_t>(m_pad / 16) * ((n + 127) / 128));
+        return L;
+    }
+
+    Lin upload_lin(std::vector<const RlTensor*> ts, int rows, int n) {
+        const RlTensor* t = ts[0];
+        if (t->quant == RL_Q_FP8_E4M3_B128 || t->quant == RL_Q_BF16) {
+            Lin L = alloc_dense(t->quant, align16(rows), n);
+            place_dense(L, t, rows, n, 1, 0);
+            return L;
+        }
+        RL_REQUIRE(t->quant == RL_Q_Q4_K || t->quant == RL_Q_Q6_K, RL_ERR_UNSUPPORTED,
+                   std::string(t->name) + ": linear must be FP8_E4M3_B128, BF16, Q4_K or Q6_K");
+        RL_REQUIRE(t->rows == rows && t->cols == n && n % 256 == 0, RL_ERR_FORMAT, std::string(t->name) + ": shape");
+        Lin L;
+        L.kind = t->quant;
+        L.m = rows;
+        L.n = n;
+        kq_need_ = std::max(kq_need_, kq_workspace_bytes(rows, n, tmax_));
+        const size_t tb = rl_hip_kquant_tiled_bytes(t->quant, rows, n);
+        L.w = static_cast<uint8_t*>(mem_.get(tb));
+        const size_t bb = static_cast<size_t>(rows) * (n / 256) * (t->quant == RL_Q_Q4_K ? 144 : 210);
+        uint8_t* tmp = nullptr;
+        RL_HIP(hipMalloc(&tmp, bb));
+        RL_HIP(hipMemcpyAsync(tmp, t->data, bb, hipMemcpyHostToDevice, st_));
+        const int rc = rl_hip_pack_kquant(t->quant, tmp, L.w, rows, n, st_);
+        RL_HIP(hipStreamSynchronize(st_));
+        (void)hipFree(tmp);
+        if (rc != RL_OK) throw Error(rc, rl_hip_last_error());
+        return L;
+    }
+
+    // Fused linear over several weights sharing the input: one tiled matrix when
+    // all parts are FP8 or all BF16 (parts start on 16-row boundaries = the output
+    // column offsets), else one Lin per part.
+    template <class Find>
+    void make_fused(Find& find, const std::vector<std::string>& names, const std::vector<int>& rows,
+                    const std::vector<int>& offs, int n, std::vector<Lin>& parts, std::vector<int>& out_offs) {
+        const int total = offs.back() + align16(rows.back());
+        if (synthetic_) {
+            Lin L = alloc_dense(RL_Q_FP8_E4M3_B128, total, n);
+            synth_fill_dense(L, total, n);
+            parts = {L};
+            out_offs = {0};
+            return;
+        }
+        std::vector<const RlTensor*> ts;
+        for (auto& nm : names) ts.push_back(need(find, nm));
+        bool same = true;
+        for (auto* t : ts) same = same && t->quant == ts[0]->quant;
+        if (same && (ts[0]->quant == RL_Q_FP8_E4M3_B128 || ts[0]->quant == RL_Q_BF16)) {
+            Lin L = alloc_dense(ts[0]->quant, total, n);
+            for (size_t k = 0; k < ts.size(); ++k) place_dense(L, ts[k], rows[k], n, 1, offs[k] / 16);
+            parts = {L};
+            out_offs = {0};
+            return;
+        }
+        parts.clear();
+        out_offs.clear();
+        for (size_t k = 0; k < ts.size(); ++k) {
+            parts.push_back(upload_lin({ts[k]}, rows[k], n));
+            out_offs.push_back(offs[k]);
+        }
+    }
+
+    Lin upload_gate_up(const RlTensor* g, const RlTensor* u, int I, int H) {
+        const int tiles = (I + 15) / 16;
+        Lin L = alloc_dense(g->quant, 2 * tiles * 16, H);
+        place_dense(L, g, I, H, 2, 0);
+        place_dense(L, u, I, H, 2, 1);
+        return L;
+    }
+
+    void synth_fill_dense(Lin& L, int rows, int n) {
+        // random row-major source, then the same packing path as loaded weights
+        if (L.kind == RL_Q_FP8_E4M3_B128) {
+            const size_t wb = static_cast<size_t>(rows) * n;
+            const size_t ns = static_cast<size_t>((rows + 127) / 128) * ((n + 127) / 128);
+            uint8_t* tmp = nullptr;
+            float* stmp = nullptr;
+            RL_HIP(hipMalloc(&tmp, wb));
+            RL_HIP(hipMalloc(&stmp, ns * 4));
+            fill_fp8(tmp, wb, next_seed(), st_);
+            fill_loguniform(stmp, ns, 1e-3f, 1e-1f, next_seed(), st_);
+            pack_fp8_rows(tmp, stmp, L.w, L.ts, rows, n, 1, 0, st_);
+            RL_HIP(hipStreamSynchronize(st_));
+            (void)hipFree(tmp);
+            (void)hipFree(stmp);
+        } else {
+            const size_t ne = static_cast<size_t>(rows) * n;
+            uint16_t* tmp = nullptr;
+            RL_HIP(hipMalloc(&tmp, ne * 2));
+            fill_normal_bf16(tmp, ne, 0.02f, next_seed(), st_);
+            pack_bf16_rows(tmp, reinterpret_cast<uint16_t*>(L.w), rows, n, 1, 0, st_);
+            RL_HIP(hipStreamSynchronize(st_));
+            (void)hipFree(tmp);
+        }
+    }
+
+    Lin synth_lin(int kind, int rows, int n) {
+        Lin L = alloc_dense(kind, align16(rows), n);
+        synth_fill_dense(L, rows, n);
+        return L;
+    }
+
+    Lin synth_gate_up(int I, int H) {
+        // gate and up rows interleaved per 16-row tile; each half random like a
+        // loaded matrix (the interleave only changes where tiles sit)
+        const int tiles = (I + 15) / 16;
+        Lin L = alloc_dense(RL_Q_FP8_E4M3_B128, 2 * tiles * 16, H);
+        for (int half = 0; half < 2; ++half) {
+            const size_t wb = static_cast<size_t>(I) * H;
+            const size_t ns = static_cast<size_t>((I + 127) / 128) * ((H + 127) / 128);
+            uint8_t* tmp = nullptr;
+            float* stmp = nullptr;
+            RL_HIP(hipMalloc(&tmp, wb));
+            RL_HIP(hipMalloc(&stmp, ns * 4));
+            fill_fp8(tmp, wb, next_seed(), st_);
+            fill_loguniform(stmp, ns, 1e-3f, 1e-1f, next_seed(), st_);
+            pack_fp8_rows(tmp, stmp, L.w, L.ts, I, H, 2, half, st_);
+            RL_HIP(hipStreamSynchronize(st_));
+            (void)hipFree(tmp);
+            (void)hipFree(stmp);
+        }
+        return L;
+    }
+
+    void check_ids(const int32_t* ids, int n) const {
+        for (int i = 0; i < n; ++i)
+            if (ids[i] < 0 || ids[i] >= c_.vocab) throw Error(RL_ERR_RANGE, "token id out of range");
+    }
+
+    // ---------------------------------------------------------------- step
+    // Linear on the current activation: FP8 / BF16 read the packed fragments frag_,
+    // K-quants read the fp32 rows x32 (the same values, written by the producer).
+    void linear(const Lin& L, const float* x32, float* Y, int ldy, int m_valid, int T, int epi) {
+        if (L.kind == RL_Q_FP8_E4M3_B128)
+            gemm_fp8_frag(L.w, L.ts, frag_, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
+        else if (L.kind == RL_Q_BF16)
+            gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), frag_, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
+        else
+            kq_gemm(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, x32, Y, kq_ws_, kq_ws_bytes_, L.m, L.n, T, epi == kEpiAdd, ldy,
+                    st_);
+    }
+
+    void linear_parts(const std::vector<Lin>& parts, const std::vector<int>& offs, const float* x32, float* Y,
+                      int ldy, int T) {
+        for (size_t k = 0; k < parts.size(); ++k) linear(parts[k], x32, Y + offs[k], ldy, parts[k].m, T, kEpiStore);
+    }
+
+    void step(int T, int force_all, bool feed) {
+        const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
+        const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
+        const float eps = c_.rms_eps;
+        if (feed) copy_int(scal_ + kNextTok, tok_, st_);
+        embed_rows(embed_, embed_kind_, tok_, x_, H, c_.vocab, T, st_);
+        for (int i = 0; i < c_.n_layers; ++i) {
+            Layer& Ly = L_[i];
+            rmsnorm_pack(x_, H, Ly.attn_norm, xn_, frag_, H, T, eps, st_);
+            if (Ly.kind == RL_LAYER_DELTA) {
+                linear_parts(Ly.in_parts, Ly.in_offs, xn_, ybuf_, Ly.in_width, T);
+                gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
+                           conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_, s_slot_, R_, o_,
+                           T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
+                linear(Ly.out_proj, xn_, x_, H, H, T, kEpiAdd);
+            } else {
+                linear_parts(Ly.qkv_parts, Ly.qkv_offs, xn_, ybuf_, Ly.qkv_width, T);
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
+                                  scal_ + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                                  attn_ws_bytes_, xn_, frag_, st_);
+                linear(Ly.o_proj, xn_, x_, H, H, T, kEpiAdd);
+            }
+            rmsnorm_pack(x_, H, Ly.ffn_norm, xn_, frag_, H, T, eps, st_);
+            if (Ly.gate_up.kind >= 0) {
+                linear(Ly.gate_up, xn_, h_, I, I, T, kEpiSwiGLU);
+            } else {
+                linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
+                linear(Ly.up, xn_, u_, I, I, T, kEpiStore);
+                swiglu(g_, I, u_, I, h_, I, T, st_);
+            }
+            if (Ly.down.kind == RL_Q_FP8_E4M3_B128 || Ly.down.kind == RL_Q_BF16) pack_act(h_, frag_, I, T, st_);
+            linear(Ly.down, h_, x_, H, H, T, kEpiAdd);
+        }
+        rmsnorm_pack(x_, H, final_norm_, xn_, frag_, H, T, eps, st_);
+        linear(lm_head_, xn_, logits_, c_.vocab, c_.vocab, T, kEpiStore);
+        argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
+        accept(tok_, preds_, T, force_all, scal_ + kPos, scal_ + kSlot, R_, scal_ + kNCons, scal_ + kNextTok, gen_,
+               scal_ + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
+    }
+
+    // MTP stem draft of n tokens: tok_[0] = next token, tok_[1..n] = drafts.
+    void mtp_body(int n) {
+        const int H = c_.hidden;
+        const float eps = c_.rms_eps;
+        copy_int(scal_ + kNextTok, tok_, st_);
+        const size_t half_units = static_cast<size_t>(H / 128) * 16 * 2;  // fragment units of H columns, T = 1
+        for (int i = 0; i < n; ++i) {
+            embed_rows(embed_, embed_kind_, tok_ + i, mtp_e_, H, c_.vocab, 1, st_);
+            // cat = [norm_e(embed(tok)) ; norm_h(h)]  (session.cpp:650-658)
+            rmsnorm_pack(mtp_e_, H, mtp_ne_, xn_, frag_, H, 1, eps, st_);
+            rmsnorm_pack(i == 0 ? h_last_ : h_prev_, H, mtp_nh_, xn_ + H, static_cast<i32x4*>(frag_) + half_units, H, 1,
+                         eps, st_);
+            linear(mtp_fc_, xn_, mtp_hp_, H, H, 1, kEpiStore);
+            rmsnorm_pack(mtp_hp_, H, mtp_norm_, xn_, frag_, H, 1, eps, st_);
+            linear(lm_head_, xn_, mtp_logits_, c_.vocab, c_.vocab, 1, kEpiStore);
+            argmax_rows(mtp_logits_, 1, c_.vocab, tok_ + i + 1, nullptr, arg_ws_, st_);
+        }
+    }
+
+    // Replay (capturing on first use) the graph for a T-token step.  T = 1 feeds the
+    // device's next token; T > 1 reads tok_ as written by the host or the MTP draft.
+    void run_graph(int T, bool from_host = false) {
+        (void)from_host;
+        launch_captured(T, [&] { step(T, T == 1 ? 1 : 0, /*feed=*/T == 1); });
+    }
+
+    void run_mtp(int n) {
+        launch_captured(100 + n, [&] { mtp_body(n); });
+    }
+
+    template <class F>
+    void launch_captured(int key, F body) {
+        auto it = graphs_.find(key);
+        if (it == graphs_.end()) {
+            hipGraph_t g = nullptr;
+            hipGraphExec_t ex = nullptr;
+            RL_HIP(hipStreamBeginCapture(st_, hipStreamCaptureModeThreadLocal));
+            try {
+                body();
+            } catch (...) {
+                hipGraph_t dead = nullptr;
+                (void)hipStreamEndCapture(st_, &dead);
+                if (dead) (void)hipGraphDestroy(dead);
+                throw;
+            }
+            RL_HIP(hipStreamEndCapture(st_, &g));
+            RL_HIP(hipGraphInstantiate(&ex, g, nullptr, nullptr, 0));
+            (void)hipGraphDestroy(g);
+            it = graphs_.emplace(key, ex).first;
+        }
+        RL_HIP(hipGraphLaunch(it->second, st_));
+    }
+
+    void sync_graph_state() { RL_HIP(hipStreamSynchronize(st_)); }
+
+    void readback() {
+        RL_HIP(hipMemcpyAsync(host_rb_, scal_, kScalars * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipMemcpyAsync(host_rb_ + kRbToks, tok_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+        pos_ = host_rb_[kPos];
+        n_last_ = host_rb_[kNCons];
+        greedy_ = host_rb_[kNextTok];
+    }
+};
+
+}  // namespace rl
+
+struct RlEngine {
+    std::unique_ptr<rl::Engine> e;
+};
+
+extern "C" {
+
+RlEngine* rl_hip_engine_create(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx, int max_T,
+                               int* status) {
+    RlEngine* out = nullptr;
+    const int rc = guard([&] {
+        RL_REQUIRE(cfg && tensors && n_tensors > 0, RL_ERR_RANGE, "engine_create: null config or weights");
+        auto e = std::make_unique<rl::Engine>(*cfg, ctx, max_T);
+        e->load(tensors, n_tensors);
+        e->reset();
+        out = new RlEngine{std::move(e)};
+    });
+    if (status) *status = rc;
+    return out;
+}
+
+RlEngine* rl_hip_engine_create_synthetic(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T, int* status) {
+    RlEngine* out = nullptr;
+    const int rc = guard([&] {
+        RL_REQUIRE(cfg != nullptr, RL_ERR_RANGE, "engine_create_synthetic: null config");
+        auto e = std::make_unique<rl::Engine>(*cfg, ctx, max_T);
+        e->load_synthetic(seed);
+        e->reset();
+        out = new RlEngine{std::move(e)};
+    });
+    if (status) *status = rc;
+    return out;
+}
+
+void rl_hip_engine_destroy(RlEngine* e) { delete e; }
+
+#define RL_ENGINE(e) RL_REQUIRE((e) && (e)->e, RL_ERR_RANGE, "null engine")
+
+int rl_hip_engine_reset(RlEngine* e) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->reset();
+    });
+}
+int rl_hip_engine_prefill(RlEngine* e, const int32_t* ids, int n) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->prefill(ids, n);
+    });
+}
+int rl_hip_engine_decode_token(RlEngine* e, int32_t token) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->decode_token(token);
+    });
+}
+int rl_hip_engine_decode_steps(RlEngine* e, int n) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->decode_steps(n);
+    });
+}
+int rl_hip_engine_copy_gen_tokens(RlEngine* e, int32_t* host, int n) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->copy_gen_tokens(host, n);
+    });
+}
+int rl_hip_engine_copy_logits(RlEngine* e, float* host) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->copy_logits(host);
+    });
+}
+int rl_hip_engine_copy_last_hidden(RlEngine* e, float* host) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->copy_last_hidden(host);
+    });
+}
+int rl_hip_engine_mtp_draft(RlEngine* e, int32_t first, int n, int32_t* out, int* n_out) {
+    return guard([&] {
+        RL_ENGINE(e);
+        const int k = e->e->mtp_draft(first, n, out);
+        if (n_out) *n_out = k;
+    });
+}
+int rl_hip_engine_spec_verify(RlEngine* e, const int32_t* toks, int T, int32_t* preds, int* n_consumed) {
+    return guard([&] {
+        RL_ENGINE(e);
+        const int k = e->e->spec_verify(toks, T, preds);
+        if (n_consumed) *n_consumed = k;
+    });
+}
+int rl_hip_engine_mtp_spec(RlEngine* e, int32_t t0, int T, int32_t* toks_out, int32_t* preds, int* n_consumed) {
+    return guard([&] {
+        RL_ENGINE(e);
+        const int k = e->e->mtp_spec(t0, T, toks_out, preds);
+        if (n_consumed) *n_consumed = k;
+    });
+}
+int rl_hip_engine_greedy(RlEngine* e, int32_t* tok) {
+    return guard([&] {
+        RL_ENGINE(e);
+        *tok = e->e->greedy();
+    });
+}
+int rl_hip_engine_pos(RlEngine* e, int* pos) {
+    return guard([&] {
+        RL_ENGINE(e);
+        *pos = e->e->pos();
+    });
+}
+int rl_hip_engine_set_pos(RlEngine* e, int pos) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->set_pos(pos);
+    });
+}
+int rl_hip_engine_synthetic_context(RlEngine* e, int n, uint64_t seed) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->synthetic_context(n, seed);
+    });
+}
+int rl_hip_engine_time_steps(RlEngine* e, int T, int iters, int mtp_drafts, float* ms) {
+    return guard([&] {
+        RL_ENGINE(e);
+        *ms = e->e->time_steps(T, iters, mtp_drafts);
+    });
+}
+int rl_hip_engine_info(RlEngine* e, int* vocab, int* hidden, int* ctx_capacity, size_t* device_bytes) {
+    return guard([&] {
+        RL_ENGINE(e);
+        if (vocab) *vocab = e->e->vocab();
+        if (hidden) *hidden = e->e->hidden();
+        if (ctx_capacity) *ctx_capacity = e->e->ctx_capacity();
+        if (device_bytes) *device_bytes = e->e->device_bytes();
+    });
+}
+void* rl_hip_engine_stream(RlEngine* e) { return e && e->e ? e->e->stream() : nullptr; }
+
+}  // extern "C"

@@ -16,7 +16,7 @@
 // State layout in HBM (transposed per head): St[h][j][i] = S[h][i][j], so each
 // thread's 16 values are 64 contiguous bytes and a wave reads 4 KiB contiguously.
 // Conv window layout is the reference's [channel][tap] (tap 0 oldest).
-#include "common.h"
+#include "internal.h"
 
 using namespace rl;
 

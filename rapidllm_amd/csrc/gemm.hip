@@ -25,7 +25,7 @@
 // Work split: a workgroup = KSPLIT waves over RT row-tiles; wave w walks a
 // contiguous 1/KSPLIT of the column blocks, partial C tiles are summed through LDS
 // in a fixed order (deterministic), then the epilogue stores or accumulates Y.
-#include "common.h"
+#include "internal.h"
 
 using namespace rl;
 namespace {
@@ -59,7 +59,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
                                                                 float* __restrict__ Y, int m, int n_kb, int T,
-                                                                int epilogue) {
+                                                                int epilogue, int ldy, int m_valid) {
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
     constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
@@ -168,19 +168,19 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         for (int it = threadIdx.x; it < (RT / 2) * T * kTileRows; it += 64 * KSPLIT) {
             const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
             const int orow = ((rt0 + 2 * r) / 2) * kTileRows + row;
-            if ((rt0 + 2 * r) * kTileRows + row < m) {
+            if (rt0 + 2 * r + 1 < m_tiles && orow < m_valid) {
                 const float gv = final_value(2 * r, t, row);
                 const float uv = final_value(2 * r + 1, t, row);
-                Y[static_cast<size_t>(t) * (m / 2) + orow] = gv / (1.f + __expf(-gv)) * uv;
+                Y[static_cast<size_t>(t) * ldy + orow] = gv / (1.f + __expf(-gv)) * uv;
             }
         }
     } else {
         for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
             const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
             const int orow = (rt0 + r) * kTileRows + row;
-            if (orow < m) {
+            if (orow < m_valid) {
                 const float val = final_value(r, t, row);
-                float* dst = Y + static_cast<size_t>(t) * m + orow;
+                float* dst = Y + static_cast<size_t>(t) * ldy + orow;
                 if (epilogue == kAdd)
                     *dst += val;
                 else
@@ -220,7 +220,8 @@ __global__ void pack_act_kernel(const float* __restrict__ X, i32x4* __restrict__
 // Row-major e4m3 [m][n] + block scales -> tiled bytes + per-tile scales.
 // One thread per (row-tile, column block, lane): 32 bytes.
 __global__ void pack_fp8_kernel(const uint8_t* __restrict__ w, const float* __restrict__ scale,
-                                uint8_t* __restrict__ out, float* __restrict__ tscale, int m, int n, int n_kb) {
+                                uint8_t* __restrict__ out, float* __restrict__ tscale, int m, int n, int n_kb,
+                                int rt_stride, int rt_offset) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     if (idx >= static_cast<size_t>(m_tiles) * n_kb * 64) return;
@@ -232,7 +233,8 @@ __global__ void pack_fp8_kernel(const uint8_t* __restrict__ w, const float* __re
     uint8_t b[32];
 #pragma unroll
     for (int e = 0; e < 32; ++e) b[e] = (row < m && c0 + e < n) ? w[static_cast<size_t>(row) * n + c0 + e] : 0;
-    uint8_t* tile = out + (static_cast<size_t>(rt) * n_kb + kb) * 2048;
+    const size_t drt = static_cast<size_t>(rt) * rt_stride + rt_offset;  // destination tile row
+    uint8_t* tile = out + (drt * n_kb + kb) * 2048;
 #pragma unroll
     for (int e = 0; e < 16; ++e) {
         tile[16 * lane + e] = b[e];
@@ -240,12 +242,12 @@ __global__ void pack_fp8_kernel(const uint8_t* __restrict__ w, const float* __re
     }
     if (lane == 0) {
         const int sb_cols = (n + 127) / 128;
-        tscale[static_cast<size_t>(rt) * n_kb + kb] = scale[static_cast<size_t>((rt * kTileRows) / 128) * sb_cols + kb];
+        tscale[drt * n_kb + kb] = scale[static_cast<size_t>((rt * kTileRows) / 128) * sb_cols + kb];
     }
 }
 
 __global__ void pack_bf16_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int m, int n,
-                                 int n_kb) {
+                                 int n_kb, int rt_stride, int rt_offset) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     if (idx >= static_cast<size_t>(m_tiles) * n_kb * 64) return;
@@ -254,7 +256,8 @@ __global__ void pack_bf16_kernel(const uint16_t* __restrict__ w, uint16_t* __res
     const int rt = static_cast<int>((idx >> 6) / n_kb);
     const int row = rt * kTileRows + (lane & 15);
     const int c0 = kb * kBlockCols + 32 * (lane >> 4);
-    uint16_t* tile = out + (static_cast<size_t>(rt) * n_kb + kb) * 2048;  // 4096 B = 2048 halves
+    const size_t drt = static_cast<size_t>(rt) * rt_stride + rt_offset;
+    uint16_t* tile = out + (drt * n_kb + kb) * 2048;  // 4096 B = 2048 halves
 #pragma unroll
     for (int q = 0; q < 4; ++q)
 #pragma unroll
@@ -291,16 +294,18 @@ static GemmCfg g_force{0, 0, 0};
 
 template <bool kFp8, int RT, int KS, int D>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
-                     int epilogue, hipStream_t s) {
+                     int epilogue, int ldy, int m_valid, hipStream_t s) {
     const int groups = (m_tiles_of(m) + RT - 1) / RT;
     hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups), dim3(64 * KS), 0, s,
                        static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue);
+                       epilogue, ldy, m_valid);
 }
 
+// m = rows of the (tiled) weight; outputs go to Y[t * ldy + row] for row < m_valid
+// (for kSwiGLU, output rows are m/2 and m_valid bounds those).
 template <bool kFp8>
 void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y, int m, int n, int T, int epilogue,
-                 hipStream_t s) {
+                 int ldy, int m_valid, hipStream_t s) {
     RL_REQUIRE(m > 0 && n > 0, RL_ERR_RANGE, "gemm: empty shape");
     RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "gemm: T must be in 1..8");
     RL_REQUIRE(W && frag && Y, RL_ERR_RANGE, "gemm: null pointer");
@@ -314,7 +319,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
 #define RL_GEMM_CASE(R, K, DD)                                                            \
     if (c.rt == R && c.ks == K && c.d == DD) {                                            \
-        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, s);     \
+        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, s); \
         check_launch("gemm_frag_kernel");                                                 \
         return;                                                                           \
     }
@@ -336,13 +341,28 @@ void launch_pack_act(const float* X, void* frag, int n, int T, hipStream_t s) {
 }  // namespace
 
 namespace rl {
+size_t act_frag_bytes(int n, int T) { return static_cast<size_t>(n_kb_of(n)) * 16 * 2 * T * 16; }
 // Internal entry points shared with the engine.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   hipStream_t s) {
-    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, s);
+                   int ldy, int m_valid, hipStream_t s) {
+    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s);
 }
-void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, hipStream_t s) {
-    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, s);
+void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
+                    hipStream_t s) {
+    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s);
+}
+void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
+                   int rt_offset, hipStream_t s) {
+    const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;
+    hipLaunchKernelGGL(pack_fp8_kernel, dim3((total + 255) / 256), dim3(256), 0, s, w, scale, dst, tscale, m, n,
+                       n_kb_of(n), rt_stride, rt_offset);
+    check_launch("pack_fp8_kernel");
+}
+void pack_bf16_rows(const uint16_t* w, uint16_t* dst, int m, int n, int rt_stride, int rt_offset, hipStream_t s) {
+    const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;
+    hipLaunchKernelGGL(pack_bf16_kernel, dim3((total + 255) / 256), dim3(256), 0, s, w, dst, m, n, n_kb_of(n),
+                       rt_stride, rt_offset);
+    check_launch("pack_bf16_kernel");
 }
 void pack_act(const float* X, void* frag, int n, int T, hipStream_t s) { launch_pack_act(X, frag, n, T, s); }
 }  // namespace rl
@@ -365,20 +385,14 @@ int rl_hip_pack_fp8(const uint8_t* w, const float* scale, uint8_t* w_tiled, floa
                     void* stream) {
     return guard([&] {
         RL_REQUIRE(m > 0 && n > 0 && w && scale && w_tiled && tile_scale, RL_ERR_RANGE, "pack_fp8: bad args");
-        const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;
-        hipLaunchKernelGGL(pack_fp8_kernel, dim3((total + 255) / 256), dim3(256), 0, S(stream), w, scale, w_tiled,
-                           tile_scale, m, n, n_kb_of(n));
-        check_launch("pack_fp8_kernel");
+        rl::pack_fp8_rows(w, scale, w_tiled, tile_scale, m, n, 1, 0, S(stream));
     });
 }
 
 int rl_hip_pack_bf16(const uint16_t* w, uint16_t* w_tiled, int m, int n, void* stream) {
     return guard([&] {
         RL_REQUIRE(m > 0 && n > 0 && w && w_tiled, RL_ERR_RANGE, "pack_bf16: bad args");
-        const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;
-        hipLaunchKernelGGL(pack_bf16_kernel, dim3((total + 255) / 256), dim3(256), 0, S(stream), w, w_tiled, m, n,
-                           n_kb_of(n));
-        check_launch("pack_bf16_kernel");
+        rl::pack_bf16_rows(w, w_tiled, m, n, 1, 0, S(stream));
     });
 }
 
@@ -388,19 +402,19 @@ int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream) {
 
 int rl_hip_gemm_fp8_frag(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                          int T, int accumulate, void* stream) {
-    return guard([&] { launch_gemm<true>(w_tiled, tile_scale, frag, Y, m, n, T, accumulate ? kAdd : kStore, S(stream)); });
+    return guard([&] { launch_gemm<true>(w_tiled, tile_scale, frag, Y, m, n, T, accumulate ? kAdd : kStore, m, m, S(stream)); });
 }
 
 int rl_hip_gemm_bf16_frag(const uint16_t* w_tiled, const void* frag, float* Y, int m, int n, int T, int accumulate,
                           void* stream) {
-    return guard([&] { launch_gemm<false>(w_tiled, nullptr, frag, Y, m, n, T, accumulate ? kAdd : kStore, S(stream)); });
+    return guard([&] { launch_gemm<false>(w_tiled, nullptr, frag, Y, m, n, T, accumulate ? kAdd : kStore, m, m, S(stream)); });
 }
 
 int rl_hip_gemm_fp8(const uint8_t* w_tiled, const float* tile_scale, const float* X, float* Y, void* frag_scratch,
                     int m, int n, int T, void* stream) {
     return guard([&] {
         launch_pack_act(X, frag_scratch, n, T, S(stream));
-        launch_gemm<true>(w_tiled, tile_scale, frag_scratch, Y, m, n, T, kStore, S(stream));
+        launch_gemm<true>(w_tiled, tile_scale, frag_scratch, Y, m, n, T, kStore, m, m, S(stream));
     });
 }
 

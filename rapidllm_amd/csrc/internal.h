@@ -1,0 +1,62 @@
+// internal.h -- launchers shared between the kernel files and the engine.
+#pragma once
+
+#include "common.h"
+
+namespace rl {
+
+enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2 };
+
+// gemm.hip
+void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
+                   int ldy, int m_valid, hipStream_t s);
+void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
+                    hipStream_t s);
+void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
+void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
+                   int rt_offset, hipStream_t s);
+void pack_bf16_rows(const uint16_t* w, uint16_t* dst, int m, int n, int rt_stride, int rt_offset, hipStream_t s);
+
+// kquant.hip
+size_t kq_workspace_bytes(int m, int n, int T);
+void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_t ws_bytes, int m, int n, int T,
+             int accumulate, int ldy, hipStream_t s);
+
+// norms.hip
+void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
+                  hipStream_t s);
+void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, int gamma_n, float* y, void* frag,
+                int n, int T, float eps, hipStream_t s);
+void embed_rows(const void* table, int kind, const int* tokens, float* out, int H, int vocab, int T, hipStream_t s);
+void swiglu(const float* g, int ldg, const float* u, int ldu, float* h, int n, int T, hipStream_t s);
+void copy_int(const int* src, int* dst, hipStream_t s);
+
+// gdn.hip
+void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log, const float* dt_bias,
+                const float* conv_w, const float* conv_in, float* conv_out, const float* S_in, float* S_out,
+                const int* cur, size_t conv_slot, size_t s_slot, int R, float* o, int T, int nk, int nv, int dk,
+                int dv, int K, int v_tiled, hipStream_t s);
+
+// attn.hip
+size_t attn_workspace_bytes(int nkv, int ctx);
+void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,
+                       int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot, float theta, float eps,
+                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s);
+
+// sample.hip
+size_t argmax_workspace_bytes(int rows, int V);
+void argmax_rows(const float* logits, int rows, int V, int* out, float* out_val, void* ws, hipStream_t s);
+void accept(const int* toks, const int* preds, int T, int force_all, int* pos, int* slot, int R, int* n_out,
+            int* next_tok, int* gen_ring, int* gen_count, int gen_cap, const float* xout, float* h_last,
+            float* h_prev, int H, hipStream_t s);
+
+// synth.hip
+void fill_fp8(uint8_t* p, size_t n, uint64_t seed, hipStream_t s);
+void fill_loguniform(float* p, size_t n, float lo, float hi, uint64_t seed, hipStream_t s);
+void fill_normal_f32(float* p, size_t n, float mean, float stdv, uint64_t seed, hipStream_t s);
+void fill_normal_bf16(uint16_t* p, size_t n, float stdv, uint64_t seed, hipStream_t s);
+void fill_normal_f16(uint16_t* p, size_t n, float stdv, uint64_t seed, hipStream_t s);
+
+size_t act_frag_bytes(int n, int T);
+
+}  // namespace rl

@@ -17,7 +17,7 @@
 // All 64 lanes of a wave work on the same super-block at the same time, so the
 // activation element multiplying every lane's weight is the same: x is read with
 // scalar loads into SGPRs and used directly as the FMA operand (no LDS, no VGPRs).
-#include "common.h"
+#include "internal.h"
 
 using namespace rl;
 
@@ -164,7 +164,7 @@ template <int QT, int T, int KS>
 __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                           const float* __restrict__ xs, float* __restrict__ Y,
                                                           float* __restrict__ partial, int m, int n, int S,
-                                                          int accumulate) {
+                                                          int accumulate, int ldy) {
     using F = KFmt<QT>;
     const int lane = threadIdx.x & 63;
     // wave index is uniform: make that visible so the super-block loop (and the x
@@ -219,22 +219,23 @@ __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restr
         if (S > 1)
             partial[(static_cast<size_t>(slice) * T + t) * m + row] = s;
         else if (accumulate)
-            Y[static_cast<size_t>(t) * m + row] += s;
+            Y[static_cast<size_t>(t) * ldy + row] += s;
         else
-            Y[static_cast<size_t>(t) * m + row] = s;
+            Y[static_cast<size_t>(t) * ldy + row] = s;
     }
 }
 
 __global__ void kq_reduce_kernel(const float* __restrict__ partial, float* __restrict__ Y, int m, int T, int S,
-                                 int accumulate) {
+                                 int accumulate, int ldy) {
     const int i = blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= T * m) return;
     float s = 0.f;
     for (int q = 0; q < S; ++q) s += partial[static_cast<size_t>(q) * T * m + i];
+    float* dst = Y + static_cast<size_t>(i / m) * ldy + i % m;
     if (accumulate)
-        Y[i] += s;
+        *dst += s;
     else
-        Y[i] = s;
+        *dst = s;
 }
 
 // Sums of x over 16- and 32-element sub-blocks: xs16 [T][n/16] then xs32 [T][n/32].
@@ -260,6 +261,7 @@ __global__ void kq_xsum_kernel(const float* __restrict__ x, float* __restrict__ 
 // Row-major GGUF blocks [m][n/256 * bb] -> K-tiled.
 template <int QT>
 __global__ void kq_pack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int m, int nsb) {
+    // rows past m are written as zero blocks (d = 0: every weight is 0)
     using F = KFmt<QT>;
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rg, sb, lane)
     const int m_groups = (m + kRows - 1) / kRows;
@@ -342,20 +344,20 @@ void kq_split(int m, int nsb, int& S, int& KS) {
 
 template <int QT, int T>
 void launch_kq_t(const uint8_t* W, const float* x, const float* xs, float* Y, float* partial, int m, int n, int S,
-                 int accumulate, hipStream_t s) {
+                 int accumulate, int ldy, hipStream_t s) {
     const int groups = (m + kRows - 1) / kRows;
     hipLaunchKernelGGL((kq_gemm_kernel<QT, T, 4>), dim3(groups * S), dim3(256), 0, s, W, x, xs, Y, partial, m, n, S,
-                       accumulate);
+                       accumulate, ldy);
 }
 
 template <int QT>
 void launch_kq(const uint8_t* W, const float* x, const float* xs, float* Y, float* partial, int m, int n, int T,
-               int S, int accumulate, hipStream_t s) {
+               int S, int accumulate, int ldy, hipStream_t s) {
     switch (T) {
-    case 1: launch_kq_t<QT, 1>(W, x, xs, Y, partial, m, n, S, accumulate, s); break;
-    case 2: launch_kq_t<QT, 2>(W, x, xs, Y, partial, m, n, S, accumulate, s); break;
-    case 3: launch_kq_t<QT, 3>(W, x, xs, Y, partial, m, n, S, accumulate, s); break;
-    default: launch_kq_t<QT, 4>(W, x, xs, Y, partial, m, n, S, accumulate, s); break;
+    case 1: launch_kq_t<QT, 1>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 2: launch_kq_t<QT, 2>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 3: launch_kq_t<QT, 3>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
+    default: launch_kq_t<QT, 4>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
     }
 }
 
@@ -372,7 +374,7 @@ size_t kq_workspace_bytes(int m, int n, int T) {
 
 // Y[T][m] (=, +=) W . x for Q4_K (qt=4) / Q6_K (qt=6) K-tiled weights.
 void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_t ws_bytes, int m, int n, int T,
-             int accumulate, hipStream_t s) {
+             int accumulate, int ldy, hipStream_t s) {
     RL_REQUIRE(qt == 4 || qt == 6, RL_ERR_UNSUPPORTED, "kquant: type must be Q4_K or Q6_K");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
     RL_REQUIRE(T >= 1 && T <= 4, RL_ERR_RANGE, "kquant: T must be in 1..4");
@@ -387,13 +389,13 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     check_launch("kq_xsum_kernel");
     const float* xs_use = qt == 4 ? xs + static_cast<size_t>(T) * (n / 16) : xs;
     if (qt == 4)
-        launch_kq<4>(W, x, xs_use, Y, partial, m, n, T, S, accumulate, s);
+        launch_kq<4>(W, x, xs_use, Y, partial, m, n, T, S, accumulate, ldy, s);
     else
-        launch_kq<6>(W, x, xs_use, Y, partial, m, n, T, S, accumulate, s);
+        launch_kq<6>(W, x, xs_use, Y, partial, m, n, T, S, accumulate, ldy, s);
     check_launch("kq_gemm_kernel");
     if (S > 1) {
         hipLaunchKernelGGL(kq_reduce_kernel, dim3((T * m + 255) / 256), dim3(256), 0, s, partial, Y, m, T, S,
-                           accumulate);
+                           accumulate, ldy);
         check_launch("kq_reduce_kernel");
     }
 }
@@ -429,7 +431,7 @@ int rl_hip_gemm_kquant(int type, const uint8_t* tiled, const float* X, float* Y,
                        size_t workspace_bytes, int m, int n, int T, int accumulate, void* stream) {
     return guard([&] {
         RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "gemm_kquant: Q4_K or Q6_K only");
-        rl::kq_gemm(type == RL_Q_Q4_K ? 4 : 6, tiled, X, Y, workspace, workspace_bytes, m, n, T, accumulate,
+        rl::kq_gemm(type == RL_Q_Q4_K ? 4 : 6, tiled, X, Y, workspace, workspace_bytes, m, n, T, accumulate, m,
                     S(stream));
     });
 }

@@ -10,7 +10,7 @@
 //   embed_rows   : token ids -> fp32 rows of an F32 / F16 / BF16 table
 //                  (src/runtime/session.cpp:122-140).
 // Sums of squares are accumulated in double as in the reference scalar path.
-#include "common.h"
+#include "internal.h"
 
 using namespace rl;
 
@@ -134,9 +134,31 @@ __global__ void embed_rows_kernel(const void* __restrict__ table, int kind, cons
     out[static_cast<size_t>(t) * H + i] = v;
 }
 
+__global__ void swiglu_kernel(const float* __restrict__ g, int ldg, const float* __restrict__ u, int ldu,
+                              float* __restrict__ h, int n) {
+    const int t = blockIdx.y;
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    h[static_cast<size_t>(t) * n + i] = silu_f(g[static_cast<size_t>(t) * ldg + i]) * u[static_cast<size_t>(t) * ldu + i];
+}
+
+__global__ void copy_int_kernel(const int* __restrict__ src, int* __restrict__ dst) { *dst = *src; }
+
 }  // namespace
 
 namespace rl {
+
+// silu(g) * u (reference ops.cpp:607-609), rows at strides ldg / ldu, h dense [T][n].
+void swiglu(const float* g, int ldg, const float* u, int ldu, float* h, int n, int T, hipStream_t s) {
+    hipLaunchKernelGGL(swiglu_kernel, dim3((n + 255) / 256, T), dim3(256), 0, s, g, ldg, u, ldu, h, n);
+    check_launch("swiglu_kernel");
+}
+
+// one int device-to-device as a kernel (graph-safe, no memcpy node)
+void copy_int(const int* src, int* dst, hipStream_t s) {
+    hipLaunchKernelGGL(copy_int_kernel, dim3(1), dim3(1), 0, s, src, dst);
+    check_launch("copy_int_kernel");
+}
 
 void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
                   hipStream_t s) {

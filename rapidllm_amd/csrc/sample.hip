@@ -11,7 +11,7 @@
 // preds[i] = greedy after toks[i]; n = 1 + longest prefix with preds[i] == toks[i+1].
 // It advances the device position and recurrent-state slot by n, so the next step
 // runs without a host round trip.
-#include "common.h"
+#include "internal.h"
 
 using namespace rl;
 

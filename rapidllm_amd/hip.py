@@ -65,6 +65,26 @@ _SIGS = {
     "rl_hip_argmax_workspace_bytes": (_sz, [_i, _i]),
     "rl_hip_argmax_rows": (_i, [_vp, _i, _i, _vp, _vp, _vp, _vp]),
     "rl_hip_accept_prefix": (_i, [_vp, _vp, _i, _vp, _vp, _vp, _vp]),
+    "rl_hip_engine_create": (_vp, [_vp, _vp, _i, _i, _i, C.POINTER(_i)]),
+    "rl_hip_engine_create_synthetic": (_vp, [_vp, C.c_uint64, _i, _i, C.POINTER(_i)]),
+    "rl_hip_engine_destroy": (None, [_vp]),
+    "rl_hip_engine_reset": (_i, [_vp]),
+    "rl_hip_engine_prefill": (_i, [_vp, _vp, _i]),
+    "rl_hip_engine_decode_token": (_i, [_vp, C.c_int32]),
+    "rl_hip_engine_decode_steps": (_i, [_vp, _i]),
+    "rl_hip_engine_copy_gen_tokens": (_i, [_vp, _vp, _i]),
+    "rl_hip_engine_copy_logits": (_i, [_vp, _vp]),
+    "rl_hip_engine_copy_last_hidden": (_i, [_vp, _vp]),
+    "rl_hip_engine_mtp_draft": (_i, [_vp, C.c_int32, _i, _vp, C.POINTER(_i)]),
+    "rl_hip_engine_spec_verify": (_i, [_vp, _vp, _i, _vp, C.POINTER(_i)]),
+    "rl_hip_engine_mtp_spec": (_i, [_vp, C.c_int32, _i, _vp, _vp, C.POINTER(_i)]),
+    "rl_hip_engine_greedy": (_i, [_vp, C.POINTER(C.c_int32)]),
+    "rl_hip_engine_pos": (_i, [_vp, C.POINTER(_i)]),
+    "rl_hip_engine_info": (_i, [_vp, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(_sz)]),
+    "rl_hip_engine_set_pos": (_i, [_vp, _i]),
+    "rl_hip_engine_synthetic_context": (_i, [_vp, _i, C.c_uint64]),
+    "rl_hip_engine_time_steps": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "rl_hip_engine_stream": (_vp, [_vp]),
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
     "rl_hip_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),

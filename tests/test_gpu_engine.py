@@ -1,0 +1,136 @@
+"""GPU parity of the whole decode engine against the CPU oracle model on small
+models of the real architecture (head dims 128/256, FP8 or K-quant linears):
+logits within 1e-3 relative L2, identical greedy tokens where the top-1 margin
+exceeds that tolerance, MTP stem drafts, the greedy invariant (spec == spec off)
+and speculative rollback."""
+import numpy as np
+import pytest
+
+from oracle.oracle import OracleModel
+from rapidllm_amd import model as M
+from rapidllm_amd.engine import Engine
+
+pytestmark = pytest.mark.gpu
+
+TOL = 1e-3
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def mini_spec(**kw):
+    base = dict(vocab=1000, hidden=256, n_layers=4, intermediate=512, n_k_heads=2, n_v_heads=4, n_q=4, n_kv=2,
+                layer_kinds=[0, 0, 0, 1])
+    base.update(kw)
+    return M.ModelSpec(**base)
+
+
+def margin_ok(logits, tol=TOL):
+    s = np.sort(logits.astype(np.float64))
+    return (s[-1] - s[-2]) > tol * np.linalg.norm(logits)
+
+
+@pytest.fixture(scope="module")
+def fp8_pair(orc):
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=3, w_scale=(1e-3, 1e-2))
+    return spec, W, Engine(spec, W, ctx=1024), OracleModel(spec, W, ctx=1024)
+
+
+def test_decode_logits_match_oracle(gpu, fp8_pair):
+    spec, W, eng, orc_m = fp8_pair
+    prompt = [1, 2, 3, 4, 5, 6, 7]
+    eng.prefill(prompt)
+    orc_m.reset()
+    for t in prompt:
+        g, lg, hd = orc_m.decode(t)
+    assert rel_l2(eng.copy_logits(), lg) < TOL
+    assert rel_l2(eng.copy_last_hidden(), hd) < TOL
+    if margin_ok(lg):
+        assert eng.greedy() == g
+    tok = g
+    for _ in range(6):
+        eng.decode_token(tok)
+        g, lg, _ = orc_m.decode(tok)
+        assert rel_l2(eng.copy_logits(), lg) < TOL
+        if margin_ok(lg):
+            assert eng.greedy() == g
+        tok = g
+
+
+def test_greedy_generate_matches_oracle(gpu, fp8_pair):
+    spec, W, eng, orc_m = fp8_pair
+    prompt = [5, 9, 13]
+    want, _, _ = orc_m.generate(prompt, 12)
+    got, _, _ = eng.generate(prompt, 12)
+    assert got == want
+
+
+def test_mtp_draft_matches_oracle(gpu, fp8_pair):
+    spec, W, eng, orc_m = fp8_pair
+    prompt = [7, 8, 9, 10, 11]
+    eng.prefill(prompt)
+    orc_m.reset()
+    for t in prompt:
+        g, _, _ = orc_m.decode(t)
+    assert eng.greedy() == g
+    assert eng.mtp_draft(g, 3).tolist() == orc_m.mtp_draft(g, 3).tolist()
+
+
+def test_spec_invariant_and_oracle_spec(gpu, fp8_pair):
+    """Greedy invariant (tests/test_spec.cpp:46-79): MTP speculation changes speed,
+    never tokens; GPU T=4 verify == GPU T=1 decode == CPU oracle with MTP."""
+    spec, W, eng, orc_m = fp8_pair
+    prompt = [3, 1, 4, 1, 5]
+    off, _, _ = eng.generate(prompt, 16, spec_n=0)
+    on, prop, acc = eng.generate(prompt, 16, spec_n=3)
+    assert on == off
+    ref_on, rprop, racc = orc_m.generate(prompt, 16, spec_n=3)
+    assert ref_on == off
+    assert acc == racc
+
+
+def test_spec_verify_rollback(gpu, fp8_pair):
+    """A rejected draft leaves the state exactly as the accepted prefix: after
+    verifying [t0, d1, wrong, x] the next logits equal a T=1 replay."""
+    spec, W, eng, orc_m = fp8_pair
+    prompt = [2, 4, 6]
+    eng.prefill(prompt)
+    t0 = eng.greedy()
+    eng.decode_token(t0)
+    d1 = eng.greedy()
+    ref_logits = eng.copy_logits()
+    eng.prefill(prompt)
+    wrong = (d1 + 1) % spec.vocab
+    k, preds = eng.spec_verify([t0, d1, wrong, 17])
+    assert preds[0] == d1
+    assert k == (3 if preds[1] == wrong else 2)
+    if k == 2:
+        # state = after [prompt, t0, d1]; compare with a plain T=1 run
+        eng2_logits = eng.copy_logits()
+        eng.prefill(prompt)
+        eng.decode_token(t0)
+        eng.decode_token(d1)
+        assert np.array_equal(eng.copy_logits(), eng2_logits)
+        assert eng.pos() == len(prompt) + 2
+    del ref_logits
+
+
+@pytest.mark.parametrize("quant", [M.Q_Q4_K, M.Q_Q6_K, M.Q_BF16])
+def test_other_weight_formats_match_oracle(gpu, orc, quant):
+    spec = mini_spec(n_layers=4, layer_kinds=[0, 1, 0, 0])
+    W = M.random_weights(spec, seed=11, linear_quant=quant)
+    eng = Engine(spec, W, ctx=512)
+    orc_m = OracleModel(spec, W, ctx=512)
+    prompt = [10, 20, 30, 40, 50]
+    eng.prefill(prompt)
+    for t in prompt:
+        g, lg, _ = orc_m.decode(t)
+    assert rel_l2(eng.copy_logits(), lg) < TOL
+    for _ in range(3):
+        eng.decode_token(g)
+        g, lg, _ = orc_m.decode(g)
+        assert rel_l2(eng.copy_logits(), lg) < TOL
