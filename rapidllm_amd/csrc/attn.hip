@@ -270,46 +270,74 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     }
 }
 
-// grid (G*T pairs, nkv), 256 threads (one per d).
+// grid (G*T pairs, nkv, hd/64), 256 threads = 4 chunk groups x 64 dims.
+// Chunk weights w_c = exp(m_c - M) are computed once into LDS; each thread sums
+// its chunk group's O_c[d] * w_c, the 4 groups are added in a fixed order.
+constexpr int kMaxChunksLds = 4096;  // 1M positions
+
 __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
-    const int k = blockIdx.x, kv = blockIdx.y, d = threadIdx.x;
+    const int k = blockIdx.x, kv = blockIdx.y;
+    const int tid = threadIdx.x, q = tid >> 6, dl = tid & 63;
+    const int d = blockIdx.z * 64 + dl;
     const int t = k / p.G;
     const int h = kv * p.G + k % p.G;
     const int L = *p.pos + p.T;
     const int nch = (L + kChunk - 1) / kChunk;
     const size_t base = static_cast<size_t>(kv) * p.max_chunks;
-    float M = -INFINITY;
-    for (int c = 0; c < nch; ++c) M = fmaxf(M, p.part_m[(base + c) * kMaxPairs + k]);
-    float acc = 0.f, Ls = 0.f;
-    for (int c = 0; c < nch; ++c) {
+    __shared__ float w_s[kMaxChunksLds];
+    __shared__ float red[4][64];
+    __shared__ float sh[8];
+    // chunk max
+    float mx = -INFINITY;
+    for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, p.part_m[(base + c) * kMaxPairs + k]);
+    mx = wave_max(mx);
+    if ((tid & 63) == 0) sh[tid >> 6] = mx;
+    __syncthreads();
+    const float M = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    // weights and the softmax denominator
+    float ls = 0.f;
+    for (int c = tid; c < nch; c += 256) {
         const float m = p.part_m[(base + c) * kMaxPairs + k];
-        if (m == -INFINITY) continue;
-        const float w = expf(m - M);
-        Ls += p.part_l[(base + c) * kMaxPairs + k] * w;
-        acc += p.part_o[((base + c) * kMaxPairs + k) * kHD + d] * w;
+        const float w = m == -INFINITY ? 0.f : expf(m - M);
+        w_s[c] = w;
+        ls += p.part_l[(base + c) * kMaxPairs + k] * w;
     }
+    ls = wave_sum(ls);
+    __syncthreads();
+    if ((tid & 63) == 0) sh[4 + (tid >> 6)] = ls;
+    __syncthreads();
+    const float Ls = (sh[4] + sh[5]) + (sh[6] + sh[7]);
+    // weighted sum of the chunk outputs for dim d over chunks c = q (mod 4)
+    float acc = 0.f;
+    const float* po = p.part_o + (base * kMaxPairs + k) * kHD + d;
+    const size_t cstride = static_cast<size_t>(kMaxPairs) * kHD;
+#pragma unroll 8
+    for (int c = q; c < nch; c += 4) acc += po[c * cstride] * w_s[c];
+    red[q][dl] = acc;
+    __syncthreads();
+    if (q != 0) return;
+    const float o = ((red[0][dl] + red[1][dl]) + (red[2][dl] + red[3][dl])) / Ls;
     const float gate = p.Y[static_cast<size_t>(t) * p.ld_y + static_cast<size_t>(h) * 2 * kHD + kHD + d];
-    const float val = acc / Ls * sigmoid_f(gate);
+    const float val = o * sigmoid_f(gate);
     const int n = p.nq * kHD;
     const int j = h * kHD + d;
     if (p.out) p.out[static_cast<size_t>(t) * n + j] = val;
     if (p.frag) {
-        __shared__ float vals[kHD];
-        vals[d] = val;
-        __syncthreads();
-        if (d < kHD / 8) {
-            const int col8 = (h * kHD) / 8 + d;
+        red[1][dl] = val;  // wave 0 only from here on: reuse a row of red
+        __builtin_amdgcn_wave_barrier();
+        if (dl < 8) {  // 8 units of 8 columns cover this workgroup's 64 dims
+            const int unit = (h * kHD + blockIdx.z * 64) / 8 + dl;
             union {
                 uint16_t hh[8];
-                i32x4 q;
+                i32x4 v;
             } hi, mid;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) split_bf16(vals[8 * d + e], hi.hh[e], mid.hh[e]);
-            const int kb = col8 >> 4, jb = (col8 & 15) * 8;
+            for (int e = 0; e < 8; ++e) split_bf16(red[1][8 * dl + e], hi.hh[e], mid.hh[e]);
+            const int kb = unit >> 4, jb = (unit & 15) * 8;
             const int gg = jb >> 5, i = (jb >> 3) & 3;
             const size_t u = ((static_cast<size_t>(kb) * 4 + i) * 4 + gg) * (2 * p.T) + t;
-            p.frag[u] = hi.q;
-            p.frag[u + p.T] = mid.q;
+            p.frag[u] = hi.v;
+            p.frag[u + p.T] = mid.v;
         }
     }
 }
@@ -332,6 +360,7 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     const int G = nq / nkv;
     RL_REQUIRE(T >= 1 && G * T <= kMaxPairs, RL_ERR_RANGE, "attn: (n_q/n_kv) * T must be <= 32");
     RL_REQUIRE(ctx > 0 && ctx % kChunk == 0, RL_ERR_RANGE, "attn: cache capacity must be a multiple of 256");
+    RL_REQUIRE(ctx / kChunk <= kMaxChunksLds, RL_ERR_RANGE, "attn: cache capacity above 1M positions");
     RL_REQUIRE(rot >= 2 && rot % 2 == 0 && rot <= hd, RL_ERR_RANGE, "attn: bad rotary dim");
     RL_REQUIRE(Y && kc && vt && pos_dev && ws && (out || frag), RL_ERR_RANGE, "attn: null pointer");
     RL_REQUIRE(ws_bytes >= attn_workspace_bytes(nkv, ctx), RL_ERR_RANGE, "attn: workspace too small");
@@ -370,7 +399,7 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     else
         hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks, nkv), dim3(256), 0, s, p);
     check_launch("attn_part_kernel");
-    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv, kHD / 64), dim3(256), 0, s, p);
     check_launch("attn_comb_kernel");
 }
 

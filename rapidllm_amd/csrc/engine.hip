@@ -26,6 +26,7 @@
 // verify step to its own slot and acceptance just advances the slot index by the
 // number of tokens kept.  KV rows of rejected tokens are overwritten later and are
 // never read (attention masks positions past each query).
+#include <cstdlib>
 #include <cstring>
 #include <map>
 #include <memory>
@@ -316,6 +317,9 @@ class Engine {
     // host readback block (ints): scalars, then preds, then toks
     enum { kRbPreds = 8, kRbToks = 16, kRbInts = 24 };
     static constexpr int kGenCap = 4096;
+    // K-slices of the residual-add linears (o_proj, out_proj, down): their outputs
+    // are partial sums that the next RMSNorm adds to the residual in slice order.
+    static constexpr int kSplit = 4;
 
     RlModelConfig c_;
     int ctx_ = 0, tmax_ = 4, R_ = 5;
@@ -344,7 +348,9 @@ class Engine {
     int* tok_ = nullptr;    // [Tmax]
     int* preds_ = nullptr;  // [Tmax]
     int* gen_ = nullptr;    // [kGenCap]
-    float* x_ = nullptr;    // [Tmax][H] residual stream
+    float* xres_[2] = {nullptr, nullptr};  // [Tmax][H] residual stream (ping-pong)
+    float* part_ = nullptr;  // [kSplit][Tmax][H] partial sums of the residual-add linears
+    float* x_ = nullptr;     // residual after the last step (set by step())
     float* xn_ = nullptr;   // [Tmax][max_in] fp32 copy of the packed activation
     void* frag_ = nullptr;  // GEMM fragments
     float* ybuf_ = nullptr; // [Tmax][max_width] fused projection outputs
@@ -510,7 +516,9 @@ class Engine {
         tok_ = mem_.get_n<int>(8);
         preds_ = mem_.get_n<int>(8);
         gen_ = mem_.get_n<int>(kGenCap);
-        x_ = mem_.get_n<float>(static_cast<size_t>(T) * H);
+        xres_[0] = mem_.get_n<float>(static_cast<size_t>(T) * H);
+        xres_[1] = mem_.get_n<float>(static_cast<size_t>(T) * H);
+        part_ = mem_.get_n<float>(static_cast<size_t>(kSplit) * T * H);
         xn_ = mem_.get_n<float>(static_cast<size_t>(T) * max_in_);
         frag_ = mem_.get(act_frag_bytes(max_in_, T));
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
@@ -743,6 +751,36 @@ class Engine {
                     st_);
     }
 
+    // Residual-add linear [H rows]: writes partial sums into part_ and returns the
+    // number of slices the next residual_rmsnorm_pack must add.
+    int linear_residual(const Lin& L, const float* x32, int T) {
+        const int H = c_.hidden;
+        if (L.kind == RL_Q_FP8_E4M3_B128) {
+            gemm_fp8_frag(L.w, L.ts, frag_, part_, L.m, L.n, T, kEpiPartial, H, H, st_, kSplit);
+            return kSplit;
+        }
+        if (L.kind == RL_Q_BF16) {
+            gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), frag_, part_, L.m, L.n, T, kEpiPartial, H, H, st_,
+                           kSplit);
+            return kSplit;
+        }
+        linear(L, x32, part_, H, H, T, kEpiStore);
+        return 1;
+    }
+
+    // x <- x + pending partials (if any), then RMSNorm into xn_ / frag_.
+    void norm_residual(int& cur, int& pending, const float* gamma, int T) {
+        const int H = c_.hidden;
+        if (pending > 0) {
+            residual_rmsnorm_pack(xres_[cur], part_, pending, xres_[cur ^ 1], gamma, xn_, frag_, H, T, c_.rms_eps,
+                                  st_);
+            cur ^= 1;
+            pending = 0;
+        } else {
+            rmsnorm_pack(xres_[cur], H, gamma, xn_, frag_, H, T, c_.rms_eps, st_);
+        }
+    }
+
     void linear_parts(const std::vector<Lin>& parts, const std::vector<int>& offs, const float* x32, float* Y,
                       int ldy, int T) {
         for (size_t k = 0; k < parts.size(); ++k) linear(parts[k], x32, Y + offs[k], ldy, parts[k].m, T, kEpiStore);
@@ -752,26 +790,27 @@ class Engine {
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
+        int cur = 0, pending = 0;
         if (feed) copy_int(scal_ + kNextTok, tok_, st_);
-        embed_rows(embed_, embed_kind_, tok_, x_, H, c_.vocab, T, st_);
+        embed_rows(embed_, embed_kind_, tok_, xres_[cur], H, c_.vocab, T, st_);
         for (int i = 0; i < c_.n_layers; ++i) {
             Layer& Ly = L_[i];
-            rmsnorm_pack(x_, H, Ly.attn_norm, xn_, frag_, H, T, eps, st_);
+            norm_residual(cur, pending, Ly.attn_norm, T);
             if (Ly.kind == RL_LAYER_DELTA) {
                 linear_parts(Ly.in_parts, Ly.in_offs, xn_, ybuf_, Ly.in_width, T);
                 gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
                            conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_, s_slot_, R_, o_,
                            T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                 gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
-                linear(Ly.out_proj, xn_, x_, H, H, T, kEpiAdd);
+                pending = linear_residual(Ly.out_proj, xn_, T);
             } else {
                 linear_parts(Ly.qkv_parts, Ly.qkv_offs, xn_, ybuf_, Ly.qkv_width, T);
                 attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
                                   scal_ + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
                                   attn_ws_bytes_, xn_, frag_, st_);
-                linear(Ly.o_proj, xn_, x_, H, H, T, kEpiAdd);
+                pending = linear_residual(Ly.o_proj, xn_, T);
             }
-            rmsnorm_pack(x_, H, Ly.ffn_norm, xn_, frag_, H, T, eps, st_);
+            norm_residual(cur, pending, Ly.ffn_norm, T);
             if (Ly.gate_up.kind >= 0) {
                 linear(Ly.gate_up, xn_, h_, I, I, T, kEpiSwiGLU);
             } else {
@@ -780,9 +819,10 @@ class Engine {
                 swiglu(g_, I, u_, I, h_, I, T, st_);
             }
             if (Ly.down.kind == RL_Q_FP8_E4M3_B128 || Ly.down.kind == RL_Q_BF16) pack_act(h_, frag_, I, T, st_);
-            linear(Ly.down, h_, x_, H, H, T, kEpiAdd);
+            pending = linear_residual(Ly.down, h_, T);
         }
-        rmsnorm_pack(x_, H, final_norm_, xn_, frag_, H, T, eps, st_);
+        norm_residual(cur, pending, final_norm_, T);
+        x_ = xres_[cur];  // hidden after the layers (pre final norm), for the MTP history
         linear(lm_head_, xn_, logits_, c_.vocab, c_.vocab, T, kEpiStore);
         argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
         accept(tok_, preds_, T, force_all, scal_ + kPos, scal_ + kSlot, R_, scal_ + kNCons, scal_ + kNextTok, gen_,
@@ -819,8 +859,22 @@ class Engine {
         launch_captured(100 + n, [&] { mtp_body(n); });
     }
 
+    // RL_HIP_GRAPHS=0 runs every step eagerly (same kernels, launched one by one):
+    // for tools that cannot follow graph launches.
+    static bool graphs_enabled() {
+        static const bool on = [] {
+            const char* v = std::getenv("RL_HIP_GRAPHS");
+            return !(v && v[0] == '0');
+        }();
+        return on;
+    }
+
     template <class F>
     void launch_captured(int key, F body) {
+        if (!graphs_enabled()) {
+            body();
+            return;
+        }
         auto it = graphs_.find(key);
         if (it == graphs_.end()) {
             hipGraph_t g = nullptr;

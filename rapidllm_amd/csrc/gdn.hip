@@ -7,14 +7,14 @@
 // delta_recurrent_step (ops.cpp:495-534).  Output o is the raw recurrent output;
 // the gated RMSNorm is fused into the packing kernel of the next linear (norms.hip).
 //
-// Work split: one workgroup per (v-head h, 32 value columns).  Thread (c, jj)
-// keeps S[h][16c .. 16c+15][32*cg + jj] in registers; column j of S evolves
+// Work split: one workgroup per (v-head h, 16 value columns).  Thread (c, jj)
+// keeps S[h][8c .. 8c+7][16*cg + jj] in registers; column j of S evolves
 // independently given k, q, g, beta and v_j, so the only cross-thread work per
-// token is two 8-lane sums (k^T S and q^T S) done with lane shuffles.
+// token is two 16-lane sums (k^T S and q^T S) done with lane shuffles.
 // The state is read once and written once for all T tokens.
 //
 // State layout in HBM (transposed per head): St[h][j][i] = S[h][i][j], so each
-// thread's 16 values are 64 contiguous bytes and a wave reads 4 KiB contiguously.
+// thread's 8 values are 32 contiguous bytes and a wave reads 2 KiB contiguously.
 // Conv window layout is the reference's [channel][tap] (tap 0 oldest).
 #include "internal.h"
 
@@ -23,7 +23,9 @@ using namespace rl;
 namespace {
 
 constexpr int kDK = 128;    // key head dim (rows of S)
-constexpr int kCols = 32;   // value columns per workgroup
+constexpr int kCols = 16;   // value columns per workgroup
+constexpr int kRowChunks = 16;  // threads per column (8 rows each)
+constexpr int kRowsPer = kDK / kRowChunks;
 constexpr int kMaxT = 8;
 constexpr int kConvK = 4;   // conv taps (Qwen3.6/3.8: 4)
 
@@ -59,8 +61,8 @@ struct GdnArgs {
 
 __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
     const int tid = threadIdx.x;
-    const int c = tid & 7;    // row chunk: rows 16c .. 16c+15
-    const int jj = tid >> 3;  // column within the group
+    const int c = tid & (kRowChunks - 1);  // row chunk: rows 8c .. 8c+7
+    const int jj = tid / kRowChunks;       // column within the group
     const int groups_per_head = p.dv / kCols;
     const int h = blockIdx.x / groups_per_head;
     const int cg = blockIdx.x % groups_per_head;
@@ -89,13 +91,13 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
     };
     const bool per_token = p.cur != nullptr;
 
-    // ---- state: 16 rows of column j, contiguous in the transposed layout
-    const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + 16 * c;
-    float S[16];
+    // ---- state: 8 rows of column j, contiguous in the transposed layout
+    const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + kRowsPer * c;
+    float S[kRowsPer];
     {
         const float4* sp = reinterpret_cast<const float4*>(S_in + s_off);
 #pragma unroll
-        for (int r = 0; r < 4; ++r) {
+        for (int r = 0; r < kRowsPer / 4; ++r) {
             const float4 v = sp[r];
             S[4 * r] = v.x;
             S[4 * r + 1] = v.y;
@@ -183,28 +185,27 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
         const float g = gate_s[t][0], beta = gate_s[t][1];
         float kv = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
+        for (int r = 0; r < kRowsPer; ++r) {
             S[r] *= g;
-            kv += S[r] * k_s[t][16 * c + r];
+            kv += S[r] * k_s[t][kRowsPer * c + r];
         }
-        kv += __shfl_xor(kv, 1, 64);
-        kv += __shfl_xor(kv, 2, 64);
-        kv += __shfl_xor(kv, 4, 64);
+#pragma unroll
+        for (int o = 1; o < kRowChunks; o <<= 1) kv += __shfl_xor(kv, o, 64);
         const float delta = (v_s[t][jj] - kv) * beta;
         float ov = 0.f;
 #pragma unroll
-        for (int r = 0; r < 16; ++r) {
-            S[r] += k_s[t][16 * c + r] * delta;
-            ov += S[r] * q_s[t][16 * c + r];
+        for (int r = 0; r < kRowsPer; ++r) {
+            S[r] += k_s[t][kRowsPer * c + r] * delta;
+            ov += S[r] * q_s[t][kRowsPer * c + r];
         }
-        ov += __shfl_xor(ov, 1, 64);
-        ov += __shfl_xor(ov, 2, 64);
-        ov += __shfl_xor(ov, 4, 64);
+#pragma unroll
+        for (int o = 1; o < kRowChunks; o <<= 1) ov += __shfl_xor(ov, o, 64);
         if (c == 0) p.o[static_cast<size_t>(t) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
         if (per_token || t == T - 1) {
             float4* dp = reinterpret_cast<float4*>(s_dst(t) + s_off);
 #pragma unroll
-            for (int r = 0; r < 4; ++r) dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
+            for (int r = 0; r < kRowsPer / 4; ++r)
+                dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
         }
     }
 }
@@ -218,7 +219,7 @@ void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, con
                 const int* cur, size_t conv_slot, size_t s_slot, int R, float* o, int T, int nk, int nv, int dk,
                 int dv, int K, int v_tiled, hipStream_t s) {
     RL_REQUIRE(dk == kDK, RL_ERR_UNSUPPORTED, "gdn_decode: key head dim must be 128");
-    RL_REQUIRE(dv % kCols == 0 && dv > 0, RL_ERR_UNSUPPORTED, "gdn_decode: value head dim must be a multiple of 32");
+    RL_REQUIRE(dv % 32 == 0 && dv > 0, RL_ERR_UNSUPPORTED, "gdn_decode: value head dim must be a multiple of 32");
     RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode: T must be in 1..8");
     RL_REQUIRE(K == kConvK, RL_ERR_UNSUPPORTED, "gdn_decode: conv width must be 4");
     RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode: nv must be a multiple of nk");

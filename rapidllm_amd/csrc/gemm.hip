@@ -49,7 +49,9 @@ __device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
     hi = __builtin_bit_cast(uint32_t, b);
 }
 
-enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2 };
+// kPartial: split-K over S workgroups per row group; slice s writes its partial sum
+// to Y + (s*T + t)*ldy (the consumer adds the S slices in order).
+enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3 };
 
 // Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
@@ -59,7 +61,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
                                                                 float* __restrict__ Y, int m, int n_kb, int T,
-                                                                int epilogue, int ldy, int m_valid) {
+                                                                int epilogue, int ldy, int m_valid, int S) {
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
     constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
@@ -67,13 +69,16 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     const int g = lane >> 4;
     const int col = lane & 15;
     const int NC = 2 * T;
-    const int rt0 = blockIdx.x * RT;
+    const int slice = blockIdx.x % S;
+    const int rt0 = (blockIdx.x / S) * RT;
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
 
-    // contiguous run of column blocks for this wave
-    const int per = (n_kb + KSPLIT - 1) / KSPLIT;
-    const int kb_begin = min(n_kb, wave * per);
-    const int kb_end = min(n_kb, kb_begin + per);
+    // contiguous run of column blocks for this workgroup's slice, then this wave
+    const int per_s = (n_kb + S - 1) / S;
+    const int s_begin = min(n_kb, slice * per_s), s_end = min(n_kb, s_begin + per_s);
+    const int per = (s_end - s_begin + KSPLIT - 1) / KSPLIT;
+    const int kb_begin = min(s_end, s_begin + wave * per);
+    const int kb_end = min(s_end, kb_begin + per);
 
     f32x4 tot[RT];
 #pragma unroll
@@ -180,7 +185,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
             const int orow = (rt0 + r) * kTileRows + row;
             if (orow < m_valid) {
                 const float val = final_value(r, t, row);
-                float* dst = Y + static_cast<size_t>(t) * ldy + orow;
+                float* dst = Y + (static_cast<size_t>(slice) * T + t) * ldy + orow;
                 if (epilogue == kAdd)
                     *dst += val;
                 else
@@ -294,18 +299,18 @@ static GemmCfg g_force{0, 0, 0};
 
 template <bool kFp8, int RT, int KS, int D>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
-                     int epilogue, int ldy, int m_valid, hipStream_t s) {
+                     int epilogue, int ldy, int m_valid, int S, hipStream_t s) {
     const int groups = (m_tiles_of(m) + RT - 1) / RT;
-    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups), dim3(64 * KS), 0, s,
+    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups * S), dim3(64 * KS), 0, s,
                        static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue, ldy, m_valid);
+                       epilogue, ldy, m_valid, S);
 }
 
 // m = rows of the (tiled) weight; outputs go to Y[t * ldy + row] for row < m_valid
 // (for kSwiGLU, output rows are m/2 and m_valid bounds those).
 template <bool kFp8>
 void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y, int m, int n, int T, int epilogue,
-                 int ldy, int m_valid, hipStream_t s) {
+                 int ldy, int m_valid, hipStream_t s, int S = 1) {
     RL_REQUIRE(m > 0 && n > 0, RL_ERR_RANGE, "gemm: empty shape");
     RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "gemm: T must be in 1..8");
     RL_REQUIRE(W && frag && Y, RL_ERR_RANGE, "gemm: null pointer");
@@ -314,12 +319,13 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     const int m_tiles = m_tiles_of(m);
     if (epilogue == kSwiGLU)
         RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm swiglu: interleaved rows must be a multiple of 32");
-    GemmCfg c{2, (m_tiles + 1) / 2 >= 256 ? 8 : 16, 2};
+    RL_REQUIRE(S >= 1 && (S == 1 || epilogue == kPartial), RL_ERR_RANGE, "gemm: split-K needs the partial epilogue");
+    GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, 2};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
 #define RL_GEMM_CASE(R, K, DD)                                                            \
     if (c.rt == R && c.ks == K && c.d == DD) {                                            \
-        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, s); \
+        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, s); \
         check_launch("gemm_frag_kernel");                                                 \
         return;                                                                           \
     }
@@ -344,12 +350,12 @@ namespace rl {
 size_t act_frag_bytes(int n, int T) { return static_cast<size_t>(n_kb_of(n)) * 16 * 2 * T * 16; }
 // Internal entry points shared with the engine.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   int ldy, int m_valid, hipStream_t s) {
-    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s);
+                   int ldy, int m_valid, hipStream_t s, int S) {
+    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s, S);
 }
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
-                    hipStream_t s) {
-    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s);
+                    hipStream_t s, int S) {
+    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S);
 }
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s) {

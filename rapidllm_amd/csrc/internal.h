@@ -5,13 +5,14 @@
 
 namespace rl {
 
-enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2 };
+enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3 };
 
 // gemm.hip
+// S > 1 (split-K) requires epi == kEpiPartial: slice s writes Y + (s*T + t)*ldy.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   int ldy, int m_valid, hipStream_t s);
+                   int ldy, int m_valid, hipStream_t s, int S = 1);
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
-                    hipStream_t s);
+                    hipStream_t s, int S = 1);
 void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s);
@@ -25,6 +26,11 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
 // norms.hip
 void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
                   hipStream_t s);
+// Residual update fused with the next RMSNorm: x_out = x_in + sum_{s<S} P[s] (rows
+// [T][n], slices P + s*T*n, added in slice order), then y / frag = rmsnorm(x_out).
+// x_out must not alias x_in.  P may be NULL (S ignored).
+void residual_rmsnorm_pack(const float* x_in, const float* P, int S, float* x_out, const float* gamma, float* y,
+                           void* frag, int n, int T, float eps, hipStream_t s);
 void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, int gamma_n, float* y, void* frag,
                 int n, int T, float eps, hipStream_t s);
 void embed_rows(const void* table, int kind, const int* tokens, float* out, int H, int vocab, int T, hipStream_t s);

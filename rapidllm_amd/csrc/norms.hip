@@ -41,60 +41,98 @@ __device__ inline void write_frag8(i32x4* frag, int col8, int t, int T, const fl
     frag[u + T] = mid.q;
 }
 
-__device__ inline double block_sum_d(double v, double* sh) {
-    v = wave_sum_d(v);
-    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
-    __syncthreads();
-    if (lane == 0) sh[wave] = v;
-    __syncthreads();
-    double s = 0.0;
-    for (int w = 0; w < static_cast<int>(blockDim.x >> 6); ++w) s += sh[w];
-    return s;
-}
+// Residual update + Qwen RMSNorm + packing.  One workgroup of 1024 threads per
+// token; thread u owns the 8 columns [8u, 8u+8) (a second pass for n > 8192).  Each
+// thread loads its x and partial-sum slices at once (no serial chain), forms
+// v = x_in + P[0] + ... + P[S-1] in slice order, and the block sums v^2 in double.
+// Columns past n up to the next multiple of 128 are written as zero fragments.
+constexpr int kNormThreads = 1024;
+constexpr int kNormMaxUnits = 2 * kNormThreads;  // n <= 16384
 
-// grid: T workgroups (one per token); n % 8 == 0.  Columns past n up to the next
-// multiple of 128 are written as zeros so the fragment buffer is fully defined.
-__global__ __launch_bounds__(256) void rmsnorm_pack_kernel(const float* __restrict__ x, int ld_x,
-                                                           const float* __restrict__ gamma, float* __restrict__ y,
-                                                           i32x4* __restrict__ frag, int n, int T, float eps) {
-    __shared__ double sh[4];
-    const int t = blockIdx.x;
-    const float* xt = x + static_cast<size_t>(t) * ld_x;
-    double ss = 0.0;
-    for (int i = threadIdx.x; i < n; i += blockDim.x) ss += static_cast<double>(xt[i]) * xt[i];
-    ss = block_sum_d(ss, sh);
-    const float inv = 1.f / sqrtf(static_cast<float>(ss / n) + eps);
+__global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(const float* __restrict__ x_in, int ld_x,
+                                                                        const float* __restrict__ P, int S,
+                                                                        float* __restrict__ x_out,
+                                                                        const float* __restrict__ gamma,
+                                                                        float* __restrict__ y,
+                                                                        i32x4* __restrict__ frag, int n, int T,
+                                                                        float eps) {
+    __shared__ double red[kNormThreads / 64];
+    const int t = blockIdx.x, tid = threadIdx.x;
+    const float* xt = x_in + static_cast<size_t>(t) * ld_x;
+    const size_t pstride = static_cast<size_t>(T) * n;
+    const int nu = n / 8;
     const int units = ((n + kBlockCols - 1) / kBlockCols) * 16;
-    for (int u = threadIdx.x; u < units; u += blockDim.x) {
-        float v[8];
+    float v[2][8];
+    double ss = 0.0;
 #pragma unroll
-        for (int e = 0; e < 8; ++e) {
-            const int i = 8 * u + e;
-            v[e] = i < n ? xt[i] * inv * (gamma ? 1.f + gamma[i] : 1.f) : 0.f;
-            if (y && i < n) y[static_cast<size_t>(t) * n + i] = v[e];
+    for (int pass = 0; pass < 2; ++pass) {
+        const int u = tid + pass * kNormThreads;
+        if (u < nu) {
+            float4 a = reinterpret_cast<const float4*>(xt)[2 * u];
+            float4 b = reinterpret_cast<const float4*>(xt)[2 * u + 1];
+            for (int q = 0; q < S; ++q) {
+                const float4* pp = reinterpret_cast<const float4*>(P + q * pstride + static_cast<size_t>(t) * n);
+                const float4 pa = pp[2 * u], pb = pp[2 * u + 1];
+                a.x += pa.x, a.y += pa.y, a.z += pa.z, a.w += pa.w;
+                b.x += pb.x, b.y += pb.y, b.z += pb.z, b.w += pb.w;
+            }
+            const float r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                v[pass][e] = r[e];
+                ss += static_cast<double>(r[e]) * r[e];
+            }
+            if (x_out) {
+                float4* xo = reinterpret_cast<float4*>(x_out + static_cast<size_t>(t) * n);
+                xo[2 * u] = a;
+                xo[2 * u + 1] = b;
+            }
         }
-        if (frag) write_frag8(frag, u, t, T, v);
+    }
+    ss = wave_sum_d(ss);
+    if ((tid & 63) == 0) red[tid >> 6] = ss;
+    __syncthreads();
+    double tot = 0.0;
+#pragma unroll
+    for (int w = 0; w < kNormThreads / 64; ++w) tot += red[w];
+    const float inv = 1.f / sqrtf(static_cast<float>(tot / n) + eps);
+#pragma unroll
+    for (int pass = 0; pass < 2; ++pass) {
+        const int u = tid + pass * kNormThreads;
+        if (u >= units) continue;
+        float o[8];
+        if (u < nu) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = v[pass][e] * inv * (gamma ? 1.f + gamma[8 * u + e] : 1.f);
+            if (y) {
+                float4* yo = reinterpret_cast<float4*>(y + static_cast<size_t>(t) * n);
+                yo[2 * u] = make_float4(o[0], o[1], o[2], o[3]);
+                yo[2 * u + 1] = make_float4(o[4], o[5], o[6], o[7]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = 0.f;
+        }
+        if (frag) write_frag8(frag, u, t, T, o);
     }
 }
 
-// grid: (segments, T); one workgroup per normalisation segment (a head, or the
-// whole vector).  seg = gamma_n when per_head, else n.
-__global__ __launch_bounds__(256) void gnorm_pack_kernel(const float* __restrict__ o, const float* __restrict__ z,
-                                                         int ld_z, const float* __restrict__ gamma, int gamma_n,
-                                                         int per_head, float* __restrict__ y,
-                                                         i32x4* __restrict__ frag, int n, int T, float eps) {
-    __shared__ double sh[4];
-    const int t = blockIdx.y;
+// Gated RMSNorm + packing.  grid (segments, T), one wave per segment (a head when
+// per_head, else the whole vector).  seg % 8 == 0.
+__global__ __launch_bounds__(64) void gnorm_pack_kernel(const float* __restrict__ o, const float* __restrict__ z,
+                                                        int ld_z, const float* __restrict__ gamma, int gamma_n,
+                                                        int per_head, float* __restrict__ y,
+                                                        i32x4* __restrict__ frag, int n, int T, float eps) {
+    const int t = blockIdx.y, lane = threadIdx.x;
     const int seg = per_head ? gamma_n : n;
     const int h0 = blockIdx.x * seg;
     const float* ot = o + static_cast<size_t>(t) * n;
     const float* zt = z + static_cast<size_t>(t) * ld_z;
     double ss = 0.0;
-    for (int i = threadIdx.x; i < seg; i += blockDim.x) ss += static_cast<double>(ot[h0 + i]) * ot[h0 + i];
-    ss = block_sum_d(ss, sh);
+    for (int i = lane; i < seg; i += 64) ss += static_cast<double>(ot[h0 + i]) * ot[h0 + i];
+    ss = wave_sum_d(ss);
     const float inv = 1.f / sqrtf(static_cast<float>(ss / seg) + eps);
-    // units of 8 columns inside this segment (segments are multiples of 8)
-    for (int u = threadIdx.x; u < seg / 8; u += blockDim.x) {
+    for (int u = lane; u < seg / 8; u += 64) {
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
@@ -105,10 +143,10 @@ __global__ __launch_bounds__(256) void gnorm_pack_kernel(const float* __restrict
         }
         if (frag) write_frag8(frag, (h0 >> 3) + u, t, T, v);
     }
-    // zero the padding columns of the last 128-block once (by the last segment)
+    // zero the padding columns of the last 128-block (last segment only)
     if (frag && blockIdx.x == gridDim.x - 1) {
         const int units = ((n + kBlockCols - 1) / kBlockCols) * 16;
-        for (int u = n / 8 + threadIdx.x; u < units; u += blockDim.x) {
+        for (int u = n / 8 + lane; u < units; u += 64) {
             const float zero8[8] = {0, 0, 0, 0, 0, 0, 0, 0};
             write_frag8(frag, u, t, T, zero8);
         }
@@ -160,13 +198,26 @@ void copy_int(const int* src, int* dst, hipStream_t s) {
     check_launch("copy_int_kernel");
 }
 
+void residual_rmsnorm_pack(const float* x_in, const float* P, int S, float* x_out, const float* gamma, float* y,
+                           void* frag, int n, int T, float eps, hipStream_t s) {
+    RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "rmsnorm: n % 8 == 0, T in 1..8");
+    RL_REQUIRE(x_in && (y || frag || x_out), RL_ERR_RANGE, "rmsnorm: null pointer");
+    RL_REQUIRE(x_out != x_in, RL_ERR_RANGE, "rmsnorm: residual output must not alias the input");
+    RL_REQUIRE(((n + kBlockCols - 1) / kBlockCols) * 16 <= kNormMaxUnits, RL_ERR_RANGE, "rmsnorm: n > 16384");
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, s, x_in, n, P, P ? S : 0, x_out,
+                       gamma, y, static_cast<i32x4*>(frag), n, T, eps);
+    check_launch("residual_rmsnorm_kernel");
+}
+
 void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
                   hipStream_t s) {
     RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "rmsnorm_pack: n % 8 == 0, T in 1..8");
     RL_REQUIRE(x && (y || frag), RL_ERR_RANGE, "rmsnorm_pack: null pointer");
-    hipLaunchKernelGGL(rmsnorm_pack_kernel, dim3(T), dim3(256), 0, s, x, ld_x, gamma, y, static_cast<i32x4*>(frag),
-                       n, T, eps);
-    check_launch("rmsnorm_pack_kernel");
+    RL_REQUIRE(ld_x % 4 == 0, RL_ERR_RANGE, "rmsnorm_pack: row stride must be a multiple of 4");
+    RL_REQUIRE(((n + kBlockCols - 1) / kBlockCols) * 16 <= kNormMaxUnits, RL_ERR_RANGE, "rmsnorm: n > 16384");
+    hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, s, x, ld_x, nullptr, 0, nullptr,
+                       gamma, y, static_cast<i32x4*>(frag), n, T, eps);
+    check_launch("residual_rmsnorm_kernel");
 }
 
 void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, int gamma_n, float* y, void* frag,
@@ -176,8 +227,8 @@ void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, in
     const int seg = per_head ? gamma_n : n;
     RL_REQUIRE(seg % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "gnorm_pack: segment % 8 == 0, T in 1..8");
     RL_REQUIRE(o && z && (y || frag), RL_ERR_RANGE, "gnorm_pack: null pointer");
-    hipLaunchKernelGGL(gnorm_pack_kernel, dim3(n / seg, T), dim3(seg >= 256 ? 256 : 128), 0, s, o, z, ld_z, gamma,
-                       gamma_n, per_head ? 1 : 0, y, static_cast<i32x4*>(frag), n, T, eps);
+    hipLaunchKernelGGL(gnorm_pack_kernel, dim3(n / seg, T), dim3(64), 0, s, o, z, ld_z, gamma, gamma_n,
+                       per_head ? 1 : 0, y, static_cast<i32x4*>(frag), n, T, eps);
     check_launch("gnorm_pack_kernel");
 }
 
