@@ -3,6 +3,8 @@
 // A plain streaming copy and a streaming read of a known number of bytes.  They
 // give the achievable HBM rate on the box and the scale factor between rocprof's
 // FETCH_SIZE / WRITE_SIZE counters and bytes actually moved.
+#include <cstdlib>
+
 #include "common.h"
 
 using namespace rl;
@@ -15,8 +17,8 @@ __global__ void copy_probe_kernel(const i32x4* __restrict__ src, i32x4* __restri
         __builtin_nontemporal_store(__builtin_nontemporal_load(src + i), dst + i);
 }
 
-// Each thread keeps UNROLL independent 16-byte loads in flight.
-template <int UNROLL>
+// Each thread keeps UNROLL independent 16-byte loads in flight.  NT: non-temporal.
+template <int UNROLL, bool NT>
 __global__ void read_probe_kernel(const i32x4* __restrict__ src, size_t n16, unsigned* __restrict__ out) {
     const size_t stride = static_cast<size_t>(gridDim.x) * blockDim.x;
     size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -24,7 +26,7 @@ __global__ void read_probe_kernel(const i32x4* __restrict__ src, size_t n16, uns
     for (; i + (UNROLL - 1) * stride < n16; i += UNROLL * stride) {
         i32x4 v[UNROLL];
 #pragma unroll
-        for (int u = 0; u < UNROLL; ++u) v[u] = __builtin_nontemporal_load(src + i + u * stride);
+        for (int u = 0; u < UNROLL; ++u) v[u] = NT ? __builtin_nontemporal_load(src + i + u * stride) : src[i + u * stride];
 #pragma unroll
         for (int u = 0; u < UNROLL; ++u) acc ^= v[u];
     }
@@ -49,8 +51,17 @@ int rl_hip_copy_probe(const void* src, void* dst, size_t bytes, void* stream) {
 int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream) {
     return guard([&] {
         RL_REQUIRE(bytes % 16 == 0 && src && out4, RL_ERR_RANGE, "read_probe: bytes must be a multiple of 16");
-        hipLaunchKernelGGL(read_probe_kernel<8>, dim3(256 * 8), dim3(256), 0, S(stream),
-                           static_cast<const i32x4*>(src), bytes / 16, static_cast<unsigned*>(out4));
+        // env RL_PROBE_TEMPORAL=1: ordinary loads (allocate in caches) instead of non-temporal
+        static const bool temporal = [] {
+            const char* v = std::getenv("RL_PROBE_TEMPORAL");
+            return v && v[0] == '1';
+        }();
+        if (temporal)
+            hipLaunchKernelGGL((read_probe_kernel<8, false>), dim3(256 * 8), dim3(256), 0, S(stream),
+                               static_cast<const i32x4*>(src), bytes / 16, static_cast<unsigned*>(out4));
+        else
+            hipLaunchKernelGGL((read_probe_kernel<8, true>), dim3(256 * 8), dim3(256), 0, S(stream),
+                               static_cast<const i32x4*>(src), bytes / 16, static_cast<unsigned*>(out4));
         check_launch("read_probe_kernel");
     });
 }

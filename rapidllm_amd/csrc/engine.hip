@@ -353,6 +353,7 @@ class Engine {
     float* x_ = nullptr;     // residual after the last step (set by step())
     float* xn_ = nullptr;   // [Tmax][max_in] fp32 copy of the packed activation
     void* frag_ = nullptr;  // GEMM fragments
+    void* frag_h_ = nullptr;  // fragments of the SwiGLU output (input of mlp.down)
     float* ybuf_ = nullptr; // [Tmax][max_width] fused projection outputs
     float* o_ = nullptr;    // [Tmax][zdim]
     float* h_ = nullptr;    // [Tmax][I]
@@ -521,6 +522,7 @@ class Engine {
         part_ = mem_.get_n<float>(static_cast<size_t>(kSplit) * T * H);
         xn_ = mem_.get_n<float>(static_cast<size_t>(T) * max_in_);
         frag_ = mem_.get(act_frag_bytes(max_in_, T));
+        frag_h_ = mem_.get(act_frag_bytes(I, T));
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
@@ -753,14 +755,15 @@ class Engine {
 
     // Residual-add linear [H rows]: writes partial sums into part_ and returns the
     // number of slices the next residual_rmsnorm_pack must add.
-    int linear_residual(const Lin& L, const float* x32, int T) {
+    int linear_residual(const Lin& L, const float* x32, int T, const void* frag_in = nullptr) {
         const int H = c_.hidden;
+        const void* fr = frag_in ? frag_in : frag_;
         if (L.kind == RL_Q_FP8_E4M3_B128) {
-            gemm_fp8_frag(L.w, L.ts, frag_, part_, L.m, L.n, T, kEpiPartial, H, H, st_, kSplit);
+            gemm_fp8_frag(L.w, L.ts, fr, part_, L.m, L.n, T, kEpiPartial, H, H, st_, kSplit);
             return kSplit;
         }
         if (L.kind == RL_Q_BF16) {
-            gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), frag_, part_, L.m, L.n, T, kEpiPartial, H, H, st_,
+            gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), fr, part_, L.m, L.n, T, kEpiPartial, H, H, st_,
                            kSplit);
             return kSplit;
         }
@@ -811,15 +814,23 @@ class Engine {
                 pending = linear_residual(Ly.o_proj, xn_, T);
             }
             norm_residual(cur, pending, Ly.ffn_norm, T);
+            const bool down_frag = Ly.down.kind == RL_Q_FP8_E4M3_B128 || Ly.down.kind == RL_Q_BF16;
             if (Ly.gate_up.kind >= 0) {
-                linear(Ly.gate_up, xn_, h_, I, I, T, kEpiSwiGLU);
+                // SwiGLU epilogue: fp32 h only when a K-quant down needs it
+                if (Ly.gate_up.kind == RL_Q_FP8_E4M3_B128)
+                    gemm_fp8_frag(Ly.gate_up.w, Ly.gate_up.ts, frag_, down_frag ? nullptr : h_, Ly.gate_up.m,
+                                  Ly.gate_up.n, T, kEpiSwiGLU, I, I, st_, 1, down_frag ? frag_h_ : nullptr);
+                else
+                    gemm_bf16_frag(reinterpret_cast<const uint16_t*>(Ly.gate_up.w), frag_, down_frag ? nullptr : h_,
+                                   Ly.gate_up.m, Ly.gate_up.n, T, kEpiSwiGLU, I, I, st_, 1,
+                                   down_frag ? frag_h_ : nullptr);
             } else {
                 linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
                 linear(Ly.up, xn_, u_, I, I, T, kEpiStore);
                 swiglu(g_, I, u_, I, h_, I, T, st_);
+                if (down_frag) pack_act(h_, frag_h_, I, T, st_);
             }
-            if (Ly.down.kind == RL_Q_FP8_E4M3_B128 || Ly.down.kind == RL_Q_BF16) pack_act(h_, frag_, I, T, st_);
-            pending = linear_residual(Ly.down, h_, T);
+            pending = linear_residual(Ly.down, h_, T, down_frag ? frag_h_ : frag_);
         }
         norm_residual(cur, pending, final_norm_, T);
         x_ = xres_[cur];  // hidden after the layers (pre final norm), for the MTP history

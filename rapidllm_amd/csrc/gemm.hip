@@ -51,6 +51,10 @@ __device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 
 // kPartial: split-K over S workgroups per row group; slice s writes its partial sum
 // to Y + (s*T + t)*ldy (the consumer adds the S slices in order).
+// Weight loads: non-temporal by default (streamed once); temporal when the
+// __constant__ flag is set by rl_hip_set_gemm_config (measurement hook).
+__constant__ int g_temporal_loads = 0;
+
 enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3 };
 
 // Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
@@ -61,7 +65,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
                                                                 float* __restrict__ Y, int m, int n_kb, int T,
-                                                                int epilogue, int ldy, int m_valid, int S) {
+                                                                int epilogue, int ldy, int m_valid, int S,
+                                                                i32x4* __restrict__ frag_out) {
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
     constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
@@ -104,8 +109,10 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         for (int r = 0; r < RT; ++r)
 #pragma unroll
             for (int c = 0; c < NW; ++c)
-                wbuf[d][r][c] = __builtin_nontemporal_load(
-                    reinterpret_cast<const i32x4*>(wbase[r] + static_cast<size_t>(kb) * kTileBytes + c * 1024));
+                wbuf[d][r][c] = g_temporal_loads
+                                    ? *reinterpret_cast<const i32x4*>(wbase[r] + static_cast<size_t>(kb) * kTileBytes + c * 1024)
+                                    : __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
+                                          wbase[r] + static_cast<size_t>(kb) * kTileBytes + c * 1024));
 #pragma unroll
         for (int i = 0; i < 4; ++i) bbuf[d][i] = has_col ? fbase[kb * fstride + i * 4 * NC] : zero4;
     };
@@ -169,14 +176,41 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     auto final_value = [&](int r, int t, int row) -> float { return wg_value(r, t, row); };
 
     if (epilogue == kSwiGLU) {
-        // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs
+        // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs.
+        // h = silu(g) * u goes to Y (fp32, if given) and, if frag_out is given, to the
+        // bf16 hi/mid fragments of the next linear (input column = output row).
+        __shared__ float hsh[RT / 2 > 0 ? RT / 2 : 1][8][kTileRows];
         for (int it = threadIdx.x; it < (RT / 2) * T * kTileRows; it += 64 * KSPLIT) {
             const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
             const int orow = ((rt0 + 2 * r) / 2) * kTileRows + row;
+            float h = 0.f;
             if (rt0 + 2 * r + 1 < m_tiles && orow < m_valid) {
                 const float gv = final_value(2 * r, t, row);
                 const float uv = final_value(2 * r + 1, t, row);
-                Y[static_cast<size_t>(t) * ldy + orow] = gv / (1.f + __expf(-gv)) * uv;
+                h = gv / (1.f + __expf(-gv)) * uv;
+                if (Y) Y[static_cast<size_t>(t) * ldy + orow] = h;
+            }
+            hsh[r][t][row] = h;
+        }
+        if (frag_out) {
+            __syncthreads();
+            // units of 8 output columns: (r, t, half)
+            for (int it = threadIdx.x; it < (RT / 2) * T * 2; it += 64 * KSPLIT) {
+                const int half = it & 1, t = (it >> 1) % T, r = (it >> 1) / T;
+                const int ptile = (rt0 + 2 * r) / 2;
+                if (rt0 + 2 * r + 1 >= m_tiles) continue;
+                union {
+                    uint16_t h[8];
+                    i32x4 v;
+                } hi, mid;
+#pragma unroll
+                for (int e = 0; e < 8; ++e) split_bf16(hsh[r][t][8 * half + e], hi.h[e], mid.h[e]);
+                const int col8 = 2 * ptile + half;
+                const int kb = col8 >> 4, jb = (col8 & 15) * 8;
+                const int g2 = jb >> 5, i2 = (jb >> 3) & 3;
+                const size_t u = ((static_cast<size_t>(kb) * 4 + i2) * 4 + g2) * (2 * T) + t;
+                frag_out[u] = hi.v;
+                frag_out[u + T] = mid.v;
             }
         }
     } else {
@@ -299,21 +333,23 @@ static GemmCfg g_force{0, 0, 0};
 
 template <bool kFp8, int RT, int KS, int D>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
-                     int epilogue, int ldy, int m_valid, int S, hipStream_t s) {
+                     int epilogue, int ldy, int m_valid, int S, void* frag_out, hipStream_t s) {
     const int groups = (m_tiles_of(m) + RT - 1) / RT;
     hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups * S), dim3(64 * KS), 0, s,
                        static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue, ldy, m_valid, S);
+                       epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out));
 }
 
 // m = rows of the (tiled) weight; outputs go to Y[t * ldy + row] for row < m_valid
 // (for kSwiGLU, output rows are m/2 and m_valid bounds those).
 template <bool kFp8>
 void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y, int m, int n, int T, int epilogue,
-                 int ldy, int m_valid, hipStream_t s, int S = 1) {
+                 int ldy, int m_valid, hipStream_t s, int S = 1, void* frag_out = nullptr) {
     RL_REQUIRE(m > 0 && n > 0, RL_ERR_RANGE, "gemm: empty shape");
     RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "gemm: T must be in 1..8");
-    RL_REQUIRE(W && frag && Y, RL_ERR_RANGE, "gemm: null pointer");
+    RL_REQUIRE(W && frag && (Y || frag_out), RL_ERR_RANGE, "gemm: null pointer");
+    RL_REQUIRE(!frag_out || epilogue == kSwiGLU, RL_ERR_RANGE, "gemm: fragment output only with the SwiGLU epilogue");
+    RL_REQUIRE(!frag_out || frag_out != frag, RL_ERR_RANGE, "gemm: fragment output must not alias the input");
     RL_REQUIRE(!kFp8 || tscale, RL_ERR_RANGE, "gemm: FP8 weights need tile scales");
     const int n_kb = n_kb_of(n);
     const int m_tiles = m_tiles_of(m);
@@ -325,7 +361,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
 #define RL_GEMM_CASE(R, K, DD)                                                            \
     if (c.rt == R && c.ks == K && c.d == DD) {                                            \
-        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, s); \
+        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, s); \
         check_launch("gemm_frag_kernel");                                                 \
         return;                                                                           \
     }
@@ -350,12 +386,12 @@ namespace rl {
 size_t act_frag_bytes(int n, int T) { return static_cast<size_t>(n_kb_of(n)) * 16 * 2 * T * 16; }
 // Internal entry points shared with the engine.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   int ldy, int m_valid, hipStream_t s, int S) {
-    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s, S);
+                   int ldy, int m_valid, hipStream_t s, int S, void* frag_out) {
+    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out);
 }
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
-                    hipStream_t s, int S) {
-    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S);
+                    hipStream_t s, int S, void* frag_out) {
+    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out);
 }
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s) {
@@ -380,6 +416,13 @@ extern "C" {
 int rl_hip_set_gemm_config(int row_tiles, int k_waves, int depth) {
     g_force = GemmCfg{row_tiles, k_waves, depth > 0 ? depth : 2};
     return RL_OK;
+}
+
+int rl_hip_set_gemm_load_policy(int temporal) {
+    return guard([&] {
+        const int v = temporal ? 1 : 0;
+        RL_HIP(hipMemcpyToSymbol(HIP_SYMBOL(g_temporal_loads), &v, sizeof(int)));
+    });
 }
 
 size_t rl_hip_fp8_packed_bytes(int m, int n) { return static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 2048; }

@@ -9,10 +9,11 @@ enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3 
 
 // gemm.hip
 // S > 1 (split-K) requires epi == kEpiPartial: slice s writes Y + (s*T + t)*ldy.
+// frag_out (SwiGLU only): also write h as the next linear's input fragments.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   int ldy, int m_valid, hipStream_t s, int S = 1);
+                   int ldy, int m_valid, hipStream_t s, int S = 1, void* frag_out = nullptr);
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
-                    hipStream_t s, int S = 1);
+                    hipStream_t s, int S = 1, void* frag_out = nullptr);
 void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s);
