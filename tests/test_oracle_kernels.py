@@ -400,3 +400,22 @@ def test_accept_prefix(orc):
     assert acc([7, 1, 2, 3], [1, 5, 3, 9]) == 2
     assert acc([7, 1, 2, 3], [0, 2, 3, 9]) == 1
     assert acc([7], [4]) == 1
+
+
+def test_oracle_model_tiny_hybrid_golden(orc):
+    """Whole-model pin: the oracle model reproduces the reference golden script's
+    greedy tokens (forward(), tiny_hybrid.py:221-354) and MTP stem drafts
+    (mtp_draft_py(), tiny_hybrid.py:357-430) on its 8-layer hybrid fixture."""
+    from oracle.oracle import OracleModel
+    from tests.tiny_hybrid import load
+
+    spec, W, meta = load()
+    m = OracleModel(spec, W, ctx=64, kv_fp16=False, threads=1)
+    got, _, _ = m.generate(meta["prompt_ids"], len(meta["greedy_ids"]))
+    assert got == meta["greedy_ids"]
+    m.reset()
+    for t in meta["prompt_ids"]:
+        g, _, _ = m.decode(t)
+    assert g == meta["greedy_ids"][0]
+    drafts = m.mtp_draft(g, 3).tolist()
+    assert drafts == meta["mtp_draft_ids"]
