@@ -56,8 +56,14 @@ def step_bytes(spec, T, ctx):
     return {"linears": lin, "lm_head": head, "kv": kv, "state": state, "total": lin + head + kv + state}
 
 
+EPI_STORE, EPI_SWIGLU, EPI_PARTIAL = 0, 2, 3
+SPLIT = 4  # split-K of the residual-add GEMMs in the step (partials summed by the next norm)
+
+
 def gemm_shapes(spec):
-    """(m, n, count per step) of the block-FP8 GEMM launches in one step."""
+    """(m, n, count per step, epilogue) of the block-FP8 GEMM launches in one step,
+    as the engine issues them: fused [qkv|z|a|b] and [q|gate;k;v] stores, split-K
+    partials for the residual GEMMs, interleaved gate/up with the SwiGLU epilogue."""
     H, I = spec.hidden, spec.intermediate
     nv, dv = spec.n_v_heads, spec.v_dim
     nq, nkv, hd = spec.n_q, spec.n_kv, spec.head_dim
@@ -66,46 +72,61 @@ def gemm_shapes(spec):
     a16 = lambda v: (v + 15) // 16 * 16
     m_in = a16(spec.conv_dim) + a16(nv * dv) + 2 * a16(nv)
     return [
-        (m_in, H, n_d), (H, nv * dv, n_d),
-        (2 * nq * hd + 2 * nkv * hd, H, n_a), (H, nq * hd, n_a),
-        (2 * a16(I), H, spec.n_layers), (H, I, spec.n_layers),
+        (m_in, H, n_d, EPI_STORE), (H, nv * dv, n_d, EPI_PARTIAL),
+        (2 * nq * hd + 2 * nkv * hd, H, n_a, EPI_STORE), (H, nq * hd, n_a, EPI_PARTIAL),
+        (2 * a16(I), H, spec.n_layers, EPI_SWIGLU), (H, I, spec.n_layers, EPI_PARTIAL),
     ]
 
 
-def measure_gemm(spec, T, iters=30):
-    """Average duration (HIP events on the launch stream) of the block-FP8 GEMM over
-    the step's launch mix, each shape timed standalone with its step's count."""
-    from rapidllm_amd import hip, ops, synth
-    from rapidllm_amd.hip import DeviceBuffer, Timer, call
+def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
+    """Average duration of the block-FP8 GEMM over the step's launch mix: per shape,
+    `iters` back-to-back launches from C++ (rl_hip_time_gemm_fp8: HIP events on the
+    launch stream around the loop), each with the epilogue the step uses.
+
+    Each shape cycles through enough copies of its packed weight (>= rotate_bytes,
+    three times the 256 MB Infinity Cache) that every launch reads its weight from
+    HBM, as in the decode step; the cache-resident figure (one copy re-read) is
+    reported beside it as "warm_us"."""
+    import ctypes as C
+
+    from rapidllm_amd import ops, synth
+    from rapidllm_amd.hip import DeviceBuffer, call
 
     r = synth.rng(5)
     tot_ms = tot_bytes = 0.0
     n_launch = 0
     per = []
     s = C_stream()
-    for m, n, count in gemm_shapes(spec):
+    for m, n, count, epi in gemm_shapes(spec):
         W = synth.fp8_weight(r, m, n)
         sc = synth.fp8_scales(r, m, n)
         lin = ops.Fp8Linear(W, sc)
+        nb = lin.w.nbytes
+        copies = [lin.w] + [DeviceBuffer(nb) for _ in range(max(1, -(-rotate_bytes // nb)) - 1)]
+        for c in copies[1:]:
+            call("rl_hip_memcpy_d2d", c.ptr, lin.w.ptr, nb, s)
         X = r.standard_normal((T, n)).astype(np.float32)
         xd = DeviceBuffer.from_numpy(X)
         frag = ops.act_frag_buffer(n, T)
-        yd = DeviceBuffer(4 * T * m)
+        yd = DeviceBuffer(4 * T * m * SPLIT)
+        fo = ops.act_frag_buffer(m // 2, T) if epi == EPI_SWIGLU else None
         call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, s)
-        for _ in range(5):
-            lin.forward_frag(frag.ptr, yd.ptr, T, stream=s)
-        tm = Timer(s)
-        tm.start()
-        for _ in range(iters):
-            lin.forward_frag(frag.ptr, yd.ptr, T, stream=s)
-        ms = tm.stop() / iters
+        ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
+        one = (C.c_void_p * 1)(lin.w.ptr)
+        ms, warm = C.c_float(), C.c_float()
+        args = (lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr if fo else None, m, n, T, epi, SPLIT)
+        call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, len(copies), s, C.byref(ms))  # warm-up
+        call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, iters, s, C.byref(ms))
+        call("rl_hip_time_gemm_fp8", one, 1, *args, iters, s, C.byref(warm))
+        ms, warm = ms.value, warm.value
         b = m * n + 4 * ((m + 127) // 128) * ((n + 127) // 128) + 4 * T * (m + n)
-        per.append({"m": m, "n": n, "per_step": count, "us": round(ms * 1e3, 2),
-                    "GBps": round(b / ms / 1e6, 1)})
+        per.append({"m": m, "n": n, "epilogue": {0: "store", 2: "swiglu", 3: f"split{SPLIT}"}[epi],
+                    "per_step": count, "us": round(ms * 1e3, 2), "GBps": round(b / ms / 1e6, 1),
+                    "warm_us": round(warm * 1e3, 2), "copies": len(copies)})
         tot_ms += ms * count
         tot_bytes += b * count
         n_launch += count
-        del lin, xd, frag, yd
+        del lin, xd, frag, yd, fo, copies
     avg_ms = tot_ms / n_launch
     avg_bytes = tot_bytes / n_launch
     return avg_ms, avg_bytes, per
@@ -123,6 +144,38 @@ def C_stream():
         call("rl_hip_stream_create", C.byref(p))
         _stream = p.value
     return _stream
+
+
+def copy_probe(mib, reps=10):
+    """A plain 16-byte-vector device copy of known size: the scale for the
+    FETCH_SIZE / WRITE_SIZE counters (each copy reads and writes mib MiB once)."""
+    from rapidllm_amd.hip import DeviceBuffer, Timer, call
+
+    n = mib << 20
+    a, b = DeviceBuffer(n), DeviceBuffer(n)
+    s = C_stream()
+    call("rl_hip_memset", a.ptr, 1, n, s)
+    tm = Timer(s)
+    tm.start()
+    for _ in range(reps):
+        call("rl_hip_copy_probe", a.ptr, b.ptr, n, s)
+    ms = tm.stop() / reps
+    print(json.dumps({"copy_bytes_each_way": n, "us": round(ms * 1e3, 2), "GBps_rd_plus_wr": round(2 * n / ms / 1e6, 1)}))
+
+
+TRAFFIC_FILE = os.path.join(ROOT, "profiles", "gemm_fp8_t1_mix_traffic.txt")
+
+
+def measured_traffic():
+    """HBM bytes per launch of the roofline kernel, from the committed counter
+    summary (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE, scaled by the copy kernel)."""
+    try:
+        for line in open(TRAFFIC_FILE):
+            if line.startswith("traffic_bytes_per_launch"):
+                return int(float(line.split("=")[1]))
+    except OSError:
+        pass
+    return None
 
 
 def cpu_baseline(spec, sbytes_total, budget_s=20.0):
@@ -174,6 +227,10 @@ def main():
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--layers", type=int, default=64)
+    ap.add_argument("--gemm-only", action="store_true",
+                    help="time only the block-FP8 GEMM launch mix (the roofline kernel), for counter runs")
+    ap.add_argument("--copy-probe-mb", type=int, default=0,
+                    help="run only a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(f"bench.py: this build runs on one GPU; --gpus {args.gpus} is not supported "
@@ -186,6 +243,13 @@ def main():
 
     hip.require_gpu()
     spec = ModelSpec(n_layers=args.layers)
+    if args.copy_probe_mb:
+        copy_probe(args.copy_probe_mb)
+        return
+    if args.gemm_only:
+        g_ms, g_bytes, per = measure_gemm(spec, 1, iters=args.steps)
+        print(json.dumps({"avg_launch_us": round(g_ms * 1e3, 2), "bytes_per_launch": int(g_bytes), "shapes": per}))
+        return
     t0 = time.time()
     eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234)
     build_s = time.time() - t0
@@ -211,9 +275,9 @@ def main():
     b1 = step_bytes(spec, 1, CTX)
     b4 = step_bytes(spec, 4, CTX)
     g_ms, g_bytes, per = measure_gemm(spec, 1)
-    roof = {"bound": "hbm", "kernel": "gemm_frag_kernel (block-FP8, T=1 step launch mix)",
+    roof = {"bound": "hbm", "kernel": "gemm_frag_kernel (block-FP8, T=1 step launch mix, weights read from HBM)",
             "achieved": round(g_bytes / g_ms / 1e6, 1), "peak": PEAK_GBS, "unit": "GB/s",
-            "frac": round(g_bytes / g_ms / 1e6 / PEAK_GBS, 4), "traffic": None,
+            "frac": round(g_bytes / g_ms / 1e6 / PEAK_GBS, 4), "traffic": measured_traffic(),
             "bytes_per_launch": int(g_bytes), "avg_launch_us": round(g_ms * 1e3, 2), "shapes": per}
     out = {
         "metric": METRIC,

@@ -237,6 +237,16 @@ void* rl_hip_engine_stream(RlEngine* e);
 int rl_hip_copy_probe(const void* src, void* dst, size_t bytes, void* stream);
 int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
 
+/* GEMM timing (no counterpart in the reference): `iters` back-to-back launches of the
+ * block-FP8 GEMM on `stream`, launch i reading weight copy i % n_copies (so weights
+ * come from HBM, not from the Infinity Cache), with one event pair around the loop;
+ * *avg_ms = average launch duration.  epilogue: 0 store (Y [T][m]), 3 split-K
+ * partials (Y [split][T][m]), 2 SwiGLU over interleaved gate/up tiles writing the
+ * next linear's fragments to frag_out (act_frag_bytes(m/2, T)). */
+int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
+                         float* Y, void* frag_out, int m, int n, int T, int epilogue, int split, int iters,
+                         void* stream, float* avg_ms);
+
 #ifdef __cplusplus
 }
 #endif

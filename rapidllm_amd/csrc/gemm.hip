@@ -61,7 +61,11 @@ enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3 };
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
 // weights in flight while one is computed).
 template <int RT, int KSPLIT, int D, bool kFp8>
-__global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* __restrict__ W,
+// FP8, 8-wave, depth <= 2 variants: at least 6 waves per SIMD (<= 80 VGPRs), i.e. three
+// 512-thread workgroups per CU, so the common launches (<= 768 workgroups) are
+// resident at once with no second-round tail.
+__global__ __launch_bounds__(64 * KSPLIT)
+__attribute__((amdgpu_waves_per_eu((kFp8 && RT <= 2 && KSPLIT == 8 && D <= 2) ? 6 : 1))) void gemm_frag_kernel(const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
                                                                 float* __restrict__ Y, int m, int n_kb, int T,
@@ -70,7 +74,10 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
     constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
-    const int wave = threadIdx.x >> 6;
+    // wave-uniform: keeps the column-block bounds, the tile-scale loads and the loop
+    // control in scalar registers (scale loads then wait on their own counter and
+    // never on the weight loads queued behind them)
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4;
     const int col = lane & 15;
     const int NC = 2 * T;
@@ -89,32 +96,46 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 #pragma unroll
     for (int r = 0; r < RT; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
-    const bool has_col = col < NC;
-    const i32x4 zero4 = {0, 0, 0, 0};
+    // Lanes of B columns >= 2T read a valid column: those MFMA output columns are
+    // never used, and unconditional loads keep the load count identical on every
+    // path, so the compiler's waits stay exact.
+    const int bcol = min(col, NC - 1);
     const uint8_t* wbase[RT];
     const float* sbase[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) {
         const int rt = min(rt0 + r, m_tiles - 1);
-        wbase[r] = W + static_cast<size_t>(rt) * n_kb * kTileBytes + 16 * lane;
+        wbase[r] = W + static_cast<size_t>(rt) * n_kb * kTileBytes;  // uniform tile-row base
         sbase[r] = kFp8 ? tscale + static_cast<size_t>(rt) * n_kb : nullptr;
     }
-    const i32x4* fbase = frag + static_cast<size_t>(g) * NC + col;
+    const i32x4* fbase = frag + static_cast<size_t>(g) * NC + bcol;
     const size_t fstride = static_cast<size_t>(16) * NC;  // per column block
 
     i32x4 wbuf[D][RT][NW];
     i32x4 bbuf[D][4];
-    auto load = [&](int d, int kb) {
+    float sbuf[D][RT];
+    // kb >= kb_end: a pipeline slot past the wave's range.  Its loads still issue (so
+    // the load count is the same on every path) but read the small, cache-resident
+    // activation fragments instead of weights; the values are never used.
+    // (the fragments hold n_kb * 512 * T bytes; narrower inputs use this group's
+    // first weight tile instead)
+    const uint8_t* dummy = n_kb * 512 * T >= kTileBytes ? reinterpret_cast<const uint8_t*>(frag) : wbase[0];
+    auto load = [&](int d, int kb, bool live) {
+        if constexpr (kFp8) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) sbuf[d][r] = sbase[r][live ? kb : 0];
+        }
 #pragma unroll
         for (int r = 0; r < RT; ++r)
 #pragma unroll
-            for (int c = 0; c < NW; ++c)
-                wbuf[d][r][c] = g_temporal_loads
-                                    ? *reinterpret_cast<const i32x4*>(wbase[r] + static_cast<size_t>(kb) * kTileBytes + c * 1024)
-                                    : __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
-                                          wbase[r] + static_cast<size_t>(kb) * kTileBytes + c * 1024));
+            for (int c = 0; c < NW; ++c) {
+                const uint8_t* base = live ? wbase[r] + static_cast<size_t>(kb) * kTileBytes : dummy;
+                const i32x4* p = reinterpret_cast<const i32x4*>(base + c * 1024) + lane;
+                wbuf[d][r][c] = g_temporal_loads ? *p : __builtin_nontemporal_load(p);
+            }
+        kb = live ? kb : 0;
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bbuf[d][i] = has_col ? fbase[kb * fstride + i * 4 * NC] : zero4;
+        for (int i = 0; i < 4; ++i) bbuf[d][i] = fbase[kb * fstride + i * 4 * NC];
     };
     auto compute = [&](int d, int kb) {
 #pragma unroll
@@ -136,21 +157,31 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
             }
             if constexpr (kFp8)
-                tot[r] += sbase[r][kb] * acc;
+                tot[r] += sbuf[d][r] * acc;
             else
                 tot[r] += acc;
         }
     };
 
+    // Software pipeline, D stages.
+    if (kb_begin < kb_end) {
 #pragma unroll
-    for (int d = 0; d < D; ++d)
-        if (kb_begin + d < kb_end) load(d, kb_begin + d);
-    for (int kb = kb_begin; kb < kb_end; kb += D) {
+        for (int d = 0; d < D; ++d) load(d, kb_begin + d, kb_begin + d < kb_end);
+        // Phase order pinned (compiler memory barrier + scheduling barrier): no
+        // load may move past a compute phase, or the in-order load counter would
+        // make that compute wait for the loads queued behind its own.
+        if constexpr (D > 1) asm volatile("" ::: "memory");
+        for (int kb = kb_begin; kb < kb_end; kb += D) {
 #pragma unroll
-        for (int d = 0; d < D; ++d) {
-            if (kb + d < kb_end) {
-                compute(d, kb + d);
-                if (kb + d + D < kb_end) load(d, kb + d + D);
+            for (int d = 0; d < D; ++d) {
+                if constexpr (D > 1) __builtin_amdgcn_sched_barrier(0);
+                if (kb + d < kb_end) compute(d, kb + d);
+                if constexpr (D > 1) {
+                    asm volatile("" ::: "memory");
+                    __builtin_amdgcn_sched_barrier(0);
+                }
+                load(d, kb + d + D, kb + d + D < kb_end);
+                if constexpr (D > 1) asm volatile("" ::: "memory");
             }
         }
     }
@@ -323,9 +354,10 @@ inline int n_kb_of(int n) { return (n + kBlockCols - 1) / kBlockCols; }
 inline int m_tiles_of(int m) { return (m + kTileRows - 1) / kTileRows; }
 
 // Work split per launch: row-tiles per workgroup (RT), waves per workgroup along K
-// (KS), load pipeline depth (D).  Measured on MI355X (17408x5120 / 5120x17408,
-// T=1..4): RT=2, D=2 with 8 waves is best when there are >= 256 workgroups; short
-// m (fewer workgroups than CUs) does better with 16 waves per workgroup.
+// (KS), load pipeline depth (D).  Measured on MI355X with weights cold in HBM
+// (16480/34816 x 5120, 5120 x 17408/6144, T=1..4): RT=2 with 8 waves is best when
+// there are >= 256 workgroups; short m (fewer workgroups than CUs) does better
+// with 16 waves per workgroup.
 struct GemmCfg {
     int rt, ks, d;
 };
@@ -356,7 +388,11 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     if (epilogue == kSwiGLU)
         RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm swiglu: interleaved rows must be a multiple of 32");
     RL_REQUIRE(S >= 1 && (S == 1 || epilogue == kPartial), RL_ERR_RANGE, "gemm: split-K needs the partial epilogue");
-    GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, 2};
+    // FP8 launches are one round of workgroups (all resident); depth 1 (loads
+    // scheduled by the compiler) measured best there: 19.3 us vs 24.2 us (depth 2)
+    // for 16480x5120 with weights cold in HBM.  BF16 (lm_head: many rounds) keeps
+    // depth 2 (6.4 TB/s).
+    GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, kFp8 ? 1 : 2};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
 #define RL_GEMM_CASE(R, K, DD)                                                            \
@@ -366,7 +402,8 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
         return;                                                                           \
     }
     RL_GEMM_CASE(2, 8, 2) RL_GEMM_CASE(2, 16, 2) RL_GEMM_CASE(2, 4, 2) RL_GEMM_CASE(1, 8, 2)
-    RL_GEMM_CASE(1, 16, 2) RL_GEMM_CASE(2, 8, 3)
+    RL_GEMM_CASE(1, 16, 2) RL_GEMM_CASE(2, 8, 3) RL_GEMM_CASE(2, 8, 1) RL_GEMM_CASE(2, 16, 1) RL_GEMM_CASE(2, 4, 1)
+    RL_GEMM_CASE(2, 4, 3) RL_GEMM_CASE(2, 4, 4) RL_GEMM_CASE(4, 4, 2) RL_GEMM_CASE(4, 8, 1)
 #undef RL_GEMM_CASE
     throw Error(RL_ERR_UNSUPPORTED, "gemm: unsupported work split");
 }

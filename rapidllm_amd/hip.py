@@ -88,6 +88,7 @@ _SIGS = {
     "rl_hip_engine_stream": (_vp, [_vp]),
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
+    "rl_hip_time_gemm_fp8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp, C.POINTER(C.c_float)]),
     "rl_hip_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
 }
 
@@ -198,6 +199,12 @@ class Timer:
 
     def stop(self) -> float:
         call("rl_hip_event_record", self.b, self.stream)
+        ms = C.c_float()
+        call("rl_hip_event_elapsed_ms", self.a, self.b, C.byref(ms))
+        return ms.value
+
+    def elapsed(self) -> float:
+        """ms between the two recorded events (waits for the second)."""
         ms = C.c_float()
         call("rl_hip_event_elapsed_ms", self.a, self.b, C.byref(ms))
         return ms.value
