@@ -10,7 +10,7 @@
 // build with -ffp-contract=off and without -mfma (oracle/Makefile), as the
 // reference's scalar TU is built (CMakeLists.txt:20-70: no ISA flags on ops.cpp).
 //
-// Pinning (tests/test_oracle_*.py):
+// Pinning (tests/test_oracle_kernels.py, tests/test_golden_vectors.py):
 //   e4m3/fp16 decode     exhaustive vs closed form + numpy float16 + oracle/_ref
 //   fp8 GEMV             brute force in exact rational arithmetic (tiny) + _ref
 //   Q4_K / Q6_K dequant  bit-exact vs _ref + hand-built blocks with known values
@@ -18,6 +18,8 @@
 //   attention            _ref + softmax closed forms (uniform keys, one-hot)
 //   model forward / MTP  tiny-hybrid greedy tokens from the reference's golden
 //                        generator (tests/golden/) + greedy invariant
+//   committed vectors    tests/golden/ref_vectors.npz from the _ref kernels, so the
+//                        oracle stays pinned where the reference tree is absent
 #include "../include/rl_model.h"
 
 #include <algorithm>

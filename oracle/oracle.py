@@ -58,6 +58,8 @@ def lib():
         L.orc_gemv_q4_k.argtypes = [_u8, _f, _f, C.c_int, C.c_int, C.c_int]
         L.orc_gemv_q6_k.argtypes = [_u8, _f, _f, C.c_int, C.c_int, C.c_int]
         L.orc_gemv_bf16.argtypes = [_u16, _f, _f, C.c_int, C.c_int, C.c_int]
+        L.orc_gemv_f16.argtypes = [_u16, _f, _f, C.c_int, C.c_int]
+        L.orc_gemv_f32.argtypes = [_f, _f, _f, C.c_int, C.c_int]
         L.orc_qwen3_rmsnorm.argtypes = [_f, _f, _f, C.c_int, C.c_float]
         L.orc_gated_rmsnorm.argtypes = [_f, _f, _f, _f, C.c_int, C.c_float, C.c_int]
         L.orc_l2norm.argtypes = [_f, _f, C.c_int, C.c_float]
@@ -180,6 +182,35 @@ def gemv_bf16(W, x, threads=1):
     y = np.empty(m, np.float32)
     lib().orc_gemv_bf16(P(W, _u16), P(f32(x)), P(y), m, n, threads)
     return y
+
+
+def gemv_f16(W, x):
+    m, n = W.shape
+    y = np.empty(m, np.float32)
+    lib().orc_gemv_f16(P(W, _u16), P(f32(x)), P(y), m, n)
+    return y
+
+
+def gemv_f32(W, x):
+    m, n = W.shape
+    y = np.empty(m, np.float32)
+    lib().orc_gemv_f32(P(f32(W)), P(f32(x)), P(y), m, n)
+    return y
+
+
+def swiglu(g, u):
+    g = f32(g)
+    y = np.empty_like(g)
+    lib().orc_swiglu(P(g), P(f32(u)), P(y), g.size)
+    return y
+
+
+def argmax_rows(logits):
+    logits = f32(logits)
+    rows, V = logits.shape
+    out = np.empty(rows, np.int32)
+    lib().orc_argmax_rows(P(logits), rows, V, out.ctypes.data_as(_i32))
+    return out
 
 
 def qwen3_rmsnorm(x, gamma, eps=1e-6):

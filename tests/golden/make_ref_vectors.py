@@ -118,6 +118,12 @@ def main():
     o = np.empty(nq * hd, np.float32)
     R.ref_attn_decode(P(q), P(kc), P(vc), P(o), L - 1, nq, nkv, hd)
     v.update({"attn.q": q, "attn.kc": kc, "attn.vc": vc, "attn.o": o})
+    # SwiGLU silu(g) * u (ops.cpp:607-609)
+    g = (r.standard_normal(512) * 4).astype(np.float32)
+    u = r.standard_normal(512).astype(np.float32)
+    y = np.empty_like(g)
+    R.ref_swiglu(P(g), P(u), P(y), 512)
+    v.update({"swiglu.g": g, "swiglu.u": u, "swiglu.y": y})
     # greedy argmax with ties
     lg = r.integers(-4, 4, 3000).astype(np.float32)
     v.update({"greedy.x": lg, "greedy.i": np.array([R.ref_greedy(P(lg), lg.size)], np.int32)})

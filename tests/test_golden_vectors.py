@@ -96,3 +96,7 @@ def test_attn_decode():
 
 def test_greedy():
     assert O.greedy(V["greedy.x"]) == int(V["greedy.i"][0])
+
+
+def test_swiglu():
+    eq(O.swiglu(V["swiglu.g"], V["swiglu.u"]), V["swiglu.y"])

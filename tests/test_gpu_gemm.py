@@ -91,3 +91,68 @@ def test_gemm_bf16_vs_oracle(gpu, orc, m, n, T):
     for t in range(T):
         yo = orc.gemv_bf16(Wb, X[t])
         assert rel_l2(Y[t], yo) <= REL_L2
+
+
+def _time_gemm(lin, X, epi, split=4, frag_out=None):
+    """One launch through rl_hip_time_gemm_fp8 (iters=1): exposes the split-K and
+    SwiGLU epilogues the engine uses on the real GEMM kernel."""
+    import ctypes as C
+
+    from rapidllm_amd.hip import DeviceBuffer, call
+
+    T, n = X.shape
+    m = lin.m
+    xd = DeviceBuffer.from_numpy(np.ascontiguousarray(X, np.float32))
+    frag = ops.act_frag_buffer(n, T)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
+    rows = split * T * m if epi == 3 else T * (m // 2 if epi == 2 else m)
+    yd = DeviceBuffer(4 * rows)
+    yd.zero()
+    ptrs = (C.c_void_p * 1)(lin.w.ptr)
+    ms = C.c_float()
+    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, m, n, T, epi, split, 1, None,
+         C.byref(ms))
+    return yd.numpy(np.float32, (rows,))
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_gemm_fp8_split_k_partials(gpu, orc, T):
+    """Split-K epilogue (residual GEMMs: out_proj, o_proj, down): 4 partial slices
+    whose sum is the product, as the next RMSNorm kernel consumes them."""
+    r = synth.rng(300 + T)
+    m, n = 5120, 6144
+    W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    lin = ops.Fp8Linear(W, s)
+    P = _time_gemm(lin, X, 3).reshape(4, T, m)
+    Yo = orc.gemm_fp8(W, s, X)
+    Y = P.astype(np.float64).sum(0)
+    for t in range(T):
+        assert rel_l2(Y[t], Yo[t]) <= REL_L2, (t, rel_l2(Y[t], Yo[t]))
+    assert np.any(P[1] != 0) and np.any(P[3] != 0)  # every slice did work
+
+
+@pytest.mark.parametrize("T", [1, 3])
+def test_gemm_fp8_swiglu_epilogue(gpu, orc, T):
+    """Gate/up interleaved by 16-row tile, SwiGLU in the epilogue:
+    h = silu(gate . x) * (up . x) (ops_fused.cpp:66-82, ops.cpp:607-609)."""
+    r = synth.rng(400 + T)
+    I, n = 512, 1024
+    Wg, Wu = synth.fp8_weight(r, I, n), synth.fp8_weight(r, I, n)
+    # one scale per column block for every row, so row interleaving keeps the
+    # 128x128 scale blocks valid for both source matrices
+    col_s = synth.fp8_scales(r, 128, n)[0]
+    sg = np.tile(col_s, (I // 128, 1))
+    Wi = np.empty((2 * I, n), np.uint8)
+    for k in range(I // 16):
+        Wi[32 * k:32 * k + 16] = Wg[16 * k:16 * k + 16]
+        Wi[32 * k + 16:32 * k + 32] = Wu[16 * k:16 * k + 16]
+    lin = ops.Fp8Linear(Wi, np.tile(col_s, (2 * I // 128, 1)))
+    X = r.standard_normal((T, n)).astype(np.float32)
+    H = _time_gemm(lin, X, 2).reshape(T, I)
+    g = orc.gemm_fp8(Wg, sg, X).astype(np.float64)
+    u = orc.gemm_fp8(Wu, sg, X).astype(np.float64)
+    with np.errstate(over="ignore"):
+        want = g / (1 + np.exp(-g)) * u
+    for t in range(T):
+        assert rel_l2(H[t], want[t]) <= REL_L2, (t, rel_l2(H[t], want[t]))

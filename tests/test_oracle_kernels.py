@@ -419,3 +419,35 @@ def test_oracle_model_tiny_hybrid_golden(orc):
     assert g == meta["greedy_ids"][0]
     drafts = m.mtp_draft(g, 3).tolist()
     assert drafts == meta["mtp_draft_ids"]
+
+
+def test_gemm_fp8_rows_are_gemv(orc):
+    """The T-row oracle GEMM is T independent GEMVs (the reference's CUDA T=4 verify
+    runs four T=1 GEMVs, cuda_engine.cu:11997-12005), bit for bit."""
+    r = synth.rng(21)
+    m, n = 48, 384
+    W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n)
+    X = r.standard_normal((4, n)).astype(np.float32)
+    Y = orc.gemm_fp8(W, s, X)
+    for t in range(4):
+        assert np.array_equal(Y[t], orc.gemv_fp8(W, s, X[t]))
+
+
+def test_dense_gemv_f16_f32_error_bound(orc):
+    """F16 / F32 linears (float accumulator, ops.cpp:165-172 restated for f32 in
+    double): against an exact float64 product within fp32 summation error."""
+    r = synth.rng(22)
+    m, n = 16, 300
+    W = r.standard_normal((m, n)).astype(np.float16)
+    x = r.standard_normal(n).astype(np.float32)
+    exact = W.astype(np.float64) @ x.astype(np.float64)
+    bound = 1.2e-7 * n * (np.abs(W.astype(np.float64)) @ np.abs(x.astype(np.float64)))
+    assert np.all(np.abs(orc.gemv_f16(W.view(np.uint16), x) - exact) <= bound)
+    W32 = W.astype(np.float32)
+    assert np.all(np.abs(orc.gemv_f32(W32, x) - exact) <= bound)
+
+
+def test_argmax_rows_matches_numpy(orc):
+    r = synth.rng(23)
+    L = r.integers(-5, 5, (6, 1000)).astype(np.float32)
+    assert np.array_equal(orc.argmax_rows(L), np.argmax(L, axis=1))
