@@ -354,6 +354,12 @@ class Engine {
     float* xn_ = nullptr;   // [Tmax][max_in] fp32 copy of the packed activation
     void* frag_ = nullptr;  // GEMM fragments
     void* frag_h_ = nullptr;  // fragments of the SwiGLU output (input of mlp.down)
+    // RMSNorm folded into the GEMMs (all layer linears FP8 / BF16): the residual
+    // GEMMs write x in place plus frag_x_ = fragments of x * (1 + next gamma) and
+    // ss_ = per-group sums of x^2; the next GEMM scales its outputs by 1/rms.
+    bool fold_norm_ = false;
+    void* frag_x_ = nullptr;
+    float* ss_ = nullptr;  // [add_norm_groups(H)][Tmax]
     float* ybuf_ = nullptr; // [Tmax][max_width] fused projection outputs
     float* o_ = nullptr;    // [Tmax][zdim]
     float* h_ = nullptr;    // [Tmax][I]
@@ -523,6 +529,11 @@ class Engine {
         xn_ = mem_.get_n<float>(static_cast<size_t>(T) * max_in_);
         frag_ = mem_.get(act_frag_bytes(max_in_, T));
         frag_h_ = mem_.get(act_frag_bytes(I, T));
+        frag_x_ = mem_.get(act_frag_bytes(H, T));
+        ss_ = mem_.get_n<float>(static_cast<size_t>(add_norm_groups(H)) * T);
+        // RL_FOLD_NORM=0 keeps the separate RMSNorm kernels (for A/B measurement)
+        const char* fold_env = std::getenv("RL_FOLD_NORM");
+        fold_norm_ = can_fold_norm() && !(fold_env && fold_env[0] == '0');
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
@@ -789,7 +800,84 @@ class Engine {
         for (size_t k = 0; k < parts.size(); ++k) linear(parts[k], x32, Y + offs[k], ldy, parts[k].m, T, kEpiStore);
     }
 
+    static bool frag_kind(const Lin& L) { return L.kind == RL_Q_FP8_E4M3_B128 || L.kind == RL_Q_BF16; }
+
+    // The folded-norm step needs every linear that reads or writes the residual
+    // stream on the fragment path, one fused input projection per layer, and an
+    // interleaved gate/up; otherwise the step keeps the separate norm kernels.
+    bool can_fold_norm() const {
+        if (!frag_kind(lm_head_) || add_norm_groups(c_.hidden) > 256 || tmax_ > 8) return false;
+        for (const Layer& Ly : L_) {
+            const auto& in = Ly.kind == RL_LAYER_DELTA ? Ly.in_parts : Ly.qkv_parts;
+            const Lin& res = Ly.kind == RL_LAYER_DELTA ? Ly.out_proj : Ly.o_proj;
+            if (in.size() != 1 || !frag_kind(in[0]) || !frag_kind(res) || !frag_kind(Ly.down)) return false;
+            if (Ly.gate_up.kind < 0 || !frag_kind(Ly.gate_up)) return false;
+        }
+        return true;
+    }
+
+    // FP8 / BF16 GEMM on given input fragments.
+    void gemm_on(const Lin& L, const void* fr, float* Y, int ldy, int m_valid, int T, int epi,
+                 void* frag_out = nullptr, const NormIO* io = nullptr) {
+        if (L.kind == RL_Q_FP8_E4M3_B128)
+            gemm_fp8_frag(L.w, L.ts, fr, Y, L.m, L.n, T, epi, ldy, m_valid, st_, 1, frag_out, io);
+        else
+            gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), fr, Y, L.m, L.n, T, epi, ldy, m_valid, st_, 1,
+                           frag_out, io);
+    }
+
+    // One step with the RMSNorms folded into the GEMMs (see fold_norm_): per layer
+    // in_proj/qkv -> mixer -> out/o_proj (+= x) -> gate/up -> down (+= x).
+    void step_folded(int T, int force_all, bool feed) {
+        const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
+        const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
+        const float eps = c_.rms_eps;
+        float* x = xres_[0];
+        if (feed) copy_int(scal_ + kNextTok, tok_, st_);
+        embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, T, st_);
+        rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_x_, H, T, eps, st_);
+        NormIO in;
+        in.ss_in = ss_;
+        in.groups_in = add_norm_groups(H);
+        in.n_norm = H;
+        in.eps = eps;
+        for (int i = 0; i < c_.n_layers; ++i) {
+            Layer& Ly = L_[i];
+            const NormIO* io_in = i == 0 ? nullptr : &in;  // layer 0 reads normalised fragments
+            NormIO out;
+            out.gamma_out = Ly.ffn_norm;
+            out.ss_out = ss_;
+            if (Ly.kind == RL_LAYER_DELTA) {
+                gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, T, kEpiStore, nullptr, io_in);
+                gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
+                           conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_, s_slot_, R_, o_,
+                           T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
+                gemm_on(Ly.out_proj, frag_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
+            } else {
+                gemm_on(Ly.qkv_parts[0], frag_x_, ybuf_, Ly.qkv_width, Ly.qkv_parts[0].m, T, kEpiStore, nullptr,
+                        io_in);
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
+                                  scal_ + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                                  attn_ws_bytes_, xn_, frag_, st_);
+                gemm_on(Ly.o_proj, frag_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
+            }
+            gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, T, kEpiSwiGLU, frag_h_, &in);
+            out.gamma_out = i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_;
+            gemm_on(Ly.down, frag_h_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
+        }
+        x_ = x;  // hidden after the layers (pre final norm), for the MTP history
+        gemm_on(lm_head_, frag_x_, logits_, c_.vocab, c_.vocab, T, kEpiStore, nullptr, &in);
+        argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
+        accept(tok_, preds_, T, force_all, scal_ + kPos, scal_ + kSlot, R_, scal_ + kNCons, scal_ + kNextTok, gen_,
+               scal_ + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
+    }
+
     void step(int T, int force_all, bool feed) {
+        if (fold_norm_) {
+            step_folded(T, force_all, feed);
+            return;
+        }
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;

@@ -55,22 +55,18 @@ __device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 // __constant__ flag is set by rl_hip_set_gemm_config (measurement hook).
 __constant__ int g_temporal_loads = 0;
 
-enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3 };
+enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4 };
 
 // Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
 // weights in flight while one is computed).
 template <int RT, int KSPLIT, int D, bool kFp8>
-// FP8, 8-wave, depth <= 2 variants: at least 6 waves per SIMD (<= 80 VGPRs), i.e. three
-// 512-thread workgroups per CU, so the common launches (<= 768 workgroups) are
-// resident at once with no second-round tail.
-__global__ __launch_bounds__(64 * KSPLIT)
-__attribute__((amdgpu_waves_per_eu((kFp8 && RT <= 2 && KSPLIT == 8 && D <= 2) ? 6 : 1))) void gemm_frag_kernel(const uint8_t* __restrict__ W,
+__global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
                                                                 float* __restrict__ Y, int m, int n_kb, int T,
                                                                 int epilogue, int ldy, int m_valid, int S,
-                                                                i32x4* __restrict__ frag_out) {
+                                                                i32x4* __restrict__ frag_out, NormIO io) {
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
     constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
@@ -95,6 +91,21 @@ __attribute__((amdgpu_waves_per_eu((kFp8 && RT <= 2 && KSPLIT == 8 && D <= 2) ? 
     f32x4 tot[RT];
 #pragma unroll
     for (int r = 0; r < RT; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    // RMSNorm folded into this GEMM (io.ss_in): the input fragments hold x * (1+gamma)
+    // unnormalised, and the outputs are scaled by 1/rms(x_t).  Wave w < T sums the
+    // producer's per-group sums of squares of token w (issued here, consumed in the
+    // epilogue, so the loads overlap the weight stream).
+    constexpr int kMaxSsPerLane = 4;  // groups <= 256
+    float ssv[kMaxSsPerLane];
+    const bool ss_wave = io.ss_in && wave < T;
+    if (ss_wave) {
+#pragma unroll
+        for (int k = 0; k < kMaxSsPerLane; ++k) {
+            const int gi = lane + 64 * k;
+            ssv[k] = gi < io.groups_in ? io.ss_in[static_cast<size_t>(gi) * T + wave] : 0.f;
+        }
+    }
 
     // Lanes of B columns >= 2T read a valid column: those MFMA output columns are
     // never used, and unconditional loads keep the load count identical on every
@@ -189,8 +200,16 @@ __attribute__((amdgpu_waves_per_eu((kFp8 && RT <= 2 && KSPLIT == 8 && D <= 2) ? 
     // Cross-wave reduction in a fixed order.  red[w][r][lane] holds C rows
     // 4*(lane/16)+v, column lane%16.
     __shared__ f32x4 red[KSPLIT][RT][64];
+    __shared__ float s_inv[8];
 #pragma unroll
     for (int r = 0; r < RT; ++r) red[wave][r][lane] = tot[r];
+    if (ss_wave) {
+        double ss = 0.0;
+#pragma unroll
+        for (int k = 0; k < kMaxSsPerLane; ++k) ss += static_cast<double>(ssv[k]);  // group order
+        ss = wave_sum_d(ss);                                  // fixed butterfly order
+        if (lane == 0) s_inv[wave] = 1.f / sqrtf(static_cast<float>(ss / io.n_norm) + io.eps);
+    }
     __syncthreads();
 
     // items: (r, t, row); value = hi column + mid column, summed over waves
@@ -204,7 +223,10 @@ __attribute__((amdgpu_waves_per_eu((kFp8 && RT <= 2 && KSPLIT == 8 && D <= 2) ? 
         return s;
     };
 
-    auto final_value = [&](int r, int t, int row) -> float { return wg_value(r, t, row); };
+    auto final_value = [&](int r, int t, int row) -> float {
+        const float v = wg_value(r, t, row);
+        return io.ss_in ? v * s_inv[t] : v;
+    };
 
     if (epilogue == kSwiGLU) {
         // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs.
@@ -243,6 +265,52 @@ __attribute__((amdgpu_waves_per_eu((kFp8 && RT <= 2 && KSPLIT == 8 && D <= 2) ? 
                 frag_out[u] = hi.v;
                 frag_out[u + T] = mid.v;
             }
+        }
+    } else if (epilogue == kAddNorm) {
+        // Residual add fused with the next RMSNorm's data movement: x += W.a in place
+        // (one writer per row), then for the next linear: fragments of x * (1 + gamma)
+        // (its input columns = these rows) and this group's sum of x^2 per token,
+        // summed in double over the rows in order, stored as float (io.ss_out[group][t]).
+        __shared__ float xsh[RT][8][kTileRows];
+        for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
+            const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
+            const int orow = (rt0 + r) * kTileRows + row;
+            float x = 0.f;
+            if (rt0 + r < m_tiles && orow < m_valid) {
+                float* dst = Y + static_cast<size_t>(t) * ldy + orow;
+                x = *dst + final_value(r, t, row);
+                *dst = x;
+            }
+            xsh[r][t][row] = x;
+        }
+        __syncthreads();
+        if (threadIdx.x < T) {
+            const int t = threadIdx.x;
+            double ss = 0.0;
+            for (int r = 0; r < RT; ++r)
+                for (int row = 0; row < kTileRows; ++row) ss += static_cast<double>(xsh[r][t][row]) * xsh[r][t][row];
+            io.ss_out[static_cast<size_t>(blockIdx.x) * T + t] = static_cast<float>(ss);
+        }
+        // units of 8 columns: (r, t, half)
+        for (int it = threadIdx.x; it < RT * T * 2; it += 64 * KSPLIT) {
+            const int half = it & 1, t = (it >> 1) % T, r = (it >> 1) / T;
+            if (rt0 + r >= m_tiles) continue;
+            union {
+                uint16_t h[8];
+                i32x4 v;
+            } hi, mid;
+            const int c0 = (rt0 + r) * kTileRows + 8 * half;
+#pragma unroll
+            for (int e = 0; e < 8; ++e) {
+                const float g = c0 + e < m_valid ? 1.f + io.gamma_out[c0 + e] : 0.f;
+                split_bf16(xsh[r][t][8 * half + e] * g, hi.h[e], mid.h[e]);
+            }
+            const int col8 = c0 >> 3;
+            const int kb = col8 >> 4, jb = (col8 & 15) * 8;
+            const int g2 = jb >> 5, i2 = (jb >> 3) & 3;
+            const size_t u = ((static_cast<size_t>(kb) * 4 + i2) * 4 + g2) * (2 * T) + t;
+            frag_out[u] = hi.v;
+            frag_out[u + T] = mid.v;
         }
     } else {
         for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
@@ -365,22 +433,29 @@ static GemmCfg g_force{0, 0, 0};
 
 template <bool kFp8, int RT, int KS, int D>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
-                     int epilogue, int ldy, int m_valid, int S, void* frag_out, hipStream_t s) {
+                     int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
     const int groups = (m_tiles_of(m) + RT - 1) / RT;
     hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups * S), dim3(64 * KS), 0, s,
                        static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out));
+                       epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out), io);
 }
 
 // m = rows of the (tiled) weight; outputs go to Y[t * ldy + row] for row < m_valid
 // (for kSwiGLU, output rows are m/2 and m_valid bounds those).
 template <bool kFp8>
 void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y, int m, int n, int T, int epilogue,
-                 int ldy, int m_valid, hipStream_t s, int S = 1, void* frag_out = nullptr) {
+                 int ldy, int m_valid, hipStream_t s, int S = 1, void* frag_out = nullptr,
+                 const NormIO* norm = nullptr) {
+    const NormIO io = norm ? *norm : NormIO{};
     RL_REQUIRE(m > 0 && n > 0, RL_ERR_RANGE, "gemm: empty shape");
     RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "gemm: T must be in 1..8");
     RL_REQUIRE(W && frag && (Y || frag_out), RL_ERR_RANGE, "gemm: null pointer");
-    RL_REQUIRE(!frag_out || epilogue == kSwiGLU, RL_ERR_RANGE, "gemm: fragment output only with the SwiGLU epilogue");
+    RL_REQUIRE(!frag_out || epilogue == kSwiGLU || epilogue == kAddNorm, RL_ERR_RANGE,
+               "gemm: fragment output only with the SwiGLU / add-norm epilogues");
+    RL_REQUIRE(epilogue != kAddNorm || (Y && frag_out && io.gamma_out && io.ss_out && S == 1), RL_ERR_RANGE,
+               "gemm add-norm: needs Y, fragment output, gamma and the sum-of-squares output, no split");
+    RL_REQUIRE(!io.ss_in || (io.groups_in >= 1 && io.groups_in <= 256 && io.n_norm > 0), RL_ERR_RANGE,
+               "gemm: folded RMSNorm needs 1..256 partial groups");
     RL_REQUIRE(!frag_out || frag_out != frag, RL_ERR_RANGE, "gemm: fragment output must not alias the input");
     RL_REQUIRE(!kFp8 || tscale, RL_ERR_RANGE, "gemm: FP8 weights need tile scales");
     const int n_kb = n_kb_of(n);
@@ -395,15 +470,17 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, kFp8 ? 1 : 2};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
+    if (epilogue == kAddNorm) c.rt = 2;  // the sum-of-squares groups are 2 row tiles (add_norm_groups)
+    if (io.ss_in || epilogue == kAddNorm)
+        RL_REQUIRE(c.ks >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
 #define RL_GEMM_CASE(R, K, DD)                                                            \
     if (c.rt == R && c.ks == K && c.d == DD) {                                            \
-        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, s); \
+        launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); \
         check_launch("gemm_frag_kernel");                                                 \
         return;                                                                           \
     }
-    RL_GEMM_CASE(2, 8, 2) RL_GEMM_CASE(2, 16, 2) RL_GEMM_CASE(2, 4, 2) RL_GEMM_CASE(1, 8, 2)
-    RL_GEMM_CASE(1, 16, 2) RL_GEMM_CASE(2, 8, 3) RL_GEMM_CASE(2, 8, 1) RL_GEMM_CASE(2, 16, 1) RL_GEMM_CASE(2, 4, 1)
-    RL_GEMM_CASE(2, 4, 3) RL_GEMM_CASE(2, 4, 4) RL_GEMM_CASE(4, 4, 2) RL_GEMM_CASE(4, 8, 1)
+    RL_GEMM_CASE(2, 8, 1) RL_GEMM_CASE(2, 16, 1) RL_GEMM_CASE(2, 8, 2) RL_GEMM_CASE(2, 16, 2)
+    RL_GEMM_CASE(2, 4, 1) RL_GEMM_CASE(2, 4, 2) RL_GEMM_CASE(1, 8, 1) RL_GEMM_CASE(1, 16, 1)
 #undef RL_GEMM_CASE
     throw Error(RL_ERR_UNSUPPORTED, "gemm: unsupported work split");
 }
@@ -423,13 +500,14 @@ namespace rl {
 size_t act_frag_bytes(int n, int T) { return static_cast<size_t>(n_kb_of(n)) * 16 * 2 * T * 16; }
 // Internal entry points shared with the engine.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   int ldy, int m_valid, hipStream_t s, int S, void* frag_out) {
-    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out);
+                   int ldy, int m_valid, hipStream_t s, int S, void* frag_out, const NormIO* norm) {
+    launch_gemm<true>(W, ts, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out, norm);
 }
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
-                    hipStream_t s, int S, void* frag_out) {
-    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out);
+                    hipStream_t s, int S, void* frag_out, const NormIO* norm) {
+    launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out, norm);
 }
+int add_norm_groups(int m) { return (m_tiles_of(m) + 1) / 2; }
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s) {
     const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;

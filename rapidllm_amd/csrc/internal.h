@@ -5,15 +5,33 @@
 
 namespace rl {
 
-enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3 };
+enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3, kEpiAddNorm = 4 };
+
+// RMSNorm folded across a residual GEMM and the next linear (y = rmsnorm(x) * (1+g)
+// never materialised):
+//   producer (kEpiAddNorm): Y = x += W.a in place; frag_out = fragments of
+//     x * (1 + gamma_out); ss_out[group][t] = sum of x^2 over the group's rows
+//     (add_norm_groups(m) groups of 32 rows, summed in double, stored as float);
+//   consumer (ss_in != null): its input fragments are x * (1 + gamma); outputs are
+//     scaled by 1/sqrt(sum_groups ss_in / n_norm + eps) per token.
+struct NormIO {
+    const float* ss_in = nullptr;
+    int groups_in = 0;
+    int n_norm = 0;
+    float eps = 0.f;
+    const float* gamma_out = nullptr;
+    float* ss_out = nullptr;
+};
 
 // gemm.hip
 // S > 1 (split-K) requires epi == kEpiPartial: slice s writes Y + (s*T + t)*ldy.
-// frag_out (SwiGLU only): also write h as the next linear's input fragments.
+// frag_out (SwiGLU / add-norm): also write the next linear's input fragments.
 void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                   int ldy, int m_valid, hipStream_t s, int S = 1, void* frag_out = nullptr);
+                   int ldy, int m_valid, hipStream_t s, int S = 1, void* frag_out = nullptr,
+                   const NormIO* norm = nullptr);
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
-                    hipStream_t s, int S = 1, void* frag_out = nullptr);
+                    hipStream_t s, int S = 1, void* frag_out = nullptr, const NormIO* norm = nullptr);
+int add_norm_groups(int m);
 void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s);

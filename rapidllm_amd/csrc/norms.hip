@@ -48,6 +48,7 @@ __device__ inline void write_frag8(i32x4* frag, int col8, int t, int T, const fl
 // Columns past n up to the next multiple of 128 are written as zero fragments.
 constexpr int kNormThreads = 1024;
 constexpr int kNormMaxUnits = 2 * kNormThreads;  // n <= 16384
+constexpr int kNormMaxSplit = 4;                 // split-K partial slices
 
 __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(const float* __restrict__ x_in, int ld_x,
                                                                         const float* __restrict__ P, int S,
@@ -70,11 +71,24 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(const fl
         if (u < nu) {
             float4 a = reinterpret_cast<const float4*>(xt)[2 * u];
             float4 b = reinterpret_cast<const float4*>(xt)[2 * u + 1];
-            for (int q = 0; q < S; ++q) {
-                const float4* pp = reinterpret_cast<const float4*>(P + q * pstride + static_cast<size_t>(t) * n);
-                const float4 pa = pp[2 * u], pb = pp[2 * u + 1];
-                a.x += pa.x, a.y += pa.y, a.z += pa.z, a.w += pa.w;
-                b.x += pb.x, b.y += pb.y, b.z += pb.z, b.w += pb.w;
+            // all partial slices are loaded before the first add: one memory round
+            // trip instead of S dependent ones; the sum keeps slice order
+            float4 pa[kNormMaxSplit], pb[kNormMaxSplit];
+#pragma unroll
+            for (int q = 0; q < kNormMaxSplit; ++q) {
+                if (q < S) {
+                    const float4* pp =
+                        reinterpret_cast<const float4*>(P + q * pstride + static_cast<size_t>(t) * n);
+                    pa[q] = pp[2 * u];
+                    pb[q] = pp[2 * u + 1];
+                }
+            }
+#pragma unroll
+            for (int q = 0; q < kNormMaxSplit; ++q) {
+                if (q < S) {
+                    a.x += pa[q].x, a.y += pa[q].y, a.z += pa[q].z, a.w += pa[q].w;
+                    b.x += pb[q].x, b.y += pb[q].y, b.z += pb[q].z, b.w += pb[q].w;
+                }
             }
             const float r[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
 #pragma unroll
@@ -128,6 +142,18 @@ __global__ __launch_bounds__(64) void gnorm_pack_kernel(const float* __restrict_
     const int h0 = blockIdx.x * seg;
     const float* ot = o + static_cast<size_t>(t) * n;
     const float* zt = z + static_cast<size_t>(t) * ld_z;
+    // segments up to 512 (the common case: 128-wide heads): the lane's z and gamma
+    // are loaded together with o, before the reduction
+    float zp[8], gp[8];
+    const bool pre = seg <= 512 && lane < seg / 8;
+    if (pre) {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int i = h0 + 8 * lane + e;
+            zp[e] = zt[i];
+            gp[e] = gamma ? gamma[per_head ? (i - h0) : (i % gamma_n)] : 1.f;
+        }
+    }
     double ss = 0.0;
     for (int i = lane; i < seg; i += 64) ss += static_cast<double>(ot[h0 + i]) * ot[h0 + i];
     ss = wave_sum_d(ss);
@@ -137,8 +163,10 @@ __global__ __launch_bounds__(64) void gnorm_pack_kernel(const float* __restrict_
 #pragma unroll
         for (int e = 0; e < 8; ++e) {
             const int i = h0 + 8 * u + e;
-            const float g = gamma ? gamma[per_head ? (i - h0) : (i % gamma_n)] : 1.f;
-            v[e] = g * (ot[i] * inv) * silu_f(zt[i]);
+            const bool p = pre && u == lane;
+            const float g = p ? gp[e] : (gamma ? gamma[per_head ? (i - h0) : (i % gamma_n)] : 1.f);
+            const float zz = p ? zp[e] : zt[i];
+            v[e] = g * (ot[i] * inv) * silu_f(zz);
             if (y) y[static_cast<size_t>(t) * n + i] = v[e];
         }
         if (frag) write_frag8(frag, (h0 >> 3) + u, t, T, v);
@@ -203,6 +231,7 @@ void residual_rmsnorm_pack(const float* x_in, const float* P, int S, float* x_ou
     RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "rmsnorm: n % 8 == 0, T in 1..8");
     RL_REQUIRE(x_in && (y || frag || x_out), RL_ERR_RANGE, "rmsnorm: null pointer");
     RL_REQUIRE(x_out != x_in, RL_ERR_RANGE, "rmsnorm: residual output must not alias the input");
+    RL_REQUIRE(!P || (S >= 1 && S <= kNormMaxSplit), RL_ERR_RANGE, "rmsnorm: 1..4 partial slices");
     RL_REQUIRE(((n + kBlockCols - 1) / kBlockCols) * 16 <= kNormMaxUnits, RL_ERR_RANGE, "rmsnorm: n > 16384");
     hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, s, x_in, n, P, P ? S : 0, x_out,
                        gamma, y, static_cast<i32x4*>(frag), n, T, eps);

@@ -134,3 +134,30 @@ def test_other_weight_formats_match_oracle(gpu, orc, quant):
         eng.decode_token(g)
         g, lg, _ = orc_m.decode(g)
         assert rel_l2(eng.copy_logits(), lg) < TOL
+
+
+def test_norm_kernels_and_folded_norm_agree(gpu, orc, monkeypatch):
+    """The step with RMSNorm folded into the GEMMs (default for FP8 / BF16 models)
+    and the step with separate norm kernels (RL_FOLD_NORM=0) both match the oracle
+    on the same model, at T=1 and in a T=4 verify."""
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=11, w_scale=(1e-3, 1e-2))
+    orc_m = OracleModel(spec, W, ctx=512)
+    prompt = [3, 1, 4, 1, 5, 9, 2]
+    orc_m.reset()
+    for t in prompt:
+        g, lg, _ = orc_m.decode(t)
+    outs = []
+    for fold in ("1", "0"):
+        monkeypatch.setenv("RL_FOLD_NORM", fold)
+        eng = Engine(spec, W, ctx=512)
+        eng.prefill(prompt)
+        assert rel_l2(eng.copy_logits(), lg) < TOL, fold
+        if margin_ok(lg):
+            assert eng.greedy() == g
+        toks = [g, 7, 8, 9]
+        n, preds = eng.spec_verify(toks)
+        outs.append((eng.copy_logits(), list(preds[:n]), n))
+        eng.close()
+    assert outs[0][1:] == outs[1][1:]
+    assert rel_l2(outs[0][0], outs[1][0]) < TOL
