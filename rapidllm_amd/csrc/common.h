@@ -100,3 +100,26 @@ __device__ inline void split_bf16(float x, uint16_t& hi, uint16_t& mid) {
     const float r = x - __uint_as_float(xb & 0xffff0000u);
     mid = static_cast<uint16_t>(__float_as_uint(r) >> 16);
 }
+
+// Fragment unit (16 B = 8 bf16) holding columns [8u, 8u+8) of token t, hi part.
+// The mid part sits T units later.  Layout of the GEMM input
+// fragments (pack_act_kernel, gemm.hip): [kb][i][g][2T][8 bf16].
+__device__ inline size_t frag_unit(int col8, int t, int T) {
+    const int kb = col8 >> 4;           // 16 units per 128-column block
+    const int jb = (col8 & 15) * 8;     // first column within the block
+    const int g = jb >> 5, i = (jb >> 3) & 3;
+    return ((static_cast<size_t>(kb) * 4 + i) * 4 + g) * (2 * T) + t;
+}
+
+__device__ inline void write_frag8(i32x4* frag, int col8, int t, int T, const float (&v)[8]) {
+    union {
+        uint16_t h[8];
+        i32x4 q;
+    } hi, mid;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_bf16(v[e], hi.h[e], mid.h[e]);
+    const size_t u = frag_unit(col8, t, T);
+    frag[u] = hi.q;
+    frag[u + T] = mid.q;
+}
+

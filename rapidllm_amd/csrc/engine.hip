@@ -358,6 +358,7 @@ class Engine {
     // GEMMs write x in place plus frag_x_ = fragments of x * (1 + next gamma) and
     // ss_ = per-group sums of x^2; the next GEMM scales its outputs by 1/rms.
     bool fold_norm_ = false;
+    bool gdn_fused_norm_ = false;
     void* frag_x_ = nullptr;
     float* ss_ = nullptr;  // [add_norm_groups(H)][Tmax]
     float* ybuf_ = nullptr; // [Tmax][max_width] fused projection outputs
@@ -534,6 +535,15 @@ class Engine {
         // RL_FOLD_NORM=0 keeps the separate RMSNorm kernels (for A/B measurement)
         const char* fold_env = std::getenv("RL_FOLD_NORM");
         fold_norm_ = can_fold_norm() && !(fold_env && fold_env[0] == '0');
+        // per-head gated norm (gamma of dv values, zdim >= 256: ops.cpp:129-156) in the
+        // DeltaNet kernel, when one workgroup can hold a head
+        {
+            const int zd = c_.n_v_heads * c_.v_dim;
+            bool per_head = gdn_head_supported(c_.k_dim, c_.v_dim, c_.conv_k) && zd >= 256;
+            for (const Layer& Ly : L_)
+                if (Ly.kind == RL_LAYER_DELTA && Ly.gnorm_n != c_.v_dim) per_head = false;
+            gdn_fused_norm_ = fold_norm_ && per_head;
+        }
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
@@ -849,10 +859,19 @@ class Engine {
             out.ss_out = ss_;
             if (Ly.kind == RL_LAYER_DELTA) {
                 gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, T, kEpiStore, nullptr, io_in);
-                gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
-                           conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_, s_slot_, R_, o_,
-                           T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
-                gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
+                if (gdn_fused_norm_) {
+                    // recurrent update + per-head gated RMSNorm + out_proj packing in one kernel
+                    gdn_decode_head(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
+                                    Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot,
+                                    conv_slot_, s_slot_, R_, nullptr, ybuf_ + Ly.off_z, Ly.gnorm, frag_, T, nk, nv,
+                                    c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                } else {
+                    gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
+                               Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_,
+                               s_slot_, R_, o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                    gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f,
+                               st_);
+                }
                 gemm_on(Ly.out_proj, frag_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
             } else {
                 gemm_on(Ly.qkv_parts[0], frag_x_, ybuf_, Ly.qkv_width, Ly.qkv_parts[0].m, T, kEpiStore, nullptr,

@@ -106,6 +106,16 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
         }
     }
 
+    // gate inputs of token tid, loaded with the state (before any store of this
+    // thread, whose completion a later wait would otherwise include)
+    float gin_a = 0.f, gin_b = 0.f, gin_A = 0.f, gin_dt = 0.f;
+    if (tid < T) {
+        gin_a = p.a[static_cast<size_t>(tid) * p.ld_in + h];
+        gin_b = p.b[static_cast<size_t>(tid) * p.ld_in + h];
+        gin_A = p.A_log[h];
+        gin_dt = p.dt_bias[h];
+    }
+
     // ---- conv1d over T tokens for the 2*128 q/k channels of the source k-head and
     // the 32 v channels of this workgroup (288 channels, 256 threads).
     // The q/k window state is written back only by one workgroup per source head.
@@ -127,11 +137,27 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
             win[2] = wv.z;
             win[3] = wv.w;
         }
-        const float* w = p.conv_w + static_cast<size_t>(chan) * K;
-        for (int t = 0; t < T; ++t) {
+        // taps in registers: the per-token window stores below could alias conv_w
+        // as far as the compiler knows, which would reload it after every store
+        float w[K];
+        {
+            const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan) * K);
+            w[0] = w4.x;
+            w[1] = w4.y;
+            w[2] = w4.z;
+            w[3] = w4.w;
+        }
+        // every token's input for this channel, loaded together (one memory round
+        // trip instead of T dependent ones)
+        float xin[kMaxT];
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) xin[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan] : 0.f;
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            if (t >= T) break;
 #pragma unroll
             for (int q = 0; q + 1 < K; ++q) win[q] = win[q + 1];
-            win[K - 1] = p.qkv[static_cast<size_t>(t) * p.ld_in + chan];
+            win[K - 1] = xin[t];
             double acc = 0.0;
 #pragma unroll
             for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
@@ -149,11 +175,10 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
         }
     }
     if (tid < T) {
-        const int t = tid;
-        const float beta = sigmoid_f(p.b[static_cast<size_t>(t) * p.ld_in + h]);
-        const float g_log = -expf(p.A_log[h]) * softplus_f(p.a[static_cast<size_t>(t) * p.ld_in + h] + p.dt_bias[h]);
-        gate_s[t][0] = expf(g_log);
-        gate_s[t][1] = beta;
+        const float beta = sigmoid_f(gin_b);
+        const float g_log = -expf(gin_A) * softplus_f(gin_a + gin_dt);
+        gate_s[tid][0] = expf(g_log);
+        gate_s[tid][1] = beta;
     }
     __syncthreads();
 
@@ -210,9 +235,269 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
     }
 }
 
+// ---------------------------------------------------------------- one head per WG
+// Same arithmetic as gdn_decode_kernel, one workgroup of 1024 threads per v-head
+// (dv <= 128): thread (c, j) keeps S rows 16c .. 16c+15 of column j.  With the whole
+// head in one workgroup the gated RMSNorm of the head's output (reference
+// ops.cpp:129-156, per head of dv, eps 1e-6, double sum) and the packing into the
+// out_proj fragments are done here too: y = gamma * (o / rms(o)) * silu(z).
+constexpr int kHT = 1024;
+constexpr int kHChunks = 8;
+constexpr int kHRows = kDK / kHChunks;  // 16
+constexpr int kHMaxDv = kHT / kHChunks;  // 128
+
+struct GdnHeadArgs {
+    GdnArgs g;
+    const float* z;      // [T][ld_in] at the head-0 z column (gated norm gate)
+    const float* gamma;  // [dv]
+    i32x4* frag;         // out_proj input fragments (may be null)
+};
+
+__global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
+    const GdnArgs& p = a.g;
+    const int tid = threadIdx.x;
+    const int c = tid & (kHChunks - 1);
+    const int j = tid / kHChunks;  // value column
+    const int h = blockIdx.x;
+    const int dv = p.dv;
+    const bool col_ok = j < dv;
+    const int rep = p.nv / p.nk;
+    const int src = p.v_tiled ? (h % p.nk) : (h / rep);
+    const int qdim = p.nk * kDK;
+    const int T = p.T;
+    constexpr int K = kConvK;
+
+    __shared__ float q_s[kMaxT][kDK];
+    __shared__ float k_s[kMaxT][kDK];
+    __shared__ float v_s[kMaxT][kHMaxDv];
+    __shared__ float o_s[kMaxT][kHMaxDv];
+    __shared__ float gate_s[kMaxT][2];
+    __shared__ double red_s[2][kMaxT];
+    __shared__ float inv_s[kMaxT];
+
+    const int slot0 = p.cur ? *p.cur : 0;
+    const float* S_in = p.cur ? p.S_in + static_cast<size_t>(slot0) * p.s_slot : p.S_in;
+    const float* conv_in = p.cur ? p.conv_in + static_cast<size_t>(slot0) * p.conv_slot : p.conv_in;
+    auto s_dst = [&](int t) -> float* {
+        return p.cur ? const_cast<float*>(p.S_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.s_slot : p.S_out;
+    };
+    auto conv_dst = [&](int t) -> float* {
+        return p.cur ? const_cast<float*>(p.conv_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.conv_slot
+                     : p.conv_out;
+    };
+    const bool per_token = p.cur != nullptr;
+
+    // state: 16 rows of column j (64 contiguous bytes of the transposed layout)
+    const size_t s_off = (static_cast<size_t>(h) * dv + (col_ok ? j : 0)) * kDK + kHRows * c;
+    float S[kHRows];
+    {
+        const float4* sp = reinterpret_cast<const float4*>(S_in + s_off);
+#pragma unroll
+        for (int r = 0; r < kHRows / 4; ++r) {
+            const float4 v = sp[r];
+            S[4 * r] = v.x;
+            S[4 * r + 1] = v.y;
+            S[4 * r + 2] = v.z;
+            S[4 * r + 3] = v.w;
+        }
+    }
+
+    // gate inputs of token tid, loaded with the state (before any store of this
+    // thread, whose completion a later wait would otherwise include)
+    float gin_a = 0.f, gin_b = 0.f, gin_A = 0.f, gin_dt = 0.f;
+    if (tid < T) {
+        gin_a = p.a[static_cast<size_t>(tid) * p.ld_in + h];
+        gin_b = p.b[static_cast<size_t>(tid) * p.ld_in + h];
+        gin_A = p.A_log[h];
+        gin_dt = p.dt_bias[h];
+    }
+
+    // conv1d over T tokens: 128 q + 128 k channels of the source k-head, dv v channels
+    const bool owns_qk = p.v_tiled ? (h == src) : (h == src * rep);
+    if (tid < 2 * kDK + dv) {
+        const int ch = tid;
+        int chan;
+        if (ch < kDK)
+            chan = src * kDK + ch;
+        else if (ch < 2 * kDK)
+            chan = qdim + src * kDK + (ch - kDK);
+        else
+            chan = 2 * qdim + h * dv + (ch - 2 * kDK);
+        const bool write_state = ch >= 2 * kDK || owns_qk;
+        float win[K];
+        {
+            const float4 wv = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan) * K);
+            win[0] = wv.x;
+            win[1] = wv.y;
+            win[2] = wv.z;
+            win[3] = wv.w;
+        }
+        // taps in registers: the per-token window stores below could alias conv_w
+        // as far as the compiler knows, which would reload it after every store
+        float w[K];
+        {
+            const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan) * K);
+            w[0] = w4.x;
+            w[1] = w4.y;
+            w[2] = w4.z;
+            w[3] = w4.w;
+        }
+        // every token's input for this channel, loaded together (one memory round
+        // trip instead of T dependent ones)
+        float xin[kMaxT];
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) xin[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan] : 0.f;
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) {
+            if (t >= T) break;
+#pragma unroll
+            for (int q = 0; q + 1 < K; ++q) win[q] = win[q + 1];
+            win[K - 1] = xin[t];
+            double acc = 0.0;
+#pragma unroll
+            for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
+            const float y = silu_f(static_cast<float>(acc));
+            if (ch < kDK)
+                q_s[t][ch] = y;
+            else if (ch < 2 * kDK)
+                k_s[t][ch - kDK] = y;
+            else
+                v_s[t][ch - 2 * kDK] = y;
+            if (write_state && (per_token || t == T - 1))
+                *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan) * K) =
+                    make_float4(win[0], win[1], win[2], win[3]);
+        }
+    }
+    if (tid < T) {
+        const float beta = sigmoid_f(gin_b);
+        const float g_log = -expf(gin_A) * softplus_f(gin_a + gin_dt);
+        gate_s[tid][0] = expf(g_log);
+        gate_s[tid][1] = beta;
+    }
+    // the gated-norm operands of this thread's column, loaded before the barriers
+    float zt[kMaxT];
+    float gam = 0.f;
+    const bool gn = a.frag != nullptr && c == 0 && col_ok;
+    if (gn) {
+        gam = a.gamma[j];
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) zt[t] = t < T ? a.z[static_cast<size_t>(t) * p.ld_in + h * dv + j] : 0.f;
+    }
+    __syncthreads();
+
+    // L2 norms of q and k (double sums over 128), waves 0 / 1
+    {
+        const int wave = tid >> 6, lane = tid & 63;
+        if (wave < 2) {
+            float(*vec)[kDK] = wave == 0 ? q_s : k_s;
+            for (int t = 0; t < T; ++t) {
+                const double a0 = vec[t][lane], a1 = vec[t][lane + 64];
+                const double ss = wave_sum_d(a0 * a0 + a1 * a1);
+                if (lane == 0) red_s[wave][t] = ss;
+            }
+        }
+    }
+    __syncthreads();
+    const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
+    for (int e = tid; e < T * kDK; e += kHT) {
+        const int t = e / kDK, i = e % kDK;
+        const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t]) + 1e-6f);
+        const float ik = 1.f / sqrtf(static_cast<float>(red_s[1][t]) + 1e-6f);
+        q_s[t][i] = (q_s[t][i] * iq) * qscale;
+        k_s[t][i] = k_s[t][i] * ik;
+    }
+    __syncthreads();
+
+    // delta rule, token by token
+    for (int t = 0; t < T; ++t) {
+        const float g = gate_s[t][0], beta = gate_s[t][1];
+        float kv = 0.f;
+#pragma unroll
+        for (int r = 0; r < kHRows; ++r) {
+            S[r] *= g;
+            kv += S[r] * k_s[t][kHRows * c + r];
+        }
+#pragma unroll
+        for (int o = 1; o < kHChunks; o <<= 1) kv += __shfl_xor(kv, o, 64);
+        const float delta = ((col_ok ? v_s[t][j] : 0.f) - kv) * beta;
+        float ov = 0.f;
+#pragma unroll
+        for (int r = 0; r < kHRows; ++r) {
+            S[r] += k_s[t][kHRows * c + r] * delta;
+            ov += S[r] * q_s[t][kHRows * c + r];
+        }
+#pragma unroll
+        for (int o = 1; o < kHChunks; o <<= 1) ov += __shfl_xor(ov, o, 64);
+        if (c == 0 && col_ok) {
+            o_s[t][j] = ov;
+            if (p.o) p.o[static_cast<size_t>(t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
+        }
+        if (col_ok && (per_token || t == T - 1)) {
+            float4* dp = reinterpret_cast<float4*>(s_dst(t) + s_off);
+#pragma unroll
+            for (int r = 0; r < kHRows / 4; ++r)
+                dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
+        }
+    }
+    if (!a.frag) return;
+
+    // gated RMSNorm of the head (wave t reduces token t) and packing
+    __syncthreads();
+    {
+        const int wave = tid >> 6, lane = tid & 63;
+        if (wave < T) {
+            double ss = 0.0;
+            for (int i = lane; i < dv; i += 64) ss += static_cast<double>(o_s[wave][i]) * o_s[wave][i];
+            ss = wave_sum_d(ss);
+            if (lane == 0) inv_s[wave] = 1.f / sqrtf(static_cast<float>(ss / dv) + 1e-6f);
+        }
+    }
+    __syncthreads();
+    if (gn) {
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t)
+            if (t < T) o_s[t][j] = gam * (o_s[t][j] * inv_s[t]) * silu_f(zt[t]);
+    }
+    __syncthreads();
+    if (tid < T * (dv / 8)) {
+        const int t = tid / (dv / 8), u = tid % (dv / 8);
+        float v[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) v[e] = o_s[t][8 * u + e];
+        write_frag8(a.frag, (h * dv) / 8 + u, t, T, v);
+    }
+}
+
 }  // namespace
 
 namespace rl {
+
+bool gdn_head_supported(int dk, int dv, int K) { return dk == kDK && dv <= kHMaxDv && dv % 8 == 0 && K == kConvK; }
+
+void gdn_decode_head(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
+                     const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
+                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, size_t s_slot, int R, float* o,
+                     const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv, int K,
+                     int v_tiled, hipStream_t s) {
+    RL_REQUIRE(gdn_head_supported(dk, dv, K), RL_ERR_UNSUPPORTED, "gdn_decode_head: dk 128, dv <= 128, conv 4");
+    RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_head: T must be in 1..8");
+    RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode_head: nv must be a multiple of nk");
+    RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && (o || frag), RL_ERR_RANGE,
+               "gdn_decode_head: null pointer");
+    RL_REQUIRE(!frag || (z && gamma), RL_ERR_RANGE, "gdn_decode_head: the gated norm needs z and gamma");
+    if (cur) {
+        RL_REQUIRE(R > T, RL_ERR_RANGE, "gdn_decode_head: ring needs more slots than tokens");
+    } else {
+        RL_REQUIRE(conv_out && S_out && conv_out != conv_in, RL_ERR_RANGE, "gdn_decode_head: bad output state");
+    }
+    GdnHeadArgs p{{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, s_slot,
+                   R, o, T, nk, nv, dv, K, v_tiled},
+                  z,
+                  gamma,
+                  static_cast<i32x4*>(frag)};
+    hipLaunchKernelGGL(gdn_head_kernel, dim3(nv), dim3(kHT), 0, s, p);
+    check_launch("gdn_head_kernel");
+}
 
 void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log, const float* dt_bias,
                 const float* conv_w, const float* conv_in, float* conv_out, const float* S_in, float* S_out,
@@ -246,8 +531,12 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k,
                       int v_tiled, void* stream) {
     return guard([&] {
-        rl::gdn_decode(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0, 0, 0, o,
-                       T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));
+        if (rl::gdn_head_supported(dk, dv, conv_k))
+            rl::gdn_decode_head(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0,
+                                0, 0, o, nullptr, nullptr, nullptr, T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));
+        else
+            rl::gdn_decode(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0, 0,
+                           0, o, T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));
     });
 }
 

@@ -96,6 +96,22 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     // unnormalised, and the outputs are scaled by 1/rms(x_t).  Wave w < T sums the
     // producer's per-group sums of squares of token w (issued here, consumed in the
     // epilogue, so the loads overlap the weight stream).
+    // add-norm epilogue: thread `it` owns item it = (r, t, row) of the epilogue; its
+    // residual value is loaded now, not after the main loop
+    // (token-major: item it = t * RT*16 + r*16 + row, so each token's rows are one
+    // run of RT*16 lanes), together with its gamma
+    float xpre = 0.f, gpre = 0.f;
+    // (indices recomputed where used, so only the two values stay live)
+    auto an_orow_of = [&]() { return (rt0 + (threadIdx.x / kTileRows) % RT) * kTileRows + threadIdx.x % kTileRows; };
+    auto an_valid_of = [&]() {
+        return epilogue == kAddNorm && static_cast<int>(threadIdx.x) < RT * T * kTileRows &&
+               rt0 + static_cast<int>((threadIdx.x / kTileRows) % RT) < m_tiles && an_orow_of() < m_valid;
+    };
+    if (an_valid_of()) {
+        xpre = Y[static_cast<size_t>(threadIdx.x / (RT * kTileRows)) * ldy + an_orow_of()];
+        gpre = 1.f + io.gamma_out[an_orow_of()];
+    }
+
     constexpr int kMaxSsPerLane = 4;  // groups <= 256
     float ssv[kMaxSsPerLane];
     const bool ss_wave = io.ss_in && wave < T;
@@ -231,86 +247,54 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     if (epilogue == kSwiGLU) {
         // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs.
         // h = silu(g) * u goes to Y (fp32, if given) and, if frag_out is given, to the
-        // bf16 hi/mid fragments of the next linear (input column = output row).
-        __shared__ float hsh[RT / 2 > 0 ? RT / 2 : 1][8][kTileRows];
+        // bf16 hi/mid fragments of the next linear (input column = output row), each
+        // thread storing its element's two halves directly.
         for (int it = threadIdx.x; it < (RT / 2) * T * kTileRows; it += 64 * KSPLIT) {
             const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
             const int orow = ((rt0 + 2 * r) / 2) * kTileRows + row;
-            float h = 0.f;
             if (rt0 + 2 * r + 1 < m_tiles && orow < m_valid) {
                 const float gv = final_value(2 * r, t, row);
                 const float uv = final_value(2 * r + 1, t, row);
-                h = gv / (1.f + __expf(-gv)) * uv;
+                const float h = gv / (1.f + __expf(-gv)) * uv;
                 if (Y) Y[static_cast<size_t>(t) * ldy + orow] = h;
-            }
-            hsh[r][t][row] = h;
-        }
-        if (frag_out) {
-            __syncthreads();
-            // units of 8 output columns: (r, t, half)
-            for (int it = threadIdx.x; it < (RT / 2) * T * 2; it += 64 * KSPLIT) {
-                const int half = it & 1, t = (it >> 1) % T, r = (it >> 1) / T;
-                const int ptile = (rt0 + 2 * r) / 2;
-                if (rt0 + 2 * r + 1 >= m_tiles) continue;
-                union {
-                    uint16_t h[8];
-                    i32x4 v;
-                } hi, mid;
-#pragma unroll
-                for (int e = 0; e < 8; ++e) split_bf16(hsh[r][t][8 * half + e], hi.h[e], mid.h[e]);
-                const int col8 = 2 * ptile + half;
-                const int kb = col8 >> 4, jb = (col8 & 15) * 8;
-                const int g2 = jb >> 5, i2 = (jb >> 3) & 3;
-                const size_t u = ((static_cast<size_t>(kb) * 4 + i2) * 4 + g2) * (2 * T) + t;
-                frag_out[u] = hi.v;
-                frag_out[u + T] = mid.v;
+                if (frag_out) {
+                    uint16_t hi, mid;
+                    split_bf16(h, hi, mid);
+                    uint16_t* f16 = reinterpret_cast<uint16_t*>(frag_out);
+                    const size_t u = frag_unit(orow >> 3, t, T);
+                    f16[u * 8 + (orow & 7)] = hi;
+                    f16[(u + T) * 8 + (orow & 7)] = mid;
+                }
             }
         }
     } else if (epilogue == kAddNorm) {
-        // Residual add fused with the next RMSNorm's data movement: x += W.a in place
-        // (one writer per row), then for the next linear: fragments of x * (1 + gamma)
-        // (its input columns = these rows) and this group's sum of x^2 per token,
-        // summed in double over the rows in order, stored as float (io.ss_out[group][t]).
-        __shared__ float xsh[RT][8][kTileRows];
-        for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
-            const int row = it % kTileRows, t = (it / kTileRows) % T, r = it / (kTileRows * T);
-            const int orow = (rt0 + r) * kTileRows + row;
-            float x = 0.f;
-            if (rt0 + r < m_tiles && orow < m_valid) {
-                float* dst = Y + static_cast<size_t>(t) * ldy + orow;
-                x = *dst + final_value(r, t, row);
-                *dst = x;
+        // Residual add fused with the next RMSNorm's data movement (one writer per
+        // row): x += W.a in place; this thread's element of the next linear's input
+        // fragments, x * (1 + gamma), written as its two bf16 halves; and the group's
+        // sum of x^2 per token, reduced over the token's RT*16 lanes in a fixed
+        // butterfly order (double), stored as float (io.ss_out[group][t]).
+        const bool an_item = static_cast<int>(threadIdx.x) < RT * T * kTileRows;
+        const int an_t = threadIdx.x / (RT * kTileRows);
+        const int an_r = (threadIdx.x / kTileRows) % RT;
+        const int an_row = threadIdx.x % kTileRows;
+        const int an_orow = an_orow_of();
+        if (an_item) {
+            double sq = 0.0;
+            if (an_valid_of()) {
+                const float x = xpre + final_value(an_r, an_t, an_row);
+                Y[static_cast<size_t>(an_t) * ldy + an_orow] = x;
+                uint16_t hi, mid;
+                split_bf16(x * gpre, hi, mid);
+                uint16_t* f16 = reinterpret_cast<uint16_t*>(frag_out);
+                const size_t u = frag_unit(an_orow >> 3, an_t, T);
+                f16[u * 8 + (an_orow & 7)] = hi;
+                f16[(u + T) * 8 + (an_orow & 7)] = mid;
+                sq = static_cast<double>(x) * x;
             }
-            xsh[r][t][row] = x;
-        }
-        __syncthreads();
-        if (threadIdx.x < T) {
-            const int t = threadIdx.x;
-            double ss = 0.0;
-            for (int r = 0; r < RT; ++r)
-                for (int row = 0; row < kTileRows; ++row) ss += static_cast<double>(xsh[r][t][row]) * xsh[r][t][row];
-            io.ss_out[static_cast<size_t>(blockIdx.x) * T + t] = static_cast<float>(ss);
-        }
-        // units of 8 columns: (r, t, half)
-        for (int it = threadIdx.x; it < RT * T * 2; it += 64 * KSPLIT) {
-            const int half = it & 1, t = (it >> 1) % T, r = (it >> 1) / T;
-            if (rt0 + r >= m_tiles) continue;
-            union {
-                uint16_t h[8];
-                i32x4 v;
-            } hi, mid;
-            const int c0 = (rt0 + r) * kTileRows + 8 * half;
 #pragma unroll
-            for (int e = 0; e < 8; ++e) {
-                const float g = c0 + e < m_valid ? 1.f + io.gamma_out[c0 + e] : 0.f;
-                split_bf16(xsh[r][t][8 * half + e] * g, hi.h[e], mid.h[e]);
-            }
-            const int col8 = c0 >> 3;
-            const int kb = col8 >> 4, jb = (col8 & 15) * 8;
-            const int g2 = jb >> 5, i2 = (jb >> 3) & 3;
-            const size_t u = ((static_cast<size_t>(kb) * 4 + i2) * 4 + g2) * (2 * T) + t;
-            frag_out[u] = hi.v;
-            frag_out[u + T] = mid.v;
+            for (int o = 1; o < RT * kTileRows; o <<= 1) sq += __shfl_xor(sq, o, 64);
+            if (threadIdx.x % (RT * kTileRows) == 0)
+                io.ss_out[static_cast<size_t>(blockIdx.x) * T + an_t] = static_cast<float>(sq);
         }
     } else {
         for (int it = threadIdx.x; it < items; it += 64 * KSPLIT) {
@@ -470,7 +454,9 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, kFp8 ? 1 : 2};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
-    if (epilogue == kAddNorm) c.rt = 2;  // the sum-of-squares groups are 2 row tiles (add_norm_groups)
+    // residual GEMMs (m = hidden: 160 groups): 8 waves measured faster than 16 there
+    // (5120x17408: 21.2 vs 22.8 us cold); the sum-of-squares groups are 2 row tiles
+    if (epilogue == kAddNorm && !g_force.rt) c = GemmCfg{2, 8, kFp8 ? 1 : 2};
     if (io.ss_in || epilogue == kAddNorm)
         RL_REQUIRE(c.ks >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
 #define RL_GEMM_CASE(R, K, DD)                                                            \

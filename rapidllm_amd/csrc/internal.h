@@ -62,6 +62,16 @@ void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, con
                 const int* cur, size_t conv_slot, size_t s_slot, int R, float* o, int T, int nk, int nv, int dk,
                 int dv, int K, int v_tiled, hipStream_t s);
 
+// One workgroup per v-head (dk 128, dv <= 128) with the gated RMSNorm of the head
+// (gamma [dv], gate z at z[t*ld_in + h*dv + j]) and the packing into fragments fused
+// (frag may be null; o may be null when frag is given).
+bool gdn_head_supported(int dk, int dv, int K);
+void gdn_decode_head(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
+                     const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
+                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, size_t s_slot, int R, float* o,
+                     const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv, int K,
+                     int v_tiled, hipStream_t s);
+
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);
 void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,

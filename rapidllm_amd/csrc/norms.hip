@@ -20,27 +20,6 @@ constexpr int kBlockCols = 128;
 
 __device__ inline float silu_f(float x) { return x / (1.f + expf(-x)); }
 
-// Fragment unit (16 B = 8 bf16) holding columns [8u, 8u+8) of token t, hi part.
-// The mid part sits T units later.  Layout matches pack_act_kernel (gemm.hip).
-__device__ inline size_t frag_unit(int col8, int t, int T) {
-    const int kb = col8 >> 4;           // 16 units per 128-column block
-    const int jb = (col8 & 15) * 8;     // first column within the block
-    const int g = jb >> 5, i = (jb >> 3) & 3;
-    return ((static_cast<size_t>(kb) * 4 + i) * 4 + g) * (2 * T) + t;
-}
-
-__device__ inline void write_frag8(i32x4* frag, int col8, int t, int T, const float (&v)[8]) {
-    union {
-        uint16_t h[8];
-        i32x4 q;
-    } hi, mid;
-#pragma unroll
-    for (int e = 0; e < 8; ++e) split_bf16(v[e], hi.h[e], mid.h[e]);
-    const size_t u = frag_unit(col8, t, T);
-    frag[u] = hi.q;
-    frag[u + T] = mid.q;
-}
-
 // Residual update + Qwen RMSNorm + packing.  One workgroup of 1024 threads per
 // token; thread u owns the 8 columns [8u, 8u+8) (a second pass for n > 8192).  Each
 // thread loads its x and partial-sum slices at once (no serial chain), forms

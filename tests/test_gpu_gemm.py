@@ -110,8 +110,8 @@ def _time_gemm(lin, X, epi, split=4, frag_out=None):
     yd.zero()
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
-    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, m, n, T, epi, split, 1, None,
-         C.byref(ms))
+    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, None, None, m, n, T, epi, split, 1,
+         None, C.byref(ms))
     return yd.numpy(np.float32, (rows,))
 
 
@@ -156,3 +156,49 @@ def test_gemm_fp8_swiglu_epilogue(gpu, orc, T):
         want = g / (1 + np.exp(-g)) * u
     for t in range(T):
         assert rel_l2(H[t], want[t]) <= REL_L2, (t, rel_l2(H[t], want[t]))
+
+
+def _unpack_frag(raw, n, T):
+    """GEMM input fragments [kb][i][g][2T][8 bf16] -> fp32 [T][n] (hi + mid)."""
+    u16 = raw.view(np.uint16).reshape(n // 128, 4, 4, 2 * T, 8)
+    f = (u16.astype(np.uint32) << 16).view(np.float32).astype(np.float64)
+    val = f[:, :, :, :T, :] + f[:, :, :, T:, :]          # [kb][i][g][t][e]
+    # column = kb*128 + 32g + 8i + e
+    return val.transpose(3, 0, 2, 1, 4).reshape(T, n)
+
+
+@pytest.mark.parametrize("T", [1, 4])
+def test_gemm_fp8_add_norm_epilogue(gpu, orc, T):
+    """Residual GEMM fused with the next RMSNorm's data: x += W.a in place,
+    fragments of x * (1 + gamma) for the next linear, and sum of x^2 per 32 rows."""
+    import ctypes as C
+
+    from rapidllm_amd.hip import DeviceBuffer, call
+
+    r = synth.rng(500 + T)
+    m, n = 512, 1024
+    W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n, 1e-3, 1e-2)
+    lin = ops.Fp8Linear(W, s)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    x0 = r.standard_normal((T, m)).astype(np.float32)
+    gamma = (0.1 * r.standard_normal(m)).astype(np.float32)
+    xd = DeviceBuffer.from_numpy(X)
+    frag = ops.act_frag_buffer(n, T)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
+    yd = DeviceBuffer.from_numpy(x0)
+    fo = ops.act_frag_buffer(m, T)
+    gd = DeviceBuffer.from_numpy(gamma)
+    ssd = DeviceBuffer(4 * T * (m // 32))
+    ptrs = (C.c_void_p * 1)(lin.w.ptr)
+    ms = C.c_float()
+    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr, gd.ptr, ssd.ptr, m, n, T, 4, 1, 1,
+         None, C.byref(ms))
+    x = yd.numpy(np.float32, (T, m)).astype(np.float64)
+    want = x0.astype(np.float64) + orc.gemm_fp8(W, s, X)
+    for t in range(T):
+        assert rel_l2(x[t], want[t]) <= REL_L2
+    ss = ssd.numpy(np.float32, (m // 32, T)).astype(np.float64)
+    assert np.allclose(ss, (x ** 2).reshape(T, m // 32, 32).sum(2).T, rtol=1e-5)
+    fr = _unpack_frag(fo.numpy(np.uint8, (fo.nbytes,)), m, T)
+    xg = x * (1.0 + gamma.astype(np.float64))
+    assert np.all(np.abs(fr - xg) <= 2.0 ** -15 * np.abs(xg) + 1e-30)
