@@ -16,13 +16,13 @@
 //              S^T = K . Q^T on v_mfma_f32_16x16x32_f16 with A = K rows straight
 //              from the cache and B = the fragments of all G*T query rows of the
 //              kv group (hi and lo in two column tiles, summed per lane); chunk
-//              softmax; P (fp16) staged in LDS in B-operand order; O^T = V^T . P^T
-//              with V stored transposed ([d][pos]) so A rows are contiguous.  Every
+//              softmax; P (fp16) staged in LDS by position; O^T = V^T . P^T.  Every
 //              K and V byte of the chunk is read once for all heads and tokens.
 //  attn_comb   merges the chunk partials (max, sum, O) per query row, applies
 //              sigmoid(gate) and writes fp32 and/or the o_proj GEMM fragments.
 //
-// Cache layouts: K [n_kv][ctx][hd] fp16;  V^T [n_kv][hd][ctx] fp16;  ctx % 256 == 0.
+// Cache layouts: K and V fp16 [n_kv][ctx * hd] in MFMA fragment order (k_off / v_off
+// below); ctx % 256 == 0.
 #include "internal.h"
 
 using namespace rl;
@@ -32,6 +32,9 @@ namespace {
 constexpr int kHD = 256;
 constexpr int kChunk = 256;
 constexpr int kMaxPairs = 32;  // G * T query rows per kv head (<= 2 tiles of 16)
+#ifndef ATTN_UNROLL
+#define ATTN_UNROLL 2
+#endif
 
 typedef _Float16 half4 __attribute__((ext_vector_type(4)));
 
@@ -59,6 +62,17 @@ struct AttnArgs {
 
 __host__ __device__ inline int pair_tiles(int G, int T) { return (G * T + 15) / 16; }
 
+// Cache layouts (per kv head, ctx * 256 fp16), in MFMA fragment order so that every
+// wave load is one contiguous 1 KiB run (lane l reads 16 B at 16 l):
+//   K: [pos/16][d/32][(d/8)%4][pos%16][d%8]  -- A operand of S^T = K . Q^T
+//   V: [pos/32][d/16][(pos/8)%4][d%16][pos%8] -- A operand of O^T = V^T . P^T
+__host__ __device__ inline size_t k_off(int pos, int d) {
+    return (((static_cast<size_t>(pos >> 4) * 8 + (d >> 5)) * 4 + ((d >> 3) & 3)) * 16 + (pos & 15)) * 8 + (d & 7);
+}
+__host__ __device__ inline size_t v_off(int pos, int d) {
+    return (((static_cast<size_t>(pos >> 5) * 16 + (d >> 4)) * 4 + ((pos >> 3) & 3)) * 16 + (d & 15)) * 8 + (pos & 7);
+}
+
 // grid (nq + 2*nkv, T), 64 threads.  Heads [0,nq): q; [nq, nq+nkv): k; then v.
 __global__ __launch_bounds__(64) void qk_prep_kernel(AttnArgs p) {
     __shared__ float vec[kHD];
@@ -69,9 +83,8 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(AttnArgs p) {
     if (head >= p.nq + p.nkv) {  // v: straight to the transposed cache
         const int kv = head - p.nq - p.nkv;
         const float* src = row + qcols + p.nkv * kHD + kv * kHD;
-        for (int d = lane; d < kHD; d += 64)
-            p.vt[(static_cast<size_t>(kv) * kHD + d) * p.ctx + pos] =
-                __builtin_bit_cast(uint16_t, static_cast<_Float16>(src[d]));
+        uint16_t* vb = p.vt + static_cast<size_t>(kv) * p.ctx * kHD;
+        for (int d = lane; d < kHD; d += 64) vb[v_off(pos, d)] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(src[d]));
         return;
     }
     const bool is_q = head < p.nq;
@@ -101,8 +114,8 @@ __global__ __launch_bounds__(64) void qk_prep_kernel(AttnArgs p) {
     __syncthreads();
     if (!is_q) {
         const int kv = head - p.nq;
-        uint16_t* dst = p.kc + (static_cast<size_t>(kv) * p.ctx + pos) * kHD;
-        for (int d = lane; d < kHD; d += 64) dst[d] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vec[d]));
+        uint16_t* kb = p.kc + static_cast<size_t>(kv) * p.ctx * kHD;
+        for (int d = lane; d < kHD; d += 64) kb[k_off(pos, d)] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vec[d]));
         return;
     }
     // q -> fp16 hi/lo fragments: dim d = 32 s + 8 g + e; pair k = t*G + head%G
@@ -139,31 +152,40 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     const int npairs = p.G * p.T;
     const float scale = 1.f / sqrtf(static_cast<float>(kHD));
 
-    __shared__ i32x4 P_lds[8][PT][4][16];  // [u][pt][g][col] : 8 fp16 of P^T
+    // [u][pair tile][pair col][32 positions + 8 pad]: the 80-byte row stride puts the
+    // 16 pair columns of a write instruction on distinct banks
+    __shared__ _Float16 P_lds[8][PT][16][40];
     __shared__ float max_s[4][PT][16];
     __shared__ float sum_s[4][PT][16];
 
     // ---- scores for positions c0 + 64*wave + 16*ptile + row
-    f32x4 acc[4][2 * PT];
+    // S^T = K . (Q_hi + Q_lo).  One pair tile: hi and lo in separate accumulators
+    // (independent MFMA chains); two pair tiles: both parts accumulate into the
+    // same tile (half the accumulator registers, keeping 4 waves per SIMD).
+    constexpr int NA = PT == 1 ? 2 : 1;
+    f32x4 acc[4][PT * NA];
 #pragma unroll
     for (int a = 0; a < 4; ++a)
 #pragma unroll
-        for (int b = 0; b < 2 * PT; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int b = 0; b < PT * NA; ++b) acc[a][b] = f32x4{0.f, 0.f, 0.f, 0.f};
     const uint16_t* kbase = p.kc + static_cast<size_t>(kv) * p.ctx * kHD;
     const i32x4* qbase = p.qf + static_cast<size_t>(kv) * 8 * 4 * (2 * PT) * 16;
-#pragma unroll 2
+#pragma unroll ATTN_UNROLL
     for (int s = 0; s < 8; ++s) {
         H8 bq[2 * PT];
 #pragma unroll
         for (int ct = 0; ct < 2 * PT; ++ct) bq[ct].i = qbase[((s * 4 + g) * (2 * PT) + ct) * 16 + col];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
-            const int prow = min(c0 + 64 * wave + 16 * pt + col, p.ctx - 1);
+            const int ptile = (c0 + 64 * wave + 16 * pt) >> 4;
             H8 a;
-            a.i = *reinterpret_cast<const i32x4*>(kbase + static_cast<size_t>(prow) * kHD + 32 * s + 8 * g);
+            a.i = reinterpret_cast<const i32x4*>(kbase + (static_cast<size_t>(ptile) * 8 + s) * 512)[lane];
 #pragma unroll
-            for (int ct = 0; ct < 2 * PT; ++ct)
-                acc[pt][ct] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bq[ct].v, acc[pt][ct], 0, 0, 0);
+            for (int q = 0; q < PT; ++q) {
+                acc[pt][NA * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bq[2 * q].v, acc[pt][NA * q], 0, 0, 0);
+                acc[pt][NA * q + NA - 1] =
+                    __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bq[2 * q + 1].v, acc[pt][NA * q + NA - 1], 0, 0, 0);
+            }
         }
     }
 
@@ -182,7 +204,7 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
             for (int v = 0; v < 4; ++v) {
                 const int pos = c0 + 64 * wave + 16 * pt + 4 * g + v;
                 const bool ok = k < npairs && pos <= p0 + t;
-                const float val = (acc[pt][2 * q][v] + acc[pt][2 * q + 1][v]) * scale;
+                const float val = (NA == 2 ? acc[pt][2 * q][v] + acc[pt][2 * q + 1][v] : acc[pt][q][v]) * scale;
                 sc[pt][q][v] = ok ? val : -INFINITY;
                 mx[q] = fmaxf(mx[q], sc[pt][q][v]);
             }
@@ -200,19 +222,18 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
         M[q] = fmaxf(fmaxf(max_s[0][q][col], max_s[1][q][col]), fmaxf(max_s[2][q][col], max_s[3][q][col]));
         sum[q] = 0.f;
     }
-    // P = exp(s - M) (0 where masked), staged as fp16 in PV B-operand order:
-    // unit (u, q, g, col) element e <-> chunk position 32u + 16*(e>=4) + 4g + (e&3)
+    // P = exp(s - M) (0 where masked), staged as fp16 by chunk position:
+    // P_lds[u][q][pair col][j] holds position 32u + j
 #pragma unroll
     for (int pt = 0; pt < 4; ++pt) {
-        const int tile = 4 * wave + pt;
 #pragma unroll
         for (int q = 0; q < PT; ++q) {
-            _Float16* unit = reinterpret_cast<_Float16*>(&P_lds[tile >> 1][q][g][col]);
 #pragma unroll
             for (int v = 0; v < 4; ++v) {
+                const int pl = 64 * wave + 16 * pt + 4 * g + v;
                 const float e = M[q] == -INFINITY ? 0.f : expf(sc[pt][q][v] - M[q]);
                 sum[q] += e;
-                unit[(tile & 1) * 4 + v] = static_cast<_Float16>(e);
+                P_lds[pl >> 5][q][col][pl & 31] = static_cast<_Float16>(e);
             }
         }
     }
@@ -230,22 +251,17 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int q = 0; q < PT; ++q) o[a][q] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;
-#pragma unroll 2
+    const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;  // fragment-ordered V
+#pragma unroll ATTN_UNROLL
     for (int u = 0; u < 8; ++u) {
         H8 bp[PT];
 #pragma unroll
-        for (int q = 0; q < PT; ++q) bp[q].i = P_lds[u][q][g][col];
+        for (int q = 0; q < PT; ++q) bp[q].i = *reinterpret_cast<const i32x4*>(&P_lds[u][q][col][8 * g]);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt) {
-            const int d = 64 * wave + 16 * dt + col;
-            const uint16_t* vr = vbase + static_cast<size_t>(d) * p.ctx + c0 + 32 * u + 4 * g;
-            union {
-                f16x8 v;
-                i32x2 q2[2];
-            } a;
-            a.q2[0] = *reinterpret_cast<const i32x2*>(vr);
-            a.q2[1] = *reinterpret_cast<const i32x2*>(vr + 16);
+            const int grp = (c0 >> 5) + u, dtile = 4 * wave + dt;
+            H8 a;
+            a.i = reinterpret_cast<const i32x4*>(vbase + (static_cast<size_t>(grp) * 16 + dtile) * 512)[lane];
 #pragma unroll
             for (int q = 0; q < PT; ++q)
                 o[dt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bp[q].v, o[dt][q], 0, 0, 0);

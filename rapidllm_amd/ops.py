@@ -234,8 +234,23 @@ def gdn_decode(qkv, a, b, A_log, dt_bias, conv_w, conv_state, S, nk, nv, v_tiled
 # ------------------------------------------------------------------ attention
 
 
+def kv_layout_k(K):
+    """[n_kv][ctx][256] fp16 -> the device K layout, per kv head
+    [pos/16][d/32][(d/8)%4][pos%16][d%8]."""
+    n_kv, ctx, hd = K.shape
+    return np.ascontiguousarray(K.reshape(n_kv, ctx // 16, 16, hd // 32, 4, 8).transpose(0, 1, 3, 4, 2, 5))
+
+
+def kv_layout_v(V):
+    """[n_kv][ctx][256] fp16 -> the device V layout, per kv head
+    [pos/32][d/16][(pos/8)%4][d%16][pos%8]."""
+    n_kv, ctx, hd = V.shape
+    return np.ascontiguousarray(V.reshape(n_kv, ctx // 32, 4, 8, hd // 16, 16).transpose(0, 1, 4, 2, 5, 3))
+
+
 class AttnCache:
-    """fp16 K [n_kv][ctx][hd] and transposed V [n_kv][hd][ctx] caches in HBM."""
+    """fp16 K and V caches in HBM, in the device's MFMA fragment order
+    (include/rapidllm_hip.h, rl_hip_attn_decode_layer)."""
 
     def __init__(self, n_kv: int, ctx: int, hd: int = 256):
         assert ctx % 256 == 0
@@ -250,11 +265,11 @@ class AttnCache:
         """K, V: [pos][n_kv][hd] float values (rounded to fp16 here)."""
         L = K.shape[0]
         kc = np.zeros((self.n_kv, self.ctx, self.hd), np.float16)
-        vt = np.zeros((self.n_kv, self.hd, self.ctx), np.float16)
+        vc = np.zeros((self.n_kv, self.ctx, self.hd), np.float16)
         kc[:, :L, :] = np.transpose(K, (1, 0, 2)).astype(np.float16)
-        vt[:, :, :L] = np.transpose(V, (1, 2, 0)).astype(np.float16)
-        self.k.upload(kc)
-        self.vt.upload(vt)
+        vc[:, :L, :] = np.transpose(V, (1, 0, 2)).astype(np.float16)
+        self.k.upload(kv_layout_k(kc))
+        self.vt.upload(kv_layout_v(vc))
 
 
 def attn_decode_layer(Y, cache: AttnCache, pos: int, q_norm, k_norm, n_q, n_kv, rotary_dim=64, theta=1e7,
