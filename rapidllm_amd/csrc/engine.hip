@@ -123,6 +123,7 @@ class Engine {
             if (g.second) (void)hipGraphExecDestroy(g.second);
         if (st_) (void)hipStreamDestroy(st_);
         if (host_rb_) (void)hipHostFree(host_rb_);
+        if (host_in_) (void)hipHostFree(host_in_);
     }
 
     // ------------------------------------------------------------ weights
@@ -165,14 +166,22 @@ class Engine {
         n_last_ = 0;
     }
 
+    // Stage n ints in pinned memory and enqueue their upload to dst (stream order).
+    // Every public call ends with a stream synchronisation, so the stage is free.
+    void upload_ints(int* dst, const int32_t* src, int n) {
+        std::memcpy(host_in_, src, static_cast<size_t>(n) * sizeof(int));
+        RL_HIP(hipMemcpyAsync(dst, host_in_, static_cast<size_t>(n) * sizeof(int), hipMemcpyHostToDevice, st_));
+    }
+
     void prefill(const int32_t* ids, int n) {
         RL_REQUIRE(n >= 1 && ids, RL_ERR_RANGE, "prefill: empty prompt");
         RL_REQUIRE(n <= ctx_capacity(), RL_ERR_RANGE, "prefill: prompt longer than the context");
         check_ids(ids, n);
         reset();
+        upload_ints(tok_all_, ids, n);
         for (int i = 0; i < n; i += tmax_) {
             const int T = std::min(tmax_, n - i);
-            RL_HIP(hipMemcpyAsync(tok_, ids + i, T * sizeof(int), hipMemcpyHostToDevice, st_));
+            RL_HIP(hipMemcpyAsync(tok_, tok_all_ + i, T * sizeof(int), hipMemcpyDeviceToDevice, st_));
             step(T, /*force_all=*/1, /*feed=*/false);
         }
         readback();
@@ -181,7 +190,7 @@ class Engine {
     void decode_token(int32_t token) {
         check_ids(&token, 1);
         RL_REQUIRE(pos_ + 1 <= ctx_capacity(), RL_ERR_RANGE, "decode: context full");
-        RL_HIP(hipMemcpyAsync(scal_ + kNextTok, &token, sizeof(int), hipMemcpyHostToDevice, st_));
+        upload_ints(scal_ + kNextTok, &token, 1);
         run_graph(1);
         readback();
     }
@@ -219,7 +228,7 @@ class Engine {
         if (!has_mtp_ || n <= 0) return 0;
         RL_REQUIRE(n <= 7, RL_ERR_RANGE, "mtp_draft: at most 7 drafts");
         check_ids(&first, 1);
-        RL_HIP(hipMemcpyAsync(scal_ + kNextTok, &first, sizeof(int), hipMemcpyHostToDevice, st_));
+        upload_ints(scal_ + kNextTok, &first, 1);
         run_mtp(n);
         RL_HIP(hipMemcpyAsync(out, tok_ + 1, n * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipStreamSynchronize(st_));
@@ -232,9 +241,9 @@ class Engine {
         RL_REQUIRE(pos_ + T <= ctx_capacity(), RL_ERR_RANGE, "spec_verify: context full");
         check_ids(toks, T);
         if (T == 1)  // the T = 1 step feeds the device's next token
-            RL_HIP(hipMemcpyAsync(scal_ + kNextTok, toks, sizeof(int), hipMemcpyHostToDevice, st_));
+            upload_ints(scal_ + kNextTok, toks, 1);
         else
-            RL_HIP(hipMemcpyAsync(tok_, toks, T * sizeof(int), hipMemcpyHostToDevice, st_));
+            upload_ints(tok_, toks, T);
         run_graph(T, /*from_host=*/true);
         readback();
         if (preds) std::memcpy(preds, host_rb_ + kRbPreds, T * sizeof(int));
@@ -247,7 +256,7 @@ class Engine {
         RL_REQUIRE(T >= 2 && T <= tmax_, RL_ERR_RANGE, "mtp_spec: T out of range");
         RL_REQUIRE(pos_ + T <= ctx_capacity(), RL_ERR_RANGE, "mtp_spec: context full");
         check_ids(&t0, 1);
-        RL_HIP(hipMemcpyAsync(scal_ + kNextTok, &t0, sizeof(int), hipMemcpyHostToDevice, st_));
+        upload_ints(scal_ + kNextTok, &t0, 1);
         run_mtp(T - 1);
         run_graph(T, /*from_host=*/true);
         readback();
@@ -263,7 +272,7 @@ class Engine {
     // rows below pos are whatever the cache holds: zeros or synthetic values).
     void set_pos(int pos) {
         RL_REQUIRE(pos >= 0 && pos <= ctx_capacity(), RL_ERR_RANGE, "set_pos: out of range");
-        RL_HIP(hipMemcpyAsync(scal_ + kPos, &pos, sizeof(int), hipMemcpyHostToDevice, st_));
+        upload_ints(scal_ + kPos, &pos, 1);
         RL_HIP(hipStreamSynchronize(st_));
         pos_ = pos;
     }
@@ -383,6 +392,12 @@ class Engine {
 
     std::map<int, hipGraphExec_t> graphs_;  // key: T (1..Tmax), 100 + n for MTP drafts
     int* host_rb_ = nullptr;
+    // Host inputs (token ids, positions) are staged in pinned memory and uploaded
+    // with stream-ordered copies; a call rewrites host_in_ only after its previous
+    // call's final stream synchronisation, and the prompt of a prefill is uploaded
+    // once to tok_all_ (chunks are fed by device-to-device copies).
+    int* host_in_ = nullptr;  // [ctx capacity + 16]
+    int* tok_all_ = nullptr;  // device [ctx capacity]
     int pos_ = 0, n_last_ = 0;
     int32_t greedy_ = 0;
 
@@ -562,6 +577,9 @@ class Engine {
         kq_ws_bytes_ = std::max<size_t>(kq_need_, 256);
         kq_ws_ = mem_.get(kq_ws_bytes_);
         RL_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_rb_), kRbInts * sizeof(int), hipHostMallocDefault));
+        RL_HIP(hipHostMalloc(reinterpret_cast<void**>(&host_in_), (static_cast<size_t>(ctx_capacity()) + 16) * sizeof(int),
+                             hipHostMallocDefault));
+        tok_all_ = mem_.get_n<int>(static_cast<size_t>(ctx_capacity()) + 16);
         RL_HIP(hipStreamSynchronize(st_));
         tab_.clear();
     }

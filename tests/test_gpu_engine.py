@@ -161,3 +161,26 @@ def test_norm_kernels_and_folded_norm_agree(gpu, orc, monkeypatch):
         eng.close()
     assert outs[0][1:] == outs[1][1:]
     assert rel_l2(outs[0][0], outs[1][0]) < TOL
+
+
+def test_long_prefill_chunks_match_oracle_and_decode(gpu, fp8_pair):
+    """A prompt of many max_T chunks (uploaded once, chunks fed on the device):
+    logits equal the oracle's and equal a token-by-token decode of the same prompt,
+    and a decode after the prefill continues correctly."""
+    spec, W, eng, orc_m = fp8_pair
+    rng = np.random.default_rng(99)
+    prompt = [int(t) for t in rng.integers(0, spec.vocab, 41)]
+    eng.prefill(prompt)
+    lg_prefill = eng.copy_logits()
+    orc_m.reset()
+    for t in prompt:
+        g, lg, _ = orc_m.decode(t)
+    assert rel_l2(lg_prefill, lg) < TOL
+    eng.prefill(prompt[:1])
+    for t in prompt[1:]:
+        eng.decode_token(t)
+    assert rel_l2(eng.copy_logits(), lg_prefill) < TOL
+    eng.prefill(prompt)
+    eng.decode_token(g)
+    g2, lg2, _ = orc_m.decode(g)
+    assert rel_l2(eng.copy_logits(), lg2) < TOL
