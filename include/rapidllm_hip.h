@@ -100,9 +100,6 @@ int rl_hip_gemm_bf16_frag(const uint16_t* w_tiled, const void* frag, float* Y, i
 /* Tuning hook: force the work split (row-tiles per workgroup, waves per workgroup
  * along K, load pipeline depth); row_tiles = 0 restores the shape-based choice. */
 int rl_hip_set_gemm_config(int row_tiles, int k_waves, int depth);
-/* Measurement hook: 1 = ordinary (cache-allocating) weight loads, 0 = non-temporal
- * (default). */
-int rl_hip_set_gemm_load_policy(int temporal);
 /* Convenience: pack X into `frag_scratch` then GEMM (two launches). */
 int rl_hip_gemm_fp8(const uint8_t* w_tiled, const float* tile_scale, const float* X, float* Y, void* frag_scratch,
                     int m, int n, int T, void* stream);

@@ -49,7 +49,6 @@ _SIGS = {
     "rl_hip_gemm_fp8_frag": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rl_hip_gemm_bf16_frag": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rl_hip_set_gemm_config": (_i, [_i, _i, _i]),
-    "rl_hip_set_gemm_load_policy": (_i, [_i]),
     "rl_hip_kquant_tiled_bytes": (_sz, [_i, _i, _i]),
     "rl_hip_kquant_workspace_bytes": (_sz, [_i, _i, _i]),
     "rl_hip_pack_kquant": (_i, [_i, _vp, _vp, _i, _i, _vp]),
