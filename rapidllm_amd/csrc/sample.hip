@@ -11,13 +11,15 @@
 // preds[i] = greedy after toks[i]; n = 1 + longest prefix with preds[i] == toks[i+1].
 // It advances the device position and recurrent-state slot by n, so the next step
 // runs without a host round trip.
+#include <algorithm>
+
 #include "internal.h"
 
 using namespace rl;
 
 namespace {
 
-constexpr int kArgChunk = 4096;
+constexpr int kArgChunk = 1024;  // 4 values per thread, loaded together
 
 __device__ inline bool better(float v, int i, float bv, int bi) { return v > bv || (v == bv && i < bi); }
 
@@ -29,10 +31,17 @@ __global__ __launch_bounds__(256) void argmax_partial_kernel(const float* __rest
     const int b = chunk * kArgChunk, e = min(V, b + kArgChunk);
     float bv = -INFINITY;
     int bi = 0x7fffffff;
-    for (int i = b + threadIdx.x; i < e; i += 256) {
-        const float v = x[i];
-        if (better(v, i, bv, bi)) {
-            bv = v;
+    float vals[kArgChunk / 256];
+#pragma unroll
+    for (int k = 0; k < kArgChunk / 256; ++k) {
+        const int i = b + threadIdx.x + 256 * k;
+        vals[k] = i < e ? x[i] : -INFINITY;
+    }
+#pragma unroll
+    for (int k = 0; k < kArgChunk / 256; ++k) {
+        const int i = b + threadIdx.x + 256 * k;
+        if (i < e && better(vals[k], i, bv, bi)) {
+            bv = vals[k];
             bi = i;
         }
     }
@@ -114,27 +123,37 @@ struct AcceptArgs {
     int H;
 };
 
+// grid: one workgroup per 256 hidden elements (at least one).  Every workgroup
+// derives n from toks / preds (loaded together, compared in order); workgroup 0
+// also advances the device scalars.
+constexpr int kAcceptMaxT = 8;
+
 __global__ __launch_bounds__(256) void accept_kernel(AcceptArgs a) {
-    __shared__ int n_s;
-    if (threadIdx.x == 0) {
-        int n = 1;
-        if (a.force_all)
-            n = a.T;
-        else
-            while (n < a.T && a.preds[n - 1] == a.toks[n]) ++n;
-        n_s = n;
+    int n = 1;
+    if (a.force_all) {
+        n = a.T;
+    } else {
+        int tk[kAcceptMaxT], pr[kAcceptMaxT];
+#pragma unroll
+        for (int i = 0; i < kAcceptMaxT; ++i) {
+            tk[i] = i < a.T ? a.toks[i] : -1;
+            pr[i] = i < a.T ? a.preds[i] : -2;
+        }
+#pragma unroll
+        for (int i = 1; i < kAcceptMaxT; ++i)
+            if (n == i && i < a.T && pr[i - 1] == tk[i]) n = i + 1;
     }
-    __syncthreads();
-    const int n = n_s;
     if (a.h_last && a.xout) {
         // h_prev <- hidden of token n-2 (or the previous h_last), h_last <- token n-1
-        for (int i = threadIdx.x; i < a.H; i += blockDim.x) {
+        const int i = blockIdx.x * blockDim.x + threadIdx.x;
+        if (i < a.H) {
+            const float last = a.xout[static_cast<size_t>(n - 1) * a.H + i];
             const float prev = n >= 2 ? a.xout[static_cast<size_t>(n - 2) * a.H + i] : a.h_last[i];
             a.h_prev[i] = prev;
-            a.h_last[i] = a.xout[static_cast<size_t>(n - 1) * a.H + i];
+            a.h_last[i] = last;
         }
     }
-    if (threadIdx.x == 0) {
+    if (blockIdx.x == 0 && threadIdx.x == 0) {
         *a.n_out = n;
         *a.pos += n;
         if (a.slot) *a.slot = (*a.slot + n) % a.R;
@@ -173,9 +192,11 @@ void argmax_rows(const float* logits, int rows, int V, int* out, float* out_val,
 void accept(const int* toks, const int* preds, int T, int force_all, int* pos, int* slot, int R, int* n_out,
             int* next_tok, int* gen_ring, int* gen_count, int gen_cap, const float* xout, float* h_last,
             float* h_prev, int H, hipStream_t s) {
+    RL_REQUIRE(T >= 1 && T <= kAcceptMaxT, RL_ERR_RANGE, "accept: T must be in 1..8");
     AcceptArgs a{toks, preds, T, force_all, pos, slot, R, n_out, next_tok, gen_ring, gen_count, gen_cap,
                  xout, h_last, h_prev, H};
-    hipLaunchKernelGGL(accept_kernel, dim3(1), dim3(256), 0, s, a);
+    const int blocks = h_last && xout ? std::max(1, (H + 255) / 256) : 1;
+    hipLaunchKernelGGL(accept_kernel, dim3(blocks), dim3(256), 0, s, a);
     check_launch("accept_kernel");
 }
 
