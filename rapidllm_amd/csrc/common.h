@@ -90,6 +90,25 @@ __device__ inline float wave_max(float v) {
     return v;
 }
 
+// Sum over aligned groups of 8 (or 16) consecutive lanes with DPP lane moves
+// (no LDS round trip).  Butterfly pairing as xor 1, 2, 4 (, 8): every lane of a
+// group ends with the bitwise same sum.
+template <int kCtrl>
+__device__ inline float dpp_move(float v) {
+    return __int_as_float(__builtin_amdgcn_update_dpp(0, __float_as_int(v), kCtrl, 0xF, 0xF, false));
+}
+__device__ inline float group8_sum(float v) {
+    v += dpp_move<0xB1>(v);   // quad_perm [1,0,3,2]: xor 1
+    v += dpp_move<0x4E>(v);   // quad_perm [2,3,0,1]: xor 2
+    v += dpp_move<0x141>(v);  // row_half_mirror: the other quad of the 8-lane half row
+    return v;
+}
+__device__ inline float group16_sum(float v) {
+    v = group8_sum(v);
+    v += dpp_move<0x140>(v);  // row_mirror: the other half of the 16-lane row
+    return v;
+}
+
 // Split an fp32 value into two bf16 terms whose sum carries 16 significant bits:
 // hi = x truncated to bf16, mid = (x - hi) truncated to bf16.  x - hi is exact in
 // fp32; the remainder lost is < 2^-16 |x|.  bf16 keeps fp32's exponent range, so

@@ -214,8 +214,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
             S[r] *= g;
             kv += S[r] * k_s[t][kRowsPer * c + r];
         }
-#pragma unroll
-        for (int o = 1; o < kRowChunks; o <<= 1) kv += __shfl_xor(kv, o, 64);
+        kv = group16_sum(kv);
         const float delta = (v_s[t][jj] - kv) * beta;
         float ov = 0.f;
 #pragma unroll
@@ -223,8 +222,7 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
             S[r] += k_s[t][kRowsPer * c + r] * delta;
             ov += S[r] * q_s[t][kRowsPer * c + r];
         }
-#pragma unroll
-        for (int o = 1; o < kRowChunks; o <<= 1) ov += __shfl_xor(ov, o, 64);
+        ov = group16_sum(ov);
         if (c == 0) p.o[static_cast<size_t>(t) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
         if (per_token || t == T - 1) {
             float4* dp = reinterpret_cast<float4*>(s_dst(t) + s_off);
@@ -385,16 +383,16 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
     }
     __syncthreads();
 
-    // L2 norms of q and k (double sums over 128), waves 0 / 1
+    // L2 norms of q and k (double sums over 128): wave 2t + {0, 1} takes q / k of
+    // token t, all tokens at once
     {
         const int wave = tid >> 6, lane = tid & 63;
-        if (wave < 2) {
-            float(*vec)[kDK] = wave == 0 ? q_s : k_s;
-            for (int t = 0; t < T; ++t) {
-                const double a0 = vec[t][lane], a1 = vec[t][lane + 64];
-                const double ss = wave_sum_d(a0 * a0 + a1 * a1);
-                if (lane == 0) red_s[wave][t] = ss;
-            }
+        if (wave < 2 * T) {
+            const int t = wave >> 1, which = wave & 1;
+            float(*vec)[kDK] = which == 0 ? q_s : k_s;
+            const double a0 = vec[t][lane], a1 = vec[t][lane + 64];
+            const double ss = wave_sum_d(a0 * a0 + a1 * a1);
+            if (lane == 0) red_s[which][t] = ss;
         }
     }
     __syncthreads();
@@ -417,8 +415,7 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
             S[r] *= g;
             kv += S[r] * k_s[t][kHRows * c + r];
         }
-#pragma unroll
-        for (int o = 1; o < kHChunks; o <<= 1) kv += __shfl_xor(kv, o, 64);
+        kv = group8_sum(kv);
         const float delta = ((col_ok ? v_s[t][j] : 0.f) - kv) * beta;
         float ov = 0.f;
 #pragma unroll
@@ -426,8 +423,7 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
             S[r] += k_s[t][kHRows * c + r] * delta;
             ov += S[r] * q_s[t][kHRows * c + r];
         }
-#pragma unroll
-        for (int o = 1; o < kHChunks; o <<= 1) ov += __shfl_xor(ov, o, 64);
+        ov = group8_sum(ov);
         if (c == 0 && col_ok) {
             o_s[t][j] = ov;
             if (p.o) p.o[static_cast<size_t>(t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
