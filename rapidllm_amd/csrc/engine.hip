@@ -158,6 +158,7 @@ class Engine {
             RL_HIP(hipMemsetAsync(S_[l], 0, s_slot_ * sizeof(float), st_));
             RL_HIP(hipMemsetAsync(conv_[l], 0, conv_slot_ * sizeof(float), st_));
         }
+        for (int* n : rec_n_) RL_HIP(hipMemsetAsync(n, 0, c_.n_v_heads * sizeof(int), st_));
         RL_HIP(hipMemsetAsync(h_last_, 0, c_.hidden * sizeof(float), st_));
         RL_HIP(hipMemsetAsync(h_prev_, 0, c_.hidden * sizeof(float), st_));
         RL_HIP(hipStreamSynchronize(st_));
@@ -351,6 +352,8 @@ class Engine {
     // states
     std::vector<float*> S_, conv_;
     size_t s_slot_ = 0, conv_slot_ = 0;
+    std::vector<float*> rec_;   // DeltaNet replay records per layer (head kernel)
+    std::vector<int*> rec_n_;
     std::vector<uint16_t*> kc_, vt_;
     // activations / workspaces
     int* scal_ = nullptr;
@@ -519,13 +522,10 @@ class Engine {
             }
         }
 
-        // states
+        // states (the recurrent state S is allocated below, once the kernel is chosen)
         s_slot_ = static_cast<size_t>(nv) * dv * dk;
         conv_slot_ = static_cast<size_t>(conv_dim) * c_.conv_k;
-        for (int l = 0; l < nd; ++l) {
-            S_.push_back(mem_.get_n<float>(s_slot_ * R_));
-            conv_.push_back(mem_.get_n<float>(conv_slot_ * R_));
-        }
+        for (int l = 0; l < nd; ++l) conv_.push_back(mem_.get_n<float>(conv_slot_ * R_));
         const size_t kv = static_cast<size_t>(nkv) * ctx_ * hd;
         for (int l = 0; l < na; ++l) {
             kc_.push_back(mem_.get_n<uint16_t>(kv));
@@ -558,6 +558,15 @@ class Engine {
             for (const Layer& Ly : L_)
                 if (Ly.kind == RL_LAYER_DELTA && Ly.gnorm_n != c_.v_dim) per_head = false;
             gdn_fused_norm_ = fold_norm_ && per_head;
+        }
+        // one committed S per layer plus per-token records with the head kernel, a
+        // ring of R states with the multi-workgroup kernel
+        for (int l = 0; l < nd; ++l) {
+            S_.push_back(mem_.get_n<float>(s_slot_ * (gdn_fused_norm_ ? 1 : R_)));
+            if (gdn_fused_norm_) {
+                rec_.push_back(mem_.get_n<float>(static_cast<size_t>(tmax_) * nv * kGdnRecFloats));
+                rec_n_.push_back(mem_.get_n<int>(nv));
+            }
         }
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
@@ -879,9 +888,11 @@ class Engine {
                 gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, T, kEpiStore, nullptr, io_in);
                 if (gdn_fused_norm_) {
                     // recurrent update + per-head gated RMSNorm + out_proj packing in one kernel
+                    // a step that consumes all its tokens commits S directly
+                    const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, T > 1 && !force_all};
                     gdn_decode_head(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
-                                    Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot,
-                                    conv_slot_, s_slot_, R_, nullptr, ybuf_ + Ly.off_z, Ly.gnorm, frag_, T, nk, nv,
+                                    Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot,
+                                    conv_slot_, R_, &rec, nullptr, ybuf_ + Ly.off_z, Ly.gnorm, frag_, T, nk, nv,
                                     c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                 } else {
                     gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,

@@ -239,6 +239,9 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
 // head in one workgroup the gated RMSNorm of the head's output (reference
 // ops.cpp:129-156, per head of dv, eps 1e-6, double sum) and the packing into the
 // out_proj fragments are done here too: y = gamma * (o / rms(o)) * silu(z).
+// The recurrent state is not kept in the ring: with the conv ring the kernel keeps
+// one committed S and the per-token records of GdnRecords (about 1 KiB per head and
+// token instead of a 64 KiB state slice per head and token).
 constexpr int kHT = 1024;
 constexpr int kHChunks = 8;
 constexpr int kHRows = kDK / kHChunks;  // 16
@@ -249,6 +252,7 @@ struct GdnHeadArgs {
     const float* z;      // [T][ld_in] at the head-0 z column (gated norm gate)
     const float* gamma;  // [dv]
     i32x4* frag;         // out_proj input fragments (may be null)
+    GdnRecords rec;      // rec.rec == nullptr: no records (direct mode)
 };
 
 __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
@@ -272,13 +276,12 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
     __shared__ float gate_s[kMaxT][2];
     __shared__ double red_s[2][kMaxT];
     __shared__ float inv_s[kMaxT];
+    __shared__ float rk_s[kMaxT][kDK];     // replayed records: k, delta, g
+    __shared__ float rd_s[kMaxT][kHMaxDv];
+    __shared__ float rg_s[kMaxT];
 
     const int slot0 = p.cur ? *p.cur : 0;
-    const float* S_in = p.cur ? p.S_in + static_cast<size_t>(slot0) * p.s_slot : p.S_in;
     const float* conv_in = p.cur ? p.conv_in + static_cast<size_t>(slot0) * p.conv_slot : p.conv_in;
-    auto s_dst = [&](int t) -> float* {
-        return p.cur ? const_cast<float*>(p.S_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.s_slot : p.S_out;
-    };
     auto conv_dst = [&](int t) -> float* {
         return p.cur ? const_cast<float*>(p.conv_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.conv_slot
                      : p.conv_out;
@@ -289,7 +292,7 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
     const size_t s_off = (static_cast<size_t>(h) * dv + (col_ok ? j : 0)) * kDK + kHRows * c;
     float S[kHRows];
     {
-        const float4* sp = reinterpret_cast<const float4*>(S_in + s_off);
+        const float4* sp = reinterpret_cast<const float4*>(p.S_in + s_off);
 #pragma unroll
         for (int r = 0; r < kHRows / 4; ++r) {
             const float4 v = sp[r];
@@ -297,6 +300,24 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
             S[4 * r + 1] = v.y;
             S[4 * r + 2] = v.z;
             S[4 * r + 3] = v.w;
+        }
+    }
+
+    const bool records = a.rec.rec != nullptr;
+    const bool keep = records && a.rec.keep;
+    const int n_rep = records ? min(min(*a.rec.n_cons, a.rec.count[h]), kMaxT) : 0;
+    float* rec_h = records ? a.rec.rec + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
+    const size_t rec_t = static_cast<size_t>(p.nv) * kGdnRecFloats;  // token stride of the records
+
+    // the previous call's records of this head: thread (t, i) loads k[i], delta[i]
+    // of token t (8 x 128 = 1024 threads), before any record store of this call
+    if (n_rep > 0) {
+        const int t = tid / kDK, i = tid % kDK;
+        if (t < n_rep) {
+            const float* r = rec_h + t * rec_t;
+            rk_s[t][i] = r[i];
+            if (i < dv) rd_s[t][i] = r[kDK + i];
+            if (i == 0) rg_s[t] = r[2 * kDK];
         }
     }
 
@@ -402,8 +423,25 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
         const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t]) + 1e-6f);
         const float ik = 1.f / sqrtf(static_cast<float>(red_s[1][t]) + 1e-6f);
         q_s[t][i] = (q_s[t][i] * iq) * qscale;
-        k_s[t][i] = k_s[t][i] * ik;
+        const float kn = k_s[t][i] * ik;
+        k_s[t][i] = kn;
+        if (keep) rec_h[t * rec_t + i] = kn;
     }
+    if (keep && tid < T) rec_h[tid * rec_t + 2 * kDK] = gate_s[tid][0];
+
+    // replay the consumed records of the previous call (same operations as below)
+    for (int t = 0; t < n_rep; ++t) {
+        const float g = rg_s[t];
+        const float delta = col_ok ? rd_s[t][j] : 0.f;
+#pragma unroll
+        for (int r = 0; r < kHRows; ++r) S[r] = __fmaf_rn(rk_s[t][kHRows * c + r], delta, __fmul_rn(S[r], g));
+    }
+    auto store_state = [&] {
+        float4* dp = reinterpret_cast<float4*>(p.S_out + s_off);
+#pragma unroll
+        for (int r = 0; r < kHRows / 4; ++r) dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
+    };
+    if (keep && n_rep > 0 && col_ok) store_state();
     __syncthreads();
 
     // delta rule, token by token
@@ -412,29 +450,26 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
         float kv = 0.f;
 #pragma unroll
         for (int r = 0; r < kHRows; ++r) {
-            S[r] *= g;
-            kv += S[r] * k_s[t][kHRows * c + r];
+            S[r] = __fmul_rn(S[r], g);
+            kv = __fmaf_rn(S[r], k_s[t][kHRows * c + r], kv);
         }
         kv = group8_sum(kv);
         const float delta = ((col_ok ? v_s[t][j] : 0.f) - kv) * beta;
         float ov = 0.f;
 #pragma unroll
         for (int r = 0; r < kHRows; ++r) {
-            S[r] += k_s[t][kHRows * c + r] * delta;
-            ov += S[r] * q_s[t][kHRows * c + r];
+            S[r] = __fmaf_rn(k_s[t][kHRows * c + r], delta, S[r]);
+            ov = __fmaf_rn(S[r], q_s[t][kHRows * c + r], ov);
         }
         ov = group8_sum(ov);
         if (c == 0 && col_ok) {
             o_s[t][j] = ov;
             if (p.o) p.o[static_cast<size_t>(t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
-        }
-        if (col_ok && (per_token || t == T - 1)) {
-            float4* dp = reinterpret_cast<float4*>(s_dst(t) + s_off);
-#pragma unroll
-            for (int r = 0; r < kHRows / 4; ++r)
-                dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
+            if (keep) rec_h[t * rec_t + kDK + j] = delta;
         }
     }
+    if (!keep && col_ok) store_state();
+    if (records && tid == 0) a.rec.count[h] = keep ? T : 0;
     if (!a.frag) return;
 
     // gated RMSNorm of the head (wave t reduces token t) and packing
@@ -472,25 +507,29 @@ bool gdn_head_supported(int dk, int dv, int K) { return dk == kDK && dv <= kHMax
 
 void gdn_decode_head(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
                      const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
-                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, size_t s_slot, int R, float* o,
-                     const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv, int K,
-                     int v_tiled, hipStream_t s) {
+                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R, const GdnRecords* rec,
+                     float* o, const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv,
+                     int K, int v_tiled, hipStream_t s) {
     RL_REQUIRE(gdn_head_supported(dk, dv, K), RL_ERR_UNSUPPORTED, "gdn_decode_head: dk 128, dv <= 128, conv 4");
     RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_head: T must be in 1..8");
     RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode_head: nv must be a multiple of nk");
     RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && (o || frag), RL_ERR_RANGE,
                "gdn_decode_head: null pointer");
     RL_REQUIRE(!frag || (z && gamma), RL_ERR_RANGE, "gdn_decode_head: the gated norm needs z and gamma");
+    RL_REQUIRE(S_out, RL_ERR_RANGE, "gdn_decode_head: null output state");
     if (cur) {
         RL_REQUIRE(R > T, RL_ERR_RANGE, "gdn_decode_head: ring needs more slots than tokens");
+        RL_REQUIRE(rec && rec->rec && rec->count && rec->n_cons && S_out == S_in, RL_ERR_RANGE,
+                   "gdn_decode_head: the conv ring needs records and one committed state");
     } else {
-        RL_REQUIRE(conv_out && S_out && conv_out != conv_in, RL_ERR_RANGE, "gdn_decode_head: bad output state");
+        RL_REQUIRE(conv_out && conv_out != conv_in, RL_ERR_RANGE, "gdn_decode_head: bad output conv window");
     }
-    GdnHeadArgs p{{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, s_slot,
-                   R, o, T, nk, nv, dv, K, v_tiled},
+    GdnHeadArgs p{{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, 0, R,
+                   o, T, nk, nv, dv, K, v_tiled},
                   z,
                   gamma,
-                  static_cast<i32x4*>(frag)};
+                  static_cast<i32x4*>(frag),
+                  rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0}};
     hipLaunchKernelGGL(gdn_head_kernel, dim3(nv), dim3(kHT), 0, s, p);
     check_launch("gdn_head_kernel");
 }
@@ -529,7 +568,8 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
     return guard([&] {
         if (rl::gdn_head_supported(dk, dv, conv_k))
             rl::gdn_decode_head(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0,
-                                0, 0, o, nullptr, nullptr, nullptr, T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));
+                                0, nullptr, o, nullptr, nullptr, nullptr, T, nk, nv, dk, dv, conv_k, v_tiled,
+                                S(stream));
         else
             rl::gdn_decode(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0, 0,
                            0, o, T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));

@@ -66,11 +66,29 @@ void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, con
 // (gamma [dv], gate z at z[t*ld_in + h*dv + j]) and the packing into fragments fused
 // (frag may be null; o may be null when frag is given).
 bool gdn_head_supported(int dk, int dv, int K);
+// Speculative bookkeeping of the one-head-per-workgroup DeltaNet kernel.  The state
+// S is kept once, committed up to the last consumed token.  A call that may be
+// partly rejected (keep = 1) stores, per head and token, the normalised k, the
+// update delta = (v - S^T k) * beta and the decay g (kGdnRecFloats floats), and
+// leaves S at the committed point; the next call first replays the first
+// min(*n_cons, count[h]) records onto S (the same float operations the update
+// performs, so the result is bit-identical to having kept S after that token).
+constexpr int kGdnRecFloats = 264;  // k[128] | delta[dv <= 128] | g
+struct GdnRecords {
+    float* rec;          // [max_t][nv][kGdnRecFloats]
+    int* count;          // [nv]: tokens recorded by the previous call
+    const int* n_cons;   // tokens the previous call consumed
+    int keep;            // record this call's tokens instead of committing them
+};
+// conv window: a ring of R slots when cur != nullptr (slot *cur read, slot
+// (*cur + 1 + t) % R written after token t), else conv_in -> conv_out.
+// S: S_in -> S_out (may alias); with cur != nullptr, rec must be given and
+// S_out == S_in is the committed state.
 void gdn_decode_head(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
                      const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
-                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, size_t s_slot, int R, float* o,
-                     const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv, int K,
-                     int v_tiled, hipStream_t s);
+                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R, const GdnRecords* rec,
+                     float* o, const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv,
+                     int K, int v_tiled, hipStream_t s);
 
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);
