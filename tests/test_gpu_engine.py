@@ -119,6 +119,40 @@ def test_spec_verify_rollback(gpu, fp8_pair):
     del ref_logits
 
 
+@pytest.mark.parametrize("n_ok", [1, 2, 3, 4])
+def test_spec_verify_then_decode_matches_plain_decode(gpu, fp8_pair, n_ok):
+    """After a verify that consumes n_ok of 4 tokens, the following steps see the
+    recurrent state after exactly those tokens: two more T=1 steps and another
+    verify give the logits of plain T=1 decoding, bit for bit."""
+    spec, W, eng, orc_m = fp8_pair
+    prompt = [3, 1, 4, 1, 5]
+    eng.prefill(prompt)
+    chain = [eng.greedy()]
+    for _ in range(7):
+        eng.decode_token(chain[-1])
+        chain.append(eng.greedy())
+    # plain decoding of chain[0 .. n_ok + 3], logits after each token
+    eng.prefill(prompt)
+    plain = []
+    for t in chain[: n_ok + 4]:
+        eng.decode_token(t)
+        plain.append(eng.copy_logits())
+    # verify [chain[0], .., chain[n_ok - 1], wrong ...]: exactly n_ok consumed
+    eng.prefill(prompt)
+    toks = chain[:n_ok] + [(chain[n_ok] + 1) % spec.vocab] * (4 - n_ok)
+    k, preds = eng.spec_verify(toks[:4])
+    assert k == n_ok and list(preds[:k]) == chain[1 : k + 1]
+    assert eng.pos() == len(prompt) + n_ok
+    eng.decode_token(chain[n_ok])
+    assert np.array_equal(eng.copy_logits(), plain[n_ok])
+    eng.decode_token(chain[n_ok + 1])
+    assert np.array_equal(eng.copy_logits(), plain[n_ok + 1])
+    # a second verify after the replayed records: its first row again
+    k2, preds2 = eng.spec_verify([chain[n_ok + 2], (chain[n_ok + 3] + 1) % spec.vocab])
+    assert k2 == 1 and preds2[0] == chain[n_ok + 3]
+    assert np.array_equal(eng.copy_logits(), plain[n_ok + 2])
+
+
 @pytest.mark.parametrize("quant", [M.Q_Q4_K, M.Q_Q6_K, M.Q_BF16])
 def test_other_weight_formats_match_oracle(gpu, orc, quant):
     spec = mini_spec(n_layers=4, layer_kinds=[0, 1, 0, 0])
