@@ -57,6 +57,7 @@ def step_bytes(spec, T, ctx):
 
 
 EPI_STORE, EPI_SWIGLU, EPI_PARTIAL, EPI_ADDNORM = 0, 2, 3, 4
+EPI_ADDNORM_BS = 104  # add-norm with the per-block input scale (DeltaNet out_proj)
 SPLIT = 4
 
 
@@ -64,7 +65,8 @@ def gemm_shapes(spec):
     """(m, n, count per step, epilogue) of the block-FP8 GEMM launches in one step,
     as the engine issues them: fused [qkv|z|a|b] and [q|gate;k;v] stores, residual
     GEMMs adding into x with the next RMSNorm's fragments and sums of squares,
-    interleaved gate/up with the SwiGLU epilogue."""
+    interleaved gate/up with the SwiGLU epilogue.  The DeltaNet out_proj also
+    scales each 128-column input block by the head's gated-RMSNorm factor."""
     H, I = spec.hidden, spec.intermediate
     nv, dv = spec.n_v_heads, spec.v_dim
     nq, nkv, hd = spec.n_q, spec.n_kv, spec.head_dim
@@ -73,7 +75,7 @@ def gemm_shapes(spec):
     a16 = lambda v: (v + 15) // 16 * 16
     m_in = a16(spec.conv_dim) + a16(nv * dv) + 2 * a16(nv)
     return [
-        (m_in, H, n_d, EPI_STORE), (H, nv * dv, n_d, EPI_ADDNORM),
+        (m_in, H, n_d, EPI_STORE), (H, nv * dv, n_d, EPI_ADDNORM_BS if dv == 128 else EPI_ADDNORM),
         (2 * nq * hd + 2 * nkv * hd, H, n_a, EPI_STORE), (H, nq * hd, n_a, EPI_ADDNORM),
         (2 * a16(I), H, spec.n_layers, EPI_SWIGLU), (H, I, spec.n_layers, EPI_ADDNORM),
     ]
@@ -98,7 +100,9 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
     n_launch = 0
     per = []
     s = C_stream()
-    for m, n, count, epi in gemm_shapes(spec):
+    for m, n, count, epi_kind in gemm_shapes(spec):
+        block_scale = epi_kind == EPI_ADDNORM_BS
+        epi = EPI_ADDNORM if block_scale else epi_kind
         W = synth.fp8_weight(r, m, n)
         sc = synth.fp8_scales(r, m, n)
         lin = ops.Fp8Linear(W, sc)
@@ -113,24 +117,27 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
         fo = ops.act_frag_buffer(m // 2 if epi == EPI_SWIGLU else m, T) if epi in (EPI_SWIGLU, EPI_ADDNORM) else None
         gam = DeviceBuffer.from_numpy(np.zeros(m, np.float32))
         ssq = DeviceBuffer(4 * T * ((m + 31) // 32))
+        bss = DeviceBuffer.from_numpy(np.full((n // 128) * T * 4, 32.0, np.float32)) if block_scale else None
         yd.zero(s)
         call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, s)
         ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
         one = (C.c_void_p * 1)(lin.w.ptr)
         ms, warm = C.c_float(), C.c_float()
-        args = (lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr if fo else None, gam.ptr, ssq.ptr, m, n, T, epi, SPLIT)
+        args = (lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr if fo else None, gam.ptr, ssq.ptr, bss.ptr if bss else None, m,
+                n, T, epi, SPLIT)
         call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, len(copies), s, C.byref(ms))  # warm-up
         call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, iters, s, C.byref(ms))
         call("rl_hip_time_gemm_fp8", one, 1, *args, iters, s, C.byref(warm))
         ms, warm = ms.value, warm.value
         b = m * n + 4 * ((m + 127) // 128) * ((n + 127) // 128) + 4 * T * (m + n)
-        per.append({"m": m, "n": n, "epilogue": {0: "store", 2: "swiglu", 3: f"split{SPLIT}", 4: "add+norm"}[epi],
+        label = {0: "store", 2: "swiglu", 3: f"split{SPLIT}", 4: "add+norm", 104: "add+norm+block-scale"}[epi_kind]
+        per.append({"m": m, "n": n, "epilogue": label,
                     "per_step": count, "us": round(ms * 1e3, 2), "GBps": round(b / ms / 1e6, 1),
                     "warm_us": round(warm * 1e3, 2), "copies": len(copies)})
         tot_ms += ms * count
         tot_bytes += b * count
         n_launch += count
-        del lin, xd, frag, yd, fo, gam, ssq, copies
+        del lin, xd, frag, yd, fo, gam, ssq, bss, copies
     avg_ms = tot_ms / n_launch
     avg_bytes = tot_bytes / n_launch
     return avg_ms, avg_bytes, per

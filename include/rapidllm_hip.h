@@ -243,10 +243,13 @@ int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
  * partials (Y [split][T][m]), 2 SwiGLU over interleaved gate/up tiles writing the
  * next linear's fragments to frag_out (act_frag_bytes(m/2, T)), 4 residual add with
  * the next RMSNorm's data (Y [T][m] += result; frag_out = fragments of Y * (1 + gamma),
- * act_frag_bytes(m, T); sumsq [ceil(m/32)][T] = per-32-row sums of squares). */
+ * act_frag_bytes(m, T); sumsq [ceil(m/32)][T] = per-32-row sums of squares).
+ * block_sumsq (add-norm only, may be null): [n/128][T][4] partial sums of squares of
+ * the input per 128-column block, each block's products then scaled per token by
+ * 1/sqrt(sum/128 + 1e-6) (the DeltaNet out_proj's folded gated RMSNorm). */
 int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
-                         float* Y, void* frag_out, const float* gamma, float* sumsq, int m, int n, int T,
-                         int epilogue, int split, int iters, void* stream, float* avg_ms);
+                         float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
+                         int m, int n, int T, int epilogue, int split, int iters, void* stream, float* avg_ms);
 
 #ifdef __cplusplus
 }

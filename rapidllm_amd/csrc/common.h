@@ -72,17 +72,6 @@ typedef int i32x4 __attribute__((ext_vector_type(4)));
 typedef int i32x2 __attribute__((ext_vector_type(2)));
 
 // Wave-wide sum / max through cross-lane moves (DPP/permute lowered by the compiler).
-__device__ inline float wave_sum(float v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
-
-__device__ inline double wave_sum_d(double v) {
-#pragma unroll
-    for (int o = 32; o > 0; o >>= 1) v += __shfl_xor(v, o, 64);
-    return v;
-}
 
 __device__ inline float wave_max(float v) {
 #pragma unroll
@@ -107,6 +96,45 @@ __device__ inline float group16_sum(float v) {
     v = group8_sum(v);
     v += dpp_move<0x140>(v);  // row_mirror: the other half of the 16-lane row
     return v;
+}
+
+// Whole-wave sums (all 64 lanes active): the 16-lane row sums by DPP, then the four
+// rows combined as (row0 + row1) + (row2 + row3) from lanes 0, 16, 32, 48; every
+// lane returns the same value.
+__device__ inline float wave_sum(float v) {
+    v = group16_sum(v);
+    const float a = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 0));
+    const float b = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 16));
+    const float c = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 32));
+    const float d = __int_as_float(__builtin_amdgcn_readlane(__float_as_int(v), 48));
+    return (a + b) + (c + d);
+}
+
+template <int kCtrl>
+__device__ inline double dpp_move_d(double v) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const int lo = __builtin_amdgcn_update_dpp(0, static_cast<int>(u & 0xffffffffu), kCtrl, 0xF, 0xF, false);
+    const int hi = __builtin_amdgcn_update_dpp(0, static_cast<int>(u >> 32), kCtrl, 0xF, 0xF, false);
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(static_cast<unsigned>(hi)) << 32) |
+                                                       static_cast<unsigned>(lo)));
+}
+__device__ inline double readlane_d(double v, int lane) {
+    const unsigned long long u = static_cast<unsigned long long>(__double_as_longlong(v));
+    const unsigned lo = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u & 0xffffffffu), lane));
+    const unsigned hi = static_cast<unsigned>(__builtin_amdgcn_readlane(static_cast<int>(u >> 32), lane));
+    return __longlong_as_double(static_cast<long long>((static_cast<unsigned long long>(hi) << 32) | lo));
+}
+// 16-lane row sum of doubles (every lane of the row gets the same value)
+__device__ inline double group16_sum_d(double v) {
+    v += dpp_move_d<0xB1>(v);
+    v += dpp_move_d<0x4E>(v);
+    v += dpp_move_d<0x141>(v);
+    v += dpp_move_d<0x140>(v);
+    return v;
+}
+__device__ inline double wave_sum_d(double v) {
+    v = group16_sum_d(v);
+    return (readlane_d(v, 0) + readlane_d(v, 16)) + (readlane_d(v, 32) + readlane_d(v, 48));
 }
 
 // Split an fp32 value into two bf16 terms whose sum carries 16 significant bits:

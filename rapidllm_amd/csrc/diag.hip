@@ -68,8 +68,8 @@ int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream) {
 }
 
 int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
-                         float* Y, void* frag_out, const float* gamma, float* sumsq, int m, int n, int T,
-                         int epilogue, int split, int iters, void* stream, float* avg_ms) {
+                         float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
+                         int m, int n, int T, int epilogue, int split, int iters, void* stream, float* avg_ms) {
     return guard([&] {
         RL_REQUIRE(w_copies && n_copies >= 1 && iters >= 1 && avg_ms, RL_ERR_RANGE, "time_gemm: bad arguments");
         RL_REQUIRE(epilogue == kEpiStore || epilogue == kEpiPartial || epilogue == kEpiSwiGLU ||
@@ -83,6 +83,10 @@ int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float*
         NormIO io;
         io.gamma_out = gamma;
         io.ss_out = sumsq;
+        RL_REQUIRE(!block_sumsq || epilogue == kEpiAddNorm, RL_ERR_RANGE, "time_gemm: block scale with add-norm only");
+        io.kss = block_sumsq;
+        io.kss_n = 128;
+        io.kss_eps = 1e-6f;
         const NormIO* iop = epilogue == kEpiAddNorm ? &io : nullptr;
         hipEvent_t a, b;
         RL_HIP(hipEventCreate(&a));

@@ -158,7 +158,7 @@ class Engine {
             RL_HIP(hipMemsetAsync(S_[l], 0, s_slot_ * sizeof(float), st_));
             RL_HIP(hipMemsetAsync(conv_[l], 0, conv_slot_ * sizeof(float), st_));
         }
-        for (int* n : rec_n_) RL_HIP(hipMemsetAsync(n, 0, c_.n_v_heads * sizeof(int), st_));
+        for (int* n : rec_n_) RL_HIP(hipMemsetAsync(n, 0, static_cast<size_t>(R_) * c_.n_v_heads * sizeof(int), st_));
         RL_HIP(hipMemsetAsync(h_last_, 0, c_.hidden * sizeof(float), st_));
         RL_HIP(hipMemsetAsync(h_prev_, 0, c_.hidden * sizeof(float), st_));
         RL_HIP(hipStreamSynchronize(st_));
@@ -354,6 +354,7 @@ class Engine {
     size_t s_slot_ = 0, conv_slot_ = 0;
     std::vector<float*> rec_;   // DeltaNet replay records per layer (head kernel)
     std::vector<int*> rec_n_;
+    float* gss_ = nullptr;      // per-head partial sums of o^2 for the folded gated norm
     std::vector<uint16_t*> kc_, vt_;
     // activations / workspaces
     int* scal_ = nullptr;
@@ -554,20 +555,22 @@ class Engine {
         // DeltaNet kernel, when one workgroup can hold a head
         {
             const int zd = c_.n_v_heads * c_.v_dim;
-            bool per_head = gdn_head_supported(c_.k_dim, c_.v_dim, c_.conv_k) && zd >= 256;
+            bool per_head = gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && c_.v_dim == 128 && zd >= 256 &&
+                            zd <= 8192;  // out_proj's block-scale GEMM: n <= 8192
             for (const Layer& Ly : L_)
                 if (Ly.kind == RL_LAYER_DELTA && Ly.gnorm_n != c_.v_dim) per_head = false;
             gdn_fused_norm_ = fold_norm_ && per_head;
         }
-        // one committed S per layer plus per-token records with the head kernel, a
-        // ring of R states with the multi-workgroup kernel
+        // one committed S per layer plus R banks of per-token records with the fused
+        // kernel, a ring of R states with the unfused one
         for (int l = 0; l < nd; ++l) {
             S_.push_back(mem_.get_n<float>(s_slot_ * (gdn_fused_norm_ ? 1 : R_)));
             if (gdn_fused_norm_) {
-                rec_.push_back(mem_.get_n<float>(static_cast<size_t>(tmax_) * nv * kGdnRecFloats));
-                rec_n_.push_back(mem_.get_n<int>(nv));
+                rec_.push_back(mem_.get_n<float>(static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats));
+                rec_n_.push_back(mem_.get_n<int>(static_cast<size_t>(R_) * nv));
             }
         }
+        gss_ = mem_.get_n<float>(static_cast<size_t>(nv) * tmax_ * 4);
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
@@ -887,13 +890,18 @@ class Engine {
             if (Ly.kind == RL_LAYER_DELTA) {
                 gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, T, kEpiStore, nullptr, io_in);
                 if (gdn_fused_norm_) {
-                    // recurrent update + per-head gated RMSNorm + out_proj packing in one kernel
-                    // a step that consumes all its tokens commits S directly
-                    const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, T > 1 && !force_all};
-                    gdn_decode_head(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
-                                    Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot,
-                                    conv_slot_, R_, &rec, nullptr, ybuf_ + Ly.off_z, Ly.gnorm, frag_, T, nk, nv,
-                                    c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                    // recurrent update + gated RMSNorm's elementwise part + out_proj
+                    // packing in one kernel; out_proj applies the per-head 1/rms.  A step
+                    // that consumes all its tokens commits S directly.
+                    const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, tmax_,
+                                         T > 1 && !force_all};
+                    gdn_decode_fused(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
+                                     Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot,
+                                     conv_slot_, R_, &rec, nullptr, ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, T, nk,
+                                     nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                    out.kss = gss_;
+                    out.kss_n = dv;
+                    out.kss_eps = 1e-6f;
                 } else {
                     gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
                                Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_,
@@ -902,6 +910,7 @@ class Engine {
                                st_);
                 }
                 gemm_on(Ly.out_proj, frag_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
+                out.kss = nullptr;
             } else {
                 gemm_on(Ly.qkv_parts[0], frag_x_, ybuf_, Ly.qkv_width, Ly.qkv_parts[0].m, T, kEpiStore, nullptr,
                         io_in);

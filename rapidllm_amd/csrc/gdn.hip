@@ -233,51 +233,57 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
     }
 }
 
-// ---------------------------------------------------------------- one head per WG
-// Same arithmetic as gdn_decode_kernel, one workgroup of 1024 threads per v-head
-// (dv <= 128): thread (c, j) keeps S rows 16c .. 16c+15 of column j.  With the whole
-// head in one workgroup the gated RMSNorm of the head's output (reference
-// ops.cpp:129-156, per head of dv, eps 1e-6, double sum) and the packing into the
-// out_proj fragments are done here too: y = gamma * (o / rms(o)) * silu(z).
+// ------------------------------------------------------- (head, 32 columns) per WG
+// Same arithmetic as gdn_decode_kernel with 32 value columns per workgroup
+// (nv * dv / 32 workgroups: the state slices stream through that many CUs) and
+// thread (c, jj) keeping S rows 16c .. 16c+15 of column j = 32*cc + jj.  The gated
+// RMSNorm of the head (reference ops.cpp:129-156, per head of dv, eps 1e-6, double
+// sum) is split: this kernel packs y = gamma * o * silu(z) into the out_proj input
+// fragments and writes the chunk's sum of o^2 per token; out_proj scales the
+// head's column block by 1/rms (NormIO::kss).
 // The recurrent state is not kept in the ring: with the conv ring the kernel keeps
-// one committed S and the per-token records of GdnRecords (about 1 KiB per head and
-// token instead of a 64 KiB state slice per head and token).
-constexpr int kHT = 1024;
-constexpr int kHChunks = 8;
-constexpr int kHRows = kDK / kHChunks;  // 16
-constexpr int kHMaxDv = kHT / kHChunks;  // 128
+// one committed S and the per-token records of GdnRecords.
+constexpr int kCW = 32;                  // value columns per workgroup
+constexpr int kCChunks = 8;              // threads per column
+constexpr int kCRows = kDK / kCChunks;   // 16 rows per thread
+constexpr int kCT = kCW * kCChunks;      // 256 threads
+constexpr int kCWaves = kCT / 64;
 
-struct GdnHeadArgs {
+struct GdnFusedArgs {
     GdnArgs g;
     const float* z;      // [T][ld_in] at the head-0 z column (gated norm gate)
     const float* gamma;  // [dv]
     i32x4* frag;         // out_proj input fragments (may be null)
+    float* gss;          // [nv][T][4] partial sums of o^2 (with frag)
     GdnRecords rec;      // rec.rec == nullptr: no records (direct mode)
 };
 
-__global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
+__global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const GdnArgs& p = a.g;
     const int tid = threadIdx.x;
-    const int c = tid & (kHChunks - 1);
-    const int j = tid / kHChunks;  // value column
-    const int h = blockIdx.x;
+    const int wave = tid >> 6, lane = tid & 63;
+    const int c = tid & (kCChunks - 1);
+    const int jj = tid / kCChunks;  // column within the chunk
     const int dv = p.dv;
-    const bool col_ok = j < dv;
+    const int chunks = dv / kCW;
+    const int h = blockIdx.x / chunks;
+    const int cc = blockIdx.x % chunks;
+    const int j = cc * kCW + jj;
     const int rep = p.nv / p.nk;
     const int src = p.v_tiled ? (h % p.nk) : (h / rep);
     const int qdim = p.nk * kDK;
     const int T = p.T;
     constexpr int K = kConvK;
 
-    __shared__ float q_s[kMaxT][kDK];
+    __shared__ float q_s[kMaxT][kDK];   // conv outputs (q, k not yet normalised)
     __shared__ float k_s[kMaxT][kDK];
-    __shared__ float v_s[kMaxT][kHMaxDv];
-    __shared__ float o_s[kMaxT][kHMaxDv];
+    __shared__ float v_s[kMaxT][kCW];
+    __shared__ float o_s[kMaxT][kCW];
+    __shared__ float y_s[kMaxT][kCW];
     __shared__ float gate_s[kMaxT][2];
-    __shared__ double red_s[2][kMaxT];
-    __shared__ float inv_s[kMaxT];
-    __shared__ float rk_s[kMaxT][kDK];     // replayed records: k, delta, g
-    __shared__ float rd_s[kMaxT][kHMaxDv];
+    __shared__ double red_s[4][kMaxT];  // sums of squares: q lanes 0-63, 64-127, k 0-63, 64-127
+    __shared__ float rk_s[kMaxT][kDK];  // replayed records: k, delta, g
+    __shared__ float rd_s[kMaxT][kCW];
     __shared__ float rg_s[kMaxT];
 
     const int slot0 = p.cur ? *p.cur : 0;
@@ -288,41 +294,33 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
     };
     const bool per_token = p.cur != nullptr;
 
-    // state: 16 rows of column j (64 contiguous bytes of the transposed layout)
-    const size_t s_off = (static_cast<size_t>(h) * dv + (col_ok ? j : 0)) * kDK + kHRows * c;
-    float S[kHRows];
+    // ---- loads, in the order they are needed (vector loads complete in order):
+    // conv inputs of this thread's channels (tid: q/k channel; tid < 32 also v
+    // channel 256 + tid), gate inputs, gated-norm operands, then the state slice and
+    // the previous call's records, which are first needed after the barrier.
+    auto chan_of = [&](int ch) {
+        if (ch < kDK) return src * kDK + ch;
+        if (ch < 2 * kDK) return qdim + src * kDK + (ch - kDK);
+        return 2 * qdim + h * dv + cc * kCW + (ch - 2 * kDK);
+    };
+    const bool has_v = tid < kCW;
+    const int chan0 = chan_of(tid), chan1 = chan_of(2 * kDK + (has_v ? tid : 0));
+    float win0[K], win1[K], w0[K], w1[K], xin0[kMaxT], xin1[kMaxT];
     {
-        const float4* sp = reinterpret_cast<const float4*>(p.S_in + s_off);
+        const float4 a0 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan0) * K);
+        const float4 a1 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan1) * K);
+        const float4 b0 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan0) * K);
+        const float4 b1 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan1) * K);
+        win0[0] = a0.x, win0[1] = a0.y, win0[2] = a0.z, win0[3] = a0.w;
+        win1[0] = a1.x, win1[1] = a1.y, win1[2] = a1.z, win1[3] = a1.w;
+        w0[0] = b0.x, w0[1] = b0.y, w0[2] = b0.z, w0[3] = b0.w;
+        w1[0] = b1.x, w1[1] = b1.y, w1[2] = b1.z, w1[3] = b1.w;
 #pragma unroll
-        for (int r = 0; r < kHRows / 4; ++r) {
-            const float4 v = sp[r];
-            S[4 * r] = v.x;
-            S[4 * r + 1] = v.y;
-            S[4 * r + 2] = v.z;
-            S[4 * r + 3] = v.w;
+        for (int t = 0; t < kMaxT; ++t) {
+            xin0[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan0] : 0.f;
+            xin1[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan1] : 0.f;
         }
     }
-
-    const bool records = a.rec.rec != nullptr;
-    const bool keep = records && a.rec.keep;
-    const int n_rep = records ? min(min(*a.rec.n_cons, a.rec.count[h]), kMaxT) : 0;
-    float* rec_h = records ? a.rec.rec + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
-    const size_t rec_t = static_cast<size_t>(p.nv) * kGdnRecFloats;  // token stride of the records
-
-    // the previous call's records of this head: thread (t, i) loads k[i], delta[i]
-    // of token t (8 x 128 = 1024 threads), before any record store of this call
-    if (n_rep > 0) {
-        const int t = tid / kDK, i = tid % kDK;
-        if (t < n_rep) {
-            const float* r = rec_h + t * rec_t;
-            rk_s[t][i] = r[i];
-            if (i < dv) rd_s[t][i] = r[kDK + i];
-            if (i == 0) rg_s[t] = r[2 * kDK];
-        }
-    }
-
-    // gate inputs of token tid, loaded with the state (before any store of this
-    // thread, whose completion a later wait would otherwise include)
     float gin_a = 0.f, gin_b = 0.f, gin_A = 0.f, gin_dt = 0.f;
     if (tid < T) {
         gin_a = p.a[static_cast<size_t>(tid) * p.ld_in + h];
@@ -330,62 +328,90 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
         gin_A = p.A_log[h];
         gin_dt = p.dt_bias[h];
     }
+    float zt[kMaxT];
+    float gam = 0.f;
+    const bool gn = a.frag != nullptr && c == 0;
+    if (gn) {
+        gam = a.gamma[j];
+#pragma unroll
+        for (int t = 0; t < kMaxT; ++t) zt[t] = t < T ? a.z[static_cast<size_t>(t) * p.ld_in + h * dv + j] : 0.f;
+    }
+    // state: 16 rows of column j (64 contiguous bytes of the transposed layout)
+    const size_t s_off = (static_cast<size_t>(h) * dv + j) * kDK + kCRows * c;
+    float S[kCRows];
+    {
+        const float4* sp = reinterpret_cast<const float4*>(p.S_in + s_off);
+#pragma unroll
+        for (int r = 0; r < kCRows / 4; ++r) {
+            const float4 v = sp[r];
+            S[4 * r] = v.x;
+            S[4 * r + 1] = v.y;
+            S[4 * r + 2] = v.z;
+            S[4 * r + 3] = v.w;
+        }
+    }
+    // records: bank *cur is written, the previous call's bank is read
+    const bool records = a.rec.rec != nullptr;
+    const bool keep = records && a.rec.keep;
+    const int n_cons = records ? *a.rec.n_cons : 0;
+    const int rbank = records ? ((slot0 - n_cons) % p.R + p.R) % p.R : 0;
+    const int n_rep = records ? min(min(n_cons, a.rec.count[rbank * p.nv + h]), kMaxT) : 0;
+    const size_t rec_t = static_cast<size_t>(p.nv) * kGdnRecFloats;  // token stride
+    const size_t bank = static_cast<size_t>(a.rec.max_t) * rec_t;
+    const float* rec_r = records ? a.rec.rec + rbank * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
+    float* rec_w = records ? a.rec.rec + slot0 * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
+    float rk[kMaxT / 2], rd = 0.f, rg = 0.f;  // thread (t = tid / 128, i): two tokens per thread
+#pragma unroll
+    for (int q = 0; q < kMaxT / 2; ++q) {
+        const int e = tid + q * kCT;
+        rk[q] = e < n_rep * kDK ? rec_r[(e / kDK) * rec_t + e % kDK] : 0.f;
+    }
+    if (tid < n_rep * kCW) rd = rec_r[(tid / kCW) * rec_t + kDK + cc * kCW + tid % kCW];
+    if (tid < n_rep) rg = rec_r[tid * rec_t + 2 * kDK];
 
-    // conv1d over T tokens: 128 q + 128 k channels of the source k-head, dv v channels
-    const bool owns_qk = p.v_tiled ? (h == src) : (h == src * rep);
-    if (tid < 2 * kDK + dv) {
-        const int ch = tid;
-        int chan;
-        if (ch < kDK)
-            chan = src * kDK + ch;
-        else if (ch < 2 * kDK)
-            chan = qdim + src * kDK + (ch - kDK);
+    // ---- conv1d over T tokens (+ SiLU); q/k lanes also sum their squares per token
+    // (double), reduced per wave: the L2 norms need no pass of their own.  The
+    // q/k window state is written back by one workgroup per source k-head.
+    const bool owns_qk = cc == 0 && (p.v_tiled ? (h == src) : (h == src * rep));
+    double sq[kMaxT];
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+        sq[t] = 0.0;
+        if (t >= T) continue;
+#pragma unroll
+        for (int q = 0; q + 1 < K; ++q) {
+            win0[q] = win0[q + 1];
+            win1[q] = win1[q + 1];
+        }
+        win0[K - 1] = xin0[t];
+        win1[K - 1] = xin1[t];
+        double acc0 = 0.0, acc1 = 0.0;
+#pragma unroll
+        for (int q = 0; q < K; ++q) {
+            acc0 += static_cast<double>(w0[q]) * win0[q];
+            acc1 += static_cast<double>(w1[q]) * win1[q];
+        }
+        const float y0 = silu_f(static_cast<float>(acc0));
+        if (tid < kDK)
+            q_s[t][tid] = y0;
         else
-            chan = 2 * qdim + h * dv + (ch - 2 * kDK);
-        const bool write_state = ch >= 2 * kDK || owns_qk;
-        float win[K];
-        {
-            const float4 wv = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan) * K);
-            win[0] = wv.x;
-            win[1] = wv.y;
-            win[2] = wv.z;
-            win[3] = wv.w;
+            k_s[t][tid - kDK] = y0;
+        sq[t] = static_cast<double>(y0) * y0;
+        if (owns_qk && (per_token || t == T - 1))
+            *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan0) * K) =
+                make_float4(win0[0], win0[1], win0[2], win0[3]);
+        if (has_v) {
+            v_s[t][tid] = silu_f(static_cast<float>(acc1));
+            if (per_token || t == T - 1)
+                *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan1) * K) =
+                    make_float4(win1[0], win1[1], win1[2], win1[3]);
         }
-        // taps in registers: the per-token window stores below could alias conv_w
-        // as far as the compiler knows, which would reload it after every store
-        float w[K];
-        {
-            const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan) * K);
-            w[0] = w4.x;
-            w[1] = w4.y;
-            w[2] = w4.z;
-            w[3] = w4.w;
-        }
-        // every token's input for this channel, loaded together (one memory round
-        // trip instead of T dependent ones)
-        float xin[kMaxT];
+    }
 #pragma unroll
-        for (int t = 0; t < kMaxT; ++t) xin[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan] : 0.f;
-#pragma unroll
-        for (int t = 0; t < kMaxT; ++t) {
-            if (t >= T) break;
-#pragma unroll
-            for (int q = 0; q + 1 < K; ++q) win[q] = win[q + 1];
-            win[K - 1] = xin[t];
-            double acc = 0.0;
-#pragma unroll
-            for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
-            const float y = silu_f(static_cast<float>(acc));
-            if (ch < kDK)
-                q_s[t][ch] = y;
-            else if (ch < 2 * kDK)
-                k_s[t][ch - kDK] = y;
-            else
-                v_s[t][ch - 2 * kDK] = y;
-            if (write_state && (per_token || t == T - 1))
-                *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan) * K) =
-                    make_float4(win[0], win[1], win[2], win[3]);
-        }
+    for (int t = 0; t < kMaxT; ++t) {
+        if (t >= T) break;
+        const double ws = wave_sum_d(sq[t]);
+        if (lane == 0) red_s[wave][t] = ws;
     }
     if (tid < T) {
         const float beta = sigmoid_f(gin_b);
@@ -393,109 +419,92 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
         gate_s[tid][0] = expf(g_log);
         gate_s[tid][1] = beta;
     }
-    // the gated-norm operands of this thread's column, loaded before the barriers
-    float zt[kMaxT];
-    float gam = 0.f;
-    const bool gn = a.frag != nullptr && c == 0 && col_ok;
-    if (gn) {
-        gam = a.gamma[j];
 #pragma unroll
-        for (int t = 0; t < kMaxT; ++t) zt[t] = t < T ? a.z[static_cast<size_t>(t) * p.ld_in + h * dv + j] : 0.f;
+    for (int q = 0; q < kMaxT / 2; ++q) {
+        const int e = tid + q * kCT;
+        if (e < n_rep * kDK) rk_s[e / kDK][e % kDK] = rk[q];
     }
+    if (tid < n_rep * kCW) rd_s[tid / kCW][tid % kCW] = rd;
+    if (tid < n_rep) rg_s[tid] = rg;
     __syncthreads();
 
-    // L2 norms of q and k (double sums over 128): wave 2t + {0, 1} takes q / k of
-    // token t, all tokens at once
-    {
-        const int wave = tid >> 6, lane = tid & 63;
-        if (wave < 2 * T) {
-            const int t = wave >> 1, which = wave & 1;
-            float(*vec)[kDK] = which == 0 ? q_s : k_s;
-            const double a0 = vec[t][lane], a1 = vec[t][lane + 64];
-            const double ss = wave_sum_d(a0 * a0 + a1 * a1);
-            if (lane == 0) red_s[which][t] = ss;
-        }
-    }
-    __syncthreads();
-    const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
-    for (int e = tid; e < T * kDK; e += kHT) {
-        const int t = e / kDK, i = e % kDK;
-        const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t]) + 1e-6f);
-        const float ik = 1.f / sqrtf(static_cast<float>(red_s[1][t]) + 1e-6f);
-        q_s[t][i] = (q_s[t][i] * iq) * qscale;
-        const float kn = k_s[t][i] * ik;
-        k_s[t][i] = kn;
-        if (keep) rec_h[t * rec_t + i] = kn;
-    }
-    if (keep && tid < T) rec_h[tid * rec_t + 2 * kDK] = gate_s[tid][0];
-
-    // replay the consumed records of the previous call (same operations as below)
+    // ---- replay the consumed records of the previous call (same operations as the
+    // update below)
     for (int t = 0; t < n_rep; ++t) {
         const float g = rg_s[t];
-        const float delta = col_ok ? rd_s[t][j] : 0.f;
+        const float delta = rd_s[t][jj];
 #pragma unroll
-        for (int r = 0; r < kHRows; ++r) S[r] = __fmaf_rn(rk_s[t][kHRows * c + r], delta, __fmul_rn(S[r], g));
+        for (int r = 0; r < kCRows; ++r) S[r] = __fmaf_rn(rk_s[t][kCRows * c + r], delta, __fmul_rn(S[r], g));
     }
     auto store_state = [&] {
         float4* dp = reinterpret_cast<float4*>(p.S_out + s_off);
 #pragma unroll
-        for (int r = 0; r < kHRows / 4; ++r) dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
+        for (int r = 0; r < kCRows / 4; ++r) dp[r] = make_float4(S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]);
     };
-    if (keep && n_rep > 0 && col_ok) store_state();
-    __syncthreads();
+    if (keep && n_rep > 0) store_state();
 
-    // delta rule, token by token
+    // ---- delta rule, token by token; q and k normalised as read:
+    // q = (q * 1/|q|) * 1/sqrt(dk), k = k * 1/|k| (eps 1e-6 inside the root)
+    const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
+    const bool rec_k = keep && cc == 0 && jj == 0;  // one writer of the per-head k and g records
     for (int t = 0; t < T; ++t) {
+        const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t] + red_s[1][t]) + 1e-6f);
+        const float ik = 1.f / sqrtf(static_cast<float>(red_s[2][t] + red_s[3][t]) + 1e-6f);
         const float g = gate_s[t][0], beta = gate_s[t][1];
-        float kv = 0.f;
+        float kn[kCRows];
 #pragma unroll
-        for (int r = 0; r < kHRows; ++r) {
+        for (int r = 0; r < kCRows; ++r) kn[r] = k_s[t][kCRows * c + r] * ik;
+        if (rec_k) {
+            float4* kp = reinterpret_cast<float4*>(rec_w + t * rec_t + kCRows * c);
+#pragma unroll
+            for (int r = 0; r < kCRows / 4; ++r) kp[r] = make_float4(kn[4 * r], kn[4 * r + 1], kn[4 * r + 2], kn[4 * r + 3]);
+            if (c == 0) rec_w[t * rec_t + 2 * kDK] = g;
+        }
+        float kv4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < kCRows; ++r) {
             S[r] = __fmul_rn(S[r], g);
-            kv = __fmaf_rn(S[r], k_s[t][kHRows * c + r], kv);
+            kv4[r & 3] = __fmaf_rn(S[r], kn[r], kv4[r & 3]);
         }
-        kv = group8_sum(kv);
-        const float delta = ((col_ok ? v_s[t][j] : 0.f) - kv) * beta;
-        float ov = 0.f;
+        const float kv = group8_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
+        const float delta = (v_s[t][jj] - kv) * beta;
+        float ov4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int r = 0; r < kHRows; ++r) {
-            S[r] = __fmaf_rn(k_s[t][kHRows * c + r], delta, S[r]);
-            ov = __fmaf_rn(S[r], q_s[t][kHRows * c + r], ov);
+        for (int r = 0; r < kCRows; ++r) {
+            S[r] = __fmaf_rn(kn[r], delta, S[r]);
+            ov4[r & 3] = __fmaf_rn(S[r], (q_s[t][kCRows * c + r] * iq) * qscale, ov4[r & 3]);
         }
-        ov = group8_sum(ov);
-        if (c == 0 && col_ok) {
-            o_s[t][j] = ov;
+        const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
+        if (c == 0) {
             if (p.o) p.o[static_cast<size_t>(t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
-            if (keep) rec_h[t * rec_t + kDK + j] = delta;
+            if (keep) rec_w[t * rec_t + kDK + j] = delta;
+            if (gn) {
+                o_s[t][jj] = ov;
+                y_s[t][jj] = gam * ov * silu_f(zt[t]);
+            }
         }
     }
-    if (!keep && col_ok) store_state();
-    if (records && tid == 0) a.rec.count[h] = keep ? T : 0;
+    if (!keep) store_state();
+    if (records && cc == 0 && tid == 0) a.rec.count[slot0 * p.nv + h] = keep ? T : 0;
     if (!a.frag) return;
 
-    // gated RMSNorm of the head (wave t reduces token t) and packing
+    // ---- per token: the chunk's sum of o^2 (double; 16-lane rows, then the row
+    // pair) and the fragments of y (thread t*4 + u packs columns 8u .. 8u+7)
     __syncthreads();
-    {
-        const int wave = tid >> 6, lane = tid & 63;
-        if (wave < T) {
-            double ss = 0.0;
-            for (int i = lane; i < dv; i += 64) ss += static_cast<double>(o_s[wave][i]) * o_s[wave][i];
-            ss = wave_sum_d(ss);
-            if (lane == 0) inv_s[wave] = 1.f / sqrtf(static_cast<float>(ss / dv) + 1e-6f);
-        }
+    if (wave * 2 < T) {  // wave w: tokens 2w (lanes 0-31) and 2w + 1 (lanes 32-63)
+        const int t = 2 * wave + (lane >> 5), i = lane & 31;
+        const double v = t < T ? static_cast<double>(o_s[t][i]) * o_s[t][i] : 0.0;
+        const double r = group16_sum_d(v);
+        const double s0 = readlane_d(r, 0) + readlane_d(r, 16), s1 = readlane_d(r, 32) + readlane_d(r, 48);
+        if (lane == 0) a.gss[(static_cast<size_t>(h) * T + t) * 4 + cc] = static_cast<float>(s0);
+        if (lane == 32 && t < T) a.gss[(static_cast<size_t>(h) * T + t) * 4 + cc] = static_cast<float>(s1);
     }
-    __syncthreads();
-    if (gn) {
-#pragma unroll
-        for (int t = 0; t < kMaxT; ++t)
-            if (t < T) o_s[t][j] = gam * (o_s[t][j] * inv_s[t]) * silu_f(zt[t]);
-    }
-    __syncthreads();
-    if (tid < T * (dv / 8)) {
-        const int t = tid / (dv / 8), u = tid % (dv / 8);
+    if (tid < T * (kCW / 8)) {
+        const int t = tid / (kCW / 8), u = tid % (kCW / 8);
         float v[8];
 #pragma unroll
-        for (int e = 0; e < 8; ++e) v[e] = o_s[t][8 * u + e];
-        write_frag8(a.frag, (h * dv) / 8 + u, t, T, v);
+        for (int e = 0; e < 8; ++e) v[e] = y_s[t][8 * u + e];
+        write_frag8(a.frag, (h * dv + cc * kCW) / 8 + u, t, T, v);
     }
 }
 
@@ -503,35 +512,37 @@ __global__ __launch_bounds__(kHT) void gdn_head_kernel(GdnHeadArgs a) {
 
 namespace rl {
 
-bool gdn_head_supported(int dk, int dv, int K) { return dk == kDK && dv <= kHMaxDv && dv % 8 == 0 && K == kConvK; }
+bool gdn_fused_supported(int dk, int dv, int K) { return dk == kDK && dv % kCW == 0 && dv > 0 && K == kConvK; }
 
-void gdn_decode_head(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
-                     const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
-                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R, const GdnRecords* rec,
-                     float* o, const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv,
-                     int K, int v_tiled, hipStream_t s) {
-    RL_REQUIRE(gdn_head_supported(dk, dv, K), RL_ERR_UNSUPPORTED, "gdn_decode_head: dk 128, dv <= 128, conv 4");
-    RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_head: T must be in 1..8");
-    RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode_head: nv must be a multiple of nk");
-    RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && (o || frag), RL_ERR_RANGE,
-               "gdn_decode_head: null pointer");
-    RL_REQUIRE(!frag || (z && gamma), RL_ERR_RANGE, "gdn_decode_head: the gated norm needs z and gamma");
-    RL_REQUIRE(S_out, RL_ERR_RANGE, "gdn_decode_head: null output state");
+void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
+                      const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
+                      const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
+                      const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
+                      int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s) {
+    RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED,
+               "gdn_decode_fused: dk 128, dv a multiple of 32, conv 4");
+    RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: T must be in 1..8");
+    RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode_fused: nv must be a multiple of nk");
+    RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && S_out && (o || frag),
+               RL_ERR_RANGE, "gdn_decode_fused: null pointer");
+    RL_REQUIRE(!frag || (z && gamma && gss && dv == 4 * kCW), RL_ERR_RANGE,
+               "gdn_decode_fused: the gated norm needs z, gamma, gss and dv 128");
     if (cur) {
-        RL_REQUIRE(R > T, RL_ERR_RANGE, "gdn_decode_head: ring needs more slots than tokens");
-        RL_REQUIRE(rec && rec->rec && rec->count && rec->n_cons && S_out == S_in, RL_ERR_RANGE,
-                   "gdn_decode_head: the conv ring needs records and one committed state");
+        RL_REQUIRE(R > T, RL_ERR_RANGE, "gdn_decode_fused: ring needs more slots than tokens");
+        RL_REQUIRE(rec && rec->rec && rec->count && rec->n_cons && rec->max_t >= T && S_out == S_in, RL_ERR_RANGE,
+                   "gdn_decode_fused: the conv ring needs records and one committed state");
     } else {
-        RL_REQUIRE(conv_out && conv_out != conv_in, RL_ERR_RANGE, "gdn_decode_head: bad output conv window");
+        RL_REQUIRE(!rec && conv_out && conv_out != conv_in, RL_ERR_RANGE, "gdn_decode_fused: bad conv output");
     }
-    GdnHeadArgs p{{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, 0, R,
-                   o, T, nk, nv, dv, K, v_tiled},
-                  z,
-                  gamma,
-                  static_cast<i32x4*>(frag),
-                  rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0}};
-    hipLaunchKernelGGL(gdn_head_kernel, dim3(nv), dim3(kHT), 0, s, p);
-    check_launch("gdn_head_kernel");
+    GdnFusedArgs p{{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, 0, R,
+                    o, T, nk, nv, dv, K, v_tiled},
+                   z,
+                   gamma,
+                   static_cast<i32x4*>(frag),
+                   gss,
+                   rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0, 0}};
+    hipLaunchKernelGGL(gdn_fused_kernel, dim3(nv * (dv / kCW)), dim3(kCT), 0, s, p);
+    check_launch("gdn_fused_kernel");
 }
 
 void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log, const float* dt_bias,
@@ -566,10 +577,10 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k,
                       int v_tiled, void* stream) {
     return guard([&] {
-        if (rl::gdn_head_supported(dk, dv, conv_k))
-            rl::gdn_decode_head(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0,
-                                0, nullptr, o, nullptr, nullptr, nullptr, T, nk, nv, dk, dv, conv_k, v_tiled,
-                                S(stream));
+        if (rl::gdn_fused_supported(dk, dv, conv_k))
+            rl::gdn_decode_fused(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr,
+                                 0, 0, nullptr, o, nullptr, nullptr, nullptr, nullptr, T, nk, nv, dk, dv, conv_k,
+                                 v_tiled, S(stream));
         else
             rl::gdn_decode(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0, 0,
                            0, o, T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));

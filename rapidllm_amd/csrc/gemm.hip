@@ -22,8 +22,9 @@
 // at tile offsets 16l and 1024+16l, so every 16-byte wave load is one contiguous
 // 1 KiB stream.  Tiles of one row-tile are contiguous along kb.
 //
-// Work split: a workgroup = KSPLIT waves over RT row-tiles; wave w walks a
-// contiguous 1/KSPLIT of the column blocks, partial C tiles are summed through LDS
+// Work split: a workgroup = KSPLIT waves over RT row-tiles; wave w walks every
+// KSPLIT-th column block (depth 1) or a contiguous 1/KSPLIT of them (deeper
+// pipelines), partial C tiles are summed through LDS
 // in a fixed order (deterministic), then the epilogue stores or accumulates Y.
 #include "internal.h"
 
@@ -58,7 +59,10 @@ enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4 };
 // Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
 // weights in flight while one is computed).
-template <int RT, int KSPLIT, int D, bool kFp8>
+// kKs: per-column-block input scale (NormIO::kss, the folded gated RMSNorm); depth 1
+// and at most kKsMaxIt column blocks per wave.
+constexpr int kKsMaxIt = 8;
+template <int RT, int KSPLIT, int D, bool kFp8, bool kKs = false>
 __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
@@ -79,7 +83,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     const int rt0 = (blockIdx.x / S) * RT;
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
 
-    // contiguous run of column blocks for this workgroup's slice, then this wave
+    // column blocks of this workgroup's slice; for depth > 1 a contiguous run per wave
     const int per_s = (n_kb + S - 1) / S;
     const int s_begin = min(n_kb, slice * per_s), s_end = min(n_kb, s_begin + per_s);
     const int per = (s_end - s_begin + KSPLIT - 1) / KSPLIT;
@@ -139,6 +143,18 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     i32x4 wbuf[D][RT][NW];
     i32x4 bbuf[D][4];
     float sbuf[D][RT];
+    // kKs: the four partial sums of squares of this wave's blocks for this lane's
+    // token, all loaded before the weight stream (blocks w + i*KSPLIT, i < kKsMaxIt)
+    const int ktok = bcol < T ? bcol : bcol - T;
+    const float kss_inv_n = kKs ? 1.f / static_cast<float>(io.kss_n) : 0.f;
+    float4 kq[kKs ? kKsMaxIt : 1];
+    if constexpr (kKs) {
+#pragma unroll
+        for (int i = 0; i < kKsMaxIt; ++i) {
+            const int kb = min(s_begin + wave + i * KSPLIT, n_kb - 1);
+            kq[i] = reinterpret_cast<const float4*>(io.kss)[static_cast<size_t>(kb) * T + ktok];
+        }
+    }
     // kb >= kb_end: a pipeline slot past the wave's range.  Its loads still issue (so
     // the load count is the same on every path) but read the small, cache-resident
     // activation fragments instead of weights; the values are never used.
@@ -162,7 +178,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 #pragma unroll
         for (int i = 0; i < 4; ++i) bbuf[d][i] = fbase[kb * fstride + i * 4 * NC];
     };
-    auto compute = [&](int d, int kb) {
+    auto compute = [&](int d, int kb, float ks = 1.f) {
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -181,8 +197,12 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                 }
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
             }
-            if constexpr (kFp8)
+            if constexpr (kFp8 && kKs)
+                tot[r] += (sbuf[d][r] * ks) * acc;
+            else if constexpr (kFp8)
                 tot[r] += sbuf[d][r] * acc;
+            else if constexpr (kKs)
+                tot[r] += ks * acc;
             else
                 tot[r] += acc;
         }
@@ -190,10 +210,23 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 
     if constexpr (D == 1) {
         // depth 1: load a column block, compute it (the compiler schedules the
-        // loads; measured as fast as any explicit pipeline for the FP8 launches)
-        for (int kb = kb_begin; kb < kb_end; ++kb) {
-            load(0, kb, true);
-            compute(0, kb);
+        // loads; measured as fast as any explicit pipeline for the FP8 launches).
+        // Wave w takes blocks w, w + KSPLIT, ...: at any moment the workgroup reads
+        // KSPLIT adjacent tiles per row-tile (1-3% faster than contiguous runs)
+        if constexpr (kKs) {
+#pragma unroll
+            for (int i = 0; i < kKsMaxIt; ++i) {
+                const int kb = s_begin + wave + i * KSPLIT;
+                if (kb >= s_end) break;
+                load(0, kb, true);
+                const float4 q = kq[i];
+                compute(0, kb, __builtin_amdgcn_rsqf(((q.x + q.y) + (q.z + q.w)) * kss_inv_n + io.kss_eps));
+            }
+        } else {
+            for (int kb = s_begin + wave; kb < s_end; kb += KSPLIT) {
+                load(0, kb, true);
+                compute(0, kb);
+            }
         }
     } else if (kb_begin < kb_end) {
         // software pipeline, D stages
@@ -420,11 +453,11 @@ struct GemmCfg {
 };
 static GemmCfg g_force{0, 0, 0};
 
-template <bool kFp8, int RT, int KS, int D>
+template <bool kFp8, int RT, int KS, int D, bool kKs = false>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                      int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
     const int groups = (m_tiles_of(m) + RT - 1) / RT;
-    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8>), dim3(groups * S), dim3(64 * KS), 0, s,
+    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8, kKs>), dim3(groups * S), dim3(64 * KS), 0, s,
                        static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
                        epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out), io);
 }
@@ -464,6 +497,16 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     if (epilogue == kAddNorm && !g_force.rt) c = GemmCfg{2, 8, kFp8 ? 1 : 2};
     if (io.ss_in || epilogue == kAddNorm)
         RL_REQUIRE(c.ks >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
+    if (io.kss) {
+        // folded gated norm (out_proj): the residual configuration only
+        RL_REQUIRE(!io.ss_in && io.kss_n > 0 && S == 1, RL_ERR_RANGE, "gemm: bad block input scale");
+        RL_REQUIRE(n_kb <= kKsMaxIt * 8, RL_ERR_UNSUPPORTED, "gemm: block input scale needs n <= 8192");
+        RL_REQUIRE(!g_force.rt, RL_ERR_UNSUPPORTED, "gemm: block input scale uses the residual work split");
+        launch_gemm_cfg<kFp8, 2, 8, 1, true>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out,
+                                             io, s);
+        check_launch("gemm_frag_kernel");
+        return;
+    }
 #define RL_GEMM_CASE(R, K, DD)                                                            \
     if (c.rt == R && c.ks == K && c.d == DD) {                                            \
         launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); \

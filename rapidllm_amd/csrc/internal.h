@@ -21,6 +21,13 @@ struct NormIO {
     float eps = 0.f;
     const float* gamma_out = nullptr;
     float* ss_out = nullptr;
+    // Gated RMSNorm folded into the consuming GEMM, one norm group per 128-column
+    // block: kss[kb][t][4] holds four partial sums of squares of block kb's
+    // un-normalised inputs for token t, and the block's products are scaled by
+    // 1/sqrt(sum / kss_n + kss_eps).
+    const float* kss = nullptr;
+    int kss_n = 0;
+    float kss_eps = 0.f;
 };
 
 // gemm.hip
@@ -62,33 +69,40 @@ void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, con
                 const int* cur, size_t conv_slot, size_t s_slot, int R, float* o, int T, int nk, int nv, int dk,
                 int dv, int K, int v_tiled, hipStream_t s);
 
-// One workgroup per v-head (dk 128, dv <= 128) with the gated RMSNorm of the head
-// (gamma [dv], gate z at z[t*ld_in + h*dv + j]) and the packing into fragments fused
-// (frag may be null; o may be null when frag is given).
-bool gdn_head_supported(int dk, int dv, int K);
-// Speculative bookkeeping of the one-head-per-workgroup DeltaNet kernel.  The state
-// S is kept once, committed up to the last consumed token.  A call that may be
-// partly rejected (keep = 1) stores, per head and token, the normalised k, the
-// update delta = (v - S^T k) * beta and the decay g (kGdnRecFloats floats), and
-// leaves S at the committed point; the next call first replays the first
-// min(*n_cons, count[h]) records onto S (the same float operations the update
+// Fused DeltaNet decode (dk 128, dv a multiple of 32, conv 4) with the gated
+// RMSNorm's elementwise part and the packing into out_proj fragments (gamma [dv],
+// gate z at z[t*ld_in + h*dv + j]).
+// Speculative bookkeeping of the fused DeltaNet kernel.  The state S is kept once,
+// committed up to the last consumed token.  A call that may be partly rejected
+// (keep = 1) stores, per head and token, the normalised k, the update
+// delta = (v - S^T k) * beta and the decay g (kGdnRecFloats floats), and leaves S
+// at the committed point; the next call first replays the first
+// min(*n_cons, count) records onto S (the same float operations the update
 // performs, so the result is bit-identical to having kept S after that token).
+// Records live in R banks, one per conv-ring slot: a call writes bank *cur and
+// reads bank (*cur - *n_cons) mod R, the previous call's (distinct, as
+// 1 <= n_cons <= T < R), so workgroups of one call never read what others write.
 constexpr int kGdnRecFloats = 264;  // k[128] | delta[dv <= 128] | g
 struct GdnRecords {
-    float* rec;          // [max_t][nv][kGdnRecFloats]
-    int* count;          // [nv]: tokens recorded by the previous call
+    float* rec;          // [R][max_t][nv][kGdnRecFloats]
+    int* count;          // [R][nv]: tokens recorded per head
     const int* n_cons;   // tokens the previous call consumed
+    int max_t;           // token capacity of a bank
     int keep;            // record this call's tokens instead of committing them
 };
-// conv window: a ring of R slots when cur != nullptr (slot *cur read, slot
-// (*cur + 1 + t) % R written after token t), else conv_in -> conv_out.
-// S: S_in -> S_out (may alias); with cur != nullptr, rec must be given and
-// S_out == S_in is the committed state.
-void gdn_decode_head(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
-                     const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
-                     const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R, const GdnRecords* rec,
-                     float* o, const float* z, const float* gamma, void* frag, int T, int nk, int nv, int dk, int dv,
-                     int K, int v_tiled, hipStream_t s);
+// Workgroup = (v-head, 32 value columns).  conv window: a ring of R slots when
+// cur != nullptr (slot *cur read, slot (*cur + 1 + t) % R written after token t),
+// else conv_in -> conv_out.  S: S_in -> S_out (may alias); with cur, rec must be
+// given and S_out == S_in is the committed state.  Outputs: o [T][nv*dv] (may be
+// null) and/or, with frag, the out_proj input fragments of
+// y = gamma * o * silu(z) with the per-head norm left to the GEMM: gss[h][t][4]
+// receives the four 32-column partial sums of o^2 (dv must be 128 then).
+bool gdn_fused_supported(int dk, int dv, int K);
+void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
+                      const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
+                      const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
+                      const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
+                      int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s);
 
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);

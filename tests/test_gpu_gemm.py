@@ -110,8 +110,8 @@ def _time_gemm(lin, X, epi, split=4, frag_out=None):
     yd.zero()
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
-    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, None, None, m, n, T, epi, split, 1,
-         None, C.byref(ms))
+    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, None, None, None, m, n, T, epi,
+         split, 1, None, C.byref(ms))
     return yd.numpy(np.float32, (rows,))
 
 
@@ -167,10 +167,13 @@ def _unpack_frag(raw, n, T):
     return val.transpose(3, 0, 2, 1, 4).reshape(T, n)
 
 
-@pytest.mark.parametrize("T", [1, 4])
-def test_gemm_fp8_add_norm_epilogue(gpu, orc, T):
+@pytest.mark.parametrize("T,block_scale", [(1, False), (4, False), (1, True), (4, True)])
+def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
     """Residual GEMM fused with the next RMSNorm's data: x += W.a in place,
-    fragments of x * (1 + gamma) for the next linear, and sum of x^2 per 32 rows."""
+    fragments of x * (1 + gamma) for the next linear, and sum of x^2 per 32 rows.
+    block_scale: the input's 128-column blocks are scaled per token by
+    1/sqrt(sum/128 + 1e-6) of four given partial sums (the DeltaNet out_proj's
+    folded gated RMSNorm)."""
     import ctypes as C
 
     from rapidllm_amd.hip import DeviceBuffer, call
@@ -189,12 +192,19 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T):
     fo = ops.act_frag_buffer(m, T)
     gd = DeviceBuffer.from_numpy(gamma)
     ssd = DeviceBuffer(4 * T * (m // 32))
+    Xin = X
+    bsd = None
+    if block_scale:
+        bsum = (r.random((n // 128, T, 4)) * 64 + 1).astype(np.float32)
+        bsd = DeviceBuffer.from_numpy(bsum)
+        sc = 1.0 / np.sqrt(bsum.astype(np.float64).sum(2) / 128 + 1e-6)  # [kb][t]
+        Xin = (X.astype(np.float64) * np.repeat(sc.T, 128, axis=1)).astype(np.float32)
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
-    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr, gd.ptr, ssd.ptr, m, n, T, 4, 1, 1,
-         None, C.byref(ms))
+    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr, gd.ptr, ssd.ptr,
+         bsd.ptr if bsd else None, m, n, T, 4, 1, 1, None, C.byref(ms))
     x = yd.numpy(np.float32, (T, m)).astype(np.float64)
-    want = x0.astype(np.float64) + orc.gemm_fp8(W, s, X)
+    want = x0.astype(np.float64) + orc.gemm_fp8(W, s, Xin)
     for t in range(T):
         assert rel_l2(x[t], want[t]) <= REL_L2
     ss = ssd.numpy(np.float32, (m // 32, T)).astype(np.float64)
