@@ -166,7 +166,7 @@ int rl_hip_embed_rows(const void* table, int kind, const int* tokens_dev, float*
  * and V are stored as fp16 (round to nearest even) and it attends to positions
  * 0 .. *pos_dev + t.  Caches (n_kv * ctx * hd fp16 each, ctx a multiple of 256,
  * zero-filled at allocation) in MFMA fragment order, per kv head:
- *   k_cache element (pos, d): [pos/16][d/32][(d/8)%4][pos%16][d%8]
+ *   k_cache element (pos, d): [pos/256][d/32][(pos/16)%16][(d/8)%4][pos%16][d%8]
  *   vt_cache element (pos, d): [pos/32][d/16][(pos/8)%4][d%16][pos%8].  head_dim 256,
  * (n_q/n_kv)*T <= 32.  Outputs o * sigmoid(gate): fp32 `out` [T][n_q*hd] and/or
  * o_proj fragments `frag`.  *pos_dev is not modified. */

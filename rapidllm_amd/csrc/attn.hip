@@ -63,11 +63,14 @@ struct AttnArgs {
 __host__ __device__ inline int pair_tiles(int G, int T) { return (G * T + 15) / 16; }
 
 // Cache layouts (per kv head, ctx * 256 fp16), in MFMA fragment order so that every
-// wave load is one contiguous 1 KiB run (lane l reads 16 B at 16 l):
-//   K: [pos/16][d/32][(d/8)%4][pos%16][d%8]  -- A operand of S^T = K . Q^T
-//   V: [pos/32][d/16][(pos/8)%4][d%16][pos%8] -- A operand of O^T = V^T . P^T
+// wave load is one contiguous 1 KiB run (lane l reads 16 B at 16 l), and the 4 waves
+// of a chunk workgroup read adjacent runs at every step (one 16 KiB stretch):
+//   K: [pos/256][d/32][(pos/16)%16][(d/8)%4][pos%16][d%8] -- A operand of S^T = K . Q^T
+//   V: [pos/32][d/16][(pos/8)%4][d%16][pos%8]              -- A operand of O^T = V^T . P^T
 __host__ __device__ inline size_t k_off(int pos, int d) {
-    return (((static_cast<size_t>(pos >> 4) * 8 + (d >> 5)) * 4 + ((d >> 3) & 3)) * 16 + (pos & 15)) * 8 + (d & 7);
+    return ((((static_cast<size_t>(pos >> 8) * 8 + (d >> 5)) * 16 + ((pos >> 4) & 15)) * 4 + ((d >> 3) & 3)) * 16 +
+            (pos & 15)) * 8 +
+           (d & 7);
 }
 __host__ __device__ inline size_t v_off(int pos, int d) {
     return (((static_cast<size_t>(pos >> 5) * 16 + (d >> 4)) * 4 + ((pos >> 3) & 3)) * 16 + (d & 15)) * 8 + (pos & 7);
@@ -177,9 +180,9 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
         for (int ct = 0; ct < 2 * PT; ++ct) bq[ct].i = qbase[((s * 4 + g) * (2 * PT) + ct) * 16 + col];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
-            const int ptile = (c0 + 64 * wave + 16 * pt) >> 4;
+            const int ptile = 4 * wave + pt;  // 16-position tile within the chunk
             H8 a;
-            a.i = reinterpret_cast<const i32x4*>(kbase + (static_cast<size_t>(ptile) * 8 + s) * 512)[lane];
+            a.i = reinterpret_cast<const i32x4*>(kbase + ((static_cast<size_t>(chunk) * 8 + s) * 16 + ptile) * 512)[lane];
 #pragma unroll
             for (int q = 0; q < PT; ++q) {
                 acc[pt][NA * q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bq[2 * q].v, acc[pt][NA * q], 0, 0, 0);
@@ -188,6 +191,19 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
             }
         }
     }
+
+    // ---- V of the chunk's first 64 positions requested now, so the loads are in flight
+    // across the softmax (the V loop below keeps two steps ahead)
+    const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;  // fragment-ordered V
+    H8 va[3][4];
+    auto vload = [&](int u, H8* dst) {
+        const int grp = (c0 >> 5) + u;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt)
+            dst[dt].i = reinterpret_cast<const i32x4*>(vbase + (static_cast<size_t>(grp) * 16 + 4 * wave + dt) * 512)[lane];
+    };
+    vload(0, va[0]);
+    vload(1, va[1]);
 
     // ---- masked scores, chunk max (lane: query row `col` of pair tile, 4 rows each)
     float sc[4][PT][4];
@@ -251,21 +267,17 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     for (int a = 0; a < 4; ++a)
 #pragma unroll
         for (int q = 0; q < PT; ++q) o[a][q] = f32x4{0.f, 0.f, 0.f, 0.f};
-    const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;  // fragment-ordered V
-#pragma unroll ATTN_UNROLL
+#pragma unroll
     for (int u = 0; u < 8; ++u) {
+        if (u + 2 < 8) vload(u + 2, va[(u + 2) % 3]);
         H8 bp[PT];
 #pragma unroll
         for (int q = 0; q < PT; ++q) bp[q].i = *reinterpret_cast<const i32x4*>(&P_lds[u][q][col][8 * g]);
 #pragma unroll
-        for (int dt = 0; dt < 4; ++dt) {
-            const int grp = (c0 >> 5) + u, dtile = 4 * wave + dt;
-            H8 a;
-            a.i = reinterpret_cast<const i32x4*>(vbase + (static_cast<size_t>(grp) * 16 + dtile) * 512)[lane];
+        for (int dt = 0; dt < 4; ++dt)
 #pragma unroll
             for (int q = 0; q < PT; ++q)
-                o[dt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.v, bp[q].v, o[dt][q], 0, 0, 0);
-        }
+                o[dt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[u % 3][dt].v, bp[q].v, o[dt][q], 0, 0, 0);
     }
 
     // ---- partials: O^T lane (pair col, g) holds d = 64*wave + 16*dt + 4g + v

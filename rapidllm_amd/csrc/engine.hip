@@ -413,6 +413,18 @@ class Engine {
         const int nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim;
         int I = c_.intermediate;
 
+        // KV caches first, as one block
+        {
+            int n_attn = 0;
+            for (int i = 0; i < c_.n_layers; ++i) n_attn += c_.layer_kind[i] == RL_LAYER_ATTN;
+            const size_t kv = static_cast<size_t>(nkv) * ctx_ * hd;
+            uint16_t* blk = mem_.get_n<uint16_t>(2 * kv * n_attn);
+            for (int l = 0; l < n_attn; ++l) {
+                kc_.push_back(blk + 2 * l * kv);
+                vt_.push_back(blk + (2 * l + 1) * kv);
+            }
+        }
+
         // embedding / head / final norm
         if (synthetic_) {
             embed_kind_ = RL_Q_BF16;
@@ -527,11 +539,7 @@ class Engine {
         s_slot_ = static_cast<size_t>(nv) * dv * dk;
         conv_slot_ = static_cast<size_t>(conv_dim) * c_.conv_k;
         for (int l = 0; l < nd; ++l) conv_.push_back(mem_.get_n<float>(conv_slot_ * R_));
-        const size_t kv = static_cast<size_t>(nkv) * ctx_ * hd;
-        for (int l = 0; l < na; ++l) {
-            kc_.push_back(mem_.get_n<uint16_t>(kv));
-            vt_.push_back(mem_.get_n<uint16_t>(kv));
-        }
+        RL_REQUIRE(static_cast<int>(kc_.size()) == na, RL_ERR_INTERNAL, "engine: attention layer count");
 
         // activations
         const int T = tmax_;

@@ -236,9 +236,10 @@ def gdn_decode(qkv, a, b, A_log, dt_bias, conv_w, conv_state, S, nk, nv, v_tiled
 
 def kv_layout_k(K):
     """[n_kv][ctx][256] fp16 -> the device K layout, per kv head
-    [pos/16][d/32][(d/8)%4][pos%16][d%8]."""
+    [pos/256][d/32][(pos/16)%16][(d/8)%4][pos%16][d%8]."""
     n_kv, ctx, hd = K.shape
-    return np.ascontiguousarray(K.reshape(n_kv, ctx // 16, 16, hd // 32, 4, 8).transpose(0, 1, 3, 4, 2, 5))
+    return np.ascontiguousarray(
+        K.reshape(n_kv, ctx // 256, 16, 16, hd // 32, 4, 8).transpose(0, 1, 4, 2, 5, 3, 6))
 
 
 def kv_layout_v(V):
