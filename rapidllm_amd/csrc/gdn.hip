@@ -7,11 +7,14 @@
 // delta_recurrent_step (ops.cpp:495-534).  Output o is the raw recurrent output;
 // the gated RMSNorm is fused into the packing kernel of the next linear (norms.hip).
 //
-// Work split: one workgroup per (v-head h, 16 value columns).  Thread (c, jj)
-// keeps S[h][8c .. 8c+7][16*cg + jj] in registers; column j of S evolves
-// independently given k, q, g, beta and v_j, so the only cross-thread work per
-// token is two 16-lane sums (k^T S and q^T S) done with lane shuffles.
-// The state is read once and written once for all T tokens.
+// Two kernels.  gdn_decode_kernel (any dv multiple of 32, state ring for the
+// unfused engine path): one workgroup per (v-head h, 16 value columns), thread
+// (c, jj) keeps S[h][8c .. 8c+7][16*cg + jj] in registers.  gdn_fused_kernel (below;
+// dk 128, dv multiple of 32): one workgroup per (v-head, 32 value columns), the gated
+// norm's elementwise part and the out_proj packing fused, speculative records
+// instead of a state ring.  Column j of S evolves independently given k, q, g, beta
+// and v_j, so the only cross-thread work per token is two lane-group sums
+// (k^T S and q^T S).  The state is read once and written once for all T tokens.
 //
 // State layout in HBM (transposed per head): St[h][j][i] = S[h][i][j], so each
 // thread's 8 values are 32 contiguous bytes and a wave reads 2 KiB contiguously.
