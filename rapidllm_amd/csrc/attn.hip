@@ -145,7 +145,9 @@ union H8 {
 
 template <int PT>
 __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
-    const int chunk = blockIdx.x, kv = blockIdx.y;
+    // chunk-major dispatch order: the chunks past the current position (early exit)
+    // come last, so the active workgroups spread evenly over the CUs
+    const int chunk = blockIdx.x / p.nkv, kv = blockIdx.x % p.nkv;
     const int p0 = *p.pos;
     const int L = p0 + p.T;  // keys 0 .. L-1 exist after this step's writes
     const int c0 = chunk * kChunk;
@@ -180,7 +182,9 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
         for (int ct = 0; ct < 2 * PT; ++ct) bq[ct].i = qbase[((s * 4 + g) * (2 * PT) + ct) * 16 + col];
 #pragma unroll
         for (int pt = 0; pt < 4; ++pt) {
-            const int ptile = 4 * wave + pt;  // 16-position tile within the chunk
+            // tiles past the last key (masked) re-read the chunk's first tile, which
+            // is cached: the partial last chunk costs about what it holds in HBM reads
+            const int ptile = c0 + 16 * (4 * wave + pt) < L ? 4 * wave + pt : 0;
             H8 a;
             a.i = reinterpret_cast<const i32x4*>(kbase + ((static_cast<size_t>(chunk) * 8 + s) * 16 + ptile) * 512)[lane];
 #pragma unroll
@@ -197,7 +201,8 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;  // fragment-ordered V
     H8 va[3][4];
     auto vload = [&](int u, H8* dst) {
-        const int grp = (c0 >> 5) + u;
+        // positions past the last key have P = 0: their group re-reads the first one
+        const int grp = 32 * ((c0 >> 5) + u) < L ? (c0 >> 5) + u : (c0 >> 5);
 #pragma unroll
         for (int dt = 0; dt < 4; ++dt)
             dst[dt].i = reinterpret_cast<const i32x4*>(vbase + (static_cast<size_t>(grp) * 16 + 4 * wave + dt) * 512)[lane];
@@ -423,9 +428,9 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     hipLaunchKernelGGL(qk_prep_kernel, dim3(nq + 2 * nkv, T), dim3(64), 0, s, p);
     check_launch("qk_prep_kernel");
     if (pair_tiles(G, T) == 1)
-        hipLaunchKernelGGL(attn_part_kernel<1>, dim3(chunks, nkv), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_part_kernel<1>, dim3(chunks * nkv), dim3(256), 0, s, p);
     else
-        hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks, nkv), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks * nkv), dim3(256), 0, s, p);
     check_launch("attn_part_kernel");
     hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv, kHD / 64), dim3(256), 0, s, p);
     check_launch("attn_comb_kernel");
