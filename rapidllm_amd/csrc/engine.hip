@@ -355,6 +355,10 @@ class Engine {
     std::vector<float*> rec_;   // DeltaNet replay records per layer (head kernel)
     std::vector<int*> rec_n_;
     float* gss_ = nullptr;      // per-head partial sums of o^2 for the folded gated norm
+    // in_proj rows past two workgroups per CU (the a/b block) as K-slice partials
+    static constexpr int kAbSlices = 8;
+    float* abpart_ = nullptr;
+    int ab_tile0_ = 0, ab_rows_ = 0;
     std::vector<uint16_t*> kc_, vt_;
     // activations / workspaces
     int* scal_ = nullptr;
@@ -579,6 +583,22 @@ class Engine {
             }
         }
         gss_ = mem_.get_n<float>(static_cast<size_t>(nv) * tmax_ * 4);
+        // in_proj = [qkv; z; a; b]: when its row-tile pairs overflow two workgroups per
+        // CU and the overflow is the a/b block, the a/b rows are computed as K-slices
+        if (gdn_fused_norm_ && nd > 0) {
+            const Layer* d0 = nullptr;
+            for (const Layer& Ly : L_)
+                if (Ly.kind == RL_LAYER_DELTA) d0 = &Ly;
+            const int m_tiles = d0->in_parts[0].m / 16, n_kb = (H + 127) / 128;
+            const int tile0 = d0->off_a / 16;
+            if (d0->in_parts[0].kind == RL_Q_FP8_E4M3_B128 && m_tiles / 2 > 2 * device_cus() && d0->off_a % 32 == 0 &&
+                tile0 / 2 <= 2 * device_cus() && (m_tiles - tile0) * kAbSlices <= tile0 / 2 &&
+                (n_kb + kAbSlices - 1) / kAbSlices <= 8 && d0->in_width == m_tiles * 16) {
+                ab_tile0_ = tile0;
+                ab_rows_ = (m_tiles - tile0) * 16;
+                abpart_ = mem_.get_n<float>(static_cast<size_t>(kAbSlices) * tmax_ * ab_rows_);
+            }
+        }
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
@@ -896,17 +916,27 @@ class Engine {
             out.gamma_out = Ly.ffn_norm;
             out.ss_out = ss_;
             if (Ly.kind == RL_LAYER_DELTA) {
-                gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, T, kEpiStore, nullptr, io_in);
+                NormIO in_ab = io_in ? *io_in : NormIO{};
+                if (abpart_) {
+                    in_ab.xpart = abpart_;
+                    in_ab.x_tile0 = ab_tile0_;
+                    in_ab.x_slices = kAbSlices;
+                    in_ab.x_rows = ab_rows_;
+                }
+                gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, T, kEpiStore, nullptr,
+                        abpart_ ? &in_ab : io_in);
                 if (gdn_fused_norm_) {
                     // recurrent update + gated RMSNorm's elementwise part + out_proj
                     // packing in one kernel; out_proj applies the per-head 1/rms.  A step
                     // that consumes all its tokens commits S directly.
                     const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, tmax_,
                                          T > 1 && !force_all};
-                    gdn_decode_fused(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
-                                     Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot,
-                                     conv_slot_, R_, &rec, nullptr, ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, T, nk,
-                                     nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                    const float* a_in = abpart_ ? abpart_ : ybuf_ + Ly.off_a;
+                    const float* b_in = abpart_ ? abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b;
+                    gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, conv_[Ly.dslot],
+                                     nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot, conv_slot_, R_, &rec, nullptr,
+                                     ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, T, nk, nv, c_.k_dim, dv, c_.conv_k,
+                                     c_.v_tiled, st_, abpart_ ? kAbSlices : 1, ab_rows_);
                     out.kss = gss_;
                     out.kss_n = dv;
                     out.kss_eps = 1e-6f;

@@ -60,6 +60,9 @@ struct GdnArgs {
     int R;
     float* o;             // [T][nv*dv]
     int T, nk, nv, dv, K, v_tiled;
+    // fused kernel: a and b are the sums of ab_slices partials,
+    // a[(s * T + t) * ab_ld + h] (1 slice with ab_ld = ld_in: the plain layout)
+    int ab_slices = 1, ab_ld = 0;
 };
 
 __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
@@ -251,6 +254,7 @@ constexpr int kCChunks = 8;              // threads per column
 constexpr int kCRows = kDK / kCChunks;   // 16 rows per thread
 constexpr int kCT = kCW * kCChunks;      // 256 threads
 constexpr int kCWaves = kCT / 64;
+constexpr int kMaxAbSlices = 8;
 
 struct GdnFusedArgs {
     GdnArgs g;
@@ -324,10 +328,14 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
             xin1[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan1] : 0.f;
         }
     }
-    float gin_a = 0.f, gin_b = 0.f, gin_A = 0.f, gin_dt = 0.f;
-    if (tid < T) {
-        gin_a = p.a[static_cast<size_t>(tid) * p.ld_in + h];
-        gin_b = p.b[static_cast<size_t>(tid) * p.ld_in + h];
+    // gate inputs: lane e = 16t + 8(b) + s holds slice s of a (or b) of token t; the 8
+    // slices are summed by a DPP 8-lane reduction (fixed order)
+    float gin = 0.f, gin_A = 0.f, gin_dt = 0.f;
+    const bool gate_lane = tid < 16 * T;
+    if (gate_lane) {
+        const int t = tid >> 4, sl = tid & 7;
+        const float* src = (tid & 8) ? p.b : p.a;
+        if (sl < p.ab_slices) gin = src[(static_cast<size_t>(sl) * T + t) * p.ab_ld + h];
         gin_A = p.A_log[h];
         gin_dt = p.dt_bias[h];
     }
@@ -420,11 +428,16 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         const double ws = wave_sum_d(sq[t]);
         if (lane == 0) red_s[wave][t] = ws;
     }
-    if (tid < T) {
-        const float beta = sigmoid_f(gin_b);
-        const float g_log = -expf(gin_A) * softplus_f(gin_a + gin_dt);
-        gate_s[tid][0] = expf(g_log);
-        gate_s[tid][1] = beta;
+    if (wave * 4 < T) {  // waves holding gate lanes (all lanes take part in the DPP sums)
+        const float sum = group8_sum(gin);
+        const float bsum = __shfl_down(sum, 8, 64);  // b of the same token, 8 lanes up
+        if (gate_lane && (tid & 15) == 0) {
+            const int t = tid >> 4;
+            const float beta = sigmoid_f(bsum);
+            const float g_log = -expf(gin_A) * softplus_f(sum + gin_dt);
+            gate_s[t][0] = expf(g_log);
+            gate_s[t][1] = beta;
+        }
     }
 #pragma unroll
     for (int q = 0; q < kMaxT / 2; ++q) {
@@ -526,7 +539,8 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
-                      int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s) {
+                      int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices,
+                      int ab_ld) {
     RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED,
                "gdn_decode_fused: dk 128, dv a multiple of 32, conv 4");
     RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: T must be in 1..8");
@@ -542,8 +556,9 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
     } else {
         RL_REQUIRE(!rec && conv_out && conv_out != conv_in, RL_ERR_RANGE, "gdn_decode_fused: bad conv output");
     }
+    RL_REQUIRE(ab_slices >= 1 && ab_slices <= kMaxAbSlices, RL_ERR_RANGE, "gdn_decode_fused: 1..8 a/b slices");
     GdnFusedArgs p{{qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, cur, conv_slot, 0, R,
-                    o, T, nk, nv, dv, K, v_tiled},
+                    o, T, nk, nv, dv, K, v_tiled, ab_slices, ab_slices > 1 ? ab_ld : ld_in},
                    z,
                    gamma,
                    static_cast<i32x4*>(frag),

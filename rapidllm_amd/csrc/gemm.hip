@@ -348,6 +348,33 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
             }
         }
     }
+
+    // overflow row tiles (NormIO::xpart): workgroup u < (tiles) * x_slices computes
+    // K-slice u % x_slices of tile x_tile0 + u / x_slices, one column block per wave
+    if (io.xpart && static_cast<int>(blockIdx.x) < (io.x_rows / kTileRows) * io.x_slices) {
+        const int u = blockIdx.x;
+        const int xt = io.x_tile0 + u / io.x_slices, sl = u % io.x_slices;
+        const int per = (n_kb + io.x_slices - 1) / io.x_slices;
+        const int kb = sl * per + wave;
+#pragma unroll
+        for (int r = 0; r < RT; ++r) {
+            wbase[r] = W + static_cast<size_t>(xt) * n_kb * kTileBytes;
+            sbase[r] = kFp8 ? tscale + static_cast<size_t>(xt) * n_kb : nullptr;
+            tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+        }
+        if (wave < per && kb < n_kb) {
+            load(0, kb, true);
+            compute(0, kb);
+        }
+        __syncthreads();  // the row epilogue above has read red
+        red[wave][0][lane] = tot[0];
+        __syncthreads();
+        if (static_cast<int>(threadIdx.x) < kTileRows * T) {
+            const int row = threadIdx.x % kTileRows, t = threadIdx.x / kTileRows;
+            io.xpart[(static_cast<size_t>(sl) * T + t) * io.x_rows + (xt - io.x_tile0) * kTileRows + row] =
+                final_value(0, t, row);
+        }
+    }
 }
 
 // X fp32 [T][n] -> fragments [kb][i][g][c][8 bf16]; c < T: hi of token c, else mid of
@@ -507,6 +534,19 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
         check_launch("gemm_frag_kernel");
         return;
     }
+    if (io.xpart) {
+        // the rows from x_tile0 on as K-slices run by the first workgroups
+        RL_REQUIRE(epilogue == kStore && S == 1 && !g_force.rt && !io.kss, RL_ERR_RANGE,
+                   "gemm: overflow slices need a plain store launch");
+        RL_REQUIRE(io.x_tile0 > 0 && io.x_tile0 % 2 == 0 && io.x_tile0 < m_tiles && io.x_slices >= 1 &&
+                       io.x_rows == (m_tiles - io.x_tile0) * kTileRows && (n_kb + io.x_slices - 1) / io.x_slices <= 8 &&
+                       (m_tiles - io.x_tile0) * io.x_slices <= io.x_tile0 / 2,
+                   RL_ERR_RANGE, "gemm: bad overflow slices");
+        launch_gemm_cfg<kFp8, 2, 8, 1>(W, tscale, frag, Y, io.x_tile0 * kTileRows, n_kb, T, epilogue, ldy,
+                                       std::min(m_valid, io.x_tile0 * kTileRows), S, frag_out, io, s);
+        check_launch("gemm_frag_kernel");
+        return;
+    }
 #define RL_GEMM_CASE(R, K, DD)                                                            \
     if (c.rt == R && c.ks == K && c.d == DD) {                                            \
         launch_gemm_cfg<kFp8, R, K, DD>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); \
@@ -542,6 +582,14 @@ void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n,
     launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out, norm);
 }
 int add_norm_groups(int m) { return (m_tiles_of(m) + 1) / 2; }
+int device_cus() {
+    static int cus[64] = {0};
+    int dev = 0;
+    RL_HIP(hipGetDevice(&dev));
+    if (dev < 0 || dev >= 64) return 256;
+    if (!cus[dev]) RL_HIP(hipDeviceGetAttribute(&cus[dev], hipDeviceAttributeMultiprocessorCount, dev));
+    return cus[dev];
+}
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s) {
     const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;

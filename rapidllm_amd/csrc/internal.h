@@ -28,6 +28,15 @@ struct NormIO {
     const float* kss = nullptr;
     int kss_n = 0;
     float kss_eps = 0.f;
+    // Store launches: the row tiles from x_tile0 on are not given workgroups of their
+    // own (so the launch fits two workgroups per CU); the first workgroups compute
+    // them after their own rows as x_slices K-slices.  Slice s of token t, row r
+    // (counted from row 16 * x_tile0) goes to xpart[(s * T + t) * x_rows + r]; the
+    // consumer adds the slices in order.
+    float* xpart = nullptr;
+    int x_tile0 = 0;
+    int x_slices = 0;
+    int x_rows = 0;
 };
 
 // gemm.hip
@@ -39,6 +48,7 @@ void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
                     hipStream_t s, int S = 1, void* frag_out = nullptr, const NormIO* norm = nullptr);
 int add_norm_groups(int m);
+int device_cus();  // CUs of the current device
 void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s);
@@ -97,12 +107,15 @@ struct GdnRecords {
 // null) and/or, with frag, the out_proj input fragments of
 // y = gamma * o * silu(z) with the per-head norm left to the GEMM: gss[h][t][4]
 // receives the four 32-column partial sums of o^2 (dv must be 128 then).
+// a / b (per head h, token t): the sum over s < ab_slices of a[(s * T + t) * ab_ld + h]
+// (ab_slices 1: a[t * ld_in + h]).
 bool gdn_fused_supported(int dk, int dv, int K);
 void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_in, const float* A_log,
                       const float* dt_bias, const float* conv_w, const float* conv_in, float* conv_out,
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
-                      int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s);
+                      int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices = 1,
+                      int ab_ld = 0);
 
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);

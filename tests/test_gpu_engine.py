@@ -153,6 +153,40 @@ def test_spec_verify_then_decode_matches_plain_decode(gpu, fp8_pair, n_ok):
     assert np.array_equal(eng.copy_logits(), plain[n_ok + 2])
 
 
+def test_wide_delta_in_proj_slices_match_oracle(gpu, orc):
+    """27B DeltaNet head counts (16 k-heads, 48 v-heads) on a narrow model: the fused
+    in_proj has 16480 rows, past two workgroups per CU, so its a/b rows are computed
+    as K-slice partials that the DeltaNet kernel sums.  Prefill, decode and a
+    partly rejected verify match the oracle and plain decoding."""
+    spec = mini_spec(n_k_heads=16, n_v_heads=48, n_layers=4, layer_kinds=[0, 0, 0, 1])
+    W = M.random_weights(spec, seed=21, w_scale=(1e-3, 1e-2))
+    eng, orc_m = Engine(spec, W, ctx=512), OracleModel(spec, W, ctx=512)
+    prompt = [5, 9, 2, 7, 1]
+    eng.prefill(prompt)
+    orc_m.reset()
+    for t in prompt:
+        g, lg, _ = orc_m.decode(t)
+    assert rel_l2(eng.copy_logits(), lg) < TOL
+    chain = []
+    tok = g
+    for _ in range(4):
+        eng.decode_token(tok)
+        g, lg, _ = orc_m.decode(tok)
+        assert rel_l2(eng.copy_logits(), lg) < TOL
+        chain.append((tok, eng.copy_logits()))
+        tok = g
+    # verify consuming 2 of 4, then plain decode equality
+    eng.prefill(prompt)
+    t0 = chain[0][0]
+    toks = [t0, chain[1][0], (chain[2][0] + 1) % spec.vocab, 3]
+    k, preds = eng.spec_verify(toks)
+    if preds[0] == chain[1][0] and preds[1] != toks[2]:
+        assert k == 2
+        eng.decode_token(chain[2][0])
+        assert np.array_equal(eng.copy_logits(), chain[2][1])
+    eng.close()
+
+
 @pytest.mark.parametrize("quant", [M.Q_Q4_K, M.Q_Q6_K, M.Q_BF16])
 def test_other_weight_formats_match_oracle(gpu, orc, quant):
     spec = mini_spec(n_layers=4, layer_kinds=[0, 1, 0, 0])

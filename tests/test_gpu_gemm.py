@@ -67,6 +67,23 @@ def test_gemm_fp8_config1_full_shape(gpu, orc):
     assert rel_l2(y, yo) <= REL_L2, rel_l2(y, yo)
 
 
+@pytest.mark.parametrize("m,T", [(16480, 1), (16480, 4), (16400, 2)])
+def test_gemm_fp8_overflow_row_tiles(gpu, orc, m, T):
+    """Launches with a few row tiles past two workgroups per CU (the DeltaNet in_proj:
+    16480 rows = 1030 tiles) give the overflow tiles single-tile workgroups; every
+    row, including the last ones, matches the oracle."""
+    r = synth.rng(900 + m + T)
+    n = 512
+    W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    Y = ops.linear_T(ops.Fp8Linear(W, s), X)
+    Yo = orc.gemm_fp8(W, s, X)
+    for t in range(T):
+        assert rel_l2(Y[t], Yo[t]) <= REL_L2
+        tail = slice(m - 6 * 16, m)
+        assert rel_l2(Y[t][tail], Yo[t][tail]) <= REL_L2
+
+
 def test_gemm_fp8_large_activations(gpu, orc):
     """Activations far outside fp16 range (the split keeps fp32's exponent range)."""
     r = synth.rng(8)
