@@ -262,7 +262,7 @@ def main():
         print(json.dumps({"avg_launch_us": round(g_ms * 1e3, 2), "bytes_per_launch": int(g_bytes), "shapes": per}))
         return
     t0 = time.time()
-    eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234)
+    eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=4)
     build_s = time.time() - t0
     print(f"[bench] engine built in {build_s:.1f}s, {eng.device_bytes/1e9:.2f} GB on device", file=sys.stderr,
           flush=True)
@@ -281,6 +281,11 @@ def main():
     eng.time_steps(1, 1)
     eng.time_steps(1, W, mtp_drafts=3)
     tm = eng.time_steps(1, K, mtp_drafts=3) / K
+    # continuous batch of 4 sequences at 32K context each (one weight pass per step)
+    eng.synthetic_context(CTX)
+    eng.replicate_slot0(4)
+    eng.time_batch(4, W)
+    tb4 = eng.time_batch(4, K) / K
     eng.close()
 
     b1 = step_bytes(spec, 1, CTX)
@@ -310,6 +315,8 @@ def main():
         "t4_over_t1": round(t4 / t1, 4),
         "mtp_draft3_ms": round(tm, 4),
         "spec_tok_s_full_accept": round(4000.0 / (t4 + tm), 3),
+        "batch4_step_ms": round(tb4, 4),
+        "batch4_tok_s": round(4000.0 / tb4, 3),
         "step_roofline": {"t1_bytes": b1["total"], "t1_GBps": round(b1["total"] / t1 / 1e6, 1),
                           "t1_frac": round(b1["total"] / t1 / 1e6 / PEAK_GBS, 4),
                           "t4_bytes": b4["total"], "t4_GBps": round(b4["total"] / t4 / 1e6, 1),

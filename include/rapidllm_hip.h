@@ -229,6 +229,33 @@ int rl_hip_engine_synthetic_context(RlEngine* e, int n, uint64_t seed);
 int rl_hip_engine_time_steps(RlEngine* e, int T, int iters, int mtp_drafts, float* ms);
 void* rl_hip_engine_stream(RlEngine* e);
 
+/* ---- continuous batch (cuda_engine.h:46-66) ------------------------------------
+ * Replaces: Engine::max_batch / decode_tokens / copy_logits_n / copy_greedy_n /
+ * replicate_slot0 / zero_slots / prefill_slot (include/rapidllm/runtime/
+ * cuda_engine.h:46-66) and the CUDA launch_decode_batch (cuda_engine.cu:18999-19113)
+ * that Session::generate_batch drives (src/runtime/session.cpp:832-964).
+ * An engine created with max_batch > 1 keeps max_batch independent sequences
+ * (slots): DeltaNet state, conv window, KV cache and position each.  Slot 0 is the
+ * sequence every single-sequence call works on.  decode_tokens consumes tokens[b]
+ * at position poss[b] for slots 0 .. B-1 in one weight pass (B = 1: set_pos +
+ * decode_token, as the reference); copy_logits_n / copy_greedy_n return its B rows.
+ * prefill_slot runs the prefill on slot `slot` (copy_logits then has its last row).
+ * Needs the folded path (FP8 / BF16 linears, v_dim 128), max_batch <= 8. */
+RlEngine* rl_hip_engine_create_batch(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx,
+                                     int max_T, int max_batch, int* status);
+RlEngine* rl_hip_engine_create_synthetic_batch(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T,
+                                               int max_batch, int* status);
+int rl_hip_engine_max_batch(RlEngine* e, int* max_batch);                              /* :46 */
+int rl_hip_engine_decode_tokens(RlEngine* e, const int32_t* tokens, const int* poss, int B); /* :48 */
+int rl_hip_engine_copy_logits_n(RlEngine* e, float* host, int B);                      /* :53 */
+int rl_hip_engine_copy_greedy_n(RlEngine* e, int32_t* host, int B);                    /* :57 */
+int rl_hip_engine_replicate_slot0(RlEngine* e, int n_slots);                           /* :59 */
+int rl_hip_engine_zero_slots(RlEngine* e, int n_slots);                                /* :60 */
+int rl_hip_engine_prefill_slot(RlEngine* e, const int32_t* ids, int n, int slot);      /* :62 */
+/* Benchmark support: time `iters` graph replays of the B-sequence batch step (the
+ * slots' positions advance; the tokens in place are re-fed). */
+int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms);
+
 /* ---- bandwidth calibration ------------------------------------------------
  * No counterpart in the reference.  A streaming copy / read of `bytes` (multiple of
  * 16) that measures the achievable HBM rate and calibrates rocprof's FETCH_SIZE /

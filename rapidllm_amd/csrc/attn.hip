@@ -50,6 +50,7 @@ struct AttnArgs {
     int ctx;
     const int* pos;  // device: position of token 0
     int T, nq, nkv, G, rot;
+    int t_off, T_out;  // outputs: token t goes to column t_off + t of T_out
     float theta, eps;
     i32x4* qf;     // [nkv][8 s][4 g][2*PT ct][16 col] x 16 B
     float* part_o; // [nkv][chunks][kMaxPairs][hd]
@@ -354,7 +355,7 @@ __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
     const float val = o * sigmoid_f(gate);
     const int n = p.nq * kHD;
     const int j = h * kHD + d;
-    if (p.out) p.out[static_cast<size_t>(t) * n + j] = val;
+    if (p.out) p.out[static_cast<size_t>(p.t_off + t) * n + j] = val;
     if (p.frag) {
         red[1][dl] = val;  // wave 0 only from here on: reuse a row of red
         __builtin_amdgcn_wave_barrier();
@@ -368,9 +369,9 @@ __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
             for (int e = 0; e < 8; ++e) split_bf16(red[1][8 * dl + e], hi.hh[e], mid.hh[e]);
             const int kb = unit >> 4, jb = (unit & 15) * 8;
             const int gg = jb >> 5, i = (jb >> 3) & 3;
-            const size_t u = ((static_cast<size_t>(kb) * 4 + i) * 4 + gg) * (2 * p.T) + t;
+            const size_t u = ((static_cast<size_t>(kb) * 4 + i) * 4 + gg) * (2 * p.T_out) + p.t_off + t;
             p.frag[u] = hi.v;
-            p.frag[u + p.T] = mid.v;
+            p.frag[u + p.T_out] = mid.v;
         }
     }
 }
@@ -387,8 +388,10 @@ size_t attn_workspace_bytes(int nkv, int ctx) {
 
 void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,
                        int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot, float theta, float eps,
-                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s) {
+                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s, int t_off, int T_out) {
     RL_REQUIRE(hd == kHD, RL_ERR_UNSUPPORTED, "attn: head_dim must be 256");
+    if (T_out <= 0) T_out = T;
+    RL_REQUIRE(t_off >= 0 && t_off + T <= T_out && T_out <= 8, RL_ERR_RANGE, "attn: bad output columns");
     RL_REQUIRE(nkv > 0 && nq % nkv == 0, RL_ERR_RANGE, "attn: n_q must be a multiple of n_kv");
     const int G = nq / nkv;
     RL_REQUIRE(T >= 1 && G * T <= kMaxPairs, RL_ERR_RANGE, "attn: (n_q/n_kv) * T must be <= 32");
@@ -425,6 +428,8 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     p.max_chunks = chunks;
     p.out = out;
     p.frag = static_cast<i32x4*>(frag);
+    p.t_off = t_off;
+    p.T_out = T_out;
     hipLaunchKernelGGL(qk_prep_kernel, dim3(nq + 2 * nkv, T), dim3(64), 0, s, p);
     check_launch("qk_prep_kernel");
     if (pair_tiles(G, T) == 1)

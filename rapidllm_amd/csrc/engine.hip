@@ -104,8 +104,10 @@ struct Layer {
 
 class Engine {
    public:
-    Engine(const RlModelConfig& cfg, int ctx, int tmax) : c_(cfg), tmax_(tmax) {
+    Engine(const RlModelConfig& cfg, int ctx, int tmax, int max_batch = 1) : c_(cfg), tmax_(tmax), mb_(max_batch) {
         RL_REQUIRE(tmax >= 1 && tmax <= 4, RL_ERR_RANGE, "engine: max_T must be in 1..4");
+        RL_REQUIRE(max_batch >= 1 && max_batch <= 8, RL_ERR_RANGE, "engine: max_batch must be in 1..8");
+        tcap_ = std::max(tmax_, mb_);
         RL_REQUIRE(c_.n_layers >= 1 && c_.n_layers <= RL_MAX_LAYERS, RL_ERR_RANGE, "engine: bad layer count");
         RL_REQUIRE(c_.hidden % 128 == 0, RL_ERR_UNSUPPORTED, "engine: hidden must be a multiple of 128");
         RL_REQUIRE(c_.k_dim == 128 && c_.v_dim % 32 == 0, RL_ERR_UNSUPPORTED, "engine: DeltaNet dims 128 / 32k");
@@ -151,14 +153,11 @@ class Engine {
     int max_t() const { return tmax_; }
     size_t device_bytes() const { return mem_.total; }
 
+    // Clear the current slot's sequence state (slot 0 outside prefill_slot).
     void reset() {
         sync_graph_state();
-        RL_HIP(hipMemsetAsync(scal_, 0, kScalars * sizeof(int), st_));
-        for (size_t l = 0; l < S_.size(); ++l) {
-            RL_HIP(hipMemsetAsync(S_[l], 0, s_slot_ * sizeof(float), st_));
-            RL_HIP(hipMemsetAsync(conv_[l], 0, conv_slot_ * sizeof(float), st_));
-        }
-        for (int* n : rec_n_) RL_HIP(hipMemsetAsync(n, 0, static_cast<size_t>(R_) * c_.n_v_heads * sizeof(int), st_));
+        zero_slot_state(cs_);
+        RL_HIP(hipStreamSynchronize(st_));
         RL_HIP(hipMemsetAsync(h_last_, 0, c_.hidden * sizeof(float), st_));
         RL_HIP(hipMemsetAsync(h_prev_, 0, c_.hidden * sizeof(float), st_));
         RL_HIP(hipStreamSynchronize(st_));
@@ -191,7 +190,7 @@ class Engine {
     void decode_token(int32_t token) {
         check_ids(&token, 1);
         RL_REQUIRE(pos_ + 1 <= ctx_capacity(), RL_ERR_RANGE, "decode: context full");
-        upload_ints(scal_ + kNextTok, &token, 1);
+        upload_ints(sc() + kNextTok, &token, 1);
         run_graph(1);
         readback();
     }
@@ -200,7 +199,7 @@ class Engine {
     void decode_steps(int n) {
         RL_REQUIRE(n >= 0, RL_ERR_RANGE, "decode_steps: n < 0");
         RL_REQUIRE(pos_ + n <= ctx_capacity(), RL_ERR_RANGE, "decode_steps: context full");
-        RL_HIP(hipMemsetAsync(scal_ + kGenCount, 0, sizeof(int), st_));
+        RL_HIP(hipMemsetAsync(sc() + kGenCount, 0, sizeof(int), st_));
         for (int i = 0; i < n; ++i) run_graph(1);
         readback();
     }
@@ -229,7 +228,7 @@ class Engine {
         if (!has_mtp_ || n <= 0) return 0;
         RL_REQUIRE(n <= 7, RL_ERR_RANGE, "mtp_draft: at most 7 drafts");
         check_ids(&first, 1);
-        upload_ints(scal_ + kNextTok, &first, 1);
+        upload_ints(sc() + kNextTok, &first, 1);
         run_mtp(n);
         RL_HIP(hipMemcpyAsync(out, tok_ + 1, n * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipStreamSynchronize(st_));
@@ -242,7 +241,7 @@ class Engine {
         RL_REQUIRE(pos_ + T <= ctx_capacity(), RL_ERR_RANGE, "spec_verify: context full");
         check_ids(toks, T);
         if (T == 1)  // the T = 1 step feeds the device's next token
-            upload_ints(scal_ + kNextTok, toks, 1);
+            upload_ints(sc() + kNextTok, toks, 1);
         else
             upload_ints(tok_, toks, T);
         run_graph(T, /*from_host=*/true);
@@ -257,7 +256,7 @@ class Engine {
         RL_REQUIRE(T >= 2 && T <= tmax_, RL_ERR_RANGE, "mtp_spec: T out of range");
         RL_REQUIRE(pos_ + T <= ctx_capacity(), RL_ERR_RANGE, "mtp_spec: context full");
         check_ids(&t0, 1);
-        upload_ints(scal_ + kNextTok, &t0, 1);
+        upload_ints(sc() + kNextTok, &t0, 1);
         run_mtp(T - 1);
         run_graph(T, /*from_host=*/true);
         readback();
@@ -273,7 +272,7 @@ class Engine {
     // rows below pos are whatever the cache holds: zeros or synthetic values).
     void set_pos(int pos) {
         RL_REQUIRE(pos >= 0 && pos <= ctx_capacity(), RL_ERR_RANGE, "set_pos: out of range");
-        upload_ints(scal_ + kPos, &pos, 1);
+        upload_ints(sc() + kPos, &pos, 1);
         RL_HIP(hipStreamSynchronize(st_));
         pos_ = pos;
     }
@@ -284,13 +283,13 @@ class Engine {
         RL_REQUIRE(n >= 0 && n <= ctx_capacity(), RL_ERR_RANGE, "synthetic_context: out of range");
         reset();
         const size_t kv = static_cast<size_t>(c_.n_kv) * ctx_ * c_.head_dim;
-        for (size_t l = 0; l < kc_.size(); ++l) {
-            fill_normal_f16(kc_[l], kv, 1.f, seed + 11 * l + 1, st_);
-            fill_normal_f16(vt_[l], kv, 1.f, seed + 11 * l + 2, st_);
+        for (int l = 0; l < static_cast<int>(kc_.size()); ++l) {
+            fill_normal_f16(slot_kc(l), kv, 1.f, seed + 11 * l + 1, st_);
+            fill_normal_f16(slot_vt(l), kv, 1.f, seed + 11 * l + 2, st_);
         }
-        for (size_t l = 0; l < S_.size(); ++l) {
-            fill_normal_f32(S_[l], s_slot_, 0.f, 0.02f, seed + 13 * l + 3, st_);
-            fill_normal_f32(conv_[l], conv_slot_, 0.f, 1.f, seed + 13 * l + 4, st_);
+        for (int l = 0; l < static_cast<int>(S_.size()); ++l) {
+            fill_normal_f32(slot_S(l), s_slot_, 0.f, 0.02f, seed + 13 * l + 3, st_);
+            fill_normal_f32(slot_conv(l), conv_slot_, 0.f, 1.f, seed + 13 * l + 4, st_);
         }
         RL_HIP(hipStreamSynchronize(st_));
         set_pos(n);
@@ -321,6 +320,118 @@ class Engine {
 
     void* stream() const { return st_; }
 
+    float time_batch(int B, int iters) {
+        RL_REQUIRE(B >= 2 && B <= mb_, RL_ERR_RANGE, "time_batch: B must be in 2..max_batch");
+        hipEvent_t a, b;
+        RL_HIP(hipEventCreate(&a));
+        RL_HIP(hipEventCreate(&b));
+        RL_HIP(hipEventRecord(a, st_));
+        for (int i = 0; i < iters; ++i) launch_captured(200 + B, [&] { step_batch(B); });
+        RL_HIP(hipEventRecord(b, st_));
+        RL_HIP(hipEventSynchronize(b));
+        float ms = 0.f;
+        RL_HIP(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        return ms;
+    }
+
+    // ------------------------------------------------------------ batch decode
+    // Slots 0 .. max_batch-1 each hold one sequence (DeltaNet state, conv ring,
+    // records, KV cache, scalars); slot 0 is the single-sequence state
+    // (cuda_engine.h:46-66).
+    int max_batch() const { return mb_; }
+
+    // One token for each of B sequences (slot b at position poss[b]) in one weight
+    // pass: the linears run with B rows, DeltaNet and attention per slot.
+    void decode_tokens(const int32_t* tokens, const int* poss, int B) {
+        RL_REQUIRE(B >= 1 && B <= mb_ && tokens && poss, RL_ERR_RANGE, "decode_tokens: B out of range");
+        check_ids(tokens, B);
+        for (int b = 0; b < B; ++b)
+            RL_REQUIRE(poss[b] >= 0 && poss[b] < ctx_capacity(), RL_ERR_RANGE, "decode_tokens: position out of range");
+        if (B == 1) {  // the single-sequence step, as the reference does
+            set_pos(poss[0]);
+            decode_token(tokens[0]);
+            batch_rows_ = 1;
+            return;
+        }
+        // one staging of tokens and positions (every call ends with a sync)
+        std::memcpy(host_in_, tokens, static_cast<size_t>(B) * sizeof(int));
+        std::memcpy(host_in_ + 8, poss, static_cast<size_t>(B) * sizeof(int));
+        RL_HIP(hipMemcpyAsync(tok_, host_in_, static_cast<size_t>(B) * sizeof(int), hipMemcpyHostToDevice, st_));
+        for (int b = 0; b < B; ++b)
+            RL_HIP(hipMemcpyAsync(scal_ + b * kScalars + kPos, host_in_ + 8 + b, sizeof(int), hipMemcpyHostToDevice,
+                                  st_));
+        launch_captured(200 + B, [&] { step_batch(B); });
+        RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+        batch_rows_ = B;
+    }
+
+    // logits rows of the last decode_tokens (row b = slot b)
+    void copy_logits_n(float* host, int B) {
+        RL_REQUIRE(host && B >= 1 && B <= batch_rows_, RL_ERR_RANGE, "copy_logits_n: B out of range");
+        if (batch_rows_ == 1) {
+            copy_logits(host);
+            return;
+        }
+        RL_HIP(hipMemcpyAsync(host, logits_, static_cast<size_t>(B) * c_.vocab * sizeof(float), hipMemcpyDeviceToHost,
+                              st_));
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+
+    void copy_greedy_n(int32_t* host, int B) {
+        RL_REQUIRE(host && B >= 1 && B <= batch_rows_, RL_ERR_RANGE, "copy_greedy_n: B out of range");
+        if (batch_rows_ == 1) {
+            host[0] = greedy_;
+            return;
+        }
+        std::memcpy(host, host_rb_ + kRbPreds, static_cast<size_t>(B) * sizeof(int));
+    }
+
+    // Copy slot 0's sequence state into slots 1 .. n_slots-1 (same-prompt batch).
+    void replicate_slot0(int n_slots) {
+        RL_REQUIRE(n_slots >= 1 && n_slots <= mb_, RL_ERR_RANGE, "replicate_slot0: n_slots out of range");
+        sync_graph_state();
+        auto copy = [&](void* dst, const void* src, size_t bytes) {
+            RL_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyDeviceToDevice, st_));
+        };
+        for (int b = 1; b < n_slots; ++b) {
+            copy(scal_ + b * kScalars, scal_, kScalars * sizeof(int));
+            for (size_t l = 0; l < S_.size(); ++l) {
+                copy(S_[l] + b * s_bstride_, S_[l], s_bstride_ * sizeof(float));
+                copy(conv_[l] + b * conv_bstride_, conv_[l], conv_bstride_ * sizeof(float));
+            }
+            for (size_t l = 0; l < rec_.size(); ++l) {
+                copy(rec_[l] + b * rec_bstride_, rec_[l], rec_bstride_ * sizeof(float));
+                copy(rec_n_[l] + b * recn_bstride_, rec_n_[l], recn_bstride_ * sizeof(int));
+            }
+            if (!kc_.empty()) copy(kc_[0] + b * kv_bstride_, kc_[0], kv_bstride_ * sizeof(uint16_t));
+        }
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+
+    void zero_slots(int n_slots) {
+        RL_REQUIRE(n_slots >= 1 && n_slots <= mb_, RL_ERR_RANGE, "zero_slots: n_slots out of range");
+        sync_graph_state();
+        for (int b = 0; b < n_slots; ++b) zero_slot_state(b);
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+
+    // Prefill one sequence into slot `slot` (the single-sequence prefill on that
+    // slot's state); copy_logits then returns its last row.
+    void prefill_slot(const int32_t* ids, int n, int slot) {
+        RL_REQUIRE(slot >= 0 && slot < mb_, RL_ERR_RANGE, "prefill_slot: slot out of range");
+        cs_ = slot;
+        try {
+            prefill(ids, n);
+        } catch (...) {
+            cs_ = 0;
+            throw;
+        }
+        cs_ = 0;
+    }
+
    private:
     // device scalar block
     enum { kPos = 0, kSlot = 1, kNCons = 2, kNextTok = 3, kGenCount = 4, kScalars = 8 };
@@ -333,6 +444,19 @@ class Engine {
 
     RlModelConfig c_;
     int ctx_ = 0, tmax_ = 4, R_ = 5;
+    int mb_ = 1;    // sequences (slots) for batch decode
+    int tcap_ = 4;  // activation rows: max(tmax_, mb_)
+    int cs_ = 0;    // slot the single-sequence calls work on (prefill_slot)
+    int batch_rows_ = 1;  // rows of the last decode_tokens
+    size_t s_bstride_ = 0, conv_bstride_ = 0, rec_bstride_ = 0, kv_bstride_ = 0;
+    int recn_bstride_ = 0;
+    int* sc() const { return scal_ + cs_ * kScalars; }
+    float* slot_S(int l) const { return S_[l] + cs_ * s_bstride_; }
+    float* slot_conv(int l) const { return conv_[l] + cs_ * conv_bstride_; }
+    float* slot_rec(int l) const { return rec_[l] + cs_ * rec_bstride_; }
+    int* slot_recn(int l) const { return rec_n_[l] + cs_ * recn_bstride_; }
+    uint16_t* slot_kc(int l) const { return kc_[l] + cs_ * kv_bstride_; }
+    uint16_t* slot_vt(int l) const { return vt_[l] + cs_ * kv_bstride_; }
     hipStream_t st_ = nullptr;
     DevAlloc mem_;
     std::map<std::string, const RlTensor*> tab_;
@@ -422,7 +546,9 @@ class Engine {
             int n_attn = 0;
             for (int i = 0; i < c_.n_layers; ++i) n_attn += c_.layer_kind[i] == RL_LAYER_ATTN;
             const size_t kv = static_cast<size_t>(nkv) * ctx_ * hd;
-            uint16_t* blk = mem_.get_n<uint16_t>(2 * kv * n_attn);
+            // slot b's caches follow slot 0's at kv_bstride_
+            kv_bstride_ = 2 * kv * n_attn;
+            uint16_t* blk = mem_.get_n<uint16_t>(kv_bstride_ * mb_);
             for (int l = 0; l < n_attn; ++l) {
                 kc_.push_back(blk + 2 * l * kv);
                 vt_.push_back(blk + (2 * l + 1) * kv);
@@ -542,13 +668,14 @@ class Engine {
         // states (the recurrent state S is allocated below, once the kernel is chosen)
         s_slot_ = static_cast<size_t>(nv) * dv * dk;
         conv_slot_ = static_cast<size_t>(conv_dim) * c_.conv_k;
-        for (int l = 0; l < nd; ++l) conv_.push_back(mem_.get_n<float>(conv_slot_ * R_));
+        conv_bstride_ = conv_slot_ * R_;  // a ring of R windows per layer and slot
+        for (int l = 0; l < nd; ++l) conv_.push_back(mem_.get_n<float>(conv_bstride_ * mb_));
         RL_REQUIRE(static_cast<int>(kc_.size()) == na, RL_ERR_INTERNAL, "engine: attention layer count");
 
         // activations
-        const int T = tmax_;
+        const int T = tcap_;  // rows: verify tokens or batch sequences
         max_in_ = std::max({H, zdim, nq * hd, I, 2 * H});
-        scal_ = mem_.get_n<int>(kScalars);
+        scal_ = mem_.get_n<int>(static_cast<size_t>(kScalars) * mb_);  // one block per slot
         tok_ = mem_.get_n<int>(8);
         preds_ = mem_.get_n<int>(8);
         gen_ = mem_.get_n<int>(kGenCap);
@@ -575,14 +702,19 @@ class Engine {
         }
         // one committed S per layer plus R banks of per-token records with the fused
         // kernel, a ring of R states with the unfused one
+        RL_REQUIRE(mb_ == 1 || gdn_fused_norm_ || nd == 0, RL_ERR_UNSUPPORTED,
+                   "engine: batch decode needs the fused DeltaNet path (FP8/BF16 linears, v_dim 128)");
+        s_bstride_ = s_slot_ * (gdn_fused_norm_ ? 1 : R_);
+        rec_bstride_ = static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats;
+        recn_bstride_ = R_ * nv;
         for (int l = 0; l < nd; ++l) {
-            S_.push_back(mem_.get_n<float>(s_slot_ * (gdn_fused_norm_ ? 1 : R_)));
+            S_.push_back(mem_.get_n<float>(s_bstride_ * mb_));
             if (gdn_fused_norm_) {
-                rec_.push_back(mem_.get_n<float>(static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats));
-                rec_n_.push_back(mem_.get_n<int>(static_cast<size_t>(R_) * nv));
+                rec_.push_back(mem_.get_n<float>(rec_bstride_ * mb_));
+                rec_n_.push_back(mem_.get_n<int>(static_cast<size_t>(recn_bstride_) * mb_));
             }
         }
-        gss_ = mem_.get_n<float>(static_cast<size_t>(nv) * tmax_ * 4);
+        gss_ = mem_.get_n<float>(static_cast<size_t>(nv) * tcap_ * 4);
         // in_proj = [qkv; z; a; b]: when its row-tile pairs overflow two workgroups per
         // CU and the overflow is the a/b block, the a/b rows are computed as K-slices
         if (gdn_fused_norm_ && nd > 0) {
@@ -596,7 +728,7 @@ class Engine {
                 (n_kb + kAbSlices - 1) / kAbSlices <= 8 && d0->in_width == m_tiles * 16) {
                 ab_tile0_ = tile0;
                 ab_rows_ = (m_tiles - tile0) * 16;
-                abpart_ = mem_.get_n<float>(static_cast<size_t>(kAbSlices) * tmax_ * ab_rows_);
+                abpart_ = mem_.get_n<float>(static_cast<size_t>(kAbSlices) * tcap_ * ab_rows_);
             }
         }
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
@@ -901,7 +1033,7 @@ class Engine {
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
         float* x = xres_[0];
-        if (feed) copy_int(scal_ + kNextTok, tok_, st_);
+        if (feed) copy_int(sc() + kNextTok, tok_, st_);
         embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, T, st_);
         rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_x_, H, T, eps, st_);
         NormIO in;
@@ -929,12 +1061,12 @@ class Engine {
                     // recurrent update + gated RMSNorm's elementwise part + out_proj
                     // packing in one kernel; out_proj applies the per-head 1/rms.  A step
                     // that consumes all its tokens commits S directly.
-                    const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, tmax_,
+                    const GdnRecords rec{slot_rec(Ly.dslot), slot_recn(Ly.dslot), sc() + kNCons, tmax_,
                                          T > 1 && !force_all};
                     const float* a_in = abpart_ ? abpart_ : ybuf_ + Ly.off_a;
                     const float* b_in = abpart_ ? abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b;
-                    gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, conv_[Ly.dslot],
-                                     nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot, conv_slot_, R_, &rec, nullptr,
+                    gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, slot_conv(Ly.dslot),
+                                     nullptr, slot_S(Ly.dslot), slot_S(Ly.dslot), sc() + kSlot, conv_slot_, R_, &rec, nullptr,
                                      ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, T, nk, nv, c_.k_dim, dv, c_.conv_k,
                                      c_.v_tiled, st_, abpart_ ? kAbSlices : 1, ab_rows_);
                     out.kss = gss_;
@@ -942,7 +1074,7 @@ class Engine {
                     out.kss_eps = 1e-6f;
                 } else {
                     gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
-                               Ly.conv_w, conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_,
+                               Ly.conv_w, slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_,
                                s_slot_, R_, o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                     gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f,
                                st_);
@@ -952,8 +1084,8 @@ class Engine {
             } else {
                 gemm_on(Ly.qkv_parts[0], frag_x_, ybuf_, Ly.qkv_width, Ly.qkv_parts[0].m, T, kEpiStore, nullptr,
                         io_in);
-                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
-                                  scal_ + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot), ctx_,
+                                  sc() + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
                                   attn_ws_bytes_, xn_, frag_, st_);
                 gemm_on(Ly.o_proj, frag_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
             }
@@ -964,8 +1096,8 @@ class Engine {
         x_ = x;  // hidden after the layers (pre final norm), for the MTP history
         gemm_on(lm_head_, frag_x_, logits_, c_.vocab, c_.vocab, T, kEpiStore, nullptr, &in);
         argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
-        accept(tok_, preds_, T, force_all, scal_ + kPos, scal_ + kSlot, R_, scal_ + kNCons, scal_ + kNextTok, gen_,
-               scal_ + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
+        accept(tok_, preds_, T, force_all, sc() + kPos, sc() + kSlot, R_, sc() + kNCons, sc() + kNextTok, gen_,
+               sc() + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
     }
 
     void step(int T, int force_all, bool feed) {
@@ -977,7 +1109,7 @@ class Engine {
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
         int cur = 0, pending = 0;
-        if (feed) copy_int(scal_ + kNextTok, tok_, st_);
+        if (feed) copy_int(sc() + kNextTok, tok_, st_);
         embed_rows(embed_, embed_kind_, tok_, xres_[cur], H, c_.vocab, T, st_);
         for (int i = 0; i < c_.n_layers; ++i) {
             Layer& Ly = L_[i];
@@ -985,14 +1117,14 @@ class Engine {
             if (Ly.kind == RL_LAYER_DELTA) {
                 linear_parts(Ly.in_parts, Ly.in_offs, xn_, ybuf_, Ly.in_width, T);
                 gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
-                           conv_[Ly.dslot], nullptr, S_[Ly.dslot], nullptr, scal_ + kSlot, conv_slot_, s_slot_, R_, o_,
+                           slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_, s_slot_, R_, o_,
                            T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                 gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
                 pending = linear_residual(Ly.out_proj, xn_, T);
             } else {
                 linear_parts(Ly.qkv_parts, Ly.qkv_offs, xn_, ybuf_, Ly.qkv_width, T);
-                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
-                                  scal_ + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot), ctx_,
+                                  sc() + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
                                   attn_ws_bytes_, xn_, frag_, st_);
                 pending = linear_residual(Ly.o_proj, xn_, T);
             }
@@ -1019,15 +1151,15 @@ class Engine {
         x_ = xres_[cur];  // hidden after the layers (pre final norm), for the MTP history
         linear(lm_head_, xn_, logits_, c_.vocab, c_.vocab, T, kEpiStore);
         argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
-        accept(tok_, preds_, T, force_all, scal_ + kPos, scal_ + kSlot, R_, scal_ + kNCons, scal_ + kNextTok, gen_,
-               scal_ + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
+        accept(tok_, preds_, T, force_all, sc() + kPos, sc() + kSlot, R_, sc() + kNCons, sc() + kNextTok, gen_,
+               sc() + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
     }
 
     // MTP stem draft of n tokens: tok_[0] = next token, tok_[1..n] = drafts.
     void mtp_body(int n) {
         const int H = c_.hidden;
         const float eps = c_.rms_eps;
-        copy_int(scal_ + kNextTok, tok_, st_);
+        copy_int(sc() + kNextTok, tok_, st_);
         const size_t half_units = static_cast<size_t>(H / 128) * 16 * 2;  // fragment units of H columns, T = 1
         for (int i = 0; i < n; ++i) {
             embed_rows(embed_, embed_kind_, tok_ + i, mtp_e_, H, c_.vocab, 1, st_);
@@ -1092,8 +1224,83 @@ class Engine {
 
     void sync_graph_state() { RL_HIP(hipStreamSynchronize(st_)); }
 
+    // Zero slot b's sequence state: scalars, DeltaNet state and the conv window the
+    // ring starts from, record counts.
+    void zero_slot_state(int b) {
+        RL_HIP(hipMemsetAsync(scal_ + b * kScalars, 0, kScalars * sizeof(int), st_));
+        for (size_t l = 0; l < S_.size(); ++l) {
+            RL_HIP(hipMemsetAsync(S_[l] + b * s_bstride_, 0, s_slot_ * sizeof(float), st_));
+            RL_HIP(hipMemsetAsync(conv_[l] + b * conv_bstride_, 0, conv_slot_ * sizeof(float), st_));
+        }
+        for (size_t l = 0; l < rec_n_.size(); ++l)
+            RL_HIP(hipMemsetAsync(rec_n_[l] + b * recn_bstride_, 0, recn_bstride_ * sizeof(int), st_));
+    }
+
+    // Batch step: B sequences, one token each (tok_[b] at slot b's position); the
+    // folded-norm linears with B rows, the DeltaNet kernel over the B slots, attention
+    // per slot writing its column of o_proj's input.
+    void step_batch(int B) {
+        const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
+        const int nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
+        const float eps = c_.rms_eps;
+        float* x = xres_[0];
+        embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, B, st_);
+        rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_x_, H, B, eps, st_);
+        NormIO in;
+        in.ss_in = ss_;
+        in.groups_in = add_norm_groups(H);
+        in.n_norm = H;
+        in.eps = eps;
+        const GdnBatch bt{B, s_bstride_, conv_bstride_, rec_bstride_, recn_bstride_, kScalars};
+        for (int i = 0; i < c_.n_layers; ++i) {
+            Layer& Ly = L_[i];
+            const NormIO* io_in = i == 0 ? nullptr : &in;
+            NormIO out;
+            out.gamma_out = Ly.ffn_norm;
+            out.ss_out = ss_;
+            if (Ly.kind == RL_LAYER_DELTA) {
+                NormIO in_ab = io_in ? *io_in : NormIO{};
+                if (abpart_) {
+                    in_ab.xpart = abpart_;
+                    in_ab.x_tile0 = ab_tile0_;
+                    in_ab.x_slices = kAbSlices;
+                    in_ab.x_rows = ab_rows_;
+                }
+                gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, B, kEpiStore, nullptr,
+                        abpart_ ? &in_ab : io_in);
+                const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, tmax_, 0};
+                const float* a_in = abpart_ ? abpart_ : ybuf_ + Ly.off_a;
+                const float* b_in = abpart_ ? abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b;
+                gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, conv_[Ly.dslot],
+                                 nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot, conv_slot_, R_, &rec, nullptr,
+                                 ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, 1, nk, nv, c_.k_dim, dv, c_.conv_k,
+                                 c_.v_tiled, st_, abpart_ ? kAbSlices : 1, ab_rows_, &bt);
+                out.kss = gss_;
+                out.kss_n = dv;
+                out.kss_eps = 1e-6f;
+                gemm_on(Ly.out_proj, frag_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
+                out.kss = nullptr;
+            } else {
+                gemm_on(Ly.qkv_parts[0], frag_x_, ybuf_, Ly.qkv_width, Ly.qkv_parts[0].m, B, kEpiStore, nullptr,
+                        io_in);
+                for (int b = 0; b < B; ++b)
+                    attn_decode_layer(ybuf_ + static_cast<size_t>(b) * Ly.qkv_width, Ly.qkv_width, Ly.q_norm,
+                                      Ly.k_norm, kc_[Ly.aslot] + b * kv_bstride_, vt_[Ly.aslot] + b * kv_bstride_,
+                                      ctx_, scal_ + b * kScalars + kPos, 1, nq, nkv, hd, c_.rotary_dim,
+                                      c_.rope_theta, eps, attn_ws_, attn_ws_bytes_, xn_, frag_, st_, b, B);
+                gemm_on(Ly.o_proj, frag_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
+            }
+            gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, B, kEpiSwiGLU, frag_h_, &in);
+            out.gamma_out = i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_;
+            gemm_on(Ly.down, frag_h_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
+        }
+        gemm_on(lm_head_, frag_x_, logits_, c_.vocab, c_.vocab, B, kEpiStore, nullptr, &in);
+        argmax_rows(logits_, B, c_.vocab, preds_, nullptr, arg_ws_, st_);
+        batch_advance(scal_, kScalars, B, R_, kPos, kSlot, kNCons, st_);
+    }
+
     void readback() {
-        RL_HIP(hipMemcpyAsync(host_rb_, scal_, kScalars * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipMemcpyAsync(host_rb_, sc(), kScalars * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipMemcpyAsync(host_rb_ + kRbToks, tok_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipStreamSynchronize(st_));
@@ -1131,6 +1338,36 @@ RlEngine* rl_hip_engine_create_synthetic(const RlModelConfig* cfg, uint64_t seed
         RL_REQUIRE(cfg != nullptr, RL_ERR_RANGE, "engine_create_synthetic: null config");
         auto e = std::make_unique<rl::Engine>(*cfg, ctx, max_T);
         e->load_synthetic(seed);
+        e->reset();
+        out = new RlEngine{std::move(e)};
+    });
+    if (status) *status = rc;
+    return out;
+}
+
+RlEngine* rl_hip_engine_create_batch(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx,
+                                     int max_T, int max_batch, int* status) {
+    RlEngine* out = nullptr;
+    const int rc = guard([&] {
+        RL_REQUIRE(cfg && tensors && n_tensors > 0, RL_ERR_RANGE, "engine_create: null config or weights");
+        auto e = std::make_unique<rl::Engine>(*cfg, ctx, max_T, max_batch);
+        e->load(tensors, n_tensors);
+        e->zero_slots(max_batch);
+        e->reset();
+        out = new RlEngine{std::move(e)};
+    });
+    if (status) *status = rc;
+    return out;
+}
+
+RlEngine* rl_hip_engine_create_synthetic_batch(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T,
+                                               int max_batch, int* status) {
+    RlEngine* out = nullptr;
+    const int rc = guard([&] {
+        RL_REQUIRE(cfg != nullptr, RL_ERR_RANGE, "engine_create_synthetic: null config");
+        auto e = std::make_unique<rl::Engine>(*cfg, ctx, max_T, max_batch);
+        e->load_synthetic(seed);
+        e->zero_slots(max_batch);
         e->reset();
         out = new RlEngine{std::move(e)};
     });
@@ -1245,5 +1482,56 @@ int rl_hip_engine_info(RlEngine* e, int* vocab, int* hidden, int* ctx_capacity, 
     });
 }
 void* rl_hip_engine_stream(RlEngine* e) { return e && e->e ? e->e->stream() : nullptr; }
+
+int rl_hip_engine_max_batch(RlEngine* e, int* max_batch) {
+    return guard([&] {
+        RL_ENGINE(e);
+        RL_REQUIRE(max_batch, RL_ERR_RANGE, "max_batch: null output");
+        *max_batch = e->e->max_batch();
+    });
+}
+int rl_hip_engine_decode_tokens(RlEngine* e, const int32_t* tokens, const int* poss, int B) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->decode_tokens(tokens, poss, B);
+    });
+}
+int rl_hip_engine_copy_logits_n(RlEngine* e, float* host, int B) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->copy_logits_n(host, B);
+    });
+}
+int rl_hip_engine_copy_greedy_n(RlEngine* e, int32_t* host, int B) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->copy_greedy_n(host, B);
+    });
+}
+int rl_hip_engine_replicate_slot0(RlEngine* e, int n_slots) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->replicate_slot0(n_slots);
+    });
+}
+int rl_hip_engine_zero_slots(RlEngine* e, int n_slots) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->zero_slots(n_slots);
+    });
+}
+int rl_hip_engine_prefill_slot(RlEngine* e, const int32_t* ids, int n, int slot) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->prefill_slot(ids, n, slot);
+    });
+}
+int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms) {
+    return guard([&] {
+        RL_ENGINE(e);
+        RL_REQUIRE(ms && iters >= 1, RL_ERR_RANGE, "time_batch: bad arguments");
+        *ms = e->e->time_batch(B, iters);
+    });
+}
 
 }  // extern "C"

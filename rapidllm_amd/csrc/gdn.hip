@@ -263,6 +263,7 @@ struct GdnFusedArgs {
     i32x4* frag;         // out_proj input fragments (may be null)
     float* gss;          // [nv][T][4] partial sums of o^2 (with frag)
     GdnRecords rec;      // rec.rec == nullptr: no records (direct mode)
+    GdnBatch batch;
 };
 
 __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
@@ -281,6 +282,14 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const int qdim = p.nk * kDK;
     const int T = p.T;
     constexpr int K = kConvK;
+    // sequence of the batch: state / ring / records / scalars at its strides, its
+    // tokens are rows row0 .. row0 + T - 1 of T_tot
+    const int bs = blockIdx.y;
+    const int T_tot = a.batch.B * T, row0 = bs * T;
+    const float* S_in = p.S_in + bs * a.batch.s_stride;
+    float* S_out = p.S_out + bs * a.batch.s_stride;
+    const float* conv_base = p.conv_in + bs * a.batch.conv_stride;
+    const int* cur = p.cur ? p.cur + bs * a.batch.scal_stride : nullptr;
 
     __shared__ float q_s[kMaxT][kDK];   // conv outputs (q, k not yet normalised)
     __shared__ float k_s[kMaxT][kDK];
@@ -293,13 +302,13 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     __shared__ float rd_s[kMaxT][kCW];
     __shared__ float rg_s[kMaxT];
 
-    const int slot0 = p.cur ? *p.cur : 0;
-    const float* conv_in = p.cur ? p.conv_in + static_cast<size_t>(slot0) * p.conv_slot : p.conv_in;
+    const int slot0 = cur ? *cur : 0;
+    const float* conv_in = cur ? conv_base + static_cast<size_t>(slot0) * p.conv_slot : conv_base;
     auto conv_dst = [&](int t) -> float* {
-        return p.cur ? const_cast<float*>(p.conv_in) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.conv_slot
-                     : p.conv_out;
+        return cur ? const_cast<float*>(conv_base) + static_cast<size_t>((slot0 + 1 + t) % p.R) * p.conv_slot
+                   : p.conv_out + bs * a.batch.conv_stride;
     };
-    const bool per_token = p.cur != nullptr;
+    const bool per_token = cur != nullptr;
 
     // ---- loads, in the order they are needed (vector loads complete in order):
     // conv inputs of this thread's channels (tid: q/k channel; tid < 32 also v
@@ -324,8 +333,8 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         w1[0] = b1.x, w1[1] = b1.y, w1[2] = b1.z, w1[3] = b1.w;
 #pragma unroll
         for (int t = 0; t < kMaxT; ++t) {
-            xin0[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan0] : 0.f;
-            xin1[t] = t < T ? p.qkv[static_cast<size_t>(t) * p.ld_in + chan1] : 0.f;
+            xin0[t] = t < T ? p.qkv[static_cast<size_t>(row0 + t) * p.ld_in + chan0] : 0.f;
+            xin1[t] = t < T ? p.qkv[static_cast<size_t>(row0 + t) * p.ld_in + chan1] : 0.f;
         }
     }
     // gate inputs: lane e = 16t + 8(b) + s holds slice s of a (or b) of token t; the 8
@@ -335,7 +344,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     if (gate_lane) {
         const int t = tid >> 4, sl = tid & 7;
         const float* src = (tid & 8) ? p.b : p.a;
-        if (sl < p.ab_slices) gin = src[(static_cast<size_t>(sl) * T + t) * p.ab_ld + h];
+        if (sl < p.ab_slices) gin = src[(static_cast<size_t>(sl) * T_tot + row0 + t) * p.ab_ld + h];
         gin_A = p.A_log[h];
         gin_dt = p.dt_bias[h];
     }
@@ -345,7 +354,8 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     if (gn) {
         gam = a.gamma[j];
 #pragma unroll
-        for (int t = 0; t < kMaxT; ++t) zt[t] = t < T ? a.z[static_cast<size_t>(t) * p.ld_in + h * dv + j] : 0.f;
+        for (int t = 0; t < kMaxT; ++t)
+            zt[t] = t < T ? a.z[static_cast<size_t>(row0 + t) * p.ld_in + h * dv + j] : 0.f;
     }
     // state: 16 rows of column j (64 contiguous bytes of the transposed layout)
     const size_t s_off = (static_cast<size_t>(h) * dv + j) * kDK + kCRows * c;
@@ -355,7 +365,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         // caches, so the stores stream out instead of dirtying cached lines that a
         // later kernel's loads would have to evict (measured: the following
         // attention kernel ran ~4 us slower with cached state lines)
-        const f32x4* sp = reinterpret_cast<const f32x4*>(p.S_in + s_off);
+        const f32x4* sp = reinterpret_cast<const f32x4*>(S_in + s_off);
 #pragma unroll
         for (int r = 0; r < kCRows / 4; ++r) {
             const f32x4 v = __builtin_nontemporal_load(sp + r);
@@ -368,13 +378,15 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     // records: bank *cur is written, the previous call's bank is read
     const bool records = a.rec.rec != nullptr;
     const bool keep = records && a.rec.keep;
-    const int n_cons = records ? *a.rec.n_cons : 0;
+    float* rec_base = records ? a.rec.rec + bs * a.batch.rec_stride : nullptr;
+    int* count = records ? a.rec.count + bs * a.batch.count_stride : nullptr;
+    const int n_cons = records ? a.rec.n_cons[bs * a.batch.scal_stride] : 0;
     const int rbank = records ? ((slot0 - n_cons) % p.R + p.R) % p.R : 0;
-    const int n_rep = records ? min(min(n_cons, a.rec.count[rbank * p.nv + h]), kMaxT) : 0;
+    const int n_rep = records ? min(min(n_cons, count[rbank * p.nv + h]), kMaxT) : 0;
     const size_t rec_t = static_cast<size_t>(p.nv) * kGdnRecFloats;  // token stride
     const size_t bank = static_cast<size_t>(a.rec.max_t) * rec_t;
-    const float* rec_r = records ? a.rec.rec + rbank * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
-    float* rec_w = records ? a.rec.rec + slot0 * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
+    const float* rec_r = records ? rec_base + rbank * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
+    float* rec_w = records ? rec_base + slot0 * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
     float rk[kMaxT / 2], rd = 0.f, rg = 0.f;  // thread (t = tid / 128, i): two tokens per thread
 #pragma unroll
     for (int q = 0; q < kMaxT / 2; ++q) {
@@ -457,7 +469,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         for (int r = 0; r < kCRows; ++r) S[r] = __fmaf_rn(rk_s[t][kCRows * c + r], delta, __fmul_rn(S[r], g));
     }
     auto store_state = [&] {
-        f32x4* dp = reinterpret_cast<f32x4*>(p.S_out + s_off);
+        f32x4* dp = reinterpret_cast<f32x4*>(S_out + s_off);
 #pragma unroll
         for (int r = 0; r < kCRows / 4; ++r)
             __builtin_nontemporal_store(f32x4{S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]}, dp + r);
@@ -497,7 +509,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         }
         const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
         if (c == 0) {
-            if (p.o) p.o[static_cast<size_t>(t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
+            if (p.o) p.o[static_cast<size_t>(row0 + t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
             if (keep) rec_w[t * rec_t + kDK + j] = delta;
             if (gn) {
                 o_s[t][jj] = ov;
@@ -506,7 +518,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         }
     }
     if (!keep) store_state();
-    if (records && cc == 0 && tid == 0) a.rec.count[slot0 * p.nv + h] = keep ? T : 0;
+    if (records && cc == 0 && tid == 0) count[slot0 * p.nv + h] = keep ? T : 0;
     if (!a.frag) return;
 
     // ---- per token: the chunk's sum of o^2 (double; 16-lane rows, then the row
@@ -517,15 +529,15 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         const double v = t < T ? static_cast<double>(o_s[t][i]) * o_s[t][i] : 0.0;
         const double r = group16_sum_d(v);
         const double s0 = readlane_d(r, 0) + readlane_d(r, 16), s1 = readlane_d(r, 32) + readlane_d(r, 48);
-        if (lane == 0) a.gss[(static_cast<size_t>(h) * T + t) * 4 + cc] = static_cast<float>(s0);
-        if (lane == 32 && t < T) a.gss[(static_cast<size_t>(h) * T + t) * 4 + cc] = static_cast<float>(s1);
+        if (lane == 0) a.gss[(static_cast<size_t>(h) * T_tot + row0 + t) * 4 + cc] = static_cast<float>(s0);
+        if (lane == 32 && t < T) a.gss[(static_cast<size_t>(h) * T_tot + row0 + t) * 4 + cc] = static_cast<float>(s1);
     }
     if (tid < T * (kCW / 8)) {
         const int t = tid / (kCW / 8), u = tid % (kCW / 8);
         float v[8];
 #pragma unroll
         for (int e = 0; e < 8; ++e) v[e] = y_s[t][8 * u + e];
-        write_frag8(a.frag, (h * dv + cc * kCW) / 8 + u, t, T, v);
+        write_frag8(a.frag, (h * dv + cc * kCW) / 8 + u, row0 + t, T_tot, v);
     }
 }
 
@@ -540,7 +552,7 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices,
-                      int ab_ld) {
+                      int ab_ld, const GdnBatch* batch) {
     RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED,
                "gdn_decode_fused: dk 128, dv a multiple of 32, conv 4");
     RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: T must be in 1..8");
@@ -563,8 +575,11 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                    gamma,
                    static_cast<i32x4*>(frag),
                    gss,
-                   rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0, 0}};
-    hipLaunchKernelGGL(gdn_fused_kernel, dim3(nv * (dv / kCW)), dim3(kCT), 0, s, p);
+                   rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0, 0},
+                   batch ? *batch : GdnBatch{}};
+    RL_REQUIRE(p.batch.B >= 1 && p.batch.B * T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: batch x T must be <= 8");
+    RL_REQUIRE(p.batch.B == 1 || cur, RL_ERR_RANGE, "gdn_decode_fused: a batch needs the conv ring");
+    hipLaunchKernelGGL(gdn_fused_kernel, dim3(nv * (dv / kCW), p.batch.B), dim3(kCT), 0, s, p);
     check_launch("gdn_fused_kernel");
 }
 

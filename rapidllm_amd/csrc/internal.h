@@ -100,6 +100,14 @@ struct GdnRecords {
     int max_t;           // token capacity of a bank
     int keep;            // record this call's tokens instead of committing them
 };
+// Batch of independent sequences (grid dimension y): sequence b's state, conv ring,
+// records and scalars sit at the given strides from sequence 0's; its T tokens are
+// input / output rows b * T + t of B * T.
+struct GdnBatch {
+    int B = 1;
+    size_t s_stride = 0, conv_stride = 0, rec_stride = 0;  // floats
+    int count_stride = 0, scal_stride = 0;                // ints
+};
 // Workgroup = (v-head, 32 value columns).  conv window: a ring of R slots when
 // cur != nullptr (slot *cur read, slot (*cur + 1 + t) % R written after token t),
 // else conv_in -> conv_out.  S: S_in -> S_out (may alias); with cur, rec must be
@@ -115,17 +123,21 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices = 1,
-                      int ab_ld = 0);
+                      int ab_ld = 0, const GdnBatch* batch = nullptr);
 
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);
+// Outputs of token t go to column t_off + t of T_out (T_out 0: T), so one sequence
+// of a batch can write its column of the next linear's input.
 void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,
                        int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot, float theta, float eps,
-                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s);
+                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s, int t_off = 0,
+                       int T_out = 0);
 
 // sample.hip
 size_t argmax_workspace_bytes(int rows, int V);
 void argmax_rows(const float* logits, int rows, int V, int* out, float* out_val, void* ws, hipStream_t s);
+void batch_advance(int* scal, int stride, int B, int R, int k_pos, int k_slot, int k_ncons, hipStream_t s);
 void accept(const int* toks, const int* preds, int T, int force_all, int* pos, int* slot, int R, int* n_out,
             int* next_tok, int* gen_ring, int* gen_count, int gen_cap, const float* xout, float* h_last,
             float* h_prev, int H, hipStream_t s);

@@ -169,9 +169,26 @@ __global__ __launch_bounds__(256) void accept_kernel(AcceptArgs a) {
     }
 }
 
+// Batch decode: every sequence consumed its one token.  Slot b's scalar block
+// (stride ints): position += 1, conv-ring slot += 1 (mod R), consumed = 1.
+__global__ void batch_advance_kernel(int* scal, int stride, int B, int R, int k_pos, int k_slot, int k_ncons) {
+    const int b = threadIdx.x;
+    if (b >= B) return;
+    int* sb = scal + static_cast<size_t>(b) * stride;
+    sb[k_pos] += 1;
+    sb[k_slot] = (sb[k_slot] + 1) % R;
+    sb[k_ncons] = 1;
+}
+
 }  // namespace
 
 namespace rl {
+
+void batch_advance(int* scal, int stride, int B, int R, int k_pos, int k_slot, int k_ncons, hipStream_t s) {
+    RL_REQUIRE(B >= 1 && B <= 64, RL_ERR_RANGE, "batch_advance: bad batch");
+    hipLaunchKernelGGL(batch_advance_kernel, dim3(1), dim3(64), 0, s, scal, stride, B, R, k_pos, k_slot, k_ncons);
+    check_launch("batch_advance_kernel");
+}
 
 size_t argmax_workspace_bytes(int rows, int V) {
     const size_t nch = (static_cast<size_t>(V) + kArgChunk - 1) / kArgChunk;

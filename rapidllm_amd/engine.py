@@ -3,7 +3,9 @@
 
 Method names and meaning follow the reference: prefill, decode_token,
 decode_steps, copy_gen_tokens, copy_logits, copy_last_hidden, mtp_draft,
-spec_verify (returns n_consumed; preds[i] = greedy after toks[i]), greedy, pos.
+spec_verify (returns n_consumed; preds[i] = greedy after toks[i]), greedy, pos,
+and the continuous-batch calls max_batch, decode_tokens, copy_logits_n,
+copy_greedy_n, replicate_slot0, zero_slots, prefill_slot (cuda_engine.h:46-66).
 """
 from __future__ import annotations
 
@@ -18,16 +20,16 @@ from .model import ModelSpec, WeightTable
 
 class Engine:
     def __init__(self, spec: ModelSpec, weights: WeightTable | None = None, ctx: int = 4096, max_T: int = 4,
-                 seed: int = 0):
+                 seed: int = 0, max_batch: int = 1):
         L = hip.lib()
         self.spec = spec
         self._cfg = spec.c_config()
         st = C.c_int(0)
         if weights is None:
-            h = L.rl_hip_engine_create_synthetic(C.byref(self._cfg), seed, ctx, max_T, C.byref(st))
+            h = L.rl_hip_engine_create_synthetic_batch(C.byref(self._cfg), seed, ctx, max_T, max_batch, C.byref(st))
         else:
             arr, n = weights.c_array()
-            h = L.rl_hip_engine_create(C.byref(self._cfg), arr, n, ctx, max_T, C.byref(st))
+            h = L.rl_hip_engine_create_batch(C.byref(self._cfg), arr, n, ctx, max_T, max_batch, C.byref(st))
         if not h:
             raise hip.HipError("rl_hip_engine_create", st.value, L.rl_hip_last_error().decode(errors="replace"))
         self.h = h
@@ -141,3 +143,64 @@ class Engine:
             else:
                 self.decode_token(t0)
         return out[:max_new], proposed, accepted
+
+    # ---- continuous batch (cuda_engine.h:46-66)
+    def max_batch(self) -> int:
+        b = C.c_int()
+        call("rl_hip_engine_max_batch", self.h, C.byref(b))
+        return b.value
+
+    def decode_tokens(self, tokens, poss):
+        tokens = np.ascontiguousarray(tokens, np.int32)
+        poss = np.ascontiguousarray(poss, np.int32)
+        assert tokens.size == poss.size
+        call("rl_hip_engine_decode_tokens", self.h, tokens.ctypes.data, poss.ctypes.data, tokens.size)
+
+    def copy_logits_n(self, B: int) -> np.ndarray:
+        out = np.empty((B, self.vocab), np.float32)
+        call("rl_hip_engine_copy_logits_n", self.h, out.ctypes.data, B)
+        return out
+
+    def copy_greedy_n(self, B: int) -> list:
+        out = np.zeros(B, np.int32)
+        call("rl_hip_engine_copy_greedy_n", self.h, out.ctypes.data, B)
+        return [int(v) for v in out]
+
+    def replicate_slot0(self, n_slots: int):
+        call("rl_hip_engine_replicate_slot0", self.h, n_slots)
+
+    def zero_slots(self, n_slots: int):
+        call("rl_hip_engine_zero_slots", self.h, n_slots)
+
+    def prefill_slot(self, ids, slot: int):
+        ids = np.ascontiguousarray(ids, np.int32)
+        call("rl_hip_engine_prefill_slot", self.h, ids.ctypes.data, ids.size, slot)
+
+    def time_batch(self, B: int, iters: int) -> float:
+        ms = C.c_float()
+        call("rl_hip_engine_time_batch", self.h, B, iters, C.byref(ms))
+        return ms.value
+
+    def generate_batch(self, prompts, max_new: int):
+        """Session::generate_batch (src/runtime/session.cpp:832-964) for unequal or
+        distinct prompts: prefill each sequence into its slot, then one decode_tokens
+        per step for the sequences still running."""
+        B = len(prompts)
+        assert 1 <= B <= self.max_batch()
+        outs, toks, poss = [], [], []
+        for b, p in enumerate(prompts):
+            self.prefill_slot(p, b)
+            t0 = int(np.argmax(self.copy_logits()))
+            outs.append([t0])
+            toks.append(t0)
+            poss.append(len(p))
+        while min(len(o) for o in outs) < max_new:
+            self.decode_tokens(toks, poss)
+            nxt = self.copy_greedy_n(B)
+            for b in range(B):
+                poss[b] += 1
+                toks[b] = nxt[b]
+                if len(outs[b]) < max_new:
+                    outs[b].append(nxt[b])
+        return outs
+

@@ -85,6 +85,16 @@ _SIGS = {
     "rl_hip_engine_synthetic_context": (_i, [_vp, _i, C.c_uint64]),
     "rl_hip_engine_time_steps": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
     "rl_hip_engine_stream": (_vp, [_vp]),
+    "rl_hip_engine_create_batch": (_vp, [_vp, _vp, _i, _i, _i, _i, C.POINTER(_i)]),
+    "rl_hip_engine_create_synthetic_batch": (_vp, [_vp, C.c_uint64, _i, _i, _i, C.POINTER(_i)]),
+    "rl_hip_engine_max_batch": (_i, [_vp, C.POINTER(_i)]),
+    "rl_hip_engine_decode_tokens": (_i, [_vp, _vp, _vp, _i]),
+    "rl_hip_engine_copy_logits_n": (_i, [_vp, _vp, _i]),
+    "rl_hip_engine_copy_greedy_n": (_i, [_vp, _vp, _i]),
+    "rl_hip_engine_replicate_slot0": (_i, [_vp, _i]),
+    "rl_hip_engine_zero_slots": (_i, [_vp, _i]),
+    "rl_hip_engine_prefill_slot": (_i, [_vp, _vp, _i, _i]),
+    "rl_hip_engine_time_batch": (_i, [_vp, _i, _i, C.POINTER(C.c_float)]),
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
     "rl_hip_time_gemm_fp8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
