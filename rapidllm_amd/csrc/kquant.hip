@@ -17,6 +17,9 @@
 // All 64 lanes of a wave work on the same super-block at the same time, so the
 // activation element multiplying every lane's weight is the same: x is read with
 // scalar loads into SGPRs and used directly as the FMA operand (no LDS, no VGPRs).
+#include <algorithm>
+#include <cstdlib>
+
 #include "internal.h"
 
 using namespace rl;
@@ -63,9 +66,11 @@ __device__ inline void q4k_scale_min(const uint8_t* s12, int j, int& sc, int& mn
 }
 
 // One super-block of one row (this lane), accumulated into y[t].
+// xs32: sums of x over the 32-element sub-blocks of this workgroup's K-slice
+// (sub-block sbl*8 + j of token t at xs32[t * xs_ld + sbl*8 + j]).
 template <int T>
-__device__ inline void q4k_block(const i32x4 (&c)[16], const float* __restrict__ x, const float* __restrict__ xs32,
-                                 int n, int sb, float (&y)[4]) {
+__device__ inline void q4k_block(const i32x4 (&c)[16], const float* __restrict__ x, const float* xs32, int xs_ld,
+                                 int n, int sb, int sbl, float (&y)[4]) {
     union {
         i32x4 v;
         uint8_t b[16];
@@ -73,7 +78,6 @@ __device__ inline void q4k_block(const i32x4 (&c)[16], const float* __restrict__
     hdr.v = c[0];
     const float d = half_bits_to_f32(hdr.b[0] | (hdr.b[1] << 8));
     const float dmin = half_bits_to_f32(hdr.b[2] | (hdr.b[3] << 8));
-    const int n_sub = n / 32;
 #pragma unroll
     for (int grp = 0; grp < 4; ++grp) {
         int s0, m0, s1, m1;
@@ -98,24 +102,24 @@ __device__ inline void q4k_block(const i32x4 (&c)[16], const float* __restrict__
         }
         const float a0 = d * static_cast<float>(s0), b0 = dmin * static_cast<float>(m0);
         const float a1 = d * static_cast<float>(s1), b1 = dmin * static_cast<float>(m1);
-        const int j0 = sb * 8 + 2 * grp;
+        const int j0 = sbl * 8 + 2 * grp;
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const float* st = xs32 + static_cast<size_t>(t) * n_sub + j0;
+            const float* st = xs32 + t * xs_ld + j0;
             y[t] += a0 * acc_lo[t] - b0 * st[0] + a1 * acc_hi[t] - b1 * st[1];
         }
     }
 }
 
+// xs16: sums of x over the 16-element sub-blocks of the K-slice (as q4k_block).
 template <int T>
-__device__ inline void q6k_block(const i32x4 (&c)[16], float d, const float* __restrict__ x,
-                                 const float* __restrict__ xs16, int n, int sb, float (&y)[4]) {
+__device__ inline void q6k_block(const i32x4 (&c)[16], float d, const float* __restrict__ x, const float* xs16,
+                                 int xs_ld, int n, int sb, int sbl, float (&y)[4]) {
     union {
         i32x4 v;
         int8_t b[16];
     } scb;
     scb.v = c[12];
-    const int n_sub = n / 16;
 #pragma unroll
     for (int half = 0; half < 2; ++half) {
 #pragma unroll
@@ -149,23 +153,37 @@ __device__ inline void q6k_block(const i32x4 (&c)[16], float d, const float* __r
 #pragma unroll
             for (int k = 0; k < 4; ++k) {
                 const float a = d * static_cast<float>(scb.b[8 * half + l16 + 2 * k]);
-                const int j = sb * 16 + 8 * half + 2 * k + l16;
+                const int j = sbl * 16 + 8 * half + 2 * k + l16;
 #pragma unroll
-                for (int t = 0; t < T; ++t) y[t] += a * (acc[k][t] - 32.f * xs16[static_cast<size_t>(t) * n_sub + j]);
+                for (int t = 0; t < T; ++t) y[t] += a * (acc[k][t] - 32.f * xs16[t * xs_ld + j]);
             }
         }
     }
 }
 
+// Split-K tickets: one counter per row group, 64 bytes apart (atomics on one cache
+// line serialise).  Zero at load; the workgroup that takes a group's last ticket
+// resets it, so every launch finds them zero.  Launches on one device must not
+// overlap in time (they share the counters).
+constexpr int kKqMaxGroups = 4096;
+__device__ unsigned g_kq_ticket[kKqMaxGroups * 16];
+
 // Grid: blockIdx.x = row-group * S + k-slice; KS waves per workgroup split the
-// slice's super-blocks.  S == 1: the workgroup writes Y (store or add);
-// S > 1: it writes partial[slice][t][row] and kq_reduce finishes.
+// slice's super-blocks.  The sub-block sums of x that the min / offset terms need
+// are computed per workgroup for its slice, into LDS (summed in double, as
+// written by ops.cpp's dot of the dequantised block).  S == 1: the workgroup writes
+// Y (store or add).  S > 1: it writes partial[slice][t][row] and takes a ticket;
+// the last workgroup of the row group adds the S partials in slice order (a fixed
+// order) and writes Y.  Partials and tickets use agent-scope atomic accesses,
+// which are coherent across the XCDs' L2 caches without cache maintenance.
 template <int QT, int T, int KS>
 __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                          const float* __restrict__ xs, float* __restrict__ Y,
-                                                          float* __restrict__ partial, int m, int n, int S,
-                                                          int accumulate, int ldy) {
+                                                          float* __restrict__ Y, float* __restrict__ partial, int m,
+                                                          int n, int S, int accumulate, int ldy) {
     using F = KFmt<QT>;
+    constexpr int kSubPerSb = QT == 4 ? 8 : 16;
+    constexpr int kSubLen = 256 / kSubPerSb;
+    extern __shared__ float xs_l[];  // [T][per_slice * kSubPerSb]
     const int lane = threadIdx.x & 63;
     // wave index is uniform: make that visible so the super-block loop (and the x
     // addresses derived from it) stay scalar
@@ -177,6 +195,7 @@ __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restr
     const int s0 = min(nsb, slice * per_slice), s1 = min(nsb, s0 + per_slice);
     const int per = (s1 - s0 + KS - 1) / KS;
     const int b0 = min(s1, s0 + wave * per), b1 = min(s1, b0 + per);
+    const int xs_ld = per_slice * kSubPerSb;
 
     float y[4] = {0.f, 0.f, 0.f, 0.f};
     const uint8_t* rowtiles = W + static_cast<size_t>(rg) * nsb * F::kTileBytes;
@@ -191,13 +210,32 @@ __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restr
             c[15] = i32x4{static_cast<int>(dh), 0, 0, 0};
         }
     };
+    // the first weights are requested before the slice's x sums are formed
     if (b0 < b1) load(b0, cur);
+    {
+        const int nsub = (s1 - s0) * kSubPerSb;
+        for (int i = threadIdx.x; i < T * nsub; i += 64 * KS) {
+            const int t = i / nsub, j = i % nsub;
+            const float* p = x + static_cast<size_t>(t) * n + static_cast<size_t>(s0) * 256 + j * kSubLen;
+            double acc = 0.0;
+#pragma unroll
+            for (int e = 0; e < kSubLen; e += 4) {
+                const float4 v = *reinterpret_cast<const float4*>(p + e);
+                acc += v.x;
+                acc += v.y;
+                acc += v.z;
+                acc += v.w;
+            }
+            xs_l[t * xs_ld + j] = static_cast<float>(acc);
+        }
+    }
+    __syncthreads();
     for (int sb = b0; sb < b1; ++sb) {
         if (sb + 1 < b1) load(sb + 1, nxt);
         if constexpr (QT == 4)
-            q4k_block<T>(cur, x, xs, n, sb, y);
+            q4k_block<T>(cur, x, xs_l, xs_ld, n, sb, sb - s0, y);
         else
-            q6k_block<T>(cur, half_bits_to_f32(static_cast<uint32_t>(cur[15][0])), x, xs, n, sb, y);
+            q6k_block<T>(cur, half_bits_to_f32(static_cast<uint32_t>(cur[15][0])), x, xs_l, xs_ld, n, sb, sb - s0, y);
         if (sb + 1 < b1) {
 #pragma unroll
             for (int k = 0; k < F::kChunks; ++k) cur[k] = nxt[k];
@@ -206,9 +244,48 @@ __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restr
     }
 
     __shared__ float red[KS][4][64];
+    __shared__ int s_last;
 #pragma unroll
     for (int t = 0; t < 4; ++t) red[wave][t][lane] = y[t];
     __syncthreads();
+    if (S > 1) {
+        for (int it = threadIdx.x; it < T * kRows; it += 64 * KS) {
+            const int t = it / kRows, l = it % kRows;
+            const int row = rg * kRows + l;
+            if (row >= m) continue;
+            float s = 0.f;
+#pragma unroll
+            for (int w = 0; w < KS; ++w) s += red[w][t][l];
+            __hip_atomic_store(partial + (static_cast<size_t>(slice) * T + t) * m + row, s, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
+        }
+        asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete before the ticket
+        __syncthreads();
+        if (threadIdx.x == 0) {
+            unsigned* tk = g_kq_ticket + static_cast<size_t>(rg) * 16;
+            const unsigned old = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            const int last = old == static_cast<unsigned>(S - 1);
+            if (last) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+            s_last = last;
+        }
+        __syncthreads();
+        if (!s_last) return;
+        for (int it = threadIdx.x; it < T * kRows; it += 64 * KS) {
+            const int t = it / kRows, l = it % kRows;
+            const int row = rg * kRows + l;
+            if (row >= m) continue;
+            float s = 0.f;
+            for (int q = 0; q < S; ++q)
+                s += __hip_atomic_load(partial + (static_cast<size_t>(q) * T + t) * m + row, __ATOMIC_RELAXED,
+                                       __HIP_MEMORY_SCOPE_AGENT);
+            float* dst = Y + static_cast<size_t>(t) * ldy + row;
+            if (accumulate)
+                *dst += s;
+            else
+                *dst = s;
+        }
+        return;
+    }
     for (int it = threadIdx.x; it < T * kRows; it += 64 * KS) {
         const int t = it / kRows, l = it % kRows;
         const int row = rg * kRows + l;
@@ -216,45 +293,10 @@ __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restr
         float s = 0.f;
 #pragma unroll
         for (int w = 0; w < KS; ++w) s += red[w][t][l];
-        if (S > 1)
-            partial[(static_cast<size_t>(slice) * T + t) * m + row] = s;
-        else if (accumulate)
+        if (accumulate)
             Y[static_cast<size_t>(t) * ldy + row] += s;
         else
             Y[static_cast<size_t>(t) * ldy + row] = s;
-    }
-}
-
-__global__ void kq_reduce_kernel(const float* __restrict__ partial, float* __restrict__ Y, int m, int T, int S,
-                                 int accumulate, int ldy) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i >= T * m) return;
-    float s = 0.f;
-    for (int q = 0; q < S; ++q) s += partial[static_cast<size_t>(q) * T * m + i];
-    float* dst = Y + static_cast<size_t>(i / m) * ldy + i % m;
-    if (accumulate)
-        *dst += s;
-    else
-        *dst = s;
-}
-
-// Sums of x over 16- and 32-element sub-blocks: xs16 [T][n/16] then xs32 [T][n/32].
-__global__ void kq_xsum_kernel(const float* __restrict__ x, float* __restrict__ xs, int n, int T) {
-    const int n16 = n / 16, n32 = n / 32;
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < T * n16) {
-        const int t = i / n16, j = i % n16;
-        const float* p = x + static_cast<size_t>(t) * n + 16 * j;
-        double s = 0.0;
-        for (int e = 0; e < 16; ++e) s += p[e];
-        xs[i] = static_cast<float>(s);
-    } else if (i < T * n16 + T * n32) {
-        const int k = i - T * n16;
-        const int t = k / n32, j = k % n32;
-        const float* p = x + static_cast<size_t>(t) * n + 32 * j;
-        double s = 0.0;
-        for (int e = 0; e < 32; ++e) s += p[e];
-        xs[i] = static_cast<float>(s);
     }
 }
 
@@ -334,30 +376,40 @@ size_t kq_tiled_bytes(int qt, int m, int n) {
     return static_cast<size_t>((m + kRows - 1) / kRows) * (n / 256) * tile;
 }
 
-// Work split: keep >= ~512 workgroups where the row groups alone are too few.
-void kq_split(int m, int nsb, int& S, int& KS) {
+// Work split: keep >= ~512 workgroups where the row groups alone are too few, and
+// the slice's x sums within 32 KiB of LDS.
+constexpr size_t kKqXsLds = 32768;
+size_t kq_xs_bytes(int qt, int nsb, int S, int T) {
+    return static_cast<size_t>(T) * ((nsb + S - 1) / S) * (qt == 4 ? 8 : 16) * sizeof(float);
+}
+void kq_split(int qt, int m, int nsb, int T, int& S, int& KS) {
     const int groups = (m + kRows - 1) / kRows;
     KS = 4;
     S = 1;
     while (groups * S < 512 && nsb / (S * 2) >= 4) S *= 2;
+    while (kq_xs_bytes(qt, nsb, S, T) > kKqXsLds) S *= 2;
+    static const char* env = std::getenv("RL_KQ_SPLIT");  // measurement override "S"
+    if (env && std::atoi(env) > 0) S = std::atoi(env);
+    S = std::min(S, nsb);
 }
 
 template <int QT, int T>
-void launch_kq_t(const uint8_t* W, const float* x, const float* xs, float* Y, float* partial, int m, int n, int S,
-                 int accumulate, int ldy, hipStream_t s) {
+void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int S, int accumulate,
+                 int ldy, hipStream_t s) {
     const int groups = (m + kRows - 1) / kRows;
-    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, 4>), dim3(groups * S), dim3(256), 0, s, W, x, xs, Y, partial, m, n, S,
+    const size_t lds = kq_xs_bytes(QT, n / 256, S, T);
+    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, 4>), dim3(groups * S), dim3(256), lds, s, W, x, Y, partial, m, n, S,
                        accumulate, ldy);
 }
 
 template <int QT>
-void launch_kq(const uint8_t* W, const float* x, const float* xs, float* Y, float* partial, int m, int n, int T,
-               int S, int accumulate, int ldy, hipStream_t s) {
+void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int T, int S, int accumulate,
+               int ldy, hipStream_t s) {
     switch (T) {
-    case 1: launch_kq_t<QT, 1>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
-    case 2: launch_kq_t<QT, 2>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
-    case 3: launch_kq_t<QT, 3>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
-    default: launch_kq_t<QT, 4>(W, x, xs, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    default: launch_kq_t<QT, 4>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
     }
 }
 
@@ -366,10 +418,12 @@ void launch_kq(const uint8_t* W, const float* x, const float* xs, float* Y, floa
 namespace rl {
 
 size_t kq_workspace_bytes(int m, int n, int T) {
-    int S, KS;
-    kq_split(m, n / 256, S, KS);
-    // sums: T*(n/16 + n/32) floats; partials: S*T*m floats
-    return (static_cast<size_t>(T) * (n / 16 + n / 32) + (S > 1 ? static_cast<size_t>(S) * T * m : 0)) * 4 + 256;
+    // partials for the largest split either type uses: S*T*m floats
+    int S4, S6, KS;
+    kq_split(4, m, n / 256, T, S4, KS);
+    kq_split(6, m, n / 256, T, S6, KS);
+    const int S = std::max(S4, S6);
+    return (S > 1 ? static_cast<size_t>(S) * T * m : 0) * 4 + 256;
 }
 
 // Y[T][m] (=, +=) W . x for Q4_K (qt=4) / Q6_K (qt=6) K-tiled weights.
@@ -381,23 +435,15 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     RL_REQUIRE(W && x && Y && ws, RL_ERR_RANGE, "kquant: null pointer");
     RL_REQUIRE(ws_bytes >= kq_workspace_bytes(m, n, T), RL_ERR_RANGE, "kquant: workspace too small");
     int S, KS;
-    kq_split(m, n / 256, S, KS);
-    float* xs = static_cast<float*>(ws);
-    float* partial = xs + static_cast<size_t>(T) * (n / 16 + n / 32);
-    const int nsum = T * (n / 16 + n / 32);
-    hipLaunchKernelGGL(kq_xsum_kernel, dim3((nsum + 255) / 256), dim3(256), 0, s, x, xs, n, T);
-    check_launch("kq_xsum_kernel");
-    const float* xs_use = qt == 4 ? xs + static_cast<size_t>(T) * (n / 16) : xs;
+    kq_split(qt, m, n / 256, T, S, KS);
+    RL_REQUIRE(S == 1 || (m + kRows - 1) / kRows <= kKqMaxGroups, RL_ERR_UNSUPPORTED, "kquant: too many rows");
+    RL_REQUIRE(kq_xs_bytes(qt, n / 256, S, T) <= kKqXsLds, RL_ERR_UNSUPPORTED, "kquant: K-slice too long");
+    float* partial = static_cast<float*>(ws);
     if (qt == 4)
-        launch_kq<4>(W, x, xs_use, Y, partial, m, n, T, S, accumulate, ldy, s);
+        launch_kq<4>(W, x, Y, partial, m, n, T, S, accumulate, ldy, s);
     else
-        launch_kq<6>(W, x, xs_use, Y, partial, m, n, T, S, accumulate, ldy, s);
+        launch_kq<6>(W, x, Y, partial, m, n, T, S, accumulate, ldy, s);
     check_launch("kq_gemm_kernel");
-    if (S > 1) {
-        hipLaunchKernelGGL(kq_reduce_kernel, dim3((T * m + 255) / 256), dim3(256), 0, s, partial, Y, m, T, S,
-                           accumulate, ldy);
-        check_launch("kq_reduce_kernel");
-    }
 }
 
 }  // namespace rl
