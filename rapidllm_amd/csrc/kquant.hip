@@ -4,19 +4,33 @@
 //   Q4_K (ops.cpp:245-284): w = (d * sc_j) * q - (dmin * m_j), each product rounded
 //   Q6_K (ops.cpp:357-387): w = (d * sc) * (q - 32)
 // The GEMV (ops.cpp:292-305, 389-402; threaded by cpu_caps.cpp:200-222) is computed
-// in the factorised form sum_j [ (d sc_j) * sum_l q_l x_l - (dmin m_j) * sum_l x_l ]
-// with an fp32 accumulator: the same real number, within the 1e-3 relative-L2
-// budget of the north star.
+// per sub-block j in the factorised form a_j * sum_l q_l x_l - b_j * sum_l x_l with
+// fp32 accumulation: the same real number, within the 1e-3 relative-L2 budget of
+// the north star.
 //
-// Device layout ("K-tiled"): a tile = 64 rows x 1 super-block.  Lane l of a wave
-// owns row 64*rg + l; the 144-byte (Q4_K) / 208+2-byte (Q6_K) block of that row is
-// cut into 16-byte chunks stored chunk-major, lane-minor, so each of the wave's
-// 16-byte loads is one contiguous 1 KiB stream.  The Q6_K fp16 d of the 64 rows
-// follows the 13 chunks.  Bytes are only moved, never re-rounded.
+// The quant dot products run on the matrix cores (v_mfma_f32_16x16x32_bf16):
+//   * a quant q (4 or 6 bits) becomes the bf16 value 128 + q by placing its byte
+//     under the exponent byte 0x43 (one v_perm per two values, exact);
+//   * x is split into bf16 hi + mid parts (16 significant bits, as for the FP8
+//     linears) in LDS; A-operand row 4g + p carries token column p only in the
+//     k-range of lane group g (block-diagonal), so the MFMA returns, in every lane,
+//     the dot product of that lane's own 8 quants with x for up to 4 token
+//     columns -- 32 fp32 products per lane per instruction, no cross-lane sums;
+//   * a lane's 8-quant runs never cross a sub-block, so the four MFMAs of a
+//     32-quant sub-block accumulate in place and the per-(row, sub-block) scale is
+//     applied once: y += a_j * C_j - (128 a_j + b_j) * X_j  (Q4_K), with X_j the
+//     sub-block sum of the split x; Q6_K: y += a_j * C_j - 160 a_j X_j.
 //
-// All 64 lanes of a wave work on the same super-block at the same time, so the
-// activation element multiplying every lane's weight is the same: x is read with
-// scalar loads into SGPRs and used directly as the FMA operand (no LDS, no VGPRs).
+// Device layout: a tile = 16 rows x 1 super-block (256 quants).  Lane l of a wave
+// owns row 16rt + l % 16 and a quarter of the super-block (g = l / 16):
+//   Q4_K: bytes 16+32g .. 16+32g+31 of the block (sub-blocks 2g low nibbles and
+//         2g+1 high nibbles) as two 16-byte chunks, chunk-major and lane-minor (each
+//         wave load is one contiguous 1 KiB run), then the 16 rows' 16-byte headers
+//         (d, dmin, 12 scale bytes): 2304 B = 16 x 144;
+//   Q6_K: ql[64h + 16e .. +16], ql[64h + 32 + 16e .. +16], qh[32h + 16e .. +16]
+//         with h = g / 2, e = g % 2 (three chunks), then the rows' 16 int8 scales
+//         (16 B each) and fp16 d (2 B each): 3360 B = 16 x 210.
+// Bytes are only moved, never re-rounded.
 #include <algorithm>
 #include <cstdlib>
 
@@ -26,32 +40,31 @@ using namespace rl;
 
 namespace {
 
-constexpr int kRows = 64;  // rows per tile (one per lane)
+constexpr int kTR = 16;       // rows per tile
 
 template <int QT>
 struct KFmt;
 template <>
 struct KFmt<4> {
     static constexpr int kBlockBytes = 144;
-    static constexpr int kChunks = 9;
-    static constexpr int kTileBytes = kRows * 144;
+    static constexpr int kChunks = 2;       // 16-byte quant chunks per lane
+    static constexpr int kHdr = 2048;       // offset of the row headers
+    static constexpr int kTileBytes = 2304;
+    static constexpr int kNSub = 8;         // sub-blocks per super-block
+    static constexpr int kSubLen = 32;
 };
 template <>
 struct KFmt<6> {
     static constexpr int kBlockBytes = 210;
-    static constexpr int kChunks = 13;
-    static constexpr int kTileBytes = kRows * 210;
+    static constexpr int kChunks = 3;
+    static constexpr int kHdr = 3072;       // row scales (16 B each), then d (2 B each)
+    static constexpr int kTileBytes = 3360;
+    static constexpr int kNSub = 16;
+    static constexpr int kSubLen = 16;
 };
 
 __device__ inline float half_bits_to_f32(uint32_t h) {
     return static_cast<float>(__builtin_bit_cast(_Float16, static_cast<uint16_t>(h)));
-}
-
-// byte e of a dword as float (the compiler selects v_cvt_f32_ubyte{0..3})
-__device__ inline float ubyte(uint32_t w, int e) { return static_cast<float>((w >> (8 * e)) & 0xffu); }
-
-__device__ inline uint32_t lane_dword(const i32x4 (&c)[16], int byte_off) {
-    return static_cast<uint32_t>(c[byte_off >> 4][(byte_off >> 2) & 3]);
 }
 
 // 6-bit scale and min of sub-block j from the 12 scale bytes (block bytes 4..15).
@@ -65,100 +78,54 @@ __device__ inline void q4k_scale_min(const uint8_t* s12, int j, int& sc, int& mn
     }
 }
 
-// One super-block of one row (this lane), accumulated into y[t].
-// xs32: sums of x over the 32-element sub-blocks of this workgroup's K-slice
-// (sub-block sbl*8 + j of token t at xs32[t * xs_ld + sbl*8 + j]).
-template <int T>
-__device__ inline void q4k_block(const i32x4 (&c)[16], const float* __restrict__ x, const float* xs32, int xs_ld,
-                                 int n, int sb, int sbl, float (&y)[4]) {
-    union {
-        i32x4 v;
-        uint8_t b[16];
-    } hdr;
-    hdr.v = c[0];
-    const float d = half_bits_to_f32(hdr.b[0] | (hdr.b[1] << 8));
-    const float dmin = half_bits_to_f32(hdr.b[2] | (hdr.b[3] << 8));
-#pragma unroll
-    for (int grp = 0; grp < 4; ++grp) {
-        int s0, m0, s1, m1;
-        q4k_scale_min(hdr.b + 4, 2 * grp, s0, m0);
-        q4k_scale_min(hdr.b + 4, 2 * grp + 1, s1, m1);
-        float acc_lo[T], acc_hi[T];
-#pragma unroll
-        for (int t = 0; t < T; ++t) acc_lo[t] = acc_hi[t] = 0.f;
-        const int k0 = sb * 256 + 64 * grp;
-#pragma unroll
-        for (int dw = 0; dw < 8; ++dw) {
-            const uint32_t w = lane_dword(c, 16 + 32 * grp + 4 * dw);
-            const uint32_t lo = w & 0x0f0f0f0fu;
-            const uint32_t hi = (w >> 4) & 0x0f0f0f0fu;
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const float4 xl = *reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + k0 + 4 * dw);
-                const float4 xh = *reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + k0 + 32 + 4 * dw);
-                acc_lo[t] += ubyte(lo, 0) * xl.x + ubyte(lo, 1) * xl.y + ubyte(lo, 2) * xl.z + ubyte(lo, 3) * xl.w;
-                acc_hi[t] += ubyte(hi, 0) * xh.x + ubyte(hi, 1) * xh.y + ubyte(hi, 2) * xh.z + ubyte(hi, 3) * xh.w;
-            }
-        }
-        const float a0 = d * static_cast<float>(s0), b0 = dmin * static_cast<float>(m0);
-        const float a1 = d * static_cast<float>(s1), b1 = dmin * static_cast<float>(m1);
-        const int j0 = sbl * 8 + 2 * grp;
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float* st = xs32 + t * xs_ld + j0;
-            y[t] += a0 * acc_lo[t] - b0 * st[0] + a1 * acc_hi[t] - b1 * st[1];
-        }
-    }
+// q4k_scale_min on the 16 header bytes held in registers (h[1..3] = scale bytes
+// s12[0..11]); j may differ per lane, so bytes are taken by shifts, not by index
+// (an indexed local array would live in scratch memory).
+__device__ inline void q4k_scale_min_reg(const i32x4& h, int j, int& sc, int& mn) {
+    const int sh = 8 * (j & 3);
+    const int b1 = (static_cast<uint32_t>(h[1]) >> sh) & 255;  // s12[j & 3]
+    const int b2 = (static_cast<uint32_t>(h[2]) >> sh) & 255;  // s12[4 + (j & 3)]
+    const int b3 = (static_cast<uint32_t>(h[3]) >> sh) & 255;  // s12[8 + (j & 3)]
+    const bool lo = j < 4;
+    sc = lo ? (b1 & 63) : ((b3 & 15) | ((b1 >> 6) << 4));
+    mn = lo ? (b2 & 63) : ((b3 >> 4) | ((b2 >> 6) << 4));
 }
 
-// xs16: sums of x over the 16-element sub-blocks of the K-slice (as q4k_block).
-template <int T>
-__device__ inline void q6k_block(const i32x4 (&c)[16], float d, const float* __restrict__ x, const float* xs16,
-                                 int xs_ld, int n, int sb, int sbl, float (&y)[4]) {
-    union {
-        i32x4 v;
-        int8_t b[16];
-    } scb;
-    scb.v = c[12];
-#pragma unroll
-    for (int half = 0; half < 2; ++half) {
-#pragma unroll
-        for (int l16 = 0; l16 < 2; ++l16) {
-            float acc[4][T];
-#pragma unroll
-            for (int k = 0; k < 4; ++k)
-#pragma unroll
-                for (int t = 0; t < T; ++t) acc[k][t] = 0.f;
-#pragma unroll
-            for (int dw = 0; dw < 4; ++dw) {
-                const uint32_t qa = lane_dword(c, 64 * half + 16 * l16 + 4 * dw);
-                const uint32_t qb = lane_dword(c, 64 * half + 32 + 16 * l16 + 4 * dw);
-                const uint32_t qh = lane_dword(c, 128 + 32 * half + 16 * l16 + 4 * dw);
-                uint32_t q[4];
-                q[0] = (qa & 0x0f0f0f0fu) | ((qh & 0x03030303u) << 4);
-                q[1] = (qb & 0x0f0f0f0fu) | (((qh >> 2) & 0x03030303u) << 4);
-                q[2] = ((qa >> 4) & 0x0f0f0f0fu) | (((qh >> 4) & 0x03030303u) << 4);
-                q[3] = ((qb >> 4) & 0x0f0f0f0fu) | (((qh >> 6) & 0x03030303u) << 4);
-#pragma unroll
-                for (int k = 0; k < 4; ++k) {
-                    const int kk = sb * 256 + 128 * half + 32 * k + 16 * l16 + 4 * dw;
-#pragma unroll
-                    for (int t = 0; t < T; ++t) {
-                        const float4 xv = *reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + kk);
-                        acc[k][t] += ubyte(q[k], 0) * xv.x + ubyte(q[k], 1) * xv.y + ubyte(q[k], 2) * xv.z +
-                                     ubyte(q[k], 3) * xv.w;
-                    }
-                }
-            }
-#pragma unroll
-            for (int k = 0; k < 4; ++k) {
-                const float a = d * static_cast<float>(scb.b[8 * half + l16 + 2 * k]);
-                const int j = sbl * 16 + 8 * half + 2 * k + l16;
-#pragma unroll
-                for (int t = 0; t < T; ++t) y[t] += a * (acc[k][t] - 32.f * xs16[t * xs_ld + j]);
-            }
-        }
-    }
+// Four quant bytes (each < 128) -> two dwords of bf16 (128 + q): byte b under 0x43.
+__device__ inline void q_to_bf16x4(uint32_t q, uint32_t& lo, uint32_t& hi) {
+    lo = __builtin_amdgcn_perm(0x43434343u, q, 0x04010400u);  // [q0, 43, q1, 43]
+    hi = __builtin_amdgcn_perm(0x43434343u, q, 0x04030402u);  // [q2, 43, q3, 43]
+}
+
+union Frag8 {
+    bf16x8 v;
+    uint32_t u[4];
+    i32x4 i;
+};
+
+// Offset (within the super-block) of the 8 x values multiplying the quants of MFMA
+// mi of lane group g.  Q4_K: mi = 4 * (high nibble) + run; Q6_K: mi = 2 * kk + half.
+template <int QT>
+__device__ inline int x_off(int g, int mi) {
+    if constexpr (QT == 4)
+        return 64 * g + 32 * (mi >> 2) + 8 * (mi & 3);
+    else
+        return 128 * (g >> 1) + 32 * (mi >> 1) + 16 * (g & 1) + 8 * (mi & 1);
+}
+
+// Run (8 values) of MFMA mi within its sub-block, and runs per sub-block.
+template <int QT>
+__device__ inline int run_of(int mi) {
+    return QT == 4 ? (mi & 3) : (mi & 1);
+}
+
+// Sub-block of MFMA mi of lane group g (its scale index).
+template <int QT>
+__device__ inline int sub_of(int g, int mi) {
+    if constexpr (QT == 4)
+        return 2 * g + (mi >> 2);
+    else
+        return 8 * (g >> 1) + 2 * (mi >> 1) + (g & 1);
 }
 
 // Split-K tickets: one counter per row group, 64 bytes apart (atomics on one cache
@@ -168,101 +135,253 @@ __device__ inline void q6k_block(const i32x4 (&c)[16], float d, const float* __r
 constexpr int kKqMaxGroups = 4096;
 __device__ unsigned g_kq_ticket[kKqMaxGroups * 16];
 
-// Grid: blockIdx.x = row-group * S + k-slice; KS waves per workgroup split the
-// slice's super-blocks.  The sub-block sums of x that the min / offset terms need
-// are computed per workgroup for its slice, into LDS (summed in double, as
-// written by ops.cpp's dot of the dequantised block).  S == 1: the workgroup writes
-// Y (store or add).  S > 1: it writes partial[slice][t][row] and takes a ticket;
-// the last workgroup of the row group adds the S partials in slice order (a fixed
+// Target of the pipeline's idle load slots (never written).
+constexpr int kKqDummyWindows = 64;
+__device__ __align__(4096) uint8_t g_kq_dummy[kKqDummyWindows * 4096];
+
+// LDS of a workgroup (K-slice of P super-blocks, NSET token sets of 2 tokens):
+//   afrag[set][sbl][mi][p][g]: 16 B (8 bf16) -- x hi (p even) / mid (p odd) of
+//                              token 2*set + p/2 at x_off(g, mi)
+//   zero16: 16 zero bytes (A operand of the off-diagonal lanes)
+//   xsum[t][sbl][j][run]:      sums of hi + mid over the 8-value runs of sub-block j
+//                              (4 runs for Q4_K, 2 for Q6_K)
+template <int QT>
+__host__ __device__ constexpr int kq_afrag_bytes(int P, int nset) { return nset * P * 8 * 4 * 4 * 16; }
+template <int QT>
+__host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
+    return kq_afrag_bytes<QT>(P, nset) + 16 + T * P * KFmt<QT>::kNSub * (QT == 4 ? 4 : 2) * 4;
+}
+
+// Grid: blockIdx.x = row-group * S + k-slice.  Wave w of the workgroup takes tile
+// row RW * row-group + w over the slice's super-blocks.  S == 1: the workgroup writes
+// Y (store or add).  S > 1: it writes partial[slice][t][row] and takes a ticket; the
+// last workgroup of the row group adds the S partials in slice order (a fixed
 // order) and writes Y.  Partials and tickets use agent-scope atomic accesses,
 // which are coherent across the XCDs' L2 caches without cache maintenance.
-template <int QT, int T, int KS>
-__global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                          float* __restrict__ Y, float* __restrict__ partial, int m,
-                                                          int n, int S, int accumulate, int ldy) {
+template <int QT, int T, int D, int RW>
+__global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
+                                                      float* __restrict__ Y, float* __restrict__ partial, int m,
+                                                      int n, int S, int accumulate, int ldy) {
     using F = KFmt<QT>;
-    constexpr int kSubPerSb = QT == 4 ? 8 : 16;
-    constexpr int kSubLen = 256 / kSubPerSb;
-    extern __shared__ float xs_l[];  // [T][per_slice * kSubPerSb]
+    constexpr int NSET = (T + 1) / 2;  // token sets of two (hi, mid, hi, mid columns)
+    constexpr int kRuns = QT == 4 ? 4 : 2;
+    extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
-    // wave index is uniform: make that visible so the super-block loop (and the x
-    // addresses derived from it) stay scalar
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-    const int rg = blockIdx.x / S;
+    const int g = lane >> 4, r16 = lane & 15;
+    const int rgp = blockIdx.x / S;
     const int slice = blockIdx.x % S;
     const int nsb = n / 256;
     const int per_slice = (nsb + S - 1) / S;
     const int s0 = min(nsb, slice * per_slice), s1 = min(nsb, s0 + per_slice);
-    const int per = (s1 - s0 + KS - 1) / KS;
-    const int b0 = min(s1, s0 + wave * per), b1 = min(s1, b0 + per);
-    const int xs_ld = per_slice * kSubPerSb;
+    const int P = per_slice;
+    const int m_tiles = (m + kTR - 1) / kTR;
+    const int rt = min(rgp * RW + wave, m_tiles - 1);
+    const bool wave_live = rgp * RW + wave < m_tiles;
 
-    float y[4] = {0.f, 0.f, 0.f, 0.f};
-    const uint8_t* rowtiles = W + static_cast<size_t>(rg) * nsb * F::kTileBytes;
-    i32x4 cur[16], nxt[16];
-    auto load = [&](int sb, i32x4 (&c)[16]) {
-        const uint8_t* tile = rowtiles + static_cast<size_t>(sb) * F::kTileBytes;
+    i32x4* afrag = reinterpret_cast<i32x4*>(lds);
+    i32x4* zero16 = reinterpret_cast<i32x4*>(lds + kq_afrag_bytes<QT>(P, NSET));
+    float* xsum = reinterpret_cast<float*>(lds + kq_afrag_bytes<QT>(P, NSET) + 16);
+
+    const uint8_t* tiles = W + static_cast<size_t>(rt) * nsb * F::kTileBytes;
+    // loads per lane per tile: quant chunks, the row's header (Q4_K d, dmin and scale
+    // bytes; Q6_K the 16 int8 scales) and, for Q6_K, the row's fp16 d
+    constexpr int NL = F::kChunks + 1;
+    // D tiles in flight per wave.  Pipeline slots past the slice still issue their
+    // loads (so every wait has a static count), from a zero block that stays in the
+    // caches; each wave reads its own 4 KiB window of it (one shared address would
+    // queue every wave on one L2 channel).
+    i32x4 buf[D][NL];
+    uint32_t dbits[D];
+    const uint8_t* dummy = g_kq_dummy + ((blockIdx.x * RW + wave) % kKqDummyWindows) * 4096;
+    auto load = [&](int d, int sb, bool live) {
+        const uint8_t* tile = live ? tiles + static_cast<size_t>(sb) * F::kTileBytes : dummy;
 #pragma unroll
-        for (int k = 0; k < F::kChunks; ++k)
-            c[k] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(tile + k * 1024 + 16 * lane));
-        if constexpr (QT == 6) {
-            const uint16_t dh = reinterpret_cast<const uint16_t*>(tile + F::kChunks * 1024)[lane];
-            c[15] = i32x4{static_cast<int>(dh), 0, 0, 0};
+        for (int k = 0; k < F::kChunks; ++k) {
+            const i32x4* p = reinterpret_cast<const i32x4*>(tile + k * 1024 + 16 * lane);
+            buf[d][k] = live ? __builtin_nontemporal_load(p) : *p;
         }
+        buf[d][NL - 1] = *reinterpret_cast<const i32x4*>(tile + F::kHdr + 16 * r16);
+        if constexpr (QT == 6) dbits[d] = reinterpret_cast<const uint16_t*>(tile + F::kHdr + 256)[r16];
     };
-    // the first weights are requested before the slice's x sums are formed
-    if (b0 < b1) load(b0, cur);
-    {
-        const int nsub = (s1 - s0) * kSubPerSb;
-        for (int i = threadIdx.x; i < T * nsub; i += 64 * KS) {
-            const int t = i / nsub, j = i % nsub;
-            const float* p = x + static_cast<size_t>(t) * n + static_cast<size_t>(s0) * 256 + j * kSubLen;
-            double acc = 0.0;
+    // the first weights are requested before the slice's x fragments are built
 #pragma unroll
-            for (int e = 0; e < kSubLen; e += 4) {
-                const float4 v = *reinterpret_cast<const float4*>(p + e);
-                acc += v.x;
-                acc += v.y;
-                acc += v.z;
-                acc += v.w;
+    for (int d = 0; d < D; ++d) load(d, s0 + d, s0 + d < s1);
+
+    // ---- x fragments and sub-block sums of this slice
+    {
+        const int nsl = s1 - s0;
+        if (threadIdx.x == 0) *zero16 = i32x4{0, 0, 0, 0};
+        // items (set, sbl, mi, g, token-in-set): 8 x values split into bf16 hi + mid,
+        // and their sum (hi + mid, fixed order) as one run of the sub-block's sum
+        const int items = NSET * P * 8 * 4 * 2;
+        for (int it = threadIdx.x; it < items; it += 64 * RW) {
+            const int tt = it & 1, gg = (it >> 1) & 3, mi = (it >> 3) & 7;
+            const int sbl = (it >> 6) % P, set = (it >> 6) / P;
+            const int t = 2 * set + tt;
+            union {
+                uint16_t h[8];
+                i32x4 v;
+            } hi, mid;
+            float run = 0.f;
+            if (t < T && sbl < nsl) {
+                const float* px = x + static_cast<size_t>(t) * n + static_cast<size_t>(s0 + sbl) * 256 + x_off<QT>(gg, mi);
+                const float4 a = reinterpret_cast<const float4*>(px)[0];
+                const float4 b = reinterpret_cast<const float4*>(px)[1];
+                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+#pragma unroll
+                for (int e = 0; e < 8; ++e) {
+                    split_bf16(v[e], hi.h[e], mid.h[e]);
+                    run += __uint_as_float(static_cast<uint32_t>(hi.h[e]) << 16) +
+                           __uint_as_float(static_cast<uint32_t>(mid.h[e]) << 16);
+                }
+            } else {
+                hi.v = i32x4{0, 0, 0, 0};
+                mid.v = i32x4{0, 0, 0, 0};
             }
-            xs_l[t * xs_ld + j] = static_cast<float>(acc);
+            const int base = (((set * P + sbl) * 8 + mi) * 4) * 4;  // [set][sbl][mi][p][g]
+            afrag[base + (2 * tt) * 4 + gg] = hi.v;
+            afrag[base + (2 * tt + 1) * 4 + gg] = mid.v;
+            if (t < T) xsum[((t * P + sbl) * F::kNSub + sub_of<QT>(gg, mi)) * kRuns + run_of<QT>(mi)] = run;
         }
     }
     __syncthreads();
-    for (int sb = b0; sb < b1; ++sb) {
-        if (sb + 1 < b1) load(sb + 1, nxt);
-        if constexpr (QT == 4)
-            q4k_block<T>(cur, x, xs_l, xs_ld, n, sb, sb - s0, y);
-        else
-            q6k_block<T>(cur, half_bits_to_f32(static_cast<uint32_t>(cur[15][0])), x, xs_l, xs_ld, n, sb, sb - s0, y);
-        if (sb + 1 < b1) {
+
+    // A operand source of this lane: token column p = r16 % 4 of lane group g when
+    // r16 / 4 == g, else the zero block
+    const bool diag = (r16 >> 2) == g;
+    const int p_lane = r16 & 3;
+
+    float tot[4] = {0.f, 0.f, 0.f, 0.f};  // per token
+    for (int sb0 = s0; sb0 < s1; sb0 += D) {
 #pragma unroll
-            for (int k = 0; k < F::kChunks; ++k) cur[k] = nxt[k];
-            if constexpr (QT == 6) cur[15] = nxt[15];
+        for (int ps = 0; ps < D; ++ps) {
+            const int sb = sb0 + ps;
+            if (sb < s1) {
+                const int sbl = sb - s0;
+                const i32x4* cb = buf[ps];
+                const float dq6d = QT == 6 ? half_bits_to_f32(dbits[ps]) : 0.f;
+                // this super-block's x fragments (A operands) and sub-block sums, read
+                // from LDS together before the MFMAs need them
+                i32x4 af[NSET][8];
+                {
+                    const i32x4* fa = diag ? afrag + (((sbl * 8) * 4 + p_lane) * 4 + g) : zero16;
+                    const int fstep = diag ? 16 : 0;  // i32x4 per mi
+#pragma unroll
+                    for (int st = 0; st < NSET; ++st)
+#pragma unroll
+                        for (int mi = 0; mi < 8; ++mi) af[st][mi] = fa[(st * P * 8 + mi) * fstep];
+                }
+                constexpr int kLaneSubs = QT == 4 ? 2 : 4;
+                float xsv[T][kLaneSubs];
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int k = 0; k < kLaneSubs; ++k) {
+                        const int j = QT == 4 ? 2 * g + k : sub_of<6>(g, 2 * k);
+                        const float* xr = xsum + ((t * P + sbl) * F::kNSub + j) * kRuns;
+                        if constexpr (QT == 4) {
+                            const float4 r4 = *reinterpret_cast<const float4*>(xr);
+                            xsv[t][k] = (r4.x + r4.y) + (r4.z + r4.w);
+                        } else {
+                            const float2 r2 = *reinterpret_cast<const float2*>(xr);
+                            xsv[t][k] = r2.x + r2.y;
+                        }
+                    }
+                // quants -> bf16 B operands, MFMA per 8 quants, one accumulator per sub-block
+                f32x4 acc[NSET][QT == 4 ? 2 : 4];
+#pragma unroll
+                for (int st = 0; st < NSET; ++st)
+#pragma unroll
+                    for (int k = 0; k < (QT == 4 ? 2 : 4); ++k) acc[st][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+                for (int mi = 0; mi < 8; ++mi) {
+                    Frag8 b;
+                    if constexpr (QT == 4) {
+                        // run = mi & 3: quant bytes 8*run .. 8*run+7 of the lane's 32; nibble mi >> 2
+                        const i32x4 ch = cb[(mi & 3) >> 1];
+                        const uint32_t w0 = static_cast<uint32_t>(ch[2 * (mi & 1)]);
+                        const uint32_t w1 = static_cast<uint32_t>(ch[2 * (mi & 1) + 1]);
+                        const uint32_t q0 = (mi >> 2) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
+                        const uint32_t q1 = (mi >> 2) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
+                        q_to_bf16x4(q0, b.u[0], b.u[1]);
+                        q_to_bf16x4(q1, b.u[2], b.u[3]);
+                    } else {
+                        // kk = mi >> 1, half = mi & 1: bytes 8*half .. 8*half+7 of the lane's 16
+                        const int kk = mi >> 1, hf = mi & 1;
+                        const i32x4 ql = cb[kk & 1];
+                        const i32x4 qh = cb[2];
+#pragma unroll
+                        for (int d = 0; d < 2; ++d) {
+                            const uint32_t lo4 = static_cast<uint32_t>(ql[2 * hf + d]);
+                            const uint32_t h2 = static_cast<uint32_t>(qh[2 * hf + d]);
+                            const uint32_t low = (kk >> 1) ? (lo4 >> 4) & 0x0f0f0f0fu : lo4 & 0x0f0f0f0fu;
+                            const uint32_t q6 = low | (((h2 >> (2 * kk)) & 0x03030303u) << 4);
+                            q_to_bf16x4(q6, b.u[2 * d], b.u[2 * d + 1]);
+                        }
+                    }
+#pragma unroll
+                    for (int st = 0; st < NSET; ++st) {
+                        Frag8 a;
+                        a.i = af[st][mi];
+                        const int k = QT == 4 ? (mi >> 2) : (mi >> 1);
+                        acc[st][k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[st][k], 0, 0, 0);
+                    }
+                }
+                // per (row, sub-block) scales of this lane's sub-blocks
+                if constexpr (QT == 4) {
+                    // header dwords: d | dmin, then scale bytes s12[0..3], [4..7], [8..11]
+                    const uint32_t h0 = static_cast<uint32_t>(cb[NL - 1][0]);
+                    const float d = half_bits_to_f32(h0 & 0xffffu);
+                    const float dmin = half_bits_to_f32(h0 >> 16);
+#pragma unroll
+                    for (int k = 0; k < 2; ++k) {
+                        int sc, mn;
+                        q4k_scale_min_reg(cb[NL - 1], 2 * g + k, sc, mn);
+                        const float a = d * static_cast<float>(sc);
+                        const float c = fmaf(128.f, a, dmin * static_cast<float>(mn));
+#pragma unroll
+                        for (int t = 0; t < T; ++t)
+                            tot[t] += a * (acc[t >> 1][k][2 * (t & 1)] + acc[t >> 1][k][2 * (t & 1) + 1]) - c * xsv[t][k];
+                    }
+                } else {
+#pragma unroll
+                    for (int kk = 0; kk < 4; ++kk) {
+                        // scale j = 8h + 2kk + e (h = g / 2, e = g % 2): dword 2h + kk / 2,
+                        // byte 2 (kk % 2) + e of the row's 16 int8 scales
+                        const i32x4 sv = cb[NL - 1];
+                        const int dw = (g >> 1) ? ((kk >> 1) ? sv[3] : sv[2]) : ((kk >> 1) ? sv[1] : sv[0]);
+                        const int scv = __builtin_amdgcn_sbfe(dw, 8 * (2 * (kk & 1) + (g & 1)), 8);
+                        const float a = dq6d * static_cast<float>(scv);
+                        const float c = 160.f * a;
+#pragma unroll
+                        for (int t = 0; t < T; ++t)
+                            tot[t] += a * (acc[t >> 1][kk][2 * (t & 1)] + acc[t >> 1][kk][2 * (t & 1) + 1]) - c * xsv[t][kk];
+                    }
+                }
+            }
+            load(ps, sb + D, sb + D < s1);
         }
     }
 
-    __shared__ float red[KS][4][64];
+    // the four lane groups of a row hold quarters of it: fixed-order sum
+#pragma unroll
+    for (int t = 0; t < 4; ++t) {
+        tot[t] += __shfl_xor(tot[t], 16, 64);
+        tot[t] += __shfl_xor(tot[t], 32, 64);
+    }
+    const int row = rt * kTR + r16;
+    const bool own = wave_live && g == 0 && row < m;
     __shared__ int s_last;
-#pragma unroll
-    for (int t = 0; t < 4; ++t) red[wave][t][lane] = y[t];
-    __syncthreads();
     if (S > 1) {
-        for (int it = threadIdx.x; it < T * kRows; it += 64 * KS) {
-            const int t = it / kRows, l = it % kRows;
-            const int row = rg * kRows + l;
-            if (row >= m) continue;
-            float s = 0.f;
-#pragma unroll
-            for (int w = 0; w < KS; ++w) s += red[w][t][l];
-            __hip_atomic_store(partial + (static_cast<size_t>(slice) * T + t) * m + row, s, __ATOMIC_RELAXED,
-                               __HIP_MEMORY_SCOPE_AGENT);
-        }
+        if (own)
+            for (int t = 0; t < T; ++t)
+                __hip_atomic_store(partial + (static_cast<size_t>(slice) * T + t) * m + row, tot[t], __ATOMIC_RELAXED,
+                                   __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete before the ticket
         __syncthreads();
         if (threadIdx.x == 0) {
-            unsigned* tk = g_kq_ticket + static_cast<size_t>(rg) * 16;
+            unsigned* tk = g_kq_ticket + static_cast<size_t>(rgp) * 16;
             const unsigned old = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const int last = old == static_cast<unsigned>(S - 1);
             if (last) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -270,56 +389,64 @@ __global__ __launch_bounds__(64 * KS) void kq_gemm_kernel(const uint8_t* __restr
         }
         __syncthreads();
         if (!s_last) return;
-        for (int it = threadIdx.x; it < T * kRows; it += 64 * KS) {
-            const int t = it / kRows, l = it % kRows;
-            const int row = rg * kRows + l;
-            if (row >= m) continue;
-            float s = 0.f;
-            for (int q = 0; q < S; ++q)
-                s += __hip_atomic_load(partial + (static_cast<size_t>(q) * T + t) * m + row, __ATOMIC_RELAXED,
-                                       __HIP_MEMORY_SCOPE_AGENT);
-            float* dst = Y + static_cast<size_t>(t) * ldy + row;
-            if (accumulate)
-                *dst += s;
-            else
-                *dst = s;
-        }
+        if (own)
+            for (int t = 0; t < T; ++t) {
+                float v = 0.f;
+                for (int q = 0; q < S; ++q)
+                    v += __hip_atomic_load(partial + (static_cast<size_t>(q) * T + t) * m + row, __ATOMIC_RELAXED,
+                                           __HIP_MEMORY_SCOPE_AGENT);
+                float* dst = Y + static_cast<size_t>(t) * ldy + row;
+                if (accumulate)
+                    *dst += v;
+                else
+                    *dst = v;
+            }
         return;
     }
-    for (int it = threadIdx.x; it < T * kRows; it += 64 * KS) {
-        const int t = it / kRows, l = it % kRows;
-        const int row = rg * kRows + l;
-        if (row >= m) continue;
-        float s = 0.f;
-#pragma unroll
-        for (int w = 0; w < KS; ++w) s += red[w][t][l];
-        if (accumulate)
-            Y[static_cast<size_t>(t) * ldy + row] += s;
-        else
-            Y[static_cast<size_t>(t) * ldy + row] = s;
-    }
+    if (own)
+        for (int t = 0; t < T; ++t) {
+            float* dst = Y + static_cast<size_t>(t) * ldy + row;
+            if (accumulate)
+                *dst += tot[t];
+            else
+                *dst = tot[t];
+        }
 }
 
-// Row-major GGUF blocks [m][n/256 * bb] -> K-tiled.
+// Row-major GGUF blocks [m][n/256 * bb] -> tiles.  One thread per (tile, lane).
 template <int QT>
 __global__ void kq_pack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int m, int nsb) {
     // rows past m are written as zero blocks (d = 0: every weight is 0)
     using F = KFmt<QT>;
-    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rg, sb, lane)
-    const int m_groups = (m + kRows - 1) / kRows;
-    if (idx >= static_cast<size_t>(m_groups) * nsb * kRows) return;
-    const int lane = idx % kRows;
-    const int sb = (idx / kRows) % nsb;
-    const int rg = static_cast<int>(idx / (static_cast<size_t>(kRows) * nsb));
-    const int row = rg * kRows + lane;
-    uint8_t* tile = dst + (static_cast<size_t>(rg) * nsb + sb) * F::kTileBytes;
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rt, sb, lane)
+    const int m_tiles = (m + kTR - 1) / kTR;
+    if (idx >= static_cast<size_t>(m_tiles) * nsb * 64) return;
+    const int lane = idx % 64;
+    const int sb = (idx / 64) % nsb;
+    const int rt = static_cast<int>(idx / (static_cast<size_t>(64) * nsb));
+    const int r16 = lane & 15, g = lane >> 4;
+    const int row = rt * kTR + r16;
+    uint8_t* tile = dst + (static_cast<size_t>(rt) * nsb + sb) * F::kTileBytes;
     const uint8_t* blk = src + (static_cast<size_t>(row) * nsb + sb) * F::kBlockBytes;
     const bool ok = row < m;
-    for (int k = 0; k < F::kChunks; ++k)
-        for (int e = 0; e < 16; ++e) tile[k * 1024 + 16 * lane + e] = ok ? blk[16 * k + e] : 0;
-    if constexpr (QT == 6) {
-        tile[F::kChunks * 1024 + 2 * lane] = ok ? blk[208] : 0;
-        tile[F::kChunks * 1024 + 2 * lane + 1] = ok ? blk[209] : 0;
+    auto put = [&](int chunk, int off) {
+        for (int e = 0; e < 16; ++e) tile[chunk * 1024 + 16 * lane + e] = ok ? blk[off + e] : 0;
+    };
+    if constexpr (QT == 4) {
+        put(0, 16 + 32 * g);
+        put(1, 16 + 32 * g + 16);
+        if (g == 0)
+            for (int e = 0; e < 16; ++e) tile[F::kHdr + 16 * r16 + e] = ok ? blk[e] : 0;
+    } else {
+        const int h = g >> 1, e16 = g & 1;
+        put(0, 64 * h + 16 * e16);
+        put(1, 64 * h + 32 + 16 * e16);
+        put(2, 128 + 32 * h + 16 * e16);
+        if (g == 0) {
+            for (int e = 0; e < 16; ++e) tile[F::kHdr + 16 * r16 + e] = ok ? blk[192 + e] : 0;
+            tile[F::kHdr + 256 + 2 * r16] = ok ? blk[208] : 0;
+            tile[F::kHdr + 256 + 2 * r16 + 1] = ok ? blk[209] : 0;
+        }
     }
 }
 
@@ -373,33 +500,53 @@ __global__ void q6k_dequant_kernel(const uint8_t* __restrict__ src, float* __res
 
 size_t kq_tiled_bytes(int qt, int m, int n) {
     const size_t tile = qt == 4 ? KFmt<4>::kTileBytes : KFmt<6>::kTileBytes;
-    return static_cast<size_t>((m + kRows - 1) / kRows) * (n / 256) * tile;
+    return static_cast<size_t>((m + kTR - 1) / kTR) * (n / 256) * tile;
 }
 
-// Work split: keep >= ~512 workgroups where the row groups alone are too few, and
-// the slice's x sums within 32 KiB of LDS.
-constexpr size_t kKqXsLds = 32768;
-size_t kq_xs_bytes(int qt, int nsb, int S, int T) {
-    return static_cast<size_t>(T) * ((nsb + S - 1) / S) * (qt == 4 ? 8 : 16) * sizeof(float);
+// Work split: keep >= ~512 workgroups where the row groups alone are too few, and a
+// K-slice short enough for the LDS fragments of four tokens (so the split, and
+// with it every token's summation order, does not depend on T).
+constexpr int kKqMaxSlice = 12;
+constexpr int kKqDepth = 4;  // tiles in flight per wave
+// Row tiles (waves) per workgroup.  RL_KQ_RW overrides it for measurement.
+int kq_rw() {
+    static const int rw = [] {
+        const char* v = std::getenv("RL_KQ_RW");
+        const int r = v ? std::atoi(v) : 0;
+        return r == 1 || r == 2 || r == 4 ? r : 4;
+    }();
+    return rw;
 }
-void kq_split(int qt, int m, int nsb, int T, int& S, int& KS) {
-    const int groups = (m + kRows - 1) / kRows;
-    KS = 4;
-    S = 1;
-    while (groups * S < 512 && nsb / (S * 2) >= 4) S *= 2;
-    while (kq_xs_bytes(qt, nsb, S, T) > kKqXsLds) S *= 2;
-    static const char* env = std::getenv("RL_KQ_SPLIT");  // measurement override "S"
-    if (env && std::atoi(env) > 0) S = std::atoi(env);
+void kq_split(int m, int nsb, int& S) {
+    // about two workgroups per CU in total (5120 x 17408: 80 row groups x 6 slices
+    // measured best, 15.5 us against 17.1 us with 8 slices and 21.6 us with 16),
+    // slices of at least 4 super-blocks
+    const int groups = (m + kTR * kq_rw() - 1) / (kTR * kq_rw());
+    S = std::max(1, std::min(512 / groups, nsb / 4));
+    while ((nsb + S - 1) / S > kKqMaxSlice) ++S;
+    static const char* env = std::getenv("RL_KQ_SPLIT");  // measurement override
+    if (env && std::atoi(env) > 0) S = std::max(std::atoi(env), (nsb + kKqMaxSlice - 1) / kKqMaxSlice);
     S = std::min(S, nsb);
+}
+
+template <int QT, int T, int RW>
+void launch_kq_rw(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int S, int accumulate,
+                  int ldy, hipStream_t s) {
+    const int groups = (m + kTR * RW - 1) / (kTR * RW);
+    const int P = (n / 256 + S - 1) / S;
+    const size_t lds = kq_lds_bytes<QT>(P, (T + 1) / 2, T);
+    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW>), dim3(groups * S), dim3(64 * RW), lds, s, W, x, Y,
+                       partial, m, n, S, accumulate, ldy);
 }
 
 template <int QT, int T>
 void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int S, int accumulate,
                  int ldy, hipStream_t s) {
-    const int groups = (m + kRows - 1) / kRows;
-    const size_t lds = kq_xs_bytes(QT, n / 256, S, T);
-    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, 4>), dim3(groups * S), dim3(256), lds, s, W, x, Y, partial, m, n, S,
-                       accumulate, ldy);
+    switch (kq_rw()) {
+    case 1: launch_kq_rw<QT, T, 1>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 2: launch_kq_rw<QT, T, 2>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    default: launch_kq_rw<QT, T, 4>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    }
 }
 
 template <int QT>
@@ -419,10 +566,8 @@ namespace rl {
 
 size_t kq_workspace_bytes(int m, int n, int T) {
     // partials for the largest split either type uses: S*T*m floats
-    int S4, S6, KS;
-    kq_split(4, m, n / 256, T, S4, KS);
-    kq_split(6, m, n / 256, T, S6, KS);
-    const int S = std::max(S4, S6);
+    int S;
+    kq_split(m, n / 256, S);
     return (S > 1 ? static_cast<size_t>(S) * T * m : 0) * 4 + 256;
 }
 
@@ -434,10 +579,10 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     RL_REQUIRE(T >= 1 && T <= 4, RL_ERR_RANGE, "kquant: T must be in 1..4");
     RL_REQUIRE(W && x && Y && ws, RL_ERR_RANGE, "kquant: null pointer");
     RL_REQUIRE(ws_bytes >= kq_workspace_bytes(m, n, T), RL_ERR_RANGE, "kquant: workspace too small");
-    int S, KS;
-    kq_split(qt, m, n / 256, T, S, KS);
-    RL_REQUIRE(S == 1 || (m + kRows - 1) / kRows <= kKqMaxGroups, RL_ERR_UNSUPPORTED, "kquant: too many rows");
-    RL_REQUIRE(kq_xs_bytes(qt, n / 256, S, T) <= kKqXsLds, RL_ERR_UNSUPPORTED, "kquant: K-slice too long");
+    int S;
+    kq_split(m, n / 256, S);
+    RL_REQUIRE(S == 1 || (m + kTR * kq_rw() - 1) / (kTR * kq_rw()) <= kKqMaxGroups, RL_ERR_UNSUPPORTED,
+               "kquant: too many rows");
     float* partial = static_cast<float*>(ws);
     if (qt == 4)
         launch_kq<4>(W, x, Y, partial, m, n, T, S, accumulate, ldy, s);
@@ -462,7 +607,7 @@ int rl_hip_pack_kquant(int type, const uint8_t* blocks, uint8_t* tiled, int m, i
         RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "pack_kquant: Q4_K or Q6_K only");
         RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0 && blocks && tiled, RL_ERR_RANGE, "pack_kquant: bad shape");
         const int nsb = n / 256;
-        const size_t total = static_cast<size_t>((m + kRows - 1) / kRows) * nsb * kRows;
+        const size_t total = static_cast<size_t>((m + kTR - 1) / kTR) * nsb * 64;
         if (type == RL_Q_Q4_K)
             hipLaunchKernelGGL(kq_pack_kernel<4>, dim3((total + 255) / 256), dim3(256), 0, S(stream), blocks, tiled, m,
                                nsb);
