@@ -143,6 +143,110 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
     return avg_ms, avg_bytes, per
 
 
+def measure_configs(spec, gemm_t1, gemm_t4, iters=30, rotate_bytes=768 << 20):
+    """Per-config kernel lines, each on weights / states read
+    from HBM (rotated over >= rotate_bytes), timed with HIP events around
+    back-to-back launches from C++.  `gemm_t1` / `gemm_t4` are measure_gemm's
+    per-shape results at T=1 / T=4."""
+    import ctypes as C
+
+    from rapidllm_amd import ops, synth
+    from rapidllm_amd.hip import DeviceBuffer, call
+
+    s = C_stream()
+    r = synth.rng(11)
+    out = {}
+
+    def frac(b, us):
+        return round(b / us / 1e3 / PEAK_GBS, 4)
+
+    # C1: one block-FP8 GEMV, W [17408 x 5120], T = 1
+    m, n = 17408, 5120
+    W = synth.fp8_weight(r, m, n)
+    lin = ops.Fp8Linear(W, synth.fp8_scales(r, m, n))
+    nb = lin.w.nbytes
+    copies = [lin.w] + [DeviceBuffer(nb) for _ in range(max(1, -(-rotate_bytes // nb)) - 1)]
+    for c in copies[1:]:
+        call("rl_hip_memcpy_d2d", c.ptr, lin.w.ptr, nb, s)
+    xd = DeviceBuffer.from_numpy(r.standard_normal((1, n)).astype(np.float32))
+    frag = ops.act_frag_buffer(n, 1)
+    yd = DeviceBuffer(4 * m)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, n, 1, s)
+    ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
+    ms = C.c_float()
+    args = (lin.ts.ptr, frag.ptr, yd.ptr, None, None, None, None, m, n, 1, EPI_STORE, SPLIT)
+    call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, len(copies), s, C.byref(ms))
+    call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, iters, s, C.byref(ms))
+    b = m * n + 4 * ((m + 127) // 128) * ((n + 127) // 128) + 4 * (m + n)
+    us = ms.value * 1e3
+    out["c1_fp8_gemv_17408x5120_t1"] = {"us": round(us, 2), "bytes": b, "GBps": round(b / us / 1e3, 1),
+                                        "frac": frac(b, us)}
+    del lin, copies, xd, frag, yd, ptrs
+
+    # C2: GGUF Q4_K / Q6_K GEMV, W [5120 x 17408], T = 1 (and T = 4)
+    m, n = 5120, 17408
+    for name, qt, gen, bb in (("q4_k", ops.Q4_K, synth.q4k_blocks, 144), ("q6_k", ops.Q6_K, synth.q6k_blocks, 210)):
+        lin = ops.KQuantLinear(qt, gen(r, m, n), m, n)
+        nb = lin.w.nbytes
+        copies = [lin.w] + [DeviceBuffer(nb) for _ in range(max(1, -(-rotate_bytes // nb)) - 1)]
+        for c in copies[1:]:
+            call("rl_hip_memcpy_d2d", c.ptr, lin.w.ptr, nb, s)
+        ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
+        res = {}
+        for T in (1, 4):
+            xd = DeviceBuffer.from_numpy(r.standard_normal((T, n)).astype(np.float32))
+            yd = DeviceBuffer(4 * T * m)
+            ws = ops.kquant_workspace(m, n, T)
+            targs = (qt, ptrs, len(copies), xd.ptr, yd.ptr, ws.ptr, ws.nbytes, m, n, T)
+            call("rl_hip_time_gemm_kquant", *targs, len(copies), s, C.byref(ms))
+            call("rl_hip_time_gemm_kquant", *targs, iters, s, C.byref(ms))
+            b = m * (n // 256) * bb + 4 * T * (m + n)
+            us = ms.value * 1e3
+            res[f"t{T}"] = {"us": round(us, 2), "bytes": b, "GBps": round(b / us / 1e3, 1), "frac": frac(b, us)}
+        out[f"c2_{name}_gemv_5120x17408"] = res
+        del lin, copies, ptrs
+
+    # C3: one layer's block-FP8 linear set at T = 4 (DeltaNet in_proj, q|gate;k;v,
+    # o, gate/up, down): gemm_shapes entries 0, 2, 3, 4, 5 (1 is the DeltaNet
+    # out_proj, not in the set)
+    res = {}
+    for T, per in ((1, gemm_t1), (4, gemm_t4)):
+        us = b = 0.0
+        for sh in (per[i] for i in (0, 2, 3, 4, 5)):
+            us += sh["us"]
+            b += sh["m"] * sh["n"] + 4 * ((sh["m"] + 127) // 128) * ((sh["n"] + 127) // 128) + \
+                4 * T * (sh["m"] + sh["n"])
+        res[f"t{T}"] = {"us": round(us, 2), "bytes": int(b), "GBps": round(b / us / 1e3, 1), "frac": frac(b, us)}
+    res["t4_over_t1"] = round(res["t4"]["us"] / res["t1"]["us"], 4)
+    out["c3_fp8_linear_set"] = res
+
+    # C4: Gated DeltaNet recurrent decode, T = 4, over 48 layer states
+    T, nk, nv, dk, dv, K = 4, spec.n_k_heads, spec.n_v_heads, spec.k_dim, spec.v_dim, spec.conv_k
+    conv = spec.conv_dim
+    n_d = sum(1 for k in spec.layer_kinds if k == 0)
+    Ss = [DeviceBuffer.from_numpy((0.02 * r.standard_normal(nv * dk * dv)).astype(np.float32)) for _ in range(n_d)]
+    ld = conv + 2 * nv
+    qkv = DeviceBuffer.from_numpy(r.standard_normal((T, ld)).astype(np.float32))
+    A_log = DeviceBuffer.from_numpy(r.standard_normal(nv).astype(np.float32))
+    dt_b = DeviceBuffer.from_numpy(r.standard_normal(nv).astype(np.float32))
+    cw = DeviceBuffer.from_numpy((0.5 * r.standard_normal(conv * K)).astype(np.float32))
+    cin = DeviceBuffer.from_numpy(r.standard_normal(conv * K).astype(np.float32))
+    cout = DeviceBuffer(4 * conv * K)
+    o = DeviceBuffer(4 * T * nv * dv)
+    sp = (C.c_void_p * n_d)(*[x.ptr for x in Ss])
+    gargs = (sp, n_d, qkv.ptr, qkv.ptr + 4 * conv, qkv.ptr + 4 * (conv + nv), ld, A_log.ptr, dt_b.ptr, cw.ptr,
+             cin.ptr, cout.ptr, o.ptr, T, nk, nv, dk, dv, K, 0)
+    call("rl_hip_time_gdn", *gargs, 1, s, C.byref(ms))
+    call("rl_hip_time_gdn", *gargs, 5, s, C.byref(ms))
+    us = ms.value * 1e3
+    b = 2 * nv * dk * dv * 4 + 2 * conv * K * 4 + 4 * T * (ld + nv * dv)
+    out["c4_deltanet_t4_per_layer"] = {"us": round(us, 2), "bytes": b, "GBps": round(b / us / 1e3, 1),
+                                       "frac": frac(b, us), "layers": n_d,
+                                       "all_layers_us": round(us * n_d, 1)}
+    del Ss
+    return out
+
+
 _stream = None
 
 
@@ -291,6 +395,8 @@ def main():
     b1 = step_bytes(spec, 1, CTX)
     b4 = step_bytes(spec, 4, CTX)
     g_ms, g_bytes, per = measure_gemm(spec, 1)
+    _, _, per4 = measure_gemm(spec, 4)
+    configs = measure_configs(spec, per, per4)
     roof = {"bound": "hbm", "kernel": "gemm_frag_kernel (block-FP8, T=1 step launch mix, weights read from HBM)",
             "achieved": round(g_bytes / g_ms / 1e6, 1), "peak": PEAK_GBS, "unit": "GB/s",
             "frac": round(g_bytes / g_ms / 1e6 / PEAK_GBS, 4), "traffic": measured_traffic(),
@@ -322,6 +428,7 @@ def main():
                           "t4_bytes": b4["total"], "t4_GBps": round(b4["total"] / t4 / 1e6, 1),
                           "t4_frac": round(b4["total"] / t4 / 1e6 / PEAK_GBS, 4), "bytes_t1": b1},
         "roofline": roof,
+        "configs": configs,
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(spec, b1["total"])

@@ -278,6 +278,21 @@ int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float*
                          float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
                          int m, int n, int T, int epilogue, int split, int iters, void* stream, float* avg_ms);
 
+/* Average duration of `iters` back-to-back rl_hip_gemm_kquant launches (store),
+ * cycling over n_copies packed weight copies.  No counterpart in the reference
+ * (bench / roofline measurement). */
+int rl_hip_time_gemm_kquant(int type, const void* const* w_copies, int n_copies, const float* X, float* Y,
+                            void* workspace, size_t workspace_bytes, int m, int n, int T, int iters, void* stream,
+                            float* avg_ms);
+
+/* Average duration of one DeltaNet decode launch (rl_hip_gdn_decode semantics with
+ * S updated in place) over `iters` passes across n_layers layer states.  No
+ * counterpart in the reference (bench / roofline measurement). */
+int rl_hip_time_gdn(float* const* S_layers, int n_layers, const float* qkv, const float* a, const float* b, int ld_in,
+                    const float* A_log, const float* dt_bias, const float* conv_w, const float* conv_in,
+                    float* conv_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k, int v_tiled,
+                    int iters, void* stream, float* avg_ms);
+
 #ifdef __cplusplus
 }
 #endif

@@ -106,4 +106,59 @@ int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float*
     });
 }
 
+// Average duration of `iters` back-to-back K-quant GEMVs (HIP events on the launch
+// stream), cycling over n_copies weight copies so every launch reads from HBM.
+int rl_hip_time_gemm_kquant(int type, const void* const* w_copies, int n_copies, const float* X, float* Y,
+                            void* workspace, size_t workspace_bytes, int m, int n, int T, int iters, void* stream,
+                            float* avg_ms) {
+    return guard([&] {
+        RL_REQUIRE(w_copies && n_copies >= 1 && iters >= 1 && avg_ms, RL_ERR_RANGE, "time_kquant: bad arguments");
+        RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "time_kquant: Q4_K or Q6_K only");
+        const hipStream_t s = S(stream);
+        hipEvent_t a, b;
+        RL_HIP(hipEventCreate(&a));
+        RL_HIP(hipEventCreate(&b));
+        RL_HIP(hipEventRecord(a, s));
+        for (int i = 0; i < iters; ++i)
+            rl::kq_gemm(type == RL_Q_Q4_K ? 4 : 6, static_cast<const uint8_t*>(w_copies[i % n_copies]), X, Y,
+                        workspace, workspace_bytes, m, n, T, 0, m, s);
+        RL_HIP(hipEventRecord(b, s));
+        RL_HIP(hipEventSynchronize(b));
+        float ms = 0.f;
+        RL_HIP(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        *avg_ms = ms / iters;
+    });
+}
+
+// Average duration of one DeltaNet decode launch (rl_hip_gdn_decode semantics, S
+// updated in place) over `iters` passes across n_layers separate layer states.
+int rl_hip_time_gdn(float* const* S_layers, int n_layers, const float* qkv, const float* a, const float* b, int ld_in,
+                    const float* A_log, const float* dt_bias, const float* conv_w, const float* conv_in,
+                    float* conv_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k, int v_tiled,
+                    int iters, void* stream, float* avg_ms) {
+    return guard([&] {
+        RL_REQUIRE(S_layers && n_layers >= 1 && iters >= 1 && avg_ms, RL_ERR_RANGE, "time_gdn: bad arguments");
+        RL_REQUIRE(rl::gdn_fused_supported(dk, dv, conv_k), RL_ERR_UNSUPPORTED, "time_gdn: fused kernel shapes only");
+        const hipStream_t s = S(stream);
+        hipEvent_t ea, eb;
+        RL_HIP(hipEventCreate(&ea));
+        RL_HIP(hipEventCreate(&eb));
+        RL_HIP(hipEventRecord(ea, s));
+        for (int i = 0; i < iters; ++i)
+            for (int l = 0; l < n_layers; ++l)
+                rl::gdn_decode_fused(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_layers[l],
+                                     S_layers[l], nullptr, 0, 0, nullptr, o, nullptr, nullptr, nullptr, nullptr, T, nk,
+                                     nv, dk, dv, conv_k, v_tiled, s);
+        RL_HIP(hipEventRecord(eb, s));
+        RL_HIP(hipEventSynchronize(eb));
+        float ms = 0.f;
+        RL_HIP(hipEventElapsedTime(&ms, ea, eb));
+        (void)hipEventDestroy(ea);
+        (void)hipEventDestroy(eb);
+        *avg_ms = ms / (static_cast<float>(iters) * n_layers);
+    });
+}
+
 }  // extern "C"
