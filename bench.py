@@ -344,6 +344,8 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only the block-FP8 GEMM launch mix (the roofline kernel), for counter runs")
+    ap.add_argument("--configs-only", action="store_true",
+                    help="run only the per-config kernel lines (configs 1-4), for kernel traces")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
                     help="run only a plain device copy of this many MiB (counter calibration)")
     args = ap.parse_args()
@@ -364,6 +366,11 @@ def main():
     if args.gemm_only:
         g_ms, g_bytes, per = measure_gemm(spec, 1, iters=args.steps)
         print(json.dumps({"avg_launch_us": round(g_ms * 1e3, 2), "bytes_per_launch": int(g_bytes), "shapes": per}))
+        return
+    if args.configs_only:
+        _, _, per1 = measure_gemm(spec, 1)
+        _, _, per4 = measure_gemm(spec, 4)
+        print(json.dumps(measure_configs(spec, per1, per4)))
         return
     t0 = time.time()
     eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=4)

@@ -66,3 +66,70 @@ def test_gemm_kquant_tokens_independent_of_T(gpu):
     for t in range(4):
         Y1 = ops.kquant_linear_T(lin, X[t:t + 1])[0]
         assert np.array_equal(Y1.view(np.uint32), Y4[t].view(np.uint32))
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("m,n,T", [(17, 256, 3), (200, 4096, 3), (300, 3072, 1)])
+def test_gemm_kquant_ragged_and_odd_T(gpu, orc, kind, m, n, T):
+    """Row counts that leave a partial 16-row tile and a partial 4-tile workgroup,
+    one super-block per row, three tokens (the second token set half empty)."""
+    r = synth.rng(7 + m + n + T)
+    blocks = _blocks(kind, r, m, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    lin = ops.KQuantLinear(ops.Q4_K if kind == "q4k" else ops.Q6_K, blocks, m, n)
+    Y = ops.kquant_linear_T(lin, X)
+    fo = orc.gemv_q4_k if kind == "q4k" else orc.gemv_q6_k
+    for t in range(T):
+        assert rel_l2(Y[t], fo(blocks, X[t], m, n, 8)) <= 1e-3, (kind, m, n, T, t)
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+def test_gemm_kquant_extreme_blocks(gpu, orc, kind):
+    """Maximal 6-bit scales / mins and quants (all-ones bytes), zero scales and an
+    fp16 subnormal d, mixed into random blocks."""
+    r = synth.rng(77)
+    m, n = 128, 2048
+    blocks = _blocks(kind, r, m, n)
+    bb = 144 if kind == "q4k" else 210
+    flat = blocks.reshape(-1, bb)
+    flat[::7] = 0xFF
+    if kind == "q4k":
+        flat[::7, 0:4] = np.frombuffer(np.array([1e-3, 2e-3], np.float16).tobytes(), np.uint8)
+        flat[3::11, 0:2] = 0
+        flat[5::13, 0:2] = np.frombuffer(np.array([6.0e-8], np.float16).tobytes(), np.uint8)
+    else:
+        flat[::7, 208:210] = np.frombuffer(np.array([1e-3], np.float16).tobytes(), np.uint8)
+        flat[3::11, 192:208] = 0
+        flat[5::13, 208:210] = np.frombuffer(np.array([6.0e-8], np.float16).tobytes(), np.uint8)
+    X = r.standard_normal((2, n)).astype(np.float32)
+    lin = ops.KQuantLinear(ops.Q4_K if kind == "q4k" else ops.Q6_K, blocks, m, n)
+    Y = ops.kquant_linear_T(lin, X)
+    fo = orc.gemv_q4_k if kind == "q4k" else orc.gemv_q6_k
+    for t in range(2):
+        assert rel_l2(Y[t], fo(blocks, X[t], m, n, 8)) <= 1e-3, (kind, t)
+
+
+def test_gemm_kquant_repeat_and_accumulate(gpu):
+    """Split-K launches share ticket counters that the last workgroup of each row
+    group resets: back-to-back launches must give bit-identical results, and the
+    accumulate mode adds the product to Y."""
+    from rapidllm_amd.hip import DeviceBuffer
+    r = synth.rng(12)
+    m, n, T = 5120, 17408, 2
+    blocks = synth.q4k_blocks(r, m, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    lin = ops.KQuantLinear(ops.Q4_K, blocks, m, n)
+    ws = ops.kquant_workspace(m, n, T)
+    xd = DeviceBuffer.from_numpy(X)
+    outs = []
+    for _ in range(3):
+        yd = DeviceBuffer(4 * T * m)
+        lin.forward(xd.ptr, yd.ptr, T, ws)
+        outs.append(yd.numpy(np.float32, (T, m)))
+    for o in outs[1:]:
+        assert np.array_equal(o.view(np.uint32), outs[0].view(np.uint32))
+    Y0 = r.standard_normal((T, m)).astype(np.float32)
+    yd = DeviceBuffer.from_numpy(Y0)
+    lin.forward(xd.ptr, yd.ptr, T, ws, accumulate=True)
+    got = yd.numpy(np.float32, (T, m))
+    assert rel_l2(got, Y0 + outs[0]) <= 1e-6
