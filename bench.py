@@ -247,6 +247,91 @@ def measure_configs(spec, gemm_t1, gemm_t4, iters=30, rotate_bytes=768 << 20):
     return out
 
 
+def cpu_configs(spec, budget_s=6.0):
+    """The reference CPU path for configs 1, 2 and 4 on the host cores, timed in the
+    same run (oracle/_ref: the reference's own compiled ops; the oracle restatement,
+    kind "port", where they were not built).  Median of up to 3 runs per line."""
+    from oracle import oracle as O
+    from rapidllm_amd import synth
+
+    R = O.ref()
+    kind = "reference" if R is not None else "port"
+    threads = int(R.ref_num_threads()) if R is not None else 1
+    r = synth.rng(21)
+    out = {}
+
+    def med(fn):
+        ts = []
+        t_end = time.time() + budget_s
+        while time.time() < t_end and len(ts) < 3:
+            t = time.perf_counter()
+            fn()
+            ts.append(time.perf_counter() - t)
+        return float(np.median(ts)) * 1e6, len(ts)
+
+    # C1: ops::gemv_fp8 (scalar, one thread: the reference's only FP8 CPU GEMV)
+    m, n = 17408, 5120
+    W, sc = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n)
+    x = r.standard_normal(n).astype(np.float32)
+    y = np.empty(m, np.float32)
+    if R is not None:
+        us, k = med(lambda: R.ref_gemv_fp8(O.P(W, O._u8), O.P(sc), O.P(x), O.P(y), m, n))
+    else:
+        us, k = med(lambda: O.gemv_fp8(W, sc, x))
+    out["c1"] = {"us": round(us, 1), "cores": 1, "kind": kind, "runs": k, "what": "ops::gemv_fp8 17408x5120"}
+    del W
+    # C2: ops::gemv_q4_k / gemv_q6_k (row-parallel over the reference WorkerPool)
+    m, n = 5120, 17408
+    x = r.standard_normal(n).astype(np.float32)
+    y = np.empty(m, np.float32)
+    for name, gen, fr, fo in (("q4_k", synth.q4k_blocks, "ref_gemv_q4_k", O.gemv_q4_k),
+                              ("q6_k", synth.q6k_blocks, "ref_gemv_q6_k", O.gemv_q6_k)):
+        blk = np.ascontiguousarray(gen(r, m, n)).reshape(-1)
+        if R is not None:
+            f = getattr(R, fr)
+            us, k = med(lambda: f(O.P(blk, O._u8), O.P(x), O.P(y), m, n))
+            cores = threads
+        else:
+            us, k = med(lambda: fo(blk, x, m, n, 8))
+            cores = 8
+        out[f"c2_{name}"] = {"us": round(us, 1), "cores": cores, "kind": kind, "runs": k,
+                             "what": f"ops::gemv_{name} 5120x17408"}
+    # C4: per token conv1d_update over the 10240 channels + the delta-rule step over
+    # 48 heads (ops::delta_recurrent_step_simd), 4 tokens, one layer; x 48 layers
+    nv, dk, dv, conv, K = spec.n_v_heads, spec.k_dim, spec.v_dim, spec.conv_dim, spec.conv_k
+    S = (0.02 * r.standard_normal(nv * dk * dv)).astype(np.float32)
+    st = r.standard_normal(conv * K).astype(np.float32)
+    cw = (0.5 * r.standard_normal(conv * K)).astype(np.float32)
+    xs = r.standard_normal((4, conv)).astype(np.float32)
+    q = r.standard_normal((4, nv * dk)).astype(np.float32)
+    kk = r.standard_normal((4, nv * dk)).astype(np.float32)
+    v = r.standard_normal((4, nv * dv)).astype(np.float32)
+    beta = (1 / (1 + np.exp(-r.standard_normal((4, nv))))).astype(np.float32)
+    gl = (-np.log1p(np.exp(r.standard_normal((4, nv))))).astype(np.float32)
+    ycv = np.empty(conv, np.float32)
+    o = np.empty(nv * dv, np.float32)
+
+    def layer_ref():
+        for t in range(4):
+            R.ref_conv1d_update(O.P(xs[t]), O.P(cw), O.P(st), O.P(ycv), conv, K)
+            R.ref_delta_step_simd(O.P(S), O.P(q[t]), O.P(kk[t]), O.P(v[t]), O.P(beta[t]), O.P(gl[t]), O.P(o), nv, dk,
+                                  dv, 1e-6)
+
+    def layer_port():
+        Sm = S.reshape(nv, dk, dv).copy()
+        stm = st.reshape(conv, K).copy()
+        for t in range(4):
+            O.conv1d_update(xs[t], cw.reshape(conv, K), stm)
+            O.delta_step(Sm, q[t].reshape(nv, dk), kk[t].reshape(nv, dk), v[t].reshape(nv, dv), beta[t], gl[t])
+
+    us, k = med(layer_ref if R is not None else layer_port)
+    n_d = sum(1 for kd in spec.layer_kinds if kd == 0)
+    out["c4"] = {"us_per_layer": round(us, 1), "all_layers_us": round(us * n_d, 1),
+                 "cores": threads if R is not None else 1, "kind": kind, "runs": k,
+                 "what": "4 x (ops::conv1d_update 10240 ch + ops::delta_recurrent_step_simd 48 heads) per layer"}
+    return out
+
+
 _stream = None
 
 
@@ -370,7 +455,10 @@ def main():
     if args.configs_only:
         _, _, per1 = measure_gemm(spec, 1)
         _, _, per4 = measure_gemm(spec, 4)
-        print(json.dumps(measure_configs(spec, per1, per4)))
+        cfg = measure_configs(spec, per1, per4)
+        if not args.no_cpu:
+            cfg["cpu"] = cpu_configs(spec)
+        print(json.dumps(cfg))
         return
     t0 = time.time()
     eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=4)
@@ -439,6 +527,7 @@ def main():
     }
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline(spec, b1["total"])
+        configs["cpu"] = cpu_configs(spec)
     print(json.dumps(out), flush=True)
 
 
