@@ -93,6 +93,14 @@ int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream);
 /* Y[T][m] (=, or += when accumulate) W . X for T in 1..8 using a packed fragment
  * buffer.  Deterministic: partial sums are combined in a fixed order, and token t's
  * result does not depend on T. */
+/* Prompt prefill: Y[t][ldy] (=, +=) W . x_t for T (any) tokens of rl_hip_pack_act
+ * fragments, on the matrix cores (128 rows x 64 tokens per workgroup).  epilogue:
+ * 0 store, 1 add, 2 SwiGLU over interleaved gate/up 16-row tiles (m/2 output rows).
+ * ldy <= 0: m (m/2 for SwiGLU).  Replaces the reference's prefill linears
+ * (cuda_engine.cu:18338-18590 -> launch_linear for T > 8, :12008-12016). */
+int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
+                            int T, int epilogue, int ldy, void* stream);
+
 int rl_hip_gemm_fp8_frag(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                          int T, int accumulate, void* stream);
 int rl_hip_gemm_bf16_frag(const uint16_t* w_tiled, const void* frag, float* Y, int m, int n, int T, int accumulate,

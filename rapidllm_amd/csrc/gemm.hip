@@ -560,7 +560,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
 }
 
 void launch_pack_act(const float* X, void* frag, int n, int T, hipStream_t s) {
-    RL_REQUIRE(n > 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "pack_act: bad shape");
+    RL_REQUIRE(n > 0 && T >= 1 && T <= 65536, RL_ERR_RANGE, "pack_act: bad shape");
     const int n_kb = n_kb_of(n);
     const int total = n_kb * 16 * T;
     hipLaunchKernelGGL(pack_act_kernel, dim3((total + 255) / 256), dim3(256), 0, s, X, static_cast<i32x4*>(frag), n,

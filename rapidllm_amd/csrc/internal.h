@@ -48,6 +48,11 @@ void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
                     hipStream_t s, int S = 1, void* frag_out = nullptr, const NormIO* norm = nullptr);
 int add_norm_groups(int m);
+
+// prefill.hip: Y = W . X for T (any) tokens on MFMA; epi store / add / SwiGLU
+// (interleaved gate/up tiles, m_valid = m/2 output rows).  frag: act fragments of T.
+void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
+                      int ldy, int m_valid, hipStream_t s);
 int device_cus();  // CUs of the current device
 void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,

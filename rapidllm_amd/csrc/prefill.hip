@@ -1,0 +1,195 @@
+// prefill.hip -- block-FP8 linears over many tokens (prompt prefill), on MFMA.
+//
+// Same arithmetic as ops::gemv_fp8 (reference src/kernels/ops.cpp:182-194) applied
+// to every prompt token, i.e. the reference's prefill linears
+// (src/kernels/cuda/cuda_engine.cu:18338-18590 launch_prefill_chunk -> launch_linear
+// for T > 8, cuda_engine.cu:12008-12016).  At prefill sizes the work is
+// matrix-core bound, not HBM bound: one 128-row x 64-token output block per
+// workgroup reads each weight tile once for 64 tokens.
+//
+// Operands as in gemm.hip: A = 16 weight rows x 32 k, e4m3 decoded to bf16 by the
+// hardware converter (exact); B = 32 k x 16 tokens of the activation fragments
+// (bf16 hi and mid parts, two MFMAs into the same accumulator, so products carry
+// 16 significant bits of x); the 128x128 block scale multiplies each 128-column
+// block's fp32 partial.  Weights use the decode GEMM's tiled layout (16 rows x 128
+// columns per 2 KiB tile), activations its fragment layout for T tokens.
+//
+// Workgroup: 4 waves, 8 row tiles (128 rows) x 64 tokens; wave w owns tokens
+// 16w .. 16w+15 of the block for all 8 row tiles.  The 8 weight tiles of a column
+// block (16 KiB) are staged once in LDS (double buffered, the next block's loads in
+// flight during the MFMAs) and read by all four waves.
+#include "internal.h"
+
+using namespace rl;
+
+namespace {
+
+constexpr int kPfRT = 8;     // row tiles per workgroup
+constexpr int kPfTok = 64;   // tokens per workgroup
+constexpr int kTileRows = 16;
+
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+
+union Frag8 {
+    bf16x8 v;
+    uint32_t u[4];
+    i32x4 i;
+};
+
+__device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
+    const bf16x2_t a = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w), 1.0f, false);
+    const bf16x2_t b = __builtin_amdgcn_cvt_scalef32_pk_bf16_fp8(static_cast<int>(w), 1.0f, true);
+    lo = __builtin_bit_cast(uint32_t, a);
+    hi = __builtin_bit_cast(uint32_t, b);
+}
+
+__device__ inline float silu_f(float x) { return x / (1.f + __expf(-x)); }
+
+// EPI: 0 store, 1 add (Y += W.x), 2 SwiGLU over interleaved gate/up row tiles
+// (even tile = gate rows, odd = up rows of the same 16 outputs; Y row = output row).
+template <int EPI>
+__global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __restrict__ W,
+                                                           const float* __restrict__ tscale,
+                                                           const i32x4* __restrict__ frag, float* __restrict__ Y,
+                                                           int m, int n_kb, int T, int ldy, int m_valid) {
+    const int tid = threadIdx.x;
+    const int lane = tid & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+    const int g = lane >> 4, col = lane & 15;
+    const int m_tiles = (m + kTileRows - 1) / kTileRows;
+    const int rt0 = blockIdx.x * kPfRT;
+    const int tok = blockIdx.y * kPfTok + wave * 16 + col;  // B column of this lane
+    const int tokc = min(tok, T - 1);
+    const int NC = 2 * T;
+
+    __shared__ i32x4 wl[2][kPfRT][2][64];  // [buffer][row tile][16-B chunk][lane]
+
+    // staging: unit u = (row tile, chunk, lane), 4 per thread
+    i32x4 stg[4];
+    auto stage_load = [&](int kb) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int u = tid + 256 * q;
+            const int r = u >> 7, c = (u >> 6) & 1, l = u & 63;
+            const int rt = min(rt0 + r, m_tiles - 1);
+            stg[q] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
+                W + (static_cast<size_t>(rt) * n_kb + kb) * 2048 + c * 1024 + 16 * l));
+        }
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+            const int u = tid + 256 * q;
+            wl[buf][u >> 7][(u >> 6) & 1][u & 63] = stg[q];
+        }
+    };
+
+    f32x4 tot[kPfRT];
+#pragma unroll
+    for (int r = 0; r < kPfRT; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+    for (int kb = 0; kb < n_kb; ++kb) {
+        const int buf = kb & 1;
+        if (kb + 1 < n_kb) stage_load(kb + 1);
+        // activation fragments of this lane's token: 4 k-steps x (hi, mid)
+        i32x4 bh[4], bm[4];
+#pragma unroll
+        for (int i = 0; i < 4; ++i) {
+            const size_t u = (static_cast<size_t>(kb * 4 + i) * 4 + g) * NC + tokc;
+            bh[i] = frag[u];
+            bm[i] = frag[u + T];
+        }
+#pragma unroll
+        for (int r = 0; r < kPfRT; ++r) {
+            const int rt = min(rt0 + r, m_tiles - 1);
+            const float sc = tscale[static_cast<size_t>(rt) * n_kb + kb];
+            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const i32x4 wv = wl[buf][r][i >> 1][lane];
+                Frag8 a, b;
+                e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[2] : wv[0]), a.u[0], a.u[1]);
+                e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[3] : wv[1]), a.u[2], a.u[3]);
+                b.i = bh[i];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+                b.i = bm[i];
+                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+            }
+            tot[r] += sc * acc;
+        }
+        if (kb + 1 < n_kb) stage_store(buf ^ 1);
+        __syncthreads();
+    }
+
+    // lane (g, col) holds rows 4g .. 4g+3 of each row tile for token `tok`
+    if (tok >= T) return;
+    float* yrow = Y + static_cast<size_t>(tok) * ldy;
+    if constexpr (EPI == 2) {
+#pragma unroll
+        for (int r = 0; r < kPfRT; r += 2) {
+            if (rt0 + r + 1 >= m_tiles) break;
+            const int orow = ((rt0 + r) / 2) * kTileRows + 4 * g;
+#pragma unroll
+            for (int v = 0; v < 4; ++v)
+                if (orow + v < m_valid) yrow[orow + v] = silu_f(tot[r][v]) * tot[r + 1][v];
+        }
+    } else {
+#pragma unroll
+        for (int r = 0; r < kPfRT; ++r) {
+            if (rt0 + r >= m_tiles) break;
+            const int row = (rt0 + r) * kTileRows + 4 * g;
+#pragma unroll
+            for (int v = 0; v < 4; ++v) {
+                if (row + v >= m_valid) break;
+                if constexpr (EPI == 1)
+                    yrow[row + v] += tot[r][v];
+                else
+                    yrow[row + v] = tot[r][v];
+            }
+        }
+    }
+}
+
+}  // namespace
+
+namespace rl {
+
+void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
+                      int ldy, int m_valid, hipStream_t s) {
+    RL_REQUIRE(m > 0 && n > 0 && T >= 1, RL_ERR_RANGE, "gemm_prefill: empty shape");
+    RL_REQUIRE(W && ts && frag && Y, RL_ERR_RANGE, "gemm_prefill: null pointer");
+    RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU, RL_ERR_RANGE,
+               "gemm_prefill: epilogue must be store, add or swiglu");
+    const int m_tiles = (m + kTileRows - 1) / kTileRows;
+    if (epi == kEpiSwiGLU) RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows must be a multiple of 32");
+    const int n_kb = (n + 127) / 128;
+    const dim3 grid((m_tiles + kPfRT - 1) / kPfRT, (T + kPfTok - 1) / kPfTok);
+    RL_REQUIRE(grid.y <= 65535, RL_ERR_RANGE, "gemm_prefill: too many tokens");
+    if (epi == kEpiStore)
+        hipLaunchKernelGGL(gemm_prefill_kernel<0>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
+                           n_kb, T, ldy, m_valid);
+    else if (epi == kEpiAdd)
+        hipLaunchKernelGGL(gemm_prefill_kernel<1>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
+                           n_kb, T, ldy, m_valid);
+    else
+        hipLaunchKernelGGL(gemm_prefill_kernel<2>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
+                           n_kb, T, ldy, m_valid);
+    check_launch("gemm_prefill_kernel");
+}
+
+}  // namespace rl
+
+extern "C" {
+
+int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
+                            int T, int epilogue, int ldy, void* stream) {
+    return guard([&] {
+        const int mv = epilogue == kEpiSwiGLU ? m / 2 : m;
+        rl::gemm_fp8_prefill(w_tiled, tile_scale, frag, Y, m, n, T, epilogue, ldy > 0 ? ldy : mv, mv, S(stream));
+    });
+}
+
+}  // extern "C"

@@ -82,6 +82,21 @@ def linear_T(lin, X: np.ndarray, stream=None) -> np.ndarray:
     return yd.numpy(np.float32, (T, lin.m), stream)
 
 
+def linear_prefill(lin: Fp8Linear, X: np.ndarray, epilogue: int = 0, Y0: np.ndarray | None = None,
+                   stream=None) -> np.ndarray:
+    """Prefill linear over T (any) tokens: Y[T][m'] = W . X (epilogue 0 store, 1 add
+    onto Y0, 2 SwiGLU over interleaved gate/up tiles: m' = m/2)."""
+    X = _f32(X).reshape(-1, lin.n)
+    T = X.shape[0]
+    mo = lin.m // 2 if epilogue == 2 else lin.m
+    xd = DeviceBuffer.from_numpy(X, stream)
+    frag = act_frag_buffer(lin.n, T)
+    yd = DeviceBuffer.from_numpy(_f32(Y0).reshape(T, mo), stream) if Y0 is not None else DeviceBuffer(4 * T * mo)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, lin.n, T, stream)
+    call("rl_hip_gemm_fp8_prefill", lin.w.ptr, lin.ts.ptr, frag.ptr, yd.ptr, lin.m, lin.n, T, epilogue, mo, stream)
+    return yd.numpy(np.float32, (T, mo), stream)
+
+
 def gemv_fp8(W: np.ndarray, scale: np.ndarray, x: np.ndarray, block: int = 128) -> np.ndarray:
     """ops::gemv_fp8(W, scale, x, y, m, n, block) (reference src/kernels/ops.cpp:182)."""
     if block != 128:
