@@ -178,6 +178,18 @@ int rl_hip_embed_rows(const void* table, int kind, const int* tokens_dev, float*
  *   vt_cache element (pos, d): [pos/32][d/16][(pos/8)%4][d%16][pos%8].  head_dim 256,
  * (n_q/n_kv)*T <= 32.  Outputs o * sigmoid(gate): fp32 `out` [T][n_q*hd] and/or
  * o_proj fragments `frag`.  *pos_dev is not modified. */
+/* Prompt prefill of T tokens at positions *pos_dev .. *pos_dev + T - 1: the T tokens'
+ * K (after norm + RoPE) and V are written to the caches, then causal attention of
+ * every token over positions 0 .. its own, out = [T][n_q*256] fp32 times
+ * sigmoid(gate).  One workgroup per (16 tokens, kv head) with an online softmax over
+ * 256-position chunks.  Replaces the reference's prefill attention
+ * (cuda_engine.cu:18338-18590; CPU: per token ops::attn_decode, ops.cpp:575-605). */
+size_t rl_hip_attn_prefill_workspace_bytes(int n_q, int T);
+int rl_hip_attn_prefill_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* k_cache,
+                              uint16_t* vt_cache, int ctx, const int* pos_dev, int T, int n_q, int n_kv, int head_dim,
+                              int rotary_dim, float theta, float eps, void* workspace, size_t workspace_bytes,
+                              float* out, void* stream);
+
 size_t rl_hip_attn_workspace_bytes(int n_kv, int ctx);
 int rl_hip_attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* k_cache,
                              uint16_t* vt_cache, int ctx, const int* pos_dev, int T, int n_q, int n_kv, int head_dim,

@@ -376,6 +376,238 @@ __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
     }
 }
 
+// ------------------------------------------------------------------ prefill
+// Prompt prefill over T tokens at positions p0 .. p0+T-1 (the reference's prefill
+// attention, cuda_engine.cu:18338-18590, causal GQA over the cache): one
+// workgroup per (block of 16 tokens, kv head, group of up to 3 of its G heads)
+// streams the kv head's cache for those heads x 16 tokens, keeping a running max / sum / O per
+// query row across 256-position chunks (online softmax) -- no partials to combine.
+// Per chunk: S^T = K . Q^T (wave w: positions 64w .. 64w+63, hi and lo parts of q
+// in one accumulator), the chunk max and the rescale of O through LDS, P staged
+// as fp16 by position, O^T += V^T . P^T (wave w: dims 64w .. 64w+63).
+
+// grid (nq + 2*nkv, T), 64 threads: norm + RoPE + cache write as qk_prep_kernel; q
+// goes to qp[kv][tb][s][g][q][hi/lo][16 col] (16 B each; col = token % 16).
+__global__ __launch_bounds__(64) void qk_prep_pf_kernel(AttnArgs p, i32x4* __restrict__ qp) {
+    __shared__ float vec[kHD];
+    const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
+    const int pos = *p.pos + t;
+    const float* row = p.Y + static_cast<size_t>(t) * p.ld_y;
+    const int qcols = p.nq * kHD * 2;
+    if (head >= p.nq + p.nkv) {
+        const int kv = head - p.nq - p.nkv;
+        const float* src = row + qcols + p.nkv * kHD + kv * kHD;
+        uint16_t* vb = p.vt + static_cast<size_t>(kv) * p.ctx * kHD;
+        for (int d = lane; d < kHD; d += 64) vb[v_off(pos, d)] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(src[d]));
+        return;
+    }
+    const bool is_q = head < p.nq;
+    const float* src = is_q ? row + static_cast<size_t>(head) * 2 * kHD : row + qcols + (head - p.nq) * kHD;
+    const float* gam = is_q ? p.q_norm : p.k_norm;
+    double ss = 0.0;
+    float x[4];
+#pragma unroll
+    for (int r = 0; r < 4; ++r) {
+        x[r] = src[lane + 64 * r];
+        ss += static_cast<double>(x[r]) * x[r];
+    }
+    ss = wave_sum_d(ss);
+    const float inv = 1.f / sqrtf(static_cast<float>(ss / kHD) + p.eps);
+#pragma unroll
+    for (int r = 0; r < 4; ++r) vec[lane + 64 * r] = x[r] * inv * (gam ? 1.f + gam[lane + 64 * r] : 1.f);
+    __syncthreads();
+    const int half = p.rot / 2;
+    for (int i = lane; i < half; i += 64) {
+        const float freq = 1.f / powf(p.theta, static_cast<float>(i) / static_cast<float>(half));
+        const float ang = static_cast<float>(pos) * freq;
+        const float c = cosf(ang), s = sinf(ang);
+        const float x0 = vec[i], x1 = vec[i + half];
+        vec[i] = x0 * c - x1 * s;
+        vec[i + half] = x0 * s + x1 * c;
+    }
+    __syncthreads();
+    if (!is_q) {
+        const int kv = head - p.nq;
+        uint16_t* kb = p.kc + static_cast<size_t>(kv) * p.ctx * kHD;
+        for (int d = lane; d < kHD; d += 64) kb[k_off(pos, d)] = __builtin_bit_cast(uint16_t, static_cast<_Float16>(vec[d]));
+        return;
+    }
+    const int kv = head / p.G, q = head % p.G;
+    const int ntb = (p.T + 15) / 16, tb = t >> 4, col = t & 15;
+    _Float16* qh = reinterpret_cast<_Float16*>(qp);
+    for (int d = lane; d < kHD; d += 64) {
+        const int s = d >> 5, g = (d >> 3) & 3, e = d & 7;
+        const _Float16 hi = static_cast<_Float16>(vec[d]);
+        const _Float16 lo = static_cast<_Float16>(vec[d] - static_cast<float>(hi));
+        const size_t base = ((((static_cast<size_t>(kv) * ntb + tb) * 8 + s) * 4 + g) * p.G + q) * 2;
+        qh[((base + 0) * 16 + col) * 8 + e] = hi;
+        qh[((base + 1) * 16 + col) * 8 + e] = lo;
+    }
+}
+
+// grid (token blocks, nkv, G / QT), 256 threads.  QT query tiles of 16 tokens per
+// workgroup: tile q = head kv*G + blockIdx.z*QT + q (at most 3, so the score and
+// output accumulators stay in registers).
+// Output o[t][h*hd + d] = softmax(q.K/sqrt(hd)) V * sigmoid(gate).
+template <int QT>
+__global__ __launch_bounds__(256) void attn_prefill_kernel(AttnArgs p, const i32x4* __restrict__ qp,
+                                                            float* __restrict__ out) {
+    const int tb = blockIdx.x, kv = blockIdx.y, q0 = blockIdx.z * QT;
+    const int G = p.G;
+    const int ntb = (p.T + 15) / 16;
+    const int p0 = *p.pos;
+    const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+    const int g = lane >> 4, col = lane & 15;
+    const float scale = 1.f / sqrtf(static_cast<float>(kHD));
+    const int t_last = min(p.T, 16 * tb + 16) - 1;  // last token of the block
+    const int L = p0 + t_last + 1;                   // keys 0 .. L-1 seen by this block
+    const int tcol = 16 * tb + col;                  // token of query column `col`
+    const int qpos = p0 + min(tcol, p.T - 1);        // its position (masked cols: any)
+
+    __shared__ _Float16 P_lds[8][QT][16][40];
+    __shared__ float max_s[4][QT][16];
+    __shared__ float sum_s[4][QT][16];
+
+    const uint16_t* kbase = p.kc + static_cast<size_t>(kv) * p.ctx * kHD;
+    const uint16_t* vbase = p.vt + static_cast<size_t>(kv) * kHD * p.ctx;
+    const i32x4* qbase = qp + (static_cast<size_t>(kv) * ntb + tb) * 8 * 4 * G * 2 * 16;
+
+    f32x4 o[4][QT];
+#pragma unroll
+    for (int a = 0; a < 4; ++a)
+#pragma unroll
+        for (int q = 0; q < QT; ++q) o[a][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+    float Mrun[QT], Lrun[QT];
+#pragma unroll
+    for (int q = 0; q < QT; ++q) {
+        Mrun[q] = -INFINITY;
+        Lrun[q] = 0.f;
+    }
+
+    const int nch = (L + kChunk - 1) / kChunk;
+    for (int chunk = 0; chunk < nch; ++chunk) {
+        const int c0 = chunk * kChunk;
+        f32x4 acc[4][QT];
+#pragma unroll
+        for (int a = 0; a < 4; ++a)
+#pragma unroll
+            for (int q = 0; q < QT; ++q) acc[a][q] = f32x4{0.f, 0.f, 0.f, 0.f};
+        for (int s = 0; s < 8; ++s) {
+            H8 a4[4];
+#pragma unroll
+            for (int pt = 0; pt < 4; ++pt) {
+                const int ptile = c0 + 16 * (4 * wave + pt) < L ? 4 * wave + pt : 0;
+                a4[pt].i = reinterpret_cast<const i32x4*>(kbase + ((static_cast<size_t>(chunk) * 8 + s) * 16 + ptile) * 512)[lane];
+            }
+#pragma unroll
+            for (int q = 0; q < QT; ++q) {
+                H8 bh, bl;
+                const i32x4* qq = qbase + ((static_cast<size_t>(s) * 4 + g) * G + q0 + q) * 2 * 16 + col;
+                bh.i = qq[0];
+                bl.i = qq[16];
+#pragma unroll
+                for (int pt = 0; pt < 4; ++pt) {
+                    acc[pt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a4[pt].v, bh.v, acc[pt][q], 0, 0, 0);
+                    acc[pt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a4[pt].v, bl.v, acc[pt][q], 0, 0, 0);
+                }
+            }
+        }
+        // masked scores and this wave's max per query column
+        float mx[QT];
+#pragma unroll
+        for (int q = 0; q < QT; ++q) mx[q] = -INFINITY;
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+            for (int q = 0; q < QT; ++q)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int pos = c0 + 64 * wave + 16 * pt + 4 * g + v;
+                    const float val = pos <= qpos ? acc[pt][q][v] * scale : -INFINITY;
+                    acc[pt][q][v] = val;
+                    mx[q] = fmaxf(mx[q], val);
+                }
+#pragma unroll
+        for (int q = 0; q < QT; ++q) {
+            mx[q] = fmaxf(mx[q], __shfl_xor(mx[q], 16, 64));
+            mx[q] = fmaxf(mx[q], __shfl_xor(mx[q], 32, 64));
+            if (g == 0) max_s[wave][q][col] = mx[q];
+        }
+        __syncthreads();
+        float Mn[QT], alpha[QT], sum[QT];
+#pragma unroll
+        for (int q = 0; q < QT; ++q) {
+            const float mc = fmaxf(fmaxf(max_s[0][q][col], max_s[1][q][col]), fmaxf(max_s[2][q][col], max_s[3][q][col]));
+            Mn[q] = fmaxf(Mrun[q], mc);
+            alpha[q] = Mn[q] == -INFINITY ? 1.f : expf(Mrun[q] - Mn[q]);
+            sum[q] = 0.f;
+        }
+#pragma unroll
+        for (int pt = 0; pt < 4; ++pt)
+#pragma unroll
+            for (int q = 0; q < QT; ++q)
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const int pl = 64 * wave + 16 * pt + 4 * g + v;
+                    const float e = Mn[q] == -INFINITY ? 0.f : expf(acc[pt][q][v] - Mn[q]);
+                    sum[q] += e;
+                    P_lds[pl >> 5][q][col][pl & 31] = static_cast<_Float16>(e);
+                }
+#pragma unroll
+        for (int q = 0; q < QT; ++q) {
+            sum[q] += __shfl_xor(sum[q], 16, 64);
+            sum[q] += __shfl_xor(sum[q], 32, 64);
+            if (g == 0) sum_s[wave][q][col] = sum[q];
+        }
+        __syncthreads();
+        // rescale the running output and sum, then O^T += V^T . P^T
+#pragma unroll
+        for (int q = 0; q < QT; ++q) {
+            Lrun[q] = Lrun[q] * alpha[q] + ((sum_s[0][q][col] + sum_s[1][q][col]) + (sum_s[2][q][col] + sum_s[3][q][col]));
+            Mrun[q] = Mn[q];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt) o[dt][q] *= alpha[q];
+        }
+        for (int u = 0; u < 8; ++u) {
+            const int grp = 32 * ((c0 >> 5) + u) < L ? (c0 >> 5) + u : (c0 >> 5);
+            H8 va[4];
+#pragma unroll
+            for (int dt = 0; dt < 4; ++dt)
+                va[dt].i = reinterpret_cast<const i32x4*>(vbase + (static_cast<size_t>(grp) * 16 + 4 * wave + dt) * 512)[lane];
+#pragma unroll
+            for (int q = 0; q < QT; ++q) {
+                H8 bp;
+                bp.i = *reinterpret_cast<const i32x4*>(&P_lds[u][q][col][8 * g]);
+#pragma unroll
+                for (int dt = 0; dt < 4; ++dt)
+                    o[dt][q] = __builtin_amdgcn_mfma_f32_16x16x32_f16(va[dt].v, bp.v, o[dt][q], 0, 0, 0);
+            }
+        }
+        __syncthreads();  // P_lds / max_s / sum_s are rewritten by the next chunk
+    }
+
+    // lane (g, col) holds dims 64*wave + 16*dt + 4g + v of query column col
+    if (tcol >= p.T) return;
+    const int n = p.nq * kHD;
+#pragma unroll
+    for (int q = 0; q < QT; ++q) {
+        const int h = kv * G + q0 + q;
+        const float inv = 1.f / Lrun[q];
+        const float* gate = p.Y + static_cast<size_t>(tcol) * p.ld_y + static_cast<size_t>(h) * 2 * kHD + kHD;
+        float* dst = out + static_cast<size_t>(tcol) * n + static_cast<size_t>(h) * kHD;
+#pragma unroll
+        for (int dt = 0; dt < 4; ++dt) {
+            const int d0 = 64 * wave + 16 * dt + 4 * g;
+            float4 r;
+            r.x = o[dt][q][0] * inv * sigmoid_f(gate[d0]);
+            r.y = o[dt][q][1] * inv * sigmoid_f(gate[d0 + 1]);
+            r.z = o[dt][q][2] * inv * sigmoid_f(gate[d0 + 2]);
+            r.w = o[dt][q][3] * inv * sigmoid_f(gate[d0 + 3]);
+            *reinterpret_cast<float4*>(dst + d0) = r;
+        }
+    }
+}
+
 }  // namespace
 
 namespace rl {
@@ -441,6 +673,53 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     check_launch("attn_comb_kernel");
 }
 
+
+size_t attn_prefill_workspace_bytes(int nq, int T) {
+    return static_cast<size_t>(nq) * ((T + 15) / 16) * 16 * kHD * 2 * 2 + 256;
+}
+
+void attn_prefill_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc,
+                        uint16_t* vt, int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot,
+                        float theta, float eps, void* ws, size_t ws_bytes, float* out, hipStream_t s) {
+    RL_REQUIRE(hd == kHD, RL_ERR_UNSUPPORTED, "attn prefill: head_dim must be 256");
+    RL_REQUIRE(nkv > 0 && nq % nkv == 0, RL_ERR_RANGE, "attn prefill: n_q must be a multiple of n_kv");
+    const int G = nq / nkv;
+    RL_REQUIRE(G >= 1 && G <= 8, RL_ERR_UNSUPPORTED, "attn prefill: n_q/n_kv must be in 1..8");
+    RL_REQUIRE(T >= 1 && T <= 65535 * 16, RL_ERR_RANGE, "attn prefill: bad token count");
+    RL_REQUIRE(ctx > 0 && ctx % kChunk == 0, RL_ERR_RANGE, "attn prefill: cache capacity must be a multiple of 256");
+    RL_REQUIRE(rot >= 2 && rot % 2 == 0 && rot <= hd, RL_ERR_RANGE, "attn prefill: bad rotary dim");
+    RL_REQUIRE(Y && kc && vt && pos_dev && ws && out, RL_ERR_RANGE, "attn prefill: null pointer");
+    RL_REQUIRE(ws_bytes >= attn_prefill_workspace_bytes(nq, T), RL_ERR_RANGE, "attn prefill: workspace too small");
+    AttnArgs p{};
+    p.Y = Y;
+    p.ld_y = ld_y;
+    p.q_norm = q_norm;
+    p.k_norm = k_norm;
+    p.kc = kc;
+    p.vt = vt;
+    p.ctx = ctx;
+    p.pos = pos_dev;
+    p.T = T;
+    p.nq = nq;
+    p.nkv = nkv;
+    p.G = G;
+    p.rot = rot;
+    p.theta = theta;
+    p.eps = eps;
+    i32x4* qp = static_cast<i32x4*>(ws);
+    hipLaunchKernelGGL(qk_prep_pf_kernel, dim3(nq + 2 * nkv, T), dim3(64), 0, s, p, qp);
+    check_launch("qk_prep_pf_kernel");
+    // query tiles per workgroup: 3, 2 or 1 (a divisor of G; four spill registers)
+    const int QT = G % 3 == 0 ? 3 : G % 2 == 0 ? 2 : 1;
+    const dim3 grid((T + 15) / 16, nkv, G / QT);
+    switch (QT) {
+    case 3: hipLaunchKernelGGL(attn_prefill_kernel<3>, grid, dim3(256), 0, s, p, qp, out); break;
+    case 2: hipLaunchKernelGGL(attn_prefill_kernel<2>, grid, dim3(256), 0, s, p, qp, out); break;
+    default: hipLaunchKernelGGL(attn_prefill_kernel<1>, grid, dim3(256), 0, s, p, qp, out); break;
+    }
+    check_launch("attn_prefill_kernel");
+}
+
 }  // namespace rl
 
 extern "C" {
@@ -454,6 +733,18 @@ int rl_hip_attn_decode_layer(const float* Y, int ld_y, const float* q_norm, cons
     return guard([&] {
         rl::attn_decode_layer(Y, ld_y, q_norm, k_norm, k_cache, vt_cache, ctx, pos_dev, T, n_q, n_kv, head_dim,
                               rotary_dim, theta, eps, workspace, workspace_bytes, out, frag, S(stream));
+    });
+}
+
+size_t rl_hip_attn_prefill_workspace_bytes(int n_q, int T) { return rl::attn_prefill_workspace_bytes(n_q, T); }
+
+int rl_hip_attn_prefill_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* k_cache,
+                              uint16_t* vt_cache, int ctx, const int* pos_dev, int T, int n_q, int n_kv, int head_dim,
+                              int rotary_dim, float theta, float eps, void* workspace, size_t workspace_bytes,
+                              float* out, void* stream) {
+    return guard([&] {
+        rl::attn_prefill_layer(Y, ld_y, q_norm, k_norm, k_cache, vt_cache, ctx, pos_dev, T, n_q, n_kv, head_dim,
+                               rotary_dim, theta, eps, workspace, workspace_bytes, out, S(stream));
     });
 }
 

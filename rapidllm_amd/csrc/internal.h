@@ -139,6 +139,13 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
                        void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s, int t_off = 0,
                        int T_out = 0);
 
+// Prompt prefill of T tokens at *pos_dev .. *pos_dev + T - 1: K/V of all T written to
+// the cache, causal attention over the cache, out [T][nq*hd] fp32 (times sigmoid(gate)).
+size_t attn_prefill_workspace_bytes(int nq, int T);
+void attn_prefill_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc,
+                        uint16_t* vt, int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot,
+                        float theta, float eps, void* ws, size_t ws_bytes, float* out, hipStream_t s);
+
 // sample.hip
 size_t argmax_workspace_bytes(int rows, int V);
 void argmax_rows(const float* logits, int rows, int V, int* out, float* out_val, void* ws, hipStream_t s);

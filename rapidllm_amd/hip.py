@@ -60,6 +60,9 @@ _SIGS = {
     "rl_hip_gated_rmsnorm_pack": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, C.c_float, _vp]),
     "rl_hip_embed_rows": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),
     "rl_hip_attn_workspace_bytes": (_sz, [_i, _i]),
+    "rl_hip_attn_prefill_workspace_bytes": (_sz, [_i, _i]),
+    "rl_hip_attn_prefill_layer": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, C.c_float,
+                                       C.c_float, _vp, _sz, _vp, _vp]),
     "rl_hip_attn_decode_layer": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _i, _vp, _i, _i, _i, _i, _i, C.c_float, C.c_float,
                                       _vp, _sz, _vp, _vp, _vp]),
     "rl_hip_argmax_workspace_bytes": (_sz, [_i, _i]),

@@ -307,6 +307,24 @@ def attn_decode_layer(Y, cache: AttnCache, pos: int, q_norm, k_norm, n_q, n_kv, 
     return d_out.numpy(np.float32, (T, n_q * hd))
 
 
+def attn_prefill_layer(Y, cache: AttnCache, pos: int, q_norm, k_norm, n_q, n_kv, rotary_dim=64, theta=1e7,
+                       eps=1e-6):
+    """Prefill attention for T (any) tokens at positions pos..pos+T-1 (their K/V are
+    written to `cache`); returns o*sigmoid(gate) [T][n_q*hd]."""
+    Y = _f32(np.atleast_2d(Y))
+    T, ld = Y.shape
+    hd = cache.hd
+    d_Y = DeviceBuffer.from_numpy(Y)
+    d_qn = DeviceBuffer.from_numpy(_f32(q_norm))
+    d_kn = DeviceBuffer.from_numpy(_f32(k_norm))
+    d_pos = DeviceBuffer.from_numpy(np.array([pos], np.int32))
+    ws = DeviceBuffer(hip.lib().rl_hip_attn_prefill_workspace_bytes(n_q, T))
+    d_out = DeviceBuffer(4 * T * n_q * hd)
+    call("rl_hip_attn_prefill_layer", d_Y.ptr, ld, d_qn.ptr, d_kn.ptr, cache.k.ptr, cache.vt.ptr, cache.ctx,
+         d_pos.ptr, T, n_q, n_kv, hd, rotary_dim, theta, eps, ws.ptr, ws.nbytes, d_out.ptr, None)
+    return d_out.numpy(np.float32, (T, n_q * hd))
+
+
 # ------------------------------------------------------------------ sampling
 
 

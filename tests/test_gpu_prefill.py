@@ -84,3 +84,46 @@ def test_gemm_prefill_matches_decode_gemm(gpu):
     a = ops.linear_prefill(lin, X)
     b = ops.linear_T(lin, X)
     assert rel_l2(a, b) <= 1e-5
+
+
+@pytest.mark.parametrize("T,pos,nq,nkv", [(1, 0, 24, 4), (16, 0, 24, 4), (37, 300, 24, 4), (100, 1000, 24, 4),
+                                          (70, 250, 4, 2), (33, 17, 2, 2)])
+def test_attn_prefill_vs_oracle(gpu, orc, T, pos, nq, nkv):
+    """Causal prefill attention: every token over the cache and the earlier prompt
+    tokens, against the per-token oracle (fp16 K/V as the device cache holds them)."""
+    from tests.test_gpu_layers import _attn_oracle
+    r = synth.rng(60 + pos + T + nq)
+    hd = 256
+    ctx = ((pos + T + 255) // 256) * 256 + 256
+    Y = r.standard_normal((T, 2 * nq * hd + 2 * nkv * hd)).astype(np.float32)
+    qn = (r.standard_normal(hd) * 0.1).astype(np.float32)
+    kn = (r.standard_normal(hd) * 0.1).astype(np.float32)
+    K = r.standard_normal((pos, nkv, hd)).astype(np.float16).astype(np.float32)
+    V = r.standard_normal((pos, nkv, hd)).astype(np.float16).astype(np.float32)
+    cache = ops.AttnCache(nkv, ctx, hd)
+    if pos:
+        cache.fill(K, V)
+    out = ops.attn_prefill_layer(Y, cache, pos, qn, kn, nq, nkv)
+    want = _attn_oracle(orc, Y, K, V, pos, qn, kn, nq, nkv)
+    for t in range(T):
+        assert rel_l2(out[t], want[t]) < 1e-3, (t, rel_l2(out[t], want[t]))
+
+
+def test_attn_prefill_then_decode(gpu, orc):
+    """K/V written by the prefill serve a following decode step: decode at the next
+    position after a prefill equals the oracle over the whole sequence."""
+    from tests.test_gpu_layers import _attn_oracle
+    r = synth.rng(99)
+    nq, nkv, hd, pos, T = 24, 4, 256, 200, 40
+    ctx = 512
+    Y = r.standard_normal((T + 1, 2 * nq * hd + 2 * nkv * hd)).astype(np.float32)
+    qn = (r.standard_normal(hd) * 0.1).astype(np.float32)
+    kn = (r.standard_normal(hd) * 0.1).astype(np.float32)
+    K = r.standard_normal((pos, nkv, hd)).astype(np.float16).astype(np.float32)
+    V = r.standard_normal((pos, nkv, hd)).astype(np.float16).astype(np.float32)
+    cache = ops.AttnCache(nkv, ctx, hd)
+    cache.fill(K, V)
+    ops.attn_prefill_layer(Y[:T], cache, pos, qn, kn, nq, nkv)
+    got = ops.attn_decode_layer(Y[T:], cache, pos + T, qn, kn, nq, nkv)
+    want = _attn_oracle(orc, Y, K, V, pos, qn, kn, nq, nkv)
+    assert rel_l2(got[0], want[T]) < 1e-3
