@@ -179,12 +179,149 @@ class Engine {
         check_ids(ids, n);
         reset();
         upload_ints(tok_all_, ids, n);
-        for (int i = 0; i < n; i += tmax_) {
+        // all but the last (up to max_T) tokens through the chunked prefill path; the
+        // tail runs as a decode step, which leaves the logits, the next token, the MTP
+        // history and the speculative bookkeeping exactly as decoding would
+        int done = 0;
+        const int tail = std::min(tmax_, n);
+        if (n - tail >= kPfMinTokens && can_prefill_chunked()) {
+            prefill_chunks(n - tail);
+            done = n - tail;
+        }
+        for (int i = done; i < n; i += tmax_) {
             const int T = std::min(tmax_, n - i);
             RL_HIP(hipMemcpyAsync(tok_, tok_all_ + i, T * sizeof(int), hipMemcpyDeviceToDevice, st_));
             step(T, /*force_all=*/1, /*feed=*/false);
         }
         readback();
+    }
+
+    // ---------------------------------------------------------------- prefill
+    // Chunked prompt prefill (the reference's launch_prefill_chunk,
+    // cuda_engine.cu:18338-18590): per chunk of up to kPfChunk tokens, layer by
+    // layer, the block-FP8 linears run over all chunk tokens on the matrix cores
+    // (gemm_fp8_prefill), the DeltaNet recurrence steps the committed state through
+    // the chunk in sub-chunks of 8 tokens (direct mode, conv window ping-ponging
+    // between ring slots 0 and 1), attention is the causal prefill kernel (which
+    // also writes the chunk's K/V).  RMSNorms are explicit (norm + pack kernels).
+    static constexpr int kPfChunk = 512;
+    static constexpr int kPfMinTokens = 16;
+    static constexpr int kPfSub = 8;
+    int pf_cap_ = 0;
+    float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr;
+    void *pf_frag_ = nullptr, *pf_frag_h_ = nullptr, *pf_attn_ws_ = nullptr;
+    size_t pf_attn_ws_bytes_ = 0;
+    int* pf_pos_ = nullptr;
+    std::unique_ptr<DevAlloc> pf_mem_;
+
+    // RL_PREFILL_CHUNK: 0 = every prompt token through decode steps (T <= max_T);
+    // n > 0 = chunk size (default kPfChunk)
+    static int pf_chunk_setting() {
+        static const int v = [] {
+            const char* e = std::getenv("RL_PREFILL_CHUNK");
+            return e ? std::max(0, std::atoi(e)) : kPfChunk;
+        }();
+        return v;
+    }
+
+    bool can_prefill_chunked() const {
+        if (pf_chunk_setting() == 0) return false;
+        auto fp8 = [](const Lin& L) { return L.kind == RL_Q_FP8_E4M3_B128; };
+        if (!fp8(lm_head_) && lm_head_.kind != RL_Q_BF16) return false;
+        for (const Layer& Ly : L_) {
+            if (Ly.kind == RL_LAYER_DELTA) {
+                if (!gdn_fused_norm_ || Ly.in_parts.size() != 1 || !fp8(Ly.in_parts[0]) || !fp8(Ly.out_proj)) return false;
+            } else if (Ly.qkv_parts.size() != 1 || !fp8(Ly.qkv_parts[0]) || !fp8(Ly.o_proj)) {
+                return false;
+            }
+            if (Ly.gate_up.kind != RL_Q_FP8_E4M3_B128 || !fp8(Ly.down)) return false;
+        }
+        return c_.hidden % 8 == 0;
+    }
+
+    void ensure_pf_buffers(int C) {
+        if (pf_cap_ >= C) return;
+        pf_mem_ = std::make_unique<DevAlloc>();
+        const int H = c_.hidden, I = c_.intermediate;
+        int wy = 16, wo = 16, wf = H;
+        for (const Layer& Ly : L_) {
+            wy = std::max(wy, Ly.kind == RL_LAYER_DELTA ? Ly.in_width : Ly.qkv_width);
+            wo = std::max(wo, Ly.kind == RL_LAYER_DELTA ? c_.n_v_heads * c_.v_dim : c_.n_q * c_.head_dim);
+        }
+        wf = std::max(wf, wo);
+        pf_x_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * H);
+        pf_y_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * wy);
+        pf_o_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * wo);
+        pf_h_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * I);
+        pf_frag_ = pf_mem_->get(act_frag_bytes(wf, C));
+        pf_frag_h_ = pf_mem_->get(act_frag_bytes(I, C));
+        pf_attn_ws_bytes_ = attn_prefill_workspace_bytes(std::max(c_.n_q, 1), C);
+        pf_attn_ws_ = pf_mem_->get(pf_attn_ws_bytes_);
+        pf_pos_ = pf_mem_->get_n<int>(64);
+        pf_cap_ = C;
+    }
+
+    // Tokens tok_all_[0 .. N) at positions 0 .. N-1 from the reset state; leaves the
+    // KV caches, the DeltaNet states and conv windows after token N-1, and the
+    // position / ring slot scalars for the next step.
+    void prefill_chunks(int N) {
+        const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim, I = c_.intermediate;
+        const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim;
+        const float eps = c_.rms_eps;
+        const int C = std::min(pf_chunk_setting(), N);
+        ensure_pf_buffers(C);
+        // the prompt's upload reads the pinned stage that the positions below reuse
+        RL_HIP(hipStreamSynchronize(st_));
+        int slot = 0;  // conv ring slot holding the window (reset: 0)
+        for (int c0 = 0; c0 < N; c0 += C) {
+            const int T = std::min(C, N - c0);
+            upload_ints(pf_pos_, &c0, 1);
+            embed_rows(embed_, embed_kind_, tok_all_ + c0, pf_x_, H, c_.vocab, T, st_);
+            const int nsub = (T + kPfSub - 1) / kPfSub;
+            for (int i = 0; i < c_.n_layers; ++i) {
+                Layer& Ly = L_[i];
+                rmsnorm_pack(pf_x_, H, Ly.attn_norm, nullptr, pf_frag_, H, T, eps, st_);
+                if (Ly.kind == RL_LAYER_DELTA) {
+                    const Lin& in = Ly.in_parts[0];
+                    gemm_fp8_prefill(in.w, in.ts, pf_frag_, pf_y_, in.m, H, T, kEpiStore, Ly.in_width, in.m, st_);
+                    float* ring = slot_conv(Ly.dslot);
+                    int sl = slot;
+                    for (int k = 0; k < nsub; ++k) {
+                        const int Ts = std::min(kPfSub, T - k * kPfSub);
+                        gdn_decode_fused(pf_y_, pf_y_ + Ly.off_a, pf_y_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
+                                         Ly.conv_w, ring + sl * conv_slot_, ring + (sl ^ 1) * conv_slot_,
+                                         slot_S(Ly.dslot), slot_S(Ly.dslot), nullptr, 0, R_, nullptr, pf_o_, nullptr,
+                                         nullptr, nullptr, nullptr, Ts, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled,
+                                         st_, 1, 0, nullptr, k * kPfSub, T);
+                        sl ^= 1;
+                    }
+                    gnorm_pack(pf_o_, pf_y_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, nullptr, pf_frag_, zdim, T,
+                               1e-6f, st_);
+                    gemm_fp8_prefill(Ly.out_proj.w, Ly.out_proj.ts, pf_frag_, pf_x_, Ly.out_proj.m, zdim, T, kEpiAdd,
+                                     H, H, st_);
+                } else {
+                    const Lin& q = Ly.qkv_parts[0];
+                    gemm_fp8_prefill(q.w, q.ts, pf_frag_, pf_y_, q.m, H, T, kEpiStore, Ly.qkv_width, q.m, st_);
+                    attn_prefill_layer(pf_y_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot),
+                                       ctx_, pf_pos_, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, pf_attn_ws_,
+                                       pf_attn_ws_bytes_, pf_o_, st_);
+                    pack_act(pf_o_, pf_frag_, nq * hd, T, st_);
+                    gemm_fp8_prefill(Ly.o_proj.w, Ly.o_proj.ts, pf_frag_, pf_x_, Ly.o_proj.m, nq * hd, T, kEpiAdd, H,
+                                     H, st_);
+                }
+                rmsnorm_pack(pf_x_, H, Ly.ffn_norm, nullptr, pf_frag_, H, T, eps, st_);
+                gemm_fp8_prefill(Ly.gate_up.w, Ly.gate_up.ts, pf_frag_, pf_h_, Ly.gate_up.m, H, T, kEpiSwiGLU, I, I,
+                                 st_);
+                pack_act(pf_h_, pf_frag_h_, I, T, st_);
+                gemm_fp8_prefill(Ly.down.w, Ly.down.ts, pf_frag_h_, pf_x_, Ly.down.m, I, T, kEpiAdd, H, H, st_);
+            }
+            slot ^= nsub & 1;
+            RL_HIP(hipStreamSynchronize(st_));  // the pinned position stage is reused by the next chunk
+        }
+        const int scal[2] = {N, slot};  // kPos, kSlot
+        upload_ints(sc() + kPos, scal, 2);
+        RL_HIP(hipStreamSynchronize(st_));
+        pos_ = N;
     }
 
     void decode_token(int32_t token) {

@@ -264,6 +264,9 @@ struct GdnFusedArgs {
     float* gss;          // [nv][T][4] partial sums of o^2 (with frag)
     GdnRecords rec;      // rec.rec == nullptr: no records (direct mode)
     GdnBatch batch;
+    // token rows: this call's tokens are rows row_off .. row_off + T - 1 of T_rows
+    // (prompt prefill: sub-chunks of a chunk; 0: B * T rows, sequence b at b * T)
+    int row_off = 0, T_rows = 0;
 };
 
 __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
@@ -285,7 +288,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     // sequence of the batch: state / ring / records / scalars at its strides, its
     // tokens are rows row0 .. row0 + T - 1 of T_tot
     const int bs = blockIdx.y;
-    const int T_tot = a.batch.B * T, row0 = bs * T;
+    const int T_tot = a.T_rows ? a.T_rows : a.batch.B * T, row0 = a.row_off + bs * T;
     const float* S_in = p.S_in + bs * a.batch.s_stride;
     float* S_out = p.S_out + bs * a.batch.s_stride;
     const float* conv_base = p.conv_in + bs * a.batch.conv_stride;
@@ -552,7 +555,7 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices,
-                      int ab_ld, const GdnBatch* batch) {
+                      int ab_ld, const GdnBatch* batch, int row_off, int T_rows) {
     RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED,
                "gdn_decode_fused: dk 128, dv a multiple of 32, conv 4");
     RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: T must be in 1..8");
@@ -576,7 +579,11 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                    static_cast<i32x4*>(frag),
                    gss,
                    rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0, 0},
-                   batch ? *batch : GdnBatch{}};
+                   batch ? *batch : GdnBatch{},
+                   row_off,
+                   T_rows};
+    RL_REQUIRE(T_rows == 0 || (p.batch.B == 1 && row_off >= 0 && row_off + T <= T_rows), RL_ERR_RANGE,
+               "gdn_decode_fused: token rows out of range");
     RL_REQUIRE(p.batch.B >= 1 && p.batch.B * T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: batch x T must be <= 8");
     RL_REQUIRE(p.batch.B == 1 || cur, RL_ERR_RANGE, "gdn_decode_fused: a batch needs the conv ring");
     hipLaunchKernelGGL(gdn_fused_kernel, dim3(nv * (dv / kCW), p.batch.B), dim3(kCT), 0, s, p);

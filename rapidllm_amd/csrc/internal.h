@@ -128,7 +128,7 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices = 1,
-                      int ab_ld = 0, const GdnBatch* batch = nullptr);
+                      int ab_ld = 0, const GdnBatch* batch = nullptr, int row_off = 0, int T_rows = 0);
 
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);

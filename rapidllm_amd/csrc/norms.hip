@@ -207,7 +207,7 @@ void copy_int(const int* src, int* dst, hipStream_t s) {
 
 void residual_rmsnorm_pack(const float* x_in, const float* P, int S, float* x_out, const float* gamma, float* y,
                            void* frag, int n, int T, float eps, hipStream_t s) {
-    RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "rmsnorm: n % 8 == 0, T in 1..8");
+    RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 65535, RL_ERR_RANGE, "rmsnorm: n % 8 == 0, T in 1..65535");
     RL_REQUIRE(x_in && (y || frag || x_out), RL_ERR_RANGE, "rmsnorm: null pointer");
     RL_REQUIRE(x_out != x_in, RL_ERR_RANGE, "rmsnorm: residual output must not alias the input");
     RL_REQUIRE(!P || (S >= 1 && S <= kNormMaxSplit), RL_ERR_RANGE, "rmsnorm: 1..4 partial slices");
@@ -219,7 +219,7 @@ void residual_rmsnorm_pack(const float* x_in, const float* P, int S, float* x_ou
 
 void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,
                   hipStream_t s) {
-    RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "rmsnorm_pack: n % 8 == 0, T in 1..8");
+    RL_REQUIRE(n > 0 && n % 8 == 0 && T >= 1 && T <= 65535, RL_ERR_RANGE, "rmsnorm_pack: n % 8 == 0, T in 1..65535");
     RL_REQUIRE(x && (y || frag), RL_ERR_RANGE, "rmsnorm_pack: null pointer");
     RL_REQUIRE(ld_x % 4 == 0, RL_ERR_RANGE, "rmsnorm_pack: row stride must be a multiple of 4");
     RL_REQUIRE(((n + kBlockCols - 1) / kBlockCols) * 16 <= kNormMaxUnits, RL_ERR_RANGE, "rmsnorm: n > 16384");
@@ -233,7 +233,7 @@ void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, in
     if (gamma_n <= 0) gamma_n = n;
     const bool per_head = gamma_n < n && n % gamma_n == 0 && n >= 256;
     const int seg = per_head ? gamma_n : n;
-    RL_REQUIRE(seg % 8 == 0 && T >= 1 && T <= 8, RL_ERR_RANGE, "gnorm_pack: segment % 8 == 0, T in 1..8");
+    RL_REQUIRE(seg % 8 == 0 && T >= 1 && T <= 65535, RL_ERR_RANGE, "gnorm_pack: segment % 8 == 0, T in 1..65535");
     RL_REQUIRE(o && z && (y || frag), RL_ERR_RANGE, "gnorm_pack: null pointer");
     hipLaunchKernelGGL(gnorm_pack_kernel, dim3(n / seg, T), dim3(64), 0, s, o, z, ld_z, gamma, gamma_n,
                        per_head ? 1 : 0, y, static_cast<i32x4*>(frag), n, T, eps);

@@ -127,3 +127,36 @@ def test_attn_prefill_then_decode(gpu, orc):
     got = ops.attn_decode_layer(Y[T:], cache, pos + T, qn, kn, nq, nkv)
     want = _attn_oracle(orc, Y, K, V, pos, qn, kn, nq, nkv)
     assert rel_l2(got[0], want[T]) < 1e-3
+
+
+def test_engine_chunked_prefill_matches_oracle(gpu, orc):
+    """A 600-token prompt: two prefill chunks (512 + 84) through the chunked path,
+    the last max_T tokens as a decode step; logits equal the oracle's, decoding and
+    speculative generation continue exactly as from a token-by-token prefill."""
+    from oracle.oracle import OracleModel
+    from rapidllm_amd import model as M
+    from rapidllm_amd.engine import Engine
+    from tests.test_gpu_engine import margin_ok, mini_spec
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=3, w_scale=(1e-3, 1e-2))
+    eng = Engine(spec, W, ctx=1024)
+    orc_m = OracleModel(spec, W, ctx=1024)
+    rng = np.random.default_rng(5)
+    prompt = [int(t) for t in rng.integers(0, spec.vocab, 600)]
+    eng.prefill(prompt)
+    orc_m.reset()
+    for t in prompt:
+        g, lg, hd = orc_m.decode(t)
+    assert rel_l2(eng.copy_logits(), lg) < 1e-3
+    assert rel_l2(eng.copy_last_hidden(), hd) < 1e-3
+    if margin_ok(lg):
+        assert eng.greedy() == g
+    tok = g
+    for _ in range(4):
+        eng.decode_token(tok)
+        g, lg, _ = orc_m.decode(tok)
+        assert rel_l2(eng.copy_logits(), lg) < 1e-3
+        tok = g
+    want, _, _ = orc_m.generate(prompt, 8)
+    got, _, _ = eng.generate(prompt, 8, spec_n=3)
+    assert got == want
