@@ -30,6 +30,7 @@ sys.path.insert(0, ROOT)
 METRIC = "decode tok/s at T=1 and MTP-verify T=4; achieved HBM GB/s vs MI355X peak"
 PEAK_GBS = 8000.0
 CTX = 32768
+PF_TOKENS = 4096
 
 
 def step_bytes(spec, T, ctx):
@@ -429,6 +430,8 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only the block-FP8 GEMM launch mix (the roofline kernel), for counter runs")
+    ap.add_argument("--prefill-only", type=int, default=0,
+                    help="time only a prompt prefill of this many tokens (for kernel traces)")
     ap.add_argument("--configs-only", action="store_true",
                     help="run only the per-config kernel lines (configs 1-4), for kernel traces")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -460,6 +463,17 @@ def main():
             cfg["cpu"] = cpu_configs(spec)
         print(json.dumps(cfg))
         return
+    if args.prefill_only:
+        eng = Engine(spec, None, ctx=max(CTX, args.prefill_only) + 4096, max_T=4, seed=1234)
+        ids = np.random.default_rng(3).integers(0, spec.vocab, args.prefill_only).astype(np.int32)
+        eng.prefill(ids[:600])
+        t0 = time.perf_counter()
+        eng.prefill(ids)
+        pf_s = time.perf_counter() - t0
+        eng.close()
+        print(json.dumps({"prefill_tokens": args.prefill_only, "prefill_ms": round(pf_s * 1e3, 1),
+                          "prefill_tok_s": round(args.prefill_only / pf_s, 1)}))
+        return
     t0 = time.time()
     eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=4)
     build_s = time.time() - t0
@@ -485,6 +499,12 @@ def main():
     eng.replicate_slot0(4)
     eng.time_batch(4, W)
     tb4 = eng.time_batch(4, K) / K
+    # prompt prefill (chunked path: 512-token chunks on the prefill GEMM / attention)
+    ids = np.random.default_rng(3).integers(0, spec.vocab, PF_TOKENS).astype(np.int32)
+    eng.prefill(ids[:600])  # buffers and first-use costs outside the timed call
+    t0 = time.perf_counter()
+    eng.prefill(ids)
+    pf_s = time.perf_counter() - t0
     eng.close()
 
     b1 = step_bytes(spec, 1, CTX)
@@ -518,6 +538,10 @@ def main():
         "spec_tok_s_full_accept": round(4000.0 / (t4 + tm), 3),
         "batch4_step_ms": round(tb4, 4),
         "batch4_tok_s": round(4000.0 / tb4, 3),
+        "prefill_tokens": PF_TOKENS,
+        "prefill_ms": round(pf_s * 1e3, 1),
+        "prefill_tok_s": round(PF_TOKENS / pf_s, 1),
+        "prefill_speedup_vs_verify_chunks": round((PF_TOKENS / pf_s) / (4000.0 / t4), 2),
         "step_roofline": {"t1_bytes": b1["total"], "t1_GBps": round(b1["total"] / t1 / 1e6, 1),
                           "t1_frac": round(b1["total"] / t1 / 1e6 / PEAK_GBS, 4),
                           "t4_bytes": b4["total"], "t4_GBps": round(b4["total"] / t4 / 1e6, 1),

@@ -147,6 +147,19 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k,
                       int v_tiled, void* stream);
 
+/* Prompt prefill of T tokens (any T) for one DeltaNet layer, from the in_proj rows y
+ * [T][ld] (qkv channels at 0, a at off_a, b at off_b): conv window conv_in ->
+ * conv_out (window after the last token; must not alias), S (transposed, as
+ * rl_hip_gdn_decode) updated in place, o [T][nv*dv] raw recurrent output.  Workspace
+ * rl_hip_gdn_prefill_workspace_bytes(T, ...).  dk 128, dv a multiple of 32, conv 4.
+ * Replaces the reference's prefill conv + scan (cuda_engine.cu:18338-18590;
+ * CPU: per token ops::conv1d_update + delta_recurrent_step, ops.cpp:458-534). */
+size_t rl_hip_gdn_prefill_workspace_bytes(int T, int nk, int nv, int dk, int dv);
+int rl_hip_gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
+                       const float* conv_w, const float* conv_in, float* conv_out, float* S, float* o, void* workspace,
+                       size_t workspace_bytes, int T, int nk, int nv, int dk, int dv, int conv_k, int v_tiled,
+                       void* stream);
+
 /* ---- norms fused with GEMM input packing; embedding --------------------------
  * Replaces: ops::qwen3_rmsnorm (src/kernels/ops.cpp:107-127), ops::gated_rmsnorm
  * (ops.cpp:129-156), the CUDA rmsnorm_k / gated_rms_k families

@@ -200,15 +200,15 @@ class Engine {
     // Chunked prompt prefill (the reference's launch_prefill_chunk,
     // cuda_engine.cu:18338-18590): per chunk of up to kPfChunk tokens, layer by
     // layer, the block-FP8 linears run over all chunk tokens on the matrix cores
-    // (gemm_fp8_prefill), the DeltaNet recurrence steps the committed state through
-    // the chunk in sub-chunks of 8 tokens (direct mode, conv window ping-ponging
-    // between ring slots 0 and 1), attention is the causal prefill kernel (which
+    // (gemm_fp8_prefill), the DeltaNet conv runs over the chunk and the recurrence
+    // steps the committed state through it in registers (gdn_prefill; the conv
+    // window ping-pongs between ring slots 0 and 1), attention is the causal prefill kernel (which
     // also writes the chunk's K/V).  RMSNorms are explicit (norm + pack kernels).
     static constexpr int kPfChunk = 512;
     static constexpr int kPfMinTokens = 16;
-    static constexpr int kPfSub = 8;
     int pf_cap_ = 0;
-    float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr;
+    float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr, *pf_xc_ = nullptr,
+          *pf_gates_ = nullptr;
     void *pf_frag_ = nullptr, *pf_frag_h_ = nullptr, *pf_attn_ws_ = nullptr;
     size_t pf_attn_ws_bytes_ = 0;
     int* pf_pos_ = nullptr;
@@ -253,6 +253,8 @@ class Engine {
         pf_y_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * wy);
         pf_o_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * wo);
         pf_h_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * I);
+        pf_xc_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * std::max(2 * c_.n_k_heads * c_.k_dim + c_.n_v_heads * c_.v_dim, 1));
+        pf_gates_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * std::max(c_.n_v_heads, 1) * 2);
         pf_frag_ = pf_mem_->get(act_frag_bytes(wf, C));
         pf_frag_h_ = pf_mem_->get(act_frag_bytes(I, C));
         pf_attn_ws_bytes_ = attn_prefill_workspace_bytes(std::max(c_.n_q, 1), C);
@@ -277,7 +279,6 @@ class Engine {
             const int T = std::min(C, N - c0);
             upload_ints(pf_pos_, &c0, 1);
             embed_rows(embed_, embed_kind_, tok_all_ + c0, pf_x_, H, c_.vocab, T, st_);
-            const int nsub = (T + kPfSub - 1) / kPfSub;
             for (int i = 0; i < c_.n_layers; ++i) {
                 Layer& Ly = L_[i];
                 rmsnorm_pack(pf_x_, H, Ly.attn_norm, nullptr, pf_frag_, H, T, eps, st_);
@@ -285,16 +286,9 @@ class Engine {
                     const Lin& in = Ly.in_parts[0];
                     gemm_fp8_prefill(in.w, in.ts, pf_frag_, pf_y_, in.m, H, T, kEpiStore, Ly.in_width, in.m, st_);
                     float* ring = slot_conv(Ly.dslot);
-                    int sl = slot;
-                    for (int k = 0; k < nsub; ++k) {
-                        const int Ts = std::min(kPfSub, T - k * kPfSub);
-                        gdn_decode_fused(pf_y_, pf_y_ + Ly.off_a, pf_y_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias,
-                                         Ly.conv_w, ring + sl * conv_slot_, ring + (sl ^ 1) * conv_slot_,
-                                         slot_S(Ly.dslot), slot_S(Ly.dslot), nullptr, 0, R_, nullptr, pf_o_, nullptr,
-                                         nullptr, nullptr, nullptr, Ts, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled,
-                                         st_, 1, 0, nullptr, k * kPfSub, T);
-                        sl ^= 1;
-                    }
+                    gdn_prefill(pf_y_, Ly.in_width, Ly.off_a, Ly.off_b, Ly.A_log, Ly.dt_bias, Ly.conv_w,
+                                ring + slot * conv_slot_, ring + (slot ^ 1) * conv_slot_, pf_xc_, pf_gates_,
+                                slot_S(Ly.dslot), pf_o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                     gnorm_pack(pf_o_, pf_y_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, nullptr, pf_frag_, zdim, T,
                                1e-6f, st_);
                     gemm_fp8_prefill(Ly.out_proj.w, Ly.out_proj.ts, pf_frag_, pf_x_, Ly.out_proj.m, zdim, T, kEpiAdd,
@@ -315,7 +309,7 @@ class Engine {
                 pack_act(pf_h_, pf_frag_h_, I, T, st_);
                 gemm_fp8_prefill(Ly.down.w, Ly.down.ts, pf_frag_h_, pf_x_, Ly.down.m, I, T, kEpiAdd, H, H, st_);
             }
-            slot ^= nsub & 1;
+            slot ^= 1;
             RL_HIP(hipStreamSynchronize(st_));  // the pinned position stage is reused by the next chunk
         }
         const int scal[2] = {N, slot};  // kPos, kSlot

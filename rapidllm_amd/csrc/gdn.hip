@@ -19,6 +19,8 @@
 // State layout in HBM (transposed per head): St[h][j][i] = S[h][i][j], so each
 // thread's 8 values are 32 contiguous bytes and a wave reads 2 KiB contiguously.
 // Conv window layout is the reference's [channel][tap] (tap 0 oldest).
+#include <algorithm>
+
 #include "internal.h"
 
 using namespace rl;
@@ -544,6 +546,149 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     }
 }
 
+// ------------------------------------------------------------------ prefill
+// Prompt prefill over T tokens (the reference's chunked prefill,
+// cuda_engine.cu:18338-18590: conv1d_prefill / conv1d_upd_seq then the recurrent
+// scan; CPU: per token conv1d_update + delta_recurrent_step, ops.cpp:458-534).
+// Two kernels per layer instead of one launch per 8 tokens:
+//   gdn_pf_conv: one thread per channel steps its 4-tap window through the T
+//                tokens (conv + SiLU, double accumulation as conv1d_update) and
+//                writes the final window; threads also form the gates of (t, head);
+//   gdn_pf_rec:  one workgroup per (v-head, 32 value columns) keeps its slice of S
+//                in registers for all T tokens: per token the q/k L2 norms, decay,
+//                delta rule and output, with the next token's q/k/v/gates loaded
+//                while the current one is computed.
+struct GdnPfArgs {
+    const float* y;      // in_proj rows [T][ld]: qkv channels at 0, a at off_a, b at off_b
+    int ld, off_a, off_b;
+    const float* A_log;
+    const float* dt_bias;
+    const float* conv_w;  // [conv_dim][4]
+    const float* conv_in;
+    float* conv_out;      // window after the last token (must not alias conv_in)
+    float* xc;            // [T][conv_dim] conv outputs (after SiLU)
+    float* gates;         // [T][nv][2]: decay g = exp(g_log), beta
+    float* S;             // [nv][dv][dk] transposed, updated in place
+    float* o;             // [T][nv*dv]
+    int T, nk, nv, dv, conv_dim, v_tiled;
+};
+
+__global__ __launch_bounds__(256) void gdn_pf_conv_kernel(GdnPfArgs p) {
+    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    constexpr int K = kConvK;
+    if (i < p.conv_dim) {
+        const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(i) * K);
+        const float4 s4 = *reinterpret_cast<const float4*>(p.conv_in + static_cast<size_t>(i) * K);
+        const float w[K] = {w4.x, w4.y, w4.z, w4.w};
+        float win[K] = {s4.x, s4.y, s4.z, s4.w};
+        float xn = p.y[i];
+        for (int t = 0; t < p.T; ++t) {
+            const float x = xn;
+            if (t + 1 < p.T) xn = p.y[static_cast<size_t>(t + 1) * p.ld + i];
+#pragma unroll
+            for (int q = 0; q + 1 < K; ++q) win[q] = win[q + 1];
+            win[K - 1] = x;
+            double acc = 0.0;
+#pragma unroll
+            for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
+            p.xc[static_cast<size_t>(t) * p.conv_dim + i] = silu_f(static_cast<float>(acc));
+        }
+        *reinterpret_cast<float4*>(p.conv_out + static_cast<size_t>(i) * K) = make_float4(win[0], win[1], win[2], win[3]);
+    }
+    if (i < p.T * p.nv) {
+        const int t = i / p.nv, h = i % p.nv;
+        const float av = p.y[static_cast<size_t>(t) * p.ld + p.off_a + h];
+        const float bv = p.y[static_cast<size_t>(t) * p.ld + p.off_b + h];
+        const float g_log = -expf(p.A_log[h]) * softplus_f(av + p.dt_bias[h]);
+        p.gates[2 * static_cast<size_t>(i)] = expf(g_log);
+        p.gates[2 * static_cast<size_t>(i) + 1] = sigmoid_f(bv);
+    }
+}
+
+__global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
+    const int tid = threadIdx.x;
+    const int c = tid & (kCChunks - 1);
+    const int jj = tid / kCChunks;
+    const int chunks = p.dv / kCW;
+    const int h = blockIdx.x / chunks, cc = blockIdx.x % chunks;
+    const int j = cc * kCW + jj;
+    const int rep = p.nv / p.nk;
+    const int src = p.v_tiled ? (h % p.nk) : (h / rep);
+    const int qdim = p.nk * kDK;
+    const float* qrow = p.xc + src * kDK + kCRows * c;         // + t * conv_dim
+    const float* krow = p.xc + qdim + src * kDK + kCRows * c;
+    const float* vcol = p.xc + 2 * qdim + h * p.dv + j;
+    const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
+
+    const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + kCRows * c;
+    float S[kCRows];
+    {
+        const f32x4* sp = reinterpret_cast<const f32x4*>(p.S + s_off);
+#pragma unroll
+        for (int r = 0; r < kCRows / 4; ++r) {
+            const f32x4 v = sp[r];
+            S[4 * r] = v[0];
+            S[4 * r + 1] = v[1];
+            S[4 * r + 2] = v[2];
+            S[4 * r + 3] = v[3];
+        }
+    }
+    float qn[kCRows], kn[kCRows], vn, gn, bn;
+    auto fetch = [&](int t, float (&q)[kCRows], float (&k)[kCRows], float& v, float& g, float& b) {
+        const size_t ro = static_cast<size_t>(t) * p.conv_dim;
+#pragma unroll
+        for (int r = 0; r < kCRows / 4; ++r) {
+            const float4 a4 = reinterpret_cast<const float4*>(qrow + ro)[r];
+            const float4 b4 = reinterpret_cast<const float4*>(krow + ro)[r];
+            q[4 * r] = a4.x, q[4 * r + 1] = a4.y, q[4 * r + 2] = a4.z, q[4 * r + 3] = a4.w;
+            k[4 * r] = b4.x, k[4 * r + 1] = b4.y, k[4 * r + 2] = b4.z, k[4 * r + 3] = b4.w;
+        }
+        v = vcol[ro];
+        const float2 gb = reinterpret_cast<const float2*>(p.gates)[static_cast<size_t>(t) * p.nv + h];
+        g = gb.x;
+        b = gb.y;
+    };
+    fetch(0, qn, kn, vn, gn, bn);
+    for (int t = 0; t < p.T; ++t) {
+        float q[kCRows], k[kCRows];
+#pragma unroll
+        for (int r = 0; r < kCRows; ++r) q[r] = qn[r], k[r] = kn[r];
+        const float v = vn, g = gn, beta = bn;
+        if (t + 1 < p.T) fetch(t + 1, qn, kn, vn, gn, bn);
+        // L2 norms over the head's 128 dims (8 lanes of 16 rows), eps inside the root
+        float sq4[4] = {0.f, 0.f, 0.f, 0.f}, sk4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < kCRows; ++r) {
+            sq4[r & 3] = fmaf(q[r], q[r], sq4[r & 3]);
+            sk4[r & 3] = fmaf(k[r], k[r], sk4[r & 3]);
+        }
+        const float sq = group8_sum((sq4[0] + sq4[1]) + (sq4[2] + sq4[3]));
+        const float sk = group8_sum((sk4[0] + sk4[1]) + (sk4[2] + sk4[3]));
+        const float iq = 1.f / sqrtf(sq + 1e-6f) * qscale;
+        const float ik = 1.f / sqrtf(sk + 1e-6f);
+        float kv4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < kCRows; ++r) {
+            k[r] *= ik;
+            S[r] *= g;
+            kv4[r & 3] = fmaf(S[r], k[r], kv4[r & 3]);
+        }
+        const float kv = group8_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
+        const float delta = (v - kv) * beta;
+        float ov4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < kCRows; ++r) {
+            S[r] = fmaf(k[r], delta, S[r]);
+            ov4[r & 3] = fmaf(S[r], q[r] * iq, ov4[r & 3]);
+        }
+        const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
+        if (c == 0) p.o[static_cast<size_t>(t) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
+    }
+    f32x4* dp = reinterpret_cast<f32x4*>(p.S + s_off);
+#pragma unroll
+    for (int r = 0; r < kCRows / 4; ++r) dp[r] = f32x4{S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]};
+}
+
 }  // namespace
 
 namespace rl {
@@ -613,6 +758,25 @@ void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, con
     check_launch("gdn_decode_kernel");
 }
 
+
+void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
+                 const float* conv_w, const float* conv_in, float* conv_out, float* xc, float* gates, float* S,
+                 float* o, int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s) {
+    RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED, "gdn_prefill: dk 128, dv a multiple of 32, conv 4");
+    RL_REQUIRE(T >= 1 && nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_prefill: bad shape");
+    RL_REQUIRE(y && A_log && dt_bias && conv_w && conv_in && conv_out && xc && gates && S && o, RL_ERR_RANGE,
+               "gdn_prefill: null pointer");
+    RL_REQUIRE(conv_out != conv_in, RL_ERR_RANGE, "gdn_prefill: conv_out must not alias conv_in");
+    const int conv_dim = 2 * nk * dk + nv * dv;
+    GdnPfArgs p{y, ld, off_a, off_b, A_log, dt_bias, conv_w, conv_in, conv_out, xc, gates, S, o,
+                T, nk, nv, dv, conv_dim, v_tiled};
+    const int n = std::max(conv_dim, T * nv);
+    hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p);
+    check_launch("gdn_pf_conv_kernel");
+    hipLaunchKernelGGL(gdn_pf_rec_kernel, dim3(nv * (dv / kCW)), dim3(kCT), 0, s, p);
+    check_launch("gdn_pf_rec_kernel");
+}
+
 }  // namespace rl
 
 extern "C" {
@@ -629,6 +793,24 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
         else
             rl::gdn_decode(qkv, a, b, ld_in, A_log, dt_bias, conv_w, conv_in, conv_out, S_in, S_out, nullptr, 0, 0,
                            0, o, T, nk, nv, dk, dv, conv_k, v_tiled, S(stream));
+    });
+}
+
+size_t rl_hip_gdn_prefill_workspace_bytes(int T, int nk, int nv, int dk, int dv) {
+    return (static_cast<size_t>(T) * (2 * nk * dk + nv * dv) + static_cast<size_t>(T) * nv * 2) * sizeof(float) + 256;
+}
+
+int rl_hip_gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
+                       const float* conv_w, const float* conv_in, float* conv_out, float* S_state, float* o,
+                       void* workspace, size_t workspace_bytes, int T, int nk, int nv, int dk, int dv, int conv_k,
+                       int v_tiled, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(workspace && workspace_bytes >= rl_hip_gdn_prefill_workspace_bytes(T, nk, nv, dk, dv),
+                   RL_ERR_RANGE, "gdn_prefill: workspace too small");
+        float* xc = static_cast<float*>(workspace);
+        float* gates = xc + static_cast<size_t>(T) * (2 * nk * dk + nv * dv);
+        rl::gdn_prefill(y, ld, off_a, off_b, A_log, dt_bias, conv_w, conv_in, conv_out, xc, gates, S_state, o, T, nk,
+                        nv, dk, dv, conv_k, v_tiled, S(stream));
     });
 }
 

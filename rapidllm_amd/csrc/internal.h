@@ -130,6 +130,14 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices = 1,
                       int ab_ld = 0, const GdnBatch* batch = nullptr, int row_off = 0, int T_rows = 0);
 
+// Prompt prefill of T tokens from the conv window conv_in (direct mode): conv +
+// gates over all tokens (xc [T][conv_dim], gates [T][nv][2] scratch), then the
+// recurrence with S (transposed, one copy) updated in place; o [T][nv*dv] raw
+// recurrent output; conv_out = window after the last token.
+void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
+                 const float* conv_w, const float* conv_in, float* conv_out, float* xc, float* gates, float* S,
+                 float* o, int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s);
+
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);
 // Outputs of token t go to column t_off + t of T_out (T_out 0: T), so one sequence

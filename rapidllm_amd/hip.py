@@ -56,6 +56,9 @@ _SIGS = {
     "rl_hip_dequant_kquant": (_i, [_i, _vp, _vp, _sz, _vp]),
     "rl_hip_gdn_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,
                                _i, _vp]),
+    "rl_hip_gdn_prefill_workspace_bytes": (_sz, [_i, _i, _i, _i, _i]),
+    "rl_hip_gdn_prefill": (_i, [_vp, _i, _i, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _i, _i,
+                                _i, _vp]),
     "rl_hip_rmsnorm_pack": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, C.c_float, _vp]),
     "rl_hip_gated_rmsnorm_pack": (_i, [_vp, _vp, _i, _vp, _i, _vp, _vp, _i, _i, C.c_float, _vp]),
     "rl_hip_embed_rows": (_i, [_vp, _i, _vp, _vp, _i, _i, _i, _vp]),

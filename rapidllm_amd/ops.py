@@ -246,6 +246,36 @@ def gdn_decode(qkv, a, b, A_log, dt_bias, conv_w, conv_state, S, nk, nv, v_tiled
     return o, S_new, conv_new
 
 
+def gdn_prefill(qkv, a, b, A_log, dt_bias, conv_w, conv_state, S, nk, nv, v_tiled=False):
+    """Prompt prefill of T (any) tokens of one Gated DeltaNet layer (same inputs and
+    outputs as gdn_decode): conv + gates over all tokens, then the recurrence."""
+    qkv = _f32(np.atleast_2d(qkv))
+    T, conv_dim = qkv.shape
+    nv_, dk, dv = S.shape
+    assert nv_ == nv
+    ld = conv_dim + 2 * nv
+    fused = np.zeros((T, ld), np.float32)
+    fused[:, :conv_dim] = qkv
+    fused[:, conv_dim:conv_dim + nv] = np.atleast_2d(a)
+    fused[:, conv_dim + nv:] = np.atleast_2d(b)
+    d_f = DeviceBuffer.from_numpy(fused)
+    d_A = DeviceBuffer.from_numpy(_f32(A_log))
+    d_dt = DeviceBuffer.from_numpy(_f32(dt_bias))
+    d_w = DeviceBuffer.from_numpy(_f32(conv_w))
+    d_cin = DeviceBuffer.from_numpy(_f32(conv_state))
+    d_cout = DeviceBuffer(d_cin.nbytes)
+    d_S = DeviceBuffer.from_numpy(np.ascontiguousarray(np.transpose(S, (0, 2, 1)), np.float32))
+    d_o = DeviceBuffer(4 * T * nv * dv)
+    ws = DeviceBuffer(hip.lib().rl_hip_gdn_prefill_workspace_bytes(T, nk, nv, dk, dv))
+    call("rl_hip_gdn_prefill", d_f.ptr, ld, conv_dim, conv_dim + nv, d_A.ptr, d_dt.ptr, d_w.ptr, d_cin.ptr,
+         d_cout.ptr, d_S.ptr, d_o.ptr, ws.ptr, ws.nbytes, T, nk, nv, dk, dv, conv_w.shape[1], 1 if v_tiled else 0,
+         None)
+    o = d_o.numpy(np.float32, (T, nv * dv))
+    S_new = np.transpose(d_S.numpy(np.float32, (nv, dv, dk)), (0, 2, 1)).copy()
+    conv_new = d_cout.numpy(np.float32, conv_state.shape)
+    return o, S_new, conv_new
+
+
 # ------------------------------------------------------------------ attention
 
 

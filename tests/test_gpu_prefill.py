@@ -160,3 +160,19 @@ def test_engine_chunked_prefill_matches_oracle(gpu, orc):
     want, _, _ = orc_m.generate(prompt, 8)
     got, _, _ = eng.generate(prompt, 8, spec_n=3)
     assert got == want
+
+
+@pytest.mark.parametrize("T,nk,nv,v_tiled", [(1, 16, 48, False), (37, 16, 48, False), (200, 2, 6, True),
+                                             (64, 4, 4, False)])
+def test_gdn_prefill_vs_oracle(gpu, orc, T, nk, nv, v_tiled):
+    """DeltaNet prefill (conv over all tokens, then the recurrence with the state in
+    registers) against per-token oracle steps: outputs, final state, final window."""
+    from tests.test_gpu_layers import _gdn_case, _gdn_oracle
+    r = synth.rng(400 + T + nv)
+    case = _gdn_case(r, T, nk, nv, v_tiled)
+    o, S, conv = ops.gdn_prefill(*case, nk, nv, v_tiled)
+    o_ref, S_ref, conv_ref = _gdn_oracle(orc, *case, nk, nv, v_tiled)
+    for t in range(T):
+        assert rel_l2(o[t], o_ref[t]) < 1e-3, (t, rel_l2(o[t], o_ref[t]))
+    assert rel_l2(S, S_ref) < 1e-4
+    assert np.array_equal(conv, conv_ref)
