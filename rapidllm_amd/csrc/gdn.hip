@@ -551,13 +551,13 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
 // cuda_engine.cu:18338-18590: conv1d_prefill / conv1d_upd_seq then the recurrent
 // scan; CPU: per token conv1d_update + delta_recurrent_step, ops.cpp:458-534).
 // Two kernels per layer instead of one launch per 8 tokens:
-//   gdn_pf_conv: one thread per channel steps its 4-tap window through the T
-//                tokens (conv + SiLU, double accumulation as conv1d_update) and
-//                writes the final window; threads also form the gates of (t, head);
+//   gdn_pf_conv: one thread per (token, channel): conv + SiLU from the token's
+//                4-tap window (double accumulation as conv1d_update), the final
+//                window, and the gates of (t, head);
 //   gdn_pf_rec:  one workgroup per (v-head, 32 value columns) keeps its slice of S
 //                in registers for all T tokens: per token the q/k L2 norms, decay,
-//                delta rule and output, with the next token's q/k/v/gates loaded
-//                while the current one is computed.
+//                delta rule and output, the tokens' inputs staged through LDS in
+//                blocks of 32 (the next block loading during the current one).
 struct GdnPfArgs {
     const float* y;      // in_proj rows [T][ld]: qkv channels at 0, a at off_a, b at off_b
     int ld, off_a, off_b;
@@ -573,37 +573,50 @@ struct GdnPfArgs {
     int T, nk, nv, dv, conv_dim, v_tiled;
 };
 
+// One thread per (token, channel): the conv output of token t only needs the inputs
+// of tokens t-3 .. t (the window before the chunk for t < 3), so every token is
+// independent.  Threads of token T-1 also write the final window; threads past the
+// conv work form the gates of (t, head).
 __global__ __launch_bounds__(256) void gdn_pf_conv_kernel(GdnPfArgs p) {
-    const int i = blockIdx.x * blockDim.x + threadIdx.x;
+    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
     constexpr int K = kConvK;
-    if (i < p.conv_dim) {
-        const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(i) * K);
-        const float4 s4 = *reinterpret_cast<const float4*>(p.conv_in + static_cast<size_t>(i) * K);
+    const size_t n_conv = static_cast<size_t>(p.T) * p.conv_dim;
+    if (i < n_conv) {
+        const int t = static_cast<int>(i / p.conv_dim), ch = static_cast<int>(i % p.conv_dim);
+        const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(ch) * K);
+        const float4 s4 = *reinterpret_cast<const float4*>(p.conv_in + static_cast<size_t>(ch) * K);
         const float w[K] = {w4.x, w4.y, w4.z, w4.w};
-        float win[K] = {s4.x, s4.y, s4.z, s4.w};
-        float xn = p.y[i];
-        for (int t = 0; t < p.T; ++t) {
-            const float x = xn;
-            if (t + 1 < p.T) xn = p.y[static_cast<size_t>(t + 1) * p.ld + i];
+        const float st[K] = {s4.x, s4.y, s4.z, s4.w};
+        // window after token t: taps q = 0..3 hold inputs of tokens t-3+q
+        float win[K];
 #pragma unroll
-            for (int q = 0; q + 1 < K; ++q) win[q] = win[q + 1];
-            win[K - 1] = x;
-            double acc = 0.0;
-#pragma unroll
-            for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
-            p.xc[static_cast<size_t>(t) * p.conv_dim + i] = silu_f(static_cast<float>(acc));
+        for (int q = 0; q < K; ++q) {
+            const int tt = t - (K - 1) + q;
+            win[q] = tt >= 0 ? p.y[static_cast<size_t>(tt) * p.ld + ch] : st[q + t + 1];
         }
-        *reinterpret_cast<float4*>(p.conv_out + static_cast<size_t>(i) * K) = make_float4(win[0], win[1], win[2], win[3]);
-    }
-    if (i < p.T * p.nv) {
-        const int t = i / p.nv, h = i % p.nv;
+        double acc = 0.0;
+#pragma unroll
+        for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
+        p.xc[i] = silu_f(static_cast<float>(acc));
+        if (t == p.T - 1)
+            *reinterpret_cast<float4*>(p.conv_out + static_cast<size_t>(ch) * K) =
+                make_float4(win[0], win[1], win[2], win[3]);
+    } else if (i < n_conv + static_cast<size_t>(p.T) * p.nv) {
+        const int k = static_cast<int>(i - n_conv);
+        const int t = k / p.nv, h = k % p.nv;
         const float av = p.y[static_cast<size_t>(t) * p.ld + p.off_a + h];
         const float bv = p.y[static_cast<size_t>(t) * p.ld + p.off_b + h];
         const float g_log = -expf(p.A_log[h]) * softplus_f(av + p.dt_bias[h]);
-        p.gates[2 * static_cast<size_t>(i)] = expf(g_log);
-        p.gates[2 * static_cast<size_t>(i) + 1] = sigmoid_f(bv);
+        p.gates[2 * static_cast<size_t>(k)] = expf(g_log);
+        p.gates[2 * static_cast<size_t>(k) + 1] = sigmoid_f(bv);
     }
 }
+
+// Tokens are staged through LDS in blocks of kPfTB (q and k of the head's k-head,
+// the workgroup's 32 v columns, the gates): the next block's loads are in flight
+// while the current block's tokens run, so the per-token chain reads LDS only.
+constexpr int kPfTB = 32;
+constexpr int kPfTokFloats = 2 * kDK + kCW + 2;  // q | k | v | g, beta
 
 __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     const int tid = threadIdx.x;
@@ -615,10 +628,48 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     const int rep = p.nv / p.nk;
     const int src = p.v_tiled ? (h % p.nk) : (h / rep);
     const int qdim = p.nk * kDK;
-    const float* qrow = p.xc + src * kDK + kCRows * c;         // + t * conv_dim
-    const float* krow = p.xc + qdim + src * kDK + kCRows * c;
-    const float* vcol = p.xc + 2 * qdim + h * p.dv + j;
     const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
+
+    __shared__ __align__(16) float blk[2][kPfTB][kPfTokFloats];
+    // staging: element e of a block = (token, float index); 16-byte units where possible
+    constexpr int kUnits = kPfTB * (2 * kDK + kCW) / 4;  // q, k, v as float4 units
+    constexpr int kPer = (kUnits + kCT - 1) / kCT;
+    float4 stg[kPer];
+    float2 stg_g = make_float2(0.f, 0.f);
+    auto stage_load = [&](int t0) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int u = tid + q * kCT;
+            stg[q] = make_float4(0.f, 0.f, 0.f, 0.f);
+            if (u < kUnits) {
+                const int tt = u / ((2 * kDK + kCW) / 4), f = (u % ((2 * kDK + kCW) / 4)) * 4;
+                const int t = t0 + tt;
+                if (t < p.T) {
+                    const float* row = p.xc + static_cast<size_t>(t) * p.conv_dim;
+                    const float* src_p = f < kDK ? row + src * kDK + f
+                                                 : f < 2 * kDK ? row + qdim + src * kDK + (f - kDK)
+                                                               : row + 2 * qdim + h * p.dv + cc * kCW + (f - 2 * kDK);
+                    stg[q] = *reinterpret_cast<const float4*>(src_p);
+                }
+            }
+        }
+        if (tid < kPfTB && t0 + tid < p.T)
+            stg_g = reinterpret_cast<const float2*>(p.gates)[static_cast<size_t>(t0 + tid) * p.nv + h];
+    };
+    auto stage_store = [&](int buf) {
+#pragma unroll
+        for (int q = 0; q < kPer; ++q) {
+            const int u = tid + q * kCT;
+            if (u < kUnits) {
+                const int tt = u / ((2 * kDK + kCW) / 4), f = (u % ((2 * kDK + kCW) / 4)) * 4;
+                *reinterpret_cast<float4*>(&blk[buf][tt][f]) = stg[q];
+            }
+        }
+        if (tid < kPfTB) {
+            blk[buf][tid][2 * kDK + kCW] = stg_g.x;
+            blk[buf][tid][2 * kDK + kCW + 1] = stg_g.y;
+        }
+    };
 
     const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + kCRows * c;
     float S[kCRows];
@@ -633,56 +684,58 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
             S[4 * r + 3] = v[3];
         }
     }
-    float qn[kCRows], kn[kCRows], vn, gn, bn;
-    auto fetch = [&](int t, float (&q)[kCRows], float (&k)[kCRows], float& v, float& g, float& b) {
-        const size_t ro = static_cast<size_t>(t) * p.conv_dim;
+    stage_load(0);
+    stage_store(0);
+    __syncthreads();
+    for (int t0 = 0; t0 < p.T; t0 += kPfTB) {
+        const int buf = (t0 / kPfTB) & 1;
+        const bool more = t0 + kPfTB < p.T;
+        if (more) stage_load(t0 + kPfTB);
+        const int nt = min(kPfTB, p.T - t0);
+        for (int tt = 0; tt < nt; ++tt) {
+            const float* tk = blk[buf][tt];
+            float q[kCRows], k[kCRows];
 #pragma unroll
-        for (int r = 0; r < kCRows / 4; ++r) {
-            const float4 a4 = reinterpret_cast<const float4*>(qrow + ro)[r];
-            const float4 b4 = reinterpret_cast<const float4*>(krow + ro)[r];
-            q[4 * r] = a4.x, q[4 * r + 1] = a4.y, q[4 * r + 2] = a4.z, q[4 * r + 3] = a4.w;
-            k[4 * r] = b4.x, k[4 * r + 1] = b4.y, k[4 * r + 2] = b4.z, k[4 * r + 3] = b4.w;
+            for (int r = 0; r < kCRows / 4; ++r) {
+                const float4 a4 = *reinterpret_cast<const float4*>(tk + kCRows * c + 4 * r);
+                const float4 b4 = *reinterpret_cast<const float4*>(tk + kDK + kCRows * c + 4 * r);
+                q[4 * r] = a4.x, q[4 * r + 1] = a4.y, q[4 * r + 2] = a4.z, q[4 * r + 3] = a4.w;
+                k[4 * r] = b4.x, k[4 * r + 1] = b4.y, k[4 * r + 2] = b4.z, k[4 * r + 3] = b4.w;
+            }
+            const float v = tk[2 * kDK + jj];
+            const float g = tk[2 * kDK + kCW], beta = tk[2 * kDK + kCW + 1];
+            // L2 norms over the head's 128 dims (8 lanes of 16 rows), eps inside the root
+            float sq4[4] = {0.f, 0.f, 0.f, 0.f}, sk4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < kCRows; ++r) {
+                sq4[r & 3] = fmaf(q[r], q[r], sq4[r & 3]);
+                sk4[r & 3] = fmaf(k[r], k[r], sk4[r & 3]);
+            }
+            const float sq = group8_sum((sq4[0] + sq4[1]) + (sq4[2] + sq4[3]));
+            const float sk = group8_sum((sk4[0] + sk4[1]) + (sk4[2] + sk4[3]));
+            const float iq = 1.f / sqrtf(sq + 1e-6f) * qscale;
+            const float ik = 1.f / sqrtf(sk + 1e-6f);
+            float kv4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < kCRows; ++r) {
+                k[r] *= ik;
+                S[r] *= g;
+                kv4[r & 3] = fmaf(S[r], k[r], kv4[r & 3]);
+            }
+            const float kv = group8_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
+            const float delta = (v - kv) * beta;
+            float ov4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int r = 0; r < kCRows; ++r) {
+                S[r] = fmaf(k[r], delta, S[r]);
+                ov4[r & 3] = fmaf(S[r], q[r] * iq, ov4[r & 3]);
+            }
+            const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
+            if (c == 0)
+                p.o[static_cast<size_t>(t0 + tt) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
         }
-        v = vcol[ro];
-        const float2 gb = reinterpret_cast<const float2*>(p.gates)[static_cast<size_t>(t) * p.nv + h];
-        g = gb.x;
-        b = gb.y;
-    };
-    fetch(0, qn, kn, vn, gn, bn);
-    for (int t = 0; t < p.T; ++t) {
-        float q[kCRows], k[kCRows];
-#pragma unroll
-        for (int r = 0; r < kCRows; ++r) q[r] = qn[r], k[r] = kn[r];
-        const float v = vn, g = gn, beta = bn;
-        if (t + 1 < p.T) fetch(t + 1, qn, kn, vn, gn, bn);
-        // L2 norms over the head's 128 dims (8 lanes of 16 rows), eps inside the root
-        float sq4[4] = {0.f, 0.f, 0.f, 0.f}, sk4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int r = 0; r < kCRows; ++r) {
-            sq4[r & 3] = fmaf(q[r], q[r], sq4[r & 3]);
-            sk4[r & 3] = fmaf(k[r], k[r], sk4[r & 3]);
-        }
-        const float sq = group8_sum((sq4[0] + sq4[1]) + (sq4[2] + sq4[3]));
-        const float sk = group8_sum((sk4[0] + sk4[1]) + (sk4[2] + sk4[3]));
-        const float iq = 1.f / sqrtf(sq + 1e-6f) * qscale;
-        const float ik = 1.f / sqrtf(sk + 1e-6f);
-        float kv4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int r = 0; r < kCRows; ++r) {
-            k[r] *= ik;
-            S[r] *= g;
-            kv4[r & 3] = fmaf(S[r], k[r], kv4[r & 3]);
-        }
-        const float kv = group8_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
-        const float delta = (v - kv) * beta;
-        float ov4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int r = 0; r < kCRows; ++r) {
-            S[r] = fmaf(k[r], delta, S[r]);
-            ov4[r & 3] = fmaf(S[r], q[r] * iq, ov4[r & 3]);
-        }
-        const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
-        if (c == 0) p.o[static_cast<size_t>(t) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
+        if (more) stage_store(buf ^ 1);
+        __syncthreads();
     }
     f32x4* dp = reinterpret_cast<f32x4*>(p.S + s_off);
 #pragma unroll
@@ -770,8 +823,8 @@ void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_lo
     const int conv_dim = 2 * nk * dk + nv * dv;
     GdnPfArgs p{y, ld, off_a, off_b, A_log, dt_bias, conv_w, conv_in, conv_out, xc, gates, S, o,
                 T, nk, nv, dv, conv_dim, v_tiled};
-    const int n = std::max(conv_dim, T * nv);
-    hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3((n + 255) / 256), dim3(256), 0, s, p);
+    const size_t n = static_cast<size_t>(T) * (conv_dim + nv);
+    hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p);
     check_launch("gdn_pf_conv_kernel");
     hipLaunchKernelGGL(gdn_pf_rec_kernel, dim3(nv * (dv / kCW)), dim3(kCT), 0, s, p);
     check_launch("gdn_pf_rec_kernel");
