@@ -115,3 +115,25 @@ def test_batch_decode_wide_in_proj(gpu):
         toks, poss = eng.copy_greedy_n(2), [p + 1 for p in poss]
     eng.close()
     ref.close()
+
+
+def test_long_prompts_prefilled_into_slots(gpu, batch_pair):
+    """Prompts long enough for the chunked prefill path, prefilled into slots 1 and
+    0 (the chunked path works on the selected slot's caches and state only); batched
+    decoding then equals plain decoding of each sequence bit for bit."""
+    spec, eng, ref = batch_pair
+    eng.zero_slots(4)
+    rng = np.random.default_rng(77)
+    a = [int(t) for t in rng.integers(0, spec.vocab, 100)]
+    b = [int(t) for t in rng.integers(0, spec.vocab, 61)]
+    ta, la = plain_chain(ref, a, 4)
+    tb, lb = plain_chain(ref, b, 4)
+    eng.prefill_slot(b, 1)
+    eng.prefill_slot(a, 0)
+    assert np.array_equal(eng.copy_logits(), la[0])
+    toks, poss = [ta[0], tb[0]], [len(a), len(b)]
+    for step in range(1, 4):
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(2)
+        assert np.array_equal(rows[0], la[step]) and np.array_equal(rows[1], lb[step]), step
+        toks, poss = eng.copy_greedy_n(2), [p + 1 for p in poss]
