@@ -289,6 +289,37 @@ int rl_hip_engine_prefill_slot(RlEngine* e, const int32_t* ids, int n, int slot)
  * slots' positions advance; the tokens in place are re-fed). */
 int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms);
 
+/* ---- checkpoint loading ---------------------------------------------------
+ * Replaces: rapidllm::make_loader + IWeightLoader::load + WeightStore::open
+ * (include/rapidllm/frontend/weight_store.h:55-72, src/frontend/weight_store.cpp:
+ * 125-155), the HF FP8 safetensors loader (src/frontend/hf_loader.cpp:87-251), the
+ * GGUF loader (src/frontend/gguf_loader.cpp:128-397) and map_hf_name /
+ * map_gguf_name (src/frontend/name_map.cpp:115-226).  Host code only (no GPU call).
+ * `path` is an HF directory (config.json + *.safetensors, optionally sharded by
+ * model.safetensors.index.json) or a *.gguf file; max_layers > 0 keeps layers
+ * 0 .. max_layers-1.  The table holds the reference's IR names and the reference
+ * WeightStore's conversions (FP8 block scales as fp32; F16/BF16 norms, A_log,
+ * dt_bias, conv1d as F32; GGUF: quantised in_proj_a/b dequantised to F32, raw
+ * Qwen RMSNorm scales shifted by -1, llama.cpp ssm_a = -exp(A_log) turned back into
+ * A_log with cfg->v_tiled = 1).  Tensor data stays valid until rl_hip_weights_close
+ * (most of it points into the mapped files); the table is what
+ * rl_hip_engine_create takes.  Errors: RL_ERR_IO (missing files), RL_ERR_FORMAT
+ * (bad or truncated files, FP8 weight without weight_scale_inv, quantised
+ * DeltaNet leftovers), RL_ERR_UNSUPPORTED (unknown dtypes / ggml types). */
+typedef struct RlWeights RlWeights;
+RlWeights* rl_hip_weights_open(const char* path, int max_layers, int* status);
+void rl_hip_weights_close(RlWeights* w);
+/* source: 0 HF safetensors, 1 GGUF (SourceKind, weight_store.h:18) */
+int rl_hip_weights_config(const RlWeights* w, RlModelConfig* cfg, int* source);
+int rl_hip_weights_table(const RlWeights* w, const RlTensor** tensors, int* n);
+/* Per-tensor file facts (TensorDesc::src_name / shape / ndim / gguf_type / nbytes,
+ * weight_store.h:20-33) for table entry i; n_scale = number of fp32 block scales. */
+int rl_hip_weights_info(const RlWeights* w, int i, const char** src_name, int* ndim, int64_t* shape4, int* gguf_type,
+                        uint64_t* nbytes, int* n_scale);
+/* IR name of a source tensor name (gguf = 0: HF, 1: GGUF); "" when the path does not
+ * use the tensor (vision tower, unknown names). */
+int rl_hip_map_name(int gguf, const char* src, char* out, int cap);
+
 /* ---- bandwidth calibration ------------------------------------------------
  * No counterpart in the reference.  A streaming copy / read of `bytes` (multiple of
  * 16) that measures the achievable HBM rate and calibrates rocprof's FETCH_SIZE /

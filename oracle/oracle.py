@@ -127,6 +127,25 @@ def ref():
         R.ref_num_threads.restype = C.c_int
         R.ref_simd_name.restype = C.c_char_p
         R.ref_fused_mlp.argtypes = [_f, _u8, _f, _u8, _f, _u8, _f, _f, C.c_int, C.c_int, C.c_float]
+        vp = C.c_void_p
+        R.ref_weights_open.restype = vp
+        R.ref_weights_open.argtypes = [C.c_char_p, C.c_char_p, C.c_int]
+        R.ref_weights_close.argtypes = [vp]
+        R.ref_weights_count.argtypes = [vp]
+        for fn in ("ref_weights_name", "ref_weights_src"):
+            getattr(R, fn).restype = C.c_char_p
+            getattr(R, fn).argtypes = [vp, C.c_int]
+        R.ref_weights_quant.argtypes = [vp, C.c_int]
+        R.ref_weights_shape.argtypes = [vp, C.c_int, C.POINTER(C.c_int64)]
+        R.ref_weights_nbytes.restype = C.c_uint64
+        R.ref_weights_nbytes.argtypes = [vp, C.c_int]
+        R.ref_weights_data.restype = vp
+        R.ref_weights_data.argtypes = [vp, C.c_int]
+        R.ref_weights_nscale.argtypes = [vp, C.c_int]
+        R.ref_weights_scale.restype = vp
+        R.ref_weights_scale.argtypes = [vp, C.c_int]
+        R.ref_weights_model.argtypes = [vp, C.POINTER(C.c_int), C.POINTER(C.c_ubyte)]
+        R.ref_map_name.argtypes = [C.c_int, C.c_char_p, C.c_char_p, C.c_int]
         _ref = R
     return _ref
 

@@ -72,3 +72,80 @@ void ref_fused_mlp(const float* rms_w, const uint8_t* wg, const float* sg, const
     ops::fused_mlp_decode(a);
 }
 }
+
+// ---- the reference's checkpoint loaders (src/frontend/*.cpp), for cross-checking
+// the loader of the HIP library on the same files.
+#include "rapidllm/backend/device.h"
+#include "rapidllm/frontend/weight_store.h"
+
+#include <cstring>
+#include <string>
+#include <vector>
+
+namespace {
+// WeightStore::open takes a Device it does not use (weight_store.cpp:137); a device
+// with no capabilities satisfies the signature.
+class NoDevice final : public rapidllm::Device {
+public:
+    rapidllm::DeviceKind kind() const override { return rapidllm::DeviceKind::CPU; }
+    const char* name() const override { return "none"; }
+    std::unique_ptr<rapidllm::Buffer> allocate(const rapidllm::BufferDesc&) override { return nullptr; }
+    std::unique_ptr<rapidllm::Stream> create_stream() override { return nullptr; }
+    void memcpy(rapidllm::TensorView, rapidllm::TensorView, rapidllm::Stream&) override {}
+    void launch(const char*, const rapidllm::TensorView*, int, const void*, size_t, rapidllm::Stream&) override {}
+    bool has_kernel(const char*) const override { return false; }
+};
+
+struct RefWeights {
+    rapidllm::WeightStore ws;
+    std::vector<const rapidllm::TensorDesc*> v;
+};
+}  // namespace
+
+extern "C" {
+void* ref_weights_open(const char* path, char* err, int cap) {
+    try {
+        NoDevice dev;
+        rapidllm::LoadOptions opt;
+        auto* r = new RefWeights{rapidllm::WeightStore::open(path, dev, opt), {}};
+        for (auto& [_, t] : r->ws.table().tensors) r->v.push_back(&t);
+        return r;
+    } catch (const std::exception& e) {
+        std::snprintf(err, cap, "%s", e.what());
+        return nullptr;
+    }
+}
+void ref_weights_close(void* h) { delete static_cast<RefWeights*>(h); }
+int ref_weights_count(void* h) { return static_cast<int>(static_cast<RefWeights*>(h)->v.size()); }
+const char* ref_weights_name(void* h, int i) { return static_cast<RefWeights*>(h)->v[i]->ir_name.c_str(); }
+const char* ref_weights_src(void* h, int i) { return static_cast<RefWeights*>(h)->v[i]->src_name.c_str(); }
+int ref_weights_quant(void* h, int i) { return static_cast<int>(static_cast<RefWeights*>(h)->v[i]->quant); }
+int ref_weights_shape(void* h, int i, int64_t* shape4) {
+    const auto* t = static_cast<RefWeights*>(h)->v[i];
+    for (int d = 0; d < 4; ++d) shape4[d] = t->shape[d];
+    return t->ndim;
+}
+uint64_t ref_weights_nbytes(void* h, int i) { return static_cast<RefWeights*>(h)->v[i]->data.size(); }
+const uint8_t* ref_weights_data(void* h, int i) { return static_cast<RefWeights*>(h)->v[i]->data.data(); }
+int ref_weights_nscale(void* h, int i) { return static_cast<int>(static_cast<RefWeights*>(h)->v[i]->scale.size()); }
+const float* ref_weights_scale(void* h, int i) { return static_cast<RefWeights*>(h)->v[i]->scale.data(); }
+// n_layers, hidden, vocab, intermediate, gdn_v_tiled, has_mtp, source, tie_embed
+void ref_weights_model(void* h, int* out8, unsigned char* kinds) {
+    const auto& t = static_cast<RefWeights*>(h)->ws.table();
+    const auto& m = t.model;
+    out8[0] = m.n_layers;
+    out8[1] = m.hidden;
+    out8[2] = m.vocab;
+    out8[3] = m.intermediate;
+    out8[4] = m.gdn_v_tiled ? 1 : 0;
+    out8[5] = m.has_mtp ? 1 : 0;
+    out8[6] = t.source == rapidllm::SourceKind::GgufFile ? 1 : 0;
+    out8[7] = m.tie_embed ? 1 : 0;
+    for (int i = 0; i < m.n_layers; ++i) kinds[i] = static_cast<unsigned char>(m.layers[i].kind);
+}
+int ref_map_name(int gguf, const char* src, char* out, int cap) {
+    const std::string s = gguf ? rapidllm::map_gguf_name(src) : rapidllm::map_hf_name(src);
+    std::snprintf(out, cap, "%s", s.c_str());
+    return static_cast<int>(s.size());
+}
+}

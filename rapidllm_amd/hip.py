@@ -101,6 +101,13 @@ _SIGS = {
     "rl_hip_engine_zero_slots": (_i, [_vp, _i]),
     "rl_hip_engine_prefill_slot": (_i, [_vp, _vp, _i, _i]),
     "rl_hip_engine_time_batch": (_i, [_vp, _i, _i, C.POINTER(C.c_float)]),
+    "rl_hip_weights_open": (_vp, [C.c_char_p, _i, C.POINTER(C.c_int)]),
+    "rl_hip_weights_close": (None, [_vp]),
+    "rl_hip_weights_config": (_i, [_vp, _vp, C.POINTER(C.c_int)]),
+    "rl_hip_weights_table": (_i, [_vp, _vp, C.POINTER(C.c_int)]),
+    "rl_hip_weights_info": (_i, [_vp, _i, C.POINTER(C.c_char_p), C.POINTER(C.c_int), C.POINTER(C.c_int64),
+                                 C.POINTER(C.c_int), C.POINTER(C.c_uint64), C.POINTER(C.c_int)]),
+    "rl_hip_map_name": (_i, [_i, C.c_char_p, C.c_char_p, _i]),
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
     "rl_hip_time_gemm_fp8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
