@@ -556,6 +556,13 @@ struct Model {
         } else if (e.quant == RL_Q_BF16 || e.quant == RL_Q_F16) {
             const uint16_t* r = static_cast<const uint16_t*>(e.data) + static_cast<size_t>(id) * H;
             for (int i = 0; i < H; ++i) out[i] = e.quant == RL_Q_BF16 ? orc_bf16_to_f32(r[i]) : orc_fp16_to_f32(r[i]);
+        } else if (e.quant == RL_Q_Q4_K || e.quant == RL_Q_Q6_K) {
+            // block-quantised embedding row (cuda_engine.cu:19930-19955 dequantises the
+            // table with ops::dequant_q4_k / dequant_q6_k)
+            const size_t rowb = static_cast<size_t>(H / 256) * (e.quant == RL_Q_Q4_K ? 144 : 210);
+            const uint8_t* r = static_cast<const uint8_t*>(e.data) + static_cast<size_t>(id) * rowb;
+            if (e.quant == RL_Q_Q4_K) orc_dequant_q4_k(r, out, H);
+            else orc_dequant_q6_k(r, out, H);
         } else {
             throw std::runtime_error("embed quant");
         }

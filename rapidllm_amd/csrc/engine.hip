@@ -696,14 +696,36 @@ class Engine {
             final_norm_ = synth_vec(H, 0.f, 0.1f);
         } else {
             const RlTensor* e = need(find, "embed");
-            RL_REQUIRE(e->quant == RL_Q_F32 || e->quant == RL_Q_F16 || e->quant == RL_Q_BF16, RL_ERR_UNSUPPORTED,
-                       "embed must be F32, F16 or BF16");
             RL_REQUIRE(e->rows == c_.vocab && e->cols == H, RL_ERR_FORMAT, "embed shape");
-            embed_kind_ = e->quant;
-            const size_t eb = static_cast<size_t>(c_.vocab) * H * (e->quant == RL_Q_F32 ? 4 : 2);
-            void* ed = mem_.get(eb);
-            RL_HIP(hipMemcpyAsync(ed, e->data, eb, hipMemcpyHostToDevice, st_));
-            embed_ = ed;
+            if (e->quant == RL_Q_Q8_0 || e->quant == RL_Q_Q4_K || e->quant == RL_Q_Q5_K || e->quant == RL_Q_Q6_K) {
+                // block-quantised embedding (GGUF token_embd): dequantised once to an
+                // F32 table, exactly as the reference's CUDA engine stores it
+                // (cuda_engine.cu:19930-19955); rows are staged through the host in chunks
+                const int vals = e->quant == RL_Q_Q8_0 ? 32 : 256;
+                const int bsz = e->quant == RL_Q_Q8_0 ? 34 : e->quant == RL_Q_Q4_K ? 144 : e->quant == RL_Q_Q5_K ? 176 : 210;
+                RL_REQUIRE(H % vals == 0, RL_ERR_FORMAT, "embed: row length not a whole number of blocks");
+                const size_t rowb = static_cast<size_t>(H / vals) * bsz;
+                float* ed = mem_.get_n<float>(static_cast<size_t>(c_.vocab) * H);
+                const int chunk = 2048;
+                std::vector<float> stage(static_cast<size_t>(chunk) * H);
+                for (int r0 = 0; r0 < c_.vocab; r0 += chunk) {
+                    const int nr = std::min(chunk, c_.vocab - r0);
+                    dequant_host(e->quant, static_cast<const uint8_t*>(e->data) + static_cast<size_t>(r0) * rowb,
+                                 stage.data(), static_cast<int64_t>(nr) * H);
+                    RL_HIP(hipMemcpy(ed + static_cast<size_t>(r0) * H, stage.data(), sizeof(float) * nr * H,
+                                     hipMemcpyHostToDevice));
+                }
+                embed_kind_ = RL_Q_F32;
+                embed_ = ed;
+            } else {
+                RL_REQUIRE(e->quant == RL_Q_F32 || e->quant == RL_Q_F16 || e->quant == RL_Q_BF16, RL_ERR_UNSUPPORTED,
+                           "embed must be F32, F16, BF16, Q8_0, Q4_K, Q5_K or Q6_K");
+                embed_kind_ = e->quant;
+                const size_t eb = static_cast<size_t>(c_.vocab) * H * (e->quant == RL_Q_F32 ? 4 : 2);
+                void* ed = mem_.get(eb);
+                RL_HIP(hipMemcpyAsync(ed, e->data, eb, hipMemcpyHostToDevice, st_));
+                embed_ = ed;
+            }
             lm_head_ = upload_lin({need(find, "lm_head")}, c_.vocab, H);
             final_norm_ = upload_vec(need(find, "final_norm"), H);
         }

@@ -61,6 +61,9 @@ void pack_bf16_rows(const uint16_t* w, uint16_t* dst, int m, int n, int rt_strid
 
 // kquant.hip
 size_t kq_workspace_bytes(int m, int n, int T);
+// Host dequantisation of row-major GGML blocks (Q8_0 / Q4_K / Q5_K / Q6_K) with the
+// reference's rounding order (loader.cpp); n = number of values.
+void dequant_host(int quant, const uint8_t* blocks, float* out, int64_t n);
 void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_t ws_bytes, int m, int n, int T,
              int accumulate, int ldy, hipStream_t s);
 

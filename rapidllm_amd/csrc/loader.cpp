@@ -1090,6 +1090,17 @@ void finish(RlWeights& W) {
 }
 
 }  // namespace
+
+void dequant_host(int quant, const uint8_t* blocks, float* out, int64_t n) {
+    switch (quant) {
+    case RL_Q_Q8_0: deq_q8_0(blocks, out, n); break;
+    case RL_Q_Q4_K: deq_q4_k(blocks, out, n); break;
+    case RL_Q_Q5_K: deq_q5_k(blocks, out, n); break;
+    case RL_Q_Q6_K: deq_q6_k(blocks, out, n); break;
+    default: fail(RL_ERR_UNSUPPORTED, "dequant_host: not a block format");
+    }
+}
+
 }  // namespace rl
 
 extern "C" {

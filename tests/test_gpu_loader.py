@@ -1,7 +1,7 @@
 """Engines created from checkpoint files (rl_hip_weights_open -> rl_hip_engine_create):
 an HF FP8 directory gives the same logits, bit for bit, as the engine created from
 the in-memory table the file was written from; a GGUF file in llama.cpp's qwen35
-conventions (K-quant linears, raw RMSNorm scales, ssm_a = -exp(A_log), tiled V
+conventions (K-quant linears and embedding, raw RMSNorm scales, ssm_a = -exp(A_log), tiled V
 heads) matches the CPU oracle model run on the loaded table, and the untiled
 model's greedy tokens."""
 import numpy as np
@@ -58,8 +58,10 @@ def test_hf_fp8_checkpoint_equals_in_memory_table(gpu, orc, tmp_path):
 
 def test_gguf_llama_checkpoint_matches_oracle(gpu, orc, tmp_path):
     spec = mini_spec(n_layers=4, layer_kinds=[0, 1, 0, 0])
-    W = M.random_weights(spec, seed=11, linear_quant=M.Q_Q4_K)
+    W = M.random_weights(spec, seed=11, linear_quant=M.Q_Q4_K, head_quant=M.Q_Q6_K)
     r = np.random.default_rng(5)
+    # GGUF token_embd as Q4_K: the engine dequantises it to an F32 table
+    W.add("embed", M.Q_Q4_K, M.synth.q4k_blocks(r, spec.vocab, spec.hidden), spec.vocab, spec.hidden)
     for i, k in enumerate(spec.layer_kinds):
         if k == M.LAYER_DELTA:  # out_proj columns are permuted by the V-head tiling: keep it BF16
             n = f"layers[{i}].delta.gemm.out_proj"
