@@ -617,11 +617,16 @@ __global__ __launch_bounds__(256) void gdn_pf_conv_kernel(GdnPfArgs p) {
 // while the current block's tokens run, so the per-token chain reads LDS only.
 constexpr int kPfTB = 32;
 constexpr int kPfTokFloats = 2 * kDK + kCW + 2;  // q | k | v | g, beta
+// 16 threads per value column (8 state rows each): 8 waves per workgroup, twice the
+// waves of the decode layout, so the per-token chains of two waves share a SIMD
+constexpr int kPfCh = 16;
+constexpr int kPfRows = kDK / kPfCh;
+constexpr int kPfCT = kCW * kPfCh;
 
-__global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
+__global__ __launch_bounds__(kPfCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     const int tid = threadIdx.x;
-    const int c = tid & (kCChunks - 1);
-    const int jj = tid / kCChunks;
+    const int c = tid & (kPfCh - 1);
+    const int jj = tid / kPfCh;
     const int chunks = p.dv / kCW;
     const int h = blockIdx.x / chunks, cc = blockIdx.x % chunks;
     const int j = cc * kCW + jj;
@@ -631,15 +636,18 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
 
     __shared__ __align__(16) float blk[2][kPfTB][kPfTokFloats];
+    // per-token scales of the block, computed once per block off the recurrence's
+    // dependency chain: 1/|q| * 1/sqrt(dk) and 1/|k| (eps 1e-6 inside the root)
+    __shared__ float inv_s[2][kPfTB][2];
     // staging: element e of a block = (token, float index); 16-byte units where possible
     constexpr int kUnits = kPfTB * (2 * kDK + kCW) / 4;  // q, k, v as float4 units
-    constexpr int kPer = (kUnits + kCT - 1) / kCT;
+    constexpr int kPer = (kUnits + kPfCT - 1) / kPfCT;
     float4 stg[kPer];
     float2 stg_g = make_float2(0.f, 0.f);
     auto stage_load = [&](int t0) {
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const int u = tid + q * kCT;
+            const int u = tid + q * kPfCT;
             stg[q] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (u < kUnits) {
                 const int tt = u / ((2 * kDK + kCW) / 4), f = (u % ((2 * kDK + kCW) / 4)) * 4;
@@ -659,7 +667,7 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     auto stage_store = [&](int buf) {
 #pragma unroll
         for (int q = 0; q < kPer; ++q) {
-            const int u = tid + q * kCT;
+            const int u = tid + q * kPfCT;
             if (u < kUnits) {
                 const int tt = u / ((2 * kDK + kCW) / 4), f = (u % ((2 * kDK + kCW) / 4)) * 4;
                 *reinterpret_cast<float4*>(&blk[buf][tt][f]) = stg[q];
@@ -670,13 +678,23 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
             blk[buf][tid][2 * kDK + kCW + 1] = stg_g.y;
         }
     };
+    // after a block is in LDS: 8 lanes per (token, q|k) vector, 16 values each
+    auto block_norms = [&](int buf) {
+        const int v = tid >> 3, part = tid & 7;  // v = 2 * token + (0: q, 1: k)
+        const float* x = &blk[buf][v >> 1][(v & 1) * kDK + 16 * part];
+        float a4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int r = 0; r < 16; ++r) a4[r & 3] = fmaf(x[r], x[r], a4[r & 3]);
+        const float sum = group8_sum((a4[0] + a4[1]) + (a4[2] + a4[3]));
+        if (part == 0) inv_s[buf][v >> 1][v & 1] = (v & 1) ? 1.f / sqrtf(sum + 1e-6f) : 1.f / sqrtf(sum + 1e-6f) * qscale;
+    };
 
-    const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + kCRows * c;
-    float S[kCRows];
+    const size_t s_off = (static_cast<size_t>(h) * p.dv + j) * kDK + kPfRows * c;
+    float S[kPfRows];
     {
         const f32x4* sp = reinterpret_cast<const f32x4*>(p.S + s_off);
 #pragma unroll
-        for (int r = 0; r < kCRows / 4; ++r) {
+        for (int r = 0; r < kPfRows / 4; ++r) {
             const f32x4 v = sp[r];
             S[4 * r] = v[0];
             S[4 * r + 1] = v[1];
@@ -687,6 +705,8 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     stage_load(0);
     stage_store(0);
     __syncthreads();
+    block_norms(0);
+    __syncthreads();
     for (int t0 = 0; t0 < p.T; t0 += kPfTB) {
         const int buf = (t0 / kPfTB) & 1;
         const bool more = t0 + kPfTB < p.T;
@@ -694,52 +714,46 @@ __global__ __launch_bounds__(kCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
         const int nt = min(kPfTB, p.T - t0);
         for (int tt = 0; tt < nt; ++tt) {
             const float* tk = blk[buf][tt];
-            float q[kCRows], k[kCRows];
+            float q[kPfRows], k[kPfRows];
 #pragma unroll
-            for (int r = 0; r < kCRows / 4; ++r) {
-                const float4 a4 = *reinterpret_cast<const float4*>(tk + kCRows * c + 4 * r);
-                const float4 b4 = *reinterpret_cast<const float4*>(tk + kDK + kCRows * c + 4 * r);
+            for (int r = 0; r < kPfRows / 4; ++r) {
+                const float4 a4 = *reinterpret_cast<const float4*>(tk + kPfRows * c + 4 * r);
+                const float4 b4 = *reinterpret_cast<const float4*>(tk + kDK + kPfRows * c + 4 * r);
                 q[4 * r] = a4.x, q[4 * r + 1] = a4.y, q[4 * r + 2] = a4.z, q[4 * r + 3] = a4.w;
                 k[4 * r] = b4.x, k[4 * r + 1] = b4.y, k[4 * r + 2] = b4.z, k[4 * r + 3] = b4.w;
             }
             const float v = tk[2 * kDK + jj];
             const float g = tk[2 * kDK + kCW], beta = tk[2 * kDK + kCW + 1];
-            // L2 norms over the head's 128 dims (8 lanes of 16 rows), eps inside the root
-            float sq4[4] = {0.f, 0.f, 0.f, 0.f}, sk4[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-            for (int r = 0; r < kCRows; ++r) {
-                sq4[r & 3] = fmaf(q[r], q[r], sq4[r & 3]);
-                sk4[r & 3] = fmaf(k[r], k[r], sk4[r & 3]);
-            }
-            const float sq = group8_sum((sq4[0] + sq4[1]) + (sq4[2] + sq4[3]));
-            const float sk = group8_sum((sk4[0] + sk4[1]) + (sk4[2] + sk4[3]));
-            const float iq = 1.f / sqrtf(sq + 1e-6f) * qscale;
-            const float ik = 1.f / sqrtf(sk + 1e-6f);
+            const float iq = inv_s[buf][tt][0], ik = inv_s[buf][tt][1];
             float kv4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < kCRows; ++r) {
+            for (int r = 0; r < kPfRows; ++r) {
                 k[r] *= ik;
                 S[r] *= g;
                 kv4[r & 3] = fmaf(S[r], k[r], kv4[r & 3]);
             }
-            const float kv = group8_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
+            const float kv = group16_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
             const float delta = (v - kv) * beta;
             float ov4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-            for (int r = 0; r < kCRows; ++r) {
+            for (int r = 0; r < kPfRows; ++r) {
                 S[r] = fmaf(k[r], delta, S[r]);
                 ov4[r & 3] = fmaf(S[r], q[r] * iq, ov4[r & 3]);
             }
-            const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
+            const float ov = group16_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
             if (c == 0)
                 p.o[static_cast<size_t>(t0 + tt) * p.nv * p.dv + static_cast<size_t>(h) * p.dv + j] = ov;
         }
         if (more) stage_store(buf ^ 1);
         __syncthreads();
+        if (more) {
+            block_norms(buf ^ 1);
+            __syncthreads();
+        }
     }
     f32x4* dp = reinterpret_cast<f32x4*>(p.S + s_off);
 #pragma unroll
-    for (int r = 0; r < kCRows / 4; ++r) dp[r] = f32x4{S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]};
+    for (int r = 0; r < kPfRows / 4; ++r) dp[r] = f32x4{S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]};
 }
 
 }  // namespace
@@ -826,7 +840,7 @@ void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_lo
     const size_t n = static_cast<size_t>(T) * (conv_dim + nv);
     hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p);
     check_launch("gdn_pf_conv_kernel");
-    hipLaunchKernelGGL(gdn_pf_rec_kernel, dim3(nv * (dv / kCW)), dim3(kCT), 0, s, p);
+    hipLaunchKernelGGL(gdn_pf_rec_kernel, dim3(nv * (dv / kCW)), dim3(kPfCT), 0, s, p);
     check_launch("gdn_pf_rec_kernel");
 }
 
