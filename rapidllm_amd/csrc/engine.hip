@@ -204,7 +204,7 @@ class Engine {
     // steps the committed state through it in registers (gdn_prefill; the conv
     // window ping-pongs between ring slots 0 and 1), attention is the causal prefill kernel (which
     // also writes the chunk's K/V).  RMSNorms are explicit (norm + pack kernels).
-    static constexpr int kPfChunk = 512;
+    static constexpr int kPfChunk = 2048;
     static constexpr int kPfMinTokens = 16;
     int pf_cap_ = 0;
     float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr, *pf_xc_ = nullptr,
@@ -216,12 +216,14 @@ class Engine {
 
     // RL_PREFILL_CHUNK: 0 = every prompt token through decode steps (T <= max_T);
     // n > 0 = chunk size (default kPfChunk)
-    static int pf_chunk_setting() {
-        static const int v = [] {
+    // read once per engine (at its first prefill)
+    mutable int pf_chunk_ = -1;
+    int pf_chunk_setting() const {
+        if (pf_chunk_ < 0) {
             const char* e = std::getenv("RL_PREFILL_CHUNK");
-            return e ? std::max(0, std::atoi(e)) : kPfChunk;
-        }();
-        return v;
+            pf_chunk_ = e ? std::max(0, std::atoi(e)) : kPfChunk;
+        }
+        return pf_chunk_;
     }
 
     bool can_prefill_chunked() const {

@@ -129,8 +129,10 @@ def test_attn_prefill_then_decode(gpu, orc):
     assert rel_l2(got[0], want[T]) < 1e-3
 
 
-def test_engine_chunked_prefill_matches_oracle(gpu, orc):
-    """A 600-token prompt: two prefill chunks (512 + 84) through the chunked path,
+@pytest.mark.parametrize("chunk", ["512", "2048"])
+def test_engine_chunked_prefill_matches_oracle(gpu, orc, monkeypatch, chunk):
+    """A 600-token prompt: two prefill chunks (512 + 84, RL_PREFILL_CHUNK=512) or one
+    (the default chunk of 2048) through the chunked path,
     the last max_T tokens as a decode step; logits equal the oracle's, decoding and
     speculative generation continue exactly as from a token-by-token prefill."""
     from oracle.oracle import OracleModel
@@ -139,6 +141,7 @@ def test_engine_chunked_prefill_matches_oracle(gpu, orc):
     from tests.test_gpu_engine import margin_ok, mini_spec
     spec = mini_spec()
     W = M.random_weights(spec, seed=3, w_scale=(1e-3, 1e-2))
+    monkeypatch.setenv("RL_PREFILL_CHUNK", chunk)
     eng = Engine(spec, W, ctx=1024)
     orc_m = OracleModel(spec, W, ctx=1024)
     rng = np.random.default_rng(5)
