@@ -4,8 +4,8 @@
 // to every prompt token, i.e. the reference's prefill linears
 // (src/kernels/cuda/cuda_engine.cu:18338-18590 launch_prefill_chunk -> launch_linear
 // for T > 8, cuda_engine.cu:12008-12016).  At prefill sizes the work is
-// matrix-core bound, not HBM bound: one 128-row x 64-token output block per
-// workgroup reads each weight tile once for 64 tokens.
+// matrix-core bound, not HBM bound: one 128-row x 128-token output block per
+// workgroup reads each weight tile once for 128 tokens.
 //
 // Operands as in gemm.hip: A = 16 weight rows x 32 k, e4m3 decoded to bf16 by the
 // hardware converter (exact); B = 32 k x 16 tokens of the activation fragments
@@ -14,8 +14,9 @@
 // block's fp32 partial.  Weights use the decode GEMM's tiled layout (16 rows x 128
 // columns per 2 KiB tile), activations its fragment layout for T tokens.
 //
-// Workgroup: 4 waves, 8 row tiles (128 rows) x 64 tokens; wave w owns tokens
-// 16w .. 16w+15 of the block for all 8 row tiles.  The 8 weight tiles of a column
+// Workgroup: 4 waves, 8 row tiles (128 rows) x 128 tokens; wave w owns tokens
+// 32w .. 32w+31 of the block (two 16-token column tiles, so each weight fragment
+// read from LDS feeds four MFMAs) for all 8 row tiles.  The 8 weight tiles of a column
 // block (16 KiB) are staged once in LDS (double buffered, the next block's loads in
 // flight during the MFMAs) and read by all four waves.
 #include "internal.h"
@@ -25,7 +26,8 @@ using namespace rl;
 namespace {
 
 constexpr int kPfRT = 8;     // row tiles per workgroup
-constexpr int kPfTok = 64;   // tokens per workgroup
+constexpr int kPfNT = 2;     // 16-token column tiles per wave
+constexpr int kPfTok = 64 * kPfNT;  // tokens per workgroup
 constexpr int kTileRows = 16;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
@@ -58,8 +60,12 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
     const int g = lane >> 4, col = lane & 15;
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     const int rt0 = blockIdx.x * kPfRT;
-    const int tok = blockIdx.y * kPfTok + wave * 16 + col;  // B column of this lane
-    const int tokc = min(tok, T - 1);
+    int tokv[kPfNT], tokcv[kPfNT];
+#pragma unroll
+    for (int nt = 0; nt < kPfNT; ++nt) {
+        tokv[nt] = blockIdx.y * kPfTok + (wave * kPfNT + nt) * 16 + col;  // B column of this lane
+        tokcv[nt] = min(tokv[nt], T - 1);
+    }
     const int NC = 2 * T;
 
     __shared__ i32x4 wl[2][kPfRT][2][64];  // [buffer][row tile][16-B chunk][lane]
@@ -84,9 +90,11 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
         }
     };
 
-    f32x4 tot[kPfRT];
+    f32x4 tot[kPfNT][kPfRT];
 #pragma unroll
-    for (int r = 0; r < kPfRT; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int nt = 0; nt < kPfNT; ++nt)
+#pragma unroll
+        for (int r = 0; r < kPfRT; ++r) tot[nt][r] = f32x4{0.f, 0.f, 0.f, 0.f};
 
     stage_load(0);
     stage_store(0);
@@ -95,59 +103,71 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
         const int buf = kb & 1;
         if (kb + 1 < n_kb) stage_load(kb + 1);
         // activation fragments of this lane's token: 4 k-steps x (hi, mid)
-        i32x4 bh[4], bm[4];
+        i32x4 bh[kPfNT][4], bm[kPfNT][4];
 #pragma unroll
-        for (int i = 0; i < 4; ++i) {
-            const size_t u = (static_cast<size_t>(kb * 4 + i) * 4 + g) * NC + tokc;
-            bh[i] = frag[u];
-            bm[i] = frag[u + T];
-        }
+        for (int nt = 0; nt < kPfNT; ++nt)
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const size_t u = (static_cast<size_t>(kb * 4 + i) * 4 + g) * NC + tokcv[nt];
+                bh[nt][i] = frag[u];
+                bm[nt][i] = frag[u + T];
+            }
 #pragma unroll
         for (int r = 0; r < kPfRT; ++r) {
             const int rt = min(rt0 + r, m_tiles - 1);
             const float sc = tscale[static_cast<size_t>(rt) * n_kb + kb];
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[kPfNT];
+#pragma unroll
+            for (int nt = 0; nt < kPfNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
                 const i32x4 wv = wl[buf][r][i >> 1][lane];
                 Frag8 a, b;
                 e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[2] : wv[0]), a.u[0], a.u[1]);
                 e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[3] : wv[1]), a.u[2], a.u[3]);
-                b.i = bh[i];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
-                b.i = bm[i];
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+#pragma unroll
+                for (int nt = 0; nt < kPfNT; ++nt) {
+                    b.i = bh[nt][i];
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
+                    b.i = bm[nt][i];
+                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
+                }
             }
-            tot[r] += sc * acc;
+#pragma unroll
+            for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += sc * acc[nt];
         }
         if (kb + 1 < n_kb) stage_store(buf ^ 1);
         __syncthreads();
     }
 
-    // lane (g, col) holds rows 4g .. 4g+3 of each row tile for token `tok`
-    if (tok >= T) return;
-    float* yrow = Y + static_cast<size_t>(tok) * ldy;
-    if constexpr (EPI == 2) {
+    // lane (g, col) holds rows 4g .. 4g+3 of each row tile for token tokv[nt]
 #pragma unroll
-        for (int r = 0; r < kPfRT; r += 2) {
-            if (rt0 + r + 1 >= m_tiles) break;
-            const int orow = ((rt0 + r) / 2) * kTileRows + 4 * g;
+    for (int nt = 0; nt < kPfNT; ++nt) {
+        const int tok = tokv[nt];
+        if (tok >= T) break;
+        float* yrow = Y + static_cast<size_t>(tok) * ldy;
+        if constexpr (EPI == 2) {
 #pragma unroll
-            for (int v = 0; v < 4; ++v)
-                if (orow + v < m_valid) yrow[orow + v] = silu_f(tot[r][v]) * tot[r + 1][v];
-        }
-    } else {
+            for (int r = 0; r < kPfRT; r += 2) {
+                if (rt0 + r + 1 >= m_tiles) break;
+                const int orow = ((rt0 + r) / 2) * kTileRows + 4 * g;
 #pragma unroll
-        for (int r = 0; r < kPfRT; ++r) {
-            if (rt0 + r >= m_tiles) break;
-            const int row = (rt0 + r) * kTileRows + 4 * g;
+                for (int v = 0; v < 4; ++v)
+                    if (orow + v < m_valid) yrow[orow + v] = silu_f(tot[nt][r][v]) * tot[nt][r + 1][v];
+            }
+        } else {
 #pragma unroll
-            for (int v = 0; v < 4; ++v) {
-                if (row + v >= m_valid) break;
-                if constexpr (EPI == 1)
-                    yrow[row + v] += tot[r][v];
-                else
-                    yrow[row + v] = tot[r][v];
+            for (int r = 0; r < kPfRT; ++r) {
+                if (rt0 + r >= m_tiles) break;
+                const int row = (rt0 + r) * kTileRows + 4 * g;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    if (row + v >= m_valid) break;
+                    if constexpr (EPI == 1)
+                        yrow[row + v] += tot[nt][r][v];
+                    else
+                        yrow[row + v] = tot[nt][r][v];
+                }
             }
         }
     }
