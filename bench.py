@@ -33,6 +33,45 @@ CTX = 32768
 PF_TOKENS = 4096
 
 
+def measure_gguf_step(spec, K, W):
+    """The same C5 step with the layer linears and MTP fc as Q4_K super-blocks and a
+    Q6_K lm_head (the tensor mix of a Q4_K_M GGUF; in_proj a/b BF16), random blocks
+    generated on the device: T=1 and T=4 step times and the weight bytes a T=1 step
+    reads."""
+    from rapidllm_amd.engine import Engine
+
+    os.environ["RL_SYNTH_LINEAR"] = "q4_k"
+    try:
+        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321)
+    finally:
+        del os.environ["RL_SYNTH_LINEAR"]
+    eng.synthetic_context(CTX)
+    eng.time_steps(1, W)
+    t1 = eng.time_steps(1, K) / K
+    eng.synthetic_context(CTX)
+    eng.time_steps(4, W)
+    t4 = eng.time_steps(4, K) / K
+    eng.close()
+    H, I, V = spec.hidden, spec.intermediate, spec.vocab
+    nk, nv, dk, dv = spec.n_k_heads, spec.n_v_heads, spec.k_dim, spec.v_dim
+    conv = 2 * nk * dk + nv * dv
+    q4 = lambda m, n: m * (n // 256) * 144
+    lin = 0
+    for kind in spec.layer_kinds:
+        if kind == 0:
+            lin += q4(conv, H) + q4(nv * dv, H) + 2 * nv * H * 2 + q4(H, nv * dv)
+        else:
+            lin += q4(2 * spec.n_q * spec.head_dim + 2 * spec.n_kv * spec.head_dim, H) + q4(H, spec.n_q * spec.head_dim)
+        lin += 2 * q4(I, H) + q4(H, I)
+    head = V * (H // 256) * 210
+    kv = step_bytes(spec, 1, CTX)
+    total = lin + head + kv["kv"] + kv["state"]
+    return {"workload": "C5 step, Q4_K layer linears + Q6_K lm_head (Q4_K_M mix), 32K context",
+            "t1_ms": round(t1, 4), "tok_s": round(1000.0 / t1, 3), "t4_verify_ms": round(t4, 4),
+            "t4_over_t1": round(t4 / t1, 4), "t1_bytes": int(total),
+            "t1_GBps": round(total / t1 / 1e6, 1), "t1_frac": round(total / t1 / 1e6 / PEAK_GBS, 4)}
+
+
 def step_bytes(spec, T, ctx):
     """Algorithmic HBM bytes of one T-token step: every weight byte once, KV read
     once (+ the T new rows written), recurrent state read once and written once per
@@ -506,6 +545,7 @@ def main():
     eng.prefill(ids)
     pf_s = time.perf_counter() - t0
     eng.close()
+    gguf = measure_gguf_step(spec, K, W)
 
     b1 = step_bytes(spec, 1, CTX)
     b4 = step_bytes(spec, 4, CTX)
@@ -536,6 +576,7 @@ def main():
         "t4_over_t1": round(t4 / t1, 4),
         "mtp_draft3_ms": round(tm, 4),
         "spec_tok_s_full_accept": round(4000.0 / (t4 + tm), 3),
+        "gguf_q4_k": gguf,
         "batch4_step_ms": round(tb4, 4),
         "batch4_tok_s": round(4000.0 / tb4, 3),
         "prefill_tokens": PF_TOKENS,

@@ -140,9 +140,15 @@ class Engine {
     // Synthetic random-init weights of the configured architecture, generated on the
     // device (benchmark configs: e4m3 bytes uniform without NaN codes, 128x128 fp32
     // scales log-uniform in [1e-3, 1e-1], bf16 embedding / lm_head, small norms).
+    // RL_SYNTH_LINEAR=q4_k / q6_k: the layer linears and the MTP fc as GGML
+    // K-quant blocks instead (in_proj a/b BF16, lm_head Q6_K, as in a Q4_K_M file).
     void load_synthetic(uint64_t seed) {
         synth_seed_ = seed;
         synthetic_ = true;
+        if (const char* e = std::getenv("RL_SYNTH_LINEAR")) {
+            if (std::strcmp(e, "q4_k") == 0) synth_quant_ = RL_Q_Q4_K;
+            else if (std::strcmp(e, "q6_k") == 0) synth_quant_ = RL_Q_Q6_K;
+        }
         build([&](const std::string&) -> const RlTensor* { return nullptr; });
     }
 
@@ -594,6 +600,7 @@ class Engine {
     DevAlloc mem_;
     std::map<std::string, const RlTensor*> tab_;
     bool synthetic_ = false;
+    int synth_quant_ = RL_Q_FP8_E4M3_B128;  // synthetic layer-linear format
     uint64_t synth_seed_ = 0;
     uint64_t synth_ctr_ = 0;
 
@@ -694,7 +701,8 @@ class Engine {
             uint16_t* e = mem_.get_n<uint16_t>(static_cast<size_t>(c_.vocab) * H);
             fill_normal_bf16(e, static_cast<size_t>(c_.vocab) * H, 0.02f, next_seed(), st_);
             embed_ = e;
-            lm_head_ = synth_lin(RL_Q_BF16, c_.vocab, H);
+            lm_head_ = synth_quant_ == RL_Q_FP8_E4M3_B128 ? synth_lin(RL_Q_BF16, c_.vocab, H)
+                                                          : synth_kq(RL_Q_Q6_K, c_.vocab, H);
             final_norm_ = synth_vec(H, 0.f, 0.1f);
         } else {
             const RlTensor* e = need(find, "embed");
@@ -753,7 +761,7 @@ class Engine {
                 const std::vector<int> rows = {conv_dim, zdim, nv, nv};
                 const std::vector<int> offs = {0, Ly.off_z, Ly.off_a, Ly.off_b};
                 make_fused(find, names, rows, offs, H, Ly.in_parts, Ly.in_offs);
-                Ly.out_proj = synthetic_ ? synth_lin(RL_Q_FP8_E4M3_B128, H, zdim)
+                Ly.out_proj = synthetic_ ? synth_layer_lin(H, zdim)
                                          : upload_lin({need(find, p + "delta.gemm.out_proj")}, H, zdim);
                 if (synthetic_) {
                     Ly.A_log = synth_vec(nv, 0.f, 0.5f);
@@ -778,14 +786,18 @@ class Engine {
                 const std::vector<int> rows = {2 * nq * hd, nkv * hd, nkv * hd};
                 const std::vector<int> offs = {0, 2 * nq * hd, 2 * nq * hd + nkv * hd};
                 make_fused(find, names, rows, offs, H, Ly.qkv_parts, Ly.qkv_offs);
-                Ly.o_proj = synthetic_ ? synth_lin(RL_Q_FP8_E4M3_B128, H, nq * hd)
+                Ly.o_proj = synthetic_ ? synth_layer_lin(H, nq * hd)
                                        : upload_lin({need(find, p + "attn.wo")}, H, nq * hd);
                 Ly.q_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.q_norm"), hd);
                 Ly.k_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.k_norm"), hd);
                 max_width = std::max(max_width, Ly.qkv_width);
             }
             // MLP
-            if (synthetic_) {
+            if (synthetic_ && synth_quant_ != RL_Q_FP8_E4M3_B128) {
+                Ly.gate = synth_kq(synth_quant_, I, H);
+                Ly.up = synth_kq(synth_quant_, I, H);
+                Ly.down = synth_kq(synth_quant_, H, I);
+            } else if (synthetic_) {
                 Ly.gate_up = synth_gate_up(I, H);
                 Ly.down = synth_lin(RL_Q_FP8_E4M3_B128, H, I);
             } else {
@@ -808,7 +820,7 @@ class Engine {
         if (c_.has_mtp) {
             has_mtp_ = true;
             if (synthetic_) {
-                mtp_fc_ = synth_lin(RL_Q_FP8_E4M3_B128, H, 2 * H);
+                mtp_fc_ = synth_layer_lin(H, 2 * H);
                 mtp_nh_ = synth_vec(H, 0.f, 0.1f);
                 mtp_ne_ = synth_vec(H, 0.f, 0.1f);
                 mtp_norm_ = synth_vec(H, 0.f, 0.1f);
@@ -1013,6 +1025,16 @@ class Engine {
     void make_fused(Find& find, const std::vector<std::string>& names, const std::vector<int>& rows,
                     const std::vector<int>& offs, int n, std::vector<Lin>& parts, std::vector<int>& out_offs) {
         const int total = offs.back() + align16(rows.back());
+        if (synthetic_ && synth_quant_ != RL_Q_FP8_E4M3_B128) {
+            parts.clear();
+            out_offs.clear();
+            for (size_t k = 0; k < rows.size(); ++k) {
+                // DeltaNet a / b rows (a few dozen) stay BF16, as in K-quant files
+                parts.push_back(rows[k] < 256 ? synth_lin(RL_Q_BF16, rows[k], n) : synth_kq(synth_quant_, rows[k], n));
+                out_offs.push_back(offs[k]);
+            }
+            return;
+        }
         if (synthetic_) {
             Lin L = alloc_dense(RL_Q_FP8_E4M3_B128, total, n);
             synth_fill_dense(L, total, n);
@@ -1071,6 +1093,30 @@ class Engine {
             RL_HIP(hipStreamSynchronize(st_));
             (void)hipFree(tmp);
         }
+    }
+
+    Lin synth_kq(int type, int rows, int n) {
+        RL_REQUIRE(n % 256 == 0, RL_ERR_UNSUPPORTED, "synthetic K-quant: columns must be a multiple of 256");
+        Lin L;
+        L.kind = type;
+        L.m = rows;
+        L.n = n;
+        kq_need_ = std::max(kq_need_, kq_workspace_bytes(rows, n, tmax_));
+        L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(type, rows, n)));
+        const size_t nb = static_cast<size_t>(rows) * (n / 256);
+        uint8_t* tmp = nullptr;
+        RL_HIP(hipMalloc(&tmp, nb * (type == RL_Q_Q4_K ? 144 : 210)));
+        fill_kquant(tmp, type, nb, next_seed(), st_);
+        const int rc = rl_hip_pack_kquant(type, tmp, L.w, rows, n, st_);
+        RL_HIP(hipStreamSynchronize(st_));
+        (void)hipFree(tmp);
+        if (rc != RL_OK) throw Error(rc, rl_hip_last_error());
+        return L;
+    }
+
+    Lin synth_layer_lin(int rows, int n) {
+        return synth_quant_ == RL_Q_FP8_E4M3_B128 ? synth_lin(RL_Q_FP8_E4M3_B128, rows, n)
+                                                  : synth_kq(synth_quant_, rows, n);
     }
 
     Lin synth_lin(int kind, int rows, int n) {

@@ -167,6 +167,8 @@ void accept(const int* toks, const int* preds, int T, int force_all, int* pos, i
 
 // synth.hip
 void fill_fp8(uint8_t* p, size_t n, uint64_t seed, hipStream_t s);
+// random GGML Q4_K / Q6_K super-blocks (fp16 d, dmin log-uniform in [1e-4, 1e-2])
+void fill_kquant(uint8_t* p, int type, size_t n_blocks, uint64_t seed, hipStream_t s);
 void fill_loguniform(float* p, size_t n, float lo, float hi, uint64_t seed, hipStream_t s);
 void fill_normal_f32(float* p, size_t n, float mean, float stdv, uint64_t seed, hipStream_t s);
 void fill_normal_bf16(uint16_t* p, size_t n, float stdv, uint64_t seed, hipStream_t s);

@@ -60,11 +60,39 @@ __global__ void fill_normal_16_kernel(uint16_t* p, size_t n, float stdv, uint64_
     }
 }
 
+// GGML K-quant super-blocks: random quant / scale bytes, fp16 d (and dmin)
+// log-uniform in [1e-4, 1e-2]
+__global__ void fill_kquant_kernel(uint8_t* p, size_t n_bytes, int bsz, int d_off, int n_d, uint64_t seed) {
+    for (size_t i = blockIdx.x * static_cast<size_t>(blockDim.x) + threadIdx.x; i < n_bytes;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x) {
+        const size_t b = i / bsz;
+        const int off = static_cast<int>(i % bsz);
+        uint8_t v;
+        if (off >= d_off && off < d_off + 2 * n_d) {
+            const int f = (off - d_off) >> 1;
+            const float u = unit01(mix64(seed ^ mix64(2 * b + f + 0x5bd1e995ull)));
+            const float d = expf(logf(1e-4f) + (logf(1e-2f) - logf(1e-4f)) * u);
+            const uint16_t h = __builtin_bit_cast(uint16_t, static_cast<_Float16>(d));
+            v = static_cast<uint8_t>(((off - d_off) & 1) ? h >> 8 : h & 0xff);
+        } else {
+            v = static_cast<uint8_t>(mix64(seed ^ mix64(i)));
+        }
+        p[i] = v;
+    }
+}
+
 constexpr int kGrid = 4096;
 
 }  // namespace
 
 namespace rl {
+
+void fill_kquant(uint8_t* p, int type, size_t n_blocks, uint64_t seed, hipStream_t s) {
+    const int bsz = type == RL_Q_Q4_K ? 144 : 210;
+    const int d_off = type == RL_Q_Q4_K ? 0 : 208, n_d = type == RL_Q_Q4_K ? 2 : 1;
+    hipLaunchKernelGGL(fill_kquant_kernel, dim3(kGrid), dim3(256), 0, s, p, n_blocks * bsz, bsz, d_off, n_d, seed);
+    check_launch("fill_kquant_kernel");
+}
 
 void fill_fp8(uint8_t* p, size_t n, uint64_t seed, hipStream_t s) {
     hipLaunchKernelGGL(fill_fp8_kernel, dim3(kGrid), dim3(256), 0, s, p, n, seed);

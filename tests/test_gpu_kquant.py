@@ -133,3 +133,20 @@ def test_gemm_kquant_repeat_and_accumulate(gpu):
     lin.forward(xd.ptr, yd.ptr, T, ws, accumulate=True)
     got = yd.numpy(np.float32, (T, m))
     assert rel_l2(got, Y0 + outs[0]) <= 1e-6
+
+
+def test_synthetic_q4_k_engine_spec_invariant(gpu, monkeypatch):
+    """The benchmark's device-generated K-quant model (RL_SYNTH_LINEAR=q4_k: Q4_K
+    layer linears, Q6_K lm_head): T=4 verify with MTP drafts gives the tokens of
+    plain T=1 decoding (the greedy invariant, tests/test_spec.cpp:46-79)."""
+    from rapidllm_amd import model as M
+    from rapidllm_amd.engine import Engine
+
+    spec = M.ModelSpec(vocab=1000, hidden=256, n_layers=4, intermediate=512, n_k_heads=2, n_v_heads=4, n_q=4,
+                       n_kv=2, layer_kinds=[0, 0, 0, 1])
+    monkeypatch.setenv("RL_SYNTH_LINEAR", "q4_k")
+    eng = Engine(spec, None, ctx=512, seed=5)
+    off, _, _ = eng.generate([1, 2, 3], 12, spec_n=0)
+    on, _, _ = eng.generate([1, 2, 3], 12, spec_n=3)
+    assert on == off
+    eng.close()
