@@ -1029,9 +1029,18 @@ class Engine {
             parts.clear();
             out_offs.clear();
             for (size_t k = 0; k < rows.size(); ++k) {
-                // DeltaNet a / b rows (a few dozen) stay BF16, as in K-quant files
-                parts.push_back(rows[k] < 256 ? synth_lin(RL_Q_BF16, rows[k], n) : synth_kq(synth_quant_, rows[k], n));
-                out_offs.push_back(offs[k]);
+                // DeltaNet a / b rows (a few dozen) stay BF16, as in K-quant files,
+                // and share one BF16 matrix (one launch)
+                if (rows[k] < 256) {
+                    size_t e = k + 1;
+                    while (e < rows.size() && rows[e] < 256) ++e;
+                    parts.push_back(synth_lin(RL_Q_BF16, offs[e - 1] - offs[k] + rows[e - 1], n));
+                    out_offs.push_back(offs[k]);
+                    k = e - 1;
+                } else {
+                    parts.push_back(synth_kq(synth_quant_, rows[k], n));
+                    out_offs.push_back(offs[k]);
+                }
             }
             return;
         }
@@ -1053,11 +1062,25 @@ class Engine {
             out_offs = {0};
             return;
         }
+        // mixed formats: consecutive FP8 / BF16 parts of one format still share one
+        // tiled matrix (e.g. the BF16 a / b rows beside K-quant q|k|v and z)
         parts.clear();
         out_offs.clear();
-        for (size_t k = 0; k < ts.size(); ++k) {
-            parts.push_back(upload_lin({ts[k]}, rows[k], n));
+        for (size_t k = 0; k < ts.size();) {
+            const int q = ts[k]->quant;
+            size_t e = k + 1;
+            if (q == RL_Q_FP8_E4M3_B128 || q == RL_Q_BF16)
+                while (e < ts.size() && ts[e]->quant == q) ++e;
+            if (e - k > 1) {
+                const int base = offs[k];
+                Lin L = alloc_dense(q, offs[e - 1] - base + align16(rows[e - 1]), n);
+                for (size_t j = k; j < e; ++j) place_dense(L, ts[j], rows[j], n, 1, (offs[j] - base) / 16);
+                parts.push_back(L);
+            } else {
+                parts.push_back(upload_lin({ts[k]}, rows[k], n));
+            }
             out_offs.push_back(offs[k]);
+            k = e;
         }
     }
 
