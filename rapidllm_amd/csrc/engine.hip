@@ -96,7 +96,8 @@ struct Layer {
     int aslot = 0;
     // MLP
     Lin gate_up;  // FP8/BF16: interleaved gate/up tiles, SwiGLU epilogue
-    Lin gate, up; // K-quant: separate
+    Lin gate, up; // K-quant: separate, or gate_cat: gate rows then up rows in `gate`
+    bool gate_cat = false;
     Lin down;
 };
 
@@ -794,8 +795,8 @@ class Engine {
             }
             // MLP
             if (synthetic_ && synth_quant_ != RL_Q_FP8_E4M3_B128) {
-                Ly.gate = synth_kq(synth_quant_, I, H);
-                Ly.up = synth_kq(synth_quant_, I, H);
+                Ly.gate = synth_kq(synth_quant_, 2 * I, H);
+                Ly.gate_cat = true;
                 Ly.down = synth_kq(synth_quant_, H, I);
             } else if (synthetic_) {
                 Ly.gate_up = synth_gate_up(I, H);
@@ -808,6 +809,11 @@ class Engine {
                 RL_REQUIRE(I == c_.intermediate, RL_ERR_FORMAT, "mlp.down shape disagrees with intermediate");
                 if (g->quant == u->quant && (g->quant == RL_Q_FP8_E4M3_B128 || g->quant == RL_Q_BF16)) {
                     Ly.gate_up = upload_gate_up(g, u, I, H);
+                } else if (g->quant == u->quant && (g->quant == RL_Q_Q4_K || g->quant == RL_Q_Q6_K) && I % 64 == 0) {
+                    // one K-quant launch for gate and up: the tiled layout is row-tile
+                    // major, so up's tiles follow gate's
+                    Ly.gate = upload_kq_cat(g, u, I, H);
+                    Ly.gate_cat = true;
                 } else {
                     Ly.gate = upload_lin({g}, I, H);
                     Ly.up = upload_lin({u}, I, H);
@@ -901,7 +907,7 @@ class Engine {
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
-        g_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
+        g_ = mem_.get_n<float>(static_cast<size_t>(T) * 2 * I);  // [T][2I] with gate_cat
         u_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         logits_ = mem_.get_n<float>(static_cast<size_t>(T) * c_.vocab);
         mtp_logits_ = mem_.get_n<float>(c_.vocab);
@@ -1116,6 +1122,32 @@ class Engine {
             RL_HIP(hipStreamSynchronize(st_));
             (void)hipFree(tmp);
         }
+    }
+
+    Lin upload_kq_cat(const RlTensor* g, const RlTensor* u, int I, int H) {
+        RL_REQUIRE(g->rows == I && u->rows == I && g->cols == H && u->cols == H && H % 256 == 0, RL_ERR_FORMAT,
+                   std::string(g->name) + ": shape");
+        Lin L;
+        L.kind = g->quant;
+        L.m = 2 * I;
+        L.n = H;
+        kq_need_ = std::max(kq_need_, kq_workspace_bytes(2 * I, H, tmax_));
+        const size_t half = rl_hip_kquant_tiled_bytes(g->quant, I, H);
+        L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(g->quant, 2 * I, H)));
+        const size_t bb = static_cast<size_t>(I) * (H / 256) * (g->quant == RL_Q_Q4_K ? 144 : 210);
+        uint8_t* tmp = nullptr;
+        RL_HIP(hipMalloc(&tmp, bb));
+        for (int k = 0; k < 2; ++k) {
+            RL_HIP(hipMemcpyAsync(tmp, (k ? u : g)->data, bb, hipMemcpyHostToDevice, st_));
+            const int rc = rl_hip_pack_kquant(g->quant, tmp, L.w + k * half, I, H, st_);
+            RL_HIP(hipStreamSynchronize(st_));
+            if (rc != RL_OK) {
+                (void)hipFree(tmp);
+                throw Error(rc, rl_hip_last_error());
+            }
+        }
+        (void)hipFree(tmp);
+        return L;
     }
 
     Lin synth_kq(int type, int rows, int n) {
@@ -1364,9 +1396,14 @@ class Engine {
                                    Ly.gate_up.m, Ly.gate_up.n, T, kEpiSwiGLU, I, I, st_, 1,
                                    down_frag ? frag_h_ : nullptr);
             } else {
-                linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
-                linear(Ly.up, xn_, u_, I, I, T, kEpiStore);
-                swiglu(g_, I, u_, I, h_, I, T, st_);
+                if (Ly.gate_cat) {
+                    linear(Ly.gate, xn_, g_, 2 * I, 2 * I, T, kEpiStore);
+                    swiglu(g_, 2 * I, g_ + I, 2 * I, h_, I, T, st_);
+                } else {
+                    linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
+                    linear(Ly.up, xn_, u_, I, I, T, kEpiStore);
+                    swiglu(g_, I, u_, I, h_, I, T, st_);
+                }
                 if (down_frag) pack_act(h_, frag_h_, I, T, st_);
             }
             pending = linear_residual(Ly.down, h_, T, down_frag ? frag_h_ : frag_);
