@@ -1037,16 +1037,13 @@ class Engine {
             for (size_t k = 0; k < rows.size(); ++k) {
                 // DeltaNet a / b rows (a few dozen) stay BF16, as in K-quant files,
                 // and share one BF16 matrix (one launch)
-                if (rows[k] < 256) {
-                    size_t e = k + 1;
-                    while (e < rows.size() && rows[e] < 256) ++e;
-                    parts.push_back(synth_lin(RL_Q_BF16, offs[e - 1] - offs[k] + rows[e - 1], n));
-                    out_offs.push_back(offs[k]);
-                    k = e - 1;
-                } else {
-                    parts.push_back(synth_kq(synth_quant_, rows[k], n));
-                    out_offs.push_back(offs[k]);
-                }
+                const bool small = rows[k] < 256;
+                size_t e = k + 1;
+                while (e < rows.size() && (rows[e] < 256) == small) ++e;
+                const int total_k = offs[e - 1] - offs[k] + (small ? rows[e - 1] : align16(rows[e - 1]));
+                parts.push_back(small ? synth_lin(RL_Q_BF16, total_k, n) : synth_kq(synth_quant_, total_k, n));
+                out_offs.push_back(offs[k]);
+                k = e - 1;
             }
             return;
         }
@@ -1075,9 +1072,34 @@ class Engine {
         for (size_t k = 0; k < ts.size();) {
             const int q = ts[k]->quant;
             size_t e = k + 1;
-            if (q == RL_Q_FP8_E4M3_B128 || q == RL_Q_BF16)
-                while (e < ts.size() && ts[e]->quant == q) ++e;
-            if (e - k > 1) {
+            while (e < ts.size() && ts[e]->quant == q) ++e;
+            if (e - k > 1 && (q == RL_Q_Q4_K || q == RL_Q_Q6_K)) {
+                // consecutive K-quant parts of one type: one tiled matrix, each part's
+                // 16-row tiles at its (16-row aligned) output offset
+                const int base = offs[k];
+                Lin L;
+                L.kind = q;
+                L.m = offs[e - 1] - base + align16(rows[e - 1]);
+                L.n = n;
+                kq_need_ = std::max(kq_need_, kq_workspace_bytes(L.m, n, tmax_));
+                L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(q, L.m, n)));
+                const size_t tile_row_bytes = rl_hip_kquant_tiled_bytes(q, 16, n);
+                for (size_t j = k; j < e; ++j) {
+                    const RlTensor* t = ts[j];
+                    RL_REQUIRE(t->rows == rows[j] && t->cols == n && n % 256 == 0, RL_ERR_FORMAT,
+                               std::string(t->name) + ": shape");
+                    const size_t bb = static_cast<size_t>(rows[j]) * (n / 256) * (q == RL_Q_Q4_K ? 144 : 210);
+                    uint8_t* tmp = nullptr;
+                    RL_HIP(hipMalloc(&tmp, bb));
+                    RL_HIP(hipMemcpyAsync(tmp, t->data, bb, hipMemcpyHostToDevice, st_));
+                    const int rc = rl_hip_pack_kquant(q, tmp, L.w + static_cast<size_t>((offs[j] - base) / 16) * tile_row_bytes,
+                                                      rows[j], n, st_);
+                    RL_HIP(hipStreamSynchronize(st_));
+                    (void)hipFree(tmp);
+                    if (rc != RL_OK) throw Error(rc, rl_hip_last_error());
+                }
+                parts.push_back(L);
+            } else if (e - k > 1 && (q == RL_Q_FP8_E4M3_B128 || q == RL_Q_BF16)) {
                 const int base = offs[k];
                 Lin L = alloc_dense(q, offs[e - 1] - base + align16(rows[e - 1]), n);
                 for (size_t j = k; j < e; ++j) place_dense(L, ts[j], rows[j], n, 1, (offs[j] - base) / 16);
