@@ -121,7 +121,11 @@ int rl_hip_gemm_fp8(const uint8_t* w_tiled, const float* tile_scale, const float
  * `type` is RL_Q_Q4_K or RL_Q_Q6_K.  Blocks are the GGUF bytes (144 B / 210 B per
  * 256 weights, rows contiguous); rl_hip_pack_kquant moves them (bytes only) into
  * the device layout.  X is fp32 [T][n], T in 1..4, n a multiple of 256.
- * rl_hip_dequant_kquant decodes row-major blocks bit-exactly like the reference. */
+ * rl_hip_dequant_kquant decodes row-major blocks bit-exactly like the reference.
+ * workspace (rl_hip_kquant_workspace_bytes): split-K tickets then partial sums.
+ * Zero-fill it once after allocation (rl_hip_memset); every launch leaves the
+ * tickets at zero again.  Launches sharing one workspace must not overlap in time:
+ * give each stream its own workspace. */
 size_t rl_hip_kquant_tiled_bytes(int type, int m, int n);
 size_t rl_hip_kquant_workspace_bytes(int m, int n, int T);
 int rl_hip_pack_kquant(int type, const uint8_t* blocks, uint8_t* tiled, int m, int n, void* stream);

@@ -122,17 +122,22 @@ float orc_bf16_to_f32(uint16_t h) { return bits_to_f(static_cast<uint32_t>(h) <<
 // Block-FP8 GEMV: y[i] = sum_j e4m3(W[i,j]) * scale[i/B][j/B] * x[j] with a double
 // accumulator, rounded to fp32 at the end (ops.cpp:182-194).  The product
 // (double)w * s * x is exact in double (4 + 24 + 24 significant bits).
-void orc_gemv_fp8(const uint8_t* W, const float* scale, const float* x, float* y, int m, int n, int block) {
+static void gemv_fp8_rows(const uint8_t* W, const float* scale, const float* x, float* y, int n, int block, int r0,
+                          int r1) {
     const int sb_cols = (n + block - 1) / block;
     float lut[256];
     for (int c = 0; c < 256; ++c) lut[c] = orc_e4m3_to_f32(static_cast<uint8_t>(c));
-    for (int i = 0; i < m; ++i) {
+    for (int i = r0; i < r1; ++i) {
         const uint8_t* row = W + static_cast<size_t>(i) * n;
         const float* srow = scale + static_cast<size_t>(i / block) * sb_cols;
         double acc = 0.0;
         for (int j = 0; j < n; ++j) acc += static_cast<double>(lut[row[j]]) * srow[j / block] * x[j];
         y[i] = static_cast<float>(acc);
     }
+}
+
+void orc_gemv_fp8(const uint8_t* W, const float* scale, const float* x, float* y, int m, int n, int block) {
+    gemv_fp8_rows(W, scale, x, y, n, block, 0, m);
 }
 
 // T tokens through the same weights = T independent GEMVs (the reference CPU
@@ -293,7 +298,14 @@ int orc_linear(int quant, const void* w, const float* scale, const float* x, flo
     case RL_Q_BF16: orc_gemv_bf16(static_cast<const uint16_t*>(w), x, y, m, n, nthreads); return 0;
     case RL_Q_FP8_E4M3_B128:
         if (!scale) return -1;
-        orc_gemv_fp8(static_cast<const uint8_t*>(w), scale, x, y, m, n, 128);
+        // rows are independent: splitting them over threads changes no result (the
+        // reference's ops::gemv_fp8 runs them on one thread)
+        if (static_cast<long long>(m) * n < 2000000LL || nthreads <= 1)
+            orc_gemv_fp8(static_cast<const uint8_t*>(w), scale, x, y, m, n, 128);
+        else
+            run_rows(m, nthreads, [&](int r0, int r1) {
+                gemv_fp8_rows(static_cast<const uint8_t*>(w), scale, x, y, n, 128, r0, r1);
+            });
         return 0;
     case RL_Q_Q4_K: orc_gemv_q4_k(static_cast<const uint8_t*>(w), x, y, m, n, nthreads); return 0;
     case RL_Q_Q6_K: orc_gemv_q6_k(static_cast<const uint8_t*>(w), x, y, m, n, nthreads); return 0;

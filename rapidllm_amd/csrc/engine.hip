@@ -43,15 +43,19 @@ namespace {
 
 inline int align16(int v) { return (v + 15) / 16 * 16; }
 
+// Device allocations of one engine, zero-filled on the engine's stream: the stream
+// is non-blocking, so a null-stream memset would not be ordered before the kernels
+// that fill the buffer (weight packing) and could land after them.
 struct DevAlloc {
     std::vector<void*> ptrs;
     size_t total = 0;
+    hipStream_t st = nullptr;
     void* get(size_t bytes) {
         void* p = nullptr;
         hipError_t e = hipMalloc(&p, bytes ? bytes : 256);
         if (e == hipErrorOutOfMemory) throw Error(RL_ERR_NOMEM, "engine: out of device memory");
         RL_HIP(e);
-        RL_HIP(hipMemset(p, 0, bytes ? bytes : 256));
+        RL_HIP(hipMemsetAsync(p, 0, bytes ? bytes : 256, st));
         ptrs.push_back(p);
         total += bytes;
         return p;
@@ -119,6 +123,7 @@ class Engine {
         ctx_ = (ctx + 255) / 256 * 256 + 256;  // room for a verify chunk past the last position
         R_ = tmax + 1;
         RL_HIP(hipStreamCreateWithFlags(&st_, hipStreamNonBlocking));
+        mem_.st = st_;
     }
 
     ~Engine() {
@@ -251,6 +256,7 @@ class Engine {
     void ensure_pf_buffers(int C) {
         if (pf_cap_ >= C) return;
         pf_mem_ = std::make_unique<DevAlloc>();
+        pf_mem_->st = st_;
         const int H = c_.hidden, I = c_.intermediate;
         int wy = 16, wo = 16, wf = H;
         for (const Layer& Ly : L_) {
@@ -875,8 +881,11 @@ class Engine {
         }
         // one committed S per layer plus R banks of per-token records with the fused
         // kernel, a ring of R states with the unfused one
-        RL_REQUIRE(mb_ == 1 || gdn_fused_norm_ || nd == 0, RL_ERR_UNSUPPORTED,
-                   "engine: batch decode needs the fused DeltaNet path (FP8/BF16 linears, v_dim 128)");
+        // step_batch runs every linear through the folded FP8/BF16 GEMM, so batch
+        // decode needs folded norms (no K-quant linears) and, with DeltaNet layers,
+        // the fused DeltaNet kernel
+        RL_REQUIRE(mb_ == 1 || (fold_norm_ && (gdn_fused_norm_ || nd == 0)), RL_ERR_UNSUPPORTED,
+                   "engine: batch decode needs FP8/BF16 linears with folded norms (and v_dim 128 for DeltaNet)");
         s_bstride_ = s_slot_ * (gdn_fused_norm_ ? 1 : R_);
         rec_bstride_ = static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats;
         recn_bstride_ = R_ * nv;
@@ -1031,6 +1040,11 @@ class Engine {
     void make_fused(Find& find, const std::vector<std::string>& names, const std::vector<int>& rows,
                     const std::vector<int>& offs, int n, std::vector<Lin>& parts, std::vector<int>& out_offs) {
         const int total = offs.back() + align16(rows.back());
+        // every part's tiles start at its output offset / 16, and a K-quant launch
+        // writes align16(rows) outputs: offsets must sit on 16-row boundaries
+        for (size_t k = 0; k < offs.size(); ++k)
+            RL_REQUIRE(offs[k] % 16 == 0 && (k == 0 || offs[k] >= offs[k - 1] + align16(rows[k - 1])),
+                       RL_ERR_INTERNAL, "engine: fused linear part offsets must be 16-row aligned");
         if (synthetic_ && synth_quant_ != RL_Q_FP8_E4M3_B128) {
             parts.clear();
             out_offs.clear();

@@ -128,12 +128,12 @@ __device__ inline int sub_of(int g, int mi) {
         return 8 * (g >> 1) + 2 * (mi >> 1) + (g & 1);
 }
 
-// Split-K tickets: one counter per row group, 64 bytes apart (atomics on one cache
-// line serialise).  Zero at load; the workgroup that takes a group's last ticket
-// resets it, so every launch finds them zero.  Launches on one device must not
-// overlap in time (they share the counters).
-constexpr int kKqMaxGroups = 4096;
-__device__ unsigned g_kq_ticket[kKqMaxGroups * 16];
+// Split-K tickets live at the start of the caller's workspace: one counter per row
+// group, 64 bytes apart (atomics on one cache line serialise), then the partials.
+// The workspace is zero-filled once when allocated; the workgroup that takes a
+// group's last ticket resets it, so every launch finds them zero.  Launches that
+// share one workspace must not overlap in time.
+inline size_t kq_ticket_bytes(int groups) { return (static_cast<size_t>(groups) * 64 + 255) / 256 * 256; }
 
 // Target of the pipeline's idle load slots (never written).
 constexpr int kKqDummyWindows = 64;
@@ -160,8 +160,9 @@ __host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
 // which are coherent across the XCDs' L2 caches without cache maintenance.
 template <int QT, int T, int D, int RW>
 __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
-                                                      float* __restrict__ Y, float* __restrict__ partial, int m,
-                                                      int n, int S, int accumulate, int ldy) {
+                                                      float* __restrict__ Y, float* __restrict__ partial,
+                                                      unsigned* __restrict__ tickets, int m, int n, int S,
+                                                      int accumulate, int ldy) {
     using F = KFmt<QT>;
     constexpr int NSET = (T + 1) / 2;  // token sets of two (hi, mid, hi, mid columns)
     constexpr int kRuns = QT == 4 ? 4 : 2;
@@ -381,7 +382,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete before the ticket
         __syncthreads();
         if (threadIdx.x == 0) {
-            unsigned* tk = g_kq_ticket + static_cast<size_t>(rgp) * 16;
+            unsigned* tk = tickets + static_cast<size_t>(rgp) * 16;
             const unsigned old = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const int last = old == static_cast<unsigned>(S - 1);
             if (last) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -530,33 +531,33 @@ void kq_split(int m, int nsb, int& S) {
 }
 
 template <int QT, int T, int RW>
-void launch_kq_rw(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int S, int accumulate,
-                  int ldy, hipStream_t s) {
+void launch_kq_rw(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int S,
+                  int accumulate, int ldy, hipStream_t s) {
     const int groups = (m + kTR * RW - 1) / (kTR * RW);
     const int P = (n / 256 + S - 1) / S;
     const size_t lds = kq_lds_bytes<QT>(P, (T + 1) / 2, T);
     hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW>), dim3(groups * S), dim3(64 * RW), lds, s, W, x, Y,
-                       partial, m, n, S, accumulate, ldy);
+                       partial, tickets, m, n, S, accumulate, ldy);
 }
 
 template <int QT, int T>
-void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int S, int accumulate,
-                 int ldy, hipStream_t s) {
+void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int S,
+                 int accumulate, int ldy, hipStream_t s) {
     switch (kq_rw()) {
-    case 1: launch_kq_rw<QT, T, 1>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
-    case 2: launch_kq_rw<QT, T, 2>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
-    default: launch_kq_rw<QT, T, 4>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 1: launch_kq_rw<QT, T, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    case 2: launch_kq_rw<QT, T, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    default: launch_kq_rw<QT, T, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
     }
 }
 
 template <int QT>
-void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, int m, int n, int T, int S, int accumulate,
-               int ldy, hipStream_t s) {
+void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int T, int S,
+               int accumulate, int ldy, hipStream_t s) {
     switch (T) {
-    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
-    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
-    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
-    default: launch_kq_t<QT, 4>(W, x, Y, partial, m, n, S, accumulate, ldy, s); break;
+    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    default: launch_kq_t<QT, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
     }
 }
 
@@ -565,10 +566,12 @@ void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, int m
 namespace rl {
 
 size_t kq_workspace_bytes(int m, int n, int T) {
-    // partials for the largest split either type uses: S*T*m floats
+    // split-K tickets, then the partials of the split: S*T*m floats
     int S;
     kq_split(m, n / 256, S);
-    return (S > 1 ? static_cast<size_t>(S) * T * m : 0) * 4 + 256;
+    if (S == 1) return 256;
+    const int groups = (m + kTR * kq_rw() - 1) / (kTR * kq_rw());
+    return kq_ticket_bytes(groups) + static_cast<size_t>(S) * T * m * 4;
 }
 
 // Y[T][m] (=, +=) W . x for Q4_K (qt=4) / Q6_K (qt=6) K-tiled weights.
@@ -581,13 +584,13 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     RL_REQUIRE(ws_bytes >= kq_workspace_bytes(m, n, T), RL_ERR_RANGE, "kquant: workspace too small");
     int S;
     kq_split(m, n / 256, S);
-    RL_REQUIRE(S == 1 || (m + kTR * kq_rw() - 1) / (kTR * kq_rw()) <= kKqMaxGroups, RL_ERR_UNSUPPORTED,
-               "kquant: too many rows");
-    float* partial = static_cast<float*>(ws);
+    const int groups = (m + kTR * kq_rw() - 1) / (kTR * kq_rw());
+    unsigned* tickets = static_cast<unsigned*>(ws);
+    float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kq_ticket_bytes(groups));
     if (qt == 4)
-        launch_kq<4>(W, x, Y, partial, m, n, T, S, accumulate, ldy, s);
+        launch_kq<4>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s);
     else
-        launch_kq<6>(W, x, Y, partial, m, n, T, S, accumulate, ldy, s);
+        launch_kq<6>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s);
     check_launch("kq_gemm_kernel");
 }
 

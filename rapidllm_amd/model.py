@@ -108,6 +108,9 @@ class WeightTable:
         return arr, len(self.t)
 
 
+BIG = 1 << 26  # matrices of at least this many entries use the one-pass generators
+
+
 def random_weights(spec: ModelSpec, seed: int = 1, linear_quant: int = Q_FP8, embed_quant: int = Q_BF16,
                    head_quant: int = Q_BF16, w_scale=(1e-3, 1e-1)) -> WeightTable:
     """Random-init weights of the architecture (benchmark distributions): FP8 linears
@@ -118,7 +121,10 @@ def random_weights(spec: ModelSpec, seed: int = 1, linear_quant: int = Q_FP8, em
 
     def lin(name, m, n, quant=linear_quant):
         if quant == Q_FP8:
-            W.add(name, Q_FP8, synth.fp8_weight(r, m, n), m, n, synth.fp8_scales(r, m, n, *w_scale))
+            w = synth.fp8_weight_wide(r, m, n) if m * n >= BIG else synth.fp8_weight(r, m, n)
+            W.add(name, Q_FP8, w, m, n, synth.fp8_scales(r, m, n, *w_scale))
+        elif quant == Q_BF16 and m * n >= BIG:
+            W.add(name, Q_BF16, synth.bf16_random_bits(r, m, n), m, n)
         elif quant == Q_BF16:
             W.add(name, Q_BF16, synth.bf16_bits(r.standard_normal((m, n)).astype(np.float32) * 0.02), m, n)
         elif quant == Q_Q4_K:
@@ -131,11 +137,14 @@ def random_weights(spec: ModelSpec, seed: int = 1, linear_quant: int = Q_FP8, em
     def vec(name, n, mean=0.0, std=0.1):
         W.add(name, Q_F32, (mean + std * r.standard_normal(n)).astype(np.float32), n, 1)
 
-    emb = (r.standard_normal((V, H)) * 0.02).astype(np.float32)
-    if embed_quant == Q_BF16:
-        W.add("embed", Q_BF16, synth.bf16_bits(emb), V, H)
+    if V * H >= BIG and embed_quant == Q_BF16:
+        W.add("embed", Q_BF16, synth.bf16_random_bits(r, V, H), V, H)
     else:
-        W.add("embed", Q_F32, emb, V, H)
+        emb = (r.standard_normal((V, H)) * 0.02).astype(np.float32)
+        if embed_quant == Q_BF16:
+            W.add("embed", Q_BF16, synth.bf16_bits(emb), V, H)
+        else:
+            W.add("embed", Q_F32, emb, V, H)
     lin("lm_head", V, H, head_quant)
     vec("final_norm", H)
     nk, nv, dk, dv = spec.n_k_heads, spec.n_v_heads, spec.k_dim, spec.v_dim

@@ -140,7 +140,12 @@ class KQuantLinear:
 
 
 def kquant_workspace(m: int, n: int, T: int) -> DeviceBuffer:
-    return DeviceBuffer(hip.lib().rl_hip_kquant_workspace_bytes(m, n, T))
+    """Workspace of one K-quant GEMV stream: split-K tickets + partials, zero-filled
+    once (each launch leaves the tickets at zero again)."""
+    ws = DeviceBuffer(hip.lib().rl_hip_kquant_workspace_bytes(m, n, T))
+    call("rl_hip_memset", ws.ptr, 0, ws.nbytes, None)
+    call("rl_hip_stream_synchronize", None)
+    return ws
 
 
 def kquant_linear_T(lin: KQuantLinear, X: np.ndarray, stream=None) -> np.ndarray:

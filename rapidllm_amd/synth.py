@@ -64,5 +64,27 @@ def bf16_bits(a: np.ndarray) -> np.ndarray:
     return u.astype(np.uint16)
 
 
+def fp8_weight_wide(r: np.random.Generator, m: int, n: int) -> np.ndarray:
+    """Uniform over the 254 finite e4m3fn codes in one pass (codes >= 0x7F shifted
+    past the NaN code 0x7F; 0xFE stays the top): for matrices of the full model
+    width, where redrawing NaN codes costs several passes."""
+    w = r.integers(0, 254, size=(m, n), dtype=np.uint8)
+    w += (w >= 0x7F).view(np.uint8)
+    return w
+
+
+def bf16_random_bits(r: np.random.Generator, m: int, n: int) -> np.ndarray:
+    """Random bf16 values of magnitude (1 + f) * 2^e, e in -8..-5 (about 0.004 to
+    0.03), random sign and mantissa, built from one uint16 draw per entry: for
+    vocabulary-sized tables (a normal draw of 1.3G entries takes minutes)."""
+    words = (m * n + 3) // 4
+    u = r.integers(0, np.iinfo(np.uint64).max, size=words, dtype=np.uint64, endpoint=True)
+    u = u.view(np.uint16)[: m * n].reshape(m, n)
+    # sign and mantissa kept, exponent field = 119 + (two random bits 7-8)
+    out = u & np.uint16(0x81FF)
+    out += np.uint16((127 - 8) << 7)
+    return out
+
+
 def bf16_to_f32(h: np.ndarray) -> np.ndarray:
     return (h.astype(np.uint32) << 16).view(np.float32)

@@ -6,6 +6,7 @@ plain decoding of that sequence bit for bit."""
 import numpy as np
 import pytest
 
+from oracle.oracle import OracleModel
 from rapidllm_amd import model as M
 from rapidllm_amd.engine import Engine
 
@@ -17,6 +18,20 @@ def mini_spec(**kw):
                 layer_kinds=[0, 0, 0, 1])
     base.update(kw)
     return M.ModelSpec(**base)
+
+
+TOL = 1e-3
+
+
+def rel_l2(a, b):
+    a = np.asarray(a, np.float64)
+    b = np.asarray(b, np.float64)
+    return float(np.linalg.norm(a - b) / max(np.linalg.norm(b), 1e-300))
+
+
+def margin_ok(logits, tol=TOL):
+    s = np.sort(logits.astype(np.float64))
+    return (s[-1] - s[-2]) > tol * np.linalg.norm(logits)
 
 
 def plain_chain(eng, prompt, n):
@@ -137,3 +152,53 @@ def test_long_prompts_prefilled_into_slots(gpu, batch_pair):
         rows = eng.copy_logits_n(2)
         assert np.array_equal(rows[0], la[step]) and np.array_equal(rows[1], lb[step]), step
         toks, poss = eng.copy_greedy_n(2), [p + 1 for p in poss]
+
+
+@pytest.mark.parametrize("B", [2, 3, 4])
+def test_batch_decode_vs_oracle(gpu, orc, B):
+    """Each slot of the batch step against its own oracle model (the reference CPU
+    Session decoding that sequence alone, session.cpp:325-411): logits within 1e-3
+    relative L2 and identical greedy tokens where the top-1 margin exceeds that,
+    with different prompts, lengths and positions per slot (27B DeltaNet head
+    counts, so the wide in_proj path runs with B rows)."""
+    spec = mini_spec(n_k_heads=16, n_v_heads=48)
+    W = M.random_weights(spec, seed=50 + B, w_scale=(1e-3, 1e-2))
+    eng = Engine(spec, W, ctx=512, max_batch=4)
+    rng = np.random.default_rng(60 + B)
+    prompts = [[int(t) for t in rng.integers(0, spec.vocab, 2 + 3 * b)] for b in range(B)]
+    oms = [OracleModel(spec, W, ctx=512) for _ in range(B)]
+    toks, poss = [], []
+    for b, p in enumerate(prompts):
+        eng.prefill_slot(p, b)
+        for t in p:
+            g, lg, _ = oms[b].decode(t)
+        assert rel_l2(eng.copy_logits(), lg) < TOL
+        toks.append(g)
+        poss.append(len(p))
+    for step in range(4):
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(B)
+        greedy = eng.copy_greedy_n(B)
+        for b in range(B):
+            g, lg, _ = oms[b].decode(toks[b])
+            assert rel_l2(rows[b], lg) < TOL, (B, step, b, rel_l2(rows[b], lg))
+            if margin_ok(lg):
+                assert greedy[b] == g, (B, step, b)
+            toks[b] = g  # follow the oracle's chain
+        poss = [p + 1 for p in poss]
+    eng.close()
+
+
+@pytest.mark.parametrize("kinds,quant", [([1, 1], M.Q_Q4_K), ([0, 1], M.Q_Q6_K)])
+def test_batch_refused_for_kquant_models(gpu, kinds, quant):
+    """The batch step runs every linear through the folded FP8 / BF16 GEMM, so a
+    K-quant model (with or without DeltaNet layers) with max_batch > 1 is refused
+    at creation with RL_ERR_UNSUPPORTED instead of running K-quant tiles as BF16."""
+    from rapidllm_amd import hip
+
+    spec = mini_spec(n_layers=2, layer_kinds=kinds)
+    W = M.random_weights(spec, seed=9, linear_quant=quant)
+    with pytest.raises(hip.HipError) as ei:
+        Engine(spec, W, ctx=256, max_batch=2)
+    assert ei.value.code == 4  # RL_ERR_UNSUPPORTED
+    Engine(spec, W, ctx=256, max_batch=1).close()

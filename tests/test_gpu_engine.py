@@ -252,3 +252,43 @@ def test_long_prefill_chunks_match_oracle_and_decode(gpu, fp8_pair):
     eng.decode_token(g)
     g2, lg2, _ = orc_m.decode(g)
     assert rel_l2(eng.copy_logits(), lg2) < TOL
+
+
+def test_mixed_kquant_types_within_projections(gpu, orc):
+    """A Q4_K_M-style table: Q4_K linears with Q6_K parts inside fused projections
+    (DeltaNet z beside Q4_K q|k|v, attention v beside Q4_K q|gate and k, MLP up
+    beside a Q4_K gate, the way llama.cpp mixes attn_v / ffn_down types), so each
+    type boundary splits a projection into groups and gate/up take the
+    separate-launch path.  Logits match the oracle at T=1 and after a T=4 verify."""
+    spec = mini_spec(n_layers=4, layer_kinds=[0, 1, 0, 0])
+    W = M.random_weights(spec, seed=13, linear_quant=M.Q_Q4_K)
+    r = np.random.default_rng(5)
+    from rapidllm_amd import synth
+
+    g = synth.rng(17)
+    for name, (q, rows, cols, data, s) in list(W.t.items()):
+        if name.endswith(("delta.gemm.in_proj_z", "attn.wv", "mlp.up")) or (
+                name.endswith("mlp.down") and "layers[2]" in name):
+            W.add(name, M.Q_Q6_K, synth.q6k_blocks(g, rows, cols), rows, cols)
+    eng = Engine(spec, W, ctx=512)
+    orc_m = OracleModel(spec, W, ctx=512)
+    prompt = [int(t) for t in r.integers(0, spec.vocab, 6)]
+    eng.prefill(prompt)
+    for t in prompt:
+        gt, lg, _ = orc_m.decode(t)
+    assert rel_l2(eng.copy_logits(), lg) < TOL
+    for _ in range(2):
+        eng.decode_token(gt)
+        gt, lg, _ = orc_m.decode(gt)
+        assert rel_l2(eng.copy_logits(), lg) < TOL
+    toks = [gt, 5, 6, 7]
+    k, preds = eng.spec_verify(toks)
+    want = []
+    for i, t in enumerate(toks):
+        gg, lg, _ = orc_m.decode(t)
+        want.append((gg, lg))
+        if i + 1 < len(toks) and gg != toks[i + 1]:
+            break
+    assert k == len(want)
+    assert rel_l2(eng.copy_logits(), want[-1][1]) < TOL
+    eng.close()

@@ -135,6 +135,39 @@ def test_gemm_kquant_repeat_and_accumulate(gpu):
     assert rel_l2(got, Y0 + outs[0]) <= 1e-6
 
 
+def test_gemm_kquant_two_streams_own_workspaces(gpu):
+    """Split-K tickets live in the caller's workspace: two streams, each with its
+    own workspace, running interleaved K-quant GEMVs (launched without waiting for
+    each other) give the serial results bit for bit."""
+    import ctypes as C
+
+    from rapidllm_amd.hip import DeviceBuffer, call
+    r = synth.rng(13)
+    m, n, T = 5120, 17408, 4
+    lin = ops.KQuantLinear(ops.Q6_K, synth.q6k_blocks(r, m, n), m, n)
+    X = [r.standard_normal((T, n)).astype(np.float32) for _ in range(2)]
+    want = [ops.kquant_linear_T(lin, x) for x in X]
+    streams = [C.c_void_p(), C.c_void_p()]
+    for s in streams:
+        call("rl_hip_stream_create", C.byref(s))
+    try:
+        ws = [ops.kquant_workspace(m, n, T) for _ in range(2)]
+        xd = [DeviceBuffer.from_numpy(x) for x in X]
+        yd = [[DeviceBuffer(4 * T * m) for _ in range(8)] for _ in range(2)]
+        for i in range(8):
+            for k in range(2):
+                lin.forward(xd[k].ptr, yd[k][i].ptr, T, ws[k], stream=streams[k].value)
+        for s in streams:
+            call("rl_hip_stream_synchronize", s.value)
+        for k in range(2):
+            for i in range(8):
+                got = yd[k][i].numpy(np.float32, (T, m))
+                assert np.array_equal(got.view(np.uint32), want[k].view(np.uint32)), (k, i)
+    finally:
+        for s in streams:
+            call("rl_hip_stream_destroy", s.value)
+
+
 def test_synthetic_q4_k_engine_spec_invariant(gpu, monkeypatch):
     """The benchmark's device-generated K-quant model (RL_SYNTH_LINEAR=q4_k: Q4_K
     layer linears, Q6_K lm_head): T=4 verify with MTP drafts gives the tokens of
