@@ -133,6 +133,22 @@ int rl_hip_gemm_kquant(int type, const uint8_t* tiled, const float* X, float* Y,
                        size_t workspace_bytes, int m, int n, int T, int accumulate, void* stream);
 int rl_hip_dequant_kquant(int type, const uint8_t* blocks, float* out, size_t n_blocks, void* stream);
 
+/* Allocation-free variant of rl_hip_gemm_kquant.  No counterpart in the reference:
+ * it is for callers that cannot allocate device memory (code under HIP graph
+ * capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments
+ * and result as rl_hip_gemm_kquant without the workspace: the split-K tickets and
+ * partial sums live in a fixed device array of the library
+ * (rl_hip_gemm_kquant_noalloc_max_scratch() bytes = 4 MiB per device, held until
+ * the process ends), set up on the first call on each device.  Shapes whose
+ * workspace (rl_hip_kquant_workspace_bytes) exceeds it return RL_ERR_RANGE.  It
+ * calls no allocating routine.  Every call on one device shares that array: calls
+ * that overlap in time on one device (two streams, two threads) race, so serialise
+ * them (one stream per device) or use rl_hip_gemm_kquant with a workspace per
+ * stream. */
+int rl_hip_gemm_kquant_noalloc(int type, const uint8_t* tiled, const float* X, float* Y, int m, int n, int T,
+                               int accumulate, void* stream);
+size_t rl_hip_gemm_kquant_noalloc_max_scratch(void);
+
 /* ---- Gated DeltaNet recurrent decode -----------------------------------------
  * Replaces: ops::conv1d_update (src/kernels/ops.cpp:458-468), the gate math of
  * ops::fused_delta_decode (src/kernels/ops_fused.cpp:111-123), ops::l2norm and

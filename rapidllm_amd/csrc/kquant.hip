@@ -36,6 +36,8 @@
 
 #include "internal.h"
 
+#include <mutex>
+
 using namespace rl;
 
 namespace {
@@ -594,9 +596,72 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     check_launch("kq_gemm_kernel");
 }
 
+// ---- the allocation-free entry point's scratch ------------------------------
+// Split-K tickets and partials of rl_hip_gemm_kquant_noalloc live in this array
+// (each device holds its own copy until the process ends).  Host code never passes
+// the array's name to a kernel: it resolves the device address once per device
+// with hipGetSymbolAddress and uses that pointer.
+constexpr size_t kKqScratchBytes = size_t(4) << 20;
+static __device__ __align__(256) uint8_t scratch[kKqScratchBytes];
+
+namespace {
+
+__global__ void kq_zero_kernel(uint32_t* p, size_t n_words) {
+    for (size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x; i < n_words;
+         i += static_cast<size_t>(gridDim.x) * blockDim.x)
+        p[i] = 0u;
+}
+
+constexpr int kKqMaxDevices = 64;
+std::mutex g_scratch_mu;
+void* g_scratch_ptr[kKqMaxDevices] = {};
+
+// Device address of `scratch` on the current device; on the first call for a
+// device it is resolved and the array cleared (a fill kernel on `s`, so the clear
+// is stream-ordered before the first GEMM).
+void* kq_scratch(hipStream_t s) {
+    int dev = 0;
+    RL_HIP(hipGetDevice(&dev));
+    RL_REQUIRE(dev >= 0 && dev < kKqMaxDevices, RL_ERR_DEVICE, "gemm_kquant_noalloc: device index out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* p = nullptr;
+        RL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
+        RL_REQUIRE(p != nullptr, RL_ERR_DEVICE, "gemm_kquant_noalloc: scratch symbol has no device address");
+        hipLaunchKernelGGL(kq_zero_kernel, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p), kKqScratchBytes / 4);
+        check_launch("kq_zero_kernel");
+        g_scratch_ptr[dev] = p;
+    }
+    return g_scratch_ptr[dev];
+}
+
+}  // namespace
+
+size_t kq_noalloc_max_bytes() { return kKqScratchBytes; }
+
 }  // namespace rl
 
 extern "C" {
+
+int rl_hip_gemm_kquant_noalloc(int type, const uint8_t* tiled, const float* X, float* Y, int m, int n, int T,
+                               int accumulate, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "gemm_kquant_noalloc: Q4_K or Q6_K only");
+        RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0 && T >= 1 && T <= 4, RL_ERR_RANGE,
+                   "gemm_kquant_noalloc: m > 0, n a positive multiple of 256, T in 1..4");
+        const size_t need = rl::kq_workspace_bytes(m, n, T);
+        if (need > rl::kKqScratchBytes)
+            throw Error(RL_ERR_RANGE, "gemm_kquant_noalloc: shape needs " + std::to_string(need) +
+                                          " scratch bytes, more than the fixed " +
+                                          std::to_string(rl::kKqScratchBytes) + " (use rl_hip_gemm_kquant)");
+        void* ws = rl::kq_scratch(S(stream));
+        rl::kq_gemm(type == RL_Q_Q4_K ? 4 : 6, tiled, X, Y, ws, rl::kKqScratchBytes, m, n, T, accumulate, m,
+                    S(stream));
+    });
+}
+
+size_t rl_hip_gemm_kquant_noalloc_max_scratch(void) { return rl::kq_noalloc_max_bytes(); }
+
 
 size_t rl_hip_kquant_tiled_bytes(int type, int m, int n) {
     if ((type != RL_Q_Q4_K && type != RL_Q_Q6_K) || n % 256 != 0 || m <= 0) return 0;
