@@ -12,6 +12,8 @@
  * Kernel entry points are asynchronous on `stream`.
  *
  * The reference interfaces each group replaces are cited per declaration.
+ * Benchmark, tuning and calibration entry points (no reference counterpart) are
+ * declared separately, in rapidllm_hip_bench.h.
  */
 #ifndef RAPIDLLM_HIP_H
 #define RAPIDLLM_HIP_H
@@ -52,6 +54,10 @@ int rl_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream);
 int rl_hip_memcpy_d2h(void* dst, const void* src, size_t bytes, void* stream);
 int rl_hip_memcpy_d2d(void* dst, const void* src, size_t bytes, void* stream);
 int rl_hip_memset(void* ptr, int value, size_t bytes, void* stream);
+/* Pinned host memory the device can read and write (Device::allocate for
+ * host-visible buffers, BufferDesc::host_visible, device.h:15-19). */
+int rl_hip_host_alloc(void** ptr, size_t bytes);
+int rl_hip_host_free(void* ptr);
 int rl_hip_stream_create(void** stream);
 int rl_hip_stream_destroy(void* stream);
 int rl_hip_stream_synchronize(void* stream);
@@ -105,9 +111,6 @@ int rl_hip_gemm_fp8_frag(const uint8_t* w_tiled, const float* tile_scale, const 
                          int T, int accumulate, void* stream);
 int rl_hip_gemm_bf16_frag(const uint16_t* w_tiled, const void* frag, float* Y, int m, int n, int T, int accumulate,
                           void* stream);
-/* Tuning hook: force the work split (row-tiles per workgroup, waves per workgroup
- * along K, load pipeline depth); row_tiles = 0 restores the shape-based choice. */
-int rl_hip_set_gemm_config(int row_tiles, int k_waves, int depth);
 /* Convenience: pack X into `frag_scratch` then GEMM (two launches). */
 int rl_hip_gemm_fp8(const uint8_t* w_tiled, const float* tile_scale, const float* X, float* Y, void* frag_scratch,
                     int m, int n, int T, void* stream);
@@ -229,6 +232,26 @@ int rl_hip_attn_decode_layer(const float* Y, int ld_y, const float* q_norm, cons
                              int rotary_dim, float theta, float eps, void* workspace, size_t workspace_bytes,
                              float* out, void* frag, void* stream);
 
+/* ---- single ops of the kernel-name device seam -----------------------------
+ * Replaces: Device::launch("conv1d_update" / "delta_recurrent" / "attn_decode")
+ * (include/rapidllm/backend/device.h:49-60, params Conv1dParams /
+ * DeltaRecurrentParams / AttnDecodeParams, params.h:16-18) over the reference CPU
+ * path's own layouts, with the arguments of ops::conv1d_update (ops.cpp:458-468),
+ * ops::delta_recurrent_step (ops.cpp:495-540) and ops::attn_decode (ops.cpp:575-605):
+ *   conv1d_update:   state [dim][k] (tap 0 oldest) updated in place, y [dim];
+ *   delta_recurrent: S [n_v][dk][dv] row-major (the CPU Session's layout) updated
+ *                    in place; q, k [n_v][dk] raw (l2-normalised here, q scaled by
+ *                    1/sqrt(dk)); v, o [n_v][dv]; beta, g_log [n_v]; dk <= 256;
+ *   attn_decode_f32: fp32 caches [seq][n_kv][head_dim], q, o [n_q][head_dim],
+ *                    softmax(q.k / sqrt(head_dim)) over positions 0..pos; head_dim
+ *                    <= 256.
+ * The decode engine does not use them (its step runs the fused kernels). */
+int rl_hip_conv1d_update(const float* x_t, const float* w, float* state, float* y, int dim, int k, void* stream);
+int rl_hip_delta_recurrent(float* S, const float* q, const float* k, const float* v, const float* beta,
+                           const float* g_log, float* o, int n_v, int dk, int dv, float eps_l2, void* stream);
+int rl_hip_attn_decode_f32(const float* q, const float* k_cache, const float* v_cache, float* o, int pos, int n_q,
+                           int n_kv, int head_dim, void* stream);
+
 /* ---- greedy argmax and speculative acceptance --------------------------------
  * Replaces: greedy_sample (src/runtime/sampler.cpp:8-18), the CUDA
  * argmax_partial_rows_k / argmax_final_rows_k (cuda_engine.cu:9375-9433) and the
@@ -257,8 +280,6 @@ int rl_hip_accept_prefix(const int* toks, const int* preds, int T, int* pos, int
 typedef struct RlEngine RlEngine;
 RlEngine* rl_hip_engine_create(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx, int max_T,
                                int* status);
-/* Random-init weights of cfg's architecture generated on the device (benchmark). */
-RlEngine* rl_hip_engine_create_synthetic(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T, int* status);
 void rl_hip_engine_destroy(RlEngine* e);
 int rl_hip_engine_reset(RlEngine* e);
 int rl_hip_engine_prefill(RlEngine* e, const int32_t* ids, int n);                    /* cuda_engine.h:18 */
@@ -274,12 +295,6 @@ int rl_hip_engine_mtp_spec(RlEngine* e, int32_t t0, int T, int32_t* toks_out, in
 int rl_hip_engine_greedy(RlEngine* e, int32_t* tok);                                  /* :41 */
 int rl_hip_engine_pos(RlEngine* e, int* pos);                                         /* :42 */
 int rl_hip_engine_info(RlEngine* e, int* vocab, int* hidden, int* ctx_capacity, size_t* device_bytes);
-/* Benchmark support: set the position, or fill the KV cache rows [0, n) with fp16
- * N(0,1) and the recurrent states with random values, then set pos = n; time
- * `iters` graph replays of the T-token step (mtp_drafts > 0: of the MTP draft). */
-int rl_hip_engine_set_pos(RlEngine* e, int pos);
-int rl_hip_engine_synthetic_context(RlEngine* e, int n, uint64_t seed);
-int rl_hip_engine_time_steps(RlEngine* e, int T, int iters, int mtp_drafts, float* ms);
 void* rl_hip_engine_stream(RlEngine* e);
 
 /* ---- continuous batch (cuda_engine.h:46-66) ------------------------------------
@@ -296,8 +311,6 @@ void* rl_hip_engine_stream(RlEngine* e);
  * Needs the folded path (FP8 / BF16 linears, v_dim 128), max_batch <= 8. */
 RlEngine* rl_hip_engine_create_batch(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx,
                                      int max_T, int max_batch, int* status);
-RlEngine* rl_hip_engine_create_synthetic_batch(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T,
-                                               int max_batch, int* status);
 int rl_hip_engine_max_batch(RlEngine* e, int* max_batch);                              /* :46 */
 int rl_hip_engine_decode_tokens(RlEngine* e, const int32_t* tokens, const int* poss, int B); /* :48 */
 int rl_hip_engine_copy_logits_n(RlEngine* e, float* host, int B);                      /* :53 */
@@ -305,9 +318,6 @@ int rl_hip_engine_copy_greedy_n(RlEngine* e, int32_t* host, int B);             
 int rl_hip_engine_replicate_slot0(RlEngine* e, int n_slots);                           /* :59 */
 int rl_hip_engine_zero_slots(RlEngine* e, int n_slots);                                /* :60 */
 int rl_hip_engine_prefill_slot(RlEngine* e, const int32_t* ids, int n, int slot);      /* :62 */
-/* Benchmark support: time `iters` graph replays of the B-sequence batch step (the
- * slots' positions advance; the tokens in place are re-fed). */
-int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms);
 
 /* ---- checkpoint loading ---------------------------------------------------
  * Replaces: rapidllm::make_loader + IWeightLoader::load + WeightStore::open
@@ -339,43 +349,6 @@ int rl_hip_weights_info(const RlWeights* w, int i, const char** src_name, int* n
 /* IR name of a source tensor name (gguf = 0: HF, 1: GGUF); "" when the path does not
  * use the tensor (vision tower, unknown names). */
 int rl_hip_map_name(int gguf, const char* src, char* out, int cap);
-
-/* ---- bandwidth calibration ------------------------------------------------
- * No counterpart in the reference.  A streaming copy / read of `bytes` (multiple of
- * 16) that measures the achievable HBM rate and calibrates rocprof's FETCH_SIZE /
- * WRITE_SIZE counters against bytes known to be moved. */
-int rl_hip_copy_probe(const void* src, void* dst, size_t bytes, void* stream);
-int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
-
-/* GEMM timing (no counterpart in the reference): `iters` back-to-back launches of the
- * block-FP8 GEMM on `stream`, launch i reading weight copy i % n_copies (so weights
- * come from HBM, not from the Infinity Cache), with one event pair around the loop;
- * *avg_ms = average launch duration.  epilogue: 0 store (Y [T][m]), 3 split-K
- * partials (Y [split][T][m]), 2 SwiGLU over interleaved gate/up tiles writing the
- * next linear's fragments to frag_out (act_frag_bytes(m/2, T)), 4 residual add with
- * the next RMSNorm's data (Y [T][m] += result; frag_out = fragments of Y * (1 + gamma),
- * act_frag_bytes(m, T); sumsq [ceil(m/32)][T] = per-32-row sums of squares).
- * block_sumsq (add-norm only, may be null): [n/128][T][4] partial sums of squares of
- * the input per 128-column block, each block's products then scaled per token by
- * 1/sqrt(sum/128 + 1e-6) (the DeltaNet out_proj's folded gated RMSNorm). */
-int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
-                         float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
-                         int m, int n, int T, int epilogue, int split, int iters, void* stream, float* avg_ms);
-
-/* Average duration of `iters` back-to-back rl_hip_gemm_kquant launches (store),
- * cycling over n_copies packed weight copies.  No counterpart in the reference
- * (bench / roofline measurement). */
-int rl_hip_time_gemm_kquant(int type, const void* const* w_copies, int n_copies, const float* X, float* Y,
-                            void* workspace, size_t workspace_bytes, int m, int n, int T, int iters, void* stream,
-                            float* avg_ms);
-
-/* Average duration of one DeltaNet decode launch (rl_hip_gdn_decode semantics with
- * S updated in place) over `iters` passes across n_layers layer states.  No
- * counterpart in the reference (bench / roofline measurement). */
-int rl_hip_time_gdn(float* const* S_layers, int n_layers, const float* qkv, const float* a, const float* b, int ld_in,
-                    const float* A_log, const float* dt_bias, const float* conv_w, const float* conv_in,
-                    float* conv_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k, int v_tiled,
-                    int iters, void* stream, float* avg_ms);
 
 #ifdef __cplusplus
 }

@@ -9,6 +9,7 @@
 #include <string>
 
 #include "../../include/rapidllm_hip.h"
+#include "../../include/rapidllm_hip_bench.h"
 
 namespace rl {
 

@@ -60,6 +60,22 @@ int rl_hip_free(void* ptr) {
     });
 }
 
+int rl_hip_host_alloc(void** ptr, size_t bytes) {
+    return guard([&] {
+        RL_REQUIRE(ptr != nullptr, RL_ERR_RANGE, "rl_hip_host_alloc: null out pointer");
+        *ptr = nullptr;
+        hipError_t e = hipHostMalloc(ptr, bytes ? bytes : 256, hipHostMallocDefault);
+        if (e == hipErrorOutOfMemory) throw Error(RL_ERR_NOMEM, "hipHostMalloc: out of pinned host memory");
+        RL_HIP(e);
+    });
+}
+
+int rl_hip_host_free(void* ptr) {
+    return guard([&] {
+        if (ptr) RL_HIP(hipHostFree(ptr));
+    });
+}
+
 int rl_hip_memcpy_h2d(void* dst, const void* src, size_t bytes, void* stream) {
     return guard([&] { RL_HIP(hipMemcpyAsync(dst, src, bytes, hipMemcpyHostToDevice, S(stream))); });
 }

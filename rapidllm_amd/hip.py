@@ -30,6 +30,11 @@ _SIGS = {
     "rl_hip_memcpy_d2h": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_memcpy_d2d": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_memset": (_i, [_vp, _i, _sz, _vp]),
+    "rl_hip_host_alloc": (_i, [C.POINTER(_vp), _sz]),
+    "rl_hip_host_free": (_i, [_vp]),
+    "rl_hip_conv1d_update": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_delta_recurrent": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, C.c_float, _vp]),
+    "rl_hip_attn_decode_f32": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rl_hip_stream_create": (_i, [C.POINTER(_vp)]),
     "rl_hip_stream_destroy": (_i, [_vp]),
     "rl_hip_stream_synchronize": (_i, [_vp]),

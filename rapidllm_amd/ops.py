@@ -385,3 +385,37 @@ def accept_prefix(toks, preds, pos: int):
     call("rl_hip_accept_prefix", d_t.ptr, d_p.ptr, toks.size, d_pos.ptr, d_n.ptr, d_nx.ptr, None)
     return (int(d_n.numpy(np.int32, (1,))[0]), int(d_pos.numpy(np.int32, (1,))[0]),
             int(d_nx.numpy(np.int32, (1,))[0]))
+
+
+# ------------------------------------------------------------ device-seam single ops
+
+
+def conv1d_update(x_t, w, state):
+    """ops::conv1d_update(x_t, w, state, y, dim, k) (reference ops.cpp:458-468) on the
+    device: returns (y, new state)."""
+    state = _f32(state)
+    dim, k = state.shape
+    d_x, d_w, d_s = DeviceBuffer.from_numpy(_f32(x_t)), DeviceBuffer.from_numpy(_f32(w)), DeviceBuffer.from_numpy(state)
+    d_y = DeviceBuffer(4 * dim)
+    call("rl_hip_conv1d_update", d_x.ptr, d_w.ptr, d_s.ptr, d_y.ptr, dim, k, None)
+    return d_y.numpy(np.float32, (dim,)), d_s.numpy(np.float32, (dim, k))
+
+
+def delta_recurrent_step(S, q, k, v, beta, g_log, eps_l2=1e-6):
+    """ops::delta_recurrent_step (reference ops.cpp:495-540) on the device, S
+    row-major [n_v][dk][dv]: returns (o [n_v][dv], new S)."""
+    S = _f32(S)
+    n_v, dk, dv = S.shape
+    bufs = [DeviceBuffer.from_numpy(_f32(a)) for a in (S, q, k, v, beta, g_log)]
+    d_o = DeviceBuffer(4 * n_v * dv)
+    call("rl_hip_delta_recurrent", *[b.ptr for b in bufs], d_o.ptr, n_v, dk, dv, eps_l2, None)
+    return d_o.numpy(np.float32, (n_v, dv)), bufs[0].numpy(np.float32, S.shape)
+
+
+def attn_decode(q, k_cache, v_cache, pos, n_q, n_kv, head_dim):
+    """ops::attn_decode (reference ops.cpp:575-605) over fp32 caches [seq][n_kv][hd]."""
+    d_q = DeviceBuffer.from_numpy(_f32(q))
+    d_k, d_v = DeviceBuffer.from_numpy(_f32(k_cache)), DeviceBuffer.from_numpy(_f32(v_cache))
+    d_o = DeviceBuffer(4 * n_q * head_dim)
+    call("rl_hip_attn_decode_f32", d_q.ptr, d_k.ptr, d_v.ptr, d_o.ptr, pos, n_q, n_kv, head_dim, None)
+    return d_o.numpy(np.float32, (n_q * head_dim,))
