@@ -905,7 +905,8 @@ class Engine {
                 if (Ly.kind == RL_LAYER_DELTA) d0 = &Ly;
             const int m_tiles = d0->in_parts[0].m / 16, n_kb = (H + 127) / 128;
             const int tile0 = d0->off_a / 16;
-            if (d0->in_parts[0].kind == RL_Q_FP8_E4M3_B128 && m_tiles / 2 > 2 * device_cus() && d0->off_a % 32 == 0 &&
+            if (gemm_store_pairs_rows() && d0->in_parts[0].kind == RL_Q_FP8_E4M3_B128 && m_tiles / 2 > 2 * device_cus() &&
+                d0->off_a % 32 == 0 &&
                 tile0 / 2 <= 2 * device_cus() && (m_tiles - tile0) * kAbSlices <= tile0 / 2 &&
                 (n_kb + kAbSlices - 1) / kAbSlices <= 8 && d0->in_width == m_tiles * 16) {
                 ab_tile0_ = tile0;

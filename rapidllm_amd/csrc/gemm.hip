@@ -62,13 +62,26 @@ enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4 };
 // kKs: per-column-block input scale (NormIO::kss, the folded gated RMSNorm); depth 1
 // and at most kKsMaxIt column blocks per wave.
 constexpr int kKsMaxIt = 8;
-template <int RT, int KSPLIT, int D, bool kFp8, bool kKs = false>
+// TT > 0: T is the compile-time token count TT, and each column block's activation
+// fragments (16 * 2T units of 16 B) are fetched by 1, 2 or 4 coalesced loads (every
+// lane one distinct unit) and handed to the lanes that need them by ds_bpermute.
+// Loading each lane's B operand directly takes four 64-lane loads per block for
+// 128 * T distinct bytes; those load instructions, not the bytes, measured 2-4 us
+// per launch (34816 x 5120 at T=1: 31.5 -> 27.5 us cold).
+// EPI >= 0 / SSIN >= 0: the epilogue and whether the input RMSNorm is folded in
+// (io.ss_in) are compile-time, so an instantiation keeps no registers for the
+// others' state across the main loop (eight waves per SIMD need <= 64 VGPRs).
+template <int RT, int KSPLIT, int D, bool kFp8, bool kKs = false, int TT = 0, int EPI = -1, int SSIN = -1>
 __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
-                                                                float* __restrict__ Y, int m, int n_kb, int T,
-                                                                int epilogue, int ldy, int m_valid, int S,
+                                                                float* __restrict__ Y, int m, int n_kb, int T_,
+                                                                int epilogue_, int ldy, int m_valid, int S,
                                                                 i32x4* __restrict__ frag_out, NormIO io) {
+    const int T = TT > 0 ? TT : T_;
+    const int epilogue = EPI >= 0 ? EPI : epilogue_;
+    if constexpr (SSIN == 0) io.ss_in = nullptr;
+    const bool has_ss = SSIN == 1 || (SSIN < 0 && io.ss_in != nullptr);
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
     constexpr int NW = kFp8 ? 2 : 4;  // 16-byte loads per lane per tile
     const int lane = threadIdx.x & 63;
@@ -114,16 +127,37 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         gpre = 1.f + io.gamma_out[an_orow_of()];
     }
 
+    // The sums are copied straight into LDS (global_load_lds: no registers held
+    // through the main loop) and reduced in the epilogue.
     constexpr int kMaxSsPerLane = 4;  // groups <= 256
-    float ssv[kMaxSsPerLane];
-    const bool ss_wave = io.ss_in && wave < T;
+    __shared__ float ss_lds[8][64 * kMaxSsPerLane];
+    const bool ss_wave = has_ss && wave < T;
     if (ss_wave) {
 #pragma unroll
         for (int k = 0; k < kMaxSsPerLane; ++k) {
             const int gi = lane + 64 * k;
-            ssv[k] = gi < io.groups_in ? io.ss_in[static_cast<size_t>(gi) * T + wave] : 0.f;
+            const float* src = io.ss_in + static_cast<size_t>(gi < io.groups_in ? gi : 0) * T + wave;
+            __builtin_amdgcn_global_load_lds(src, &ss_lds[wave][64 * k], 4, 0, 0);
         }
     }
+    __shared__ f32x4 red[KSPLIT][RT][64];
+    __shared__ float s_inv[8];
+    // Token `wave`'s 1/rms from the sums of squares in LDS (every load of this wave,
+    // the copies included, has completed: the wait is explicit for waves that had no
+    // column block to wait on).
+    auto reduce_ss = [&]() {
+        if (ss_wave) {
+            asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < kMaxSsPerLane; ++k) {
+                const int gi = lane + 64 * k;
+                ss += gi < io.groups_in ? static_cast<double>(ss_lds[wave][gi]) : 0.0;  // group order
+            }
+            ss = wave_sum_d(ss);                                  // fixed butterfly order
+            if (lane == 0) s_inv[wave] = 1.f / sqrtf(static_cast<float>(ss / io.n_norm) + io.eps);
+        }
+    };
 
     // Lanes of B columns >= 2T read a valid column: those MFMA output columns are
     // never used, and unconditional loads keep the load count identical on every
@@ -166,17 +200,45 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 #pragma unroll
             for (int r = 0; r < RT; ++r) sbuf[d][r] = sbase[r][live ? kb : 0];
         }
-#pragma unroll
-        for (int r = 0; r < RT; ++r)
-#pragma unroll
-            for (int c = 0; c < NW; ++c) {
-                const uint8_t* base = live ? wbase[r] + static_cast<size_t>(kb) * kTileBytes : dummy;
-                const i32x4* p = reinterpret_cast<const i32x4*>(base + c * 1024) + lane;
-                wbuf[d][r][c] = __builtin_nontemporal_load(p);
-            }
+        // TT > 0: the block's fragment loads go first, so the permutes that consume
+        // them wait only for them (the load counter retires in issue order), with
+        // the block's weight loads still in flight
+        const int kbw = kb;
         kb = live ? kb : 0;
+        auto load_weights = [&]() {
 #pragma unroll
-        for (int i = 0; i < 4; ++i) bbuf[d][i] = fbase[kb * fstride + i * 4 * NC];
+            for (int r = 0; r < RT; ++r)
+#pragma unroll
+                for (int c = 0; c < NW; ++c) {
+                    const uint8_t* base = live ? wbase[r] + static_cast<size_t>(kbw) * kTileBytes : dummy;
+                    const i32x4* p = reinterpret_cast<const i32x4*>(base + c * 1024) + lane;
+                    wbuf[d][r][c] = __builtin_nontemporal_load(p);
+                }
+        };
+        if constexpr (TT == 0) load_weights();
+        if constexpr (TT > 0) {
+            // L loads of P units: load j, lane l holds unit j*P + l; MFMA i of lane
+            // (g, col) needs unit (i*4 + g)*NC + bcol, which is in load j = i*L/4
+            constexpr int NCc = 2 * TT;
+            constexpr int L = NCc <= 4 ? 1 : (NCc <= 8 ? 2 : 4);
+            constexpr int P = 16 * NCc / L;
+            const i32x4* fb = frag + kb * fstride;
+            const int li = lane < P ? lane : 0;
+            i32x4 src[L];
+#pragma unroll
+            for (int j = 0; j < L; ++j) src[j] = fb[j * P + li];
+            load_weights();
+#pragma unroll
+            for (int i = 0; i < 4; ++i) {
+                const int j = i * L / 4;
+                const int addr = ((i * 4 + g) * NCc + bcol - j * P) * 4;  // source lane, in bytes
+#pragma unroll
+                for (int c = 0; c < 4; ++c) bbuf[d][i][c] = __builtin_amdgcn_ds_bpermute(addr, src[j][c]);
+            }
+        } else {
+#pragma unroll
+            for (int i = 0; i < 4; ++i) bbuf[d][i] = fbase[kb * fstride + i * 4 * NC];
+        }
     };
     auto compute = [&](int d, int kb, float ks = 1.f) {
 #pragma unroll
@@ -253,17 +315,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 
     // Cross-wave reduction in a fixed order.  red[w][r][lane] holds C rows
     // 4*(lane/16)+v, column lane%16.
-    __shared__ f32x4 red[KSPLIT][RT][64];
-    __shared__ float s_inv[8];
 #pragma unroll
     for (int r = 0; r < RT; ++r) red[wave][r][lane] = tot[r];
-    if (ss_wave) {
-        double ss = 0.0;
-#pragma unroll
-        for (int k = 0; k < kMaxSsPerLane; ++k) ss += static_cast<double>(ssv[k]);  // group order
-        ss = wave_sum_d(ss);                                  // fixed butterfly order
-        if (lane == 0) s_inv[wave] = 1.f / sqrtf(static_cast<float>(ss / io.n_norm) + io.eps);
-    }
+    reduce_ss();
     __syncthreads();
 
     // items: (r, t, row); value = hi column + mid column, summed over waves
@@ -279,7 +333,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 
     auto final_value = [&](int r, int t, int row) -> float {
         const float v = wg_value(r, t, row);
-        return io.ss_in ? v * s_inv[t] : v;
+        return has_ss ? v * s_inv[t] : v;
     };
 
     if (epilogue == kSwiGLU) {
@@ -479,14 +533,65 @@ struct GemmCfg {
     int rt, ks, d;
 };
 static GemmCfg g_force{0, 0, 0};
+// RL_GEMM_BPERM=0 keeps the per-lane B operand loads (A/B measurement)
+inline bool bperm_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("RL_GEMM_BPERM");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
 
+template <bool kFp8, int RT, int KS, int D, bool kKs, int TT, int EPI = -1, int SSIN = -1>
+void launch_gemm_tt(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
+                    int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
+    const int groups = (m_tiles_of(m) + RT - 1) / RT;
+    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8, kKs, TT, EPI, SSIN>), dim3(groups * S), dim3(64 * KS), 0,
+                       s, static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
+                       epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out), io);
+}
+
+// The permuted-B kernel for (RT, KS) with the epilogue and folded-norm input as
+// compile-time parameters (the combinations the decode step uses; others run the
+// kernel with runtime ones).
+template <bool kFp8, int RT, int KS, bool kKs, int TT>
+void launch_gemm_spec(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
+                      int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
+    const bool ss = io.ss_in != nullptr;
+#define RL_SPEC(E, SS)                                                                                            \
+    if (epilogue == E && ss == static_cast<bool>(SS)) {                                                           \
+        launch_gemm_tt<kFp8, RT, KS, 1, kKs, TT, E, SS>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, \
+                                                       frag_out, io, s);                                          \
+        return;                                                                                                   \
+    }
+    if constexpr (RT == 1) {
+        RL_SPEC(kStore, 0) RL_SPEC(kStore, 1) RL_SPEC(kAdd, 0) RL_SPEC(kAdd, 1)
+    } else if constexpr (kKs) {
+        RL_SPEC(kAddNorm, 0)
+    } else {
+        RL_SPEC(kSwiGLU, 0) RL_SPEC(kSwiGLU, 1) RL_SPEC(kAddNorm, 0)
+    }
+#undef RL_SPEC
+    launch_gemm_tt<kFp8, RT, KS, 1, kKs, TT>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io,
+                                            s);
+}
+
+// Depth-1 launches with T <= 4 take the compile-time-T kernels (permuted B operand).
 template <bool kFp8, int RT, int KS, int D, bool kKs = false>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                      int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
-    const int groups = (m_tiles_of(m) + RT - 1) / RT;
-    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8, kKs>), dim3(groups * S), dim3(64 * KS), 0, s,
-                       static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out), io);
+    if constexpr (D == 1) {
+        if (bperm_enabled()) {
+            switch (T) {
+            case 1: launch_gemm_spec<kFp8, RT, KS, kKs, 1>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 2: launch_gemm_spec<kFp8, RT, KS, kKs, 2>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 3: launch_gemm_spec<kFp8, RT, KS, kKs, 3>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 4: launch_gemm_spec<kFp8, RT, KS, kKs, 4>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            default: break;
+            }
+        }
+    }
+    launch_gemm_tt<kFp8, RT, KS, D, kKs, 0>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s);
 }
 
 // m = rows of the (tiled) weight; outputs go to Y[t * ldy + row] for row < m_valid
@@ -517,6 +622,14 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     // for 16480x5120 with weights cold in HBM.  BF16 (lm_head: many rounds) keeps
     // depth 2 (6.4 TB/s).
     GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, kFp8 ? 1 : 2};
+    if (kFp8 && bperm_enabled() && T <= 4 && S == 1) {
+        // permuted-B kernels, measured cold (T = 1 / 4): stores one row tile per
+        // 16-wave workgroup (16480 x 5120: 15.6 / 17.7 us vs 17.7 / 18.7 with two row
+        // tiles per 8 waves), SwiGLU two (gate and up) per 16 waves (34816 x 5120:
+        // 29.6 / 30.2 us vs 30.8 / 31.1)
+        if (epilogue == kStore || epilogue == kAdd) c = GemmCfg{1, 16, 1};
+        if (epilogue == kSwiGLU) c = GemmCfg{2, 16, 1};
+    }
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
     // residual GEMMs (m = hidden: 160 groups): 8 waves measured faster than 16 there
@@ -582,6 +695,7 @@ void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n,
     launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out, norm);
 }
 int add_norm_groups(int m) { return (m_tiles_of(m) + 1) / 2; }
+bool gemm_store_pairs_rows() { return !(bperm_enabled() && !g_force.rt); }
 int device_cus() {
     static int cus[64] = {0};
     int dev = 0;
