@@ -96,7 +96,7 @@ def step_bytes(spec, T, ctx):
     return {"linears": lin, "lm_head": head, "kv": kv, "state": state, "total": lin + head + kv + state}
 
 
-EPI_STORE, EPI_SWIGLU, EPI_PARTIAL, EPI_ADDNORM = 0, 2, 3, 4
+EPI_STORE, EPI_SWIGLU, EPI_PARTIAL, EPI_ADDNORM, EPI_SWIGLU_H = 0, 2, 3, 4, 5
 EPI_ADDNORM_BS = 104  # add-norm with the per-block input scale (DeltaNet out_proj)
 SPLIT = 4
 
@@ -105,8 +105,10 @@ def gemm_shapes(spec):
     """(m, n, count per step, epilogue) of the block-FP8 GEMM launches in one step,
     as the engine issues them: fused [qkv|z|a|b] and [q|gate;k;v] stores, residual
     GEMMs adding into x with the next RMSNorm's fragments and sums of squares,
-    interleaved gate/up with the SwiGLU epilogue.  The DeltaNet out_proj also
-    scales each 128-column input block by the head's gated-RMSNorm factor."""
+    gate/up in half tiles with the SwiGLU epilogue.  The GEMMs reading the residual
+    stream (n = hidden) fold its RMSNorm (input sums of squares); the DeltaNet
+    out_proj scales each 128-column input block by the head's gated-RMSNorm
+    factor."""
     H, I = spec.hidden, spec.intermediate
     nv, dv = spec.n_v_heads, spec.v_dim
     nq, nkv, hd = spec.n_q, spec.n_kv, spec.head_dim
@@ -117,7 +119,7 @@ def gemm_shapes(spec):
     return [
         (m_in, H, n_d, EPI_STORE), (H, nv * dv, n_d, EPI_ADDNORM_BS if dv == 128 else EPI_ADDNORM),
         (2 * nq * hd + 2 * nkv * hd, H, n_a, EPI_STORE), (H, nq * hd, n_a, EPI_ADDNORM),
-        (2 * a16(I), H, spec.n_layers, EPI_SWIGLU), (H, I, spec.n_layers, EPI_ADDNORM),
+        (2 * I, H, spec.n_layers, EPI_SWIGLU_H), (H, I, spec.n_layers, EPI_ADDNORM),
     ]
 
 
@@ -143,9 +145,11 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
     for m, n, count, epi_kind in gemm_shapes(spec):
         block_scale = epi_kind == EPI_ADDNORM_BS
         epi = EPI_ADDNORM if block_scale else epi_kind
-        W = synth.fp8_weight(r, m, n)
-        sc = synth.fp8_scales(r, m, n)
-        lin = ops.Fp8Linear(W, sc)
+        if epi == EPI_SWIGLU_H:
+            lin = ops.Fp8GateUp(synth.fp8_weight(r, m // 2, n), synth.fp8_scales(r, m // 2, n),
+                                synth.fp8_weight(r, m // 2, n), synth.fp8_scales(r, m // 2, n))
+        else:
+            lin = ops.Fp8Linear(synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n))
         nb = lin.w.nbytes
         copies = [lin.w] + [DeviceBuffer(nb) for _ in range(max(1, -(-rotate_bytes // nb)) - 1)]
         for c in copies[1:]:
@@ -154,30 +158,32 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
         xd = DeviceBuffer.from_numpy(X)
         frag = ops.act_frag_buffer(n, T)
         yd = DeviceBuffer(4 * T * m * SPLIT)
-        fo = ops.act_frag_buffer(m // 2 if epi == EPI_SWIGLU else m, T) if epi in (EPI_SWIGLU, EPI_ADDNORM) else None
+        fo = ops.act_frag_buffer(m // 2 if epi == EPI_SWIGLU_H else m, T) if epi in (EPI_SWIGLU_H, EPI_ADDNORM) else None
         gam = DeviceBuffer.from_numpy(np.zeros(m, np.float32))
         ssq = DeviceBuffer(4 * T * ((m + 31) // 32))
         bss = DeviceBuffer.from_numpy(np.full((n // 128) * T * 4, 32.0, np.float32)) if block_scale else None
+        folded = epi in (EPI_STORE, EPI_SWIGLU_H) and n == spec.hidden
+        ssi = DeviceBuffer.from_numpy(np.full((n + 31) // 32 * T, 32.0, np.float32)) if folded else None
         yd.zero(s)
         call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, s)
         ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
         one = (C.c_void_p * 1)(lin.w.ptr)
         ms, warm = C.c_float(), C.c_float()
-        args = (lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr if fo else None, gam.ptr, ssq.ptr, bss.ptr if bss else None, m,
-                n, T, epi, SPLIT)
+        args = (lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr if fo else None, gam.ptr, ssq.ptr, bss.ptr if bss else None,
+                ssi.ptr if ssi else None, m, n, T, epi, SPLIT)
         call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, len(copies), s, C.byref(ms))  # warm-up
         call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, iters, s, C.byref(ms))
         call("rl_hip_time_gemm_fp8", one, 1, *args, iters, s, C.byref(warm))
         ms, warm = ms.value, warm.value
         b = m * n + 4 * ((m + 127) // 128) * ((n + 127) // 128) + 4 * T * (m + n)
-        label = {0: "store", 2: "swiglu", 3: f"split{SPLIT}", 4: "add+norm", 104: "add+norm+block-scale"}[epi_kind]
+        label = {0: "store", 5: "swiglu", 3: f"split{SPLIT}", 4: "add+norm", 104: "add+norm+block-scale"}[epi_kind]
         per.append({"m": m, "n": n, "epilogue": label,
                     "per_step": count, "us": round(ms * 1e3, 2), "GBps": round(b / ms / 1e6, 1),
                     "warm_us": round(warm * 1e3, 2), "copies": len(copies)})
         tot_ms += ms * count
         tot_bytes += b * count
         n_launch += count
-        del lin, xd, frag, yd, fo, gam, ssq, bss, copies
+        del lin, xd, frag, yd, fo, gam, ssq, bss, ssi, copies
     avg_ms = tot_ms / n_launch
     avg_bytes = tot_bytes / n_launch
     return avg_ms, avg_bytes, per
@@ -214,7 +220,7 @@ def measure_configs(spec, gemm_t1, gemm_t4, iters=30, rotate_bytes=768 << 20):
     call("rl_hip_pack_act", xd.ptr, frag.ptr, n, 1, s)
     ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
     ms = C.c_float()
-    args = (lin.ts.ptr, frag.ptr, yd.ptr, None, None, None, None, m, n, 1, EPI_STORE, SPLIT)
+    args = (lin.ts.ptr, frag.ptr, yd.ptr, None, None, None, None, None, m, n, 1, EPI_STORE, SPLIT)
     call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, len(copies), s, C.byref(ms))
     call("rl_hip_time_gemm_fp8", ptrs, len(copies), *args, iters, s, C.byref(ms))
     b = m * n + 4 * ((m + 127) // 128) * ((n + 127) // 128) + 4 * (m + n)

@@ -95,13 +95,24 @@ size_t rl_hip_act_frag_bytes(int n, int T);
 int rl_hip_pack_fp8(const uint8_t* w_dev_rowmajor, const float* scale_dev, uint8_t* w_tiled, float* tile_scale,
                     int m, int n, void* stream);
 int rl_hip_pack_bf16(const uint16_t* w_dev_rowmajor, uint16_t* w_tiled, int m, int n, void* stream);
+/* MLP gate and up ([I][n] each, I a multiple of 8) packed together for the SwiGLU
+ * epilogue: tiled row tile k holds gate rows 8k..8k+7 then up rows 8k..8k+7, so the
+ * packed matrix has 2*I rows (rl_hip_fp8_packed_bytes(2*I, n) bytes) and FP8 tile
+ * scales [I/8][ceil(n/128)][2] (rl_hip_fp8_gate_up_tile_scales(I, n) floats; each
+ * half keeps its own 128x128 block scale). */
+size_t rl_hip_fp8_gate_up_tile_scales(int I, int n);
+int rl_hip_pack_fp8_gate_up(const uint8_t* gate_w, const float* gate_scale, const uint8_t* up_w, const float* up_scale,
+                            uint8_t* w_tiled, float* tile_scale, int I, int n, void* stream);
+int rl_hip_pack_bf16_gate_up(const uint16_t* gate_w, const uint16_t* up_w, uint16_t* w_tiled, int I, int n,
+                             void* stream);
 int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream);
 /* Y[T][m] (=, or += when accumulate) W . X for T in 1..8 using a packed fragment
  * buffer.  Deterministic: partial sums are combined in a fixed order, and token t's
  * result does not depend on T. */
 /* Prompt prefill: Y[t][ldy] (=, +=) W . x_t for T (any) tokens of rl_hip_pack_act
  * fragments, on the matrix cores (128 rows x 64 tokens per workgroup).  epilogue:
- * 0 store, 1 add, 2 SwiGLU over interleaved gate/up 16-row tiles (m/2 output rows).
+ * 0 store, 1 add, 2 SwiGLU over interleaved gate/up 16-row tiles (m/2 output rows),
+ * 5 SwiGLU over the rl_hip_pack_fp8_gate_up half tiles (m/2 output rows).
  * ldy <= 0: m (m/2 for SwiGLU).  Replaces the reference's prefill linears
  * (cuda_engine.cu:18338-18590 -> launch_linear for T > 8, :12008-12016). */
 int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,

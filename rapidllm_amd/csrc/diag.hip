@@ -69,17 +69,19 @@ int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream) {
 
 int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
                          float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
-                         int m, int n, int T, int epilogue, int split, int iters, void* stream, float* avg_ms) {
+                         const float* sumsq_in, int m, int n, int T, int epilogue, int split, int iters,
+                         void* stream, float* avg_ms) {
     return guard([&] {
         RL_REQUIRE(w_copies && n_copies >= 1 && iters >= 1 && avg_ms, RL_ERR_RANGE, "time_gemm: bad arguments");
         RL_REQUIRE(epilogue == kEpiStore || epilogue == kEpiPartial || epilogue == kEpiSwiGLU ||
-                       epilogue == kEpiAddNorm,
+                       epilogue == kEpiSwiGLUH || epilogue == kEpiAddNorm,
                    RL_ERR_RANGE, "time_gemm: epilogue must be store, partial, swiglu or add-norm");
         const hipStream_t s = S(stream);
-        const int ldy = epilogue == kEpiSwiGLU ? m / 2 : m;
+        const bool sw = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH;
+        const int ldy = sw ? m / 2 : m;
         const int m_valid = ldy;
         const int S_ = epilogue == kEpiPartial ? split : 1;
-        void* fo = epilogue == kEpiSwiGLU || epilogue == kEpiAddNorm ? frag_out : nullptr;
+        void* fo = sw || epilogue == kEpiAddNorm ? frag_out : nullptr;
         NormIO io;
         io.gamma_out = gamma;
         io.ss_out = sumsq;
@@ -87,14 +89,22 @@ int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float*
         io.kss = block_sumsq;
         io.kss_n = 128;
         io.kss_eps = 1e-6f;
-        const NormIO* iop = epilogue == kEpiAddNorm ? &io : nullptr;
+        RL_REQUIRE(!sumsq_in || epilogue == kEpiStore || sw, RL_ERR_RANGE,
+                   "time_gemm: input sums of squares with store or swiglu only");
+        if (sumsq_in) {
+            io.ss_in = sumsq_in;
+            io.groups_in = add_norm_groups(n);
+            io.n_norm = n;
+            io.eps = 1e-6f;
+        }
+        const NormIO* iop = epilogue == kEpiAddNorm || sumsq_in ? &io : nullptr;
         hipEvent_t a, b;
         RL_HIP(hipEventCreate(&a));
         RL_HIP(hipEventCreate(&b));
         RL_HIP(hipEventRecord(a, s));
         for (int i = 0; i < iters; ++i)
             rl::gemm_fp8_frag(static_cast<const uint8_t*>(w_copies[i % n_copies]), tile_scales, frag,
-                              fo && epilogue == kEpiSwiGLU ? nullptr : Y, m, n, T, epilogue, ldy, m_valid, s, S_, fo,
+                              fo && sw ? nullptr : Y, m, n, T, epilogue, ldy, m_valid, s, S_, fo,
                               iop);
         RL_HIP(hipEventRecord(b, s));
         RL_HIP(hipEventSynchronize(b));

@@ -77,6 +77,8 @@ struct Lin {
     int n = 0;
     uint8_t* w = nullptr;
     float* ts = nullptr;
+    bool guh = false;  // FP8/BF16 gate/up in half tiles (SwiGLU epilogue kEpiSwiGLUH)
+    int swiglu_epi() const { return guh ? kEpiSwiGLUH : kEpiSwiGLU; }
 };
 
 struct Layer {
@@ -319,7 +321,7 @@ class Engine {
                                      H, st_);
                 }
                 rmsnorm_pack(pf_x_, H, Ly.ffn_norm, nullptr, pf_frag_, H, T, eps, st_);
-                gemm_fp8_prefill(Ly.gate_up.w, Ly.gate_up.ts, pf_frag_, pf_h_, Ly.gate_up.m, H, T, kEpiSwiGLU, I, I,
+                gemm_fp8_prefill(Ly.gate_up.w, Ly.gate_up.ts, pf_frag_, pf_h_, Ly.gate_up.m, H, T, Ly.gate_up.swiglu_epi(), I, I,
                                  st_);
                 pack_act(pf_h_, pf_frag_h_, I, T, st_);
                 gemm_fp8_prefill(Ly.down.w, Ly.down.ts, pf_frag_h_, pf_x_, Ly.down.m, I, T, kEpiAdd, H, H, st_);
@@ -1127,11 +1129,52 @@ class Engine {
         }
     }
 
+    // Gate and up in half tiles (tile k: gate rows 8k..8k+7, then up rows), each half
+    // with its own block scale; whole-tile interleave when I is not a multiple of 8.
     Lin upload_gate_up(const RlTensor* g, const RlTensor* u, int I, int H) {
-        const int tiles = (I + 15) / 16;
-        Lin L = alloc_dense(g->quant, 2 * tiles * 16, H);
-        place_dense(L, g, I, H, 2, 0);
-        place_dense(L, u, I, H, 2, 1);
+        if (I % 8 != 0) {
+            const int tiles = (I + 15) / 16;
+            Lin L = alloc_dense(g->quant, 2 * tiles * 16, H);
+            place_dense(L, g, I, H, 2, 0);
+            place_dense(L, u, I, H, 2, 1);
+            return L;
+        }
+        for (const RlTensor* t : {g, u})
+            RL_REQUIRE(t->rows == I && t->cols == H, RL_ERR_FORMAT, std::string(t->name) + ": shape mismatch");
+        Lin L = alloc_guh(g->quant, I, H);
+        const size_t wb = static_cast<size_t>(I) * H * (g->quant == RL_Q_FP8_E4M3_B128 ? 1 : 2);
+        const size_t sb = static_cast<size_t>((I + 127) / 128) * ((H + 127) / 128) * 4;
+        uint8_t *tg = nullptr, *tu = nullptr;
+        float *sg = nullptr, *su = nullptr;
+        RL_HIP(hipMalloc(&tg, wb));
+        RL_HIP(hipMalloc(&tu, wb));
+        RL_HIP(hipMemcpyAsync(tg, g->data, wb, hipMemcpyHostToDevice, st_));
+        RL_HIP(hipMemcpyAsync(tu, u->data, wb, hipMemcpyHostToDevice, st_));
+        if (g->quant == RL_Q_FP8_E4M3_B128) {
+            RL_REQUIRE(g->scale && u->scale, RL_ERR_FORMAT, std::string(g->name) + ": FP8 weight without scale");
+            RL_HIP(hipMalloc(&sg, sb));
+            RL_HIP(hipMalloc(&su, sb));
+            RL_HIP(hipMemcpyAsync(sg, g->scale, sb, hipMemcpyHostToDevice, st_));
+            RL_HIP(hipMemcpyAsync(su, u->scale, sb, hipMemcpyHostToDevice, st_));
+            pack_fp8_gate_up(tg, sg, tu, su, L.w, L.ts, I, H, st_);
+        } else {
+            pack_bf16_gate_up(reinterpret_cast<const uint16_t*>(tg), reinterpret_cast<const uint16_t*>(tu),
+                              reinterpret_cast<uint16_t*>(L.w), I, H, st_);
+        }
+        RL_HIP(hipStreamSynchronize(st_));
+        for (void* p : {static_cast<void*>(tg), static_cast<void*>(tu), static_cast<void*>(sg), static_cast<void*>(su)})
+            if (p) (void)hipFree(p);
+        return L;
+    }
+
+    Lin alloc_guh(int kind, int I, int n) {
+        Lin L;
+        L.kind = kind;
+        L.m = 2 * I;
+        L.n = n;
+        L.guh = true;
+        L.w = static_cast<uint8_t*>(mem_.get(lin_bytes(kind, 2 * I, n)));
+        if (kind == RL_Q_FP8_E4M3_B128) L.ts = mem_.get_n<float>(rl_hip_fp8_gate_up_tile_scales(I, n));
         return L;
     }
 
@@ -1218,23 +1261,24 @@ class Engine {
     }
 
     Lin synth_gate_up(int I, int H) {
-        // gate and up rows interleaved per 16-row tile; each half random like a
-        // loaded matrix (the interleave only changes where tiles sit)
-        const int tiles = (I + 15) / 16;
-        Lin L = alloc_dense(RL_Q_FP8_E4M3_B128, 2 * tiles * 16, H);
+        // gate and up each random like a loaded matrix, then packed into half tiles
+        RL_REQUIRE(I % 8 == 0, RL_ERR_UNSUPPORTED, "synthetic model: intermediate must be a multiple of 8");
+        Lin L = alloc_guh(RL_Q_FP8_E4M3_B128, I, H);
+        const size_t wb = static_cast<size_t>(I) * H;
+        const size_t ns = static_cast<size_t>((I + 127) / 128) * ((H + 127) / 128);
+        uint8_t* tmp[2] = {};
+        float* stmp[2] = {};
         for (int half = 0; half < 2; ++half) {
-            const size_t wb = static_cast<size_t>(I) * H;
-            const size_t ns = static_cast<size_t>((I + 127) / 128) * ((H + 127) / 128);
-            uint8_t* tmp = nullptr;
-            float* stmp = nullptr;
-            RL_HIP(hipMalloc(&tmp, wb));
-            RL_HIP(hipMalloc(&stmp, ns * 4));
-            fill_fp8(tmp, wb, next_seed(), st_);
-            fill_loguniform(stmp, ns, 1e-3f, 1e-1f, next_seed(), st_);
-            pack_fp8_rows(tmp, stmp, L.w, L.ts, I, H, 2, half, st_);
-            RL_HIP(hipStreamSynchronize(st_));
-            (void)hipFree(tmp);
-            (void)hipFree(stmp);
+            RL_HIP(hipMalloc(&tmp[half], wb));
+            RL_HIP(hipMalloc(&stmp[half], ns * 4));
+            fill_fp8(tmp[half], wb, next_seed(), st_);
+            fill_loguniform(stmp[half], ns, 1e-3f, 1e-1f, next_seed(), st_);
+        }
+        pack_fp8_gate_up(tmp[0], stmp[0], tmp[1], stmp[1], L.w, L.ts, I, H, st_);
+        RL_HIP(hipStreamSynchronize(st_));
+        for (int half = 0; half < 2; ++half) {
+            (void)hipFree(tmp[half]);
+            (void)hipFree(stmp[half]);
         }
         return L;
     }
@@ -1382,7 +1426,7 @@ class Engine {
                                   attn_ws_bytes_, xn_, frag_, st_);
                 gemm_on(Ly.o_proj, frag_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
             }
-            gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, T, kEpiSwiGLU, frag_h_, &in);
+            gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, T, Ly.gate_up.swiglu_epi(), frag_h_, &in);
             out.gamma_out = i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_;
             gemm_on(Ly.down, frag_h_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
         }
@@ -1427,10 +1471,10 @@ class Engine {
                 // SwiGLU epilogue: fp32 h only when a K-quant down needs it
                 if (Ly.gate_up.kind == RL_Q_FP8_E4M3_B128)
                     gemm_fp8_frag(Ly.gate_up.w, Ly.gate_up.ts, frag_, down_frag ? nullptr : h_, Ly.gate_up.m,
-                                  Ly.gate_up.n, T, kEpiSwiGLU, I, I, st_, 1, down_frag ? frag_h_ : nullptr);
+                                  Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1, down_frag ? frag_h_ : nullptr);
                 else
                     gemm_bf16_frag(reinterpret_cast<const uint16_t*>(Ly.gate_up.w), frag_, down_frag ? nullptr : h_,
-                                   Ly.gate_up.m, Ly.gate_up.n, T, kEpiSwiGLU, I, I, st_, 1,
+                                   Ly.gate_up.m, Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1,
                                    down_frag ? frag_h_ : nullptr);
             } else {
                 if (Ly.gate_cat) {
@@ -1588,7 +1632,7 @@ class Engine {
                                       c_.rope_theta, eps, attn_ws_, attn_ws_bytes_, xn_, frag_, st_, b, B);
                 gemm_on(Ly.o_proj, frag_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
             }
-            gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, B, kEpiSwiGLU, frag_h_, &in);
+            gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, B, Ly.gate_up.swiglu_epi(), frag_h_, &in);
             out.gamma_out = i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_;
             gemm_on(Ly.down, frag_h_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
         }

@@ -54,7 +54,7 @@ __device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 // to Y + (s*T + t)*ldy (the consumer adds the S slices in order).
 // Weight loads are non-temporal: every weight byte is streamed once per launch.
 
-enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4 };
+enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4, kSwiGLUH = 5 };
 
 // Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
@@ -71,7 +71,12 @@ constexpr int kKsMaxIt = 8;
 // EPI >= 0 / SSIN >= 0: the epilogue and whether the input RMSNorm is folded in
 // (io.ss_in) are compile-time, so an instantiation keeps no registers for the
 // others' state across the main loop (eight waves per SIMD need <= 64 VGPRs).
-template <int RT, int KSPLIT, int D, bool kFp8, bool kKs = false, int TT = 0, int EPI = -1, int SSIN = -1>
+// kGuh: gate/up in half tiles (SwiGLU epilogue): 16-row tile k holds gate rows
+// 8k .. 8k+7 (tile rows 0-7) and up rows 8k .. 8k+7 (rows 8-15), with one block scale
+// per half (tscale [tile][kb][2]); one tile gives 8 outputs, so a workgroup needs
+// only one row tile (the whole-tile interleave needs two).
+template <int RT, int KSPLIT, int D, bool kFp8, bool kKs = false, int TT = 0, int EPI = -1, int SSIN = -1,
+          bool kGuh = false>
 __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* __restrict__ W,
                                                                 const float* __restrict__ tscale,
                                                                 const i32x4* __restrict__ frag,
@@ -169,7 +174,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     for (int r = 0; r < RT; ++r) {
         const int rt = min(rt0 + r, m_tiles - 1);
         wbase[r] = W + static_cast<size_t>(rt) * n_kb * kTileBytes;  // uniform tile-row base
-        sbase[r] = kFp8 ? tscale + static_cast<size_t>(rt) * n_kb : nullptr;
+        sbase[r] = kFp8 ? tscale + static_cast<size_t>(rt) * n_kb * (kGuh ? 2 : 1) : nullptr;
     }
     const i32x4* fbase = frag + static_cast<size_t>(g) * NC + bcol;
     const size_t fstride = static_cast<size_t>(16) * NC;  // per column block
@@ -177,6 +182,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     i32x4 wbuf[D][RT][NW];
     i32x4 bbuf[D][4];
     float sbuf[D][RT];
+    float sbuf2[D][RT];  // kGuh: the up half's scale
     // kKs: the four partial sums of squares of this wave's blocks for this lane's
     // token, all loaded before the weight stream (blocks w + i*KSPLIT, i < kKsMaxIt)
     const int ktok = bcol < T ? bcol : bcol - T;
@@ -196,7 +202,13 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     // first weight tile instead)
     const uint8_t* dummy = n_kb * 512 * T >= kTileBytes ? reinterpret_cast<const uint8_t*>(frag) : wbase[0];
     auto load = [&](int d, int kb, bool live) {
-        if constexpr (kFp8) {
+        if constexpr (kFp8 && kGuh) {
+#pragma unroll
+            for (int r = 0; r < RT; ++r) {
+                sbuf[d][r] = sbase[r][2 * (live ? kb : 0)];
+                sbuf2[d][r] = sbase[r][2 * (live ? kb : 0) + 1];
+            }
+        } else if constexpr (kFp8) {
 #pragma unroll
             for (int r = 0; r < RT; ++r) sbuf[d][r] = sbase[r][live ? kb : 0];
         }
@@ -259,7 +271,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                 }
                 acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
             }
-            if constexpr (kFp8 && kKs)
+            if constexpr (kFp8 && kGuh)
+                tot[r] += (g < 2 ? sbuf[d][r] : sbuf2[d][r]) * acc;  // C rows 4g..4g+3: gate g < 2
+            else if constexpr (kFp8 && kKs)
                 tot[r] += (sbuf[d][r] * ks) * acc;
             else if constexpr (kFp8)
                 tot[r] += sbuf[d][r] * acc;
@@ -336,7 +350,27 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         return has_ss ? v * s_inv[t] : v;
     };
 
-    if (epilogue == kSwiGLU) {
+    if (kGuh && epilogue == kSwiGLU) {
+        // half tiles: rows j and 8 + j of a tile are gate and up of output 8k + j
+        for (int it = threadIdx.x; it < RT * T * 8; it += 64 * KSPLIT) {
+            const int j = it % 8, t = (it / 8) % T, r = it / (8 * T);
+            const int orow = (rt0 + r) * 8 + j;
+            if (rt0 + r < m_tiles && orow < m_valid) {
+                const float gv = final_value(r, t, j);
+                const float uv = final_value(r, t, 8 + j);
+                const float h = gv / (1.f + __expf(-gv)) * uv;
+                if (Y) Y[static_cast<size_t>(t) * ldy + orow] = h;
+                if (frag_out) {
+                    uint16_t hi, mid;
+                    split_bf16(h, hi, mid);
+                    uint16_t* f16 = reinterpret_cast<uint16_t*>(frag_out);
+                    const size_t u = frag_unit(orow >> 3, t, T);
+                    f16[u * 8 + (orow & 7)] = hi;
+                    f16[(u + T) * 8 + (orow & 7)] = mid;
+                }
+            }
+        }
+    } else if (epilogue == kSwiGLU) {
         // interleaved tiles: even = gate rows, odd = up rows of the same 16 outputs.
         // h = silu(g) * u goes to Y (fp32, if given) and, if frag_out is given, to the
         // bf16 hi/mid fragments of the next linear (input column = output row), each
@@ -487,6 +521,59 @@ __global__ void pack_fp8_kernel(const uint8_t* __restrict__ w, const float* __re
     }
 }
 
+// Gate or up (half = 0 / 1) [I][n] into the half-tile gate/up layout: tile k rows
+// 8*half .. 8*half+7 take source rows 8k .. 8k+7; scale [tile][kb][2].  Each lane
+// owns tile row (lane & 15), as in pack_fp8_kernel.
+__global__ void pack_fp8_guh_kernel(const uint8_t* __restrict__ w, const float* __restrict__ scale,
+                                    uint8_t* __restrict__ out, float* __restrict__ tscale, int I, int n, int n_kb,
+                                    int half) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int tiles = (I + 7) / 8;
+    if (idx >= static_cast<size_t>(tiles) * n_kb * 64) return;
+    const int lane = idx & 63;
+    const int kb = (idx >> 6) % n_kb;
+    const int rt = static_cast<int>((idx >> 6) / n_kb);
+    const int r16 = lane & 15;
+    if ((r16 >= 8) != (half != 0)) return;
+    const int row = rt * 8 + (r16 & 7);
+    const int c0 = kb * kBlockCols + 32 * (lane >> 4);
+    uint8_t b[32];
+#pragma unroll
+    for (int e = 0; e < 32; ++e) b[e] = (row < I && c0 + e < n) ? w[static_cast<size_t>(row) * n + c0 + e] : 0;
+    uint8_t* tile = out + (static_cast<size_t>(rt) * n_kb + kb) * 2048;
+#pragma unroll
+    for (int e = 0; e < 16; ++e) {
+        tile[16 * lane + e] = b[e];
+        tile[1024 + 16 * lane + e] = b[16 + e];
+    }
+    if (r16 == 8 * half) {
+        const int sb_cols = (n + 127) / 128;
+        tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + half] = scale[static_cast<size_t>((rt * 8) / 128) * sb_cols + kb];
+    }
+}
+
+__global__ void pack_bf16_guh_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int I, int n,
+                                     int n_kb, int half) {
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int tiles = (I + 7) / 8;
+    if (idx >= static_cast<size_t>(tiles) * n_kb * 64) return;
+    const int lane = idx & 63;
+    const int kb = (idx >> 6) % n_kb;
+    const int rt = static_cast<int>((idx >> 6) / n_kb);
+    const int r16 = lane & 15;
+    if ((r16 >= 8) != (half != 0)) return;
+    const int row = rt * 8 + (r16 & 7);
+    const int c0 = kb * kBlockCols + 32 * (lane >> 4);
+    uint16_t* tile = out + (static_cast<size_t>(rt) * n_kb + kb) * 2048;
+#pragma unroll
+    for (int q = 0; q < 4; ++q)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int c = c0 + 8 * q + e;
+            tile[q * 512 + 8 * lane + e] = (row < I && c < n) ? w[static_cast<size_t>(row) * n + c] : 0;
+        }
+}
+
 __global__ void pack_bf16_kernel(const uint16_t* __restrict__ w, uint16_t* __restrict__ out, int m, int n,
                                  int n_kb, int rt_stride, int rt_offset) {
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
@@ -542,29 +629,31 @@ inline bool bperm_enabled() {
     return on;
 }
 
-template <bool kFp8, int RT, int KS, int D, bool kKs, int TT, int EPI = -1, int SSIN = -1>
+template <bool kFp8, int RT, int KS, int D, bool kKs, int TT, int EPI = -1, int SSIN = -1, bool kGuh = false>
 void launch_gemm_tt(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                     int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
     const int groups = (m_tiles_of(m) + RT - 1) / RT;
-    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8, kKs, TT, EPI, SSIN>), dim3(groups * S), dim3(64 * KS), 0,
-                       s, static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag), Y, m, n_kb, T,
-                       epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out), io);
+    hipLaunchKernelGGL((gemm_frag_kernel<RT, KS, D, kFp8, kKs, TT, EPI, SSIN, kGuh>), dim3(groups * S),
+                       dim3(64 * KS), 0, s, static_cast<const uint8_t*>(W), tscale, static_cast<const i32x4*>(frag),
+                       Y, m, n_kb, T, epilogue, ldy, m_valid, S, static_cast<i32x4*>(frag_out), io);
 }
 
 // The permuted-B kernel for (RT, KS) with the epilogue and folded-norm input as
 // compile-time parameters (the combinations the decode step uses; others run the
 // kernel with runtime ones).
-template <bool kFp8, int RT, int KS, bool kKs, int TT>
+template <bool kFp8, int RT, int KS, bool kKs, int TT, bool kGuh = false>
 void launch_gemm_spec(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                       int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
     const bool ss = io.ss_in != nullptr;
-#define RL_SPEC(E, SS)                                                                                            \
-    if (epilogue == E && ss == static_cast<bool>(SS)) {                                                           \
-        launch_gemm_tt<kFp8, RT, KS, 1, kKs, TT, E, SS>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, \
-                                                       frag_out, io, s);                                          \
-        return;                                                                                                   \
+#define RL_SPEC(E, SS)                                                                                              \
+    if (epilogue == E && ss == static_cast<bool>(SS)) {                                                             \
+        launch_gemm_tt<kFp8, RT, KS, 1, kKs, TT, E, SS, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, \
+                                                             S, frag_out, io, s);                                 \
+        return;                                                                                                     \
     }
-    if constexpr (RT == 1) {
+    if constexpr (kGuh) {
+        RL_SPEC(kSwiGLU, 0) RL_SPEC(kSwiGLU, 1)
+    } else if constexpr (RT == 1) {
         RL_SPEC(kStore, 0) RL_SPEC(kStore, 1) RL_SPEC(kAdd, 0) RL_SPEC(kAdd, 1)
     } else if constexpr (kKs) {
         RL_SPEC(kAddNorm, 0)
@@ -572,26 +661,27 @@ void launch_gemm_spec(const void* W, const float* tscale, const void* frag, floa
         RL_SPEC(kSwiGLU, 0) RL_SPEC(kSwiGLU, 1) RL_SPEC(kAddNorm, 0)
     }
 #undef RL_SPEC
-    launch_gemm_tt<kFp8, RT, KS, 1, kKs, TT>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io,
-                                            s);
+    launch_gemm_tt<kFp8, RT, KS, 1, kKs, TT, -1, -1, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S,
+                                                         frag_out, io, s);
 }
 
 // Depth-1 launches with T <= 4 take the compile-time-T kernels (permuted B operand).
-template <bool kFp8, int RT, int KS, int D, bool kKs = false>
+template <bool kFp8, int RT, int KS, int D, bool kKs = false, bool kGuh = false>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                      int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
     if constexpr (D == 1) {
         if (bperm_enabled()) {
             switch (T) {
-            case 1: launch_gemm_spec<kFp8, RT, KS, kKs, 1>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
-            case 2: launch_gemm_spec<kFp8, RT, KS, kKs, 2>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
-            case 3: launch_gemm_spec<kFp8, RT, KS, kKs, 3>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
-            case 4: launch_gemm_spec<kFp8, RT, KS, kKs, 4>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 1: launch_gemm_spec<kFp8, RT, KS, kKs, 1, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 2: launch_gemm_spec<kFp8, RT, KS, kKs, 2, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 3: launch_gemm_spec<kFp8, RT, KS, kKs, 3, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 4: launch_gemm_spec<kFp8, RT, KS, kKs, 4, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
             default: break;
             }
         }
     }
-    launch_gemm_tt<kFp8, RT, KS, D, kKs, 0>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s);
+    launch_gemm_tt<kFp8, RT, KS, D, kKs, 0, -1, -1, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S,
+                                                         frag_out, io, s);
 }
 
 // m = rows of the (tiled) weight; outputs go to Y[t * ldy + row] for row < m_valid
@@ -604,7 +694,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     RL_REQUIRE(m > 0 && n > 0, RL_ERR_RANGE, "gemm: empty shape");
     RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "gemm: T must be in 1..8");
     RL_REQUIRE(W && frag && (Y || frag_out), RL_ERR_RANGE, "gemm: null pointer");
-    RL_REQUIRE(!frag_out || epilogue == kSwiGLU || epilogue == kAddNorm, RL_ERR_RANGE,
+    RL_REQUIRE(!frag_out || epilogue == kSwiGLU || epilogue == kSwiGLUH || epilogue == kAddNorm, RL_ERR_RANGE,
                "gemm: fragment output only with the SwiGLU / add-norm epilogues");
     RL_REQUIRE(epilogue != kAddNorm || (Y && frag_out && io.gamma_out && io.ss_out && S == 1), RL_ERR_RANGE,
                "gemm add-norm: needs Y, fragment output, gamma and the sum-of-squares output, no split");
@@ -614,6 +704,17 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     RL_REQUIRE(!kFp8 || tscale, RL_ERR_RANGE, "gemm: FP8 weights need tile scales");
     const int n_kb = n_kb_of(n);
     const int m_tiles = m_tiles_of(m);
+    if (epilogue == kSwiGLUH) {
+        // half-tile gate/up: one row tile per 16-wave workgroup (34816 x 5120: 27.5 us
+        // vs 29.6 us for the whole-tile interleave at two tiles per workgroup)
+        RL_REQUIRE(m % 16 == 0 && S == 1 && !io.kss && !io.xpart, RL_ERR_RANGE,
+                   "gemm swiglu (half tiles): rows a multiple of 16, no split or block scale");
+        if (io.ss_in) RL_REQUIRE(16 >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
+        launch_gemm_cfg<kFp8, 1, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
+                                                     frag_out, io, s);
+        check_launch("gemm_frag_kernel");
+        return;
+    }
     if (epilogue == kSwiGLU)
         RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm swiglu: interleaved rows must be a multiple of 32");
     RL_REQUIRE(S >= 1 && (S == 1 || epilogue == kPartial), RL_ERR_RANGE, "gemm: split-K needs the partial epilogue");
@@ -711,6 +812,23 @@ void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* ts
                        n_kb_of(n), rt_stride, rt_offset);
     check_launch("pack_fp8_kernel");
 }
+void pack_fp8_gate_up(const uint8_t* gw, const float* gs, const uint8_t* uw, const float* us, uint8_t* dst,
+                      float* tscale, int I, int n, hipStream_t s) {
+    RL_REQUIRE(I > 0 && I % 8 == 0 && n > 0, RL_ERR_RANGE, "pack gate/up: I must be a positive multiple of 8");
+    const size_t total = static_cast<size_t>(I / 8) * n_kb_of(n) * 64;
+    for (int half = 0; half < 2; ++half)
+        hipLaunchKernelGGL(pack_fp8_guh_kernel, dim3((total + 255) / 256), dim3(256), 0, s, half ? uw : gw,
+                           half ? us : gs, dst, tscale, I, n, n_kb_of(n), half);
+    check_launch("pack_fp8_guh_kernel");
+}
+void pack_bf16_gate_up(const uint16_t* gw, const uint16_t* uw, uint16_t* dst, int I, int n, hipStream_t s) {
+    RL_REQUIRE(I > 0 && I % 8 == 0 && n > 0, RL_ERR_RANGE, "pack gate/up: I must be a positive multiple of 8");
+    const size_t total = static_cast<size_t>(I / 8) * n_kb_of(n) * 64;
+    for (int half = 0; half < 2; ++half)
+        hipLaunchKernelGGL(pack_bf16_guh_kernel, dim3((total + 255) / 256), dim3(256), 0, s, half ? uw : gw, dst, I,
+                           n, n_kb_of(n), half);
+    check_launch("pack_bf16_guh_kernel");
+}
 void pack_bf16_rows(const uint16_t* w, uint16_t* dst, int m, int n, int rt_stride, int rt_offset, hipStream_t s) {
     const size_t total = static_cast<size_t>(m_tiles_of(m)) * n_kb_of(n) * 64;
     hipLaunchKernelGGL(pack_bf16_kernel, dim3((total + 255) / 256), dim3(256), 0, s, w, dst, m, n, n_kb_of(n),
@@ -740,6 +858,27 @@ int rl_hip_pack_fp8(const uint8_t* w, const float* scale, uint8_t* w_tiled, floa
     return guard([&] {
         RL_REQUIRE(m > 0 && n > 0 && w && scale && w_tiled && tile_scale, RL_ERR_RANGE, "pack_fp8: bad args");
         rl::pack_fp8_rows(w, scale, w_tiled, tile_scale, m, n, 1, 0, S(stream));
+    });
+}
+
+size_t rl_hip_fp8_gate_up_tile_scales(int I, int n) {
+    return I > 0 && n > 0 ? static_cast<size_t>((I + 7) / 8) * n_kb_of(n) * 2 : 0;
+}
+
+int rl_hip_pack_fp8_gate_up(const uint8_t* gate_w, const float* gate_scale, const uint8_t* up_w, const float* up_scale,
+                            uint8_t* w_tiled, float* tile_scale, int I, int n, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(gate_w && gate_scale && up_w && up_scale && w_tiled && tile_scale, RL_ERR_RANGE,
+                   "pack_fp8_gate_up: null pointer");
+        rl::pack_fp8_gate_up(gate_w, gate_scale, up_w, up_scale, w_tiled, tile_scale, I, n, S(stream));
+    });
+}
+
+int rl_hip_pack_bf16_gate_up(const uint16_t* gate_w, const uint16_t* up_w, uint16_t* w_tiled, int I, int n,
+                             void* stream) {
+    return guard([&] {
+        RL_REQUIRE(gate_w && up_w && w_tiled, RL_ERR_RANGE, "pack_bf16_gate_up: null pointer");
+        rl::pack_bf16_gate_up(gate_w, up_w, w_tiled, I, n, S(stream));
     });
 }
 

@@ -5,7 +5,7 @@
 
 namespace rl {
 
-enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3, kEpiAddNorm = 4 };
+enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3, kEpiAddNorm = 4, kEpiSwiGLUH = 5 };
 
 // RMSNorm folded across a residual GEMM and the next linear (y = rmsnorm(x) * (1+g)
 // never materialised):
@@ -61,6 +61,11 @@ void pack_act(const float* X, void* frag, int n, int T, hipStream_t s);
 void pack_fp8_rows(const uint8_t* w, const float* scale, uint8_t* dst, float* tscale, int m, int n, int rt_stride,
                    int rt_offset, hipStream_t s);
 void pack_bf16_rows(const uint16_t* w, uint16_t* dst, int m, int n, int rt_stride, int rt_offset, hipStream_t s);
+// Gate and up [I][n] into half tiles (tile k: gate rows 8k..8k+7, then up rows), 2*I
+// tiled rows; FP8 tile scales [tile][kb][2].  The kEpiSwiGLUH epilogue reads this.
+void pack_fp8_gate_up(const uint8_t* gw, const float* gs, const uint8_t* uw, const float* us, uint8_t* dst,
+                      float* tscale, int I, int n, hipStream_t s);
+void pack_bf16_gate_up(const uint16_t* gw, const uint16_t* uw, uint16_t* dst, int I, int n, hipStream_t s);
 
 // kquant.hip
 size_t kq_workspace_bytes(int m, int n, int T);

@@ -48,7 +48,9 @@ __device__ inline void e4m3x4_to_bf16(uint32_t w, uint32_t& lo, uint32_t& hi) {
 __device__ inline float silu_f(float x) { return x / (1.f + __expf(-x)); }
 
 // EPI: 0 store, 1 add (Y += W.x), 2 SwiGLU over interleaved gate/up row tiles
-// (even tile = gate rows, odd = up rows of the same 16 outputs; Y row = output row).
+// (even tile = gate rows, odd = up rows of the same 16 outputs; Y row = output row),
+// 5 SwiGLU over half tiles (tile k: gate rows 8k..8k+7, up rows 8k..8k+7; scales
+// [tile][kb][2]).
 template <int EPI>
 __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __restrict__ W,
                                                            const float* __restrict__ tscale,
@@ -115,7 +117,9 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
 #pragma unroll
         for (int r = 0; r < kPfRT; ++r) {
             const int rt = min(rt0 + r, m_tiles - 1);
-            const float sc = tscale[static_cast<size_t>(rt) * n_kb + kb];
+            // C rows 4g..4g+3 of a half-tile matrix: gate (g < 2) or up scale
+            const float sc = EPI == 5 ? tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + (g >> 1)]
+                                      : tscale[static_cast<size_t>(rt) * n_kb + kb];
             f32x4 acc[kPfNT];
 #pragma unroll
             for (int nt = 0; nt < kPfNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
@@ -146,7 +150,19 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
         const int tok = tokv[nt];
         if (tok >= T) break;
         float* yrow = Y + static_cast<size_t>(tok) * ldy;
-        if constexpr (EPI == 2) {
+        if constexpr (EPI == 5) {
+            // lane (g < 2, col) holds gate rows 4g..4g+3; lane + 32 the matching up rows
+#pragma unroll
+            for (int r = 0; r < kPfRT; ++r) {
+                if (rt0 + r >= m_tiles) break;
+                const int orow = (rt0 + r) * 8 + 4 * g;
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float up = __shfl_xor(tot[nt][r][v], 32, 64);
+                    if (g < 2 && orow + v < m_valid) yrow[orow + v] = silu_f(tot[nt][r][v]) * up;
+                }
+            }
+        } else if constexpr (EPI == 2) {
 #pragma unroll
             for (int r = 0; r < kPfRT; r += 2) {
                 if (rt0 + r + 1 >= m_tiles) break;
@@ -181,8 +197,9 @@ void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float
                       int ldy, int m_valid, hipStream_t s) {
     RL_REQUIRE(m > 0 && n > 0 && T >= 1, RL_ERR_RANGE, "gemm_prefill: empty shape");
     RL_REQUIRE(W && ts && frag && Y, RL_ERR_RANGE, "gemm_prefill: null pointer");
-    RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU, RL_ERR_RANGE,
+    RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU || epi == kEpiSwiGLUH, RL_ERR_RANGE,
                "gemm_prefill: epilogue must be store, add or swiglu");
+    if (epi == kEpiSwiGLUH) RL_REQUIRE(m % 16 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows a multiple of 16");
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     if (epi == kEpiSwiGLU) RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows must be a multiple of 32");
     const int n_kb = (n + 127) / 128;
@@ -194,8 +211,11 @@ void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float
     else if (epi == kEpiAdd)
         hipLaunchKernelGGL(gemm_prefill_kernel<1>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
                            n_kb, T, ldy, m_valid);
-    else
+    else if (epi == kEpiSwiGLU)
         hipLaunchKernelGGL(gemm_prefill_kernel<2>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
+                           n_kb, T, ldy, m_valid);
+    else
+        hipLaunchKernelGGL(gemm_prefill_kernel<5>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
                            n_kb, T, ldy, m_valid);
     check_launch("gemm_prefill_kernel");
 }
@@ -207,7 +227,7 @@ extern "C" {
 int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                             int T, int epilogue, int ldy, void* stream) {
     return guard([&] {
-        const int mv = epilogue == kEpiSwiGLU ? m / 2 : m;
+        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
         rl::gemm_fp8_prefill(w_tiled, tile_scale, frag, Y, m, n, T, epilogue, ldy > 0 ? ldy : mv, mv, S(stream));
     });
 }

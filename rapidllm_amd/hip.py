@@ -50,6 +50,9 @@ _SIGS = {
     "rl_hip_act_frag_bytes": (_sz, [_i, _i]),
     "rl_hip_pack_fp8": (_i, [_vp, _vp, _vp, _vp, _i, _i, _vp]),
     "rl_hip_pack_bf16": (_i, [_vp, _vp, _i, _i, _vp]),
+    "rl_hip_fp8_gate_up_tile_scales": (_sz, [_i, _i]),
+    "rl_hip_pack_fp8_gate_up": (_i, [_vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_pack_bf16_gate_up": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
     "rl_hip_pack_act": (_i, [_vp, _vp, _i, _i, _vp]),
     "rl_hip_gemm_fp8_frag": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rl_hip_gemm_bf16_frag": (_i, [_vp, _vp, _vp, _i, _i, _i, _i, _vp]),
@@ -117,7 +120,7 @@ _SIGS = {
     "rl_hip_map_name": (_i, [_i, C.c_char_p, C.c_char_p, _i]),
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
-    "rl_hip_time_gemm_fp8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
+    "rl_hip_time_gemm_fp8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
                                   C.POINTER(C.c_float)]),
     "rl_hip_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),
     "rl_hip_gemm_fp8_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),

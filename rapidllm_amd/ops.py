@@ -48,6 +48,28 @@ class Fp8Linear:
              1 if accumulate else 0, stream)
 
 
+class Fp8GateUp:
+    """MLP gate and up ([I][n] block-FP8 each) packed together for the SwiGLU
+    epilogue in half tiles (tile k: gate rows 8k..8k+7, then up rows 8k..8k+7, each
+    half with its own 128x128 block scale), as the engine keeps them.  m = 2*I."""
+
+    def __init__(self, wg, sg, wu, su, stream=None):
+        I, n = wg.shape
+        assert wu.shape == (I, n) and I % 8 == 0
+        self.m, self.n, self.I = 2 * I, n, I
+        L = hip.lib()
+        self.w = DeviceBuffer(L.rl_hip_fp8_packed_bytes(2 * I, n))
+        self.ts = DeviceBuffer(4 * L.rl_hip_fp8_gate_up_tile_scales(I, n))
+        bufs = [DeviceBuffer.from_numpy(np.ascontiguousarray(wg, np.uint8), stream),
+                DeviceBuffer.from_numpy(_f32(sg), stream),
+                DeviceBuffer.from_numpy(np.ascontiguousarray(wu, np.uint8), stream),
+                DeviceBuffer.from_numpy(_f32(su), stream)]
+        call("rl_hip_pack_fp8_gate_up", *[b.ptr for b in bufs], self.w.ptr, self.ts.ptr, I, n, stream)
+        call("rl_hip_stream_synchronize", stream)
+        for b in bufs:
+            b.free()
+
+
 class Bf16Linear:
     """BF16 weight [m][n] (QuantKind::BF16, e.g. lm_head) in the MFMA-tiled layout."""
 
@@ -85,10 +107,11 @@ def linear_T(lin, X: np.ndarray, stream=None) -> np.ndarray:
 def linear_prefill(lin: Fp8Linear, X: np.ndarray, epilogue: int = 0, Y0: np.ndarray | None = None,
                    stream=None) -> np.ndarray:
     """Prefill linear over T (any) tokens: Y[T][m'] = W . X (epilogue 0 store, 1 add
-    onto Y0, 2 SwiGLU over interleaved gate/up tiles: m' = m/2)."""
+    onto Y0, 2 SwiGLU over interleaved gate/up tiles, 5 SwiGLU over the Fp8GateUp
+    half tiles: m' = m/2)."""
     X = _f32(X).reshape(-1, lin.n)
     T = X.shape[0]
-    mo = lin.m // 2 if epilogue == 2 else lin.m
+    mo = lin.m // 2 if epilogue in (2, 5) else lin.m
     xd = DeviceBuffer.from_numpy(X, stream)
     frag = act_frag_buffer(lin.n, T)
     yd = DeviceBuffer.from_numpy(_f32(Y0).reshape(T, mo), stream) if Y0 is not None else DeviceBuffer(4 * T * mo)

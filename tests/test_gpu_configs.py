@@ -71,25 +71,25 @@ def interleave_gate_up(g: ops.Fp8Linear, u: ops.Fp8Linear) -> Tiled:
 
 
 def run_epilogue(lin, X, epi, x0=None, gamma=None, block_sumsq=None):
-    """One launch of the decode-step GEMM with epilogue `epi` (0 store, 2 SwiGLU,
-    4 residual add + next norm's data) through rl_hip_time_gemm_fp8 (iters = 1)."""
+    """One launch of the decode-step GEMM with epilogue `epi` (0 store, 2 SwiGLU over
+    whole tiles, 5 over half tiles, 4 residual add + next norm's data) through rl_hip_time_gemm_fp8 (iters = 1)."""
     T, n = X.shape
     m = lin.m
     xd = DeviceBuffer.from_numpy(np.ascontiguousarray(X, np.float32))
     frag = ops.act_frag_buffer(n, T)
     call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
-    mo = m // 2 if epi == 2 else m
+    mo = m // 2 if epi in (2, 5) else m
     yd = DeviceBuffer.from_numpy(x0) if x0 is not None else DeviceBuffer(4 * T * mo)
-    fo = ops.act_frag_buffer(mo, T) if epi in (2, 4) else None
+    fo = ops.act_frag_buffer(mo, T) if epi in (2, 4, 5) else None
     gd = DeviceBuffer.from_numpy(gamma) if gamma is not None else None
     ssd = DeviceBuffer(4 * T * (m // 32)) if epi == 4 else None
     bsd = DeviceBuffer.from_numpy(block_sumsq) if block_sumsq is not None else None
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
     call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr if fo else None,
-         gd.ptr if gd else None, ssd.ptr if ssd else None, bsd.ptr if bsd else None, m, n, T, epi, 1, 1, None,
+         gd.ptr if gd else None, ssd.ptr if ssd else None, bsd.ptr if bsd else None, None, m, n, T, epi, 1, 1, None,
          C.byref(ms))
-    y = None if epi == 2 else yd.numpy(np.float32, (T, mo))
+    y = None if epi in (2, 5) else yd.numpy(np.float32, (T, mo))
     ss = ssd.numpy(np.float32, (m // 32, T)) if ssd else None
     fr = fo.numpy(np.uint8, (fo.nbytes,)) if fo else None
     return y, fr, ss
@@ -125,8 +125,8 @@ def test_c3_gate_up_swiglu(gpu, orc, T):
     Wg, sg = synth.fp8_weight(r, I, H), synth.fp8_scales(r, I, H)
     Wu, su = synth.fp8_weight(r, I, H), synth.fp8_scales(r, I, H)
     X = bf16_normal(r, (T, H))
-    lin = interleave_gate_up(ops.Fp8Linear(Wg, sg), ops.Fp8Linear(Wu, su))
-    _, fr, _ = run_epilogue(lin, X, 2)
+    lin = ops.Fp8GateUp(Wg, sg, Wu, su)
+    _, fr, _ = run_epilogue(lin, X, 5)
     h = unpack_frag(fr, I, T)
     g = oracle_gemm(orc, Wg, sg, X).astype(np.float64)
     u = oracle_gemm(orc, Wu, su, X).astype(np.float64)

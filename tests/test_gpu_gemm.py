@@ -110,7 +110,7 @@ def test_gemm_bf16_vs_oracle(gpu, orc, m, n, T):
         assert rel_l2(Y[t], yo) <= REL_L2
 
 
-def _time_gemm(lin, X, epi, split=4, frag_out=None):
+def _time_gemm(lin, X, epi, split=4, frag_out=None, ss_in=None):
     """One launch through rl_hip_time_gemm_fp8 (iters=1): exposes the split-K and
     SwiGLU epilogues the engine uses on the real GEMM kernel."""
     import ctypes as C
@@ -122,12 +122,14 @@ def _time_gemm(lin, X, epi, split=4, frag_out=None):
     xd = DeviceBuffer.from_numpy(np.ascontiguousarray(X, np.float32))
     frag = ops.act_frag_buffer(n, T)
     call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
-    rows = split * T * m if epi == 3 else T * (m // 2 if epi == 2 else m)
+    rows = split * T * m if epi == 3 else T * (m // 2 if epi in (2, 5) else m)
     yd = DeviceBuffer(4 * rows)
     yd.zero()
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
-    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, None, None, None, m, n, T, epi,
+    ssd = DeviceBuffer.from_numpy(np.ascontiguousarray(ss_in, np.float32)) if ss_in is not None else None
+    call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, frag_out, None, None, None,
+         ssd.ptr if ssd else None, m, n, T, epi,
          split, 1, None, C.byref(ms))
     return yd.numpy(np.float32, (rows,))
 
@@ -219,7 +221,7 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
     call("rl_hip_time_gemm_fp8", ptrs, 1, lin.ts.ptr, frag.ptr, yd.ptr, fo.ptr, gd.ptr, ssd.ptr,
-         bsd.ptr if bsd else None, m, n, T, 4, 1, 1, None, C.byref(ms))
+         bsd.ptr if bsd else None, None, m, n, T, 4, 1, 1, None, C.byref(ms))
     x = yd.numpy(np.float32, (T, m)).astype(np.float64)
     want = x0.astype(np.float64) + orc.gemm_fp8(W, s, Xin)
     for t in range(T):
@@ -229,3 +231,54 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
     fr = _unpack_frag(fo.numpy(np.uint8, (fo.nbytes,)), m, T)
     xg = x * (1.0 + gamma.astype(np.float64))
     assert np.all(np.abs(fr - xg) <= 2.0 ** -15 * np.abs(xg) + 1e-30)
+
+
+@pytest.mark.parametrize("T,I", [(1, 512), (3, 520), (4, 256), (6, 136)])
+def test_gemm_fp8_swiglu_half_tiles(gpu, orc, T, I):
+    """The engine's gate/up packing (rl_hip_pack_fp8_gate_up: tile k = gate rows
+    8k..8k+7 then up rows 8k..8k+7, a block scale per half) with the SwiGLU epilogue
+    5: h = silu(gate . x) * (up . x) against the oracle, gate and up with independent
+    block scales.  I = 520 and 136 end in a partial 128-row scale block and give an
+    odd tile count; T = 6 takes the runtime-T kernel."""
+    r = synth.rng(700 + T + I)
+    n = 1024
+    Wg, Wu = synth.fp8_weight(r, I, n), synth.fp8_weight(r, I, n)
+    sg, su = synth.fp8_scales(r, I, n), synth.fp8_scales(r, I, n)
+    lin = ops.Fp8GateUp(Wg, sg, Wu, su)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    Hh = _time_gemm(lin, X, 5).reshape(T, I)
+    for t in range(T):
+        g = orc.gemv_fp8(Wg, sg, X[t]).astype(np.float64)
+        u = orc.gemv_fp8(Wu, su, X[t]).astype(np.float64)
+        want = g / (1.0 + np.exp(-g)) * u
+        assert rel_l2(Hh[t], want) <= REL_L2, (t, rel_l2(Hh[t], want))
+
+
+@pytest.mark.parametrize("T", [1, 2, 4, 5])
+@pytest.mark.parametrize("epi", [0, 5])
+def test_gemm_fp8_folded_norm_input(gpu, orc, T, epi):
+    """Store and half-tile SwiGLU launches that read the residual stream's sums of
+    squares (as the previous add-norm launch writes them: [ceil(n/32)][T]) and scale
+    each token's products by 1/sqrt(sum / n + 1e-6): the RMSNorm folded into the
+    consuming GEMM, its gamma already in the weights (ops.cpp:389-402 rmsnorm, then
+    ops::linear)."""
+    r = synth.rng(900 + 10 * T + epi)
+    n = 1536
+    X = r.standard_normal((T, n)).astype(np.float32)
+    ss = (r.random(((n + 31) // 32, T)) * 40 + 1).astype(np.float32)
+    sc = 1.0 / np.sqrt(ss.astype(np.float64).sum(0) / n + 1e-6)  # [t]
+    if epi == 0:
+        m = 384
+        W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n)
+        Y = _time_gemm(ops.Fp8Linear(W, s), X, 0, ss_in=ss).reshape(T, m)
+        want = orc.gemm_fp8(W, s, X).astype(np.float64) * sc[:, None]
+    else:
+        I = 264
+        Wg, Wu = synth.fp8_weight(r, I, n), synth.fp8_weight(r, I, n)
+        sg, su = synth.fp8_scales(r, I, n), synth.fp8_scales(r, I, n)
+        Y = _time_gemm(ops.Fp8GateUp(Wg, sg, Wu, su), X, 5, ss_in=ss).reshape(T, I)
+        g = orc.gemm_fp8(Wg, sg, X).astype(np.float64) * sc[:, None]
+        u = orc.gemm_fp8(Wu, su, X).astype(np.float64) * sc[:, None]
+        want = g / (1.0 + np.exp(-g)) * u
+    for t in range(T):
+        assert rel_l2(Y[t], want[t]) <= REL_L2, (t, rel_l2(Y[t], want[t]))

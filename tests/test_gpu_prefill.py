@@ -30,6 +30,24 @@ def test_gemm_prefill_vs_oracle(gpu, orc, m, n, T):
         assert rel_l2(Y[t], Yo[t]) <= REL_L2, (m, n, T, t, rel_l2(Y[t], Yo[t]))
 
 
+@pytest.mark.parametrize("T,I", [(70, 256), (200, 520)])
+def test_gemm_prefill_swiglu_half_tiles(gpu, orc, T, I):
+    """Prefill SwiGLU (epilogue 5) over the engine's half-tile gate/up packing,
+    gate and up with independent block scales; I = 520 ends in a partial 128-row
+    scale block."""
+    r = synth.rng(43 + I)
+    n = 768
+    Wg, Wu = synth.fp8_weight(r, I, n), synth.fp8_weight(r, I, n)
+    sg, su = synth.fp8_scales(r, I, n), synth.fp8_scales(r, I, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    g = orc.gemm_fp8(Wg, sg, X).astype(np.float64)
+    u = orc.gemm_fp8(Wu, su, X).astype(np.float64)
+    want = g / (1.0 + np.exp(-g)) * u
+    got = ops.linear_prefill(ops.Fp8GateUp(Wg, sg, Wu, su), X, epilogue=5)
+    for t in range(T):
+        assert rel_l2(got[t], want[t]) <= REL_L2, (t, rel_l2(got[t], want[t]))
+
+
 def test_gemm_prefill_add_and_swiglu(gpu, orc):
     r = synth.rng(41)
     T, n, I = 70, 768, 256
