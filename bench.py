@@ -134,7 +134,7 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
     reported beside it as "warm_us"."""
     import ctypes as C
 
-    from rapidllm_amd import ops, synth
+    from rapidllm_amd import hip, ops, synth
     from rapidllm_amd.hip import DeviceBuffer, call
 
     r = synth.rng(5)
@@ -160,10 +160,11 @@ def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
         yd = DeviceBuffer(4 * T * m * SPLIT)
         fo = ops.act_frag_buffer(m // 2 if epi == EPI_SWIGLU_H else m, T) if epi in (EPI_SWIGLU_H, EPI_ADDNORM) else None
         gam = DeviceBuffer.from_numpy(np.zeros(m, np.float32))
-        ssq = DeviceBuffer(4 * T * ((m + 31) // 32))
+        G = hip.lib().rl_hip_norm_group_rows()
+        ssq = DeviceBuffer(4 * T * ((m + G - 1) // G))
         bss = DeviceBuffer.from_numpy(np.full((n // 128) * T * 4, 32.0, np.float32)) if block_scale else None
         folded = epi in (EPI_STORE, EPI_SWIGLU_H) and n == spec.hidden
-        ssi = DeviceBuffer.from_numpy(np.full((n + 31) // 32 * T, 32.0, np.float32)) if folded else None
+        ssi = DeviceBuffer.from_numpy(np.full((n + G - 1) // G * T, 32.0 * G / 32, np.float32)) if folded else None
         yd.zero(s)
         call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, s)
         ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])

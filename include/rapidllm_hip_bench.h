@@ -53,14 +53,19 @@ int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
  * next linear's fragments to frag_out (act_frag_bytes(m/2, T)), 5 the same over the
  * rl_hip_pack_fp8_gate_up half tiles (tile scales [m/16][kb][2]), 4 residual add with
  * the next RMSNorm's data (Y [T][m] += result; frag_out = fragments of Y * (1 + gamma),
- * act_frag_bytes(m, T); sumsq [ceil(m/32)][T] = per-32-row sums of squares).
+ * act_frag_bytes(m, T); sumsq [ceil(m/G)][T] = sums of squares per G rows,
+ * G = rl_hip_norm_group_rows()).
  * block_sumsq (add-norm only, may be null): [n/128][T][4] partial sums of squares of
  * the input per 128-column block, each block's products then scaled per token by
  * 1/sqrt(sum/128 + 1e-6) (the DeltaNet out_proj's folded gated RMSNorm).
  * sumsq_in (store / SwiGLU only, may be null): the input's sums of squares as an
- * add-norm launch writes them for an n-row output ([ceil(n/32)][T]); the products
+ * add-norm launch writes them for an n-row output ([ceil(n/G)][T]); the products
  * are then scaled per token by 1/sqrt(sum/n + 1e-6) (the folded RMSNorm of the
  * GEMMs that read the residual stream). */
+/* Rows per partial sum-of-squares group written by the add-norm epilogue (the
+ * residual GEMM's rows per workgroup).  No counterpart in the reference. */
+int rl_hip_norm_group_rows(void);
+
 int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
                          float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
                          const float* sumsq_in, int m, int n, int T, int epilogue, int split, int iters,

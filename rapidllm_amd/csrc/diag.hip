@@ -67,6 +67,8 @@ int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream) {
     });
 }
 
+int rl_hip_norm_group_rows(void) { return norm_group_rows(); }
+
 int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
                          float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
                          const float* sumsq_in, int m, int n, int T, int epilogue, int split, int iters,

@@ -796,6 +796,7 @@ void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n,
     launch_gemm<false>(W, nullptr, frag, Y, m, n, T, epi, ldy, m_valid, s, S, frag_out, norm);
 }
 int add_norm_groups(int m) { return (m_tiles_of(m) + 1) / 2; }
+int norm_group_rows() { return 2 * kTileRows; }
 bool gemm_store_pairs_rows() { return !(bperm_enabled() && !g_force.rt); }
 int device_cus() {
     static int cus[64] = {0};

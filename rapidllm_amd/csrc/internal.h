@@ -48,6 +48,7 @@ void gemm_fp8_frag(const uint8_t* W, const float* ts, const void* frag, float* Y
 void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n, int T, int epi, int ldy, int m_valid,
                     hipStream_t s, int S = 1, void* frag_out = nullptr, const NormIO* norm = nullptr);
 int add_norm_groups(int m);
+int norm_group_rows();  // rows per add-norm sum-of-squares group
 // true when FP8 store launches give each workgroup two row tiles (then the
 // DeltaNet in_proj's overflow rows are worth computing as K-slices)
 bool gemm_store_pairs_rows();

@@ -24,7 +24,7 @@ from concurrent.futures import ThreadPoolExecutor
 import numpy as np
 import pytest
 
-from rapidllm_amd import ops, synth
+from rapidllm_amd import hip, ops, synth
 from rapidllm_amd.hip import DeviceBuffer, call
 
 pytestmark = pytest.mark.gpu
@@ -82,7 +82,8 @@ def run_epilogue(lin, X, epi, x0=None, gamma=None, block_sumsq=None):
     yd = DeviceBuffer.from_numpy(x0) if x0 is not None else DeviceBuffer(4 * T * mo)
     fo = ops.act_frag_buffer(mo, T) if epi in (2, 4, 5) else None
     gd = DeviceBuffer.from_numpy(gamma) if gamma is not None else None
-    ssd = DeviceBuffer(4 * T * (m // 32)) if epi == 4 else None
+    G = hip.lib().rl_hip_norm_group_rows()
+    ssd = DeviceBuffer(4 * T * (m // G)) if epi == 4 else None
     bsd = DeviceBuffer.from_numpy(block_sumsq) if block_sumsq is not None else None
     ptrs = (C.c_void_p * 1)(lin.w.ptr)
     ms = C.c_float()
@@ -90,7 +91,7 @@ def run_epilogue(lin, X, epi, x0=None, gamma=None, block_sumsq=None):
          gd.ptr if gd else None, ssd.ptr if ssd else None, bsd.ptr if bsd else None, None, m, n, T, epi, 1, 1, None,
          C.byref(ms))
     y = None if epi in (2, 5) else yd.numpy(np.float32, (T, mo))
-    ss = ssd.numpy(np.float32, (m // 32, T)) if ssd else None
+    ss = ssd.numpy(np.float32, (m // G, T)) if ssd else None
     fr = fo.numpy(np.uint8, (fo.nbytes,)) if fo else None
     return y, fr, ss
 
@@ -141,7 +142,7 @@ def test_c3_gate_up_swiglu(gpu, orc, T):
                                                 ("attn_o", ZD, False)])
 def test_c3_residual_linears(gpu, orc, name, n, block_scale, T):
     """x += W . a in place, the next linear's fragments of x * (1 + gamma) and the
-    per-32-row sums of x^2 (the folded RMSNorm's data).  out_proj also applies the
+    sums of x^2 per row group (the folded RMSNorm's data).  out_proj also applies the
     DeltaNet gated RMSNorm's per-(head, token) 1/rms to its 128-column blocks."""
     r = synth.rng(0xC3B + n + T + block_scale)
     W, s = synth.fp8_weight(r, H, n), synth.fp8_scales(r, H, n)
@@ -159,7 +160,8 @@ def test_c3_residual_linears(gpu, orc, name, n, block_scale, T):
     for t in range(T):
         assert rel_l2(x[t], want[t]) <= REL_L2, (name, t, rel_l2(x[t], want[t]))
     x64 = x.astype(np.float64)
-    assert np.allclose(ss.astype(np.float64), (x64 ** 2).reshape(T, H // 32, 32).sum(2).T, rtol=1e-5)
+    G = hip.lib().rl_hip_norm_group_rows()
+    assert np.allclose(ss.astype(np.float64), (x64 ** 2).reshape(T, H // G, G).sum(2).T, rtol=1e-5)
     xg = x64 * (1.0 + gamma.astype(np.float64))
     assert np.all(np.abs(unpack_frag(fr, H, T) - xg) <= 2.0 ** -15 * np.abs(xg) + 1e-30)
 

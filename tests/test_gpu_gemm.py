@@ -6,7 +6,7 @@ relative L2 of the reference CPU result.
 import numpy as np
 import pytest
 
-from rapidllm_amd import ops, synth
+from rapidllm_amd import hip, ops, synth
 
 pytestmark = pytest.mark.gpu
 
@@ -189,7 +189,7 @@ def _unpack_frag(raw, n, T):
 @pytest.mark.parametrize("T,block_scale", [(1, False), (4, False), (1, True), (4, True)])
 def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
     """Residual GEMM fused with the next RMSNorm's data: x += W.a in place,
-    fragments of x * (1 + gamma) for the next linear, and sum of x^2 per 32 rows.
+    fragments of x * (1 + gamma) for the next linear, and sum of x^2 per row group.
     block_scale: the input's 128-column blocks are scaled per token by
     1/sqrt(sum/128 + 1e-6) of four given partial sums (the DeltaNet out_proj's
     folded gated RMSNorm)."""
@@ -210,7 +210,8 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
     yd = DeviceBuffer.from_numpy(x0)
     fo = ops.act_frag_buffer(m, T)
     gd = DeviceBuffer.from_numpy(gamma)
-    ssd = DeviceBuffer(4 * T * (m // 32))
+    G = hip.lib().rl_hip_norm_group_rows()
+    ssd = DeviceBuffer(4 * T * (m // G))
     Xin = X
     bsd = None
     if block_scale:
@@ -226,8 +227,8 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
     want = x0.astype(np.float64) + orc.gemm_fp8(W, s, Xin)
     for t in range(T):
         assert rel_l2(x[t], want[t]) <= REL_L2
-    ss = ssd.numpy(np.float32, (m // 32, T)).astype(np.float64)
-    assert np.allclose(ss, (x ** 2).reshape(T, m // 32, 32).sum(2).T, rtol=1e-5)
+    ss = ssd.numpy(np.float32, (m // G, T)).astype(np.float64)
+    assert np.allclose(ss, (x ** 2).reshape(T, m // G, G).sum(2).T, rtol=1e-5)
     fr = _unpack_frag(fo.numpy(np.uint8, (fo.nbytes,)), m, T)
     xg = x * (1.0 + gamma.astype(np.float64))
     assert np.all(np.abs(fr - xg) <= 2.0 ** -15 * np.abs(xg) + 1e-30)
@@ -265,7 +266,8 @@ def test_gemm_fp8_folded_norm_input(gpu, orc, T, epi):
     r = synth.rng(900 + 10 * T + epi)
     n = 1536
     X = r.standard_normal((T, n)).astype(np.float32)
-    ss = (r.random(((n + 31) // 32, T)) * 40 + 1).astype(np.float32)
+    G = hip.lib().rl_hip_norm_group_rows()
+    ss = (r.random(((n + G - 1) // G, T)) * 40 + 1).astype(np.float32)
     sc = 1.0 / np.sqrt(ss.astype(np.float64).sum(0) / n + 1e-6)  # [t]
     if epi == 0:
         m = 384
