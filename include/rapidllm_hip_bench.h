@@ -45,6 +45,10 @@ int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms);
 int rl_hip_copy_probe(const void* src, void* dst, size_t bytes, void* stream);
 int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
 
+/* Rows per partial sum-of-squares group written by the add-norm epilogue (the
+ * residual GEMM's rows per workgroup).  No counterpart in the reference. */
+int rl_hip_norm_group_rows(void);
+
 /* GEMM timing (no counterpart in the reference): `iters` back-to-back launches of the
  * block-FP8 GEMM on `stream`, launch i reading weight copy i % n_copies (so weights
  * come from HBM, not from the Infinity Cache), with one event pair around the loop;
@@ -62,10 +66,6 @@ int rl_hip_read_probe(const void* src, size_t bytes, void* out4, void* stream);
  * add-norm launch writes them for an n-row output ([ceil(n/G)][T]); the products
  * are then scaled per token by 1/sqrt(sum/n + 1e-6) (the folded RMSNorm of the
  * GEMMs that read the residual stream). */
-/* Rows per partial sum-of-squares group written by the add-norm epilogue (the
- * residual GEMM's rows per workgroup).  No counterpart in the reference. */
-int rl_hip_norm_group_rows(void);
-
 int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float* tile_scales, const void* frag,
                          float* Y, void* frag_out, const float* gamma, float* sumsq, const float* block_sumsq,
                          const float* sumsq_in, int m, int n, int T, int epilogue, int split, int iters,
