@@ -476,6 +476,7 @@ def main():
     ap.add_argument("--layers", type=int, default=64)
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only the block-FP8 GEMM launch mix (the roofline kernel), for counter runs")
+    ap.add_argument("--gemm-tokens", type=int, default=1, help="tokens per GEMM launch with --gemm-only (1..4)")
     ap.add_argument("--prefill-only", type=int, default=0,
                     help="time only a prompt prefill of this many tokens (for kernel traces)")
     ap.add_argument("--configs-only", action="store_true",
@@ -500,7 +501,7 @@ def main():
         copy_probe(args.copy_probe_mb)
         return
     if args.gemm_only:
-        g_ms, g_bytes, per = measure_gemm(spec, 1, iters=args.steps)
+        g_ms, g_bytes, per = measure_gemm(spec, args.gemm_tokens, iters=args.steps)
         print(json.dumps({"avg_launch_us": round(g_ms * 1e3, 2), "bytes_per_launch": int(g_bytes), "shapes": per}))
         return
     if args.configs_only:
