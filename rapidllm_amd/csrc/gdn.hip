@@ -485,7 +485,12 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     // q = (q * 1/|q|) * 1/sqrt(dk), k = k * 1/|k| (eps 1e-6 inside the root)
     const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
     const bool rec_k = keep && cc == 0 && jj == 0;  // one writer of the per-head k and g records
-    for (int t = 0; t < T; ++t) {
+    // unrolled over the token bound: the next token's LDS reads, norms and gates and
+    // the previous token's output work are independent of the state chain, and the
+    // compiler interleaves them with it
+#pragma unroll
+    for (int t = 0; t < kMaxT; ++t) {
+        if (t >= T) break;
         const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t] + red_s[1][t]) + 1e-6f);
         const float ik = 1.f / sqrtf(static_cast<float>(red_s[2][t] + red_s[3][t]) + 1e-6f);
         const float g = gate_s[t][0], beta = gate_s[t][1];
