@@ -899,18 +899,20 @@ class Engine {
             }
         }
         gss_ = mem_.get_n<float>(static_cast<size_t>(nv) * tcap_ * 4);
-        // in_proj = [qkv; z; a; b]: when its row-tile pairs overflow two workgroups per
-        // CU and the overflow is the a/b block, the a/b rows are computed as K-slices
+        // in_proj = [qkv; z; a; b]: when the qkv and z rows fill whole rounds of two
+        // workgroups per CU and the a/b block would run as a short round of its own,
+        // the a/b rows are computed as K-slices by the first workgroups
         if (gdn_fused_norm_ && nd > 0) {
             const Layer* d0 = nullptr;
             for (const Layer& Ly : L_)
                 if (Ly.kind == RL_LAYER_DELTA) d0 = &Ly;
             const int m_tiles = d0->in_parts[0].m / 16, n_kb = (H + 127) / 128;
             const int tile0 = d0->off_a / 16;
-            if (gemm_store_pairs_rows() && d0->in_parts[0].kind == RL_Q_FP8_E4M3_B128 && m_tiles / 2 > 2 * device_cus() &&
-                d0->off_a % 32 == 0 &&
-                tile0 / 2 <= 2 * device_cus() && (m_tiles - tile0) * kAbSlices <= tile0 / 2 &&
-                (n_kb + kAbSlices - 1) / kAbSlices <= 8 && d0->in_width == m_tiles * 16) {
+            const int rpw = gemm_store_rows_per_wg(), slots = 2 * device_cus();
+            const int wg0 = tile0 / rpw;
+            if (d0->in_parts[0].kind == RL_Q_FP8_E4M3_B128 && tile0 < m_tiles && d0->off_a % (16 * rpw) == 0 &&
+                wg0 % slots == 0 && (m_tiles - tile0) * kAbSlices <= wg0 &&
+                (n_kb + kAbSlices - 1) / kAbSlices <= gemm_store_waves() && d0->in_width == m_tiles * 16) {
                 ab_tile0_ = tile0;
                 ab_rows_ = (m_tiles - tile0) * 16;
                 abpart_ = mem_.get_n<float>(static_cast<size_t>(kAbSlices) * tcap_ * ab_rows_);

@@ -750,14 +750,23 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     }
     if (io.xpart) {
         // the rows from x_tile0 on as K-slices run by the first workgroups
+        // (the store work split: two row tiles per 8 waves, or one per 16 waves with
+        // the permuted-B kernels; one column block per wave in a slice)
         RL_REQUIRE(epilogue == kStore && S == 1 && !g_force.rt && !io.kss, RL_ERR_RANGE,
                    "gemm: overflow slices need a plain store launch");
-        RL_REQUIRE(io.x_tile0 > 0 && io.x_tile0 % 2 == 0 && io.x_tile0 < m_tiles && io.x_slices >= 1 &&
-                       io.x_rows == (m_tiles - io.x_tile0) * kTileRows && (n_kb + io.x_slices - 1) / io.x_slices <= 8 &&
-                       (m_tiles - io.x_tile0) * io.x_slices <= io.x_tile0 / 2,
+        const int rpw = gemm_store_rows_per_wg(), waves = gemm_store_waves();
+        RL_REQUIRE(kFp8 || rpw == 2, RL_ERR_UNSUPPORTED, "gemm: overflow slices with BF16 need the paired split");
+        RL_REQUIRE(io.x_tile0 > 0 && io.x_tile0 % rpw == 0 && io.x_tile0 < m_tiles && io.x_slices >= 1 &&
+                       io.x_rows == (m_tiles - io.x_tile0) * kTileRows &&
+                       (n_kb + io.x_slices - 1) / io.x_slices <= waves &&
+                       (m_tiles - io.x_tile0) * io.x_slices <= io.x_tile0 / rpw,
                    RL_ERR_RANGE, "gemm: bad overflow slices");
-        launch_gemm_cfg<kFp8, 2, 8, 1>(W, tscale, frag, Y, io.x_tile0 * kTileRows, n_kb, T, epilogue, ldy,
-                                       std::min(m_valid, io.x_tile0 * kTileRows), S, frag_out, io, s);
+        if (rpw == 2)
+            launch_gemm_cfg<kFp8, 2, 8, 1>(W, tscale, frag, Y, io.x_tile0 * kTileRows, n_kb, T, epilogue, ldy,
+                                           std::min(m_valid, io.x_tile0 * kTileRows), S, frag_out, io, s);
+        else
+            launch_gemm_cfg<kFp8, 1, 16, 1>(W, tscale, frag, Y, io.x_tile0 * kTileRows, n_kb, T, epilogue, ldy,
+                                            std::min(m_valid, io.x_tile0 * kTileRows), S, frag_out, io, s);
         check_launch("gemm_frag_kernel");
         return;
     }
@@ -797,7 +806,9 @@ void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n,
 }
 int add_norm_groups(int m) { return (m_tiles_of(m) + 1) / 2; }
 int norm_group_rows() { return 2 * kTileRows; }
-bool gemm_store_pairs_rows() { return !(bperm_enabled() && !g_force.rt); }
+static bool store_pairs_rows() { return !(bperm_enabled() && !g_force.rt); }
+int gemm_store_rows_per_wg() { return store_pairs_rows() ? 2 : 1; }
+int gemm_store_waves() { return store_pairs_rows() ? 8 : 16; }
 int device_cus() {
     static int cus[64] = {0};
     int dev = 0;

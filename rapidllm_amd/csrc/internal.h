@@ -49,9 +49,10 @@ void gemm_bf16_frag(const uint16_t* W, const void* frag, float* Y, int m, int n,
                     hipStream_t s, int S = 1, void* frag_out = nullptr, const NormIO* norm = nullptr);
 int add_norm_groups(int m);
 int norm_group_rows();  // rows per add-norm sum-of-squares group
-// true when FP8 store launches give each workgroup two row tiles (then the
-// DeltaNet in_proj's overflow rows are worth computing as K-slices)
-bool gemm_store_pairs_rows();
+// FP8 store launches (T <= 4): row tiles and waves per workgroup (two workgroups
+// per CU are resident either way)
+int gemm_store_rows_per_wg();
+int gemm_store_waves();
 
 // prefill.hip: Y = W . X for T (any) tokens on MFMA; epi store / add / SwiGLU
 // (interleaved gate/up tiles, m_valid = m/2 output rows).  frag: act fragments of T.
