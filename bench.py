@@ -376,6 +376,7 @@ def cpu_configs(spec, budget_s=6.0):
     out["c4"] = {"us_per_layer": round(us, 1), "all_layers_us": round(us * n_d, 1),
                  "cores": threads if R is not None else 1, "kind": kind, "runs": k,
                  "what": "4 x (ops::conv1d_update 10240 ch + ops::delta_recurrent_step_simd 48 heads) per layer"}
+    out["host"] = host_info(R)
     return out
 
 
@@ -425,6 +426,32 @@ def measured_traffic():
     return None
 
 
+def host_info(R=None):
+    """The host the CPU lines ran on: logical CPUs (and those this process may use),
+    the CPU model string, and the SIMD path the reference's runtime dispatch picked
+    (cpu_caps.cpp: AVX-512 F/DQ/BW/VL, else AVX2 + FMA, else scalar)."""
+    import ctypes as C
+
+    model, flags = "unknown", set()
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name") and model == "unknown":
+                    model = line.split(":", 1)[1].strip()
+                elif line.startswith("flags") and not flags:
+                    flags = set(line.split(":", 1)[1].split())
+    except OSError:
+        pass
+    if R is not None:
+        R.ref_simd_name.restype = C.c_char_p
+        isa = R.ref_simd_name().decode()
+    else:
+        isa = ("avx512f+dq+bw+vl" if {"avx512f", "avx512dq", "avx512bw", "avx512vl"} <= flags
+               else "avx2+fma" if {"avx2", "fma"} <= flags else "scalar") + " (from /proc/cpuinfo)"
+    return {"nproc": os.cpu_count(), "usable_cpus": len(os.sched_getaffinity(0)), "cpu_model": model,
+            "reference_isa": isa}
+
+
 def cpu_baseline(spec, sbytes_total, budget_s=20.0):
     """The reference's own CPU decode path (oracle/_ref: ops_fused.cpp
     fused_mlp_decode -> scalar gemv_fp8, the reference's only FP8 CPU GEMV, 1
@@ -461,7 +488,7 @@ def cpu_baseline(spec, sbytes_total, budget_s=20.0):
     t_med = float(np.median(times))
     sample_bytes = wg.nbytes + wu.nbytes + wd.nbytes + 4 * (sg.size + su.size + sd.size)
     sec_per_tok = t_med * sbytes_total / sample_bytes
-    return {"value": round(1.0 / sec_per_tok, 6), "unit": "tok/s", "cores": 1, "kind": kind,
+    return {"value": round(1.0 / sec_per_tok, 6), "unit": "tok/s", "cores": 1, "kind": kind, "host": host_info(R),
             "sample": f"fused_mlp_decode of one 27B layer (3 block-FP8 GEMVs, {sample_bytes/1e6:.0f} MB) "
                       f"median of {len(times)} runs = {t_med:.2f} s, scaled by bytes to the "
                       f"{sbytes_total/1e9:.2f} GB T=1 step; scalar gemv_fp8 is single-threaded in the reference"}
