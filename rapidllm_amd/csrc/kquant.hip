@@ -43,6 +43,10 @@ using namespace rl;
 namespace {
 
 constexpr int kTR = 16;       // rows per tile
+// Work split: keep >= ~512 workgroups where the row groups alone are too few, and a
+// K-slice short enough for the LDS fragments of four tokens (so the split, and
+// with it every token's summation order, does not depend on T).
+constexpr int kKqMaxSlice = 12;
 
 template <int QT>
 struct KFmt;
@@ -218,7 +222,29 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         // items (set, sbl, mi, g, token-in-set): 8 x values split into bf16 hi + mid,
         // and their sum (hi + mid, fixed order) as one run of the sub-block's sum
         const int items = NSET * P * 8 * 4 * 2;
-        for (int it = threadIdx.x; it < items; it += 64 * RW) {
+        // at most kPer items per thread: every item's two x loads are issued before
+        // the first item is processed (one memory round trip for the whole build)
+        constexpr int kPer = (NSET * kKqMaxSlice * 8 * 4 * 2 + 64 * RW - 1) / (64 * RW);
+        float4 va[kPer], vb[kPer];
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int it = threadIdx.x + k * 64 * RW;
+            const int tt = it & 1, gg = (it >> 1) & 3, mi = (it >> 3) & 7;
+            const int sbl = (it >> 6) % P, set = (it >> 6) / P;
+            const int t = 2 * set + tt;
+            va[k] = make_float4(0.f, 0.f, 0.f, 0.f);
+            vb[k] = va[k];
+            if (it < items && t < T && sbl < nsl) {
+                const float4* px = reinterpret_cast<const float4*>(
+                    x + static_cast<size_t>(t) * n + static_cast<size_t>(s0 + sbl) * 256 + x_off<QT>(gg, mi));
+                va[k] = px[0];
+                vb[k] = px[1];
+            }
+        }
+#pragma unroll
+        for (int k = 0; k < kPer; ++k) {
+            const int it = threadIdx.x + k * 64 * RW;
+            if (it >= items) break;
             const int tt = it & 1, gg = (it >> 1) & 3, mi = (it >> 3) & 7;
             const int sbl = (it >> 6) % P, set = (it >> 6) / P;
             const int t = 2 * set + tt;
@@ -228,10 +254,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
             } hi, mid;
             float run = 0.f;
             if (t < T && sbl < nsl) {
-                const float* px = x + static_cast<size_t>(t) * n + static_cast<size_t>(s0 + sbl) * 256 + x_off<QT>(gg, mi);
-                const float4 a = reinterpret_cast<const float4*>(px)[0];
-                const float4 b = reinterpret_cast<const float4*>(px)[1];
-                const float v[8] = {a.x, a.y, a.z, a.w, b.x, b.y, b.z, b.w};
+                const float v[8] = {va[k].x, va[k].y, va[k].z, va[k].w, vb[k].x, vb[k].y, vb[k].z, vb[k].w};
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     split_bf16(v[e], hi.h[e], mid.h[e]);
@@ -392,18 +415,35 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         }
         __syncthreads();
         if (!s_last) return;
-        if (own)
+        if (own) {
+            // every token's partials of 8 slices requested together (one memory
+            // round trip per 8 slices, not one per slice and token), then added in
+            // slice order
+            float v[T];
+            float y0[T];
+#pragma unroll
             for (int t = 0; t < T; ++t) {
-                float v = 0.f;
-                for (int q = 0; q < S; ++q)
-                    v += __hip_atomic_load(partial + (static_cast<size_t>(q) * T + t) * m + row, __ATOMIC_RELAXED,
-                                           __HIP_MEMORY_SCOPE_AGENT);
-                float* dst = Y + static_cast<size_t>(t) * ldy + row;
-                if (accumulate)
-                    *dst += v;
-                else
-                    *dst = v;
+                v[t] = 0.f;
+                y0[t] = accumulate ? Y[static_cast<size_t>(t) * ldy + row] : 0.f;
             }
+            for (int q0 = 0; q0 < S; q0 += 8) {
+                float pv[T][8];
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        pv[t][j] = q0 + j < S ? __hip_atomic_load(partial + (static_cast<size_t>(q0 + j) * T + t) * m + row,
+                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                              : 0.f;
+#pragma unroll
+                for (int t = 0; t < T; ++t)
+#pragma unroll
+                    for (int j = 0; j < 8; ++j)
+                        if (q0 + j < S) v[t] += pv[t][j];
+            }
+#pragma unroll
+            for (int t = 0; t < T; ++t) Y[static_cast<size_t>(t) * ldy + row] = accumulate ? y0[t] + v[t] : v[t];
+        }
         return;
     }
     if (own)
@@ -506,10 +546,6 @@ size_t kq_tiled_bytes(int qt, int m, int n) {
     return static_cast<size_t>((m + kTR - 1) / kTR) * (n / 256) * tile;
 }
 
-// Work split: keep >= ~512 workgroups where the row groups alone are too few, and a
-// K-slice short enough for the LDS fragments of four tokens (so the split, and
-// with it every token's summation order, does not depend on T).
-constexpr int kKqMaxSlice = 12;
 constexpr int kKqDepth = 4;  // tiles in flight per wave
 // Row tiles (waves) per workgroup.  RL_KQ_RW overrides it for measurement.
 int kq_rw() {
