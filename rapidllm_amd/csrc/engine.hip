@@ -648,6 +648,13 @@ class Engine {
     // GEMMs write x in place plus frag_x_ = fragments of x * (1 + next gamma) and
     // ss_ = per-group sums of x^2; the next GEMM scales its outputs by 1/rms.
     bool fold_norm_ = false;
+    // K-quant models: the residual GEMVs (out_proj / o_proj / down) add into x and
+    // write its per-row-group sums of squares and the next linear's fragments; the
+    // consuming linears fold the RMSNorm (KqNorm / NormIO)
+    bool kq_fold_ = false;
+    float* kq_ss_ = nullptr;  // [kq_norm_groups(H)][Tmax]
+    float* xg_ = nullptr;     // [Tmax][H]: x * (1 + gamma) of the next norm
+    int kq_groups_ = 0;
     bool gdn_fused_norm_ = false;
     void* frag_x_ = nullptr;
     float* ss_ = nullptr;  // [add_norm_groups(H)][Tmax]
@@ -871,6 +878,12 @@ class Engine {
         // RL_FOLD_NORM=0 keeps the separate RMSNorm kernels (for A/B measurement)
         const char* fold_env = std::getenv("RL_FOLD_NORM");
         fold_norm_ = can_fold_norm() && !(fold_env && fold_env[0] == '0');
+        kq_fold_ = !fold_norm_ && can_fold_kquant() && !(fold_env && fold_env[0] == '0');
+        if (kq_fold_) {
+            kq_groups_ = kq_norm_groups(H);
+            kq_ss_ = mem_.get_n<float>(static_cast<size_t>(kq_groups_) * T);
+            xg_ = mem_.get_n<float>(static_cast<size_t>(T) * H);
+        }
         // per-head gated norm (gamma of dv values, zdim >= 256: ops.cpp:129-156) in the
         // DeltaNet kernel, when one workgroup can hold a head
         {
@@ -1355,6 +1368,25 @@ class Engine {
         return true;
     }
 
+    static bool is_kq(const Lin& L) { return L.kind == RL_Q_Q4_K || L.kind == RL_Q_Q6_K; }
+    static bool known_kind(const Lin& L) { return is_kq(L) || frag_kind(L); }
+
+    // K-quant folded norms: every residual linear a K-quant GEMV (one writer per row
+    // of x), every other linear of a known kind, at most 512 row groups of x
+    bool can_fold_kquant() const {
+        if (tmax_ > 4 || !kq_fold_supported() || kq_norm_groups(c_.hidden) > 512 || !known_kind(lm_head_))
+            return false;
+        for (const Layer& Ly : L_) {
+            const Lin& res = Ly.kind == RL_LAYER_DELTA ? Ly.out_proj : Ly.o_proj;
+            if (!is_kq(res) || !is_kq(Ly.down) || res.m != c_.hidden || Ly.down.m != c_.hidden) return false;
+            for (const Lin& L : Ly.kind == RL_LAYER_DELTA ? Ly.in_parts : Ly.qkv_parts)
+                if (!known_kind(L)) return false;
+            if (Ly.gate_up.kind >= 0 ? !frag_kind(Ly.gate_up) : (!is_kq(Ly.gate) || (!Ly.gate_cat && !is_kq(Ly.up))))
+                return false;
+        }
+        return true;
+    }
+
     // FP8 / BF16 GEMM on given input fragments.
     void gemm_on(const Lin& L, const void* fr, float* Y, int ldy, int m_valid, int T, int epi,
                  void* frag_out = nullptr, const NormIO* io = nullptr) {
@@ -1439,9 +1471,108 @@ class Engine {
                sc() + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
     }
 
+    // Linear on the current activation with the folded RMSNorm: K-quant from the fp32
+    // x * (1 + gamma) rows x32 (KqNorm), FP8 / BF16 from frag_ (NormIO).
+    void linear_folded(const Lin& L, const float* x32, float* Y, int ldy, int m_valid, int T, const KqNorm& kn,
+                       const NormIO& io) {
+        if (L.kind == RL_Q_FP8_E4M3_B128)
+            gemm_fp8_frag(L.w, L.ts, frag_, Y, L.m, L.n, T, kEpiStore, ldy, m_valid, st_, 1, nullptr, &io);
+        else if (L.kind == RL_Q_BF16)
+            gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), frag_, Y, L.m, L.n, T, kEpiStore, ldy, m_valid, st_,
+                           1, nullptr, &io);
+        else
+            kq_gemm(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, x32, Y, kq_ws_, kq_ws_bytes_, L.m, L.n, T, 0, ldy, st_, &kn);
+    }
+
+    // One step of a K-quant model with the RMSNorms folded (see kq_fold_): layer 0's
+    // first linears read the normalised rows; from then on the residual GEMVs add
+    // into x in place and leave the sums of squares (and x * (1 + gamma) fragments)
+    // for the next linears.
+    void step_kq_folded(int T, int force_all, bool feed) {
+        const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
+        const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
+        const float eps = c_.rms_eps;
+        float* x = xres_[0];
+        if (feed) copy_int(sc() + kNextTok, tok_, st_);
+        embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, T, st_);
+        rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_, H, T, eps, st_);
+        KqNorm kin;
+        kin.ss_in = kq_ss_;
+        kin.groups_in = kq_groups_;
+        kin.n_norm = H;
+        kin.eps = eps;
+        NormIO io;
+        io.ss_in = kq_ss_;
+        io.groups_in = kq_groups_;
+        io.n_norm = H;
+        io.eps = eps;
+        bool normalised = true;  // xn_ / frag_ hold the normalised rows (layer 0 only)
+        auto consume = [&](const Lin& L, float* Y, int ldy, int m_valid) {
+            if (normalised)
+                linear(L, xn_, Y, ldy, m_valid, T, kEpiStore);
+            else
+                linear_folded(L, xg_, Y, ldy, m_valid, T, kin, io);
+        };
+        auto produce = [&](const Lin& L, const float* a32, const float* gamma_next) {
+            KqNorm kp;
+            kp.ss_out = kq_ss_;
+            kp.gamma_out = gamma_next;
+            kp.xg_out = xg_;
+            kp.frag_out = frag_;
+            kq_gemm(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, a32, x, kq_ws_, kq_ws_bytes_, L.m, L.n, T, 1, H, st_, &kp);
+            normalised = false;
+        };
+        for (int i = 0; i < c_.n_layers; ++i) {
+            Layer& Ly = L_[i];
+            if (Ly.kind == RL_LAYER_DELTA) {
+                for (size_t k = 0; k < Ly.in_parts.size(); ++k)
+                    consume(Ly.in_parts[k], ybuf_ + Ly.in_offs[k], Ly.in_width, Ly.in_parts[k].m);
+                gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
+                           slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_, s_slot_, R_, o_,
+                           T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
+                produce(Ly.out_proj, xn_, Ly.ffn_norm);
+            } else {
+                for (size_t k = 0; k < Ly.qkv_parts.size(); ++k)
+                    consume(Ly.qkv_parts[k], ybuf_ + Ly.qkv_offs[k], Ly.qkv_width, Ly.qkv_parts[k].m);
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot), ctx_,
+                                  sc() + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                                  attn_ws_bytes_, xn_, frag_, st_);
+                produce(Ly.o_proj, xn_, Ly.ffn_norm);
+            }
+            if (Ly.gate_up.kind >= 0) {
+                // fused FP8 / BF16 gate/up reading x * (1 + gamma) fragments; the K-quant
+                // down reads fp32 h
+                if (Ly.gate_up.kind == RL_Q_FP8_E4M3_B128)
+                    gemm_fp8_frag(Ly.gate_up.w, Ly.gate_up.ts, frag_, h_, Ly.gate_up.m, Ly.gate_up.n, T,
+                                  Ly.gate_up.swiglu_epi(), I, I, st_, 1, nullptr, &io);
+                else
+                    gemm_bf16_frag(reinterpret_cast<const uint16_t*>(Ly.gate_up.w), frag_, h_, Ly.gate_up.m,
+                                   Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1, nullptr, &io);
+            } else if (Ly.gate_cat) {
+                consume(Ly.gate, g_, 2 * I, 2 * I);
+                swiglu(g_, 2 * I, g_ + I, 2 * I, h_, I, T, st_);
+            } else {
+                consume(Ly.gate, g_, I, I);
+                consume(Ly.up, u_, I, I);
+                swiglu(g_, I, u_, I, h_, I, T, st_);
+            }
+            produce(Ly.down, h_, i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_);
+        }
+        x_ = x;  // hidden after the layers (pre final norm), for the MTP history
+        consume(lm_head_, logits_, c_.vocab, c_.vocab);
+        argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
+        accept(tok_, preds_, T, force_all, sc() + kPos, sc() + kSlot, R_, sc() + kNCons, sc() + kNextTok, gen_,
+               sc() + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
+    }
+
     void step(int T, int force_all, bool feed) {
         if (fold_norm_) {
             step_folded(T, force_all, feed);
+            return;
+        }
+        if (kq_fold_) {
+            step_kq_folded(T, force_all, feed);
             return;
         }
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;

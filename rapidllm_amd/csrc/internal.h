@@ -70,12 +70,31 @@ void pack_fp8_gate_up(const uint8_t* gw, const float* gs, const uint8_t* uw, con
 void pack_bf16_gate_up(const uint16_t* gw, const uint16_t* uw, uint16_t* dst, int I, int n, hipStream_t s);
 
 // kquant.hip
+// RMSNorm folded across K-quant GEMVs (as NormIO for the FP8 path):
+//   consumer (ss_in): x is the producer's x * (1 + gamma) rows; the outputs are
+//     scaled by 1/sqrt(sum_groups ss_in / n_norm + eps);
+//   producer (ss_out, with accumulate into the residual rows x [T][m]): x += W.a,
+//     ss_out[group][t] = sum of x^2 over the row group's rows (kq_norm_groups(m)
+//     groups, double, stored as float), xg_out [T][m] = x * (1 + gamma_out) and, if
+//     frag_out, the same as the next FP8 / BF16 linear's input fragments.
+struct KqNorm {
+    const float* ss_in = nullptr;
+    int groups_in = 0;
+    int n_norm = 0;
+    float eps = 0.f;
+    float* ss_out = nullptr;
+    const float* gamma_out = nullptr;
+    float* xg_out = nullptr;
+    void* frag_out = nullptr;
+};
+int kq_norm_groups(int m);
+bool kq_fold_supported();  // the folded-norm variants run with the default work split
 size_t kq_workspace_bytes(int m, int n, int T);
 // Host dequantisation of row-major GGML blocks (Q8_0 / Q4_K / Q5_K / Q6_K) with the
 // reference's rounding order (loader.cpp); n = number of values.
 void dequant_host(int quant, const uint8_t* blocks, float* out, int64_t n);
 void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_t ws_bytes, int m, int n, int T,
-             int accumulate, int ldy, hipStream_t s);
+             int accumulate, int ldy, hipStream_t s, const KqNorm* norm = nullptr);
 
 // norms.hip
 void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* frag, int n, int T, float eps,

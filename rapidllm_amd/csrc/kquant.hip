@@ -47,6 +47,7 @@ constexpr int kTR = 16;       // rows per tile
 // K-slice short enough for the LDS fragments of four tokens (so the split, and
 // with it every token's summation order, does not depend on T).
 constexpr int kKqMaxSlice = 12;
+constexpr int kKqMaxSsPerLane = 8;  // folded input norm: up to 512 partial groups
 
 template <int QT>
 struct KFmt;
@@ -164,11 +165,14 @@ __host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
 // last workgroup of the row group adds the S partials in slice order (a fixed
 // order) and writes Y.  Partials and tickets use agent-scope atomic accesses,
 // which are coherent across the XCDs' L2 caches without cache maintenance.
-template <int QT, int T, int D, int RW>
+// NRM: 0 plain; 1 consumer of a folded RMSNorm (outputs scaled by 1/rms from
+// nrm.ss_in); 2 producer (accumulates into the residual rows and writes nrm.ss_out,
+// and the next linear's inputs x * (1 + gamma) as fp32 rows / bf16 fragments).
+template <int QT, int T, int D, int RW, int NRM = 0>
 __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                       float* __restrict__ Y, float* __restrict__ partial,
                                                       unsigned* __restrict__ tickets, int m, int n, int S,
-                                                      int accumulate, int ldy) {
+                                                      int accumulate, int ldy, KqNorm nrm) {
     using F = KFmt<QT>;
     constexpr int NSET = (T + 1) / 2;  // token sets of two (hi, mid, hi, mid columns)
     constexpr int kRuns = QT == 4 ? 4 : 2;
@@ -214,6 +218,17 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     // the first weights are requested before the slice's x fragments are built
 #pragma unroll
     for (int d = 0; d < D; ++d) load(d, s0 + d, s0 + d < s1);
+    // folded input RMSNorm: wave w < T holds token w's partial sums of squares
+    // (group l + 64k in lane l), reduced in the epilogue
+    float ssr[NRM == 1 ? kKqMaxSsPerLane : 1];
+    const bool ss_wave = NRM == 1 && wave < T;
+    if constexpr (NRM == 1) {
+#pragma unroll
+        for (int k = 0; k < kKqMaxSsPerLane; ++k) {
+            const int gi = lane + 64 * k;
+            ssr[k] = ss_wave && gi < nrm.groups_in ? nrm.ss_in[static_cast<size_t>(gi) * T + wave] : 0.f;
+        }
+    }
 
     // ---- x fragments and sub-block sums of this slice
     {
@@ -399,6 +414,15 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     const int row = rt * kTR + r16;
     const bool own = wave_live && g == 0 && row < m;
     __shared__ int s_last;
+    float v[T];
+    // the rows' old values (accumulate) are requested now, so their round trip
+    // overlaps the ticket and the partial loads
+    float y_old[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        v[t] = tot[t];
+        y_old[t] = own && accumulate ? Y[static_cast<size_t>(t) * ldy + row] : 0.f;
+    }
     if (S > 1) {
         if (own)
             for (int t = 0; t < T; ++t)
@@ -419,13 +443,8 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
             // every token's partials of 8 slices requested together (one memory
             // round trip per 8 slices, not one per slice and token), then added in
             // slice order
-            float v[T];
-            float y0[T];
 #pragma unroll
-            for (int t = 0; t < T; ++t) {
-                v[t] = 0.f;
-                y0[t] = accumulate ? Y[static_cast<size_t>(t) * ldy + row] : 0.f;
-            }
+            for (int t = 0; t < T; ++t) v[t] = 0.f;
             for (int q0 = 0; q0 < S; q0 += 8) {
                 float pv[T][8];
 #pragma unroll
@@ -441,19 +460,68 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                     for (int j = 0; j < 8; ++j)
                         if (q0 + j < S) v[t] += pv[t][j];
             }
-#pragma unroll
-            for (int t = 0; t < T; ++t) Y[static_cast<size_t>(t) * ldy + row] = accumulate ? y0[t] + v[t] : v[t];
         }
-        return;
     }
-    if (own)
-        for (int t = 0; t < T; ++t) {
-            float* dst = Y + static_cast<size_t>(t) * ldy + row;
-            if (accumulate)
-                *dst += tot[t];
-            else
-                *dst = tot[t];
+
+    // ---- final write of the row group (one writer per row)
+    __shared__ float s_inv[4];
+    __shared__ double s_sq[4][4];  // [wave][token]
+    if constexpr (NRM == 1) {
+        // folded input norm: token w's 1/rms from its partial sums (groups in order,
+        // then a fixed butterfly)
+        if (ss_wave) {
+            double ss = 0.0;
+#pragma unroll
+            for (int k = 0; k < kKqMaxSsPerLane; ++k) ss += static_cast<double>(ssr[k]);
+            ss = wave_sum_d(ss);
+            if (lane == 0) s_inv[wave] = 1.f / sqrtf(static_cast<float>(ss / nrm.n_norm) + nrm.eps);
         }
+        __syncthreads();
+    }
+    float y[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        y[t] = NRM == 1 ? v[t] * s_inv[t] : v[t];
+        if (own) {
+            y[t] = accumulate ? y_old[t] + y[t] : y[t];
+            Y[static_cast<size_t>(t) * ldy + row] = y[t];
+        }
+    }
+    if constexpr (NRM == 2) {
+        // residual add fused with the next RMSNorm's data: the row group's sum of
+        // x^2 per token (16 rows per wave by a fixed butterfly, the waves in order,
+        // double) and the next linear's inputs x * (1 + gamma): fp32 rows (xg_out) and,
+        // if asked, bf16 fragments
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            double sq = own ? static_cast<double>(y[t]) * y[t] : 0.0;
+#pragma unroll
+            for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, 64);
+            if (lane == 0) s_sq[wave][t] = sq;
+        }
+        if (own) {
+            const float gm = 1.f + nrm.gamma_out[row];
+            uint16_t* f16 = static_cast<uint16_t*>(nrm.frag_out);
+#pragma unroll
+            for (int t = 0; t < T; ++t) {
+                const float xg = y[t] * gm;
+                nrm.xg_out[static_cast<size_t>(t) * m + row] = xg;
+                if (f16) {
+                    uint16_t hi, mid;
+                    split_bf16(xg, hi, mid);
+                    const size_t u = frag_unit(row >> 3, t, T);
+                    f16[u * 8 + (row & 7)] = hi;
+                    f16[(u + T) * 8 + (row & 7)] = mid;
+                }
+            }
+        }
+        __syncthreads();
+        if (static_cast<int>(threadIdx.x) < T) {
+            double sq = 0.0;
+            for (int w = 0; w < RW; ++w) sq += s_sq[w][threadIdx.x];
+            nrm.ss_out[static_cast<size_t>(rgp) * T + threadIdx.x] = static_cast<float>(sq);
+        }
+    }
 }
 
 // Row-major GGUF blocks [m][n/256 * bb] -> tiles.  One thread per (tile, lane).
@@ -568,34 +636,45 @@ void kq_split(int m, int nsb, int& S) {
     S = std::min(S, nsb);
 }
 
-template <int QT, int T, int RW>
+template <int QT, int T, int RW, int NRM>
 void launch_kq_rw(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int S,
-                  int accumulate, int ldy, hipStream_t s) {
+                  int accumulate, int ldy, hipStream_t s, const KqNorm& nrm) {
     const int groups = (m + kTR * RW - 1) / (kTR * RW);
     const int P = (n / 256 + S - 1) / S;
     const size_t lds = kq_lds_bytes<QT>(P, (T + 1) / 2, T);
-    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW>), dim3(groups * S), dim3(64 * RW), lds, s, W, x, Y,
-                       partial, tickets, m, n, S, accumulate, ldy);
+    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW, NRM>), dim3(groups * S), dim3(64 * RW), lds, s, W, x, Y,
+                       partial, tickets, m, n, S, accumulate, ldy, nrm);
 }
 
 template <int QT, int T>
 void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int S,
-                 int accumulate, int ldy, hipStream_t s) {
+                 int accumulate, int ldy, hipStream_t s, const KqNorm& nrm) {
+    // the folded-norm variants use the default work split only
+    if (nrm.ss_in) {
+        RL_REQUIRE(kq_rw() == 4, RL_ERR_UNSUPPORTED, "kquant: folded RMSNorm needs four row tiles per workgroup");
+        launch_kq_rw<QT, T, 4, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+        return;
+    }
+    if (nrm.ss_out) {
+        RL_REQUIRE(kq_rw() == 4, RL_ERR_UNSUPPORTED, "kquant: folded RMSNorm needs four row tiles per workgroup");
+        launch_kq_rw<QT, T, 4, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+        return;
+    }
     switch (kq_rw()) {
-    case 1: launch_kq_rw<QT, T, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
-    case 2: launch_kq_rw<QT, T, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
-    default: launch_kq_rw<QT, T, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    case 1: launch_kq_rw<QT, T, 1, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    case 2: launch_kq_rw<QT, T, 2, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    default: launch_kq_rw<QT, T, 4, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
     }
 }
 
 template <int QT>
 void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int T, int S,
-               int accumulate, int ldy, hipStream_t s) {
+               int accumulate, int ldy, hipStream_t s, const KqNorm& nrm) {
     switch (T) {
-    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
-    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
-    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
-    default: launch_kq_t<QT, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s); break;
+    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    default: launch_kq_t<QT, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
     }
 }
 
@@ -613,9 +692,19 @@ size_t kq_workspace_bytes(int m, int n, int T) {
 }
 
 // Y[T][m] (=, +=) W . x for Q4_K (qt=4) / Q6_K (qt=6) K-tiled weights.
+int kq_norm_groups(int m) { return (m + kTR * kq_rw() - 1) / (kTR * kq_rw()); }
+bool kq_fold_supported() { return kq_rw() == 4; }
+
 void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_t ws_bytes, int m, int n, int T,
-             int accumulate, int ldy, hipStream_t s) {
+             int accumulate, int ldy, hipStream_t s, const KqNorm* norm) {
+    const KqNorm nrm = norm ? *norm : KqNorm{};
     RL_REQUIRE(qt == 4 || qt == 6, RL_ERR_UNSUPPORTED, "kquant: type must be Q4_K or Q6_K");
+    RL_REQUIRE(!nrm.ss_in || (nrm.groups_in >= 1 && nrm.groups_in <= 64 * kKqMaxSsPerLane && nrm.n_norm > 0),
+               RL_ERR_RANGE, "kquant: folded RMSNorm needs 1..512 partial groups");
+    RL_REQUIRE(!nrm.ss_out || (accumulate && ldy == m && nrm.gamma_out && nrm.xg_out && !nrm.ss_in), RL_ERR_RANGE,
+               "kquant: the add-norm output accumulates into the [T][m] residual rows and needs gamma and the "
+               "x * (1 + gamma) rows");
+    RL_REQUIRE(!nrm.frag_out || nrm.ss_out, RL_ERR_RANGE, "kquant: fragment output needs the add-norm output");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
     RL_REQUIRE(T >= 1 && T <= 4, RL_ERR_RANGE, "kquant: T must be in 1..4");
     RL_REQUIRE(W && x && Y && ws, RL_ERR_RANGE, "kquant: null pointer");
@@ -626,9 +715,9 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     unsigned* tickets = static_cast<unsigned*>(ws);
     float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kq_ticket_bytes(groups));
     if (qt == 4)
-        launch_kq<4>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s);
+        launch_kq<4>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s, nrm);
     else
-        launch_kq<6>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s);
+        launch_kq<6>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s, nrm);
     check_launch("kq_gemm_kernel");
 }
 

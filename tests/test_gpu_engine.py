@@ -204,12 +204,18 @@ def test_other_weight_formats_match_oracle(gpu, orc, quant):
         assert rel_l2(eng.copy_logits(), lg) < TOL
 
 
-def test_norm_kernels_and_folded_norm_agree(gpu, orc, monkeypatch):
-    """The step with RMSNorm folded into the GEMMs (default for FP8 / BF16 models)
-    and the step with separate norm kernels (RL_FOLD_NORM=0) both match the oracle
-    on the same model, at T=1 and in a T=4 verify."""
+@pytest.mark.parametrize("quant", [None, M.Q_Q4_K, M.Q_Q6_K])
+def test_norm_kernels_and_folded_norm_agree(gpu, orc, monkeypatch, quant):
+    """The step with RMSNorm folded into the GEMMs (the default: FP8 / BF16 models
+    fold it into the GEMM epilogues and prologues, K-quant models into the residual
+    GEMVs' final write and the next GEMVs' x fragments) and the step with separate
+    norm kernels (RL_FOLD_NORM=0) both match the oracle on the same model, at T=1
+    and in a T=4 verify."""
     spec = mini_spec()
-    W = M.random_weights(spec, seed=11, w_scale=(1e-3, 1e-2))
+    if quant is None:
+        W = M.random_weights(spec, seed=11, w_scale=(1e-3, 1e-2))
+    else:
+        W = M.random_weights(spec, seed=11, linear_quant=quant)
     orc_m = OracleModel(spec, W, ctx=512)
     prompt = [3, 1, 4, 1, 5, 9, 2]
     orc_m.reset()
