@@ -252,10 +252,13 @@ __global__ __launch_bounds__(256) void gdn_decode_kernel(GdnArgs p) {
 // The recurrent state is not kept in the ring: with the conv ring the kernel keeps
 // one committed S and the per-token records of GdnRecords.
 constexpr int kCW = 32;                  // value columns per workgroup
-constexpr int kCChunks = 8;              // threads per column
-constexpr int kCRows = kDK / kCChunks;   // 16 rows per thread
-constexpr int kCT = kCW * kCChunks;      // 256 threads
-constexpr int kCWaves = kCT / 64;
+constexpr int kCChunks = 16;             // threads per column
+constexpr int kCRows = kDK / kCChunks;   // 8 rows per thread
+constexpr int kCT = kCW * kCChunks;      // 512 threads (8 waves)
+constexpr int kCRecPer = kMaxT * kDK / kCT;  // replayed k values per thread
+static_assert(kCT >= 2 * kDK, "the q/k conv channels need a thread each");
+// the kCChunks threads of a column sum their rows' products (fixed DPP order)
+__device__ inline float column_sum(float v) { return kCChunks == 8 ? group8_sum(v) : group16_sum(v); }
 constexpr int kMaxAbSlices = 8;
 
 struct GdnFusedArgs {
@@ -325,7 +328,8 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         return 2 * qdim + h * dv + cc * kCW + (ch - 2 * kDK);
     };
     const bool has_v = tid < kCW;
-    const int chan0 = chan_of(tid), chan1 = chan_of(2 * kDK + (has_v ? tid : 0));
+    const bool qk_lane = tid < 2 * kDK;  // thread tid < 256 owns q/k conv channel tid
+    const int chan0 = chan_of(qk_lane ? tid : 0), chan1 = chan_of(2 * kDK + (has_v ? tid : 0));
     float win0[K], win1[K], w0[K], w1[K], xin0[kMaxT], xin1[kMaxT];
     {
         const float4 a0 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan0) * K);
@@ -392,9 +396,9 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const size_t bank = static_cast<size_t>(a.rec.max_t) * rec_t;
     const float* rec_r = records ? rec_base + rbank * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
     float* rec_w = records ? rec_base + slot0 * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
-    float rk[kMaxT / 2], rd = 0.f, rg = 0.f;  // thread (t = tid / 128, i): two tokens per thread
+    float rk[kCRecPer], rd = 0.f, rg = 0.f;  // record values e = tid + q * kCT (token e / 128)
 #pragma unroll
-    for (int q = 0; q < kMaxT / 2; ++q) {
+    for (int q = 0; q < kCRecPer; ++q) {
         const int e = tid + q * kCT;
         rk[q] = e < n_rep * kDK ? rec_r[(e / kDK) * rec_t + e % kDK] : 0.f;
     }
@@ -426,10 +430,10 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         const float y0 = silu_f(static_cast<float>(acc0));
         if (tid < kDK)
             q_s[t][tid] = y0;
-        else
+        else if (qk_lane)
             k_s[t][tid - kDK] = y0;
-        sq[t] = static_cast<double>(y0) * y0;
-        if (owns_qk && (per_token || t == T - 1))
+        sq[t] = qk_lane ? static_cast<double>(y0) * y0 : 0.0;
+        if (owns_qk && qk_lane && (per_token || t == T - 1))
             *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan0) * K) =
                 make_float4(win0[0], win0[1], win0[2], win0[3]);
         if (has_v) {
@@ -442,8 +446,10 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
 #pragma unroll
     for (int t = 0; t < kMaxT; ++t) {
         if (t >= T) break;
-        const double ws = wave_sum_d(sq[t]);
-        if (lane == 0) red_s[wave][t] = ws;
+        if (wave < 4) {  // the q/k waves
+            const double ws = wave_sum_d(sq[t]);
+            if (lane == 0) red_s[wave][t] = ws;
+        }
     }
     if (wave * 4 < T) {  // waves holding gate lanes (all lanes take part in the DPP sums)
         const float sum = group8_sum(gin);
@@ -457,7 +463,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         }
     }
 #pragma unroll
-    for (int q = 0; q < kMaxT / 2; ++q) {
+    for (int q = 0; q < kCRecPer; ++q) {
         const int e = tid + q * kCT;
         if (e < n_rep * kDK) rk_s[e / kDK][e % kDK] = rk[q];
     }
@@ -509,7 +515,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
             S[r] = __fmul_rn(S[r], g);
             kv4[r & 3] = __fmaf_rn(S[r], kn[r], kv4[r & 3]);
         }
-        const float kv = group8_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
+        const float kv = column_sum((kv4[0] + kv4[1]) + (kv4[2] + kv4[3]));
         const float delta = (v_s[t][jj] - kv) * beta;
         float ov4[4] = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
@@ -517,7 +523,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
             S[r] = __fmaf_rn(kn[r], delta, S[r]);
             ov4[r & 3] = __fmaf_rn(S[r], (q_s[t][kCRows * c + r] * iq) * qscale, ov4[r & 3]);
         }
-        const float ov = group8_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
+        const float ov = column_sum((ov4[0] + ov4[1]) + (ov4[2] + ov4[3]));
         if (c == 0) {
             if (p.o) p.o[static_cast<size_t>(row0 + t) * p.nv * dv + static_cast<size_t>(h) * dv + j] = ov;
             if (keep) rec_w[t * rec_t + kDK + j] = delta;
