@@ -246,7 +246,8 @@ class Engine {
         if (!fp8(lm_head_) && lm_head_.kind != RL_Q_BF16) return false;
         for (const Layer& Ly : L_) {
             if (Ly.kind == RL_LAYER_DELTA) {
-                if (!gdn_fused_norm_ || Ly.in_parts.size() != 1 || !fp8(Ly.in_parts[0]) || !fp8(Ly.out_proj)) return false;
+                if (!gdn_fused_norm_ || Ly.in_parts.size() != 1 || !fp8(Ly.in_parts[0]) || !fp8(Ly.out_proj))
+                    return false;
             } else if (Ly.qkv_parts.size() != 1 || !fp8(Ly.qkv_parts[0]) || !fp8(Ly.o_proj)) {
                 return false;
             }
@@ -656,6 +657,11 @@ class Engine {
     float* xg_ = nullptr;     // [Tmax][H]: x * (1 + gamma) of the next norm
     int kq_groups_ = 0;
     bool gdn_fused_norm_ = false;
+    // the fused DeltaNet kernel (one committed state + per-token records): FP8 / BF16
+    // models with the gated norm in it (gdn_fused_norm_), K-quant models with it
+    // writing o for gnorm_pack
+    bool gdn_fused_ = false;
+    float* kq_abpart_ = nullptr;  // K-quant models: in_proj a/b rows as K-slice partials
     void* frag_x_ = nullptr;
     float* ss_ = nullptr;  // [add_norm_groups(H)][Tmax]
     float* ybuf_ = nullptr; // [Tmax][max_width] fused projection outputs
@@ -883,6 +889,7 @@ class Engine {
             kq_groups_ = kq_norm_groups(H);
             kq_ss_ = mem_.get_n<float>(static_cast<size_t>(kq_groups_) * T);
             xg_ = mem_.get_n<float>(static_cast<size_t>(T) * H);
+            kq_abpart_ = mem_.get_n<float>(static_cast<size_t>(kAbSlices) * T * 2 * align16(nv));
         }
         // per-head gated norm (gamma of dv values, zdim >= 256: ops.cpp:129-156) in the
         // DeltaNet kernel, when one workgroup can hold a head
@@ -893,6 +900,8 @@ class Engine {
             for (const Layer& Ly : L_)
                 if (Ly.kind == RL_LAYER_DELTA && Ly.gnorm_n != c_.v_dim) per_head = false;
             gdn_fused_norm_ = fold_norm_ && per_head;
+            gdn_fused_ = gdn_fused_norm_ ||
+                         (kq_fold_ && nd > 0 && gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && T <= 8);
         }
         // one committed S per layer plus R banks of per-token records with the fused
         // kernel, a ring of R states with the unfused one
@@ -901,12 +910,12 @@ class Engine {
         // the fused DeltaNet kernel
         RL_REQUIRE(mb_ == 1 || (fold_norm_ && (gdn_fused_norm_ || nd == 0)), RL_ERR_UNSUPPORTED,
                    "engine: batch decode needs FP8/BF16 linears with folded norms (and v_dim 128 for DeltaNet)");
-        s_bstride_ = s_slot_ * (gdn_fused_norm_ ? 1 : R_);
+        s_bstride_ = s_slot_ * (gdn_fused_ ? 1 : R_);
         rec_bstride_ = static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats;
         recn_bstride_ = R_ * nv;
         for (int l = 0; l < nd; ++l) {
             S_.push_back(mem_.get_n<float>(s_bstride_ * mb_));
-            if (gdn_fused_norm_) {
+            if (gdn_fused_) {
                 rec_.push_back(mem_.get_n<float>(rec_bstride_ * mb_));
                 rec_n_.push_back(mem_.get_n<int>(static_cast<size_t>(recn_bstride_) * mb_));
             }
@@ -1525,11 +1534,44 @@ class Engine {
         for (int i = 0; i < c_.n_layers; ++i) {
             Layer& Ly = L_[i];
             if (Ly.kind == RL_LAYER_DELTA) {
+                // the a/b rows (an FP8 / BF16 part of their own, a few tiles) as K-slice
+                // partials that the fused DeltaNet kernel adds: one short launch over
+                // many workgroups instead of a handful of long ones
+                int ab_part = -1;
                 for (size_t k = 0; k < Ly.in_parts.size(); ++k)
-                    consume(Ly.in_parts[k], ybuf_ + Ly.in_offs[k], Ly.in_width, Ly.in_parts[k].m);
-                gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
-                           slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_, s_slot_, R_, o_,
-                           T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                    if (gdn_fused_ && Ly.in_offs[k] == Ly.off_a && frag_kind(Ly.in_parts[k]) &&
+                        Ly.off_a + Ly.in_parts[k].m == Ly.in_width)
+                        ab_part = static_cast<int>(k);
+                for (size_t k = 0; k < Ly.in_parts.size(); ++k) {
+                    const Lin& L = Ly.in_parts[k];
+                    if (static_cast<int>(k) != ab_part) {
+                        consume(L, ybuf_ + Ly.in_offs[k], Ly.in_width, L.m);
+                        continue;
+                    }
+                    const NormIO* iop = normalised ? nullptr : &io;
+                    if (L.kind == RL_Q_FP8_E4M3_B128)
+                        gemm_fp8_frag(L.w, L.ts, frag_, kq_abpart_, L.m, L.n, T, kEpiPartial, L.m, L.m, st_, kAbSlices,
+                                      nullptr, iop);
+                    else
+                        gemm_bf16_frag(reinterpret_cast<const uint16_t*>(L.w), frag_, kq_abpart_, L.m, L.n, T,
+                                       kEpiPartial, L.m, L.m, st_, kAbSlices, nullptr, iop);
+                }
+                if (gdn_fused_) {
+                    const GdnRecords rec{slot_rec(Ly.dslot), slot_recn(Ly.dslot), sc() + kNCons, tmax_,
+                                         T > 1 && !force_all};
+                    const bool split = ab_part >= 0;
+                    const int ab_rows = split ? Ly.in_parts[ab_part].m : 0;
+                    gdn_decode_fused(ybuf_, split ? kq_abpart_ : ybuf_ + Ly.off_a,
+                                     split ? kq_abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b, Ly.in_width,
+                                     Ly.A_log, Ly.dt_bias, Ly.conv_w, slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot),
+                                     slot_S(Ly.dslot), sc() + kSlot, conv_slot_, R_, &rec, o_, nullptr, nullptr, nullptr,
+                                     nullptr, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_, split ? kAbSlices : 1,
+                                     ab_rows);
+                } else {
+                    gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
+                               slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_, s_slot_,
+                               R_, o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                }
                 gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
                 produce(Ly.out_proj, xn_, Ly.ffn_norm);
             } else {

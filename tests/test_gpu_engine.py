@@ -119,12 +119,22 @@ def test_spec_verify_rollback(gpu, fp8_pair):
     del ref_logits
 
 
+@pytest.fixture(scope="module")
+def q4k_pair(orc):
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=5, linear_quant=M.Q_Q4_K)
+    return spec, W, Engine(spec, W, ctx=1024), OracleModel(spec, W, ctx=1024)
+
+
+@pytest.mark.parametrize("pair", ["fp8_pair", "q4k_pair"])
 @pytest.mark.parametrize("n_ok", [1, 2, 3, 4])
-def test_spec_verify_then_decode_matches_plain_decode(gpu, fp8_pair, n_ok):
+def test_spec_verify_then_decode_matches_plain_decode(gpu, request, pair, n_ok):
     """After a verify that consumes n_ok of 4 tokens, the following steps see the
     recurrent state after exactly those tokens: two more T=1 steps and another
-    verify give the logits of plain T=1 decoding, bit for bit."""
-    spec, W, eng, orc_m = fp8_pair
+    verify give the logits of plain T=1 decoding, bit for bit.  Block-FP8 and Q4_K
+    models (the latter with the K-quant folded norms, the DeltaNet a/b rows as
+    K-slices and the fused DeltaNet kernel's records)."""
+    spec, W, eng, orc_m = request.getfixturevalue(pair)
     prompt = [3, 1, 4, 1, 5]
     eng.prefill(prompt)
     chain = [eng.greedy()]
