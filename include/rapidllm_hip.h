@@ -147,6 +147,19 @@ int rl_hip_gemm_kquant(int type, const uint8_t* tiled, const float* X, float* Y,
                        size_t workspace_bytes, int m, int n, int T, int accumulate, void* stream);
 int rl_hip_dequant_kquant(int type, const uint8_t* blocks, float* out, size_t n_blocks, void* stream);
 
+/* Fused MLP gate / up projection with SwiGLU.  Replaces the pair gemv_q4_k /
+ * gemv_q6_k over mlp.gate and mlp.up plus ops::swiglu (ops.cpp:607-609) of the
+ * reference's MLP block (the CUDA engine's fused gate/up + SwiGLU family,
+ * cuda_engine.cu:2347-2647).  rl_hip_pack_kquant_gate_up packs the I x n gate and up
+ * blocks (one type) as half tiles: tiled = rl_hip_kquant_tiled_bytes(type, 2 I, n)
+ * bytes, I a multiple of 8.  rl_hip_gemm_kquant_swiglu writes
+ * H [T][I] = silu(gate . x) * (up . x) with the workspace of a 2 I x n launch
+ * (rl_hip_kquant_workspace_bytes(2 I, n, T)). */
+int rl_hip_pack_kquant_gate_up(int type, const uint8_t* gate_blocks, const uint8_t* up_blocks, uint8_t* tiled,
+                               int I, int n, void* stream);
+int rl_hip_gemm_kquant_swiglu(int type, const uint8_t* tiled, const float* X, float* H, void* workspace,
+                              size_t workspace_bytes, int I, int n, int T, void* stream);
+
 /* Allocation-free variant of rl_hip_gemm_kquant.  No counterpart in the reference:
  * it is for callers that cannot allocate device memory (code under HIP graph
  * capture, tight serving loops, harnesses that forbid hipMalloc).  Same arguments

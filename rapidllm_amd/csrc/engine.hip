@@ -102,7 +102,7 @@ struct Layer {
     int aslot = 0;
     // MLP
     Lin gate_up;  // FP8/BF16: interleaved gate/up tiles, SwiGLU epilogue
-    Lin gate, up; // K-quant: separate, or gate_cat: gate rows then up rows in `gate`
+    Lin gate, up; // K-quant: separate, or gate_cat: gate / up half tiles in `gate` (SwiGLU launch)
     bool gate_cat = false;
     Lin down;
 };
@@ -831,8 +831,8 @@ class Engine {
                 if (g->quant == u->quant && (g->quant == RL_Q_FP8_E4M3_B128 || g->quant == RL_Q_BF16)) {
                     Ly.gate_up = upload_gate_up(g, u, I, H);
                 } else if (g->quant == u->quant && (g->quant == RL_Q_Q4_K || g->quant == RL_Q_Q6_K) && I % 64 == 0) {
-                    // one K-quant launch for gate and up: the tiled layout is row-tile
-                    // major, so up's tiles follow gate's
+                    // one K-quant launch for gate and up over half tiles (8 gate rows,
+                    // then the same 8 up rows), writing h = silu(gate) * up
                     Ly.gate = upload_kq_cat(g, u, I, H);
                     Ly.gate_cat = true;
                 } else {
@@ -943,7 +943,7 @@ class Engine {
         ybuf_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(max_width, 16));
         o_ = mem_.get_n<float>(static_cast<size_t>(T) * std::max(zdim, nq * hd));
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
-        g_ = mem_.get_n<float>(static_cast<size_t>(T) * 2 * I);  // [T][2I] with gate_cat
+        g_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         u_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         logits_ = mem_.get_n<float>(static_cast<size_t>(T) * c_.vocab);
         mtp_logits_ = mem_.get_n<float>(c_.vocab);
@@ -1236,19 +1236,17 @@ class Engine {
         L.m = 2 * I;
         L.n = H;
         kq_need_ = std::max(kq_need_, kq_workspace_bytes(2 * I, H, tmax_));
-        const size_t half = rl_hip_kquant_tiled_bytes(g->quant, I, H);
         L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(g->quant, 2 * I, H)));
         const size_t bb = static_cast<size_t>(I) * (H / 256) * (g->quant == RL_Q_Q4_K ? 144 : 210);
         uint8_t* tmp = nullptr;
-        RL_HIP(hipMalloc(&tmp, bb));
-        for (int k = 0; k < 2; ++k) {
-            RL_HIP(hipMemcpyAsync(tmp, (k ? u : g)->data, bb, hipMemcpyHostToDevice, st_));
-            const int rc = rl_hip_pack_kquant(g->quant, tmp, L.w + k * half, I, H, st_);
-            RL_HIP(hipStreamSynchronize(st_));
-            if (rc != RL_OK) {
-                (void)hipFree(tmp);
-                throw Error(rc, rl_hip_last_error());
-            }
+        RL_HIP(hipMalloc(&tmp, 2 * bb));
+        RL_HIP(hipMemcpyAsync(tmp, g->data, bb, hipMemcpyHostToDevice, st_));
+        RL_HIP(hipMemcpyAsync(tmp + bb, u->data, bb, hipMemcpyHostToDevice, st_));
+        const int rc = rl_hip_pack_kquant_gate_up(g->quant, tmp, tmp + bb, L.w, I, H, st_);
+        RL_HIP(hipStreamSynchronize(st_));
+        if (rc != RL_OK) {
+            (void)hipFree(tmp);
+            throw Error(rc, rl_hip_last_error());
         }
         (void)hipFree(tmp);
         return L;
@@ -1592,8 +1590,10 @@ class Engine {
                     gemm_bf16_frag(reinterpret_cast<const uint16_t*>(Ly.gate_up.w), frag_, h_, Ly.gate_up.m,
                                    Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1, nullptr, &io);
             } else if (Ly.gate_cat) {
-                consume(Ly.gate, g_, 2 * I, 2 * I);
-                swiglu(g_, 2 * I, g_ + I, 2 * I, h_, I, T, st_);
+                KqNorm ks = normalised ? KqNorm{} : kin;
+                ks.swiglu = 1;
+                kq_gemm(Ly.gate.kind == RL_Q_Q4_K ? 4 : 6, Ly.gate.w, normalised ? xn_ : xg_, h_, kq_ws_, kq_ws_bytes_,
+                        Ly.gate.m, Ly.gate.n, T, 0, I, st_, &ks);
             } else {
                 consume(Ly.gate, g_, I, I);
                 consume(Ly.up, u_, I, I);
@@ -1653,8 +1653,10 @@ class Engine {
                                    down_frag ? frag_h_ : nullptr);
             } else {
                 if (Ly.gate_cat) {
-                    linear(Ly.gate, xn_, g_, 2 * I, 2 * I, T, kEpiStore);
-                    swiglu(g_, 2 * I, g_ + I, 2 * I, h_, I, T, st_);
+                    KqNorm ks;
+                    ks.swiglu = 1;
+                    kq_gemm(Ly.gate.kind == RL_Q_Q4_K ? 4 : 6, Ly.gate.w, xn_, h_, kq_ws_, kq_ws_bytes_, Ly.gate.m,
+                            Ly.gate.n, T, 0, I, st_, &ks);
                 } else {
                     linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
                     linear(Ly.up, xn_, u_, I, I, T, kEpiStore);

@@ -86,6 +86,9 @@ struct KqNorm {
     const float* gamma_out = nullptr;
     float* xg_out = nullptr;
     void* frag_out = nullptr;
+    // the rows are gate / up half tiles (rl_hip_pack_kquant_gate_up): the launch
+    // writes h [T][m/2] = silu(gate) * up at stride ldy instead of the m rows
+    int swiglu = 0;
 };
 int kq_norm_groups(int m);
 bool kq_fold_supported();  // the folded-norm variants run with the default work split

@@ -480,8 +480,21 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     }
     float y[T];
 #pragma unroll
+    for (int t = 0; t < T; ++t) y[t] = NRM == 1 ? v[t] * s_inv[t] : v[t];
+    if (NRM != 2 && nrm.swiglu) {
+        // gate / up half tiles: tile rows 8..15 are the up rows of rows 0..7, so
+        // lane r16 < 8 pairs its gate value with lane r16 + 8's up value
+        // (silu(g) * u, reference ops.cpp:607-609)
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float u = __shfl_down(y[t], 8, 64);
+            if (own && r16 < 8)
+                Y[static_cast<size_t>(t) * ldy + rt * 8 + r16] = y[t] / (1.f + expf(-y[t])) * u;
+        }
+        return;
+    }
+#pragma unroll
     for (int t = 0; t < T; ++t) {
-        y[t] = NRM == 1 ? v[t] * s_inv[t] : v[t];
         if (own) {
             y[t] = accumulate ? y_old[t] + y[t] : y[t];
             Y[static_cast<size_t>(t) * ldy + row] = y[t];
@@ -525,20 +538,23 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
 }
 
 // Row-major GGUF blocks [m][n/256 * bb] -> tiles.  One thread per (tile, lane).
+// With src_up, the tiles are gate / up half tiles: tile rt holds rows 8 rt .. 8 rt + 7
+// of src (gate) as its rows 0..7 and the same rows of src_up as its rows 8..15.
 template <int QT>
-__global__ void kq_pack_kernel(const uint8_t* __restrict__ src, uint8_t* __restrict__ dst, int m, int nsb) {
+__global__ void kq_pack_kernel(const uint8_t* __restrict__ src, const uint8_t* __restrict__ src_up,
+                               uint8_t* __restrict__ dst, int m, int nsb) {
     // rows past m are written as zero blocks (d = 0: every weight is 0)
     using F = KFmt<QT>;
     const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rt, sb, lane)
-    const int m_tiles = (m + kTR - 1) / kTR;
+    const int m_tiles = src_up ? (m + 7) / 8 : (m + kTR - 1) / kTR;
     if (idx >= static_cast<size_t>(m_tiles) * nsb * 64) return;
     const int lane = idx % 64;
     const int sb = (idx / 64) % nsb;
     const int rt = static_cast<int>(idx / (static_cast<size_t>(64) * nsb));
     const int r16 = lane & 15, g = lane >> 4;
-    const int row = rt * kTR + r16;
+    const int row = src_up ? rt * 8 + (r16 & 7) : rt * kTR + r16;
     uint8_t* tile = dst + (static_cast<size_t>(rt) * nsb + sb) * F::kTileBytes;
-    const uint8_t* blk = src + (static_cast<size_t>(row) * nsb + sb) * F::kBlockBytes;
+    const uint8_t* blk = (src_up && r16 >= 8 ? src_up : src) + (static_cast<size_t>(row) * nsb + sb) * F::kBlockBytes;
     const bool ok = row < m;
     auto put = [&](int chunk, int off) {
         for (int e = 0; e < 16; ++e) tile[chunk * 1024 + 16 * lane + e] = ok ? blk[off + e] : 0;
@@ -705,6 +721,8 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
                "kquant: the add-norm output accumulates into the [T][m] residual rows and needs gamma and the "
                "x * (1 + gamma) rows");
     RL_REQUIRE(!nrm.frag_out || nrm.ss_out, RL_ERR_RANGE, "kquant: fragment output needs the add-norm output");
+    RL_REQUIRE(!nrm.swiglu || (!nrm.ss_out && !accumulate && m % kTR == 0 && ldy >= m / 2), RL_ERR_RANGE,
+               "kquant: the SwiGLU output needs whole gate / up half tiles, no accumulate and no add-norm output");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
     RL_REQUIRE(T >= 1 && T <= 4, RL_ERR_RANGE, "kquant: T must be in 1..4");
     RL_REQUIRE(W && x && Y && ws, RL_ERR_RANGE, "kquant: null pointer");
@@ -795,19 +813,45 @@ size_t rl_hip_kquant_tiled_bytes(int type, int m, int n) {
 
 size_t rl_hip_kquant_workspace_bytes(int m, int n, int T) { return rl::kq_workspace_bytes(m, n, T); }
 
+namespace {
+void kq_pack(int type, const uint8_t* blocks, const uint8_t* up, uint8_t* tiled, int m, int n, hipStream_t s) {
+    const int nsb = n / 256;
+    const size_t total = static_cast<size_t>(up ? (m + 7) / 8 : (m + kTR - 1) / kTR) * nsb * 64;
+    if (type == RL_Q_Q4_K)
+        hipLaunchKernelGGL(kq_pack_kernel<4>, dim3((total + 255) / 256), dim3(256), 0, s, blocks, up, tiled, m, nsb);
+    else
+        hipLaunchKernelGGL(kq_pack_kernel<6>, dim3((total + 255) / 256), dim3(256), 0, s, blocks, up, tiled, m, nsb);
+    check_launch("kq_pack_kernel");
+}
+}  // namespace
+
 int rl_hip_pack_kquant(int type, const uint8_t* blocks, uint8_t* tiled, int m, int n, void* stream) {
     return guard([&] {
         RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "pack_kquant: Q4_K or Q6_K only");
         RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0 && blocks && tiled, RL_ERR_RANGE, "pack_kquant: bad shape");
-        const int nsb = n / 256;
-        const size_t total = static_cast<size_t>((m + kTR - 1) / kTR) * nsb * 64;
-        if (type == RL_Q_Q4_K)
-            hipLaunchKernelGGL(kq_pack_kernel<4>, dim3((total + 255) / 256), dim3(256), 0, S(stream), blocks, tiled, m,
-                               nsb);
-        else
-            hipLaunchKernelGGL(kq_pack_kernel<6>, dim3((total + 255) / 256), dim3(256), 0, S(stream), blocks, tiled, m,
-                               nsb);
-        check_launch("kq_pack_kernel");
+        kq_pack(type, blocks, nullptr, tiled, m, n, S(stream));
+    });
+}
+
+int rl_hip_pack_kquant_gate_up(int type, const uint8_t* gate_blocks, const uint8_t* up_blocks, uint8_t* tiled,
+                               int I, int n, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "pack_kquant_gate_up: Q4_K or Q6_K only");
+        RL_REQUIRE(I > 0 && I % 8 == 0 && n > 0 && n % 256 == 0 && gate_blocks && up_blocks && tiled, RL_ERR_RANGE,
+                   "pack_kquant_gate_up: I a positive multiple of 8, n of 256");
+        kq_pack(type, gate_blocks, up_blocks, tiled, I, n, S(stream));
+    });
+}
+
+int rl_hip_gemm_kquant_swiglu(int type, const uint8_t* tiled, const float* X, float* H, void* workspace,
+                              size_t workspace_bytes, int I, int n, int T, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "gemm_kquant_swiglu: Q4_K or Q6_K only");
+        RL_REQUIRE(I > 0 && I % 8 == 0, RL_ERR_RANGE, "gemm_kquant_swiglu: I a positive multiple of 8");
+        rl::KqNorm kn;
+        kn.swiglu = 1;
+        rl::kq_gemm(type == RL_Q_Q4_K ? 4 : 6, tiled, X, H, workspace, workspace_bytes, 2 * I, n, T, 0, I, S(stream),
+                    &kn);
     });
 }
 

@@ -62,6 +62,8 @@ _SIGS = {
     "rl_hip_pack_kquant": (_i, [_i, _vp, _vp, _i, _i, _vp]),
     "rl_hip_gemm_kquant": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp]),
     "rl_hip_dequant_kquant": (_i, [_i, _vp, _vp, _sz, _vp]),
+    "rl_hip_pack_kquant_gate_up": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_gemm_kquant_swiglu": (_i, [_i, _vp, _vp, _vp, _vp, _sz, _i, _i, _i, _vp]),
     "rl_hip_gemm_kquant_noalloc": (_i, [_i, _vp, _vp, _vp, _i, _i, _i, _i, _vp]),
     "rl_hip_gemm_kquant_noalloc_max_scratch": (_sz, []),
     "rl_hip_gdn_decode": (_i, [_vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i,

@@ -162,6 +162,39 @@ class KQuantLinear:
              1 if accumulate else 0, stream)
 
 
+class KQuantGateUp:
+    """The MLP's gate and up K-quant weights [I][n] (one type) as one launch that
+    writes h = silu(gate . x) * (up . x) (reference MLP block: two ops::linear calls
+    and ops::swiglu, ops.cpp:607-609)."""
+
+    def __init__(self, qtype: int, gate_blocks: np.ndarray, up_blocks: np.ndarray, I: int, n: int, stream=None):
+        assert qtype in (Q4_K, Q6_K) and n % 256 == 0 and I % 8 == 0
+        bb = 144 if qtype == Q4_K else 210
+        g = np.ascontiguousarray(gate_blocks, np.uint8).reshape(-1)
+        u = np.ascontiguousarray(up_blocks, np.uint8).reshape(-1)
+        assert g.size == u.size == I * (n // 256) * bb
+        self.qtype, self.I, self.n = qtype, I, n
+        self.w = DeviceBuffer(hip.lib().rl_hip_kquant_tiled_bytes(qtype, 2 * I, n))
+        gd = DeviceBuffer.from_numpy(g, stream)
+        ud = DeviceBuffer.from_numpy(u, stream)
+        call("rl_hip_pack_kquant_gate_up", qtype, gd.ptr, ud.ptr, self.w.ptr, I, n, stream)
+        call("rl_hip_stream_synchronize", stream)
+        gd.free()
+        ud.free()
+
+    def forward(self, x_ptr, h_ptr, T, ws, stream=None):
+        call("rl_hip_gemm_kquant_swiglu", self.qtype, self.w.ptr, x_ptr, h_ptr, ws.ptr, ws.nbytes, self.I, self.n, T,
+             stream)
+
+    def __call__(self, X: np.ndarray, stream=None) -> np.ndarray:
+        X = _f32(X).reshape(-1, self.n)
+        T = X.shape[0]
+        xd = DeviceBuffer.from_numpy(X, stream)
+        hd = DeviceBuffer(4 * T * self.I)
+        self.forward(xd.ptr, hd.ptr, T, kquant_workspace(2 * self.I, self.n, T), stream=stream)
+        return hd.numpy(np.float32, (T, self.I), stream)
+
+
 def kquant_workspace(m: int, n: int, T: int) -> DeviceBuffer:
     """Workspace of one K-quant GEMV stream: split-K tickets + partials, zero-filled
     once (each launch leaves the tickets at zero again)."""

@@ -183,3 +183,27 @@ def test_synthetic_q4_k_engine_spec_invariant(gpu, monkeypatch):
     on, _, _ = eng.generate([1, 2, 3], 12, spec_n=3)
     assert on == off
     eng.close()
+
+
+@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+@pytest.mark.parametrize("I,n,T", [(8, 256, 1), (200, 1024, 3), (1024, 2048, 4), (17408, 5120, 1), (17408, 5120, 4)])
+def test_gemm_kquant_swiglu(gpu, orc, kind, I, n, T):
+    """Gate / up half tiles with the SwiGLU write: against the oracle's two GEMVs
+    and swiglu (<= 1e-3 relative L2), and against the same rows as one plain
+    2I-row launch (gate rows then up rows: the same split and per-row sums)
+    followed by silu(g) * u on the host (<= 1e-6; only exp's rounding differs)."""
+    r = synth.rng(3 + I + n + T)
+    qt = ops.Q4_K if kind == "q4k" else ops.Q6_K
+    g = _blocks(kind, r, I, n)
+    u = _blocks(kind, r, I, n)
+    X = r.standard_normal((T, n)).astype(np.float32)
+    H = ops.KQuantGateUp(qt, g, u, I, n)(X)
+    assert np.isfinite(H).all()
+    cat = ops.KQuantLinear(qt, np.concatenate([g.reshape(-1), u.reshape(-1)]), 2 * I, n)
+    GU = ops.kquant_linear_T(cat, X).astype(np.float64)
+    host = GU[:, :I] / (1.0 + np.exp(-GU[:, :I])) * GU[:, I:]
+    assert rel_l2(H, host) <= 1e-6, rel_l2(H, host)
+    fo = orc.gemv_q4_k if kind == "q4k" else orc.gemv_q6_k
+    for t in range(min(T, 2) if I > 4096 else T):
+        want = orc.swiglu(fo(g, X[t], I, n, 8), fo(u, X[t], I, n, 8))
+        assert rel_l2(H[t], want) <= 1e-3, (t, rel_l2(H[t], want))
