@@ -657,6 +657,9 @@ class Engine {
     float* xg_ = nullptr;     // [Tmax][H]: x * (1 + gamma) of the next norm
     int kq_groups_ = 0;
     bool gdn_fused_norm_ = false;
+    // K-quant models: the DeltaNet kernel writes y = gamma * o * silu(z) rows and the
+    // per-head sums of o^2; out_proj applies the per-head 1/rms as it reads them
+    bool kq_gnorm_ = false;
     // the fused DeltaNet kernel (one committed state + per-token records): FP8 / BF16
     // models with the gated norm in it (gdn_fused_norm_), K-quant models with it
     // writing o for gnorm_pack
@@ -902,6 +905,7 @@ class Engine {
             gdn_fused_norm_ = fold_norm_ && per_head;
             gdn_fused_ = gdn_fused_norm_ ||
                          (kq_fold_ && nd > 0 && gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && T <= 8);
+            kq_gnorm_ = kq_fold_ && gdn_fused_ && per_head;
         }
         // one committed S per layer plus R banks of per-token records with the fused
         // kernel, a ring of R states with the unfused one
@@ -1520,8 +1524,9 @@ class Engine {
             else
                 linear_folded(L, xg_, Y, ldy, m_valid, T, kin, io);
         };
-        auto produce = [&](const Lin& L, const float* a32, const float* gamma_next) {
+        auto produce = [&](const Lin& L, const float* a32, const float* gamma_next, const float* bss = nullptr) {
             KqNorm kp;
+            kp.bss = bss;
             kp.ss_out = kq_ss_;
             kp.gamma_out = gamma_next;
             kp.xg_out = xg_;
@@ -1562,16 +1567,22 @@ class Engine {
                     gdn_decode_fused(ybuf_, split ? kq_abpart_ : ybuf_ + Ly.off_a,
                                      split ? kq_abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b, Ly.in_width,
                                      Ly.A_log, Ly.dt_bias, Ly.conv_w, slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot),
-                                     slot_S(Ly.dslot), sc() + kSlot, conv_slot_, R_, &rec, o_, nullptr, nullptr, nullptr,
-                                     nullptr, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_, split ? kAbSlices : 1,
-                                     ab_rows);
+                                     slot_S(Ly.dslot), sc() + kSlot, conv_slot_, R_, &rec, kq_gnorm_ ? nullptr : o_,
+                                     kq_gnorm_ ? ybuf_ + Ly.off_z : nullptr, kq_gnorm_ ? Ly.gnorm : nullptr, nullptr,
+                                     kq_gnorm_ ? gss_ : nullptr, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_,
+                                     split ? kAbSlices : 1, ab_rows, nullptr, 0, 0, kq_gnorm_ ? xn_ : nullptr);
                 } else {
                     gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
                                slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_, s_slot_,
                                R_, o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                 }
-                gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f, st_);
-                produce(Ly.out_proj, xn_, Ly.ffn_norm);
+                if (kq_gnorm_) {
+                    produce(Ly.out_proj, xn_, Ly.ffn_norm, gss_);
+                } else {
+                    gnorm_pack(o_, ybuf_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, xn_, frag_, zdim, T, 1e-6f,
+                               st_);
+                    produce(Ly.out_proj, xn_, Ly.ffn_norm);
+                }
             } else {
                 for (size_t k = 0; k < Ly.qkv_parts.size(); ++k)
                     consume(Ly.qkv_parts[k], ybuf_ + Ly.qkv_offs[k], Ly.qkv_width, Ly.qkv_parts[k].m);

@@ -266,7 +266,8 @@ struct GdnFusedArgs {
     const float* z;      // [T][ld_in] at the head-0 z column (gated norm gate)
     const float* gamma;  // [dv]
     i32x4* frag;         // out_proj input fragments (may be null)
-    float* gss;          // [nv][T][4] partial sums of o^2 (with frag)
+    float* gss;          // [nv][T][4] partial sums of o^2 (with frag or y32)
+    float* y32;          // [T][nv * dv] fp32 rows of y (may be null)
     GdnRecords rec;      // rec.rec == nullptr: no records (direct mode)
     GdnBatch batch;
     // token rows: this call's tokens are rows row_off .. row_off + T - 1 of T_rows
@@ -359,7 +360,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     }
     float zt[kMaxT];
     float gam = 0.f;
-    const bool gn = a.frag != nullptr && c == 0;
+    const bool gn = (a.frag != nullptr || a.y32 != nullptr) && c == 0;
     if (gn) {
         gam = a.gamma[j];
 #pragma unroll
@@ -535,10 +536,10 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     }
     if (!keep) store_state();
     if (records && cc == 0 && tid == 0) count[slot0 * p.nv + h] = keep ? T : 0;
-    if (!a.frag) return;
+    if (!a.frag && !a.y32) return;
 
     // ---- per token: the chunk's sum of o^2 (double; 16-lane rows, then the row
-    // pair) and the fragments of y (thread t*4 + u packs columns 8u .. 8u+7)
+    // pair) and y: fragments (thread t*4 + u packs columns 8u .. 8u+7) or fp32 rows
     __syncthreads();
     if (wave * 2 < T) {  // wave w: tokens 2w (lanes 0-31) and 2w + 1 (lanes 32-63)
         const int t = 2 * wave + (lane >> 5), i = lane & 31;
@@ -548,7 +549,11 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
         if (lane == 0) a.gss[(static_cast<size_t>(h) * T_tot + row0 + t) * 4 + cc] = static_cast<float>(s0);
         if (lane == 32 && t < T) a.gss[(static_cast<size_t>(h) * T_tot + row0 + t) * 4 + cc] = static_cast<float>(s1);
     }
-    if (tid < T * (kCW / 8)) {
+    if (a.y32 && tid < T * kCW) {
+        const int t = tid / kCW, i = tid % kCW;
+        a.y32[static_cast<size_t>(row0 + t) * p.nv * dv + h * dv + cc * kCW + i] = y_s[t][i];
+    }
+    if (a.frag && tid < T * (kCW / 8)) {
         const int t = tid / (kCW / 8), u = tid % (kCW / 8);
         float v[8];
 #pragma unroll
@@ -778,14 +783,14 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices,
-                      int ab_ld, const GdnBatch* batch, int row_off, int T_rows) {
+                      int ab_ld, const GdnBatch* batch, int row_off, int T_rows, float* y32) {
     RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED,
                "gdn_decode_fused: dk 128, dv a multiple of 32, conv 4");
     RL_REQUIRE(T >= 1 && T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: T must be in 1..8");
     RL_REQUIRE(nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_decode_fused: nv must be a multiple of nk");
-    RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && S_out && (o || frag),
+    RL_REQUIRE(qkv && a && b && A_log && dt_bias && conv_w && conv_in && S_in && S_out && (o || frag || y32),
                RL_ERR_RANGE, "gdn_decode_fused: null pointer");
-    RL_REQUIRE(!frag || (z && gamma && gss && dv == 4 * kCW), RL_ERR_RANGE,
+    RL_REQUIRE((!frag && !y32) || (z && gamma && gss && dv == 4 * kCW), RL_ERR_RANGE,
                "gdn_decode_fused: the gated norm needs z, gamma, gss and dv 128");
     if (cur) {
         RL_REQUIRE(R > T, RL_ERR_RANGE, "gdn_decode_fused: ring needs more slots than tokens");
@@ -801,6 +806,7 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                    gamma,
                    static_cast<i32x4*>(frag),
                    gss,
+                   y32,
                    rec ? *rec : GdnRecords{nullptr, nullptr, nullptr, 0, 0},
                    batch ? *batch : GdnBatch{},
                    row_off,

@@ -89,6 +89,10 @@ struct KqNorm {
     // the rows are gate / up half tiles (rl_hip_pack_kquant_gate_up): the launch
     // writes h [T][m/2] = silu(gate) * up at stride ldy instead of the m rows
     int swiglu = 0;
+    // with ss_out: the input's 128-column blocks are scaled per token by
+    // 1/sqrt(sum / 128 + 1e-6), sum the four partial sums bss[(blk * T + t) * 4 + 0..3]
+    // (the DeltaNet output's gated RMSNorm per head)
+    const float* bss = nullptr;
 };
 int kq_norm_groups(int m);
 bool kq_fold_supported();  // the folded-norm variants run with the default work split
@@ -154,7 +158,8 @@ struct GdnBatch {
 // given and S_out == S_in is the committed state.  Outputs: o [T][nv*dv] (may be
 // null) and/or, with frag, the out_proj input fragments of
 // y = gamma * o * silu(z) with the per-head norm left to the GEMM: gss[h][t][4]
-// receives the four 32-column partial sums of o^2 (dv must be 128 then).
+// receives the four 32-column partial sums of o^2 (dv must be 128 then); y32
+// (optional, same conditions) receives y as fp32 rows [T][nv * dv].
 // a / b (per head h, token t): the sum over s < ab_slices of a[(s * T + t) * ab_ld + h]
 // (ab_slices 1: a[t * ld_in + h]).
 bool gdn_fused_supported(int dk, int dv, int K);
@@ -163,7 +168,8 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, const int* cur, size_t conv_slot, int R,
                       const GdnRecords* rec, float* o, const float* z, const float* gamma, void* frag, float* gss,
                       int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, int ab_slices = 1,
-                      int ab_ld = 0, const GdnBatch* batch = nullptr, int row_off = 0, int T_rows = 0);
+                      int ab_ld = 0, const GdnBatch* batch = nullptr, int row_off = 0, int T_rows = 0,
+                      float* y32 = nullptr);
 
 // Prompt prefill of T tokens from the conv window conv_in (direct mode): conv +
 // gates over all tokens (xc [T][conv_dim], gates [T][nv][2] scratch), then the

@@ -167,7 +167,9 @@ __host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
 // which are coherent across the XCDs' L2 caches without cache maintenance.
 // NRM: 0 plain; 1 consumer of a folded RMSNorm (outputs scaled by 1/rms from
 // nrm.ss_in); 2 producer (accumulates into the residual rows and writes nrm.ss_out,
-// and the next linear's inputs x * (1 + gamma) as fp32 rows / bf16 fragments).
+// and the next linear's inputs x * (1 + gamma) as fp32 rows / bf16 fragments);
+// 3 producer whose input's 128-column blocks are scaled per token by their
+// gated RMSNorm's 1/rms (nrm.bss) as the x fragments are built.
 template <int QT, int T, int D, int RW, int NRM = 0>
 __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                       float* __restrict__ Y, float* __restrict__ partial,
@@ -241,6 +243,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         // the first item is processed (one memory round trip for the whole build)
         constexpr int kPer = (NSET * kKqMaxSlice * 8 * 4 * 2 + 64 * RW - 1) / (64 * RW);
         float4 va[kPer], vb[kPer];
+        float4 bs4[NRM == 3 ? kPer : 1];  // the 8 values' column block's partial sums
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int it = threadIdx.x + k * 64 * RW;
@@ -249,11 +252,14 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
             const int t = 2 * set + tt;
             va[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             vb[k] = va[k];
+            if constexpr (NRM == 3) bs4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (it < items && t < T && sbl < nsl) {
-                const float4* px = reinterpret_cast<const float4*>(
-                    x + static_cast<size_t>(t) * n + static_cast<size_t>(s0 + sbl) * 256 + x_off<QT>(gg, mi));
+                const int col = (s0 + sbl) * 256 + x_off<QT>(gg, mi);
+                const float4* px = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + col);
                 va[k] = px[0];
                 vb[k] = px[1];
+                if constexpr (NRM == 3)
+                    bs4[k] = *reinterpret_cast<const float4*>(nrm.bss + (static_cast<size_t>(col >> 7) * T + t) * 4);
             }
         }
 #pragma unroll
@@ -269,7 +275,14 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
             } hi, mid;
             float run = 0.f;
             if (t < T && sbl < nsl) {
-                const float v[8] = {va[k].x, va[k].y, va[k].z, va[k].w, vb[k].x, vb[k].y, vb[k].z, vb[k].w};
+                float v[8] = {va[k].x, va[k].y, va[k].z, va[k].w, vb[k].x, vb[k].y, vb[k].z, vb[k].w};
+                if constexpr (NRM == 3) {
+                    // the block's gated RMSNorm (sums in a fixed order)
+                    const float sum = (bs4[k].x + bs4[k].y) + (bs4[k].z + bs4[k].w);
+                    const float inv = 1.f / sqrtf(sum / 128.f + 1e-6f);
+#pragma unroll
+                    for (int e = 0; e < 8; ++e) v[e] *= inv;
+                }
 #pragma unroll
                 for (int e = 0; e < 8; ++e) {
                     split_bf16(v[e], hi.h[e], mid.h[e]);
@@ -481,7 +494,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     float y[T];
 #pragma unroll
     for (int t = 0; t < T; ++t) y[t] = NRM == 1 ? v[t] * s_inv[t] : v[t];
-    if (NRM != 2 && nrm.swiglu) {
+    if (NRM < 2 && nrm.swiglu) {
         // gate / up half tiles: tile rows 8..15 are the up rows of rows 0..7, so
         // lane r16 < 8 pairs its gate value with lane r16 + 8's up value
         // (silu(g) * u, reference ops.cpp:607-609)
@@ -500,7 +513,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
             Y[static_cast<size_t>(t) * ldy + row] = y[t];
         }
     }
-    if constexpr (NRM == 2) {
+    if constexpr (NRM >= 2) {
         // residual add fused with the next RMSNorm's data: the row group's sum of
         // x^2 per token (16 rows per wave by a fixed butterfly, the waves in order,
         // double) and the next linear's inputs x * (1 + gamma): fp32 rows (xg_out) and,
@@ -673,7 +686,10 @@ void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, uns
     }
     if (nrm.ss_out) {
         RL_REQUIRE(kq_rw() == 4, RL_ERR_UNSUPPORTED, "kquant: folded RMSNorm needs four row tiles per workgroup");
-        launch_kq_rw<QT, T, 4, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+        if (nrm.bss)
+            launch_kq_rw<QT, T, 4, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+        else
+            launch_kq_rw<QT, T, 4, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
         return;
     }
     switch (kq_rw()) {
@@ -721,6 +737,7 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
                "kquant: the add-norm output accumulates into the [T][m] residual rows and needs gamma and the "
                "x * (1 + gamma) rows");
     RL_REQUIRE(!nrm.frag_out || nrm.ss_out, RL_ERR_RANGE, "kquant: fragment output needs the add-norm output");
+    RL_REQUIRE(!nrm.bss || nrm.ss_out, RL_ERR_RANGE, "kquant: block-scaled input with the add-norm output only");
     RL_REQUIRE(!nrm.swiglu || (!nrm.ss_out && !accumulate && m % kTR == 0 && ldy >= m / 2), RL_ERR_RANGE,
                "kquant: the SwiGLU output needs whole gate / up half tiles, no accumulate and no add-norm output");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
