@@ -8,18 +8,21 @@
 // fp32 accumulation: the same real number, within the 1e-3 relative-L2 budget of
 // the north star.
 //
-// The quant dot products run on the matrix cores (v_mfma_f32_16x16x32_bf16):
-//   * a quant q (4 or 6 bits) becomes the bf16 value 128 + q by placing its byte
-//     under the exponent byte 0x43 (one v_perm per two values, exact);
-//   * x is split into bf16 hi + mid parts (16 significant bits, as for the FP8
-//     linears) in LDS; A-operand row 4g + p carries token column p only in the
-//     k-range of lane group g (block-diagonal), so the MFMA returns, in every lane,
-//     the dot product of that lane's own 8 quants with x for up to 4 token
-//     columns -- 32 fp32 products per lane per instruction, no cross-lane sums;
-//   * a lane's 8-quant runs never cross a sub-block, so the four MFMAs of a
-//     32-quant sub-block accumulate in place and the per-(row, sub-block) scale is
-//     applied once: y += a_j * C_j - (128 a_j + b_j) * X_j  (Q4_K), with X_j the
-//     sub-block sum of the split x; Q6_K: y += a_j * C_j - 160 a_j X_j.
+// The quant dot products run on the matrix cores (v_mfma_i32_16x16x64_i8):
+//   * quants are the B operand as they are stored: a Q4_K nibble or a Q6_K 6-bit
+//     value is an int8 in 0..63 after a mask (and, for Q6_K, an or of the two high
+//     bits), no conversion;
+//   * x is quantised per 32-value block and token to int8 hi + lo with one scale:
+//     x ~ s * (hi + lo / 254), s = max|x| / 127 (15 significant bits of the block
+//     maximum; about 1e-5 relative error on the outputs), in LDS;
+//   * A-operand row 4g + p carries token column p only in the k-range of lane group
+//     g (block-diagonal), so the MFMA returns, in every lane, the exact int32 dot
+//     product of that lane's own 16 quants with x hi / lo for up to 4 token
+//     columns (hi, lo of two tokens) -- no cross-lane sums;
+//   * a lane's 16-quant runs never cross a sub-block, so the MFMAs of a sub-block
+//     accumulate exactly in place and the per-(row, sub-block) scale is applied
+//     once: y += a_j * s * (C_hi + C_lo / 254) - b_j * X_j (Q4_K, b_j = dmin * m_j;
+//     Q6_K: b_j = 32 a_j), with X_j the sub-block sum of the quantised x.
 //
 // Device layout: a tile = 16 rows x 1 super-block (256 quants).  Lane l of a wave
 // owns row 16rt + l % 16 and a quarter of the super-block (g = l / 16):
@@ -98,41 +101,33 @@ __device__ inline void q4k_scale_min_reg(const i32x4& h, int j, int& sc, int& mn
     mn = lo ? (b2 & 63) : ((b3 >> 4) | ((b2 >> 6) << 4));
 }
 
-// Four quant bytes (each < 128) -> two dwords of bf16 (128 + q): byte b under 0x43.
-__device__ inline void q_to_bf16x4(uint32_t q, uint32_t& lo, uint32_t& hi) {
-    lo = __builtin_amdgcn_perm(0x43434343u, q, 0x04010400u);  // [q0, 43, q1, 43]
-    hi = __builtin_amdgcn_perm(0x43434343u, q, 0x04030402u);  // [q2, 43, q3, 43]
-}
-
-union Frag8 {
-    bf16x8 v;
-    uint32_t u[4];
-    i32x4 i;
-};
-
-// Offset (within the super-block) of the 8 x values multiplying the quants of MFMA
-// mi of lane group g.  Q4_K: mi = 4 * (high nibble) + run; Q6_K: mi = 2 * kk + half.
+// Offset (within the super-block) of the 16 x values multiplying the quants of MFMA
+// mi of lane group g.  Q4_K: mi = 2 * (high nibble) + chunk; Q6_K: mi = kk.
 template <int QT>
-__device__ inline int x_off(int g, int mi) {
+__device__ inline int x_off16(int g, int mi) {
     if constexpr (QT == 4)
-        return 64 * g + 32 * (mi >> 2) + 8 * (mi & 3);
+        return 64 * g + 32 * (mi >> 1) + 16 * (mi & 1);
     else
-        return 128 * (g >> 1) + 32 * (mi >> 1) + 16 * (g & 1) + 8 * (mi & 1);
+        return 128 * (g >> 1) + 32 * mi + 16 * (g & 1);
 }
 
-// Run (8 values) of MFMA mi within its sub-block, and runs per sub-block.
-template <int QT>
-__device__ inline int run_of(int mi) {
-    return QT == 4 ? (mi & 3) : (mi & 1);
-}
-
-// Sub-block of MFMA mi of lane group g (its scale index).
+// Weight sub-block (scale index) of MFMA mi of lane group g.
 template <int QT>
 __device__ inline int sub_of(int g, int mi) {
     if constexpr (QT == 4)
-        return 2 * g + (mi >> 2);
+        return 2 * g + (mi >> 1);
     else
-        return 8 * (g >> 1) + 2 * (mi >> 1) + (g & 1);
+        return 8 * (g >> 1) + 2 * mi + (g & 1);
+}
+
+// 16 ints in [-127, 127] -> 16 int8 bytes.
+__device__ inline i32x4 pack_i8x16(const int (&v)[16]) {
+    i32x4 r;
+#pragma unroll
+    for (int d = 0; d < 4; ++d)
+        r[d] = (v[4 * d] & 255) | ((v[4 * d + 1] & 255) << 8) | ((v[4 * d + 2] & 255) << 16) |
+               (static_cast<int>(static_cast<uint32_t>(v[4 * d + 3]) << 24));
+    return r;
 }
 
 // Split-K tickets live at the start of the caller's workspace: one counter per row
@@ -147,16 +142,17 @@ constexpr int kKqDummyWindows = 64;
 __device__ __align__(4096) uint8_t g_kq_dummy[kKqDummyWindows * 4096];
 
 // LDS of a workgroup (K-slice of P super-blocks, NSET token sets of 2 tokens):
-//   afrag[set][sbl][mi][p][g]: 16 B (8 bf16) -- x hi (p even) / mid (p odd) of
-//                              token 2*set + p/2 at x_off(g, mi)
+//   afrag[set][sbl][mi][p][g]: 16 B (16 int8) -- x hi (p even) / lo (p odd) of
+//                              token 2*set + p/2 at x_off16(g, mi)
 //   zero16: 16 zero bytes (A operand of the off-diagonal lanes)
-//   xsum[t][sbl][j][run]:      sums of hi + mid over the 8-value runs of sub-block j
-//                              (4 runs for Q4_K, 2 for Q6_K)
+//   xinf[t][sbl][j]:           float2 per weight sub-block j: the scale s of its
+//                              32-value x block and the sub-block's sum of the
+//                              quantised x, s * (sum hi + sum lo / 254)
 template <int QT>
-__host__ __device__ constexpr int kq_afrag_bytes(int P, int nset) { return nset * P * 8 * 4 * 4 * 16; }
+__host__ __device__ constexpr int kq_afrag_bytes(int P, int nset) { return nset * P * 4 * 4 * 4 * 16; }
 template <int QT>
 __host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
-    return kq_afrag_bytes<QT>(P, nset) + 16 + T * P * KFmt<QT>::kNSub * (QT == 4 ? 4 : 2) * 4;
+    return kq_afrag_bytes<QT>(P, nset) + 16 + T * P * KFmt<QT>::kNSub * 8;
 }
 
 // Grid: blockIdx.x = row-group * S + k-slice.  Wave w of the workgroup takes tile
@@ -177,7 +173,6 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                                                       int accumulate, int ldy, KqNorm nrm) {
     using F = KFmt<QT>;
     constexpr int NSET = (T + 1) / 2;  // token sets of two (hi, mid, hi, mid columns)
-    constexpr int kRuns = QT == 4 ? 4 : 2;
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -194,7 +189,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
 
     i32x4* afrag = reinterpret_cast<i32x4*>(lds);
     i32x4* zero16 = reinterpret_cast<i32x4*>(lds + kq_afrag_bytes<QT>(P, NSET));
-    float* xsum = reinterpret_cast<float*>(lds + kq_afrag_bytes<QT>(P, NSET) + 16);
+    float2* xinf = reinterpret_cast<float2*>(lds + kq_afrag_bytes<QT>(P, NSET) + 16);
 
     const uint8_t* tiles = W + static_cast<size_t>(rt) * nsb * F::kTileBytes;
     // loads per lane per tile: quant chunks, the row's header (Q4_K d, dmin and scale
@@ -232,32 +227,32 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         }
     }
 
-    // ---- x fragments and sub-block sums of this slice
+    // ---- x fragments of this slice: each 32-value block of a token is quantised
+    // to int8 hi + lo with one scale s = max|x| / 127:  x ~ s * (hi + lo / 254),
+    // |hi|, |lo| <= 127 (15 significant bits of the block maximum)
     {
         const int nsl = s1 - s0;
         if (threadIdx.x == 0) *zero16 = i32x4{0, 0, 0, 0};
-        // items (set, sbl, mi, g, token-in-set): 8 x values split into bf16 hi + mid,
-        // and their sum (hi + mid, fixed order) as one run of the sub-block's sum
-        const int items = NSET * P * 8 * 4 * 2;
-        // at most kPer items per thread: every item's two x loads are issued before
-        // the first item is processed (one memory round trip for the whole build)
-        constexpr int kPer = (NSET * kKqMaxSlice * 8 * 4 * 2 + 64 * RW - 1) / (64 * RW);
-        float4 va[kPer], vb[kPer];
-        float4 bs4[NRM == 3 ? kPer : 1];  // the 8 values' column block's partial sums
+        // items (token, sbl, r): the 16-value run r of the super-block; the two runs
+        // of a 32-value block sit in adjacent lanes
+        const int items = T * P * 16;
+        // at most kPer items per thread: every item's x loads are issued before the
+        // first item is processed (one memory round trip for the whole build)
+        constexpr int kPer = (T * kKqMaxSlice * 16 + 64 * RW - 1) / (64 * RW);
+        float4 xv[kPer][4];
+        float4 bs4[NRM == 3 ? kPer : 1];  // the run's 128-column block's partial sums
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int it = threadIdx.x + k * 64 * RW;
-            const int tt = it & 1, gg = (it >> 1) & 3, mi = (it >> 3) & 7;
-            const int sbl = (it >> 6) % P, set = (it >> 6) / P;
-            const int t = 2 * set + tt;
-            va[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-            vb[k] = va[k];
+            const int r = it & 15, sbl = (it >> 4) % P, t = (it >> 4) / P;
+#pragma unroll
+            for (int q = 0; q < 4; ++q) xv[k][q] = make_float4(0.f, 0.f, 0.f, 0.f);
             if constexpr (NRM == 3) bs4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
-            if (it < items && t < T && sbl < nsl) {
-                const int col = (s0 + sbl) * 256 + x_off<QT>(gg, mi);
+            if (it < items && sbl < nsl) {
+                const int col = (s0 + sbl) * 256 + 16 * r;
                 const float4* px = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + col);
-                va[k] = px[0];
-                vb[k] = px[1];
+#pragma unroll
+                for (int q = 0; q < 4; ++q) xv[k][q] = px[q];
                 if constexpr (NRM == 3)
                     bs4[k] = *reinterpret_cast<const float4*>(nrm.bss + (static_cast<size_t>(col >> 7) * T + t) * 4);
             }
@@ -265,39 +260,66 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int it = threadIdx.x + k * 64 * RW;
-            if (it >= items) break;
-            const int tt = it & 1, gg = (it >> 1) & 3, mi = (it >> 3) & 7;
-            const int sbl = (it >> 6) % P, set = (it >> 6) / P;
-            const int t = 2 * set + tt;
-            union {
-                uint16_t h[8];
-                i32x4 v;
-            } hi, mid;
-            float run = 0.f;
-            if (t < T && sbl < nsl) {
-                float v[8] = {va[k].x, va[k].y, va[k].z, va[k].w, vb[k].x, vb[k].y, vb[k].z, vb[k].w};
-                if constexpr (NRM == 3) {
-                    // the block's gated RMSNorm (sums in a fixed order)
-                    const float sum = (bs4[k].x + bs4[k].y) + (bs4[k].z + bs4[k].w);
-                    const float inv = 1.f / sqrtf(sum / 128.f + 1e-6f);
+            if (k * 64 * RW >= items) break;  // uniform: whole waves past the items
+            const int r = it & 15, sbl = (it >> 4) % P, t = (it >> 4) / P;
+            float v[16];
 #pragma unroll
-                    for (int e = 0; e < 8; ++e) v[e] *= inv;
-                }
-#pragma unroll
-                for (int e = 0; e < 8; ++e) {
-                    split_bf16(v[e], hi.h[e], mid.h[e]);
-                    run += __uint_as_float(static_cast<uint32_t>(hi.h[e]) << 16) +
-                           __uint_as_float(static_cast<uint32_t>(mid.h[e]) << 16);
-                }
-            } else {
-                hi.v = i32x4{0, 0, 0, 0};
-                mid.v = i32x4{0, 0, 0, 0};
+            for (int q = 0; q < 4; ++q) {
+                v[4 * q] = xv[k][q].x;
+                v[4 * q + 1] = xv[k][q].y;
+                v[4 * q + 2] = xv[k][q].z;
+                v[4 * q + 3] = xv[k][q].w;
             }
-            const int base = (((set * P + sbl) * 8 + mi) * 4) * 4;  // [set][sbl][mi][p][g]
-            afrag[base + (2 * tt) * 4 + gg] = hi.v;
-            afrag[base + (2 * tt + 1) * 4 + gg] = mid.v;
-            if (t < T) xsum[((t * P + sbl) * F::kNSub + sub_of<QT>(gg, mi)) * kRuns + run_of<QT>(mi)] = run;
+            if constexpr (NRM == 3) {
+                // the run's gated RMSNorm block (sums in a fixed order)
+                const float sum = (bs4[k].x + bs4[k].y) + (bs4[k].z + bs4[k].w);
+                const float inv = 1.f / sqrtf(sum / 128.f + 1e-6f);
+#pragma unroll
+                for (int e = 0; e < 16; ++e) v[e] *= inv;
+            }
+            float mx = 0.f;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) mx = fmaxf(mx, fabsf(v[e]));
+            mx = fmaxf(mx, __shfl_xor(mx, 1, 64));  // the 32-value block's maximum
+            const float sc = mx / 127.f;
+            const float inv = mx > 0.f ? 127.f / mx : 0.f;
+            int hi[16], lo[16], shi = 0, slo = 0;
+#pragma unroll
+            for (int e = 0; e < 16; ++e) {
+                const float u = v[e] * inv;
+                const float h = rintf(u);
+                hi[e] = static_cast<int>(h);
+                lo[e] = static_cast<int>(rintf((u - h) * 254.f));
+                shi += hi[e];
+                slo += lo[e];
+            }
+            // the weight sub-block's sum of the quantised x: Q4_K sub-blocks are the
+            // 32-value blocks (both runs), Q6_K sub-blocks the 16-value runs
+            if constexpr (QT == 4) {
+                shi += __shfl_xor(shi, 1, 64);
+                slo += __shfl_xor(slo, 1, 64);
+            }
+            if (it < items && sbl < nsl) {
+                int g, mi;
+                if constexpr (QT == 4) {
+                    g = r >> 2;
+                    mi = r & 3;
+                } else {
+                    g = 2 * (r >> 3) + (r & 1);
+                    mi = (r >> 1) & 3;
+                }
+                const int set = t >> 1, tt = t & 1;
+                const int base = (((set * P + sbl) * 4 + mi) * 4) * 4;  // [set][sbl][mi][p][g]
+                afrag[base + (2 * tt) * 4 + g] = pack_i8x16(hi);
+                afrag[base + (2 * tt + 1) * 4 + g] = pack_i8x16(lo);
+                const float X = sc * (static_cast<float>(shi) + static_cast<float>(slo) * (1.f / 254.f));
+                if (QT == 6 || (r & 1) == 0)
+                    xinf[(t * P + sbl) * F::kNSub + (QT == 4 ? (r >> 1) : sub_of<6>(g, mi))] = make_float2(sc, X);
+            }
         }
+        // (entries past the slice and the second column of an odd T's last set are
+        // never used: the loop stops at the slice end, and an unused token column
+        // only reaches its own output rows)
     }
     __syncthreads();
 
@@ -315,74 +337,59 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                 const int sbl = sb - s0;
                 const i32x4* cb = buf[ps];
                 const float dq6d = QT == 6 ? half_bits_to_f32(dbits[ps]) : 0.f;
-                // this super-block's x fragments (A operands) and sub-block sums, read
-                // from LDS together before the MFMAs need them
-                i32x4 af[NSET][8];
+                // this super-block's x fragments (A operands), scales and sub-block
+                // sums, read from LDS together before the MFMAs need them
+                i32x4 af[NSET][4];
                 {
-                    const i32x4* fa = diag ? afrag + (((sbl * 8) * 4 + p_lane) * 4 + g) : zero16;
+                    const i32x4* fa = diag ? afrag + (((sbl * 4) * 4 + p_lane) * 4 + g) : zero16;
                     const int fstep = diag ? 16 : 0;  // i32x4 per mi
 #pragma unroll
                     for (int st = 0; st < NSET; ++st)
 #pragma unroll
-                        for (int mi = 0; mi < 8; ++mi) af[st][mi] = fa[(st * P * 8 + mi) * fstep];
+                        for (int mi = 0; mi < 4; ++mi) af[st][mi] = fa[(st * P * 4 + mi) * fstep];
                 }
                 constexpr int kLaneSubs = QT == 4 ? 2 : 4;
-                float xsv[T][kLaneSubs];
+                float2 xi[T][kLaneSubs];
 #pragma unroll
                 for (int t = 0; t < T; ++t)
 #pragma unroll
-                    for (int k = 0; k < kLaneSubs; ++k) {
-                        const int j = QT == 4 ? 2 * g + k : sub_of<6>(g, 2 * k);
-                        const float* xr = xsum + ((t * P + sbl) * F::kNSub + j) * kRuns;
-                        if constexpr (QT == 4) {
-                            const float4 r4 = *reinterpret_cast<const float4*>(xr);
-                            xsv[t][k] = (r4.x + r4.y) + (r4.z + r4.w);
-                        } else {
-                            const float2 r2 = *reinterpret_cast<const float2*>(xr);
-                            xsv[t][k] = r2.x + r2.y;
-                        }
-                    }
-                // quants -> bf16 B operands, MFMA per 8 quants, one accumulator per sub-block
-                f32x4 acc[NSET][QT == 4 ? 2 : 4];
+                    for (int k = 0; k < kLaneSubs; ++k)
+                        xi[t][k] = xinf[(t * P + sbl) * F::kNSub + sub_of<QT>(g, QT == 4 ? 2 * k : k)];
+                // quants as int8 B operands (16 per MFMA, one sub-block), exact int32
+                // dot products with x hi / lo per sub-block
+                i32x4 acc[NSET][kLaneSubs];
 #pragma unroll
                 for (int st = 0; st < NSET; ++st)
 #pragma unroll
-                    for (int k = 0; k < (QT == 4 ? 2 : 4); ++k) acc[st][k] = f32x4{0.f, 0.f, 0.f, 0.f};
+                    for (int k = 0; k < kLaneSubs; ++k) acc[st][k] = i32x4{0, 0, 0, 0};
 #pragma unroll
-                for (int mi = 0; mi < 8; ++mi) {
-                    Frag8 b;
+                for (int mi = 0; mi < 4; ++mi) {
+                    i32x4 bq;
                     if constexpr (QT == 4) {
-                        // run = mi & 3: quant bytes 8*run .. 8*run+7 of the lane's 32; nibble mi >> 2
-                        const i32x4 ch = cb[(mi & 3) >> 1];
-                        const uint32_t w0 = static_cast<uint32_t>(ch[2 * (mi & 1)]);
-                        const uint32_t w1 = static_cast<uint32_t>(ch[2 * (mi & 1) + 1]);
-                        const uint32_t q0 = (mi >> 2) ? (w0 >> 4) & 0x0f0f0f0fu : w0 & 0x0f0f0f0fu;
-                        const uint32_t q1 = (mi >> 2) ? (w1 >> 4) & 0x0f0f0f0fu : w1 & 0x0f0f0f0fu;
-                        q_to_bf16x4(q0, b.u[0], b.u[1]);
-                        q_to_bf16x4(q1, b.u[2], b.u[3]);
+                        // chunk mi & 1, nibble mi >> 1: the 16 quants of sub-block 2g + (mi >> 1)
+                        const i32x4 ch = cb[mi & 1];
+#pragma unroll
+                        for (int d = 0; d < 4; ++d)
+                            bq[d] = static_cast<int>((static_cast<uint32_t>(ch[d]) >> (4 * (mi >> 1))) & 0x0f0f0f0fu);
                     } else {
-                        // kk = mi >> 1, half = mi & 1: bytes 8*half .. 8*half+7 of the lane's 16
-                        const int kk = mi >> 1, hf = mi & 1;
-                        const i32x4 ql = cb[kk & 1];
+                        // kk = mi: low 4 bits from ql chunk kk & 1 (nibble kk >> 1), high 2 bits
+                        // from qh bits 2kk, 2kk+1
+                        const i32x4 ql = cb[mi & 1];
                         const i32x4 qh = cb[2];
 #pragma unroll
-                        for (int d = 0; d < 2; ++d) {
-                            const uint32_t lo4 = static_cast<uint32_t>(ql[2 * hf + d]);
-                            const uint32_t h2 = static_cast<uint32_t>(qh[2 * hf + d]);
-                            const uint32_t low = (kk >> 1) ? (lo4 >> 4) & 0x0f0f0f0fu : lo4 & 0x0f0f0f0fu;
-                            const uint32_t q6 = low | (((h2 >> (2 * kk)) & 0x03030303u) << 4);
-                            q_to_bf16x4(q6, b.u[2 * d], b.u[2 * d + 1]);
+                        for (int d = 0; d < 4; ++d) {
+                            const uint32_t low = (static_cast<uint32_t>(ql[d]) >> (4 * (mi >> 1))) & 0x0f0f0f0fu;
+                            const uint32_t h2 = (static_cast<uint32_t>(qh[d]) >> (2 * mi)) & 0x03030303u;
+                            bq[d] = static_cast<int>(low | (h2 << 4));
                         }
                     }
+                    const int k = QT == 4 ? (mi >> 1) : mi;
 #pragma unroll
-                    for (int st = 0; st < NSET; ++st) {
-                        Frag8 a;
-                        a.i = af[st][mi];
-                        const int k = QT == 4 ? (mi >> 2) : (mi >> 1);
-                        acc[st][k] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[st][k], 0, 0, 0);
-                    }
+                    for (int st = 0; st < NSET; ++st)
+                        acc[st][k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[st][mi], bq, acc[st][k], 0, 0, 0);
                 }
-                // per (row, sub-block) scales of this lane's sub-blocks
+                // per (row, sub-block) scales of this lane's sub-blocks:
+                // y += a_j * s * (C_hi + C_lo / 254) - b_j * X_j
                 if constexpr (QT == 4) {
                     // header dwords: d | dmin, then scale bytes s12[0..3], [4..7], [8..11]
                     const uint32_t h0 = static_cast<uint32_t>(cb[NL - 1][0]);
@@ -393,10 +400,13 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                         int sc, mn;
                         q4k_scale_min_reg(cb[NL - 1], 2 * g + k, sc, mn);
                         const float a = d * static_cast<float>(sc);
-                        const float c = fmaf(128.f, a, dmin * static_cast<float>(mn));
+                        const float c = dmin * static_cast<float>(mn);
 #pragma unroll
-                        for (int t = 0; t < T; ++t)
-                            tot[t] += a * (acc[t >> 1][k][2 * (t & 1)] + acc[t >> 1][k][2 * (t & 1) + 1]) - c * xsv[t][k];
+                        for (int t = 0; t < T; ++t) {
+                            const float dot = fmaf(static_cast<float>(acc[t >> 1][k][2 * (t & 1) + 1]), 1.f / 254.f,
+                                                   static_cast<float>(acc[t >> 1][k][2 * (t & 1)]));
+                            tot[t] += a * (xi[t][k].x * dot) - c * xi[t][k].y;
+                        }
                     }
                 } else {
 #pragma unroll
@@ -407,10 +417,13 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                         const int dw = (g >> 1) ? ((kk >> 1) ? sv[3] : sv[2]) : ((kk >> 1) ? sv[1] : sv[0]);
                         const int scv = __builtin_amdgcn_sbfe(dw, 8 * (2 * (kk & 1) + (g & 1)), 8);
                         const float a = dq6d * static_cast<float>(scv);
-                        const float c = 160.f * a;
+                        const float c = 32.f * a;
 #pragma unroll
-                        for (int t = 0; t < T; ++t)
-                            tot[t] += a * (acc[t >> 1][kk][2 * (t & 1)] + acc[t >> 1][kk][2 * (t & 1) + 1]) - c * xsv[t][kk];
+                        for (int t = 0; t < T; ++t) {
+                            const float dot = fmaf(static_cast<float>(acc[t >> 1][kk][2 * (t & 1) + 1]), 1.f / 254.f,
+                                                   static_cast<float>(acc[t >> 1][kk][2 * (t & 1)]));
+                            tot[t] += a * (xi[t][kk].x * dot) - c * xi[t][kk].y;
+                        }
                     }
                 }
             }
