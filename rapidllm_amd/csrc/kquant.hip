@@ -145,8 +145,8 @@ __device__ __align__(4096) uint8_t g_kq_dummy[kKqDummyWindows * 4096];
 //   afrag[set][sbl][mi][p][g]: 16 B (16 int8) -- x hi (p even) / lo (p odd) of
 //                              token 2*set + p/2 at x_off16(g, mi)
 //   zero16: 16 zero bytes (A operand of the off-diagonal lanes)
-//   xinf[t][sbl][j]:           float2 per weight sub-block j: the scale s of its
-//                              32-value x block and the sub-block's sum of the
+//   xinf[t][sbl][j]:           float2 per weight sub-block j: s / 254 (s the scale of
+//                              its 32-value x block) and the sub-block's sum of the
 //                              quantised x, s * (sum hi + sum lo / 254)
 template <int QT>
 __host__ __device__ constexpr int kq_afrag_bytes(int P, int nset) { return nset * P * 4 * 4 * 4 * 16; }
@@ -314,7 +314,8 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                 afrag[base + (2 * tt + 1) * 4 + g] = pack_i8x16(lo);
                 const float X = sc * (static_cast<float>(shi) + static_cast<float>(slo) * (1.f / 254.f));
                 if (QT == 6 || (r & 1) == 0)
-                    xinf[(t * P + sbl) * F::kNSub + (QT == 4 ? (r >> 1) : sub_of<6>(g, mi))] = make_float2(sc, X);
+                    xinf[(t * P + sbl) * F::kNSub + (QT == 4 ? (r >> 1) : sub_of<6>(g, mi))] =
+                        make_float2(sc * (1.f / 254.f), X);
             }
         }
         // (entries past the slice and the second column of an odd T's last set are
@@ -389,7 +390,8 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                         acc[st][k] = __builtin_amdgcn_mfma_i32_16x16x64_i8(af[st][mi], bq, acc[st][k], 0, 0, 0);
                 }
                 // per (row, sub-block) scales of this lane's sub-blocks:
-                // y += a_j * s * (C_hi + C_lo / 254) - b_j * X_j
+                // y += a_j * (s / 254) * (254 C_hi + C_lo) - b_j * X_j (the integer
+                // 254 C_hi + C_lo is exact; below 2^24 for Q4_K)
                 if constexpr (QT == 4) {
                     // header dwords: d | dmin, then scale bytes s12[0..3], [4..7], [8..11]
                     const uint32_t h0 = static_cast<uint32_t>(cb[NL - 1][0]);
@@ -403,9 +405,8 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                         const float c = dmin * static_cast<float>(mn);
 #pragma unroll
                         for (int t = 0; t < T; ++t) {
-                            const float dot = fmaf(static_cast<float>(acc[t >> 1][k][2 * (t & 1) + 1]), 1.f / 254.f,
-                                                   static_cast<float>(acc[t >> 1][k][2 * (t & 1)]));
-                            tot[t] += a * (xi[t][k].x * dot) - c * xi[t][k].y;
+                            const int ci = __mul24(acc[t >> 1][k][2 * (t & 1)], 254) + acc[t >> 1][k][2 * (t & 1) + 1];
+                            tot[t] = fmaf(a * xi[t][k].x, static_cast<float>(ci), fmaf(-c, xi[t][k].y, tot[t]));
                         }
                     }
                 } else {
@@ -420,9 +421,8 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                         const float c = 32.f * a;
 #pragma unroll
                         for (int t = 0; t < T; ++t) {
-                            const float dot = fmaf(static_cast<float>(acc[t >> 1][kk][2 * (t & 1) + 1]), 1.f / 254.f,
-                                                   static_cast<float>(acc[t >> 1][kk][2 * (t & 1)]));
-                            tot[t] += a * (xi[t][kk].x * dot) - c * xi[t][kk].y;
+                            const int ci = __mul24(acc[t >> 1][kk][2 * (t & 1)], 254) + acc[t >> 1][kk][2 * (t & 1) + 1];
+                            tot[t] = fmaf(a * xi[t][kk].x, static_cast<float>(ci), fmaf(-c, xi[t][kk].y, tot[t]));
                         }
                     }
                 }
