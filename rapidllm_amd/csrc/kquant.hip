@@ -212,9 +212,6 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         buf[d][NL - 1] = *reinterpret_cast<const i32x4*>(tile + F::kHdr + 16 * r16);
         if constexpr (QT == 6) dbits[d] = reinterpret_cast<const uint16_t*>(tile + F::kHdr + 256)[r16];
     };
-    // the first weights are requested before the slice's x fragments are built
-#pragma unroll
-    for (int d = 0; d < D; ++d) load(d, s0 + d, s0 + d < s1);
     // folded input RMSNorm: wave w < T holds token w's partial sums of squares
     // (group l + 64k in lane l), reduced in the epilogue
     float ssr[NRM == 1 ? kKqMaxSsPerLane : 1];
@@ -257,6 +254,11 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                     bs4[k] = *reinterpret_cast<const float4*>(nrm.bss + (static_cast<size_t>(col >> 7) * T + t) * 4);
             }
         }
+        // the first weights are requested after the x loads and before the build:
+        // vector loads return in issue order, so the build waits only for x (L2),
+        // not for the weights (HBM)
+#pragma unroll
+        for (int d = 0; d < D; ++d) load(d, s0 + d, s0 + d < s1);
 #pragma unroll
         for (int k = 0; k < kPer; ++k) {
             const int it = threadIdx.x + k * 64 * RW;
