@@ -433,29 +433,27 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         }
     }
 
-    // the four lane groups of a row hold quarters of it: fixed-order sum
+    // the four lane groups of a row hold quarters of it: fixed-order sum (every lane
+    // ends with its row's totals); from here lane group g finishes token g
 #pragma unroll
     for (int t = 0; t < 4; ++t) {
         tot[t] += __shfl_xor(tot[t], 16, 64);
         tot[t] += __shfl_xor(tot[t], 32, 64);
     }
+    const int te = g;  // this lane's token
     const int row = rt * kTR + r16;
-    const bool own = wave_live && g == 0 && row < m;
+    const bool own = wave_live && te < T && row < m;
     __shared__ int s_last;
-    float v[T];
-    // the rows' old values (accumulate) are requested now, so their round trip
-    // overlaps the ticket and the partial loads
-    float y_old[T];
+    float v = tot[0];
 #pragma unroll
-    for (int t = 0; t < T; ++t) {
-        v[t] = tot[t];
-        y_old[t] = own && accumulate ? Y[static_cast<size_t>(t) * ldy + row] : 0.f;
-    }
+    for (int t = 1; t < T; ++t) v = te == t ? tot[t] : v;
+    // the row's old value (accumulate) is requested now, so its round trip overlaps
+    // the ticket and the partial loads
+    const float y_old = own && accumulate ? Y[static_cast<size_t>(te) * ldy + row] : 0.f;
     if (S > 1) {
         if (own)
-            for (int t = 0; t < T; ++t)
-                __hip_atomic_store(partial + (static_cast<size_t>(slice) * T + t) * m + row, tot[t], __ATOMIC_RELAXED,
-                                   __HIP_MEMORY_SCOPE_AGENT);
+            __hip_atomic_store(partial + (static_cast<size_t>(slice) * T + te) * m + row, v, __ATOMIC_RELAXED,
+                               __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete before the ticket
         __syncthreads();
         if (threadIdx.x == 0) {
@@ -468,30 +466,24 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         __syncthreads();
         if (!s_last) return;
         if (own) {
-            // every token's partials of 8 slices requested together (one memory
-            // round trip per 8 slices, not one per slice and token), then added in
-            // slice order
-#pragma unroll
-            for (int t = 0; t < T; ++t) v[t] = 0.f;
+            // the partials of 8 slices requested together (one memory round trip per
+            // 8 slices), then added in slice order
+            v = 0.f;
             for (int q0 = 0; q0 < S; q0 += 8) {
-                float pv[T][8];
+                float pv[8];
 #pragma unroll
-                for (int t = 0; t < T; ++t)
+                for (int j = 0; j < 8; ++j)
+                    pv[j] = q0 + j < S ? __hip_atomic_load(partial + (static_cast<size_t>(q0 + j) * T + te) * m + row,
+                                                           __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
+                                       : 0.f;
 #pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        pv[t][j] = q0 + j < S ? __hip_atomic_load(partial + (static_cast<size_t>(q0 + j) * T + t) * m + row,
-                                                                  __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
-                                              : 0.f;
-#pragma unroll
-                for (int t = 0; t < T; ++t)
-#pragma unroll
-                    for (int j = 0; j < 8; ++j)
-                        if (q0 + j < S) v[t] += pv[t][j];
+                for (int j = 0; j < 8; ++j)
+                    if (q0 + j < S) v += pv[j];
             }
         }
     }
 
-    // ---- final write of the row group (one writer per row)
+    // ---- final write of the row group (one writer per row and token)
     __shared__ float s_inv[4];
     __shared__ double s_sq[4][4];  // [wave][token]
     if constexpr (NRM == 1) {
@@ -506,54 +498,38 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         }
         __syncthreads();
     }
-    float y[T];
-#pragma unroll
-    for (int t = 0; t < T; ++t) y[t] = NRM == 1 ? v[t] * s_inv[t] : v[t];
+    float y = NRM == 1 ? v * s_inv[te < T ? te : 0] : v;
     if (NRM < 2 && nrm.swiglu) {
         // gate / up half tiles: tile rows 8..15 are the up rows of rows 0..7, so
         // lane r16 < 8 pairs its gate value with lane r16 + 8's up value
         // (silu(g) * u, reference ops.cpp:607-609)
-#pragma unroll
-        for (int t = 0; t < T; ++t) {
-            const float u = __shfl_down(y[t], 8, 64);
-            if (own && r16 < 8)
-                Y[static_cast<size_t>(t) * ldy + rt * 8 + r16] = y[t] / (1.f + expf(-y[t])) * u;
-        }
+        const float u = __shfl_down(y, 8, 64);
+        if (own && r16 < 8) Y[static_cast<size_t>(te) * ldy + rt * 8 + r16] = y / (1.f + expf(-y)) * u;
         return;
     }
-#pragma unroll
-    for (int t = 0; t < T; ++t) {
-        if (own) {
-            y[t] = accumulate ? y_old[t] + y[t] : y[t];
-            Y[static_cast<size_t>(t) * ldy + row] = y[t];
-        }
+    if (own) {
+        y = accumulate ? y_old + y : y;
+        Y[static_cast<size_t>(te) * ldy + row] = y;
     }
     if constexpr (NRM >= 2) {
         // residual add fused with the next RMSNorm's data: the row group's sum of
-        // x^2 per token (16 rows per wave by a fixed butterfly, the waves in order,
-        // double) and the next linear's inputs x * (1 + gamma): fp32 rows (xg_out) and,
-        // if asked, bf16 fragments
+        // x^2 per token (16 rows per wave by a fixed butterfly within the token's lane
+        // group, the waves in order, double) and the next linear's inputs
+        // x * (1 + gamma): fp32 rows (xg_out) and, if asked, bf16 fragments
+        double sq = own ? static_cast<double>(y) * y : 0.0;
 #pragma unroll
-        for (int t = 0; t < T; ++t) {
-            double sq = own ? static_cast<double>(y[t]) * y[t] : 0.0;
-#pragma unroll
-            for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, 64);
-            if (lane == 0) s_sq[wave][t] = sq;
-        }
+        for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, 64);
+        if (r16 == 0 && te < T) s_sq[wave][te] = sq;
         if (own) {
-            const float gm = 1.f + nrm.gamma_out[row];
-            uint16_t* f16 = static_cast<uint16_t*>(nrm.frag_out);
-#pragma unroll
-            for (int t = 0; t < T; ++t) {
-                const float xg = y[t] * gm;
-                nrm.xg_out[static_cast<size_t>(t) * m + row] = xg;
-                if (f16) {
-                    uint16_t hi, mid;
-                    split_bf16(xg, hi, mid);
-                    const size_t u = frag_unit(row >> 3, t, T);
-                    f16[u * 8 + (row & 7)] = hi;
-                    f16[(u + T) * 8 + (row & 7)] = mid;
-                }
+            const float xg = y * (1.f + nrm.gamma_out[row]);
+            nrm.xg_out[static_cast<size_t>(te) * m + row] = xg;
+            if (nrm.frag_out) {
+                uint16_t* f16 = static_cast<uint16_t*>(nrm.frag_out);
+                uint16_t hi, mid;
+                split_bf16(xg, hi, mid);
+                const size_t u = frag_unit(row >> 3, te, T);
+                f16[u * 8 + (row & 7)] = hi;
+                f16[(u + T) * 8 + (row & 7)] = mid;
             }
         }
         __syncthreads();
