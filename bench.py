@@ -123,6 +123,45 @@ def gemm_shapes(spec):
     ]
 
 
+def valu_compare(iters=30, rotate_bytes=768 << 20):
+    """T=1 block-FP8 GEMV: the matrix-core kernel (rl_hip_time_gemm_fp8, store) and a
+    VALU dot-product kernel over the same weight layout (rl_hip_time_gemv_fp8_valu:
+    e4m3 -> fp32 conversions, FMAs, shuffle sums), weights cold in HBM, best of 3."""
+    import ctypes as C
+
+    from rapidllm_amd import ops, synth
+    from rapidllm_amd.hip import DeviceBuffer, call
+
+    r = synth.rng(3)
+    s = C_stream()
+    out = []
+    for m, n in ((16480, 5120), (14336, 5120), (34816, 5120)):
+        lin = ops.Fp8Linear(synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n, 1e-3, 1e-2))
+        nb = lin.w.nbytes
+        copies = [lin.w] + [DeviceBuffer(nb) for _ in range(max(1, -(-rotate_bytes // nb)) - 1)]
+        for c in copies[1:]:
+            call("rl_hip_memcpy_d2d", c.ptr, lin.w.ptr, nb, s)
+        ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
+        X = r.standard_normal((1, n)).astype(np.float32)
+        xd = DeviceBuffer.from_numpy(X)
+        frag = ops.act_frag_buffer(n, 1)
+        call("rl_hip_pack_act", xd.ptr, frag.ptr, n, 1, s)
+        yd = DeviceBuffer(4 * m)
+        ms = C.c_float()
+        best = {"mfma": 1e9, "valu": 1e9}
+        for _ in range(3):
+            call("rl_hip_time_gemm_fp8", ptrs, len(copies), lin.ts.ptr, frag.ptr, yd.ptr, None, None, None, None, None,
+                 m, n, 1, EPI_STORE, 1, iters, s, C.byref(ms))
+            best["mfma"] = min(best["mfma"], ms.value * 1e3)
+            call("rl_hip_time_gemv_fp8_valu", ptrs, len(copies), lin.ts.ptr, xd.ptr, yd.ptr, m, n, iters, s,
+                 C.byref(ms))
+            best["valu"] = min(best["valu"], ms.value * 1e3)
+        out.append({"m": m, "n": n, "mfma_us": round(best["mfma"], 2), "valu_us": round(best["valu"], 2),
+                    "mfma_GBps": round(nb / best["mfma"] / 1e3, 1), "valu_GBps": round(nb / best["valu"] / 1e3, 1)})
+        del lin, copies
+    return out
+
+
 def measure_gemm(spec, T, iters=30, rotate_bytes=768 << 20):
     """Average duration of the block-FP8 GEMM over the step's launch mix: per shape,
     `iters` back-to-back launches from C++ (rl_hip_time_gemm_fp8: HIP events on the
@@ -504,6 +543,8 @@ def main():
     ap.add_argument("--gemm-only", action="store_true",
                     help="time only the block-FP8 GEMM launch mix (the roofline kernel), for counter runs")
     ap.add_argument("--gemm-tokens", type=int, default=1, help="tokens per GEMM launch with --gemm-only (1..4)")
+    ap.add_argument("--valu-compare", action="store_true",
+                    help="time only the T=1 FP8 GEMV on the matrix cores against a VALU dot-product kernel")
     ap.add_argument("--prefill-only", type=int, default=0,
                     help="time only a prompt prefill of this many tokens (for kernel traces)")
     ap.add_argument("--configs-only", action="store_true",
@@ -526,6 +567,9 @@ def main():
     spec = ModelSpec(n_layers=args.layers)
     if args.copy_probe_mb:
         copy_probe(args.copy_probe_mb)
+        return
+    if args.valu_compare:
+        print(json.dumps({"t1_gemv_fp8_mfma_vs_valu": valu_compare()}))
         return
     if args.gemm_only:
         g_ms, g_bytes, per = measure_gemm(spec, args.gemm_tokens, iters=args.steps)

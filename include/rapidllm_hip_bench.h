@@ -71,6 +71,14 @@ int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float*
                          const float* sumsq_in, int m, int n, int T, int epilogue, int split, int iters,
                          void* stream, float* avg_ms);
 
+/* T=1 block-FP8 GEMV on the VALU (e4m3 -> fp32 conversion, FMA, shuffle sums) over
+ * the rl_hip_pack_fp8 layout, for comparison with the matrix-core GEMM: Y [m] =
+ * W . X (X fp32 [n], n a multiple of 128, at most 16384); `iters` launches cycling
+ * over n_copies weight copies, *avg_ms their average duration.  No counterpart in
+ * the reference (measurement only; the engine never calls it). */
+int rl_hip_time_gemv_fp8_valu(const void* const* w_copies, int n_copies, const float* tile_scales, const float* X,
+                              float* Y, int m, int n, int iters, void* stream, float* avg_ms);
+
 /* Average duration of `iters` back-to-back rl_hip_gemm_kquant launches (store),
  * cycling over n_copies packed weight copies.  No counterpart in the reference
  * (bench / roofline measurement). */

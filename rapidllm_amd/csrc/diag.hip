@@ -1,8 +1,9 @@
-// diag.hip -- bandwidth calibration kernels (no counterpart in the reference).
+// diag.hip -- calibration and comparison kernels (no counterpart in the reference).
 //
 // A plain streaming copy and a streaming read of a known number of bytes.  They
 // give the achievable HBM rate on the box and the scale factor between rocprof's
-// FETCH_SIZE / WRITE_SIZE counters and bytes actually moved.
+// FETCH_SIZE / WRITE_SIZE counters and bytes actually moved.  A VALU T=1 FP8 GEMV
+// over the product's weight layout, timed against the matrix-core kernel.
 #include <cstdlib>
 
 #include "common.h"
@@ -34,6 +35,60 @@ __global__ void read_probe_kernel(const i32x4* __restrict__ src, size_t n16, uns
     for (; i < n16; i += stride) acc ^= src[i];
     const unsigned x = static_cast<unsigned>(acc[0] ^ acc[1] ^ acc[2] ^ acc[3]);
     if (x == 0x9e3779b9u) out[0] = x;  // practically never taken; keeps the loads live
+}
+
+// T=1 block-FP8 GEMV on the VALU, for the comparison with the matrix-core kernel:
+// the same tiled weights (tile = 16 rows x 128 columns; lane (g, row) holds row `row`
+// at columns 32 g .. 32 g + 31 of each block), 16 waves per row tile as the store
+// launches, x staged in LDS as fp32.  Per block: 32 e4m3 -> fp32 conversions and 32
+// FMAs per lane, scaled by the block's tile scale; lane groups summed by shuffles,
+// waves through LDS.
+constexpr int kValuWaves = 16;
+__global__ __launch_bounds__(64 * kValuWaves) void valu_gemv_t1_kernel(const uint8_t* __restrict__ W,
+                                                                        const float* __restrict__ ts,
+                                                                        const float* __restrict__ x,
+                                                                        float* __restrict__ y, int m, int n_kb) {
+    extern __shared__ float xs[];  // n_kb * 128 floats
+    __shared__ float red[kValuWaves][16];
+    const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+    const int g = lane >> 4, row = lane & 15;
+    const int rt = blockIdx.x;
+    const uint8_t* wb = W + static_cast<size_t>(rt) * n_kb * 2048;
+    const float* sb = ts + static_cast<size_t>(rt) * n_kb;
+    for (int i = tid; i < n_kb * 32; i += 64 * kValuWaves)
+        reinterpret_cast<float4*>(xs)[i] = reinterpret_cast<const float4*>(x)[i];
+    __syncthreads();
+    float acc = 0.f;
+    for (int kb = wave; kb < n_kb; kb += kValuWaves) {
+        const i32x4* tile = reinterpret_cast<const i32x4*>(wb + static_cast<size_t>(kb) * 2048);
+        const i32x4 w0 = __builtin_nontemporal_load(tile + lane);
+        const i32x4 w1 = __builtin_nontemporal_load(tile + 64 + lane);
+        const float s = sb[kb];
+        const float4* xp = reinterpret_cast<const float4*>(xs + kb * 128 + 32 * g);
+        float a0 = 0.f, a1 = 0.f;
+#pragma unroll
+        for (int d = 0; d < 8; ++d) {
+            const int word = d < 4 ? w0[d] : w1[d - 4];
+            const auto lo = __builtin_amdgcn_cvt_pk_f32_fp8(word, false);
+            const auto hi = __builtin_amdgcn_cvt_pk_f32_fp8(word, true);
+            const float4 xv = xp[d];
+            a0 = fmaf(lo[0], xv.x, a0);
+            a1 = fmaf(lo[1], xv.y, a1);
+            a0 = fmaf(hi[0], xv.z, a0);
+            a1 = fmaf(hi[1], xv.w, a1);
+        }
+        acc = fmaf(a0 + a1, s, acc);
+    }
+    acc += __shfl_xor(acc, 16, 64);
+    acc += __shfl_xor(acc, 32, 64);
+    if (g == 0) red[wave][row] = acc;
+    __syncthreads();
+    if (tid < 16) {
+        float t = 0.f;
+        for (int w = 0; w < kValuWaves; ++w) t += red[w][tid];
+        const int r = rt * 16 + tid;
+        if (r < m) y[r] = t;
+    }
 }
 
 }  // namespace
@@ -108,6 +163,35 @@ int rl_hip_time_gemm_fp8(const void* const* w_copies, int n_copies, const float*
             rl::gemm_fp8_frag(static_cast<const uint8_t*>(w_copies[i % n_copies]), tile_scales, frag,
                               fo && sw ? nullptr : Y, m, n, T, epilogue, ldy, m_valid, s, S_, fo,
                               iop);
+        RL_HIP(hipEventRecord(b, s));
+        RL_HIP(hipEventSynchronize(b));
+        float ms = 0.f;
+        RL_HIP(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        *avg_ms = ms / iters;
+    });
+}
+
+// The VALU T=1 GEMV above: `iters` launches cycling over n_copies weight copies,
+// one event pair around the loop.  No counterpart in the reference.
+int rl_hip_time_gemv_fp8_valu(const void* const* w_copies, int n_copies, const float* tile_scales, const float* X,
+                              float* Y, int m, int n, int iters, void* stream, float* avg_ms) {
+    return guard([&] {
+        RL_REQUIRE(w_copies && n_copies >= 1 && iters >= 1 && avg_ms && tile_scales && X && Y, RL_ERR_RANGE,
+                   "time_gemv_valu: bad arguments");
+        RL_REQUIRE(m > 0 && n > 0 && n % 128 == 0 && n <= 16384, RL_ERR_RANGE,
+                   "time_gemv_valu: n a multiple of 128, at most 16384 (x in LDS)");
+        const hipStream_t s = S(stream);
+        const int n_kb = n / 128, mt = (m + 15) / 16;
+        hipEvent_t a, b;
+        RL_HIP(hipEventCreate(&a));
+        RL_HIP(hipEventCreate(&b));
+        RL_HIP(hipEventRecord(a, s));
+        for (int i = 0; i < iters; ++i)
+            hipLaunchKernelGGL(valu_gemv_t1_kernel, dim3(mt), dim3(64 * kValuWaves), static_cast<size_t>(n) * 4, s,
+                               static_cast<const uint8_t*>(w_copies[i % n_copies]), tile_scales, X, Y, m, n_kb);
+        check_launch("valu_gemv_t1_kernel");
         RL_HIP(hipEventRecord(b, s));
         RL_HIP(hipEventSynchronize(b));
         float ms = 0.f;

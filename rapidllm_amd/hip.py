@@ -123,6 +123,7 @@ _SIGS = {
     "rl_hip_copy_probe": (_i, [_vp, _vp, _sz, _vp]),
     "rl_hip_read_probe": (_i, [_vp, _sz, _vp, _vp]),
     "rl_hip_norm_group_rows": (_i, []),
+    "rl_hip_time_gemv_fp8_valu": (_i, [_vp, _i, _vp, _vp, _vp, _i, _i, _i, _vp, C.POINTER(C.c_float)]),
     "rl_hip_time_gemm_fp8": (_i, [_vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _vp,
                                   C.POINTER(C.c_float)]),
     "rl_hip_gemm_fp8": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _vp]),

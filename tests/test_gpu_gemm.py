@@ -284,3 +284,29 @@ def test_gemm_fp8_folded_norm_input(gpu, orc, T, epi):
         want = g / (1.0 + np.exp(-g)) * u
     for t in range(T):
         assert rel_l2(Y[t], want[t]) <= REL_L2, (t, rel_l2(Y[t], want[t]))
+
+
+@pytest.mark.parametrize("m,n", [(100, 1024), (16480, 5120)])
+def test_valu_gemv_comparison_kernel(gpu, orc, m, n):
+    """The VALU T=1 GEMV that the bench times against the matrix-core kernel computes
+    the same product (<= 1e-3 relative L2 against the oracle), so the comparison is
+    between equal work."""
+    import ctypes as C
+
+    from rapidllm_amd.hip import DeviceBuffer, call
+
+    r = synth.rng(900 + m)
+    W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n, 1e-3, 1e-2)
+    lin = ops.Fp8Linear(W, s)
+    X = r.standard_normal((1, n)).astype(np.float32)
+    xd = DeviceBuffer.from_numpy(X)
+    yd = DeviceBuffer(4 * m)
+    ptrs = (C.c_void_p * 1)(lin.w.ptr)
+    ms = C.c_float()
+    call("rl_hip_time_gemv_fp8_valu", ptrs, 1, lin.ts.ptr, xd.ptr, yd.ptr, m, n, 1, None, C.byref(ms))
+    y = yd.numpy(np.float32, (m,))
+    want = orc.gemm_fp8(W, s, X)[0] if m * n <= 1 << 20 else None
+    if want is None:
+        # large shape: against the matrix-core kernel (itself checked against the oracle)
+        want = _time_gemm(lin, X, 0)[:m]
+    assert rel_l2(y, want) <= REL_L2
