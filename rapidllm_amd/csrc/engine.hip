@@ -1398,6 +1398,16 @@ class Engine {
         return true;
     }
 
+    // RL_AB_IN_KQ=0 keeps the K-quant models' BF16 a/b rows as a launch of their own
+    // (A/B measurement)
+    static bool ab_rows_in_kq_enabled() {
+        static const bool on = [] {
+            const char* v = std::getenv("RL_AB_IN_KQ");
+            return !(v && v[0] == '0');
+        }();
+        return on;
+    }
+
     // FP8 / BF16 GEMM on given input fragments.
     void gemm_on(const Lin& L, const void* fr, float* Y, int ldy, int m_valid, int T, int epi,
                  void* frag_out = nullptr, const NormIO* io = nullptr) {
@@ -1545,12 +1555,32 @@ class Engine {
                     if (gdn_fused_ && Ly.in_offs[k] == Ly.off_a && frag_kind(Ly.in_parts[k]) &&
                         Ly.off_a + Ly.in_parts[k].m == Ly.in_width)
                         ab_part = static_cast<int>(k);
+                // BF16 a/b rows beside K-quant parts: computed by extra workgroups of the
+                // last K-quant launch (same x, same partial layout), no launch of their own
+                int kq_host = -1;
+                if (ab_part >= 0 && Ly.in_parts[ab_part].kind == RL_Q_BF16 && kq_fold_supported() &&
+                    ab_rows_in_kq_enabled())
+                    for (size_t k = 0; k < Ly.in_parts.size(); ++k)
+                        if (static_cast<int>(k) != ab_part && is_kq(Ly.in_parts[k])) kq_host = static_cast<int>(k);
                 for (size_t k = 0; k < Ly.in_parts.size(); ++k) {
                     const Lin& L = Ly.in_parts[k];
+                    if (static_cast<int>(k) == kq_host) {
+                        const Lin& A = Ly.in_parts[ab_part];
+                        KqNorm kn = normalised ? KqNorm{} : kin;
+                        kn.ab_w = reinterpret_cast<const uint16_t*>(A.w);
+                        kn.ab_rows = A.m;
+                        kn.ab_slices = kAbSlices;
+                        kn.ab_out = kq_abpart_;
+                        kn.ab_ld = A.m;
+                        kq_gemm(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, normalised ? xn_ : xg_, ybuf_ + Ly.in_offs[k], kq_ws_,
+                                kq_ws_bytes_, L.m, L.n, T, 0, Ly.in_width, st_, &kn);
+                        continue;
+                    }
                     if (static_cast<int>(k) != ab_part) {
                         consume(L, ybuf_ + Ly.in_offs[k], Ly.in_width, L.m);
                         continue;
                     }
+                    if (kq_host >= 0) continue;
                     const NormIO* iop = normalised ? nullptr : &io;
                     if (L.kind == RL_Q_FP8_E4M3_B128)
                         gemm_fp8_frag(L.w, L.ts, frag_, kq_abpart_, L.m, L.n, T, kEpiPartial, L.m, L.m, st_, kAbSlices,

@@ -93,6 +93,16 @@ struct KqNorm {
     // 1/sqrt(sum / 128 + 1e-6), sum the four partial sums bss[(blk * T + t) * 4 + 0..3]
     // (the DeltaNet output's gated RMSNorm per head)
     const float* bss = nullptr;
+    // Extra rows in BF16 (the DeltaNet in_proj a / b rows beside K-quant q|k|v, z):
+    // ab_w is their tiled BF16 matrix (rl_hip_pack_bf16 layout, ab_rows rows, the
+    // launch's n columns); extra workgroups compute them from the same x as
+    // ab_slices K-slice partials, ab_out[(slice * T + t) * ab_ld + row], scaled like
+    // the main rows (1/rms with ss_in).
+    const uint16_t* ab_w = nullptr;
+    int ab_rows = 0;
+    int ab_slices = 0;
+    float* ab_out = nullptr;
+    int ab_ld = 0;
 };
 int kq_norm_groups(int m);
 bool kq_fold_supported();  // the folded-norm variants run with the default work split

@@ -155,6 +155,77 @@ __host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
     return kq_afrag_bytes<QT>(P, nset) + 16 + T * P * KFmt<QT>::kNSub * 8;
 }
 
+// Extra workgroup u of a launch with BF16 rows beside the K-quant ones (KqNorm::ab_w):
+// row tile u / ab_slices, K-slice u % ab_slices of the BF16 matrix, over the same
+// fp32 x (slices past the last column block write zeros).  Lane (g, r) of wave w
+// holds row r at columns 32 g .. 32 g + 31 of each 128-column block (four 16-byte
+// chunks); waves take blocks w, w + 4, ...; lane groups summed by shuffles, waves
+// in order through LDS.
+template <int T, int NRM>
+__device__ void kq_ab_rows(const KqNorm& nrm, const float* __restrict__ x, int n, int u) {
+    const int lane = threadIdx.x & 63;
+    const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+    const int g = lane >> 4, r16 = lane & 15;
+    const int rt = u / nrm.ab_slices, sl = u % nrm.ab_slices;
+    const int n_kb = n / 128;
+    const int per = (n_kb + nrm.ab_slices - 1) / nrm.ab_slices;
+    const int b0 = min(n_kb, sl * per), b1 = min(n_kb, b0 + per);
+    __shared__ float red[4][4][16];  // [wave][token][row]
+    __shared__ float inv_s[4];
+    float acc[T];
+#pragma unroll
+    for (int t = 0; t < T; ++t) acc[t] = 0.f;
+    for (int kb = b0 + wave; kb < b1; kb += 4) {
+        const uint8_t* tile = reinterpret_cast<const uint8_t*>(nrm.ab_w) + (static_cast<size_t>(rt) * n_kb + kb) * 4096;
+        i32x4 w[4];
+#pragma unroll
+        for (int c4 = 0; c4 < 4; ++c4) w[c4] = *reinterpret_cast<const i32x4*>(tile + c4 * 1024 + 16 * lane);
+#pragma unroll
+        for (int t = 0; t < T; ++t) {
+            const float4* xp = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + kb * 128 + 32 * g);
+            float s0 = 0.f, s1 = 0.f;
+#pragma unroll
+            for (int c4 = 0; c4 < 4; ++c4) {
+                const float4 xa = xp[2 * c4], xb = xp[2 * c4 + 1];
+                const float xv[8] = {xa.x, xa.y, xa.z, xa.w, xb.x, xb.y, xb.z, xb.w};
+#pragma unroll
+                for (int q = 0; q < 4; ++q) {
+                    const uint32_t d = static_cast<uint32_t>(w[c4][q]);
+                    s0 = fmaf(__uint_as_float(d << 16), xv[2 * q], s0);
+                    s1 = fmaf(__uint_as_float(d & 0xffff0000u), xv[2 * q + 1], s1);
+                }
+            }
+            acc[t] += s0 + s1;
+        }
+    }
+    float inv = 1.f;
+    if constexpr (NRM == 1) {
+        // token w's 1/rms from the input's partial sums (groups in order, then a
+        // fixed butterfly), as the K-quant rows
+        if (wave < T) {
+            double ss = 0.0;
+            for (int gi = lane; gi < nrm.groups_in; gi += 64) ss += static_cast<double>(nrm.ss_in[gi * T + wave]);
+            ss = wave_sum_d(ss);
+            if (lane == 0) inv_s[wave] = 1.f / sqrtf(static_cast<float>(ss / nrm.n_norm) + nrm.eps);
+        }
+    }
+#pragma unroll
+    for (int t = 0; t < T; ++t) {
+        acc[t] += __shfl_xor(acc[t], 16, 64);
+        acc[t] += __shfl_xor(acc[t], 32, 64);
+        if (g == 0) red[wave][t][r16] = acc[t];
+    }
+    __syncthreads();
+    if (static_cast<int>(threadIdx.x) < T * 16) {
+        const int t = threadIdx.x / 16, r = threadIdx.x % 16;
+        const int row = rt * 16 + r;
+        float v = ((red[0][t][r] + red[1][t][r]) + red[2][t][r]) + red[3][t][r];
+        if constexpr (NRM == 1) v *= inv_s[t];
+        (void)inv;
+        if (row < nrm.ab_rows) nrm.ab_out[(static_cast<size_t>(sl) * T + t) * nrm.ab_ld + row] = v;
+    }
+}
+
 // Grid: blockIdx.x = row-group * S + k-slice.  Wave w of the workgroup takes tile
 // row RW * row-group + w over the slice's super-blocks.  S == 1: the workgroup writes
 // Y (store or add).  S > 1: it writes partial[slice][t][row] and takes a ticket; the
@@ -173,6 +244,14 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                                                       int accumulate, int ldy, KqNorm nrm) {
     using F = KFmt<QT>;
     constexpr int NSET = (T + 1) / 2;  // token sets of two (hi, mid, hi, mid columns)
+    if constexpr (NRM < 2) {
+        // extra workgroups past the K-quant ones: the BF16 rows (KqNorm::ab_w)
+        const int ab_wgs = nrm.ab_w ? ((nrm.ab_rows + 15) / 16) * nrm.ab_slices : 0;
+        if (static_cast<int>(blockIdx.x) >= static_cast<int>(gridDim.x) - ab_wgs) {
+            kq_ab_rows<T, NRM>(nrm, x, n, blockIdx.x - (gridDim.x - ab_wgs));
+            return;
+        }
+    }
     extern __shared__ __align__(16) uint8_t lds[];
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
@@ -662,8 +741,9 @@ void launch_kq_rw(const uint8_t* W, const float* x, float* Y, float* partial, un
     const int groups = (m + kTR * RW - 1) / (kTR * RW);
     const int P = (n / 256 + S - 1) / S;
     const size_t lds = kq_lds_bytes<QT>(P, (T + 1) / 2, T);
-    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW, NRM>), dim3(groups * S), dim3(64 * RW), lds, s, W, x, Y,
-                       partial, tickets, m, n, S, accumulate, ldy, nrm);
+    const int ab_wgs = nrm.ab_w ? ((nrm.ab_rows + 15) / 16) * nrm.ab_slices : 0;
+    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW, NRM>), dim3(groups * S + ab_wgs), dim3(64 * RW), lds, s, W,
+                       x, Y, partial, tickets, m, n, S, accumulate, ldy, nrm);
 }
 
 template <int QT, int T>
@@ -729,6 +809,9 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
                "x * (1 + gamma) rows");
     RL_REQUIRE(!nrm.frag_out || nrm.ss_out, RL_ERR_RANGE, "kquant: fragment output needs the add-norm output");
     RL_REQUIRE(!nrm.bss || nrm.ss_out, RL_ERR_RANGE, "kquant: block-scaled input with the add-norm output only");
+    RL_REQUIRE(!nrm.ab_w || (!nrm.ss_out && !nrm.swiglu && nrm.ab_rows > 0 && nrm.ab_slices >= 1 &&
+                             nrm.ab_out && nrm.ab_ld >= nrm.ab_rows && kq_rw() == 4),
+               RL_ERR_RANGE, "kquant: BF16 rows need a plain or folded-norm input launch and an output");
     RL_REQUIRE(!nrm.swiglu || (!nrm.ss_out && !accumulate && m % kTR == 0 && ldy >= m / 2), RL_ERR_RANGE,
                "kquant: the SwiGLU output needs whole gate / up half tiles, no accumulate and no add-norm output");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
