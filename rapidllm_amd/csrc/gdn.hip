@@ -35,6 +35,14 @@ constexpr int kMaxT = 8;
 constexpr int kConvK = 4;   // conv taps (Qwen3.6/3.8: 4)
 
 __device__ inline float silu_f(float x) { return x / (1.f + expf(-x)); }
+// The fused kernel's SiLU and inverse square roots on the per-token path use the
+// hardware approximations (exp2, reciprocal, rsq: about 1 ulp) instead of the
+// correctly rounded sequences, which were the longest stretches of each token's
+// dependent chain.
+__device__ inline float silu_fast(float x) {
+    return x * __builtin_amdgcn_rcpf(1.f + __builtin_amdgcn_exp2f(-x * 1.44269504088896341f));
+}
+__device__ inline float rsqrt_fast(float x) { return __builtin_amdgcn_rsqf(x); }
 __device__ inline float sigmoid_f(float x) { return 1.f / (1.f + expf(-x)); }
 __device__ inline float softplus_f(float x) { return log1pf(expf(-fabsf(x))) + fmaxf(x, 0.f); }
 
@@ -275,6 +283,10 @@ struct GdnFusedArgs {
     int row_off = 0, T_rows = 0;
 };
 
+// TT > 0: the token count as a compile-time constant (the per-token loops then have
+// no branches, so the compiler overlaps a token's independent work -- LDS reads,
+// norms, gates, conv -- with the previous token's state chain); 0: runtime p.T.
+template <int TT>
 __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const GdnArgs& p = a.g;
     const int tid = threadIdx.x;
@@ -289,7 +301,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const int rep = p.nv / p.nk;
     const int src = p.v_tiled ? (h % p.nk) : (h / rep);
     const int qdim = p.nk * kDK;
-    const int T = p.T;
+    const int T = TT > 0 ? TT : p.T;
     constexpr int K = kConvK;
     // sequence of the batch: state / ring / records / scalars at its strides, its
     // tokens are rows row0 .. row0 + T - 1 of T_tot
@@ -428,7 +440,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
             acc0 += static_cast<double>(w0[q]) * win0[q];
             acc1 += static_cast<double>(w1[q]) * win1[q];
         }
-        const float y0 = silu_f(static_cast<float>(acc0));
+        const float y0 = silu_fast(static_cast<float>(acc0));
         if (tid < kDK)
             q_s[t][tid] = y0;
         else if (qk_lane)
@@ -438,7 +450,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
             *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan0) * K) =
                 make_float4(win0[0], win0[1], win0[2], win0[3]);
         if (has_v) {
-            v_s[t][tid] = silu_f(static_cast<float>(acc1));
+            v_s[t][tid] = silu_fast(static_cast<float>(acc1));
             if (per_token || t == T - 1)
                 *reinterpret_cast<float4*>(conv_dst(t) + static_cast<size_t>(chan1) * K) =
                     make_float4(win1[0], win1[1], win1[2], win1[3]);
@@ -498,8 +510,8 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
 #pragma unroll
     for (int t = 0; t < kMaxT; ++t) {
         if (t >= T) break;
-        const float iq = 1.f / sqrtf(static_cast<float>(red_s[0][t] + red_s[1][t]) + 1e-6f);
-        const float ik = 1.f / sqrtf(static_cast<float>(red_s[2][t] + red_s[3][t]) + 1e-6f);
+        const float iq = rsqrt_fast(static_cast<float>(red_s[0][t] + red_s[1][t]) + 1e-6f);
+        const float ik = rsqrt_fast(static_cast<float>(red_s[2][t] + red_s[3][t]) + 1e-6f);
         const float g = gate_s[t][0], beta = gate_s[t][1];
         float kn[kCRows];
 #pragma unroll
@@ -530,7 +542,7 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
             if (keep) rec_w[t * rec_t + kDK + j] = delta;
             if (gn) {
                 o_s[t][jj] = ov;
-                y_s[t][jj] = gam * ov * silu_f(zt[t]);
+                y_s[t][jj] = gam * ov * silu_fast(zt[t]);
             }
         }
     }
@@ -815,7 +827,14 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                "gdn_decode_fused: token rows out of range");
     RL_REQUIRE(p.batch.B >= 1 && p.batch.B * T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: batch x T must be <= 8");
     RL_REQUIRE(p.batch.B == 1 || cur, RL_ERR_RANGE, "gdn_decode_fused: a batch needs the conv ring");
-    hipLaunchKernelGGL(gdn_fused_kernel, dim3(nv * (dv / kCW), p.batch.B), dim3(kCT), 0, s, p);
+    const dim3 grid(nv * (dv / kCW), p.batch.B);
+    switch (T) {
+    case 1: hipLaunchKernelGGL(gdn_fused_kernel<1>, grid, dim3(kCT), 0, s, p); break;
+    case 2: hipLaunchKernelGGL(gdn_fused_kernel<2>, grid, dim3(kCT), 0, s, p); break;
+    case 3: hipLaunchKernelGGL(gdn_fused_kernel<3>, grid, dim3(kCT), 0, s, p); break;
+    case 4: hipLaunchKernelGGL(gdn_fused_kernel<4>, grid, dim3(kCT), 0, s, p); break;
+    default: hipLaunchKernelGGL(gdn_fused_kernel<0>, grid, dim3(kCT), 0, s, p); break;
+    }
     check_launch("gdn_fused_kernel");
 }
 
