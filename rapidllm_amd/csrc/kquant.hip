@@ -362,8 +362,12 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
 #pragma unroll
             for (int e = 0; e < 16; ++e) mx = fmaxf(mx, fabsf(v[e]));
             mx = fmaxf(mx, __shfl_xor(mx, 1, 64));  // the 32-value block's maximum
-            const float sc = mx / 127.f;
-            const float inv = mx > 0.f ? 127.f / mx : 0.f;
+            // hardware reciprocal (about 1 ulp): the quantised values stay in
+            // [-127, 127] (|v * inv| <= 127 (1 + 2^-22) rounds to 127) and x ~ sc * (hi +
+            // lo / 254) to the same 15 bits; the correctly rounded divisions were two
+            // long sequences per item on every workgroup's path to its first tile
+            const float sc = mx * (1.f / 127.f);
+            const float inv = mx > 0.f ? 127.f * __builtin_amdgcn_rcpf(mx) : 0.f;
             int hi[16], lo[16], shi = 0, slo = 0;
 #pragma unroll
             for (int e = 0; e < 16; ++e) {
