@@ -59,7 +59,28 @@ struct AttnArgs {
     int max_chunks;
     float* out;     // optional [T][nq*hd]
     i32x4* frag;    // optional o_proj fragments (n = nq*hd)
+    // batch decode: nb sequences ("slots") in one launch set.  Slot b's token t is
+    // row b*T + t of Y and output column t_off + b*T + t; its cache, position and
+    // workspace (qf, partials) sit kv_bstride elements, pos_stride ints and ws_slot
+    // bytes after slot b-1's.
+    int nb;
+    size_t kv_bstride;
+    int pos_stride;
+    size_t ws_slot;
 };
+
+// Arguments of slot b (uniform per workgroup: the offsets stay in scalar registers).
+__device__ inline void to_slot(AttnArgs& p, int b) {
+    p.kc += b * p.kv_bstride;
+    p.vt += b * p.kv_bstride;
+    p.pos += b * p.pos_stride;
+    p.Y += static_cast<size_t>(b) * p.T * p.ld_y;
+    p.qf = reinterpret_cast<i32x4*>(reinterpret_cast<char*>(p.qf) + b * p.ws_slot);
+    p.part_o = reinterpret_cast<float*>(reinterpret_cast<char*>(p.part_o) + b * p.ws_slot);
+    p.part_m = reinterpret_cast<float*>(reinterpret_cast<char*>(p.part_m) + b * p.ws_slot);
+    p.part_l = reinterpret_cast<float*>(reinterpret_cast<char*>(p.part_l) + b * p.ws_slot);
+    p.t_off += b * p.T;
+}
 
 __host__ __device__ inline int pair_tiles(int G, int T) { return (G * T + 15) / 16; }
 
@@ -77,9 +98,10 @@ __host__ __device__ inline size_t v_off(int pos, int d) {
     return (((static_cast<size_t>(pos >> 5) * 16 + (d >> 4)) * 4 + ((pos >> 3) & 3)) * 16 + (d & 15)) * 8 + (pos & 7);
 }
 
-// grid (nq + 2*nkv, T), 64 threads.  Heads [0,nq): q; [nq, nq+nkv): k; then v.
+// grid (nq + 2*nkv, T, slots), 64 threads.  Heads [0,nq): q; [nq, nq+nkv): k; then v.
 __global__ __launch_bounds__(64) void qk_prep_kernel(AttnArgs p) {
     __shared__ float vec[kHD];
+    to_slot(p, blockIdx.z);
     const int head = blockIdx.x, t = blockIdx.y, lane = threadIdx.x;
     const int pos = *p.pos + t;
     const float* row = p.Y + static_cast<size_t>(t) * p.ld_y;
@@ -146,9 +168,12 @@ union H8 {
 
 template <int PT>
 __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
-    // chunk-major dispatch order: the chunks past the current position (early exit)
-    // come last, so the active workgroups spread evenly over the CUs
-    const int chunk = blockIdx.x / p.nkv, kv = blockIdx.x % p.nkv;
+    // chunk-major dispatch order (kv head fastest, then slot): the chunks past the
+    // current position (early exit) come last, so the active workgroups spread
+    // evenly over the CUs
+    const int kv = blockIdx.x % p.nkv;
+    const int chunk = blockIdx.x / p.nkv / p.nb;
+    to_slot(p, (blockIdx.x / p.nkv) % p.nb);
     const int p0 = *p.pos;
     const int L = p0 + p.T;  // keys 0 .. L-1 exist after this step's writes
     const int c0 = chunk * kChunk;
@@ -304,15 +329,17 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     }
 }
 
-// grid (G*T pairs, nkv, hd/64), 256 threads = 4 chunk groups x 64 dims.
+// grid (G*T pairs, nkv, slots * hd/64), 256 threads = 4 chunk groups x 64 dims.
 // Chunk weights w_c = exp(m_c - M) are computed once into LDS; each thread sums
 // its chunk group's O_c[d] * w_c, the 4 groups are added in a fixed order.
 constexpr int kMaxChunksLds = 4096;  // 1M positions
 
 __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
     const int k = blockIdx.x, kv = blockIdx.y;
+    const int dz = blockIdx.z % (kHD / 64);
+    to_slot(p, blockIdx.z / (kHD / 64));
     const int tid = threadIdx.x, q = tid >> 6, dl = tid & 63;
-    const int d = blockIdx.z * 64 + dl;
+    const int d = dz * 64 + dl;
     const int t = k / p.G;
     const int h = kv * p.G + k % p.G;
     const int L = *p.pos + p.T;
@@ -360,7 +387,7 @@ __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
         red[1][dl] = val;  // wave 0 only from here on: reuse a row of red
         __builtin_amdgcn_wave_barrier();
         if (dl < 8) {  // 8 units of 8 columns cover this workgroup's 64 dims
-            const int unit = (h * kHD + blockIdx.z * 64) / 8 + dl;
+            const int unit = (h * kHD + dz * 64) / 8 + dl;
             union {
                 uint16_t hh[8];
                 i32x4 v;
@@ -615,15 +642,19 @@ namespace rl {
 size_t attn_workspace_bytes(int nkv, int ctx) {
     const size_t chunks = static_cast<size_t>(ctx) / kChunk;
     const size_t qf = static_cast<size_t>(nkv) * 8 * 4 * 4 * 16 * 16;  // PT <= 2
-    return qf + static_cast<size_t>(nkv) * chunks * kMaxPairs * (kHD + 2) * 4 + 256;
+    return (qf + static_cast<size_t>(nkv) * chunks * kMaxPairs * (kHD + 2) * 4 + 256 + 255) / 256 * 256;
 }
 
 void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,
                        int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot, float theta, float eps,
-                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s, int t_off, int T_out) {
+                       void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s, int t_off, int T_out, int nb,
+                       size_t kv_bstride, int pos_stride) {
     RL_REQUIRE(hd == kHD, RL_ERR_UNSUPPORTED, "attn: head_dim must be 256");
-    if (T_out <= 0) T_out = T;
-    RL_REQUIRE(t_off >= 0 && t_off + T <= T_out && T_out <= 8, RL_ERR_RANGE, "attn: bad output columns");
+    RL_REQUIRE(nb >= 1 && nb <= 64, RL_ERR_RANGE, "attn: slot count must be in 1..64");
+    if (T_out <= 0) T_out = T * nb;
+    RL_REQUIRE(t_off >= 0 && t_off + nb * T <= T_out && T_out <= 8, RL_ERR_RANGE, "attn: bad output columns");
+    RL_REQUIRE(nb == 1 || (kv_bstride >= static_cast<size_t>(nkv) * ctx * kHD && pos_stride >= 1), RL_ERR_RANGE,
+               "attn: slot strides must separate the slots' caches and positions");
     RL_REQUIRE(nkv > 0 && nq % nkv == 0, RL_ERR_RANGE, "attn: n_q must be a multiple of n_kv");
     const int G = nq / nkv;
     RL_REQUIRE(T >= 1 && G * T <= kMaxPairs, RL_ERR_RANGE, "attn: (n_q/n_kv) * T must be <= 32");
@@ -631,7 +662,7 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     RL_REQUIRE(ctx / kChunk <= kMaxChunksLds, RL_ERR_RANGE, "attn: cache capacity above 1M positions");
     RL_REQUIRE(rot >= 2 && rot % 2 == 0 && rot <= hd, RL_ERR_RANGE, "attn: bad rotary dim");
     RL_REQUIRE(Y && kc && vt && pos_dev && ws && (out || frag), RL_ERR_RANGE, "attn: null pointer");
-    RL_REQUIRE(ws_bytes >= attn_workspace_bytes(nkv, ctx), RL_ERR_RANGE, "attn: workspace too small");
+    RL_REQUIRE(ws_bytes >= nb * attn_workspace_bytes(nkv, ctx), RL_ERR_RANGE, "attn: workspace too small");
     const int chunks = ctx / kChunk;
     char* w = static_cast<char*>(ws);
     AttnArgs p{};
@@ -662,14 +693,18 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     p.frag = static_cast<i32x4*>(frag);
     p.t_off = t_off;
     p.T_out = T_out;
-    hipLaunchKernelGGL(qk_prep_kernel, dim3(nq + 2 * nkv, T), dim3(64), 0, s, p);
+    p.nb = nb;
+    p.kv_bstride = kv_bstride;
+    p.pos_stride = pos_stride;
+    p.ws_slot = attn_workspace_bytes(nkv, ctx);
+    hipLaunchKernelGGL(qk_prep_kernel, dim3(nq + 2 * nkv, T, nb), dim3(64), 0, s, p);
     check_launch("qk_prep_kernel");
     if (pair_tiles(G, T) == 1)
-        hipLaunchKernelGGL(attn_part_kernel<1>, dim3(chunks * nkv), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_part_kernel<1>, dim3(chunks * nkv * nb), dim3(256), 0, s, p);
     else
-        hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks * nkv), dim3(256), 0, s, p);
+        hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks * nkv * nb), dim3(256), 0, s, p);
     check_launch("attn_part_kernel");
-    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv, kHD / 64), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv, (kHD / 64) * nb), dim3(256), 0, s, p);
     check_launch("attn_comb_kernel");
 }
 

@@ -956,7 +956,8 @@ class Engine {
         mtp_hp_ = mem_.get_n<float>(H);
         h_last_ = mem_.get_n<float>(H);
         h_prev_ = mem_.get_n<float>(H);
-        attn_ws_bytes_ = attn_workspace_bytes(std::max(nkv, 1), ctx_);
+        // one workspace per batch slot (batch decode runs all slots' attention at once)
+        attn_ws_bytes_ = attn_workspace_bytes(std::max(nkv, 1), ctx_) * mb_;
         attn_ws_ = mem_.get(attn_ws_bytes_);
         arg_ws_ = mem_.get(argmax_workspace_bytes(T, c_.vocab));
         kq_ws_bytes_ = std::max<size_t>(kq_need_, 256);
@@ -1843,11 +1844,11 @@ class Engine {
             } else {
                 gemm_on(Ly.qkv_parts[0], frag_x_, ybuf_, Ly.qkv_width, Ly.qkv_parts[0].m, B, kEpiStore, nullptr,
                         io_in);
-                for (int b = 0; b < B; ++b)
-                    attn_decode_layer(ybuf_ + static_cast<size_t>(b) * Ly.qkv_width, Ly.qkv_width, Ly.q_norm,
-                                      Ly.k_norm, kc_[Ly.aslot] + b * kv_bstride_, vt_[Ly.aslot] + b * kv_bstride_,
-                                      ctx_, scal_ + b * kScalars + kPos, 1, nq, nkv, hd, c_.rotary_dim,
-                                      c_.rope_theta, eps, attn_ws_, attn_ws_bytes_, xn_, frag_, st_, b, B);
+                // all slots in one launch set (slot b: its own cache, position and
+                // workspace; output column b)
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
+                                  scal_ + kPos, 1, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                                  attn_ws_bytes_, xn_, frag_, st_, 0, B, B, kv_bstride_, kScalars);
                 gemm_on(Ly.o_proj, frag_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
             }
             gemm_on(Ly.gate_up, frag_x_, nullptr, I, I, B, Ly.gate_up.swiglu_epi(), frag_h_, &in);

@@ -196,7 +196,7 @@ size_t attn_workspace_bytes(int nkv, int ctx);
 void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const float* k_norm, uint16_t* kc, uint16_t* vt,
                        int ctx, const int* pos_dev, int T, int nq, int nkv, int hd, int rot, float theta, float eps,
                        void* ws, size_t ws_bytes, float* out, void* frag, hipStream_t s, int t_off = 0,
-                       int T_out = 0);
+                       int T_out = 0, int nb = 1, size_t kv_bstride = 0, int pos_stride = 0);
 
 // Prompt prefill of T tokens at *pos_dev .. *pos_dev + T - 1: K/V of all T written to
 // the cache, causal attention over the cache, out [T][nq*hd] fp32 (times sigmoid(gate)).
