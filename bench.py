@@ -36,15 +36,19 @@ PF_TOKENS = 4096
 def measure_gguf_step(spec, K, W):
     """The same C5 step with the layer linears and MTP fc as Q4_K super-blocks and a
     Q6_K lm_head (the tensor mix of a Q4_K_M GGUF; in_proj a/b BF16), random blocks
-    generated on the device: T=1 and T=4 step times and the weight bytes a T=1 step
-    reads."""
+    generated on the device: T=1 and T=4 step times, the batch-4 step (four
+    sequences at 32K context) and the weight bytes a T=1 step reads."""
     from rapidllm_amd.engine import Engine
 
     os.environ["RL_SYNTH_LINEAR"] = "q4_k"
     try:
-        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321)
+        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321, max_batch=4)
     finally:
         del os.environ["RL_SYNTH_LINEAR"]
+    eng.synthetic_context(CTX)
+    eng.replicate_slot0(4)
+    eng.time_batch(4, W)
+    tb4 = eng.time_batch(4, K) / K
     eng.synthetic_context(CTX)
     eng.time_steps(1, W)
     t1 = eng.time_steps(1, K) / K
@@ -69,7 +73,8 @@ def measure_gguf_step(spec, K, W):
     return {"workload": "C5 step, Q4_K layer linears + Q6_K lm_head (Q4_K_M mix), 32K context",
             "t1_ms": round(t1, 4), "tok_s": round(1000.0 / t1, 3), "t4_verify_ms": round(t4, 4),
             "t4_over_t1": round(t4 / t1, 4), "t1_bytes": int(total),
-            "t1_GBps": round(total / t1 / 1e6, 1), "t1_frac": round(total / t1 / 1e6 / PEAK_GBS, 4)}
+            "t1_GBps": round(total / t1 / 1e6, 1), "t1_frac": round(total / t1 / 1e6 / PEAK_GBS, 4),
+            "batch4_step_ms": round(tb4, 4), "batch4_tok_s": round(4000.0 / tb4, 3)}
 
 
 def step_bytes(spec, T, ctx):

@@ -909,11 +909,14 @@ class Engine {
         }
         // one committed S per layer plus R banks of per-token records with the fused
         // kernel, a ring of R states with the unfused one
-        // step_batch runs every linear through the folded FP8/BF16 GEMM, so batch
-        // decode needs folded norms (no K-quant linears) and, with DeltaNet layers,
-        // the fused DeltaNet kernel
-        RL_REQUIRE(mb_ == 1 || (fold_norm_ && (gdn_fused_norm_ || nd == 0)), RL_ERR_UNSUPPORTED,
-                   "engine: batch decode needs FP8/BF16 linears with folded norms (and v_dim 128 for DeltaNet)");
+        // batch decode runs the folded-norm steps with B rows: FP8/BF16 linears
+        // (step_batch) or K-quant linears (step_kq_folded, at most 4 rows), and with
+        // DeltaNet layers the fused DeltaNet kernel over the slots' states
+        RL_REQUIRE(mb_ == 1 || (fold_norm_ && (gdn_fused_norm_ || nd == 0)) ||
+                       (kq_fold_ && tcap_ <= 4 && (gdn_fused_ || nd == 0)),
+                   RL_ERR_UNSUPPORTED,
+                   "engine: batch decode needs folded norms: FP8/BF16 linears (v_dim 128 for DeltaNet), or "
+                   "K-quant linears with max_batch <= 4 and the fused DeltaNet kernel");
         s_bstride_ = s_slot_ * (gdn_fused_ ? 1 : R_);
         rec_bstride_ = static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats;
         recn_bstride_ = R_ * nv;
@@ -1510,7 +1513,11 @@ class Engine {
     // first linears read the normalised rows; from then on the residual GEMVs add
     // into x in place and leave the sums of squares (and x * (1 + gamma) fragments)
     // for the next linears.
-    void step_kq_folded(int T, int force_all, bool feed) {
+    // B > 1: the batch step (T == B rows, one token of each slot b at its own
+    // position; the DeltaNet kernel and attention run over the B slots' states and
+    // caches, and batch_advance replaces the acceptance)
+    void step_kq_folded(int T, int force_all, bool feed, int B = 1) {
+        const int Ts = B > 1 ? 1 : T;  // tokens per sequence
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
@@ -1591,18 +1598,24 @@ class Engine {
                                        kEpiPartial, L.m, L.m, st_, kAbSlices, nullptr, iop);
                 }
                 if (gdn_fused_) {
-                    const GdnRecords rec{slot_rec(Ly.dslot), slot_recn(Ly.dslot), sc() + kNCons, tmax_,
-                                         T > 1 && !force_all};
+                    const bool bat = B > 1;
+                    const GdnRecords rec{bat ? rec_[Ly.dslot] : slot_rec(Ly.dslot),
+                                         bat ? rec_n_[Ly.dslot] : slot_recn(Ly.dslot), bat ? scal_ + kNCons : sc() + kNCons,
+                                         tmax_, Ts > 1 && !force_all};
+                    const GdnBatch bt{B, s_bstride_, conv_bstride_, rec_bstride_, recn_bstride_, kScalars};
                     const bool split = ab_part >= 0;
                     const int ab_rows = split ? Ly.in_parts[ab_part].m : 0;
                     gdn_decode_fused(ybuf_, split ? kq_abpart_ : ybuf_ + Ly.off_a,
                                      split ? kq_abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b, Ly.in_width,
-                                     Ly.A_log, Ly.dt_bias, Ly.conv_w, slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot),
-                                     slot_S(Ly.dslot), sc() + kSlot, conv_slot_, R_, &rec, kq_gnorm_ ? nullptr : o_,
+                                     Ly.A_log, Ly.dt_bias, Ly.conv_w, bat ? conv_[Ly.dslot] : slot_conv(Ly.dslot), nullptr,
+                                     bat ? S_[Ly.dslot] : slot_S(Ly.dslot), bat ? S_[Ly.dslot] : slot_S(Ly.dslot),
+                                     bat ? scal_ + kSlot : sc() + kSlot, conv_slot_, R_, &rec, kq_gnorm_ ? nullptr : o_,
                                      kq_gnorm_ ? ybuf_ + Ly.off_z : nullptr, kq_gnorm_ ? Ly.gnorm : nullptr, nullptr,
-                                     kq_gnorm_ ? gss_ : nullptr, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_,
-                                     split ? kAbSlices : 1, ab_rows, nullptr, 0, 0, kq_gnorm_ ? xn_ : nullptr);
+                                     kq_gnorm_ ? gss_ : nullptr, Ts, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_,
+                                     split ? kAbSlices : 1, ab_rows, bat ? &bt : nullptr, 0, 0,
+                                     kq_gnorm_ ? xn_ : nullptr);
                 } else {
+                    RL_REQUIRE(B == 1, RL_ERR_UNSUPPORTED, "engine: batch decode needs the fused DeltaNet kernel");
                     gdn_decode(ybuf_, ybuf_ + Ly.off_a, ybuf_ + Ly.off_b, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w,
                                slot_conv(Ly.dslot), nullptr, slot_S(Ly.dslot), nullptr, sc() + kSlot, conv_slot_, s_slot_,
                                R_, o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
@@ -1617,9 +1630,14 @@ class Engine {
             } else {
                 for (size_t k = 0; k < Ly.qkv_parts.size(); ++k)
                     consume(Ly.qkv_parts[k], ybuf_ + Ly.qkv_offs[k], Ly.qkv_width, Ly.qkv_parts[k].m);
-                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot), ctx_,
-                                  sc() + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
-                                  attn_ws_bytes_, xn_, frag_, st_);
+                if (B > 1)
+                    attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
+                                      scal_ + kPos, 1, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                                      attn_ws_bytes_, xn_, frag_, st_, 0, B, B, kv_bstride_, kScalars);
+                else
+                    attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot),
+                                      ctx_, sc() + kPos, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                                      attn_ws_bytes_, xn_, frag_, st_);
                 produce(Ly.o_proj, xn_, Ly.ffn_norm);
             }
             if (Ly.gate_up.kind >= 0) {
@@ -1643,9 +1661,13 @@ class Engine {
             }
             produce(Ly.down, h_, i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_);
         }
-        x_ = x;  // hidden after the layers (pre final norm), for the MTP history
         consume(lm_head_, logits_, c_.vocab, c_.vocab);
         argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
+        if (B > 1) {
+            batch_advance(scal_, kScalars, B, R_, kPos, kSlot, kNCons, st_);
+            return;
+        }
+        x_ = x;  // hidden after the layers (pre final norm), for the MTP history
         accept(tok_, preds_, T, force_all, sc() + kPos, sc() + kSlot, R_, sc() + kNCons, sc() + kNextTok, gen_,
                sc() + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
     }
@@ -1801,6 +1823,10 @@ class Engine {
     // folded-norm linears with B rows, the DeltaNet kernel over the B slots, attention
     // per slot writing its column of o_proj's input.
     void step_batch(int B) {
+        if (kq_fold_) {
+            step_kq_folded(B, 0, false, B);
+            return;
+        }
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
         const int nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;

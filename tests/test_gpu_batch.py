@@ -189,16 +189,59 @@ def test_batch_decode_vs_oracle(gpu, orc, B):
     eng.close()
 
 
+KQ_CASES = [([0, 0, 0, 1], M.Q_Q4_K, 2), ([0, 1], M.Q_Q6_K, 4), ([1, 1], M.Q_Q4_K, 3), ([0, 0], M.Q_Q4_K, 4)]
+
+
+@pytest.mark.parametrize("kinds,quant,B", KQ_CASES)
+def test_kquant_batch_decode_vs_oracle(gpu, orc, kinds, quant, B):
+    """Batch decode of a K-quant (GGUF Q4_K / Q6_K) model: each slot against its own
+    oracle model (session.cpp:325-411) with different prompts and positions, and
+    every slot's logits equal to single-sequence decoding of that sequence bit for
+    bit (the K-quant GEMV quantises each row's x on its own and sums the split-K
+    slices in a fixed order, whatever the row count)."""
+    spec = mini_spec(n_layers=len(kinds), layer_kinds=kinds)
+    W = M.random_weights(spec, seed=70 + B, linear_quant=quant, w_scale=(1e-3, 1e-2))
+    eng = Engine(spec, W, ctx=512, max_batch=4)
+    ref = Engine(spec, W, ctx=512)
+    rng = np.random.default_rng(80 + B)
+    prompts = [[int(t) for t in rng.integers(0, spec.vocab, 2 + 3 * b)] for b in range(B)]
+    oms = [OracleModel(spec, W, ctx=512) for _ in range(B)]
+    n = 4
+    want = [plain_chain(ref, p, n + 1) for p in prompts]
+    toks, poss = [], []
+    for b, p in enumerate(prompts):
+        eng.prefill_slot(p, b)
+        for t in p:
+            g, lg, _ = oms[b].decode(t)
+        assert rel_l2(eng.copy_logits(), lg) < TOL
+        toks.append(want[b][0][0])
+        poss.append(len(p))
+    for step in range(1, n + 1):
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(B)
+        greedy = eng.copy_greedy_n(B)
+        for b in range(B):
+            assert np.array_equal(rows[b], want[b][1][step]), (kinds, B, step, b)
+            assert greedy[b] == want[b][0][step]
+            g, lg, _ = oms[b].decode(toks[b])
+            assert rel_l2(rows[b], lg) < TOL, (kinds, B, step, b, rel_l2(rows[b], lg))
+            if margin_ok(lg):
+                assert greedy[b] == g, (kinds, B, step, b)
+        toks = greedy
+        poss = [p + 1 for p in poss]
+    eng.close()
+    ref.close()
+
+
 @pytest.mark.parametrize("kinds,quant", [([1, 1], M.Q_Q4_K), ([0, 1], M.Q_Q6_K)])
-def test_batch_refused_for_kquant_models(gpu, kinds, quant):
-    """The batch step runs every linear through the folded FP8 / BF16 GEMM, so a
-    K-quant model (with or without DeltaNet layers) with max_batch > 1 is refused
-    at creation with RL_ERR_UNSUPPORTED instead of running K-quant tiles as BF16."""
+def test_kquant_batch_above_four_refused(gpu, kinds, quant):
+    """The K-quant GEMV takes at most 4 rows, so a K-quant model with max_batch > 4
+    is refused at creation with RL_ERR_UNSUPPORTED; max_batch 4 builds."""
     from rapidllm_amd import hip
 
     spec = mini_spec(n_layers=2, layer_kinds=kinds)
     W = M.random_weights(spec, seed=9, linear_quant=quant)
     with pytest.raises(hip.HipError) as ei:
-        Engine(spec, W, ctx=256, max_batch=2)
+        Engine(spec, W, ctx=256, max_batch=5)
     assert ei.value.code == 4  # RL_ERR_UNSUPPORTED
-    Engine(spec, W, ctx=256, max_batch=1).close()
+    Engine(spec, W, ctx=256, max_batch=4).close()
