@@ -245,3 +245,26 @@ def test_kquant_batch_above_four_refused(gpu, kinds, quant):
         Engine(spec, W, ctx=256, max_batch=5)
     assert ei.value.code == 4  # RL_ERR_UNSUPPORTED
     Engine(spec, W, ctx=256, max_batch=4).close()
+
+
+def test_batch_attention_across_chunk_boundaries(gpu, batch_pair):
+    """Slots whose positions straddle the attention's 256-position chunks (one slot
+    crossing 255 -> 256 during the steps, one starting in the second chunk, one at
+    position 1): the one attention launch set over all slots reads each slot's own
+    position, cache and workspace, so every row equals plain decoding bit for bit."""
+    spec, eng, ref = batch_pair
+    eng.zero_slots(4)
+    rng = np.random.default_rng(91)
+    lens = [253, 1, 256, 40]
+    prompts = [[int(t) for t in rng.integers(0, spec.vocab, n)] for n in lens]
+    n = 5
+    want = [plain_chain(ref, p, n) for p in prompts]
+    for b, p in enumerate(prompts):
+        eng.prefill_slot(p, b)
+    toks, poss = [w[0][0] for w in want], list(lens)
+    for step in range(1, n):
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(4)
+        for b in range(4):
+            assert np.array_equal(rows[b], want[b][1][step]), (step, b, poss[b])
+        toks, poss = eng.copy_greedy_n(4), [p + 1 for p in poss]
