@@ -295,10 +295,25 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const int jj = tid / kCChunks;  // column within the chunk
     const int dv = p.dv;
     const int chunks = dv / kCW;
-    const int h = blockIdx.x / chunks;
-    const int cc = blockIdx.x % chunks;
-    const int j = cc * kCW + jj;
     const int rep = p.nv / p.nk;
+    // XCD-aware order: workgroups are dispatched to the 8 XCDs round-robin
+    // (blockIdx % 8), each XCD with its own L2.  With n_k a multiple of 8, XCD x
+    // takes whole k-heads (all rep v-heads x chunks workgroups of each), so a
+    // k-head's q/k conv window, weights and inputs are fetched into one L2 and
+    // shared by its workgroups; otherwise workgroup = (v-head, chunk) in order.
+    int h, cc;
+    if (p.nk % 8 == 0) {
+        const int M = rep * chunks;  // workgroups per k-head
+        const int x = blockIdx.x % 8, jx = blockIdx.x / 8;
+        const int g = x * (p.nk / 8) + jx / M, m = jx % M;
+        const int r = m / chunks;
+        cc = m % chunks;
+        h = p.v_tiled ? g + r * p.nk : g * rep + r;
+    } else {
+        h = blockIdx.x / chunks;
+        cc = blockIdx.x % chunks;
+    }
+    const int j = cc * kCW + jj;
     const int src = p.v_tiled ? (h % p.nk) : (h / rep);
     const int qdim = p.nk * kDK;
     const int T = TT > 0 ? TT : p.T;
