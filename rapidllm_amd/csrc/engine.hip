@@ -492,7 +492,8 @@ class Engine {
     int max_batch() const { return mb_; }
 
     // One token for each of B sequences (slot b at position poss[b]) in one weight
-    // pass: the linears run with B rows, DeltaNet and attention per slot.
+    // pass: the linears run with B rows, DeltaNet and attention over the B slots'
+    // states and caches.
     void decode_tokens(const int32_t* tokens, const int* poss, int B) {
         RL_REQUIRE(B >= 1 && B <= mb_ && tokens && poss, RL_ERR_RANGE, "decode_tokens: B out of range");
         check_ids(tokens, B);
@@ -1820,8 +1821,9 @@ class Engine {
     }
 
     // Batch step: B sequences, one token each (tok_[b] at slot b's position); the
-    // folded-norm linears with B rows, the DeltaNet kernel over the B slots, attention
-    // per slot writing its column of o_proj's input.
+    // folded-norm linears with B rows, the DeltaNet kernel over the B slots, one
+    // attention launch set over the slots (slot b writes column b of o_proj's
+    // input).  K-quant models run the K-quant step with B rows.
     void step_batch(int B) {
         if (kq_fold_) {
             step_kq_folded(B, 0, false, B);
