@@ -268,3 +268,34 @@ def test_batch_attention_across_chunk_boundaries(gpu, batch_pair):
         for b in range(4):
             assert np.array_equal(rows[b], want[b][1][step]), (step, b, poss[b])
         toks, poss = eng.copy_greedy_n(4), [p + 1 for p in poss]
+
+
+@pytest.mark.parametrize("quant", [M.Q_Q4_K, M.Q_Q6_K])
+def test_kquant_batch_then_speculative_on_one_engine(gpu, quant):
+    """A K-quant engine alternating between batch and single-sequence work: slot 0
+    replicated into 3 slots and decoded as a batch, Session-style generate_batch with
+    distinct prompts, then speculative (MTP, spec_n = 3) generation on slot 0.  Every
+    token equals plain greedy decoding on a separate single-slot engine, so the batch
+    steps leave no state behind that the verify's rollback reads."""
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=123, linear_quant=quant, w_scale=(1e-3, 1e-2))
+    eng, ref = Engine(spec, W, ctx=512, max_batch=4), Engine(spec, W, ctx=512)
+    prompt = [7, 3, 9, 1, 4, 4]
+    toks, _ = plain_chain(ref, prompt, 6)
+    eng.prefill(prompt)
+    eng.replicate_slot0(3)
+    t, poss = [toks[0]] * 3, [len(prompt)] * 3
+    for step in range(1, 6):
+        eng.decode_tokens(t, poss)
+        g = eng.copy_greedy_n(3)
+        assert g == [toks[step]] * 3, step
+        t, poss = g, [p + 1 for p in poss]
+    prompts = [[5, 6, 7], [1, 2, 3, 4, 5, 6, 7, 8], [9]]
+    outs = eng.generate_batch(prompts, 4)
+    for b, p in enumerate(prompts):
+        assert outs[b] == plain_chain(ref, p, 4)[0], b
+    plain, _, _ = ref.generate(prompt, 12, spec_n=0)
+    on, prop, acc = eng.generate(prompt, 12, spec_n=3)
+    assert on == plain and prop > 0
+    eng.close()
+    ref.close()
