@@ -183,18 +183,18 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     i32x4 bbuf[D][4];
     float sbuf[D][RT];
     float sbuf2[D][RT];  // kGuh: the up half's scale
-    // kKs: the four partial sums of squares of this wave's blocks for this lane's
-    // token, all loaded before the weight stream (blocks w + i*KSPLIT, i < kKsMaxIt)
+    // kKs: this lane's token (B column hi / mid of token ktok) and the block scale
+    // 1 / rms of the block's four partial sums of squares
     const int ktok = bcol < T ? bcol : bcol - T;
     const float kss_inv_n = kKs ? 1.f / static_cast<float>(io.kss_n) : 0.f;
-    float4 kq[kKs ? kKsMaxIt : 1];
-    if constexpr (kKs) {
-#pragma unroll
-        for (int i = 0; i < kKsMaxIt; ++i) {
-            const int kb = min(s_begin + wave + i * KSPLIT, n_kb - 1);
-            kq[i] = reinterpret_cast<const float4*>(io.kss)[static_cast<size_t>(kb) * T + ktok];
-        }
-    }
+    auto block_sums = [&](int kb) {
+        // this lane's token's four sums of the block, requested just before the
+        // block's weights (loads return in issue order, so they are there first)
+        return reinterpret_cast<const float4*>(io.kss)[static_cast<size_t>(kb) * T + ktok];
+    };
+    auto block_scale = [&](const float4 q) {
+        return __builtin_amdgcn_rsqf(((q.x + q.y) + (q.z + q.w)) * kss_inv_n + io.kss_eps);
+    };
     // kb >= kb_end: a pipeline slot past the wave's range.  Its loads still issue (so
     // the load count is the same on every path) but read the small, cache-resident
     // activation fragments instead of weights; the values are never used.
@@ -290,13 +290,10 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         // Wave w takes blocks w, w + KSPLIT, ...: at any moment the workgroup reads
         // KSPLIT adjacent tiles per row-tile (1-3% faster than contiguous runs)
         if constexpr (kKs) {
-#pragma unroll
-            for (int i = 0; i < kKsMaxIt; ++i) {
-                const int kb = s_begin + wave + i * KSPLIT;
-                if (kb >= s_end) break;
+            for (int kb = s_begin + wave; kb < s_end; kb += KSPLIT) {
+                const float4 q = block_sums(kb);
                 load(0, kb, true);
-                const float4 q = kq[i];
-                compute(0, kb, __builtin_amdgcn_rsqf(((q.x + q.y) + (q.z + q.w)) * kss_inv_n + io.kss_eps));
+                compute(0, kb, block_scale(q));
             }
         } else {
             for (int kb = s_begin + wave; kb < s_end; kb += KSPLIT) {
