@@ -899,8 +899,7 @@ class Engine {
         // DeltaNet kernel, when one workgroup can hold a head
         {
             const int zd = c_.n_v_heads * c_.v_dim;
-            bool per_head = gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && c_.v_dim == 128 && zd >= 256 &&
-                            zd <= 8192;  // out_proj's block-scale GEMM: n <= 8192
+            bool per_head = gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && c_.v_dim == 128 && zd >= 256;
             for (const Layer& Ly : L_)
                 if (Ly.kind == RL_LAYER_DELTA && Ly.gnorm_n != c_.v_dim) per_head = false;
             gdn_fused_norm_ = fold_norm_ && per_head;

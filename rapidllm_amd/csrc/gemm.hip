@@ -59,9 +59,7 @@ enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4, k
 // Grid: one workgroup per RT row-tiles.  Each workgroup: KSPLIT waves, each wave a
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
 // weights in flight while one is computed).
-// kKs: per-column-block input scale (NormIO::kss, the folded gated RMSNorm); depth 1
-// and at most kKsMaxIt column blocks per wave.
-constexpr int kKsMaxIt = 8;
+// kKs: per-column-block input scale (NormIO::kss, the folded gated RMSNorm); depth 1.
 // TT > 0: T is the compile-time token count TT, and each column block's activation
 // fragments (16 * 2T units of 16 B) are fetched by 1, 2 or 4 coalesced loads (every
 // lane one distinct unit) and handed to the lanes that need them by ds_bpermute.
@@ -738,7 +736,6 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     if (io.kss) {
         // folded gated norm (out_proj): the residual configuration only
         RL_REQUIRE(!io.ss_in && io.kss_n > 0 && S == 1, RL_ERR_RANGE, "gemm: bad block input scale");
-        RL_REQUIRE(n_kb <= kKsMaxIt * 8, RL_ERR_UNSUPPORTED, "gemm: block input scale needs n <= 8192");
         RL_REQUIRE(!g_force.rt, RL_ERR_UNSUPPORTED, "gemm: block input scale uses the residual work split");
         launch_gemm_cfg<kFp8, 2, 8, 1, true>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out,
                                              io, s);

@@ -186,19 +186,20 @@ def _unpack_frag(raw, n, T):
     return val.transpose(3, 0, 2, 1, 4).reshape(T, n)
 
 
-@pytest.mark.parametrize("T,block_scale", [(1, False), (4, False), (1, True), (4, True)])
-def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale):
+@pytest.mark.parametrize("T,block_scale,n", [(1, False, 1024), (4, False, 1024), (1, True, 1024), (4, True, 1024),
+                                               (2, True, 10240)])
+def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale, n):
     """Residual GEMM fused with the next RMSNorm's data: x += W.a in place,
     fragments of x * (1 + gamma) for the next linear, and sum of x^2 per row group.
     block_scale: the input's 128-column blocks are scaled per token by
     1/sqrt(sum/128 + 1e-6) of four given partial sums (the DeltaNet out_proj's
-    folded gated RMSNorm)."""
+    folded gated RMSNorm; n = 10240: 80 heads, 10 blocks per wave)."""
     import ctypes as C
 
     from rapidllm_amd.hip import DeviceBuffer, call
 
-    r = synth.rng(500 + T)
-    m, n = 512, 1024
+    r = synth.rng(500 + T + n)
+    m = 512
     W, s = synth.fp8_weight(r, m, n), synth.fp8_scales(r, m, n, 1e-3, 1e-2)
     lin = ops.Fp8Linear(W, s)
     X = r.standard_normal((T, n)).astype(np.float32)
