@@ -168,10 +168,12 @@ int rl_hip_gemm_kquant_swiglu(int type, const uint8_t* tiled, const float* X, fl
  * (rl_hip_gemm_kquant_noalloc_max_scratch() bytes = 4 MiB per device, held until
  * the process ends), set up on the first call on each device.  Shapes whose
  * workspace (rl_hip_kquant_workspace_bytes) exceeds it return RL_ERR_RANGE.  It
- * calls no allocating routine.  Every call on one device shares that array: calls
- * that overlap in time on one device (two streams, two threads) race, so serialise
- * them (one stream per device) or use rl_hip_gemm_kquant with a workspace per
- * stream. */
+ * calls no allocating routine.  The first call on a device clears the array on its
+ * stream; calls on other streams issued before that clear is seen complete wait for
+ * it on the device (hipStreamWaitEvent), so first uses on several streams are safe.
+ * After that, every call on one device shares the array: calls that overlap in
+ * time on one device (two streams, two threads) race, so serialise them (one
+ * stream per device) or use rl_hip_gemm_kquant with a workspace per stream. */
 int rl_hip_gemm_kquant_noalloc(int type, const uint8_t* tiled, const float* X, float* Y, int m, int n, int T,
                                int accumulate, void* stream);
 size_t rl_hip_gemm_kquant_noalloc_max_scratch(void);

@@ -748,8 +748,11 @@ class Engine {
                     const int nr = std::min(chunk, c_.vocab - r0);
                     dequant_host(e->quant, static_cast<const uint8_t*>(e->data) + static_cast<size_t>(r0) * rowb,
                                  stage.data(), static_cast<int64_t>(nr) * H);
-                    RL_HIP(hipMemcpy(ed + static_cast<size_t>(r0) * H, stage.data(), sizeof(float) * nr * H,
-                                     hipMemcpyHostToDevice));
+                    // on the engine stream, behind the zero-fill of `ed`; the stage is
+                    // refilled only after the copy has drained
+                    RL_HIP(hipMemcpyAsync(ed + static_cast<size_t>(r0) * H, stage.data(), sizeof(float) * nr * H,
+                                          hipMemcpyHostToDevice, st_));
+                    RL_HIP(hipStreamSynchronize(st_));
                 }
                 embed_kind_ = RL_Q_F32;
                 embed_ = ed;

@@ -852,25 +852,45 @@ __global__ void kq_zero_kernel(uint32_t* p, size_t n_words) {
 
 constexpr int kKqMaxDevices = 64;
 std::mutex g_scratch_mu;
-void* g_scratch_ptr[kKqMaxDevices] = {};
+struct KqScratch {
+    void* ptr = nullptr;          // device address of `scratch`
+    hipEvent_t cleared = nullptr; // recorded after the clear on `clear_stream`
+    hipStream_t clear_stream = nullptr;
+    bool clear_done = false;      // the event has been seen complete
+};
+KqScratch g_scratch[kKqMaxDevices];
 
-// Device address of `scratch` on the current device; on the first call for a
-// device it is resolved and the array cleared (a fill kernel on `s`, so the clear
-// is stream-ordered before the first GEMM).
+// Device address of `scratch` on the current device.  The first call for a device
+// resolves it and clears the array with a fill kernel on that call's stream `s`,
+// then records an event.  Until the host has seen that event complete, a call on
+// any other stream makes its stream wait for the event first, so a first use on
+// two streams (or threads) at once cannot run a GEMM on uncleared tickets.
 void* kq_scratch(hipStream_t s) {
     int dev = 0;
     RL_HIP(hipGetDevice(&dev));
     RL_REQUIRE(dev >= 0 && dev < kKqMaxDevices, RL_ERR_DEVICE, "gemm_kquant_noalloc: device index out of range");
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    if (!g_scratch_ptr[dev]) {
+    KqScratch& g = g_scratch[dev];
+    if (!g.ptr) {
         void* p = nullptr;
         RL_HIP(hipGetSymbolAddress(&p, HIP_SYMBOL(scratch)));
         RL_REQUIRE(p != nullptr, RL_ERR_DEVICE, "gemm_kquant_noalloc: scratch symbol has no device address");
+        if (!g.cleared) RL_HIP(hipEventCreateWithFlags(&g.cleared, hipEventDisableTiming));
         hipLaunchKernelGGL(kq_zero_kernel, dim3(256), dim3(256), 0, s, static_cast<uint32_t*>(p), kKqScratchBytes / 4);
         check_launch("kq_zero_kernel");
-        g_scratch_ptr[dev] = p;
+        RL_HIP(hipEventRecord(g.cleared, s));
+        g.clear_stream = s;
+        g.ptr = p;
+    } else if (!g.clear_done) {
+        const hipError_t q = hipEventQuery(g.cleared);
+        if (q == hipSuccess) {
+            g.clear_done = true;
+        } else {
+            RL_REQUIRE(q == hipErrorNotReady, RL_ERR_DEVICE, "gemm_kquant_noalloc: scratch clear failed");
+            if (s != g.clear_stream) RL_HIP(hipStreamWaitEvent(s, g.cleared, 0));
+        }
     }
-    return g_scratch_ptr[dev];
+    return g.ptr;
 }
 
 }  // namespace

@@ -14,15 +14,24 @@
 //   delta_recurrent  {S, q, k, v, beta, g_log, o}       DeltaRecurrentParams
 //   attn_decode      {q, k_cache, v_cache, o} fp32      AttnDecodeParams (pos, kv_dtype F32)
 // The linears read the device's tiled weight layouts: the first launch on a weight
-// buffer packs it into a cache keyed by the buffer and shape (weights are
-// immutable once uploaded, as WeightStore's are); forget() drops a buffer's entry.
+// buffer packs it into a cache keyed by the buffer's serial number (unique for the
+// process, never reused when an allocator hands out the same address again) and
+// the view's offset and shape. Weights are immutable once uploaded, as
+// WeightStore's are; forget() drops a buffer's entries after its contents change,
+// and a destroyed buffer's entries are freed by the device's next call.
+// Each Stream owns its activation-fragment buffer and its K-quant split-K
+// workspace (tickets and partials), so launches on different streams never share
+// them.
 #include "hip_backend.h"
 
 #include "rapidllm/backend/params.h"
 #include "rapidllm_hip.h"
 
+#include <atomic>
 #include <cstring>
 #include <map>
+#include <memory>
+#include <mutex>
 #include <stdexcept>
 #include <string>
 #include <tuple>
@@ -38,17 +47,35 @@ void check(int st) {
 // (device.h:12 lists CPU, Vulkan, CUDA).
 constexpr DeviceKind kHipKind = static_cast<DeviceKind>(3);
 
+// Serial numbers of destroyed buffers, handed from ~HipBuffer to the device that
+// allocated them (which may already be gone: the buffer holds it weakly).
+struct Graveyard {
+    std::mutex mu;
+    std::vector<uint64_t> ids;
+};
+
+uint64_t next_serial() {
+    static std::atomic<uint64_t> n{0};
+    return ++n;
+}
+
 class HipBuffer final : public Buffer {
 public:
-    HipBuffer(size_t n, bool host) : n_(n), host_(host) {
+    HipBuffer(size_t n, bool host, std::weak_ptr<Graveyard> gy)
+        : n_(n), host_(host), serial_(next_serial()), gy_(std::move(gy)) {
         check(host ? rl_hip_host_alloc(&p_, n) : rl_hip_malloc(&p_, n));
     }
     ~HipBuffer() override {
+        if (auto g = gy_.lock()) {
+            std::lock_guard<std::mutex> lk(g->mu);
+            g->ids.push_back(serial_);
+        }
         if (host_)
             rl_hip_host_free(p_);
         else
             rl_hip_free(p_);
     }
+    uint64_t serial() const { return serial_; }
     // Host-visible buffers are pinned host memory (host and device use the same
     // address); device buffers have no host mapping.
     void* host_ptr() override { return host_ ? p_ : nullptr; }
@@ -60,19 +87,51 @@ private:
     void* p_ = nullptr;
     size_t n_ = 0;
     bool host_ = false;
+    uint64_t serial_ = 0;
+    std::weak_ptr<Graveyard> gy_;
 };
+
+// grow a device scratch buffer to `need` bytes; true when (re)allocated
+bool grow(void*& p, size_t& have, size_t need) {
+    if (have >= need && p) return false;
+    rl_hip_free(p);
+    p = nullptr;
+    check(rl_hip_malloc(&p, need));
+    have = need;
+    return true;
+}
 
 class HipStream final : public Stream {
 public:
     HipStream() { check(rl_hip_stream_create(&s_)); }
-    ~HipStream() override { rl_hip_stream_destroy(s_); }
+    ~HipStream() override {
+        if (frag_ || ws_) (void)rl_hip_stream_synchronize(s_);
+        rl_hip_free(frag_);
+        rl_hip_free(ws_);
+        rl_hip_stream_destroy(s_);
+    }
     void begin_step(const char*) override {}
     void end_step() override {}
     void synchronize() override { check(rl_hip_stream_synchronize(s_)); }
     void* handle() const { return s_; }
+    // activation fragments of a GEMM's input (this stream's launches only)
+    void* frag(size_t need) {
+        grow(frag_, frag_bytes_, need);
+        return frag_;
+    }
+    // split-K tickets and partials; tickets start at zero and the GEMV leaves them zero
+    void* ws(size_t need, size_t* have) {
+        if (grow(ws_, ws_bytes_, need)) check(rl_hip_memset(ws_, 0, ws_bytes_, s_));
+        *have = ws_bytes_;
+        return ws_;
+    }
 
 private:
     void* s_ = nullptr;
+    void* frag_ = nullptr;
+    size_t frag_bytes_ = 0;
+    void* ws_ = nullptr;
+    size_t ws_bytes_ = 0;
 };
 
 size_t dtype_bytes(DType d) {
@@ -118,13 +177,12 @@ public:
             rl_hip_free(p.ts);
         }
         for (auto& [k, w] : kq_) rl_hip_free(w);
-        rl_hip_free(frag_);
-        rl_hip_free(ws_);
     }
     DeviceKind kind() const override { return kHipKind; }
     const char* name() const override { return "hip"; }
     std::unique_ptr<Buffer> allocate(const BufferDesc& d) override {
-        return std::make_unique<HipBuffer>(d.bytes, d.host_visible || d.usage == BufferDesc::Usage::HostStaging);
+        return std::make_unique<HipBuffer>(d.bytes, d.host_visible || d.usage == BufferDesc::Usage::HostStaging,
+                                           graveyard_);
     }
     std::unique_ptr<Stream> create_stream() override { return std::make_unique<HipStream>(); }
 
@@ -157,7 +215,9 @@ public:
 
     void launch(const char* k, const TensorView* a, int nargs, const void* params, size_t pbytes,
                 Stream& s) override {
-        void* st = stream_of(s);
+        HipStream& hs = hip_stream(s);
+        void* st = hs.handle();
+        bury();
         const std::string name(k);
         if (name == "rmsnorm") {
             need_args(nargs, 3, k);
@@ -173,16 +233,16 @@ public:
             const auto& p = params_as<GemvFp8Params>(params, pbytes, k);
             if (p.block != 128) throw std::runtime_error("hip device: gemv_fp8 needs 128x128 block scales");
             const Fp8Packed& w = fp8_packed(a[0], a[1], p.m, p.n, st);
-            grow(frag_, frag_bytes_, rl_hip_act_frag_bytes(p.n, 1));
-            check(rl_hip_gemm_fp8(w.w, w.ts, f(a[2]), f(a[3]), frag_, p.m, p.n, 1, st));
+            void* frag = hs.frag(rl_hip_act_frag_bytes(p.n, 1));
+            check(rl_hip_gemm_fp8(w.w, w.ts, f(a[2]), f(a[3]), frag, p.m, p.n, 1, st));
         } else if (name == "gemv_q4k" || name == "gemv_q6k") {
             need_args(nargs, 3, k);
             const auto& p = params_as<GemvKQuantParams>(params, pbytes, k);
             const int type = name == "gemv_q4k" ? RL_Q_Q4_K : RL_Q_Q6_K;
             uint8_t* w = kq_packed(type, a[0], p.m, p.n, st);
-            const size_t need = rl_hip_kquant_workspace_bytes(p.m, p.n, 1);
-            if (grow(ws_, ws_bytes_, need)) check(rl_hip_memset(ws_, 0, ws_bytes_, st));  // tickets start at zero
-            check(rl_hip_gemm_kquant(type, w, f(a[1]), f(a[2]), ws_, ws_bytes_, p.m, p.n, 1, 0, st));
+            size_t ws_bytes = 0;
+            void* ws = hs.ws(rl_hip_kquant_workspace_bytes(p.m, p.n, 1), &ws_bytes);
+            check(rl_hip_gemm_kquant(type, w, f(a[1]), f(a[2]), ws, ws_bytes, p.m, p.n, 1, 0, st));
         } else if (name == "conv1d_update") {
             need_args(nargs, 4, k);
             const auto& p = params_as<Conv1dParams>(params, pbytes, k);
@@ -206,8 +266,15 @@ public:
 
     // Drop the packed copy of a weight buffer (after its contents change).
     void forget(const Buffer* b) {
+        const auto* hb = dynamic_cast<const HipBuffer*>(b);
+        if (hb) drop(hb->serial());
+    }
+
+private:
+    // free the packed copies of one buffer (by serial number)
+    void drop(uint64_t id) {
         for (auto it = fp8_.begin(); it != fp8_.end();) {
-            if (std::get<0>(it->first) == b) {
+            if (std::get<0>(it->first) == id) {
                 rl_hip_free(it->second.w);
                 rl_hip_free(it->second.ts);
                 it = fp8_.erase(it);
@@ -216,7 +283,7 @@ public:
             }
         }
         for (auto it = kq_.begin(); it != kq_.end();) {
-            if (std::get<0>(it->first) == b) {
+            if (std::get<0>(it->first) == id) {
                 rl_hip_free(it->second);
                 it = kq_.erase(it);
             } else {
@@ -225,31 +292,39 @@ public:
         }
     }
 
-private:
+    // free the packed copies of buffers destroyed since the last launch (hipFree
+    // waits for the device's queued work, which may still read them)
+    void bury() {
+        std::vector<uint64_t> ids;
+        {
+            std::lock_guard<std::mutex> lk(graveyard_->mu);
+            ids.swap(graveyard_->ids);
+        }
+        for (uint64_t id : ids) drop(id);
+    }
+
     struct Fp8Packed {
         uint8_t* w = nullptr;
         float* ts = nullptr;
     };
-    using Key = std::tuple<const Buffer*, uint64_t, int, int>;
+    // (buffer serial, view byte offset [K-quant: x16 + type], rows, cols)
+    using Key = std::tuple<uint64_t, uint64_t, int, int>;
 
     static float* f(const TensorView& v) { return static_cast<float*>(dptr(v)); }
-    static void* stream_of(Stream& s) {
+    static HipStream& hip_stream(Stream& s) {
         auto* hs = dynamic_cast<HipStream*>(&s);
         if (!hs) throw std::runtime_error("hip device: stream is not a HIP stream");
-        return hs->handle();
+        return *hs;
     }
-    // grow a device scratch buffer to `need` bytes; true when (re)allocated
-    static bool grow(void*& p, size_t& have, size_t need) {
-        if (have >= need && p) return false;
-        rl_hip_free(p);
-        p = nullptr;
-        check(rl_hip_malloc(&p, need));
-        have = need;
-        return true;
+    static void* stream_of(Stream& s) { return hip_stream(s).handle(); }
+    static uint64_t serial_of(const TensorView& v) {
+        const auto* b = dynamic_cast<const HipBuffer*>(v.buf);
+        if (!b) throw std::runtime_error("hip device: tensor view is not on a HIP buffer");
+        return b->serial();
     }
 
     const Fp8Packed& fp8_packed(const TensorView& w, const TensorView& scale, int m, int n, void* st) {
-        const Key key{w.buf, w.byte_offset, m, n};
+        const Key key{serial_of(w), w.byte_offset, m, n};
         auto it = fp8_.find(key);
         if (it != fp8_.end()) return it->second;
         Fp8Packed p;
@@ -260,7 +335,7 @@ private:
     }
 
     uint8_t* kq_packed(int type, const TensorView& w, int m, int n, void* st) {
-        const Key key{w.buf, w.byte_offset * 16 + static_cast<uint64_t>(type), m, n};
+        const Key key{serial_of(w), w.byte_offset * 16 + static_cast<uint64_t>(type), m, n};
         auto it = kq_.find(key);
         if (it != kq_.end()) return it->second;
         void* p = nullptr;
@@ -271,10 +346,7 @@ private:
 
     std::map<Key, Fp8Packed> fp8_;
     std::map<Key, uint8_t*> kq_;
-    void* frag_ = nullptr;
-    size_t frag_bytes_ = 0;
-    void* ws_ = nullptr;
-    size_t ws_bytes_ = 0;
+    std::shared_ptr<Graveyard> graveyard_ = std::make_shared<Graveyard>();
 };
 
 }  // namespace

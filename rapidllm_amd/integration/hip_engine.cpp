@@ -24,7 +24,17 @@ void check(int st) {
     if (st != RL_OK) throw std::runtime_error(std::string("hip backend: ") + rl_hip_last_error());
 }
 
-// RlQuant uses QuantKind's numbering (model_desc.h:14-25).
+// RlQuant uses QuantKind's numbering (model_desc.h:14-25); checked here so that a
+// reordering on either side fails the build instead of mislabelling weights.
+static_assert(static_cast<int>(QuantKind::F32) == RL_Q_F32, "QuantKind::F32");
+static_assert(static_cast<int>(QuantKind::F16) == RL_Q_F16, "QuantKind::F16");
+static_assert(static_cast<int>(QuantKind::BF16) == RL_Q_BF16, "QuantKind::BF16");
+static_assert(static_cast<int>(QuantKind::FP8_E4M3_B128) == RL_Q_FP8_E4M3_B128, "QuantKind::FP8_E4M3_B128");
+static_assert(static_cast<int>(QuantKind::PackedInt4) == RL_Q_PACKED_INT4, "QuantKind::PackedInt4");
+static_assert(static_cast<int>(QuantKind::Q8_0) == RL_Q_Q8_0, "QuantKind::Q8_0");
+static_assert(static_cast<int>(QuantKind::Q4_K) == RL_Q_Q4_K, "QuantKind::Q4_K");
+static_assert(static_cast<int>(QuantKind::Q5_K) == RL_Q_Q5_K, "QuantKind::Q5_K");
+static_assert(static_cast<int>(QuantKind::Q6_K) == RL_Q_Q6_K, "QuantKind::Q6_K");
 int quant_of(QuantKind q) { return static_cast<int>(q); }
 
 RlModelConfig config_of(const ModelDesc& md) {

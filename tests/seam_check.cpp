@@ -397,6 +397,18 @@ void check_device() {
         stream->synchronize();
         expect(rel_l2(first.data(), want.data(), m) < 1e-3, "launch(\"gemv_fp8\") vs ops::gemv_fp8");
         expect(std::memcmp(first.data(), F(by), m * 4) == 0, "gemv_fp8 second launch (cached packing) identical");
+        // a new weight buffer after the old one is freed (the allocator may hand out
+        // the same address): the packed cache must not serve the old weights
+        bw.b.reset();
+        for (auto& b : w) b = r.fp8();
+        std::memcpy(stage.b->host_ptr(), w.data(), w.size());
+        Buf bw2 = dev_buf(*dev, DType::I8, {m, n}, w.size());
+        dev->memcpy(bw2.v, stage.v, *stream);
+        const TensorView a2[4] = {bw2.v, bs.v, bx.v, by.v};
+        orc_gemv_fp8(w.data(), s.data(), x.data(), want.data(), m, n, 128);
+        dev->launch("gemv_fp8", a2, 4, &p, sizeof(p), *stream);
+        stream->synchronize();
+        expect(rel_l2(F(by), want.data(), m) < 1e-3, "gemv_fp8 on a reallocated weight buffer uses the new weights");
     }
     for (int q6 = 0; q6 < 2; ++q6) {  // gemv_q4k / gemv_q6k on kquant_gemv_selftest's bytes (cuda_engine.cu:11295)
         const int m = 64, n = 512, bsz = q6 ? 210 : 144;

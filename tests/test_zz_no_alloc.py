@@ -50,3 +50,52 @@ def test_noalloc_rejects_shapes_beyond_scratch(gpu):
     rc = L.rl_hip_gemm_kquant_noalloc(ops.Q4_K, None, None, None, m, n, T, 0, None)
     assert rc == 6  # RL_ERR_RANGE
     assert b"scratch" in L.rl_hip_last_error()
+
+
+FIRST_USE = r"""
+import sys
+sys.path.insert(0, {root!r})
+import numpy as np
+from rapidllm_amd import hip, ops, synth
+from rapidllm_amd.hip import DeviceBuffer, call
+import ctypes as C
+hip.require_gpu()
+L = hip.lib()
+m, n, T = 5120, 17408, 4
+r = synth.rng(9)
+lin = ops.KQuantLinear(ops.Q4_K, synth.q4k_blocks(r, m, n), m, n)
+X = r.standard_normal((T, n)).astype(np.float32)
+xd = DeviceBuffer.from_numpy(X)
+ys = [DeviceBuffer.from_numpy(np.zeros((T, m), np.float32)) for _ in range(3)]
+ws = ops.kquant_workspace(m, n, T)
+call("rl_hip_gemm_kquant", ops.Q4_K, lin.w.ptr, xd.ptr, ys[0].ptr, ws.ptr, ws.nbytes, m, n, T, 0, None)
+call("rl_hip_stream_synchronize", None)
+streams = []
+for _ in range(2):
+    h = C.c_void_p()
+    call("rl_hip_stream_create", C.byref(h))
+    streams.append(h)
+# the process's first two allocation-free calls, on two streams, no host sync between
+call("rl_hip_gemm_kquant_noalloc", ops.Q4_K, lin.w.ptr, xd.ptr, ys[1].ptr, m, n, T, 0, streams[0])
+call("rl_hip_gemm_kquant_noalloc", ops.Q4_K, lin.w.ptr, xd.ptr, ys[2].ptr, m, n, T, 0, streams[1])
+for h in streams:
+    call("rl_hip_stream_synchronize", h)
+want = ys[0].numpy(np.float32, (T, m)).view(np.uint32)
+for y in ys[1:]:
+    assert np.array_equal(y.numpy(np.float32, (T, m)).view(np.uint32), want)
+for h in streams:
+    call("rl_hip_stream_destroy", h)
+print("FIRST_USE_OK")
+"""
+
+
+def test_noalloc_first_use_on_two_streams(gpu):
+    # a fresh process, so these are the library's first allocation-free calls
+    import os
+    import subprocess
+    import sys
+
+    root = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+    p = subprocess.run([sys.executable, "-c", FIRST_USE.format(root=root)], capture_output=True, text=True,
+                       timeout=110)
+    assert p.returncode == 0 and "FIRST_USE_OK" in p.stdout, p.stdout[-2000:] + p.stderr[-2000:]
