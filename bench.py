@@ -567,7 +567,7 @@ def main():
         sys.exit(2)
 
     from rapidllm_amd import hip
-    from rapidllm_amd.engine import Engine
+    from rapidllm_amd.engine import MTP_LAYER, MTP_STEM, Engine
     from rapidllm_amd.model import ModelSpec
 
     hip.require_gpu()
@@ -646,6 +646,11 @@ def main():
     eng.time_steps(1, 1)
     eng.time_steps(1, W, mtp_drafts=3)
     tm = eng.time_steps(1, K, mtp_drafts=3) / K
+    # the same with the MTP decoder layer (stem + mtp.layers[0] per draft)
+    eng.set_mtp_mode(MTP_LAYER)
+    eng.time_steps(1, W, mtp_drafts=3)
+    tml = eng.time_steps(1, K, mtp_drafts=3) / K
+    eng.set_mtp_mode(MTP_STEM)
     # continuous batch of 4 sequences at 32K context each (one weight pass per step)
     eng.synthetic_context(CTX)
     eng.replicate_slot0(4)
@@ -686,7 +691,9 @@ def main():
         "t4_verify_ms": round(t4, 4),
         "t4_over_t1": round(t4 / t1, 4),
         "mtp_draft3_ms": round(tm, 4),
+        "mtp_layer_draft3_ms": round(tml, 4),
         "spec_tok_s_full_accept": round(4000.0 / (t4 + tm), 3),
+        "spec_tok_s_full_accept_layer": round(4000.0 / (t4 + tml), 3),
         "gguf_q4_k": gguf,
         "batch4_step_ms": round(tb4, 4),
         "batch4_tok_s": round(4000.0 / tb4, 3),

@@ -316,6 +316,22 @@ int rl_hip_engine_copy_logits(RlEngine* e, float* host);                        
 int rl_hip_engine_copy_last_hidden(RlEngine* e, float* host);                         /* :33 */
 int rl_hip_engine_mtp_draft(RlEngine* e, int32_t first, int n, int32_t* out, int* n_out); /* :36 */
 int rl_hip_engine_spec_verify(RlEngine* e, const int32_t* toks, int T, int32_t* preds, int* n_consumed); /* :72 */
+/* MTP draft mode.  RL_MTP_STEM (default): the stem only, as Session::mtp_draft's
+ * CPU branch (src/runtime/session.cpp:619-681).  RL_MTP_LAYER: the stem's fc output
+ * then passes through the MTP decoder layer mtp.layers[0] -- gated attention over
+ * its own fp16 KV cache at draft positions 0, 1, ... of the call, then the MLP --
+ * as Session::mtp_layer_step (session.cpp:561-617) composes fused_attn_decode and
+ * fused_mlp_decode; the reference's CUDA engine drafts through that layer for
+ * official and GGUF checkpoints (cuda_engine.cu:16304-16357, 16745-16778).
+ * set_mtp_mode returns RL_ERR_UNSUPPORTED for LAYER when the weights have no
+ * mtp.layers[0].  Applies to mtp_draft and mtp_spec. */
+#define RL_MTP_STEM 0
+#define RL_MTP_LAYER 1
+int rl_hip_engine_set_mtp_mode(RlEngine* e, int mode);
+int rl_hip_engine_mtp_mode(RlEngine* e, int* mode, int* layer_available);
+/* The last draft's hidden state before the final MTP norm ([hidden] fp32; the
+ * CUDA engine's d_mtp_h_, cuda_engine.cu:16304-16357). */
+int rl_hip_engine_copy_mtp_hidden(RlEngine* e, float* out);
 /* MTP stem draft of T-1 tokens after t0 and the T-token verify, one submission (:40). */
 int rl_hip_engine_mtp_spec(RlEngine* e, int32_t t0, int T, int32_t* toks_out, int32_t* preds, int* n_consumed);
 int rl_hip_engine_greedy(RlEngine* e, int32_t* tok);                                  /* :41 */

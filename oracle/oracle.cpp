@@ -531,6 +531,8 @@ struct Model {
     std::vector<float> logits, last_hidden;
     std::vector<float> hist_h;  // mtp_hh_: residual after the layers, per token
     std::vector<int> hist_ids;  // mtp_hids_
+    int mtp_mode = 0;           // 0: stem (Session::mtp_draft), 1: stem + mtp.layers[0]
+    mutable std::vector<float> mtp_h;  // the last draft's hidden before norm_mtp
 
     const W& get(const std::string& n) const {
         auto it = w.find(n);
@@ -690,6 +692,10 @@ struct Model {
     // decoder layer.  h' = fc([norm_e(embed tok) ; norm_h(h)]); tok = argmax(
     // lm_head(norm_mtp(h'))).  First draft from the last history hidden, later
     // drafts from the one before it.
+    // mtp_mode 1 passes h' through the MTP decoder layer first, as
+    // Session::mtp_layer_step(h', i) does (session.cpp:561-617): fused_attn_decode
+    // with the mtp.layers[0] weights on the layer's own KV cache at draft position
+    // i (zeroed per call, session.cpp:637-640), then fused_mlp_decode.
     int mtp_draft(int first, int n, int* out) const {
         if (!c.has_mtp || n <= 0) return 0;
         const int H = c.hidden;
@@ -697,6 +703,8 @@ struct Model {
         const float* h_last = nh > 0 ? &hist_h[static_cast<size_t>(nh - 1) * H] : last_hidden.data();
         const float* h_prev = nh > 1 ? &hist_h[static_cast<size_t>(nh - 2) * H] : h_last;
         std::vector<float> eh(H), ee(H), er(H), cat(2 * static_cast<size_t>(H)), hp(H), hn(H), lg(c.vocab);
+        const size_t kn = static_cast<size_t>(c.n_kv) * c.head_dim;
+        std::vector<float> mkc(mtp_mode ? static_cast<size_t>(n) * kn : 0, 0.f), mvc(mkc.size(), 0.f);
         int tok = first;
         for (int i = 0; i < n; ++i) {
             const float* href = i == 0 ? h_last : h_prev;
@@ -706,6 +714,11 @@ struct Model {
             std::memcpy(cat.data(), ee.data(), sizeof(float) * H);
             std::memcpy(cat.data() + H, eh.data(), sizeof(float) * H);
             lin(get("mtp.fc"), cat.data(), hp.data(), H, 2 * H);
+            if (mtp_mode) {
+                attn("mtp.layers[0].", 0, hp.data(), mkc, mvc, i);
+                mlp("mtp.layers[0].", hp.data());
+            }
+            mtp_h = hp;
             orc_qwen3_rmsnorm(hp.data(), get("mtp.norm").f32(), hn.data(), H, c.rms_eps);
             lin(get("lm_head"), hn.data(), lg.data(), c.vocab, H);
             tok = orc_greedy(lg.data(), c.vocab);
@@ -748,6 +761,15 @@ int orc_model_decode(void* h, int token, float* logits, float* hidden) {
     if (logits) std::memcpy(logits, m->logits.data(), sizeof(float) * m->c.vocab);
     if (hidden) std::memcpy(hidden, m->last_hidden.data(), sizeof(float) * m->c.hidden);
     return orc_greedy(m->logits.data(), m->c.vocab);
+}
+
+void orc_model_set_mtp_mode(void* h, int mode) { static_cast<Model*>(h)->mtp_mode = mode; }
+
+int orc_model_mtp_hidden(void* h, float* out) {
+    const auto* m = static_cast<Model*>(h);
+    if (static_cast<int>(m->mtp_h.size()) != m->c.hidden) return -1;
+    std::memcpy(out, m->mtp_h.data(), sizeof(float) * m->c.hidden);
+    return 0;
 }
 
 int orc_model_mtp_draft(void* h, int first, int n, int* out) {

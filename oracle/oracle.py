@@ -84,6 +84,9 @@ def lib():
         L.orc_model_decode.argtypes = [C.c_void_p, C.c_int, _f, _f]
         L.orc_model_mtp_draft.restype = C.c_int
         L.orc_model_mtp_draft.argtypes = [C.c_void_p, C.c_int, C.c_int, _i32]
+        L.orc_model_set_mtp_mode.argtypes = [C.c_void_p, C.c_int]
+        L.orc_model_mtp_hidden.restype = C.c_int
+        L.orc_model_mtp_hidden.argtypes = [C.c_void_p, _f]
         L.orc_model_generate.restype = C.c_int
         L.orc_model_generate.argtypes = [C.c_void_p, _i32, C.c_int, C.c_int, C.c_int, _i32, _i32, _i32]
         L.orc_model_layer.restype = C.c_int
@@ -127,6 +130,8 @@ def ref():
         R.ref_num_threads.restype = C.c_int
         R.ref_simd_name.restype = C.c_char_p
         R.ref_fused_mlp.argtypes = [_f, _u8, _f, _u8, _f, _u8, _f, _f, C.c_int, C.c_int, C.c_float]
+        R.ref_fused_attn.argtypes = [_f, _u8, _f, _u8, _f, _u8, _f, _u8, _f, _f, _f, _f, _f, _f, C.c_int, C.c_int,
+                                     C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float]
         vp = C.c_void_p
         R.ref_weights_open.restype = vp
         R.ref_weights_open.argtypes = [C.c_char_p, C.c_char_p, C.c_int]
@@ -337,7 +342,21 @@ class OracleModel:
     def mtp_draft(self, first, n):
         out = np.zeros(n, np.int32)
         k = lib().orc_model_mtp_draft(self.h, int(first), n, out.ctypes.data_as(_i32))
+        if k < 0:
+            raise RuntimeError("oracle mtp_draft failed")
         return out[:k]
+
+    def set_mtp_mode(self, mode):
+        """0: stem (Session::mtp_draft); 1: stem + the MTP decoder layer
+        (Session::mtp_layer_step)."""
+        lib().orc_model_set_mtp_mode(self.h, int(mode))
+
+    def mtp_hidden(self):
+        """The last draft's hidden before the final MTP norm."""
+        h = np.empty(self.spec.hidden, np.float32)
+        if lib().orc_model_mtp_hidden(self.h, P(h)) != 0:
+            raise RuntimeError("no MTP draft yet")
+        return h
 
     def generate(self, prompt, max_new, spec_n=0):
         prompt = np.ascontiguousarray(prompt, np.int32)

@@ -71,6 +71,36 @@ void ref_fused_mlp(const float* rms_w, const uint8_t* wg, const float* sg, const
     a.use_simd = true;
     ops::fused_mlp_decode(a);
 }
+
+// ops::fused_attn_decode (ops_fused.cpp:137-184) with block-FP8 projections: x += the
+// gated attention output at position pos, K / V appended to the fp32 caches.
+void ref_fused_attn(const float* rms_w, const uint8_t* wq, const float* sq, const uint8_t* wk, const float* sk,
+                    const uint8_t* wv, const float* sv, const uint8_t* wo, const float* so, const float* q_norm,
+                    const float* k_norm, float* k_cache, float* v_cache, float* x, int hidden, int n_q, int n_kv,
+                    int head_dim, int rotary_dim, int pos, float theta, float eps) {
+    ops::FusedAttnArgs a{};
+    a.x = x;
+    a.x_inout = x;
+    a.rms_w = rms_w;
+    a.Wq = {wq, sq, QuantKind::FP8_E4M3_B128};
+    a.Wk = {wk, sk, QuantKind::FP8_E4M3_B128};
+    a.Wv = {wv, sv, QuantKind::FP8_E4M3_B128};
+    a.Wo = {wo, so, QuantKind::FP8_E4M3_B128};
+    a.q_norm = q_norm;
+    a.k_norm = k_norm;
+    a.k_cache = k_cache;
+    a.v_cache = v_cache;
+    a.hidden = hidden;
+    a.n_q = n_q;
+    a.n_kv = n_kv;
+    a.head_dim = head_dim;
+    a.rotary_dim = rotary_dim;
+    a.pos = pos;
+    a.theta = theta;
+    a.eps = eps;
+    a.use_simd = true;
+    ops::fused_attn_decode(a);
+}
 }
 
 // ---- the reference's checkpoint loaders (src/frontend/*.cpp), for cross-checking

@@ -372,7 +372,24 @@ class Engine {
         RL_HIP(hipStreamSynchronize(st_));
     }
 
-    // Stem draft after the last consumed token (session.cpp:619-681).
+    // Draft mode: RL_MTP_STEM (Session::mtp_draft) or RL_MTP_LAYER (stem + the
+    // mtp.layers[0] decoder layer, Session::mtp_layer_step).
+    void set_mtp_mode(int mode) {
+        RL_REQUIRE(mode == RL_MTP_STEM || mode == RL_MTP_LAYER, RL_ERR_RANGE, "mtp mode must be STEM or LAYER");
+        RL_REQUIRE(mode == RL_MTP_STEM || has_mtp_layer_, RL_ERR_UNSUPPORTED,
+                   "mtp mode LAYER: the model has no MTP decoder layer (mtp.layers[0].*)");
+        mtp_mode_ = mode;
+    }
+    int mtp_mode() const { return mtp_mode_; }
+    // the last draft's hidden before the final MTP norm
+    void copy_mtp_hidden(float* out) {
+        RL_REQUIRE(has_mtp_, RL_ERR_UNSUPPORTED, "model has no MTP head");
+        RL_HIP(hipMemcpyAsync(out, mtp_hp_, c_.hidden * sizeof(float), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+    }
+    bool has_mtp_layer() const { return has_mtp_layer_; }
+
+    // Draft after the last consumed token (session.cpp:619-681).
     int mtp_draft(int32_t first, int n, int32_t* out) {
         if (!has_mtp_ || n <= 0) return 0;
         RL_REQUIRE(n <= 7, RL_ERR_RANGE, "mtp_draft: at most 7 drafts");
@@ -678,6 +695,16 @@ class Engine {
     float* mtp_e_ = nullptr;   // [H]
     float* mtp_cat_ = nullptr; // [2H]
     float* mtp_hp_ = nullptr;  // [H]
+    // MTP decoder layer (mtp.layers[0]) and its draft-position KV cache
+    static constexpr int kMtpCtx = 256;  // draft positions the cache holds (one chunk)
+    Layer mtp_layer_;
+    bool has_mtp_layer_ = false;
+    int mtp_mode_ = RL_MTP_STEM;
+    uint16_t *mtp_kc_ = nullptr, *mtp_vt_ = nullptr;
+    void* mtp_attn_ws_ = nullptr;
+    size_t mtp_attn_ws_bytes_ = 0;
+    int* mtp_pos_ = nullptr;    // [kMtpCtx] = 0, 1, 2, ... (device positions of the drafts)
+    float* mtp_x1_ = nullptr;  // [H] residual between the layer's attention and MLP
     float* h_last_ = nullptr;
     float* h_prev_ = nullptr;
     void* attn_ws_ = nullptr;
@@ -810,47 +837,14 @@ class Engine {
                 max_width = std::max(max_width, Ly.in_width);
             } else {
                 Ly.aslot = na++;
-                Ly.qkv_width = 2 * nq * hd + 2 * nkv * hd;
-                const std::vector<std::string> names = {p + "attn.wq", p + "attn.wk", p + "attn.wv"};
-                const std::vector<int> rows = {2 * nq * hd, nkv * hd, nkv * hd};
-                const std::vector<int> offs = {0, 2 * nq * hd, 2 * nq * hd + nkv * hd};
-                make_fused(find, names, rows, offs, H, Ly.qkv_parts, Ly.qkv_offs);
-                Ly.o_proj = synthetic_ ? synth_layer_lin(H, nq * hd)
-                                       : upload_lin({need(find, p + "attn.wo")}, H, nq * hd);
-                Ly.q_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.q_norm"), hd);
-                Ly.k_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.k_norm"), hd);
+                build_attn(Ly, p, find);
                 max_width = std::max(max_width, Ly.qkv_width);
             }
-            // MLP
-            if (synthetic_ && synth_quant_ != RL_Q_FP8_E4M3_B128) {
-                Ly.gate = synth_kq(synth_quant_, 2 * I, H);
-                Ly.gate_cat = true;
-                Ly.down = synth_kq(synth_quant_, H, I);
-            } else if (synthetic_) {
-                Ly.gate_up = synth_gate_up(I, H);
-                Ly.down = synth_lin(RL_Q_FP8_E4M3_B128, H, I);
-            } else {
-                const RlTensor* g = need(find, p + "mlp.gate");
-                const RlTensor* u = need(find, p + "mlp.up");
-                const RlTensor* d = need(find, p + "mlp.down");
-                I = static_cast<int>(d->cols);
-                RL_REQUIRE(I == c_.intermediate, RL_ERR_FORMAT, "mlp.down shape disagrees with intermediate");
-                if (g->quant == u->quant && (g->quant == RL_Q_FP8_E4M3_B128 || g->quant == RL_Q_BF16)) {
-                    Ly.gate_up = upload_gate_up(g, u, I, H);
-                } else if (g->quant == u->quant && (g->quant == RL_Q_Q4_K || g->quant == RL_Q_Q6_K) && I % 64 == 0) {
-                    // one K-quant launch for gate and up over half tiles (8 gate rows,
-                    // then the same 8 up rows), writing h = silu(gate) * up
-                    Ly.gate = upload_kq_cat(g, u, I, H);
-                    Ly.gate_cat = true;
-                } else {
-                    Ly.gate = upload_lin({g}, I, H);
-                    Ly.up = upload_lin({u}, I, H);
-                }
-                Ly.down = upload_lin({d}, H, I);
-            }
+            build_mlp(Ly, p, find);
         }
 
-        // MTP stem head
+        // MTP stem head, and its decoder layer (mtp.layers[0]: attention with its own
+        // KV cache + MLP, Session::mtp_layer_step) when the checkpoint has one
         if (c_.has_mtp) {
             has_mtp_ = true;
             if (synthetic_) {
@@ -863,6 +857,28 @@ class Engine {
                 mtp_nh_ = upload_vec(need(find, "mtp.pre_fc_norm_hidden"), H);
                 mtp_ne_ = upload_vec(need(find, "mtp.pre_fc_norm_embedding"), H);
                 mtp_norm_ = upload_vec(need(find, "mtp.norm"), H);
+            }
+            const std::string mp = "mtp.layers[0].";
+            if (nq > 0 && hd == 256 && (synthetic_ || find(mp + "attn.wq"))) {
+                Layer& Ly = mtp_layer_;
+                Ly.kind = RL_LAYER_ATTN;
+                Ly.attn_norm = synthetic_ ? synth_vec(H, 0.f, 0.1f) : upload_vec(need(find, mp + "attn_norm"), H);
+                Ly.ffn_norm = synthetic_ ? synth_vec(H, 0.f, 0.1f) : upload_vec(need(find, mp + "ffn_norm"), H);
+                build_attn(Ly, mp, find);
+                build_mlp(Ly, mp, find);
+                max_width = std::max(max_width, Ly.qkv_width);
+                // fp16 K / V of the draft positions, in the decode cache layout
+                const size_t kv = static_cast<size_t>(nkv) * kMtpCtx * hd;
+                mtp_kc_ = mem_.get_n<uint16_t>(2 * kv);
+                mtp_vt_ = mtp_kc_ + kv;
+                mtp_attn_ws_bytes_ = attn_workspace_bytes(nkv, kMtpCtx);
+                mtp_attn_ws_ = mem_.get(mtp_attn_ws_bytes_);
+                mtp_pos_ = mem_.get_n<int>(kMtpCtx);
+                std::vector<int> iota(kMtpCtx);
+                for (int i = 0; i < kMtpCtx; ++i) iota[i] = i;
+                RL_HIP(hipMemcpyAsync(mtp_pos_, iota.data(), sizeof(int) * kMtpCtx, hipMemcpyHostToDevice, st_));
+                RL_HIP(hipStreamSynchronize(st_));
+                has_mtp_layer_ = true;
             }
         }
 
@@ -960,6 +976,7 @@ class Engine {
         mtp_e_ = mem_.get_n<float>(H);
         mtp_cat_ = mem_.get_n<float>(2 * static_cast<size_t>(H));
         mtp_hp_ = mem_.get_n<float>(H);
+        mtp_x1_ = mem_.get_n<float>(H);
         h_last_ = mem_.get_n<float>(H);
         h_prev_ = mem_.get_n<float>(H);
         // one workspace per batch slot (batch decode runs all slots' attention at once)
@@ -974,6 +991,54 @@ class Engine {
         tok_all_ = mem_.get_n<int>(static_cast<size_t>(ctx_capacity()) + 16);
         RL_HIP(hipStreamSynchronize(st_));
         tab_.clear();
+    }
+
+    // Attention projections of a gated-attention layer: q|gate, k, v as one fused
+    // linear, o_proj, the q / k head norms (weights under prefix p).
+    template <class Find>
+    void build_attn(Layer& Ly, const std::string& p, Find& find) {
+        const int H = c_.hidden, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim;
+        Ly.qkv_width = 2 * nq * hd + 2 * nkv * hd;
+        const std::vector<std::string> names = {p + "attn.wq", p + "attn.wk", p + "attn.wv"};
+        const std::vector<int> rows = {2 * nq * hd, nkv * hd, nkv * hd};
+        const std::vector<int> offs = {0, 2 * nq * hd, 2 * nq * hd + nkv * hd};
+        make_fused(find, names, rows, offs, H, Ly.qkv_parts, Ly.qkv_offs);
+        Ly.o_proj = synthetic_ ? synth_layer_lin(H, nq * hd) : upload_lin({need(find, p + "attn.wo")}, H, nq * hd);
+        Ly.q_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.q_norm"), hd);
+        Ly.k_norm = synthetic_ ? synth_vec(hd, 0.f, 0.1f) : upload_vec(need(find, p + "attn.k_norm"), hd);
+    }
+
+    // MLP of a layer: gate/up in half tiles (FP8 / BF16) or as K-quant parts, down.
+    template <class Find>
+    void build_mlp(Layer& Ly, const std::string& p, Find& find) {
+        const int H = c_.hidden;
+        int I = c_.intermediate;
+        if (synthetic_ && synth_quant_ != RL_Q_FP8_E4M3_B128) {
+            Ly.gate = synth_kq(synth_quant_, 2 * I, H);
+            Ly.gate_cat = true;
+            Ly.down = synth_kq(synth_quant_, H, I);
+        } else if (synthetic_) {
+            Ly.gate_up = synth_gate_up(I, H);
+            Ly.down = synth_lin(RL_Q_FP8_E4M3_B128, H, I);
+        } else {
+            const RlTensor* g = need(find, p + "mlp.gate");
+            const RlTensor* u = need(find, p + "mlp.up");
+            const RlTensor* d = need(find, p + "mlp.down");
+            I = static_cast<int>(d->cols);
+            RL_REQUIRE(I == c_.intermediate, RL_ERR_FORMAT, "mlp.down shape disagrees with intermediate");
+            if (g->quant == u->quant && (g->quant == RL_Q_FP8_E4M3_B128 || g->quant == RL_Q_BF16)) {
+                Ly.gate_up = upload_gate_up(g, u, I, H);
+            } else if (g->quant == u->quant && (g->quant == RL_Q_Q4_K || g->quant == RL_Q_Q6_K) && I % 64 == 0) {
+                // one K-quant launch for gate and up over half tiles (8 gate rows,
+                // then the same 8 up rows), writing h = silu(gate) * up
+                Ly.gate = upload_kq_cat(g, u, I, H);
+                Ly.gate_cat = true;
+            } else {
+                Ly.gate = upload_lin({g}, I, H);
+                Ly.up = upload_lin({u}, I, H);
+            }
+            Ly.down = upload_lin({d}, H, I);
+        }
     }
 
     template <class Find>
@@ -1708,30 +1773,7 @@ class Engine {
                 pending = linear_residual(Ly.o_proj, xn_, T);
             }
             norm_residual(cur, pending, Ly.ffn_norm, T);
-            const bool down_frag = Ly.down.kind == RL_Q_FP8_E4M3_B128 || Ly.down.kind == RL_Q_BF16;
-            if (Ly.gate_up.kind >= 0) {
-                // SwiGLU epilogue: fp32 h only when a K-quant down needs it
-                if (Ly.gate_up.kind == RL_Q_FP8_E4M3_B128)
-                    gemm_fp8_frag(Ly.gate_up.w, Ly.gate_up.ts, frag_, down_frag ? nullptr : h_, Ly.gate_up.m,
-                                  Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1, down_frag ? frag_h_ : nullptr);
-                else
-                    gemm_bf16_frag(reinterpret_cast<const uint16_t*>(Ly.gate_up.w), frag_, down_frag ? nullptr : h_,
-                                   Ly.gate_up.m, Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1,
-                                   down_frag ? frag_h_ : nullptr);
-            } else {
-                if (Ly.gate_cat) {
-                    KqNorm ks;
-                    ks.swiglu = 1;
-                    kq_gemm(Ly.gate.kind == RL_Q_Q4_K ? 4 : 6, Ly.gate.w, xn_, h_, kq_ws_, kq_ws_bytes_, Ly.gate.m,
-                            Ly.gate.n, T, 0, I, st_, &ks);
-                } else {
-                    linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
-                    linear(Ly.up, xn_, u_, I, I, T, kEpiStore);
-                    swiglu(g_, I, u_, I, h_, I, T, st_);
-                }
-                if (down_frag) pack_act(h_, frag_h_, I, T, st_);
-            }
-            pending = linear_residual(Ly.down, h_, T, down_frag ? frag_h_ : frag_);
+            pending = mlp_unfolded(Ly, T);
         }
         norm_residual(cur, pending, final_norm_, T);
         x_ = xres_[cur];  // hidden after the layers (pre final norm), for the MTP history
@@ -1741,7 +1783,60 @@ class Engine {
                sc() + kGenCount, kGenCap, x_, h_last_, h_prev_, H, st_);
     }
 
-    // MTP stem draft of n tokens: tok_[0] = next token, tok_[1..n] = drafts.
+    // MLP of one layer on the normalised input (xn_ / frag_): gate/up (SwiGLU) then
+    // down into the residual partials; returns the partial count for norm_residual.
+    int mlp_unfolded(const Layer& Ly, int T) {
+        const int I = c_.intermediate;
+        const bool down_frag = Ly.down.kind == RL_Q_FP8_E4M3_B128 || Ly.down.kind == RL_Q_BF16;
+        if (Ly.gate_up.kind >= 0) {
+            // SwiGLU epilogue: fp32 h only when a K-quant down needs it
+            if (Ly.gate_up.kind == RL_Q_FP8_E4M3_B128)
+                gemm_fp8_frag(Ly.gate_up.w, Ly.gate_up.ts, frag_, down_frag ? nullptr : h_, Ly.gate_up.m,
+                              Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1, down_frag ? frag_h_ : nullptr);
+            else
+                gemm_bf16_frag(reinterpret_cast<const uint16_t*>(Ly.gate_up.w), frag_, down_frag ? nullptr : h_,
+                               Ly.gate_up.m, Ly.gate_up.n, T, Ly.gate_up.swiglu_epi(), I, I, st_, 1,
+                               down_frag ? frag_h_ : nullptr);
+        } else {
+            if (Ly.gate_cat) {
+                KqNorm ks;
+                ks.swiglu = 1;
+                kq_gemm(Ly.gate.kind == RL_Q_Q4_K ? 4 : 6, Ly.gate.w, xn_, h_, kq_ws_, kq_ws_bytes_, Ly.gate.m,
+                        Ly.gate.n, T, 0, I, st_, &ks);
+            } else {
+                linear(Ly.gate, xn_, g_, I, I, T, kEpiStore);
+                linear(Ly.up, xn_, u_, I, I, T, kEpiStore);
+                swiglu(g_, I, u_, I, h_, I, T, st_);
+            }
+            if (down_frag) pack_act(h_, frag_h_, I, T, st_);
+        }
+        return linear_residual(Ly.down, h_, T, down_frag ? frag_h_ : frag_);
+    }
+
+    // The MTP decoder layer on the draft's hidden h (in place), at draft position
+    // `dpos` of its own cache (Session::mtp_layer_step, session.cpp:561-617: the
+    // fused attention decode then the fused MLP decode with the mtp.layers[0]
+    // weights, each adding into h).  Leaves norm_mtp(h) in xn_ / frag_ for the
+    // lm_head, as the stem's final RMSNorm does.
+    void mtp_layer_step(float* h, int dpos) {
+        const int H = c_.hidden;
+        const float eps = c_.rms_eps;
+        const Layer& Ly = mtp_layer_;
+        rmsnorm_pack(h, H, Ly.attn_norm, xn_, frag_, H, 1, eps, st_);
+        linear_parts(Ly.qkv_parts, Ly.qkv_offs, xn_, ybuf_, Ly.qkv_width, 1);
+        attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, mtp_kc_, mtp_vt_, kMtpCtx, mtp_pos_ + dpos, 1,
+                          c_.n_q, c_.n_kv, c_.head_dim, c_.rotary_dim, c_.rope_theta, eps, mtp_attn_ws_,
+                          mtp_attn_ws_bytes_, xn_, frag_, st_);
+        int pending = linear_residual(Ly.o_proj, xn_, 1);
+        residual_rmsnorm_pack(h, part_, pending, mtp_x1_, Ly.ffn_norm, xn_, frag_, H, 1, eps, st_);
+        pending = mlp_unfolded(Ly, 1);
+        residual_rmsnorm_pack(mtp_x1_, part_, pending, h, mtp_norm_, xn_, frag_, H, 1, eps, st_);
+    }
+
+    // MTP draft of n tokens: tok_[0] = next token, tok_[1..n] = drafts.  The stem
+    // (Session::mtp_draft): h' = fc([norm_e(embed tok) ; norm_h(h)]), token =
+    // argmax(lm_head(norm_mtp(h'))); with the decoder layer (mtp_mode_ ==
+    // RL_MTP_LAYER) h' passes through mtp_layer_step at draft position i first.
     void mtp_body(int n) {
         const int H = c_.hidden;
         const float eps = c_.rms_eps;
@@ -1754,7 +1849,10 @@ class Engine {
             rmsnorm_pack(i == 0 ? h_last_ : h_prev_, H, mtp_nh_, xn_ + H, static_cast<i32x4*>(frag_) + half_units, H, 1,
                          eps, st_);
             linear(mtp_fc_, xn_, mtp_hp_, H, H, 1, kEpiStore);
-            rmsnorm_pack(mtp_hp_, H, mtp_norm_, xn_, frag_, H, 1, eps, st_);
+            if (mtp_mode_ == RL_MTP_LAYER)
+                mtp_layer_step(mtp_hp_, i);
+            else
+                rmsnorm_pack(mtp_hp_, H, mtp_norm_, xn_, frag_, H, 1, eps, st_);
             linear(lm_head_, xn_, mtp_logits_, c_.vocab, c_.vocab, 1, kEpiStore);
             argmax_rows(mtp_logits_, 1, c_.vocab, tok_ + i + 1, nullptr, arg_ws_, st_);
         }
@@ -1768,7 +1866,7 @@ class Engine {
     }
 
     void run_mtp(int n) {
-        launch_captured(100 + n, [&] { mtp_body(n); });
+        launch_captured((mtp_mode_ == RL_MTP_LAYER ? 200 : 100) + n, [&] { mtp_body(n); });
     }
 
     // RL_HIP_GRAPHS=0 runs every step eagerly (same kernels, launched one by one):
@@ -2026,6 +2124,28 @@ int rl_hip_engine_spec_verify(RlEngine* e, const int32_t* toks, int T, int32_t* 
         if (n_consumed) *n_consumed = k;
     });
 }
+int rl_hip_engine_set_mtp_mode(RlEngine* e, int mode) {
+    return guard([&] {
+        RL_REQUIRE(e, RL_ERR_RANGE, "null engine");
+        e->e->set_mtp_mode(mode);
+    });
+}
+
+int rl_hip_engine_mtp_mode(RlEngine* e, int* mode, int* layer_available) {
+    return guard([&] {
+        RL_REQUIRE(e && mode && layer_available, RL_ERR_RANGE, "null argument");
+        *mode = e->e->mtp_mode();
+        *layer_available = e->e->has_mtp_layer() ? 1 : 0;
+    });
+}
+
+int rl_hip_engine_copy_mtp_hidden(RlEngine* e, float* out) {
+    return guard([&] {
+        RL_REQUIRE(e && out, RL_ERR_RANGE, "null argument");
+        e->e->copy_mtp_hidden(out);
+    });
+}
+
 int rl_hip_engine_mtp_spec(RlEngine* e, int32_t t0, int T, int32_t* toks_out, int32_t* preds, int* n_consumed) {
     return guard([&] {
         RL_ENGINE(e);

@@ -18,6 +18,9 @@ from .hip import call
 from .model import ModelSpec, WeightTable
 
 
+MTP_STEM, MTP_LAYER = 0, 1
+
+
 class Engine:
     def __init__(self, spec: ModelSpec, weights: WeightTable | None = None, ctx: int = 4096, max_T: int = 4,
                  seed: int = 0, max_batch: int = 1):
@@ -90,6 +93,22 @@ class Engine:
         k = C.c_int()
         call("rl_hip_engine_spec_verify", self.h, toks.ctypes.data, toks.size, preds.ctypes.data, C.byref(k))
         return k.value, preds
+
+    def set_mtp_mode(self, mode: int) -> None:
+        """MTP_STEM (Session::mtp_draft) or MTP_LAYER (stem + mtp.layers[0],
+        Session::mtp_layer_step)."""
+        call("rl_hip_engine_set_mtp_mode", self.h, int(mode))
+
+    def mtp_mode(self):
+        """(mode, whether the model has the MTP decoder layer)."""
+        m, a = C.c_int(), C.c_int()
+        call("rl_hip_engine_mtp_mode", self.h, C.byref(m), C.byref(a))
+        return m.value, bool(a.value)
+
+    def copy_mtp_hidden(self) -> np.ndarray:
+        h = np.empty(self.spec.hidden, np.float32)
+        call("rl_hip_engine_copy_mtp_hidden", self.h, h.ctypes.data)
+        return h
 
     def mtp_spec(self, t0: int, T: int):
         toks = np.zeros(T, np.int32)

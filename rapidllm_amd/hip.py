@@ -96,6 +96,9 @@ _SIGS = {
     "rl_hip_engine_mtp_draft": (_i, [_vp, C.c_int32, _i, _vp, C.POINTER(_i)]),
     "rl_hip_engine_spec_verify": (_i, [_vp, _vp, _i, _vp, C.POINTER(_i)]),
     "rl_hip_engine_mtp_spec": (_i, [_vp, C.c_int32, _i, _vp, _vp, C.POINTER(_i)]),
+    "rl_hip_engine_set_mtp_mode": (_i, [_vp, _i]),
+    "rl_hip_engine_mtp_mode": (_i, [_vp, C.POINTER(_i), C.POINTER(_i)]),
+    "rl_hip_engine_copy_mtp_hidden": (_i, [_vp, _vp]),
     "rl_hip_engine_greedy": (_i, [_vp, C.POINTER(C.c_int32)]),
     "rl_hip_engine_pos": (_i, [_vp, C.POINTER(_i)]),
     "rl_hip_engine_info": (_i, [_vp, C.POINTER(_i), C.POINTER(_i), C.POINTER(_i), C.POINTER(_sz)]),

@@ -101,6 +101,13 @@ public:
         size_t bytes = 0;
         int cap = 0;
         check(rl_hip_engine_info(e_, &vocab_, &hidden_, &cap, &bytes));
+        // RAPIDLLM_HIP_MTP_LAYER=1: draft through the MTP decoder layer
+        // (mtp.layers[0], Session::mtp_layer_step) when the weights have it; the
+        // default is the stem, as Session::mtp_draft's CPU branch
+        const char* ml = std::getenv("RAPIDLLM_HIP_MTP_LAYER");
+        int mode = RL_MTP_STEM, have_layer = 0;
+        check(rl_hip_engine_mtp_mode(e_, &mode, &have_layer));
+        if (ml && ml[0] == '1' && have_layer) check(rl_hip_engine_set_mtp_mode(e_, RL_MTP_LAYER));
     }
     ~HipEngine() override { rl_hip_engine_destroy(e_); }
 

@@ -55,6 +55,7 @@ class ModelSpec:
     rms_eps: float = 1e-6
     v_tiled: bool = False
     has_mtp: bool = True
+    mtp_layer: bool = False  # random_weights adds the MTP decoder layer mtp.layers[0].*
     layer_kinds: list = field(default_factory=list)
 
     def __post_init__(self):
@@ -179,4 +180,17 @@ def random_weights(spec: ModelSpec, seed: int = 1, linear_quant: int = Q_FP8, em
         vec("mtp.pre_fc_norm_hidden", H)
         vec("mtp.pre_fc_norm_embedding", H)
         vec("mtp.norm", H)
+        if spec.mtp_layer:
+            p = "mtp.layers[0]."
+            vec(p + "attn_norm", H)
+            vec(p + "ffn_norm", H)
+            lin(p + "attn.wq", 2 * nq * hd, H)
+            lin(p + "attn.wk", nkv * hd, H)
+            lin(p + "attn.wv", nkv * hd, H)
+            lin(p + "attn.wo", H, nq * hd)
+            vec(p + "attn.q_norm", hd)
+            vec(p + "attn.k_norm", hd)
+            lin(p + "mlp.gate", I, H)
+            lin(p + "mlp.up", I, H)
+            lin(p + "mlp.down", H, I)
     return W

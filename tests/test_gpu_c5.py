@@ -38,7 +38,7 @@ def margin_ok(logits, tol=TOL):
 
 @pytest.fixture(scope="module")
 def wide_pair(orc):
-    spec = M.ModelSpec(n_layers=4, layer_kinds=[0, 0, 0, 1])
+    spec = M.ModelSpec(n_layers=4, layer_kinds=[0, 0, 0, 1], mtp_layer=True)
     W = M.random_weights(spec, seed=0xC5, w_scale=(1e-3, 1e-2))
     eng = Engine(spec, W, ctx=1024)
     om = OracleModel(spec, W, ctx=1024, threads=16)
@@ -111,6 +111,39 @@ def test_wide_mtp_and_verify_match_oracle(gpu, wide_pair):
         if margin_ok(want[i][1]):
             assert preds[i] == want[i][0]
     assert rel_l2(eng.copy_logits(), want[k - 1][1]) < TOL
+
+
+def test_wide_mtp_layer_drafts_match_oracle(gpu, wide_pair):
+    """The MTP decoder-layer draft (stem + mtp.layers[0], Session::mtp_layer_step)
+    at 27B width: drafts equal the oracle's and the last draft's hidden is within
+    1e-3; speculative generation with these drafts equals plain generation."""
+    from rapidllm_amd.engine import MTP_LAYER, MTP_STEM
+
+    spec, W, eng, om = wide_pair
+    assert eng.mtp_mode() == (MTP_STEM, True)
+    prompt = [2, 7, 1, 8, 2, 8]
+    eng.prefill(prompt)
+    om.reset()
+    for t in prompt:
+        g, lg, _ = om.decode(t)
+    t0 = eng.greedy()
+    stem = eng.mtp_draft(t0, 3)
+    stem_h = eng.copy_mtp_hidden()
+    eng.set_mtp_mode(MTP_LAYER)
+    om.set_mtp_mode(1)
+    try:
+        got = eng.mtp_draft(t0, 3)
+        want = om.mtp_draft(t0, 3)
+        h = eng.copy_mtp_hidden()
+        assert rel_l2(h, om.mtp_hidden()) < TOL
+        assert got.tolist() == want.tolist()
+        assert rel_l2(h, stem_h) > 0.1 or got.tolist() != stem.tolist()
+        off, _, _ = eng.generate(prompt, 12, spec_n=0)
+        on, _, _ = eng.generate(prompt, 12, spec_n=3)
+        assert on == off
+    finally:
+        eng.set_mtp_mode(MTP_STEM)
+        om.set_mtp_mode(0)
 
 
 # ----------------------------------------------------- full 64-layer C5 engine

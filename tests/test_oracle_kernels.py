@@ -451,3 +451,73 @@ def test_argmax_rows_matches_numpy(orc):
     r = synth.rng(23)
     L = r.integers(-5, 5, (6, 1000)).astype(np.float32)
     assert np.array_equal(orc.argmax_rows(L), np.argmax(L, axis=1))
+
+
+def test_oracle_mtp_layer_draft_equals_reference_composition(orc, ref_lib):
+    """The oracle's MTP decoder-layer draft against Session::mtp_layer_step composed
+    from the reference's own kernels (session.cpp:561-617 after the stem of
+    :650-680): per draft i, h' = gemv_fp8(fc, [norm_e(embed tok); norm_h(h)]), then
+    ops::fused_attn_decode with the mtp.layers[0] weights at position i of a cache
+    zeroed per call, ops::fused_mlp_decode, qwen3_rmsnorm(mtp.norm), gemv_bf16
+    (lm_head) and greedy_sample.  Drafts equal; the last hidden within 1e-6
+    relative L2 (the reference's SIMD RMSNorm / SwiGLU inside the fused decode
+    functions round a few last bits differently from the scalar restatement)."""
+    from oracle.oracle import OracleModel, P, _u8, _u16
+    from rapidllm_amd import model as M
+
+    spec = M.ModelSpec(vocab=300, hidden=256, n_layers=4, intermediate=512, n_k_heads=2, n_v_heads=4, n_q=4,
+                       n_kv=2, head_dim=64, rotary_dim=16, layer_kinds=[0, 0, 0, 1], mtp_layer=True)
+    W = M.random_weights(spec, seed=21, w_scale=(1e-3, 1e-2))
+    t = {n: (q, d, r, c, s) for n, (q, r, c, d, s) in W.t.items()}
+    om = OracleModel(spec, W, ctx=64, kv_fp16=False, threads=1)
+    hid = []
+    for tok in [5, 17, 42, 99]:
+        g, _, h = om.decode(tok)
+        hid.append(h)
+    H, V, hd, nq, nkv = spec.hidden, spec.vocab, spec.head_dim, spec.n_q, spec.n_kv
+    R = ref_lib
+
+    def f32(n):
+        return np.ascontiguousarray(t[n][1], np.float32)
+
+    def fp8(n):
+        return np.ascontiguousarray(t[n][1], np.uint8), np.ascontiguousarray(t[n][4], np.float32)
+
+    def rms(x, n):
+        y = np.empty_like(x)
+        R.ref_qwen3_rmsnorm(P(x), P(f32(n)), P(y), H, spec.rms_eps)
+        return y
+
+    emb = t["embed"][1].reshape(V, H)
+    n = 4
+    kc = np.zeros(n * nkv * hd, np.float32)
+    vc = np.zeros_like(kc)
+    tok, drafts = g, []
+    for i in range(n):
+        href = hid[-1] if i == 0 else hid[-2]
+        er = synth.bf16_to_f32(emb[tok]).astype(np.float32)
+        cat = np.concatenate([rms(er, "mtp.pre_fc_norm_embedding"), rms(href, "mtp.pre_fc_norm_hidden")])
+        hp = np.empty(H, np.float32)
+        w, s = fp8("mtp.fc")
+        R.ref_gemv_fp8(P(w, _u8), P(s), P(cat), P(hp), H, 2 * H)
+        p = "mtp.layers[0]."
+        q, k, v, o = fp8(p + "attn.wq"), fp8(p + "attn.wk"), fp8(p + "attn.wv"), fp8(p + "attn.wo")
+        R.ref_fused_attn(P(f32(p + "attn_norm")), P(q[0], _u8), P(q[1]), P(k[0], _u8), P(k[1]), P(v[0], _u8),
+                         P(v[1]), P(o[0], _u8), P(o[1]), P(f32(p + "attn.q_norm")), P(f32(p + "attn.k_norm")),
+                         P(kc), P(vc), P(hp), H, nq, nkv, hd, spec.rotary_dim, i, spec.rope_theta, spec.rms_eps)
+        gt, up, dn = fp8(p + "mlp.gate"), fp8(p + "mlp.up"), fp8(p + "mlp.down")
+        R.ref_fused_mlp(P(f32(p + "ffn_norm")), P(gt[0], _u8), P(gt[1]), P(up[0], _u8), P(up[1]), P(dn[0], _u8),
+                        P(dn[1]), P(hp), H, spec.intermediate, spec.rms_eps)
+        lg = np.empty(V, np.float32)
+        R.ref_gemv_bf16(P(np.ascontiguousarray(t["lm_head"][1], np.uint16), _u16), P(rms(hp, "mtp.norm")), P(lg), V, H)
+        tok = R.ref_greedy(P(lg), V)
+        drafts.append(tok)
+    om.set_mtp_mode(1)
+    got = om.mtp_draft(g, n).tolist()
+    assert got == drafts
+    got_h = om.mtp_hidden().astype(np.float64)
+    assert np.linalg.norm(got_h - hp) / np.linalg.norm(hp) < 1e-6
+    # the stem alone drafts from a different hidden (the layer is not a no-op)
+    om.set_mtp_mode(0)
+    om.mtp_draft(g, n)
+    assert not np.allclose(om.mtp_hidden(), hp)
