@@ -83,6 +83,14 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                                                                 i32x4* __restrict__ frag_out, NormIO io) {
     const int T = TT > 0 ? TT : T_;
     const int epilogue = EPI >= 0 ? EPI : epilogue_;
+    // Partial sums per workgroup: column block kb goes to partial kb % KP, which
+    // wave kb % KSPLIT accumulates (KP / KSPLIT of them per wave), and the partials
+    // are added in index order.  The residual add-norm kernels use 16 partials
+    // with 8 or 16 waves, so every work split gives identical sums (a row of a
+    // T = 1 step equals the same row of a T = 2..4 verify or batch step).
+    constexpr int KP = (EPI == kAddNorm && RT == 2 && KSPLIT <= 16) ? 16 : KSPLIT;
+    constexpr int NP = KP / KSPLIT;
+    static_assert(KP % KSPLIT == 0 && (NP == 1 || D == 1), "partials: a multiple of the waves, depth 1");
     if constexpr (SSIN == 0) io.ss_in = nullptr;
     const bool has_ss = SSIN == 1 || (SSIN < 0 && io.ss_in != nullptr);
     constexpr int kTileBytes = kFp8 ? 2048 : 4096;
@@ -106,9 +114,12 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     const int kb_begin = min(s_end, s_begin + wave * per);
     const int kb_end = min(s_end, kb_begin + per);
 
-    f32x4 tot[RT];
+    f32x4 tots[NP][RT];
 #pragma unroll
-    for (int r = 0; r < RT; ++r) tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) tots[q][r] = f32x4{0.f, 0.f, 0.f, 0.f};
+    f32x4* tot = tots[0];
 
     // RMSNorm folded into this GEMM (io.ss_in): the input fragments hold x * (1+gamma)
     // unnormalised, and the outputs are scaled by 1/rms(x_t).  Wave w < T sums the
@@ -143,7 +154,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
             __builtin_amdgcn_global_load_lds(src, &ss_lds[wave][64 * k], 4, 0, 0);
         }
     }
-    __shared__ f32x4 red[KSPLIT][RT][64];
+    __shared__ f32x4 red[KP][RT][64];
     __shared__ float s_inv[8];
     // Token `wave`'s 1/rms from the sums of squares in LDS (every load of this wave,
     // the copies included, has completed: the wait is explicit for waves that had no
@@ -250,7 +261,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
             for (int i = 0; i < 4; ++i) bbuf[d][i] = fbase[kb * fstride + i * 4 * NC];
         }
     };
-    auto compute = [&](int d, int kb, float ks = 1.f) {
+    auto compute = [&](int d, int kb, float ks = 1.f, int q = 0) {
+        f32x4* tot = tots[q];
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
             f32x4 acc = {0.f, 0.f, 0.f, 0.f};
@@ -287,16 +299,29 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         // loads; measured as fast as any explicit pipeline for the FP8 launches).
         // Wave w takes blocks w, w + KSPLIT, ...: at any moment the workgroup reads
         // KSPLIT adjacent tiles per row-tile (1-3% faster than contiguous runs)
+        // (with NP > 1 partials per wave, its j-th block goes to partial j % NP)
         if constexpr (kKs) {
-            for (int kb = s_begin + wave; kb < s_end; kb += KSPLIT) {
-                const float4 q = block_sums(kb);
-                load(0, kb, true);
-                compute(0, kb, block_scale(q));
+            for (int kb0 = s_begin + wave; kb0 < s_end; kb0 += KSPLIT * NP) {
+#pragma unroll
+                for (int q = 0; q < NP; ++q) {
+                    const int kb = kb0 + q * KSPLIT;
+                    if (q == 0 || kb < s_end) {
+                        const float4 qs = block_sums(kb);
+                        load(0, kb, true);
+                        compute(0, kb, block_scale(qs), q);
+                    }
+                }
             }
         } else {
-            for (int kb = s_begin + wave; kb < s_end; kb += KSPLIT) {
-                load(0, kb, true);
-                compute(0, kb);
+            for (int kb0 = s_begin + wave; kb0 < s_end; kb0 += KSPLIT * NP) {
+#pragma unroll
+                for (int q = 0; q < NP; ++q) {
+                    const int kb = kb0 + q * KSPLIT;
+                    if (q == 0 || kb < s_end) {
+                        load(0, kb, true);
+                        compute(0, kb, 1.f, q);
+                    }
+                }
             }
         }
     } else if (kb_begin < kb_end) {
@@ -325,7 +350,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     // Cross-wave reduction in a fixed order.  red[w][r][lane] holds C rows
     // 4*(lane/16)+v, column lane%16.
 #pragma unroll
-    for (int r = 0; r < RT; ++r) red[wave][r][lane] = tot[r];
+    for (int q = 0; q < NP; ++q)
+#pragma unroll
+        for (int r = 0; r < RT; ++r) red[wave + q * KSPLIT][r][lane] = tots[q][r];
     reduce_ss();
     __syncthreads();
 
@@ -336,7 +363,7 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         const int v = row & 3;
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < KSPLIT; ++w) s += red[w][r][src_lane + t][v] + red[w][r][src_lane + T + t][v];
+        for (int w = 0; w < KP; ++w) s += red[w][r][src_lane + t][v] + red[w][r][src_lane + T + t][v];
         return s;
     };
 
@@ -624,6 +651,15 @@ inline bool bperm_enabled() {
     return on;
 }
 
+// RL_ADDNORM16=0: the T = 1 residual add-norm launches keep 8 waves (A/B measurement)
+inline bool addnorm16_enabled() {
+    static const bool on = [] {
+        const char* v = std::getenv("RL_ADDNORM16");
+        return !(v && v[0] == '0');
+    }();
+    return on;
+}
+
 template <bool kFp8, int RT, int KS, int D, bool kKs, int TT, int EPI = -1, int SSIN = -1, bool kGuh = false>
 void launch_gemm_tt(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                     int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
@@ -730,15 +766,24 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
     // residual GEMMs (m = hidden: 160 groups): 8 waves measured faster than 16 there
     // (5120x17408: 21.2 vs 22.8 us cold); the sum-of-squares groups are 2 row tiles
-    if (epilogue == kAddNorm && !g_force.rt) c = GemmCfg{2, 8, kFp8 ? 1 : 2};
+    // At T = 1 (permuted-B kernels) 16 waves: 5120 x 17408 19.1 vs 20.1 us, 5120 x 6144
+    // 8.2 vs 8.4 us cold; at T = 4 they are slower (24.6 vs 22.3 us).  Both splits
+    // add the same 16 partial sums in the same order (gemm_frag_kernel's KP), so a
+    // T = 1 row equals the same row of a verify or batch step bit for bit.
+    if (epilogue == kAddNorm && !g_force.rt)
+        c = GemmCfg{2, kFp8 && bperm_enabled() && T == 1 && addnorm16_enabled() ? 16 : 8, kFp8 ? 1 : 2};
     if (io.ss_in || epilogue == kAddNorm)
         RL_REQUIRE(c.ks >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
     if (io.kss) {
         // folded gated norm (out_proj): the residual configuration only
         RL_REQUIRE(!io.ss_in && io.kss_n > 0 && S == 1, RL_ERR_RANGE, "gemm: bad block input scale");
         RL_REQUIRE(!g_force.rt, RL_ERR_UNSUPPORTED, "gemm: block input scale uses the residual work split");
-        launch_gemm_cfg<kFp8, 2, 8, 1, true>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out,
-                                             io, s);
+        if (c.ks == 16)
+            launch_gemm_cfg<kFp8, 2, 16, 1, true>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S,
+                                                  frag_out, io, s);
+        else
+            launch_gemm_cfg<kFp8, 2, 8, 1, true>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S,
+                                                 frag_out, io, s);
         check_launch("gemm_frag_kernel");
         return;
     }
