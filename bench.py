@@ -496,46 +496,121 @@ def host_info(R=None):
             "reference_isa": isa}
 
 
-def cpu_baseline(spec, sbytes_total, budget_s=20.0):
-    """The reference's own CPU decode path (oracle/_ref: ops_fused.cpp
-    fused_mlp_decode -> scalar gemv_fp8, the reference's only FP8 CPU GEMV, 1
-    thread) on one 27B MLP layer, extrapolated by algorithmic bytes to the full
-    step.  Falls back to the oracle restatement (kind "port") where the reference
-    objects were not built."""
+def cpu_baseline(spec, sbytes_total, ctx=None, budget_s=25.0):
+    """The reference's own CPU decode path (oracle/_ref, ops_fused.cpp), one layer of
+    each kind at the 27B shape, timed once each (and again while the budget lasts,
+    keeping the fastest): fused_delta_decode (block-FP8 in_proj / out_proj, the
+    recurrent update), fused_attn_decode at the step's context (FP8 projections,
+    attention over an fp32 cache of ctx positions), fused_mlp_decode (three FP8
+    GEMVs), and the bf16 lm_head GEMV.  The step is 48 / 16 / 64 / 1 of them
+    (session.cpp:325-411, 531-559).  The reference runs gemv_fp8 and attn_decode on
+    one thread (scalar loops, ops.cpp:182-194, 575-605) and gemv_bf16 and the
+    recurrent step on its WorkerPool (cpu_caps.cpp:123-131, 260-263); `cores` is
+    that pool's size.  Without the reference objects the MLP alone is timed on the
+    oracle restatement and scaled by bytes (kind "port")."""
     from oracle import oracle as O
     from rapidllm_amd import synth
 
+    ctx = ctx or CTX
     H, I = spec.hidden, spec.intermediate
+    nk, nv, dk, dv = spec.n_k_heads, spec.n_v_heads, spec.k_dim, spec.v_dim
+    nq, nkv, hd = spec.n_q, spec.n_kv, spec.head_dim
     r = synth.rng(9)
-    wg, wu = synth.fp8_weight(r, I, H), synth.fp8_weight(r, I, H)
-    wd = synth.fp8_weight(r, H, I)
-    sg, su, sd = synth.fp8_scales(r, I, H), synth.fp8_scales(r, I, H), synth.fp8_scales(r, H, I)
-    gam = (r.standard_normal(H) * 0.1).astype(np.float32)
+
+    def lin(m, n):
+        w = synth.fp8_weight_wide(r, m, n) if m * n >= 1 << 26 else synth.fp8_weight(r, m, n)
+        return w, synth.fp8_scales(r, m, n)
+
+    def vec(n, mean=0.0, sd=0.1):
+        return (mean + sd * r.standard_normal(n)).astype(np.float32)
+
+    wg, wu, wd = lin(I, H), lin(I, H), lin(H, I)
+    gam = vec(H)
     x0 = r.standard_normal(H).astype(np.float32)
     R = O.ref()
-    times = []
-    kind = "reference" if R is not None else "port"
-    t_end = time.time() + budget_s
-    while time.time() < t_end and len(times) < 5:
+    if R is None:
+        times = []
+        t_end = time.time() + budget_s
+        while time.time() < t_end and len(times) < 3:
+            x = x0.copy()
+            t = time.perf_counter()
+            xn = O.qwen3_rmsnorm(x, gam)
+            g = O.gemv_fp8(wg[0], wg[1], xn)
+            u = O.gemv_fp8(wu[0], wu[1], xn)
+            h = (g / (1 + np.exp(-g.astype(np.float64))) * u).astype(np.float32)
+            x += O.gemv_fp8(wd[0], wd[1], h)
+            times.append(time.perf_counter() - t)
+        t_m = float(min(times))
+        mlp_bytes = 3 * H * I
+        return {"value": round(mlp_bytes / (t_m * sbytes_total), 6), "unit": "tok/s", "cores": 1, "kind": "port",
+                "host": host_info(None),
+                "sample": f"oracle restatement of fused_mlp_decode (one 27B MLP layer, {t_m:.2f} s), scaled by "
+                          f"bytes to the {sbytes_total/1e9:.2f} GB step"}
+    P, u8 = O.P, O._u8
+    conv_dim = 2 * nk * dk + nv * dv
+    # DeltaNet layer
+    dq, dz, da, db, do = lin(conv_dim, H), lin(nv * dv, H), lin(nv, H), lin(nv, H), lin(H, nv * dv)
+    A_log, dt_bias, gnorm = vec(nv, 0, 0.5), vec(nv, 0, 0.5), vec(dv, 1.0, 0.1)
+    conv_w = vec(conv_dim * spec.conv_k, 0, 0.5)
+    S0 = (0.02 * r.standard_normal(nv * dk * dv)).astype(np.float32)
+    cs0 = r.standard_normal(conv_dim * spec.conv_k).astype(np.float32)
+    # attention layer: projections and a cache of ctx positions (fp32, as the CPU path keeps it)
+    aq, ak, av, ao = lin(2 * nq * hd, H), lin(nkv * hd, H), lin(nkv * hd, H), lin(H, nq * hd)
+    qn, kn = vec(hd), vec(hd)
+    kc = np.zeros((ctx + 1) * nkv * hd, np.float32)
+    vc = np.zeros_like(kc)
+    kc[: ctx * nkv * hd] = r.standard_normal(ctx * nkv * hd, dtype=np.float32)
+    vc[: ctx * nkv * hd] = r.standard_normal(ctx * nkv * hd, dtype=np.float32)
+    lm = synth.bf16_random_bits(r, spec.vocab, H)
+    logits = np.empty(spec.vocab, np.float32)
+
+    def t_delta():
+        x, S, cs = x0.copy(), S0.copy(), cs0.copy()
+        t = time.perf_counter()
+        R.ref_fused_delta(P(gam), P(dq[0], u8), P(dq[1]), P(dz[0], u8), P(dz[1]), P(da[0], u8), P(da[1]),
+                          P(db[0], u8), P(db[1]), P(do[0], u8), P(do[1]), P(A_log), P(dt_bias), P(conv_w), P(gnorm),
+                          P(S), P(cs), P(x), H, nk, nv, dk, dv, spec.conv_k, dv, spec.rms_eps)
+        return time.perf_counter() - t
+
+    def t_attn():
         x = x0.copy()
         t = time.perf_counter()
-        if R is not None:
-            R.ref_fused_mlp(O.P(gam), O.P(wg, O._u8), O.P(sg), O.P(wu, O._u8), O.P(su), O.P(wd, O._u8), O.P(sd),
-                            O.P(x), H, I, 1e-6)
-        else:
-            xn = O.qwen3_rmsnorm(x, gam)
-            g = O.gemv_fp8(wg, sg, xn)
-            u = O.gemv_fp8(wu, su, xn)
-            h = (g / (1 + np.exp(-g.astype(np.float64))) * u).astype(np.float32)
-            x += O.gemv_fp8(wd, sd, h)
-        times.append(time.perf_counter() - t)
-    t_med = float(np.median(times))
-    sample_bytes = wg.nbytes + wu.nbytes + wd.nbytes + 4 * (sg.size + su.size + sd.size)
-    sec_per_tok = t_med * sbytes_total / sample_bytes
-    return {"value": round(1.0 / sec_per_tok, 6), "unit": "tok/s", "cores": 1, "kind": kind, "host": host_info(R),
-            "sample": f"fused_mlp_decode of one 27B layer (3 block-FP8 GEMVs, {sample_bytes/1e6:.0f} MB) "
-                      f"median of {len(times)} runs = {t_med:.2f} s, scaled by bytes to the "
-                      f"{sbytes_total/1e9:.2f} GB T=1 step; scalar gemv_fp8 is single-threaded in the reference"}
+        R.ref_fused_attn(P(gam), P(aq[0], u8), P(aq[1]), P(ak[0], u8), P(ak[1]), P(av[0], u8), P(av[1]),
+                         P(ao[0], u8), P(ao[1]), P(qn), P(kn), P(kc), P(vc), P(x), H, nq, nkv, hd,
+                         spec.rotary_dim, ctx, spec.rope_theta, spec.rms_eps)
+        return time.perf_counter() - t
+
+    def t_mlp():
+        x = x0.copy()
+        t = time.perf_counter()
+        R.ref_fused_mlp(P(gam), P(wg[0], u8), P(wg[1]), P(wu[0], u8), P(wu[1]), P(wd[0], u8), P(wd[1]), P(x), H, I,
+                        spec.rms_eps)
+        return time.perf_counter() - t
+
+    def t_head():
+        t = time.perf_counter()
+        R.ref_gemv_bf16(P(lm, O._u16), P(x0), P(logits), spec.vocab, H)
+        return time.perf_counter() - t
+
+    parts = {"delta": t_delta, "attn": t_attn, "mlp": t_mlp, "lm_head": t_head}
+    best = {k: f() for k, f in parts.items()}
+    t_end = time.time() + budget_s - sum(best.values())
+    while time.time() + sum(best.values()) < t_end:
+        for k, f in parts.items():
+            best[k] = min(best[k], f())
+    n_d = sum(1 for k in spec.layer_kinds if k == 0)
+    n_a = spec.n_layers - n_d
+    step_s = n_d * best["delta"] + n_a * best["attn"] + spec.n_layers * best["mlp"] + best["lm_head"]
+    return {"value": round(1.0 / step_s, 6), "unit": "tok/s", "cores": int(R.ref_num_threads()), "kind": "reference",
+            "host": host_info(R),
+            "step_s": round(step_s, 2),
+            "per_layer_s": {k: round(v, 4) for k, v in best.items()},
+            "sample": f"one 27B layer of each kind through the reference's fused CPU decode functions "
+                      f"(fused_delta_decode {best['delta']:.3f} s, fused_attn_decode at {ctx} positions "
+                      f"{best['attn']:.3f} s, fused_mlp_decode {best['mlp']:.3f} s) and the bf16 lm_head GEMV "
+                      f"({best['lm_head']:.3f} s), fastest of repeated runs; step = {n_d} x delta + {n_a} x attn + "
+                      f"{spec.n_layers} x mlp + lm_head = {step_s:.1f} s; the FP8 GEMVs and the attention are "
+                      f"single-threaded in the reference, gemv_bf16 and the recurrent step use its worker pool"}
 
 
 def main():

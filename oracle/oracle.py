@@ -130,6 +130,8 @@ def ref():
         R.ref_num_threads.restype = C.c_int
         R.ref_simd_name.restype = C.c_char_p
         R.ref_fused_mlp.argtypes = [_f, _u8, _f, _u8, _f, _u8, _f, _f, C.c_int, C.c_int, C.c_float]
+        R.ref_fused_delta.argtypes = [_f, _u8, _f, _u8, _f, _u8, _f, _u8, _f, _u8, _f, _f, _f, _f, _f, _f, _f, _f,
+                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_int, C.c_float]
         R.ref_fused_attn.argtypes = [_f, _u8, _f, _u8, _f, _u8, _f, _u8, _f, _f, _f, _f, _f, _f, C.c_int, C.c_int,
                                      C.c_int, C.c_int, C.c_int, C.c_int, C.c_float, C.c_float]
         vp = C.c_void_p

@@ -72,6 +72,40 @@ void ref_fused_mlp(const float* rms_w, const uint8_t* wg, const float* sg, const
     ops::fused_mlp_decode(a);
 }
 
+// ops::fused_delta_decode (ops_fused.cpp:84-135) with block-FP8 projections (qkv, z,
+// a, b, out): x += the DeltaNet layer's output; S and the conv window advance.
+void ref_fused_delta(const float* rms_w, const uint8_t* wqkv, const float* sqkv, const uint8_t* wz, const float* sz,
+                     const uint8_t* wa, const float* sa, const uint8_t* wb, const float* sb, const uint8_t* wo,
+                     const float* so, const float* A_log, const float* dt_bias, const float* conv_w,
+                     const float* gnorm, float* S, float* conv_state, float* x, int hidden, int nk, int nv, int dk,
+                     int dv, int conv_k, int gnorm_n, float eps) {
+    ops::FusedDeltaArgs a{};
+    a.x = x;
+    a.x_inout = x;
+    a.rms_w = rms_w;
+    a.Wqkv = {wqkv, sqkv, QuantKind::FP8_E4M3_B128};
+    a.Wz = {wz, sz, QuantKind::FP8_E4M3_B128};
+    a.Wa = {wa, sa, QuantKind::FP8_E4M3_B128};
+    a.Wb = {wb, sb, QuantKind::FP8_E4M3_B128};
+    a.Wo = {wo, so, QuantKind::FP8_E4M3_B128};
+    a.A_log = A_log;
+    a.dt_bias = dt_bias;
+    a.conv_w = conv_w;
+    a.gnorm = gnorm;
+    a.S = S;
+    a.conv_state = conv_state;
+    a.hidden = hidden;
+    a.nk = nk;
+    a.nv = nv;
+    a.dk = dk;
+    a.dv = dv;
+    a.conv_k = conv_k;
+    a.gnorm_n = gnorm_n;
+    a.eps = eps;
+    a.use_simd = true;
+    ops::fused_delta_decode(a);
+}
+
 // ops::fused_attn_decode (ops_fused.cpp:137-184) with block-FP8 projections: x += the
 // gated attention output at position pos, K / V appended to the fp32 caches.
 void ref_fused_attn(const float* rms_w, const uint8_t* wq, const float* sq, const uint8_t* wk, const float* sk,
