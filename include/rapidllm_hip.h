@@ -361,6 +361,13 @@ int rl_hip_engine_copy_greedy_n(RlEngine* e, int32_t* host, int B);             
 int rl_hip_engine_replicate_slot0(RlEngine* e, int n_slots);                           /* :59 */
 int rl_hip_engine_zero_slots(RlEngine* e, int n_slots);                                /* :60 */
 int rl_hip_engine_prefill_slot(RlEngine* e, const int32_t* ids, int n, int slot);      /* :62 */
+/* Equal-length prompts of B sequences (ids time-major [T][B]) into slots 0 .. B-1,
+ * which the caller has zeroed (Session::generate_batch, session.cpp:882-893);
+ * afterwards copy_logits_n / copy_greedy_n return each slot's row after its last
+ * token.  Replaces Engine::prefill_eq_batch (cuda_engine.h:66-68,
+ * cuda_engine.cu:16998-17010).  T <= B runs T batch steps (B rows per weight pass);
+ * T > B runs each sequence's chunked prefill in its slot. */
+int rl_hip_engine_prefill_eq_batch(RlEngine* e, const int32_t* ids, int T, int B);
 
 /* ---- checkpoint loading ---------------------------------------------------
  * Replaces: rapidllm::make_loader + IWeightLoader::load + WeightStore::open

@@ -599,6 +599,42 @@ class Engine {
         cs_ = 0;
     }
 
+    // Equal-length prompts of B sequences into slots 0 .. B-1 (ids time-major
+    // [T][B], the slots zeroed by the caller as Session::generate_batch does,
+    // session.cpp:882-893); copy_logits_n / copy_greedy_n then return each slot's
+    // row after its last token, and every slot is at position T.
+    // T <= B: T batch steps of B rows (one weight pass each); T > B: the chunked
+    // prefill of each sequence in its slot (B passes whose GEMMs are compute-bound
+    // at prompt lengths: sharing the weight pass would save no arithmetic).
+    void prefill_eq_batch(const int32_t* ids, int T, int B) {
+        RL_REQUIRE(ids && B >= 2 && B <= mb_ && T >= 1 && T <= ctx_capacity(), RL_ERR_RANGE,
+                   "prefill_eq_batch: B must be in 2..max_batch, T in 1..ctx");
+        check_ids(ids, T * B);
+        if (T <= B) {
+            std::vector<int> poss(B);
+            for (int t = 0; t < T; ++t) {
+                for (int b = 0; b < B; ++b) poss[b] = t;
+                decode_tokens(ids + static_cast<size_t>(t) * B, poss.data(), B);
+            }
+            return;
+        }
+        std::vector<int32_t> seq(T);
+        std::vector<int32_t> preds(B);
+        const size_t V = c_.vocab;
+        for (int b = 0; b < B; ++b) {
+            for (int t = 0; t < T; ++t) seq[t] = ids[static_cast<size_t>(t) * B + b];
+            prefill_slot(seq.data(), T, b);
+            const int row = n_last_ > 0 ? n_last_ - 1 : 0;
+            RL_HIP(hipMemcpyAsync(eq_logits_ + b * V, logits_ + row * V, V * sizeof(float), hipMemcpyDeviceToDevice,
+                                  st_));
+            preds[b] = greedy_;
+        }
+        RL_HIP(hipMemcpyAsync(logits_, eq_logits_, B * V * sizeof(float), hipMemcpyDeviceToDevice, st_));
+        RL_HIP(hipStreamSynchronize(st_));
+        std::memcpy(host_rb_ + kRbPreds, preds.data(), static_cast<size_t>(B) * sizeof(int));
+        batch_rows_ = B;
+    }
+
    private:
     // device scalar block
     enum { kPos = 0, kSlot = 1, kNCons = 2, kNextTok = 3, kGenCount = 4, kScalars = 8 };
@@ -705,6 +741,7 @@ class Engine {
     size_t mtp_attn_ws_bytes_ = 0;
     int* mtp_pos_ = nullptr;    // [kMtpCtx] = 0, 1, 2, ... (device positions of the drafts)
     float* mtp_x1_ = nullptr;  // [H] residual between the layer's attention and MLP
+    float* eq_logits_ = nullptr;  // [max_batch][V]: prefill_eq_batch's last rows
     float* h_last_ = nullptr;
     float* h_prev_ = nullptr;
     void* attn_ws_ = nullptr;
@@ -972,6 +1009,7 @@ class Engine {
         g_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         u_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         logits_ = mem_.get_n<float>(static_cast<size_t>(T) * c_.vocab);
+        if (mb_ > 1) eq_logits_ = mem_.get_n<float>(static_cast<size_t>(mb_) * c_.vocab);
         mtp_logits_ = mem_.get_n<float>(c_.vocab);
         mtp_e_ = mem_.get_n<float>(H);
         mtp_cat_ = mem_.get_n<float>(2 * static_cast<size_t>(H));
@@ -2235,6 +2273,12 @@ int rl_hip_engine_prefill_slot(RlEngine* e, const int32_t* ids, int n, int slot)
     return guard([&] {
         RL_ENGINE(e);
         e->e->prefill_slot(ids, n, slot);
+    });
+}
+int rl_hip_engine_prefill_eq_batch(RlEngine* e, const int32_t* ids, int T, int B) {
+    return guard([&] {
+        RL_ENGINE(e);
+        e->e->prefill_eq_batch(ids, T, B);
     });
 }
 int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms) {

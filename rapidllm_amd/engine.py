@@ -195,6 +195,13 @@ class Engine:
         ids = np.ascontiguousarray(ids, np.int32)
         call("rl_hip_engine_prefill_slot", self.h, ids.ctypes.data, ids.size, slot)
 
+    def prefill_eq_batch(self, prompts):
+        """Equal-length prompts into slots 0 .. B-1 (zero_slots first, as the
+        Session does); then copy_logits_n / copy_greedy_n hold each slot's row."""
+        ids = np.ascontiguousarray(np.asarray(prompts, np.int32).T)  # time-major [T][B]
+        T, B = ids.shape
+        call("rl_hip_engine_prefill_eq_batch", self.h, ids.ctypes.data, T, B)
+
     def time_batch(self, B: int, iters: int) -> float:
         ms = C.c_float()
         call("rl_hip_engine_time_batch", self.h, B, iters, C.byref(ms))

@@ -115,6 +115,7 @@ _SIGS = {
     "rl_hip_engine_replicate_slot0": (_i, [_vp, _i]),
     "rl_hip_engine_zero_slots": (_i, [_vp, _i]),
     "rl_hip_engine_prefill_slot": (_i, [_vp, _vp, _i, _i]),
+    "rl_hip_engine_prefill_eq_batch": (_i, [_vp, _vp, _i, _i]),
     "rl_hip_engine_time_batch": (_i, [_vp, _i, _i, C.POINTER(C.c_float)]),
     "rl_hip_weights_open": (_vp, [C.c_char_p, _i, C.POINTER(C.c_int)]),
     "rl_hip_weights_close": (None, [_vp]),

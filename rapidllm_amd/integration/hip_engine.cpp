@@ -164,8 +164,11 @@ public:
     void prefill_slot(const int32_t* ids, int n, int slot) override {
         check(rl_hip_engine_prefill_slot(e_, ids, n, slot));
     }
-    // prefill_eq_batch keeps the base class's `return false`: the Session then
-    // feeds equal-length prompts through decode_tokens position by position.
+    bool prefill_eq_batch(const int32_t* ids, int T, int B) override {
+        if (!ids || T <= 0 || B <= 1 || B > max_batch()) return false;
+        check(rl_hip_engine_prefill_eq_batch(e_, ids, T, B));
+        return true;
+    }
 
 private:
     int spec(int32_t t0, int T, int32_t* pm) {

@@ -299,3 +299,45 @@ def test_kquant_batch_then_speculative_on_one_engine(gpu, quant):
     assert on == plain and prop > 0
     eng.close()
     ref.close()
+
+
+@pytest.mark.parametrize("T,B", [(3, 4), (9, 2), (300, 3)])
+def test_prefill_eq_batch_vs_oracle(gpu, orc, T, B):
+    """Engine::prefill_eq_batch (cuda_engine.h:66-68, called by
+    Session::generate_batch for equal-length prompts after zero_slots,
+    session.cpp:882-893): each slot's last-token logits and greedy token against its
+    own oracle model, then batch decode steps continue from position T.  T <= B
+    runs T batch steps; T > B each sequence's chunked prefill."""
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=70 + T, w_scale=(1e-3, 1e-2))
+    eng = Engine(spec, W, ctx=512, max_batch=4)
+    rng = np.random.default_rng(T * 10 + B)
+    prompts = [[int(t) for t in rng.integers(0, spec.vocab, T)] for _ in range(B)]
+    oms = [OracleModel(spec, W, ctx=512) for _ in range(B)]
+    want = []
+    for b in range(B):
+        for t in prompts[b]:
+            g, lg, _ = oms[b].decode(t)
+        want.append((g, lg))
+    eng.decode_token(5)  # slot 0 holds another sequence before the reset
+    eng.zero_slots(B)
+    eng.prefill_eq_batch(prompts)
+    rows = eng.copy_logits_n(B)
+    greedy = eng.copy_greedy_n(B)
+    toks = []
+    for b in range(B):
+        g, lg = want[b]
+        assert rel_l2(rows[b], lg) < TOL, (b, rel_l2(rows[b], lg))
+        if margin_ok(lg):
+            assert greedy[b] == g, b
+        toks.append(g)
+    poss = [T] * B
+    for step in range(2):
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(B)
+        for b in range(B):
+            g, lg, _ = oms[b].decode(toks[b])
+            assert rel_l2(rows[b], lg) < TOL, (step, b)
+            toks[b] = g
+        poss = [p + 1 for p in poss]
+    eng.close()
