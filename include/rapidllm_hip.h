@@ -350,8 +350,10 @@ void* rl_hip_engine_stream(RlEngine* e);
  * at position poss[b] for slots 0 .. B-1 in one weight pass (B = 1: set_pos +
  * decode_token, as the reference); copy_logits_n / copy_greedy_n return its B rows.
  * prefill_slot runs the prefill on slot `slot` (copy_logits then has its last row).
- * Needs the folded path: FP8 / BF16 linears (v_dim 128) with max_batch <= 8, or
- * K-quant (Q4_K / Q6_K) linears with max_batch <= 4; otherwise RL_ERR_UNSUPPORTED. */
+ * max_batch <= 16.  A step over more slots than one weight pass takes (8 rows for
+ * FP8 / BF16 linears, 4 for the K-quant GEMV) runs them in groups, one weight pass
+ * each.  Needs the folded path: FP8 / BF16 linears (v_dim 128), or K-quant
+ * (Q4_K / Q6_K) linears with max_T <= 4; otherwise RL_ERR_UNSUPPORTED. */
 RlEngine* rl_hip_engine_create_batch(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx,
                                      int max_T, int max_batch, int* status);
 int rl_hip_engine_max_batch(RlEngine* e, int* max_batch);                              /* :46 */

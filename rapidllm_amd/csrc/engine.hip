@@ -113,8 +113,8 @@ class Engine {
    public:
     Engine(const RlModelConfig& cfg, int ctx, int tmax, int max_batch = 1) : c_(cfg), tmax_(tmax), mb_(max_batch) {
         RL_REQUIRE(tmax >= 1 && tmax <= 4, RL_ERR_RANGE, "engine: max_T must be in 1..4");
-        RL_REQUIRE(max_batch >= 1 && max_batch <= 8, RL_ERR_RANGE, "engine: max_batch must be in 1..8");
-        tcap_ = std::max(tmax_, mb_);
+        RL_REQUIRE(max_batch >= 1 && max_batch <= kMaxSlots, RL_ERR_RANGE, "engine: max_batch must be in 1..16");
+        tcap_ = std::max(tmax_, std::min(mb_, kGroupRows));
         RL_REQUIRE(c_.n_layers >= 1 && c_.n_layers <= RL_MAX_LAYERS, RL_ERR_RANGE, "engine: bad layer count");
         RL_REQUIRE(c_.hidden % 128 == 0, RL_ERR_UNSUPPORTED, "engine: hidden must be a multiple of 128");
         RL_REQUIRE(c_.k_dim == 128 && c_.v_dim % 32 == 0, RL_ERR_UNSUPPORTED, "engine: DeltaNet dims 128 / 32k");
@@ -492,7 +492,7 @@ class Engine {
         RL_HIP(hipEventCreate(&a));
         RL_HIP(hipEventCreate(&b));
         RL_HIP(hipEventRecord(a, st_));
-        for (int i = 0; i < iters; ++i) launch_captured(200 + B, [&] { step_batch(B); });
+        for (int i = 0; i < iters; ++i) launch_captured(200 + B, [&] { batch_groups(B); });
         RL_HIP(hipEventRecord(b, st_));
         RL_HIP(hipEventSynchronize(b));
         float ms = 0.f;
@@ -524,13 +524,13 @@ class Engine {
         }
         // one staging of tokens and positions (every call ends with a sync)
         std::memcpy(host_in_, tokens, static_cast<size_t>(B) * sizeof(int));
-        std::memcpy(host_in_ + 8, poss, static_cast<size_t>(B) * sizeof(int));
+        std::memcpy(host_in_ + kMaxSlots, poss, static_cast<size_t>(B) * sizeof(int));
         RL_HIP(hipMemcpyAsync(tok_, host_in_, static_cast<size_t>(B) * sizeof(int), hipMemcpyHostToDevice, st_));
         for (int b = 0; b < B; ++b)
-            RL_HIP(hipMemcpyAsync(scal_ + b * kScalars + kPos, host_in_ + 8 + b, sizeof(int), hipMemcpyHostToDevice,
+            RL_HIP(hipMemcpyAsync(scal_ + b * kScalars + kPos, host_in_ + kMaxSlots + b, sizeof(int), hipMemcpyHostToDevice,
                                   st_));
-        launch_captured(200 + B, [&] { step_batch(B); });
-        RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
+        launch_captured(200 + B, [&] { batch_groups(B); });
+        RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, kMaxSlots * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipStreamSynchronize(st_));
         batch_rows_ = B;
     }
@@ -636,10 +636,13 @@ class Engine {
     }
 
    private:
+    static constexpr int kMaxSlots = 16;   // batch slots
+    static constexpr int kGroupRows = 8;   // rows of one batch step (FP8 / BF16 linears)
+    static constexpr int kKqGroupRows = 4; // rows of one batch step (K-quant GEMV)
     // device scalar block
     enum { kPos = 0, kSlot = 1, kNCons = 2, kNextTok = 3, kGenCount = 4, kScalars = 8 };
     // host readback block (ints): scalars, then preds, then toks
-    enum { kRbPreds = 8, kRbToks = 16, kRbInts = 24 };
+    enum { kRbPreds = 8, kRbToks = 8 + kMaxSlots, kRbInts = 16 + kMaxSlots };
     static constexpr int kGenCap = 4096;
     // K-slices of the residual-add linears (o_proj, out_proj, down): their outputs
     // are partial sums that the next RMSNorm adds to the residual in slice order.
@@ -648,7 +651,12 @@ class Engine {
     RlModelConfig c_;
     int ctx_ = 0, tmax_ = 4, R_ = 5;
     int mb_ = 1;    // sequences (slots) for batch decode
-    int tcap_ = 4;  // activation rows: max(tmax_, mb_)
+    int tcap_ = 4;  // activation rows: max(tmax_, one slot group)
+    // Batch slots: up to kMaxSlots; a batch step runs them in groups of at most
+    // kGroupRows (FP8 / BF16 linears) or kKqGroupRows (K-quant GEMV) rows, one weight
+    // pass per group, and gb_ is the first slot of the group being recorded.
+    int gb_ = 0;
+    int group_rows() const { return kq_fold_ ? kKqGroupRows : kGroupRows; }
     int cs_ = 0;    // slot the single-sequence calls work on (prefill_slot)
     int batch_rows_ = 1;  // rows of the last decode_tokens
     size_t s_bstride_ = 0, conv_bstride_ = 0, rec_bstride_ = 0, kv_bstride_ = 0;
@@ -660,6 +668,15 @@ class Engine {
     int* slot_recn(int l) const { return rec_n_[l] + cs_ * recn_bstride_; }
     uint16_t* slot_kc(int l) const { return kc_[l] + cs_ * kv_bstride_; }
     uint16_t* slot_vt(int l) const { return vt_[l] + cs_ * kv_bstride_; }
+    // the first slot of the batch group being recorded (gb_)
+    int* b_scal() const { return scal_ + gb_ * kScalars; }
+    float* b_S(int l) const { return S_[l] + gb_ * s_bstride_; }
+    float* b_conv(int l) const { return conv_[l] + gb_ * conv_bstride_; }
+    float* b_rec(int l) const { return rec_[l] + gb_ * rec_bstride_; }
+    int* b_recn(int l) const { return rec_n_[l] + gb_ * recn_bstride_; }
+    uint16_t* b_kc(int l) const { return kc_[l] + gb_ * kv_bstride_; }
+    uint16_t* b_vt(int l) const { return vt_[l] + gb_ * kv_bstride_; }
+    float* b_logits() const { return logits_ + static_cast<size_t>(gb_) * c_.vocab; }
     hipStream_t st_ = nullptr;
     DevAlloc mem_;
     std::map<std::string, const RlTensor*> tab_;
@@ -750,6 +767,7 @@ class Engine {
     void* kq_ws_ = nullptr;
     size_t kq_ws_bytes_ = 0;
     size_t kq_need_ = 0;  // largest K-quant workspace over the loaded linears
+    int kq_rows() const { return std::max(tmax_, std::min(mb_, kKqGroupRows)); }
     int max_in_ = 0;
 
     std::map<int, hipGraphExec_t> graphs_;  // key: T (1..Tmax), 100 + n for MTP drafts
@@ -930,8 +948,8 @@ class Engine {
         const int T = tcap_;  // rows: verify tokens or batch sequences
         max_in_ = std::max({H, zdim, nq * hd, I, 2 * H});
         scal_ = mem_.get_n<int>(static_cast<size_t>(kScalars) * mb_);  // one block per slot
-        tok_ = mem_.get_n<int>(8);
-        preds_ = mem_.get_n<int>(8);
+        tok_ = mem_.get_n<int>(kMaxSlots);
+        preds_ = mem_.get_n<int>(kMaxSlots);
         gen_ = mem_.get_n<int>(kGenCap);
         xres_[0] = mem_.get_n<float>(static_cast<size_t>(T) * H);
         xres_[1] = mem_.get_n<float>(static_cast<size_t>(T) * H);
@@ -969,10 +987,10 @@ class Engine {
         // (step_batch) or K-quant linears (step_kq_folded, at most 4 rows), and with
         // DeltaNet layers the fused DeltaNet kernel over the slots' states
         RL_REQUIRE(mb_ == 1 || (fold_norm_ && (gdn_fused_norm_ || nd == 0)) ||
-                       (kq_fold_ && tcap_ <= 4 && (gdn_fused_ || nd == 0)),
+                       (kq_fold_ && tmax_ <= kKqGroupRows && (gdn_fused_ || nd == 0)),
                    RL_ERR_UNSUPPORTED,
                    "engine: batch decode needs folded norms: FP8/BF16 linears (v_dim 128 for DeltaNet), or "
-                   "K-quant linears with max_batch <= 4 and the fused DeltaNet kernel");
+                   "K-quant linears with max_T <= 4 and the fused DeltaNet kernel");
         s_bstride_ = s_slot_ * (gdn_fused_ ? 1 : R_);
         rec_bstride_ = static_cast<size_t>(R_) * tmax_ * nv * kGdnRecFloats;
         recn_bstride_ = R_ * nv;
@@ -1008,7 +1026,7 @@ class Engine {
         h_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         g_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
         u_ = mem_.get_n<float>(static_cast<size_t>(T) * I);
-        logits_ = mem_.get_n<float>(static_cast<size_t>(T) * c_.vocab);
+        logits_ = mem_.get_n<float>(static_cast<size_t>(std::max(T, mb_)) * c_.vocab);
         if (mb_ > 1) eq_logits_ = mem_.get_n<float>(static_cast<size_t>(mb_) * c_.vocab);
         mtp_logits_ = mem_.get_n<float>(c_.vocab);
         mtp_e_ = mem_.get_n<float>(H);
@@ -1160,7 +1178,7 @@ class Engine {
         L.kind = t->quant;
         L.m = rows;
         L.n = n;
-        kq_need_ = std::max(kq_need_, kq_workspace_bytes(rows, n, tmax_));
+        kq_need_ = std::max(kq_need_, kq_workspace_bytes(rows, n, kq_rows()));
         const size_t tb = rl_hip_kquant_tiled_bytes(t->quant, rows, n);
         L.w = static_cast<uint8_t*>(mem_.get(tb));
         const size_t bb = static_cast<size_t>(rows) * (n / 256) * (t->quant == RL_Q_Q4_K ? 144 : 210);
@@ -1236,7 +1254,7 @@ class Engine {
                 L.kind = q;
                 L.m = offs[e - 1] - base + align16(rows[e - 1]);
                 L.n = n;
-                kq_need_ = std::max(kq_need_, kq_workspace_bytes(L.m, n, tmax_));
+                kq_need_ = std::max(kq_need_, kq_workspace_bytes(L.m, n, kq_rows()));
                 L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(q, L.m, n)));
                 const size_t tile_row_bytes = rl_hip_kquant_tiled_bytes(q, 16, n);
                 for (size_t j = k; j < e; ++j) {
@@ -1349,7 +1367,7 @@ class Engine {
         L.kind = g->quant;
         L.m = 2 * I;
         L.n = H;
-        kq_need_ = std::max(kq_need_, kq_workspace_bytes(2 * I, H, tmax_));
+        kq_need_ = std::max(kq_need_, kq_workspace_bytes(2 * I, H, kq_rows()));
         L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(g->quant, 2 * I, H)));
         const size_t bb = static_cast<size_t>(I) * (H / 256) * (g->quant == RL_Q_Q4_K ? 144 : 210);
         uint8_t* tmp = nullptr;
@@ -1372,7 +1390,7 @@ class Engine {
         L.kind = type;
         L.m = rows;
         L.n = n;
-        kq_need_ = std::max(kq_need_, kq_workspace_bytes(rows, n, tmax_));
+        kq_need_ = std::max(kq_need_, kq_workspace_bytes(rows, n, kq_rows()));
         L.w = static_cast<uint8_t*>(mem_.get(rl_hip_kquant_tiled_bytes(type, rows, n)));
         const size_t nb = static_cast<size_t>(rows) * (n / 256);
         uint8_t* tmp = nullptr;
@@ -1619,17 +1637,17 @@ class Engine {
     // first linears read the normalised rows; from then on the residual GEMVs add
     // into x in place and leave the sums of squares (and x * (1 + gamma) fragments)
     // for the next linears.
-    // B > 1: the batch step (T == B rows, one token of each slot b at its own
+    // batch: the batch step (T == B rows, one token of each slot b at its own
     // position; the DeltaNet kernel and attention run over the B slots' states and
     // caches, and batch_advance replaces the acceptance)
-    void step_kq_folded(int T, int force_all, bool feed, int B = 1) {
-        const int Ts = B > 1 ? 1 : T;  // tokens per sequence
+    void step_kq_folded(int T, int force_all, bool feed, int B = 1, bool batch = false) {
+        const int Ts = batch ? 1 : T;  // tokens per sequence
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
         float* x = xres_[0];
         if (feed) copy_int(sc() + kNextTok, tok_, st_);
-        embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, T, st_);
+        embed_rows(embed_, embed_kind_, tok_ + gb_, x, H, c_.vocab, T, st_);
         rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_, H, T, eps, st_);
         KqNorm kin;
         kin.ss_in = kq_ss_;
@@ -1704,18 +1722,18 @@ class Engine {
                                        kEpiPartial, L.m, L.m, st_, kAbSlices, nullptr, iop);
                 }
                 if (gdn_fused_) {
-                    const bool bat = B > 1;
-                    const GdnRecords rec{bat ? rec_[Ly.dslot] : slot_rec(Ly.dslot),
-                                         bat ? rec_n_[Ly.dslot] : slot_recn(Ly.dslot), bat ? scal_ + kNCons : sc() + kNCons,
+                    const bool bat = batch;
+                    const GdnRecords rec{bat ? b_rec(Ly.dslot) : slot_rec(Ly.dslot),
+                                         bat ? b_recn(Ly.dslot) : slot_recn(Ly.dslot), bat ? b_scal() + kNCons : sc() + kNCons,
                                          tmax_, Ts > 1 && !force_all};
                     const GdnBatch bt{B, s_bstride_, conv_bstride_, rec_bstride_, recn_bstride_, kScalars};
                     const bool split = ab_part >= 0;
                     const int ab_rows = split ? Ly.in_parts[ab_part].m : 0;
                     gdn_decode_fused(ybuf_, split ? kq_abpart_ : ybuf_ + Ly.off_a,
                                      split ? kq_abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b, Ly.in_width,
-                                     Ly.A_log, Ly.dt_bias, Ly.conv_w, bat ? conv_[Ly.dslot] : slot_conv(Ly.dslot), nullptr,
-                                     bat ? S_[Ly.dslot] : slot_S(Ly.dslot), bat ? S_[Ly.dslot] : slot_S(Ly.dslot),
-                                     bat ? scal_ + kSlot : sc() + kSlot, conv_slot_, R_, &rec, kq_gnorm_ ? nullptr : o_,
+                                     Ly.A_log, Ly.dt_bias, Ly.conv_w, bat ? b_conv(Ly.dslot) : slot_conv(Ly.dslot), nullptr,
+                                     bat ? b_S(Ly.dslot) : slot_S(Ly.dslot), bat ? b_S(Ly.dslot) : slot_S(Ly.dslot),
+                                     bat ? b_scal() + kSlot : sc() + kSlot, conv_slot_, R_, &rec, kq_gnorm_ ? nullptr : o_,
                                      kq_gnorm_ ? ybuf_ + Ly.off_z : nullptr, kq_gnorm_ ? Ly.gnorm : nullptr, nullptr,
                                      kq_gnorm_ ? gss_ : nullptr, Ts, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_,
                                      split ? kAbSlices : 1, ab_rows, bat ? &bt : nullptr, 0, 0,
@@ -1736,9 +1754,9 @@ class Engine {
             } else {
                 for (size_t k = 0; k < Ly.qkv_parts.size(); ++k)
                     consume(Ly.qkv_parts[k], ybuf_ + Ly.qkv_offs[k], Ly.qkv_width, Ly.qkv_parts[k].m);
-                if (B > 1)
-                    attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
-                                      scal_ + kPos, 1, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                if (batch)
+                    attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, b_kc(Ly.aslot), b_vt(Ly.aslot), ctx_,
+                                      b_scal() + kPos, 1, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
                                       attn_ws_bytes_, xn_, frag_, st_, 0, B, B, kv_bstride_, kScalars);
                 else
                     attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot),
@@ -1767,10 +1785,10 @@ class Engine {
             }
             produce(Ly.down, h_, i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_);
         }
-        consume(lm_head_, logits_, c_.vocab, c_.vocab);
-        argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
-        if (B > 1) {
-            batch_advance(scal_, kScalars, B, R_, kPos, kSlot, kNCons, st_);
+        consume(lm_head_, b_logits(), c_.vocab, c_.vocab);
+        argmax_rows(b_logits(), T, c_.vocab, preds_ + gb_, nullptr, arg_ws_, st_);
+        if (batch) {
+            batch_advance(b_scal(), kScalars, B, R_, kPos, kSlot, kNCons, st_);
             return;
         }
         x_ = x;  // hidden after the layers (pre final norm), for the MTP history
@@ -1962,16 +1980,30 @@ class Engine {
     // folded-norm linears with B rows, the DeltaNet kernel over the B slots, one
     // attention launch set over the slots (slot b writes column b of o_proj's
     // input).  K-quant models run the K-quant step with B rows.
+    // One batch step over slots 0 .. B-1: groups of at most group_rows() slots, one
+    // weight pass each (gb_ = the group's first slot while it is recorded).
+    void batch_groups(int B) {
+        struct Reset {
+            int& g;
+            ~Reset() { g = 0; }
+        } reset{gb_};
+        const int G = group_rows();
+        for (int off = 0; off < B; off += G) {
+            gb_ = off;
+            step_batch(std::min(G, B - off));
+        }
+    }
+
     void step_batch(int B) {
         if (kq_fold_) {
-            step_kq_folded(B, 0, false, B);
+            step_kq_folded(B, 0, false, B, true);
             return;
         }
         const int H = c_.hidden, nk = c_.n_k_heads, nv = c_.n_v_heads, dv = c_.v_dim;
         const int nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
         float* x = xres_[0];
-        embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, B, st_);
+        embed_rows(embed_, embed_kind_, tok_ + gb_, x, H, c_.vocab, B, st_);
         rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_x_, H, B, eps, st_);
         NormIO in;
         in.ss_in = ss_;
@@ -1995,11 +2027,11 @@ class Engine {
                 }
                 gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, B, kEpiStore, nullptr,
                         abpart_ ? &in_ab : io_in);
-                const GdnRecords rec{rec_[Ly.dslot], rec_n_[Ly.dslot], scal_ + kNCons, tmax_, 0};
+                const GdnRecords rec{b_rec(Ly.dslot), b_recn(Ly.dslot), b_scal() + kNCons, tmax_, 0};
                 const float* a_in = abpart_ ? abpart_ : ybuf_ + Ly.off_a;
                 const float* b_in = abpart_ ? abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b;
-                gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, conv_[Ly.dslot],
-                                 nullptr, S_[Ly.dslot], S_[Ly.dslot], scal_ + kSlot, conv_slot_, R_, &rec, nullptr,
+                gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, b_conv(Ly.dslot),
+                                 nullptr, b_S(Ly.dslot), b_S(Ly.dslot), b_scal() + kSlot, conv_slot_, R_, &rec, nullptr,
                                  ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, 1, nk, nv, c_.k_dim, dv, c_.conv_k,
                                  c_.v_tiled, st_, abpart_ ? kAbSlices : 1, ab_rows_, &bt);
                 out.kss = gss_;
@@ -2012,8 +2044,8 @@ class Engine {
                         io_in);
                 // all slots in one launch set (slot b: its own cache, position and
                 // workspace; output column b)
-                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, kc_[Ly.aslot], vt_[Ly.aslot], ctx_,
-                                  scal_ + kPos, 1, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
+                attn_decode_layer(ybuf_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, b_kc(Ly.aslot), b_vt(Ly.aslot), ctx_,
+                                  b_scal() + kPos, 1, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, attn_ws_,
                                   attn_ws_bytes_, xn_, frag_, st_, 0, B, B, kv_bstride_, kScalars);
                 gemm_on(Ly.o_proj, frag_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
             }
@@ -2021,14 +2053,14 @@ class Engine {
             out.gamma_out = i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_;
             gemm_on(Ly.down, frag_h_, x, H, H, B, kEpiAddNorm, frag_x_, &out);
         }
-        gemm_on(lm_head_, frag_x_, logits_, c_.vocab, c_.vocab, B, kEpiStore, nullptr, &in);
-        argmax_rows(logits_, B, c_.vocab, preds_, nullptr, arg_ws_, st_);
-        batch_advance(scal_, kScalars, B, R_, kPos, kSlot, kNCons, st_);
+        gemm_on(lm_head_, frag_x_, b_logits(), c_.vocab, c_.vocab, B, kEpiStore, nullptr, &in);
+        argmax_rows(b_logits(), B, c_.vocab, preds_ + gb_, nullptr, arg_ws_, st_);
+        batch_advance(b_scal(), kScalars, B, R_, kPos, kSlot, kNCons, st_);
     }
 
     void readback() {
         RL_HIP(hipMemcpyAsync(host_rb_, sc(), kScalars * sizeof(int), hipMemcpyDeviceToHost, st_));
-        RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
+        RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, kMaxSlots * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipMemcpyAsync(host_rb_ + kRbToks, tok_, 8 * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipStreamSynchronize(st_));
         pos_ = host_rb_[kPos];

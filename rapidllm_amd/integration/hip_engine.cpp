@@ -193,7 +193,7 @@ std::unique_ptr<cuda_gen::Engine> create(WeightStore& store, int ctx) {
     // slots for decode_tokens: RAPIDLLM_MAX_BATCH, as the reference engine reads it
     // (cuda_engine.cu:20057-20062)
     const char* mb = std::getenv("RAPIDLLM_MAX_BATCH");
-    const int max_batch = mb ? std::max(1, std::min(8, std::atoi(mb))) : 1;
+    const int max_batch = mb ? std::max(1, std::min(16, std::atoi(mb))) : 1;
     return create_from_table(store.table(), ctx, max_batch);
 }
 

@@ -233,18 +233,39 @@ def test_kquant_batch_decode_vs_oracle(gpu, orc, kinds, quant, B):
     ref.close()
 
 
-@pytest.mark.parametrize("kinds,quant", [([1, 1], M.Q_Q4_K), ([0, 1], M.Q_Q6_K)])
-def test_kquant_batch_above_four_refused(gpu, kinds, quant):
-    """The K-quant GEMV takes at most 4 rows, so a K-quant model with max_batch > 4
-    is refused at creation with RL_ERR_UNSUPPORTED; max_batch 4 builds."""
-    from rapidllm_amd import hip
-
-    spec = mini_spec(n_layers=2, layer_kinds=kinds)
-    W = M.random_weights(spec, seed=9, linear_quant=quant)
-    with pytest.raises(hip.HipError) as ei:
-        Engine(spec, W, ctx=256, max_batch=5)
-    assert ei.value.code == 4  # RL_ERR_UNSUPPORTED
-    Engine(spec, W, ctx=256, max_batch=4).close()
+@pytest.mark.parametrize("kinds,quant,B", [([1, 1], M.Q_Q4_K, 6), ([0, 1], M.Q_Q6_K, 5), ([0, 0, 0, 1], None, 12)])
+def test_batch_slot_groups(gpu, kinds, quant, B):
+    """More slots than one batch step's rows (the K-quant GEMV takes 4, the FP8 GEMM
+    8): decode_tokens runs the slots in groups, one weight pass each, and every
+    slot's logits equal single-sequence decoding of its sequence bit for bit (the
+    reference allows up to min(ctx, 128) slots, cuda_engine.cu:20057-20062)."""
+    spec = mini_spec(n_layers=len(kinds), layer_kinds=kinds)
+    if quant is None:
+        W = M.random_weights(spec, seed=12, w_scale=(1e-3, 1e-2))
+    else:
+        W = M.random_weights(spec, seed=9, linear_quant=quant, head_quant=M.Q_Q6_K)
+    eng = Engine(spec, W, ctx=256, max_batch=16)
+    ref = Engine(spec, W, ctx=256)
+    assert eng.max_batch() == 16
+    rng = np.random.default_rng(B)
+    prompts = [[int(t) for t in rng.integers(0, spec.vocab, 2 + b % 5)] for b in range(B)]
+    want = [plain_chain(ref, p, 3) for p in prompts]
+    eng.zero_slots(B)
+    toks, poss = [], []
+    for b, p in enumerate(prompts):
+        eng.prefill_slot(p, b)
+        toks.append(want[b][0][0])
+        poss.append(len(p))
+    for step in range(1, 3):
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(B)
+        greedy = eng.copy_greedy_n(B)
+        for b in range(B):
+            assert np.array_equal(rows[b], want[b][1][step]), (B, step, b)
+            assert greedy[b] == want[b][0][step]
+        toks, poss = greedy, [p + 1 for p in poss]
+    eng.close()
+    ref.close()
 
 
 def test_batch_attention_across_chunk_boundaries(gpu, batch_pair):
