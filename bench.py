@@ -55,6 +55,12 @@ def measure_gguf_step(spec, K, W):
     eng.synthetic_context(CTX)
     eng.time_steps(4, W)
     t4 = eng.time_steps(4, K) / K
+    # prompt prefill through the chunked path (K-quant linears as BF16 hi + lo tiles)
+    ids = np.random.default_rng(3).integers(0, spec.vocab, PF_TOKENS).astype(np.int32)
+    eng.prefill(ids[:600])
+    tp = time.perf_counter()
+    eng.prefill(ids)
+    pf_s = time.perf_counter() - tp
     eng.close()
     H, I, V = spec.hidden, spec.intermediate, spec.vocab
     nk, nv, dk, dv = spec.n_k_heads, spec.n_v_heads, spec.k_dim, spec.v_dim
@@ -74,7 +80,10 @@ def measure_gguf_step(spec, K, W):
             "t1_ms": round(t1, 4), "tok_s": round(1000.0 / t1, 3), "t4_verify_ms": round(t4, 4),
             "t4_over_t1": round(t4 / t1, 4), "t1_bytes": int(total),
             "t1_GBps": round(total / t1 / 1e6, 1), "t1_frac": round(total / t1 / 1e6 / PEAK_GBS, 4),
-            "batch4_step_ms": round(tb4, 4), "batch4_tok_s": round(4000.0 / tb4, 3)}
+            "batch4_step_ms": round(tb4, 4), "batch4_tok_s": round(4000.0 / tb4, 3),
+            "prefill_tokens": PF_TOKENS, "prefill_ms": round(pf_s * 1e3, 1),
+            "prefill_tok_s": round(PF_TOKENS / pf_s, 1),
+            "prefill_speedup_vs_verify_chunks": round((PF_TOKENS / pf_s) / (4000.0 / t4), 2)}
 
 
 def step_bytes(spec, T, ctx):

@@ -117,6 +117,19 @@ int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream);
  * (cuda_engine.cu:18338-18590 -> launch_linear for T > 8, :12008-12016). */
 int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                             int T, int epilogue, int ldy, void* stream);
+/* The same over BF16 tiles (rl_hip_pack_bf16 layout): W, or W_hi + W_lo when
+ * w_lo_tiled is given (a weight split into 16 significant bits, as
+ * rl_hip_kquant_to_bf16x2 writes a K-quant matrix).  The K-quant models' prefill
+ * linears (the reference runs them through its multi-token K-quant GEMVs,
+ * cuda_engine.cu:12076-12260). */
+int rl_hip_gemm_bf16_prefill(const uint16_t* w_tiled, const uint16_t* w_lo_tiled, const void* frag, float* Y, int m,
+                             int n, int T, int epilogue, int ldy, void* stream);
+/* A tiled Q4_K / Q6_K matrix (rl_hip_pack_kquant, or the gate / up half tiles) as
+ * two BF16 tiled matrices W_hi + W_lo of the same row order: each weight dequantised
+ * exactly as ops::dequant_q4_k / dequant_q6_k (ops.cpp:245-402), then split into
+ * its top 16 bits (hi) and the top 16 bits of the remainder (lo). */
+int rl_hip_kquant_to_bf16x2(int type, const uint8_t* tiled, uint16_t* w_hi, uint16_t* w_lo, int m, int n,
+                            void* stream);
 
 int rl_hip_gemm_fp8_frag(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                          int T, int accumulate, void* stream);

@@ -226,6 +226,8 @@ class Engine {
     void *pf_frag_ = nullptr, *pf_frag_h_ = nullptr, *pf_attn_ws_ = nullptr;
     size_t pf_attn_ws_bytes_ = 0;
     int* pf_pos_ = nullptr;
+    uint16_t *pf_whi_ = nullptr, *pf_wlo_ = nullptr;  // a K-quant linear as BF16 hi + lo tiles
+    float* pf_u_ = nullptr;                          // up rows of separate K-quant gate / up
     std::unique_ptr<DevAlloc> pf_mem_;
 
     // RL_PREFILL_CHUNK: 0 = every prompt token through decode steps (T <= max_T);
@@ -240,20 +242,55 @@ class Engine {
         return pf_chunk_;
     }
 
+    // Every layer linear FP8, BF16 or Q4_K / Q6_K (K-quant ones are dequantised to
+    // BF16 hi + lo tiles per chunk), and the DeltaNet layers on the fused kernel's
+    // state (one committed S, the conv ring), which the prefill recurrence writes.
     bool can_prefill_chunked() const {
         if (pf_chunk_setting() == 0) return false;
-        auto fp8 = [](const Lin& L) { return L.kind == RL_Q_FP8_E4M3_B128; };
-        if (!fp8(lm_head_) && lm_head_.kind != RL_Q_BF16) return false;
         for (const Layer& Ly : L_) {
-            if (Ly.kind == RL_LAYER_DELTA) {
-                if (!gdn_fused_norm_ || Ly.in_parts.size() != 1 || !fp8(Ly.in_parts[0]) || !fp8(Ly.out_proj))
-                    return false;
-            } else if (Ly.qkv_parts.size() != 1 || !fp8(Ly.qkv_parts[0]) || !fp8(Ly.o_proj)) {
+            for (const Lin& L : Ly.kind == RL_LAYER_DELTA ? Ly.in_parts : Ly.qkv_parts)
+                if (!known_kind(L)) return false;
+            if (Ly.kind == RL_LAYER_DELTA && (!gdn_fused_ || !known_kind(Ly.out_proj))) return false;
+            if (Ly.kind != RL_LAYER_DELTA && !known_kind(Ly.o_proj)) return false;
+            if (Ly.gate_up.kind >= 0 ? !frag_kind(Ly.gate_up)
+                                     : (!known_kind(Ly.gate) || (!Ly.gate_cat && !known_kind(Ly.up))))
                 return false;
-            }
-            if (Ly.gate_up.kind != RL_Q_FP8_E4M3_B128 || !fp8(Ly.down)) return false;
+            if (!known_kind(Ly.down)) return false;
         }
         return c_.hidden % 8 == 0;
+    }
+
+    // elements of the largest K-quant layer linear (its BF16 hi / lo scratch)
+    size_t kq_prefill_elems() const {
+        size_t e = 0;
+        auto see = [&](const Lin& L) {
+            if (is_kq(L)) e = std::max(e, static_cast<size_t>((L.m + 15) / 16) * 16 * L.n);
+        };
+        for (const Layer& Ly : L_) {
+            for (const Lin& L : Ly.kind == RL_LAYER_DELTA ? Ly.in_parts : Ly.qkv_parts) see(L);
+            see(Ly.out_proj);
+            see(Ly.o_proj);
+            see(Ly.gate);
+            see(Ly.up);
+            see(Ly.down);
+        }
+        return e;
+    }
+
+    // One prefill linear over T tokens of fragments: Y (=, +=, SwiGLU) W . x.
+    void pf_linear(const Lin& L, const void* frag, float* Y, int ldy, int m_valid, int T, int epi) {
+        if (L.kind == RL_Q_FP8_E4M3_B128) {
+            gemm_prefill_any(0, L.w, nullptr, L.ts, frag, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
+        } else if (L.kind == RL_Q_BF16) {
+            gemm_prefill_any(1, L.w, nullptr, nullptr, frag, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
+        } else {
+            kq_to_bf16x2(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, pf_whi_, pf_wlo_, L.m, L.n, st_);
+            gemm_prefill_any(2, reinterpret_cast<const uint8_t*>(pf_whi_), reinterpret_cast<const uint8_t*>(pf_wlo_),
+                             nullptr, frag, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
+        }
+    }
+    void pf_parts(const std::vector<Lin>& parts, const std::vector<int>& offs, float* Y, int ldy, int T) {
+        for (size_t k = 0; k < parts.size(); ++k) pf_linear(parts[k], pf_frag_, Y + offs[k], ldy, parts[k].m, T, kEpiStore);
     }
 
     void ensure_pf_buffers(int C) {
@@ -278,6 +315,12 @@ class Engine {
         pf_attn_ws_bytes_ = attn_prefill_workspace_bytes(std::max(c_.n_q, 1), C);
         pf_attn_ws_ = pf_mem_->get(pf_attn_ws_bytes_);
         pf_pos_ = pf_mem_->get_n<int>(64);
+        const size_t kqe = kq_prefill_elems();
+        if (kqe) {
+            pf_whi_ = pf_mem_->get_n<uint16_t>(kqe);
+            pf_wlo_ = pf_mem_->get_n<uint16_t>(kqe);
+            pf_u_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * I);
+        }
         pf_cap_ = C;
     }
 
@@ -301,31 +344,34 @@ class Engine {
                 Layer& Ly = L_[i];
                 rmsnorm_pack(pf_x_, H, Ly.attn_norm, nullptr, pf_frag_, H, T, eps, st_);
                 if (Ly.kind == RL_LAYER_DELTA) {
-                    const Lin& in = Ly.in_parts[0];
-                    gemm_fp8_prefill(in.w, in.ts, pf_frag_, pf_y_, in.m, H, T, kEpiStore, Ly.in_width, in.m, st_);
+                    pf_parts(Ly.in_parts, Ly.in_offs, pf_y_, Ly.in_width, T);
                     float* ring = slot_conv(Ly.dslot);
                     gdn_prefill(pf_y_, Ly.in_width, Ly.off_a, Ly.off_b, Ly.A_log, Ly.dt_bias, Ly.conv_w,
                                 ring + slot * conv_slot_, ring + (slot ^ 1) * conv_slot_, pf_xc_, pf_gates_,
                                 slot_S(Ly.dslot), pf_o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                     gnorm_pack(pf_o_, pf_y_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, nullptr, pf_frag_, zdim, T,
                                1e-6f, st_);
-                    gemm_fp8_prefill(Ly.out_proj.w, Ly.out_proj.ts, pf_frag_, pf_x_, Ly.out_proj.m, zdim, T, kEpiAdd,
-                                     H, H, st_);
+                    pf_linear(Ly.out_proj, pf_frag_, pf_x_, H, H, T, kEpiAdd);
                 } else {
-                    const Lin& q = Ly.qkv_parts[0];
-                    gemm_fp8_prefill(q.w, q.ts, pf_frag_, pf_y_, q.m, H, T, kEpiStore, Ly.qkv_width, q.m, st_);
+                    pf_parts(Ly.qkv_parts, Ly.qkv_offs, pf_y_, Ly.qkv_width, T);
                     attn_prefill_layer(pf_y_, Ly.qkv_width, Ly.q_norm, Ly.k_norm, slot_kc(Ly.aslot), slot_vt(Ly.aslot),
                                        ctx_, pf_pos_, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, pf_attn_ws_,
                                        pf_attn_ws_bytes_, pf_o_, st_);
                     pack_act(pf_o_, pf_frag_, nq * hd, T, st_);
-                    gemm_fp8_prefill(Ly.o_proj.w, Ly.o_proj.ts, pf_frag_, pf_x_, Ly.o_proj.m, nq * hd, T, kEpiAdd, H,
-                                     H, st_);
+                    pf_linear(Ly.o_proj, pf_frag_, pf_x_, H, H, T, kEpiAdd);
                 }
                 rmsnorm_pack(pf_x_, H, Ly.ffn_norm, nullptr, pf_frag_, H, T, eps, st_);
-                gemm_fp8_prefill(Ly.gate_up.w, Ly.gate_up.ts, pf_frag_, pf_h_, Ly.gate_up.m, H, T, Ly.gate_up.swiglu_epi(), I, I,
-                                 st_);
+                if (Ly.gate_up.kind >= 0) {
+                    pf_linear(Ly.gate_up, pf_frag_, pf_h_, I, I, T, Ly.gate_up.swiglu_epi());
+                } else if (Ly.gate_cat) {
+                    pf_linear(Ly.gate, pf_frag_, pf_h_, I, I, T, kEpiSwiGLUH);
+                } else {
+                    pf_linear(Ly.gate, pf_frag_, pf_h_, I, I, T, kEpiStore);
+                    pf_linear(Ly.up, pf_frag_, pf_u_, I, I, T, kEpiStore);
+                    swiglu(pf_h_, I, pf_u_, I, pf_h_, I, T, st_);
+                }
                 pack_act(pf_h_, pf_frag_h_, I, T, st_);
-                gemm_fp8_prefill(Ly.down.w, Ly.down.ts, pf_frag_h_, pf_x_, Ly.down.m, I, T, kEpiAdd, H, H, st_);
+                pf_linear(Ly.down, pf_frag_h_, pf_x_, H, H, T, kEpiAdd);
             }
             slot ^= 1;
             RL_HIP(hipStreamSynchronize(st_));  // the pinned position stage is reused by the next chunk

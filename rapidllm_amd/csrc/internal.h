@@ -56,6 +56,11 @@ int gemm_store_waves();
 
 // prefill.hip: Y = W . X for T (any) tokens on MFMA; epi store / add / SwiGLU
 // (interleaved gate/up tiles, m_valid = m/2 output rows).  frag: act fragments of T.
+// wk 0: FP8 tiles (ts); 1: BF16 tiles; 2: BF16 W + W_lo tiles (16 significant bits)
+void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float* ts, const void* frag, float* Y,
+                      int m, int n, int T, int epi, int ldy, int m_valid, hipStream_t s);
+// K-quant tiles (qt 4 / 6, m rows in 16-row tiles) -> BF16 tiles hi and lo
+void kq_to_bf16x2(int qt, const uint8_t* tiled, uint16_t* hi, uint16_t* lo, int m, int n, hipStream_t s);
 void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
                       int ldy, int m_valid, hipStream_t s);
 int device_cus();  // CUs of the current device

@@ -712,6 +712,68 @@ __global__ void q6k_dequant_kernel(const uint8_t* __restrict__ src, float* __res
     }
 }
 
+// Tiled K-quant -> BF16 tiles hi + lo (the gemm.hip BF16 tile: 16 rows x 128
+// columns, unit (chunk q, lane (row, g)) = columns 32 g + 8 q .. + 8).  One thread
+// per (row tile, super-block, row, 8 columns): the eight weights dequantised with
+// the reference's operation order (q4k_dequant_kernel / q6k_dequant_kernel), each
+// split into its top 16 bits and the top 16 bits of the remainder.
+template <int QT>
+__global__ void kq_to_bf16x2_kernel(const uint8_t* __restrict__ tiled, uint16_t* __restrict__ hi,
+                                    uint16_t* __restrict__ lo, int m_tiles, int nsb) {
+#pragma clang fp contract(off)
+    using F = KFmt<QT>;
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rt, sb, u, r16)
+    if (idx >= static_cast<size_t>(m_tiles) * nsb * 32 * 16) return;
+    const int r16 = idx & 15;
+    const int u = (idx >> 4) & 31;  // 8-column group of the super-block
+    const int sb = static_cast<int>((idx >> 9) % nsb);
+    const int rt = static_cast<int>((idx >> 9) / nsb);
+    const uint8_t* tile = tiled + (static_cast<size_t>(rt) * nsb + sb) * F::kTileBytes;
+    const uint8_t* hdr = tile + F::kHdr + 16 * r16;
+    const int c0 = 8 * u;  // first column within the super-block
+    float w[8];
+    if constexpr (QT == 4) {
+        const int g64 = c0 / 64, high = (c0 % 64) >= 32, l0 = c0 % 32;
+        const uint8_t* qs = tile + (l0 / 16) * 1024 + 16 * (r16 + 16 * g64) + (l0 % 16);
+        const float d = half_bits_to_f32(hdr[0] | (hdr[1] << 8));
+        const float dmin = half_bits_to_f32(hdr[2] | (hdr[3] << 8));
+        int sc, mn;
+        q4k_scale_min(hdr + 4, 2 * g64 + high, sc, mn);
+        const float a = __fmul_rn(d, static_cast<float>(sc)), b = __fmul_rn(dmin, static_cast<float>(mn));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int q = high ? (qs[e] >> 4) : (qs[e] & 15);
+            w[e] = __fsub_rn(__fmul_rn(a, static_cast<float>(q)), b);
+        }
+    } else {
+        const int half = c0 / 128, rem = c0 % 128, sel = rem / 32, l0 = rem % 32;
+        const int g = 2 * half + l0 / 16, off = l0 % 16;
+        const uint8_t* ql = tile + (sel & 1) * 1024 + 16 * (r16 + 16 * g) + off;  // ql[l] or ql[l + 32]
+        const uint8_t* qh = tile + 2 * 1024 + 16 * (r16 + 16 * g) + off;
+        const float d = half_bits_to_f32(tile[F::kHdr + 256 + 2 * r16] | (tile[F::kHdr + 256 + 2 * r16 + 1] << 8));
+        const int8_t scv = static_cast<int8_t>(hdr[8 * half + l0 / 16 + 2 * sel]);
+        const float a = __fmul_rn(d, static_cast<float>(scv));
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const int lq = sel < 2 ? (ql[e] & 15) : (ql[e] >> 4);
+            const int v = (lq | (((qh[e] >> (2 * sel)) & 3) << 4)) - 32;
+            w[e] = __fmul_rn(a, static_cast<float>(v));
+        }
+    }
+    // BF16 tile (rt, kb) and its unit for columns j .. j + 7 of the 128-column block
+    const int kb = 2 * sb + c0 / 128, j = c0 % 128;
+    const int g = j / 32, q = (j % 32) / 8;
+    const size_t unit = (static_cast<size_t>(rt) * (2 * nsb) + kb) * 2048 + q * 512 + 8 * (r16 + 16 * g);
+    union {
+        uint16_t h[8];
+        i32x4 v;
+    } H, L;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) split_bf16(w[e], H.h[e], L.h[e]);
+    *reinterpret_cast<i32x4*>(hi + unit) = H.v;
+    *reinterpret_cast<i32x4*>(lo + unit) = L.v;
+}
+
 size_t kq_tiled_bytes(int qt, int m, int n) {
     const size_t tile = qt == 4 ? KFmt<4>::kTileBytes : KFmt<6>::kTileBytes;
     return static_cast<size_t>((m + kTR - 1) / kTR) * (n / 256) * tile;
@@ -788,6 +850,20 @@ void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, unsig
 }  // namespace
 
 namespace rl {
+
+void kq_to_bf16x2(int qt, const uint8_t* tiled, uint16_t* hi, uint16_t* lo, int m, int n, hipStream_t s) {
+    RL_REQUIRE((qt == 4 || qt == 6) && m > 0 && n > 0 && n % 256 == 0 && tiled && hi && lo, RL_ERR_RANGE,
+               "kquant_to_bf16x2: Q4_K / Q6_K, n a multiple of 256");
+    const int m_tiles = (m + kTR - 1) / kTR, nsb = n / 256;
+    const size_t threads = static_cast<size_t>(m_tiles) * nsb * 512;
+    const dim3 grid(static_cast<unsigned>((threads + 255) / 256));
+    if (qt == 4)
+        hipLaunchKernelGGL(kq_to_bf16x2_kernel<4>, grid, dim3(256), 0, s, tiled, hi, lo, m_tiles, nsb);
+    else
+        hipLaunchKernelGGL(kq_to_bf16x2_kernel<6>, grid, dim3(256), 0, s, tiled, hi, lo, m_tiles, nsb);
+    check_launch("kq_to_bf16x2_kernel");
+}
+
 
 size_t kq_workspace_bytes(int m, int n, int T) {
     // split-K tickets, then the partials of the split: S*T*m floats
@@ -976,6 +1052,14 @@ int rl_hip_gemm_kquant(int type, const uint8_t* tiled, const float* X, float* Y,
         RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "gemm_kquant: Q4_K or Q6_K only");
         rl::kq_gemm(type == RL_Q_Q4_K ? 4 : 6, tiled, X, Y, workspace, workspace_bytes, m, n, T, accumulate, m,
                     S(stream));
+    });
+}
+
+int rl_hip_kquant_to_bf16x2(int type, const uint8_t* tiled, uint16_t* w_hi, uint16_t* w_lo, int m, int n,
+                            void* stream) {
+    return guard([&] {
+        RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "kquant_to_bf16x2: Q4_K or Q6_K");
+        rl::kq_to_bf16x2(type == RL_Q_Q4_K ? 4 : 6, tiled, w_hi, w_lo, m, n, S(stream));
     });
 }
 

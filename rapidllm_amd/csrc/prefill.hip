@@ -25,7 +25,6 @@ using namespace rl;
 
 namespace {
 
-constexpr int kPfRT = 8;     // row tiles per workgroup
 constexpr int kPfNT = 2;     // 16-token column tiles per wave
 constexpr int kPfTok = 64 * kPfNT;  // tokens per workgroup
 constexpr int kTileRows = 16;
@@ -51,11 +50,23 @@ __device__ inline float silu_f(float x) { return x / (1.f + __expf(-x)); }
 // (even tile = gate rows, odd = up rows of the same 16 outputs; Y row = output row),
 // 5 SwiGLU over half tiles (tile k: gate rows 8k..8k+7, up rows 8k..8k+7; scales
 // [tile][kb][2]).
-template <int EPI>
+// WK: the weight tiles.  0: block-FP8 (2 KiB tiles, tile scales).  1: BF16 (4 KiB
+// tiles of the decode GEMM's BF16 layout, no scales).  2: two BF16 matrices W_hi +
+// W_lo (a weight split into 16 significant bits, as the K-quant linears are
+// dequantised for prefill): three MFMAs per step, hi.x_hi + hi.x_mid + lo.x_hi.
+// RT row tiles per workgroup: 8 for FP8, 4 for BF16 (the same 16 KiB, or 32 KiB
+// for hi + lo, of weights staged per column block).
+template <int EPI, int WK = 0>
 __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __restrict__ W,
                                                            const float* __restrict__ tscale,
                                                            const i32x4* __restrict__ frag, float* __restrict__ Y,
-                                                           int m, int n_kb, int T, int ldy, int m_valid) {
+                                                           int m, int n_kb, int T, int ldy, int m_valid,
+                                                           const uint8_t* __restrict__ W_lo = nullptr) {
+    constexpr int kPfRT = WK == 0 ? 8 : 4;          // row tiles per workgroup
+    constexpr int kCh = WK == 0 ? 2 : 4;            // 16-B chunks per lane per tile
+    constexpr int kTileB = WK == 0 ? 2048 : 4096;   // bytes per tile
+    constexpr int kMat = WK == 2 ? 2 : 1;           // weight matrices staged
+    constexpr int kUnits = kPfRT * kCh * 64 * kMat / 256;  // 16-B staging units per thread
     const int tid = threadIdx.x;
     const int lane = tid & 63;
     const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -70,25 +81,26 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
     }
     const int NC = 2 * T;
 
-    __shared__ i32x4 wl[2][kPfRT][2][64];  // [buffer][row tile][16-B chunk][lane]
+    __shared__ i32x4 wl[2][kMat][kPfRT][kCh][64];  // [buffer][matrix][row tile][16-B chunk][lane]
 
-    // staging: unit u = (row tile, chunk, lane), 4 per thread
-    i32x4 stg[4];
+    // staging: unit u = (matrix, row tile, chunk, lane), kUnits per thread
+    i32x4 stg[kUnits];
     auto stage_load = [&](int kb) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kUnits; ++q) {
             const int u = tid + 256 * q;
-            const int r = u >> 7, c = (u >> 6) & 1, l = u & 63;
+            const int l = u & 63, c = (u >> 6) % kCh, r = (u / (64 * kCh)) % kPfRT, mat = u / (64 * kCh * kPfRT);
             const int rt = min(rt0 + r, m_tiles - 1);
+            const uint8_t* base = mat ? W_lo : W;
             stg[q] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
-                W + (static_cast<size_t>(rt) * n_kb + kb) * 2048 + c * 1024 + 16 * l));
+                base + (static_cast<size_t>(rt) * n_kb + kb) * kTileB + c * 1024 + 16 * l));
         }
     };
     auto stage_store = [&](int buf) {
 #pragma unroll
-        for (int q = 0; q < 4; ++q) {
+        for (int q = 0; q < kUnits; ++q) {
             const int u = tid + 256 * q;
-            wl[buf][u >> 7][(u >> 6) & 1][u & 63] = stg[q];
+            wl[buf][u / (64 * kCh * kPfRT)][(u / (64 * kCh)) % kPfRT][(u >> 6) % kCh][u & 63] = stg[q];
         }
     };
 
@@ -117,18 +129,19 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
 #pragma unroll
         for (int r = 0; r < kPfRT; ++r) {
             const int rt = min(rt0 + r, m_tiles - 1);
-            // C rows 4g..4g+3 of a half-tile matrix: gate (g < 2) or up scale
-            const float sc = EPI == 5 ? tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + (g >> 1)]
-                                      : tscale[static_cast<size_t>(rt) * n_kb + kb];
             f32x4 acc[kPfNT];
 #pragma unroll
             for (int nt = 0; nt < kPfNT; ++nt) acc[nt] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const i32x4 wv = wl[buf][r][i >> 1][lane];
                 Frag8 a, b;
-                e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[2] : wv[0]), a.u[0], a.u[1]);
-                e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[3] : wv[1]), a.u[2], a.u[3]);
+                if constexpr (WK == 0) {
+                    const i32x4 wv = wl[buf][0][r][i >> 1][lane];
+                    e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[2] : wv[0]), a.u[0], a.u[1]);
+                    e4m3x4_to_bf16(static_cast<uint32_t>((i & 1) ? wv[3] : wv[1]), a.u[2], a.u[3]);
+                } else {
+                    a.i = wl[buf][0][r][i][lane];
+                }
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) {
                     b.i = bh[nt][i];
@@ -136,9 +149,25 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
                     b.i = bm[nt][i];
                     acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
                 }
-            }
+                if constexpr (WK == 2) {
+                    a.i = wl[buf][1][r][i][lane];
 #pragma unroll
-            for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += sc * acc[nt];
+                    for (int nt = 0; nt < kPfNT; ++nt) {
+                        b.i = bh[nt][i];
+                        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
+                    }
+                }
+            }
+            if constexpr (WK == 0) {
+                // C rows 4g..4g+3 of a half-tile matrix: gate (g < 2) or up scale
+                const float sc = EPI == 5 ? tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + (g >> 1)]
+                                          : tscale[static_cast<size_t>(rt) * n_kb + kb];
+#pragma unroll
+                for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += sc * acc[nt];
+            } else {
+#pragma unroll
+                for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += acc[nt];
+            }
         }
         if (kb + 1 < n_kb) stage_store(buf ^ 1);
         __syncthreads();
@@ -193,31 +222,37 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
 
 namespace rl {
 
-void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
-                      int ldy, int m_valid, hipStream_t s) {
+void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float* ts, const void* frag, float* Y,
+                      int m, int n, int T, int epi, int ldy, int m_valid, hipStream_t s) {
     RL_REQUIRE(m > 0 && n > 0 && T >= 1, RL_ERR_RANGE, "gemm_prefill: empty shape");
-    RL_REQUIRE(W && ts && frag && Y, RL_ERR_RANGE, "gemm_prefill: null pointer");
+    RL_REQUIRE(W && frag && Y && (wk != 0 || ts) && (wk != 2 || W_lo), RL_ERR_RANGE, "gemm_prefill: null pointer");
+    RL_REQUIRE(wk >= 0 && wk <= 2, RL_ERR_RANGE, "gemm_prefill: weight kind");
     RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU || epi == kEpiSwiGLUH, RL_ERR_RANGE,
                "gemm_prefill: epilogue must be store, add or swiglu");
     if (epi == kEpiSwiGLUH) RL_REQUIRE(m % 16 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows a multiple of 16");
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     if (epi == kEpiSwiGLU) RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows must be a multiple of 32");
     const int n_kb = (n + 127) / 128;
-    const dim3 grid((m_tiles + kPfRT - 1) / kPfRT, (T + kPfTok - 1) / kPfTok);
+    const int rt = wk == 0 ? 8 : 4;
+    const dim3 grid((m_tiles + rt - 1) / rt, (T + kPfTok - 1) / kPfTok);
     RL_REQUIRE(grid.y <= 65535, RL_ERR_RANGE, "gemm_prefill: too many tokens");
-    if (epi == kEpiStore)
-        hipLaunchKernelGGL(gemm_prefill_kernel<0>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
-                           n_kb, T, ldy, m_valid);
-    else if (epi == kEpiAdd)
-        hipLaunchKernelGGL(gemm_prefill_kernel<1>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
-                           n_kb, T, ldy, m_valid);
-    else if (epi == kEpiSwiGLU)
-        hipLaunchKernelGGL(gemm_prefill_kernel<2>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
-                           n_kb, T, ldy, m_valid);
-    else
-        hipLaunchKernelGGL(gemm_prefill_kernel<5>, grid, dim3(256), 0, s, W, ts, static_cast<const i32x4*>(frag), Y, m,
-                           n_kb, T, ldy, m_valid);
-    check_launch("gemm_prefill_kernel");
+    const i32x4* fr = static_cast<const i32x4*>(frag);
+#define RL_PF(E, K)                                                                                                 \
+    if (epi == E && wk == K) {                                                                                      \
+        hipLaunchKernelGGL((gemm_prefill_kernel<E == kEpiSwiGLUH ? 5 : E, K>), grid, dim3(256), 0, s, W, ts, fr, Y, m, \
+                           n_kb, T, ldy, m_valid, W_lo);                                                            \
+        check_launch("gemm_prefill_kernel");                                                                        \
+        return;                                                                                                     \
+    }
+    RL_PF(kEpiStore, 0) RL_PF(kEpiAdd, 0) RL_PF(kEpiSwiGLU, 0) RL_PF(kEpiSwiGLUH, 0)
+    RL_PF(kEpiStore, 1) RL_PF(kEpiAdd, 1) RL_PF(kEpiSwiGLU, 1) RL_PF(kEpiSwiGLUH, 1)
+    RL_PF(kEpiStore, 2) RL_PF(kEpiAdd, 2) RL_PF(kEpiSwiGLU, 2) RL_PF(kEpiSwiGLUH, 2)
+#undef RL_PF
+}
+
+void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
+                      int ldy, int m_valid, hipStream_t s) {
+    gemm_prefill_any(0, W, nullptr, ts, frag, Y, m, n, T, epi, ldy, m_valid, s);
 }
 
 }  // namespace rl
@@ -229,6 +264,16 @@ int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, con
     return guard([&] {
         const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
         rl::gemm_fp8_prefill(w_tiled, tile_scale, frag, Y, m, n, T, epilogue, ldy > 0 ? ldy : mv, mv, S(stream));
+    });
+}
+
+int rl_hip_gemm_bf16_prefill(const uint16_t* w_tiled, const uint16_t* w_lo_tiled, const void* frag, float* Y, int m,
+                             int n, int T, int epilogue, int ldy, void* stream) {
+    return guard([&] {
+        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
+        rl::gemm_prefill_any(w_lo_tiled ? 2 : 1, reinterpret_cast<const uint8_t*>(w_tiled),
+                             reinterpret_cast<const uint8_t*>(w_lo_tiled), nullptr, frag, Y, m, n, T, epilogue,
+                             ldy > 0 ? ldy : mv, mv, S(stream));
     });
 }
 

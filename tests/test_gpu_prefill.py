@@ -197,3 +197,76 @@ def test_gdn_prefill_vs_oracle(gpu, orc, T, nk, nv, v_tiled):
         assert rel_l2(o[t], o_ref[t]) < 1e-3, (t, rel_l2(o[t], o_ref[t]))
     assert rel_l2(S, S_ref) < 1e-4
     assert np.array_equal(conv, conv_ref)
+
+
+@pytest.mark.parametrize("qt,m,n,T", [(ops.Q4_K, 256, 1024, 70), (ops.Q6_K, 160, 768, 130),
+                                      (ops.Q4_K, 5120, 4096, 300)])
+def test_kquant_prefill_gemm_vs_oracle(gpu, orc, qt, m, n, T):
+    """The K-quant prefill linear: rl_hip_kquant_to_bf16x2 turns the tiled blocks
+    into BF16 hi + lo tiles (hi + lo equal the reference's dequantised weight to 16
+    significant bits; checked against ops::dequant_q4_k / dequant_q6_k), and the
+    BF16 x2 prefill GEMM over them matches the oracle's K-quant GEMV per token."""
+    from rapidllm_amd.hip import DeviceBuffer, call
+    r = synth.rng(700 + m + T)
+    blocks = synth.q4k_blocks(r, m, n) if qt == ops.Q4_K else synth.q6k_blocks(r, m, n)
+    lin = ops.KQuantLinear(qt, blocks, m, n)
+    mt = (m + 15) // 16
+    hi, lo = DeviceBuffer(mt * 16 * n * 2), DeviceBuffer(mt * 16 * n * 2)
+    call("rl_hip_kquant_to_bf16x2", qt, lin.w.ptr, hi.ptr, lo.ptr, m, n, None)
+    # the split against the exact dequantisation, element by element (first row tile)
+    deq = orc.dequant_q4_k if qt == ops.Q4_K else orc.dequant_q6_k
+    Wd = deq(np.ascontiguousarray(blocks.reshape(-1)), m * n).reshape(m, n)
+    h = hi.numpy(np.uint16, (mt * 16 * n,))
+    l = lo.numpy(np.uint16, (mt * 16 * n,))
+    nkb = n // 128
+    for row in (0, 5, 15):
+        for c in (0, 37, 128, n - 1):
+            kb, j = c // 128, c % 128
+            g, q, e = j // 32, (j % 32) // 8, j % 8
+            i = (0 * nkb + kb) * 2048 + q * 512 + 8 * (row + 16 * g) + e
+            w = synth.bf16_to_f32(h[i:i + 1])[0] + synth.bf16_to_f32(l[i:i + 1])[0]
+            assert abs(w - Wd[row, c]) <= abs(Wd[row, c]) * 2.0 ** -15, (row, c, w, Wd[row, c])
+    X = r.standard_normal((T, n)).astype(np.float32)
+    xd = DeviceBuffer.from_numpy(X)
+    frag = ops.act_frag_buffer(n, T)
+    yd = DeviceBuffer(4 * T * m)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
+    call("rl_hip_gemm_bf16_prefill", hi.ptr, lo.ptr, frag.ptr, yd.ptr, m, n, T, 0, m, None)
+    got = yd.numpy(np.float32, (T, m))
+    gemv = orc.gemv_q4_k if qt == ops.Q4_K else orc.gemv_q6_k
+    for t in range(0, T, max(1, T // 7)):
+        want = gemv(np.ascontiguousarray(blocks.reshape(-1)), X[t], m, n, 8)
+        assert rel_l2(got[t], want) <= REL_L2, (t, rel_l2(got[t], want))
+
+
+@pytest.mark.parametrize("quant", ["q4_k", "q6_k"])
+def test_engine_kquant_chunked_prefill_matches_oracle(gpu, orc, monkeypatch, quant):
+    """A GGUF-style model (K-quant layer linears, BF16 a / b rows, Q6_K lm_head)
+    prefills a 300-token prompt through the chunked path (two chunks of 256 + the
+    decode-step tail): logits and decoding continue as the oracle's."""
+    from oracle.oracle import OracleModel
+    from rapidllm_amd import model as M
+    from rapidllm_amd.engine import Engine
+    from tests.test_gpu_engine import margin_ok, mini_spec
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=13, linear_quant=M.Q_Q4_K if quant == "q4_k" else M.Q_Q6_K,
+                         head_quant=M.Q_Q6_K)
+    monkeypatch.setenv("RL_PREFILL_CHUNK", "256")
+    eng = Engine(spec, W, ctx=1024)
+    orc_m = OracleModel(spec, W, ctx=1024)
+    rng = np.random.default_rng(15)
+    prompt = [int(t) for t in rng.integers(0, spec.vocab, 300)]
+    eng.prefill(prompt)
+    orc_m.reset()
+    for t in prompt:
+        g, lg, hd = orc_m.decode(t)
+    assert rel_l2(eng.copy_logits(), lg) < 1e-3
+    if margin_ok(lg):
+        assert eng.greedy() == g
+    tok = g
+    for _ in range(3):
+        eng.decode_token(tok)
+        g, lg, _ = orc_m.decode(tok)
+        assert rel_l2(eng.copy_logits(), lg) < 1e-3
+        tok = g
+    eng.close()
