@@ -762,6 +762,12 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
         if (epilogue == kStore || epilogue == kAdd) c = GemmCfg{1, 16, 1};
         if (epilogue == kSwiGLU) c = GemmCfg{2, 16, 1};
     }
+    // BF16 stores at T <= 4 (the lm_head: 248320 x 5120, 2.54 GB) take the same split:
+    // 370 / 360 us at T = 1 / 4 against 392 / 398 us for two row tiles per 8 waves at
+    // depth 2 (weights in HBM; every T <= 4 uses this split, so rows of a verify equal
+    // the T = 1 rows bit for bit)
+    if (!kFp8 && bperm_enabled() && T <= 4 && S == 1 && (epilogue == kStore || epilogue == kAdd))
+        c = GemmCfg{1, 16, 1};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
     // residual GEMMs (m = hidden: 160 groups): 8 waves measured faster than 16 there
