@@ -86,6 +86,25 @@ def measure_gguf_step(spec, K, W):
             "prefill_speedup_vs_verify_chunks": round((PF_TOKENS / pf_s) / (4000.0 / t4), 2)}
 
 
+def measure_wide_batch(spec, K, W):
+    """Continuous batches of 8 and 16 sequences at 32K context each (block-FP8): one
+    step advances every slot by one token; the engine runs the slots in groups of 8
+    rows, one weight pass per group."""
+    from rapidllm_amd.engine import Engine
+
+    eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=16)
+    out = {}
+    for B in (8, 16):
+        eng.synthetic_context(CTX)
+        eng.replicate_slot0(B)
+        eng.time_batch(B, W)
+        tb = eng.time_batch(B, K) / K
+        out[f"batch{B}_step_ms"] = round(tb, 4)
+        out[f"batch{B}_tok_s"] = round(1000.0 * B / tb, 3)
+    eng.close()
+    return out
+
+
 def step_bytes(spec, T, ctx):
     """Algorithmic HBM bytes of one T-token step: every weight byte once, KV read
     once (+ the T new rows written), recurrent state read once and written once per
@@ -746,6 +765,7 @@ def main():
     t1 = eng.time_steps(1, K) / K
     eng.close()
     gguf = measure_gguf_step(spec, K, W)
+    wide = measure_wide_batch(spec, K, W)
 
     b1 = step_bytes(spec, 1, CTX)
     b4 = step_bytes(spec, 4, CTX)
@@ -781,6 +801,7 @@ def main():
         "gguf_q4_k": gguf,
         "batch4_step_ms": round(tb4, 4),
         "batch4_tok_s": round(4000.0 / tb4, 3),
+        **wide,
         "prefill_tokens": PF_TOKENS,
         "prefill_ms": round(pf_s * 1e3, 1),
         "prefill_tok_s": round(PF_TOKENS / pf_s, 1),

@@ -60,9 +60,11 @@ enum Epilogue { kStore = 0, kAdd = 1, kSwiGLU = 2, kPartial = 3, kAddNorm = 4, k
 // contiguous run of column blocks.  D = load pipeline depth (D-1 column blocks of
 // weights in flight while one is computed).
 // kKs: per-column-block input scale (NormIO::kss, the folded gated RMSNorm); depth 1.
-// TT > 0: T is the compile-time token count TT, and each column block's activation
-// fragments (16 * 2T units of 16 B) are fetched by 1, 2 or 4 coalesced loads (every
-// lane one distinct unit) and handed to the lanes that need them by ds_bpermute.
+// TT > 0: T is the compile-time token count TT.  For TT <= 4 each column block's
+// activation fragments (16 * 2T units of 16 B) are fetched by 1 or 2 coalesced loads
+// (every lane one distinct unit) and handed to the lanes that need them by
+// ds_bpermute; for TT = 5..8 the four per-lane loads are all but distinct units
+// already (NC = 2T of the 16 B columns), so each lane loads its own.
 // Loading each lane's B operand directly takes four 64-lane loads per block for
 // 128 * T distinct bytes; those load instructions, not the bytes, measured 2-4 us
 // per launch (34816 x 5120 at T=1: 31.5 -> 27.5 us cold).
@@ -236,8 +238,8 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                     wbuf[d][r][c] = __builtin_nontemporal_load(p);
                 }
         };
-        if constexpr (TT == 0) load_weights();
-        if constexpr (TT > 0) {
+        if constexpr (TT == 0 || TT > 4) load_weights();
+        if constexpr (TT > 0 && TT <= 4) {
             // L loads of P units: load j, lane l holds unit j*P + l; MFMA i of lane
             // (g, col) needs unit (i*4 + g)*NC + bcol, which is in load j = i*L/4
             constexpr int NCc = 2 * TT;
@@ -651,6 +653,17 @@ inline bool bperm_enabled() {
     return on;
 }
 
+// Row tiles per workgroup of the store and half-tile SwiGLU launches at T = 5..8
+// (RL_GEMM_RT8 = 1, 2 or 4 overrides it for measurement)
+inline int rt_wide() {
+    static const int rt = [] {
+        const char* v = std::getenv("RL_GEMM_RT8");
+        const int r = v ? std::atoi(v) : 0;
+        return r == 1 || r == 2 || r == 4 ? r : 2;
+    }();
+    return rt;
+}
+
 // RL_ADDNORM16=0: the T = 1 residual add-norm launches keep 8 waves (A/B measurement)
 inline bool addnorm16_enabled() {
     static const bool on = [] {
@@ -696,7 +709,7 @@ void launch_gemm_spec(const void* W, const float* tscale, const void* frag, floa
                                                          frag_out, io, s);
 }
 
-// Depth-1 launches with T <= 4 take the compile-time-T kernels (permuted B operand).
+// Depth-1 launches take the compile-time-T kernels (permuted B operand for T <= 4).
 template <bool kFp8, int RT, int KS, int D, bool kKs = false, bool kGuh = false>
 void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float* Y, int m, int n_kb, int T,
                      int epilogue, int ldy, int m_valid, int S, void* frag_out, const NormIO& io, hipStream_t s) {
@@ -707,6 +720,10 @@ void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float
             case 2: launch_gemm_spec<kFp8, RT, KS, kKs, 2, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
             case 3: launch_gemm_spec<kFp8, RT, KS, kKs, 3, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
             case 4: launch_gemm_spec<kFp8, RT, KS, kKs, 4, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 5: launch_gemm_spec<kFp8, RT, KS, kKs, 5, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 6: launch_gemm_spec<kFp8, RT, KS, kKs, 6, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 7: launch_gemm_spec<kFp8, RT, KS, kKs, 7, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
+            case 8: launch_gemm_spec<kFp8, RT, KS, kKs, 8, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
             default: break;
             }
         }
@@ -741,8 +758,16 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
         RL_REQUIRE(m % 16 == 0 && S == 1 && !io.kss && !io.xpart, RL_ERR_RANGE,
                    "gemm swiglu (half tiles): rows a multiple of 16, no split or block scale");
         if (io.ss_in) RL_REQUIRE(16 >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
-        launch_gemm_cfg<kFp8, 1, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
-                                                     frag_out, io, s);
+        const int rtw = T > 4 ? rt_wide() : 1;
+        if (rtw == 4)
+            launch_gemm_cfg<kFp8, 4, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
+                                                         frag_out, io, s);
+        else if (rtw == 2)
+            launch_gemm_cfg<kFp8, 2, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
+                                                         frag_out, io, s);
+        else
+            launch_gemm_cfg<kFp8, 1, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
+                                                         frag_out, io, s);
         check_launch("gemm_frag_kernel");
         return;
     }
@@ -754,20 +779,20 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     // for 16480x5120 with weights cold in HBM.  BF16 (lm_head: many rounds) keeps
     // depth 2 (6.4 TB/s).
     GemmCfg c{2, (m_tiles + 1) / 2 * S >= 256 ? 8 : 16, kFp8 ? 1 : 2};
-    if (kFp8 && bperm_enabled() && T <= 4 && S == 1) {
-        // permuted-B kernels, measured cold (T = 1 / 4): stores one row tile per
+    if (kFp8 && bperm_enabled() && S == 1) {
+        // compile-time-T kernels, measured cold (T = 1 / 4): stores one row tile per
         // 16-wave workgroup (16480 x 5120: 15.6 / 17.7 us vs 17.7 / 18.7 with two row
         // tiles per 8 waves), SwiGLU two (gate and up) per 16 waves (34816 x 5120:
         // 29.6 / 30.2 us vs 30.8 / 31.1)
-        if (epilogue == kStore || epilogue == kAdd) c = GemmCfg{1, 16, 1};
+        if (epilogue == kStore || epilogue == kAdd) c = GemmCfg{T > 4 ? rt_wide() : 1, 16, 1};
         if (epilogue == kSwiGLU) c = GemmCfg{2, 16, 1};
     }
-    // BF16 stores at T <= 4 (the lm_head: 248320 x 5120, 2.54 GB) take the same split:
-    // 370 / 360 us at T = 1 / 4 against 392 / 398 us for two row tiles per 8 waves at
-    // depth 2 (weights in HBM; every T <= 4 uses this split, so rows of a verify equal
-    // the T = 1 rows bit for bit)
-    if (!kFp8 && bperm_enabled() && T <= 4 && S == 1 && (epilogue == kStore || epilogue == kAdd))
-        c = GemmCfg{1, 16, 1};
+    // BF16 stores (the lm_head: 248320 x 5120, 2.54 GB) take the same split: 370 / 360 us
+    // at T = 1 / 4 against 392 / 398 us for two row tiles per 8 waves at depth 2
+    // (weights in HBM; every T uses this split, so rows of a verify or batch step
+    // equal the T = 1 rows bit for bit)
+    if (!kFp8 && bperm_enabled() && S == 1 && (epilogue == kStore || epilogue == kAdd))
+        c = GemmCfg{T > 4 ? rt_wide() : 1, 16, 1};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
     // residual GEMMs (m = hidden: 160 groups): 8 waves measured faster than 16 there
@@ -823,6 +848,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     }
     RL_GEMM_CASE(2, 8, 1) RL_GEMM_CASE(2, 16, 1) RL_GEMM_CASE(2, 8, 2) RL_GEMM_CASE(2, 16, 2)
     RL_GEMM_CASE(2, 4, 1) RL_GEMM_CASE(2, 4, 2) RL_GEMM_CASE(1, 8, 1) RL_GEMM_CASE(1, 16, 1)
+    RL_GEMM_CASE(4, 16, 1)
 #undef RL_GEMM_CASE
     throw Error(RL_ERR_UNSUPPORTED, "gemm: unsupported work split");
 }

@@ -27,7 +27,7 @@ def test_e4m3_decode_bitexact(gpu, orc):
 
 
 @pytest.mark.parametrize("m,n", [(64, 512), (300, 1000), (17, 130), (1024, 5120)])
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 8])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 6, 7, 8])
 def test_gemm_fp8_vs_oracle(gpu, orc, m, n, T):
     r = synth.rng(100 + m + n + T)
     W = synth.fp8_weight(r, m, n)
@@ -40,19 +40,21 @@ def test_gemm_fp8_vs_oracle(gpu, orc, m, n, T):
         assert rel_l2(Y[t], Yo[t]) <= REL_L2, (m, n, T, t, rel_l2(Y[t], Yo[t]))
 
 
-def test_gemm_fp8_tokens_independent_of_T(gpu):
+@pytest.mark.parametrize("T", [4, 8])
+def test_gemm_fp8_tokens_independent_of_T(gpu, T):
     """Token t's output is bit-identical whether it runs alone (T=1) or inside a
-    T=4 verify batch: the greedy invariant needs T=4 == 4 x T=1 exactly."""
+    T=4 verify or a batch of 8 rows: the greedy invariant needs T=4 == 4 x T=1
+    exactly, and a batch slot's token equals the single-sequence step's."""
     r = synth.rng(7)
     m, n = 2048, 5120
     W = synth.fp8_weight(r, m, n)
     s = synth.fp8_scales(r, m, n)
-    X = r.standard_normal((4, n)).astype(np.float32)
+    X = r.standard_normal((T, n)).astype(np.float32)
     lin = ops.Fp8Linear(W, s)
-    Y4 = ops.linear_T(lin, X)
-    for t in range(4):
+    YT = ops.linear_T(lin, X)
+    for t in range(T):
         Y1 = ops.linear_T(lin, X[t:t + 1])[0]
-        assert np.array_equal(Y1.view(np.uint32), Y4[t].view(np.uint32)), t
+        assert np.array_equal(Y1.view(np.uint32), YT[t].view(np.uint32)), t
 
 
 def test_gemm_fp8_config1_full_shape(gpu, orc):
@@ -98,7 +100,7 @@ def test_gemm_fp8_large_activations(gpu, orc):
         assert rel_l2(Y[t], Yo[t]) <= REL_L2
 
 
-@pytest.mark.parametrize("m,n,T", [(96, 512, 1), (1000, 384, 4), (5120, 5120, 3)])
+@pytest.mark.parametrize("m,n,T", [(96, 512, 1), (1000, 384, 4), (5120, 5120, 3), (700, 640, 8), (2048, 1024, 6)])
 def test_gemm_bf16_vs_oracle(gpu, orc, m, n, T):
     r = synth.rng(200 + m)
     Wf = r.standard_normal((m, n)).astype(np.float32)
@@ -151,7 +153,7 @@ def test_gemm_fp8_split_k_partials(gpu, orc, T):
     assert np.any(P[1] != 0) and np.any(P[3] != 0)  # every slice did work
 
 
-@pytest.mark.parametrize("T", [1, 3])
+@pytest.mark.parametrize("T", [1, 3, 7])
 def test_gemm_fp8_swiglu_epilogue(gpu, orc, T):
     """Gate/up interleaved by 16-row tile, SwiGLU in the epilogue:
     h = silu(gate . x) * (up . x) (ops_fused.cpp:66-82, ops.cpp:607-609)."""
@@ -187,7 +189,7 @@ def _unpack_frag(raw, n, T):
 
 
 @pytest.mark.parametrize("T,block_scale,n", [(1, False, 1024), (4, False, 1024), (1, True, 1024), (4, True, 1024),
-                                               (2, True, 10240)])
+                                               (2, True, 10240), (8, False, 1024), (6, True, 1024)])
 def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale, n):
     """Residual GEMM fused with the next RMSNorm's data: x += W.a in place,
     fragments of x * (1 + gamma) for the next linear, and sum of x^2 per row group.
@@ -235,7 +237,7 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale, n):
     assert np.all(np.abs(fr - xg) <= 2.0 ** -15 * np.abs(xg) + 1e-30)
 
 
-@pytest.mark.parametrize("T,I", [(1, 512), (3, 520), (4, 256), (6, 136)])
+@pytest.mark.parametrize("T,I", [(1, 512), (3, 520), (4, 256), (6, 136), (8, 264)])
 def test_gemm_fp8_swiglu_half_tiles(gpu, orc, T, I):
     """The engine's gate/up packing (rl_hip_pack_fp8_gate_up: tile k = gate rows
     8k..8k+7 then up rows 8k..8k+7, a block scale per half) with the SwiGLU epilogue
@@ -256,7 +258,7 @@ def test_gemm_fp8_swiglu_half_tiles(gpu, orc, T, I):
         assert rel_l2(Hh[t], want) <= REL_L2, (t, rel_l2(Hh[t], want))
 
 
-@pytest.mark.parametrize("T", [1, 2, 4, 5])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8])
 @pytest.mark.parametrize("epi", [0, 5])
 def test_gemm_fp8_folded_norm_input(gpu, orc, T, epi):
     """Store and half-tile SwiGLU launches that read the residual stream's sums of
