@@ -106,7 +106,7 @@ int rl_hip_pack_fp8_gate_up(const uint8_t* gate_w, const float* gate_scale, cons
 int rl_hip_pack_bf16_gate_up(const uint16_t* gate_w, const uint16_t* up_w, uint16_t* w_tiled, int I, int n,
                              void* stream);
 int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream);
-/* Y[T][m] (=, or += when accumulate) W . X for T in 1..8 using a packed fragment
+/* Y[T][m] (=, or += when accumulate) W . X for T in 1..16 using a packed fragment
  * buffer.  Deterministic: partial sums are combined in a fixed order, and token t's
  * result does not depend on T. */
 /* Prompt prefill: Y[t][ldy] (=, +=) W . x_t for T (any) tokens of rl_hip_pack_act
@@ -363,9 +363,9 @@ void* rl_hip_engine_stream(RlEngine* e);
  * at position poss[b] for slots 0 .. B-1 in one weight pass (B = 1: set_pos +
  * decode_token, as the reference); copy_logits_n / copy_greedy_n return its B rows.
  * prefill_slot runs the prefill on slot `slot` (copy_logits then has its last row).
- * max_batch <= 16.  A step over more slots than one weight pass takes (8 rows for
- * FP8 / BF16 linears, 4 for the K-quant GEMV) runs them in groups, one weight pass
- * each.  Needs the folded path: FP8 / BF16 linears (v_dim 128), or K-quant
+ * max_batch <= 16.  FP8 / BF16 linears take all 16 rows in one weight pass; the
+ * K-quant GEMV takes 4, so a K-quant step over more slots runs them in groups, one
+ * weight pass each.  Needs the folded path: FP8 / BF16 linears (v_dim 128), or K-quant
  * (Q4_K / Q6_K) linears with max_T <= 4; otherwise RL_ERR_UNSUPPORTED. */
 RlEngine* rl_hip_engine_create_batch(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx,
                                      int max_T, int max_batch, int* status);

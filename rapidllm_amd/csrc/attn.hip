@@ -652,7 +652,7 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     RL_REQUIRE(hd == kHD, RL_ERR_UNSUPPORTED, "attn: head_dim must be 256");
     RL_REQUIRE(nb >= 1 && nb <= 64, RL_ERR_RANGE, "attn: slot count must be in 1..64");
     if (T_out <= 0) T_out = T * nb;
-    RL_REQUIRE(t_off >= 0 && t_off + nb * T <= T_out && T_out <= 8, RL_ERR_RANGE, "attn: bad output columns");
+    RL_REQUIRE(t_off >= 0 && t_off + nb * T <= T_out && T_out <= 16, RL_ERR_RANGE, "attn: bad output columns");
     RL_REQUIRE(nb == 1 || (kv_bstride >= static_cast<size_t>(nkv) * ctx * kHD && pos_stride >= 1), RL_ERR_RANGE,
                "attn: slot strides must separate the slots' caches and positions");
     RL_REQUIRE(nkv > 0 && nq % nkv == 0, RL_ERR_RANGE, "attn: n_q must be a multiple of n_kv");

@@ -683,7 +683,7 @@ class Engine {
 
    private:
     static constexpr int kMaxSlots = 16;   // batch slots
-    static constexpr int kGroupRows = 8;   // rows of one batch step (FP8 / BF16 linears)
+    static constexpr int kGroupRows = 16;  // rows of one batch step (FP8 / BF16 linears)
     static constexpr int kKqGroupRows = 4; // rows of one batch step (K-quant GEMV)
     // device scalar block
     enum { kPos = 0, kSlot = 1, kNCons = 2, kNextTok = 3, kGenCount = 4, kScalars = 8 };
@@ -1024,7 +1024,7 @@ class Engine {
                 if (Ly.kind == RL_LAYER_DELTA && Ly.gnorm_n != c_.v_dim) per_head = false;
             gdn_fused_norm_ = fold_norm_ && per_head;
             gdn_fused_ = gdn_fused_norm_ ||
-                         (kq_fold_ && nd > 0 && gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && T <= 8);
+                         (kq_fold_ && nd > 0 && gdn_fused_supported(c_.k_dim, c_.v_dim, c_.conv_k) && tmax_ <= 8);
             kq_gnorm_ = kq_fold_ && gdn_fused_ && per_head;
         }
         // one committed S per layer plus R banks of per-token records with the fused
@@ -2064,22 +2064,26 @@ class Engine {
             out.gamma_out = Ly.ffn_norm;
             out.ss_out = ss_;
             if (Ly.kind == RL_LAYER_DELTA) {
+                // the a/b rows as K-slices of the first workgroups (one row tile per
+                // workgroup) up to 8 rows; above that the in_proj takes four row tiles
+                // per workgroup and the a/b rows with them
+                float* abp = B <= 8 ? abpart_ : nullptr;
                 NormIO in_ab = io_in ? *io_in : NormIO{};
-                if (abpart_) {
-                    in_ab.xpart = abpart_;
+                if (abp) {
+                    in_ab.xpart = abp;
                     in_ab.x_tile0 = ab_tile0_;
                     in_ab.x_slices = kAbSlices;
                     in_ab.x_rows = ab_rows_;
                 }
                 gemm_on(Ly.in_parts[0], frag_x_, ybuf_, Ly.in_width, Ly.in_parts[0].m, B, kEpiStore, nullptr,
-                        abpart_ ? &in_ab : io_in);
+                        abp ? &in_ab : io_in);
                 const GdnRecords rec{b_rec(Ly.dslot), b_recn(Ly.dslot), b_scal() + kNCons, tmax_, 0};
-                const float* a_in = abpart_ ? abpart_ : ybuf_ + Ly.off_a;
-                const float* b_in = abpart_ ? abpart_ + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b;
+                const float* a_in = abp ? abp : ybuf_ + Ly.off_a;
+                const float* b_in = abp ? abp + (Ly.off_b - Ly.off_a) : ybuf_ + Ly.off_b;
                 gdn_decode_fused(ybuf_, a_in, b_in, Ly.in_width, Ly.A_log, Ly.dt_bias, Ly.conv_w, b_conv(Ly.dslot),
                                  nullptr, b_S(Ly.dslot), b_S(Ly.dslot), b_scal() + kSlot, conv_slot_, R_, &rec, nullptr,
                                  ybuf_ + Ly.off_z, Ly.gnorm, frag_, gss_, 1, nk, nv, c_.k_dim, dv, c_.conv_k,
-                                 c_.v_tiled, st_, abpart_ ? kAbSlices : 1, ab_rows_, &bt);
+                                 c_.v_tiled, st_, abp ? kAbSlices : 1, abp ? ab_rows_ : 0, &bt);
                 out.kss = gss_;
                 out.kss_n = dv;
                 out.kss_eps = 1e-6f;

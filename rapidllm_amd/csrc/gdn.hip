@@ -840,7 +840,10 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
                    T_rows};
     RL_REQUIRE(T_rows == 0 || (p.batch.B == 1 && row_off >= 0 && row_off + T <= T_rows), RL_ERR_RANGE,
                "gdn_decode_fused: token rows out of range");
-    RL_REQUIRE(p.batch.B >= 1 && p.batch.B * T <= kMaxT, RL_ERR_RANGE, "gdn_decode_fused: batch x T must be <= 8");
+    // T tokens per sequence (its per-token arrays), B sequences as grid rows; the
+    // token rows of all sequences (B x T) are only indexed in the global buffers
+    RL_REQUIRE(p.batch.B >= 1 && p.batch.B <= 16 && T <= kMaxT && p.batch.B * T <= 16, RL_ERR_RANGE,
+               "gdn_decode_fused: T <= 8 tokens and B x T <= 16 rows");
     RL_REQUIRE(p.batch.B == 1 || cur, RL_ERR_RANGE, "gdn_decode_fused: a batch needs the conv ring");
     const dim3 grid(nv * (dv / kCW), p.batch.B);
     switch (T) {

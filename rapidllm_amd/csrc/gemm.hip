@@ -1,4 +1,4 @@
-// gemm.hip -- skinny block-FP8 / BF16 linears for T = 1..8 tokens on gfx950 MFMA.
+// gemm.hip -- skinny block-FP8 / BF16 linears for T = 1..16 tokens on gfx950 MFMA.
 //
 // Computes Y[t][i] = sum_j W[i][j] * scale(i/128, j/128) * X[t][j], the arithmetic
 // of ops::gemv_fp8 (reference src/kernels/ops.cpp:182-194), for all T tokens in one
@@ -116,12 +116,18 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     const int kb_begin = min(s_end, s_begin + wave * per);
     const int kb_end = min(s_end, kb_begin + per);
 
-    f32x4 tots[NP][RT];
+    // TT = 9..16: the 2T B columns (hi of each token, then mid) span two 16-column
+    // MFMA tiles; every weight fragment feeds one MFMA per tile
+    constexpr int NCT = TT > 8 ? 2 : 1;
+    constexpr int kMaxTok = TT > 8 ? 16 : 8;
+    f32x4 tots[NP][RT][NCT];
 #pragma unroll
     for (int q = 0; q < NP; ++q)
 #pragma unroll
-        for (int r = 0; r < RT; ++r) tots[q][r] = f32x4{0.f, 0.f, 0.f, 0.f};
-    f32x4* tot = tots[0];
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) tots[q][r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
+    auto* tot = tots[0];
 
     // RMSNorm folded into this GEMM (io.ss_in): the input fragments hold x * (1+gamma)
     // unnormalised, and the outputs are scaled by 1/rms(x_t).  Wave w < T sums the
@@ -146,39 +152,47 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     // The sums are copied straight into LDS (global_load_lds: no registers held
     // through the main loop) and reduced in the epilogue.
     constexpr int kMaxSsPerLane = 4;  // groups <= 256
-    __shared__ float ss_lds[8][64 * kMaxSsPerLane];
+    __shared__ float ss_lds[kMaxTok][64 * kMaxSsPerLane];
+    // wave w takes tokens w, w + KSPLIT, ...
     const bool ss_wave = has_ss && wave < T;
     if (ss_wave) {
+        for (int t = wave; t < T; t += KSPLIT) {
 #pragma unroll
-        for (int k = 0; k < kMaxSsPerLane; ++k) {
-            const int gi = lane + 64 * k;
-            const float* src = io.ss_in + static_cast<size_t>(gi < io.groups_in ? gi : 0) * T + wave;
-            __builtin_amdgcn_global_load_lds(src, &ss_lds[wave][64 * k], 4, 0, 0);
+            for (int k = 0; k < kMaxSsPerLane; ++k) {
+                const int gi = lane + 64 * k;
+                const float* src = io.ss_in + static_cast<size_t>(gi < io.groups_in ? gi : 0) * T + t;
+                __builtin_amdgcn_global_load_lds(src, &ss_lds[t][64 * k], 4, 0, 0);
+            }
         }
     }
-    __shared__ f32x4 red[KP][RT][64];
-    __shared__ float s_inv[8];
+    __shared__ f32x4 red[KP][RT][NCT][64];
+    __shared__ float s_inv[kMaxTok];
     // Token `wave`'s 1/rms from the sums of squares in LDS (every load of this wave,
     // the copies included, has completed: the wait is explicit for waves that had no
     // column block to wait on).
     auto reduce_ss = [&]() {
         if (ss_wave) {
             asm volatile("s_waitcnt vmcnt(0)" ::: "memory");
-            double ss = 0.0;
+            for (int t = wave; t < T; t += KSPLIT) {
+                double ss = 0.0;
 #pragma unroll
-            for (int k = 0; k < kMaxSsPerLane; ++k) {
-                const int gi = lane + 64 * k;
-                ss += gi < io.groups_in ? static_cast<double>(ss_lds[wave][gi]) : 0.0;  // group order
+                for (int k = 0; k < kMaxSsPerLane; ++k) {
+                    const int gi = lane + 64 * k;
+                    ss += gi < io.groups_in ? static_cast<double>(ss_lds[t][gi]) : 0.0;  // group order
+                }
+                ss = wave_sum_d(ss);                                  // fixed butterfly order
+                if (lane == 0) s_inv[t] = 1.f / sqrtf(static_cast<float>(ss / io.n_norm) + io.eps);
             }
-            ss = wave_sum_d(ss);                                  // fixed butterfly order
-            if (lane == 0) s_inv[wave] = 1.f / sqrtf(static_cast<float>(ss / io.n_norm) + io.eps);
         }
     };
 
     // Lanes of B columns >= 2T read a valid column: those MFMA output columns are
     // never used, and unconditional loads keep the load count identical on every
     // path, so the compiler's waits stay exact.
-    const int bcol = min(col, NC - 1);
+    int bcolv[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) bcolv[c] = min(16 * c + col, NC - 1);
+    const int bcol = bcolv[0];
     const uint8_t* wbase[RT];
     const float* sbase[RT];
 #pragma unroll
@@ -187,21 +201,23 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         wbase[r] = W + static_cast<size_t>(rt) * n_kb * kTileBytes;  // uniform tile-row base
         sbase[r] = kFp8 ? tscale + static_cast<size_t>(rt) * n_kb * (kGuh ? 2 : 1) : nullptr;
     }
-    const i32x4* fbase = frag + static_cast<size_t>(g) * NC + bcol;
+    const i32x4* fbase = frag + static_cast<size_t>(g) * NC;
     const size_t fstride = static_cast<size_t>(16) * NC;  // per column block
 
     i32x4 wbuf[D][RT][NW];
-    i32x4 bbuf[D][4];
+    i32x4 bbuf[D][NCT][4];
     float sbuf[D][RT];
     float sbuf2[D][RT];  // kGuh: the up half's scale
     // kKs: this lane's token (B column hi / mid of token ktok) and the block scale
     // 1 / rms of the block's four partial sums of squares
-    const int ktok = bcol < T ? bcol : bcol - T;
+    int ktokv[NCT];
+#pragma unroll
+    for (int c = 0; c < NCT; ++c) ktokv[c] = bcolv[c] < T ? bcolv[c] : bcolv[c] - T;
     const float kss_inv_n = kKs ? 1.f / static_cast<float>(io.kss_n) : 0.f;
-    auto block_sums = [&](int kb) {
+    auto block_sums = [&](int kb, int c = 0) {
         // this lane's token's four sums of the block, requested just before the
         // block's weights (loads return in issue order, so they are there first)
-        return reinterpret_cast<const float4*>(io.kss)[static_cast<size_t>(kb) * T + ktok];
+        return reinterpret_cast<const float4*>(io.kss)[static_cast<size_t>(kb) * T + ktokv[c]];
     };
     auto block_scale = [&](const float4 q) {
         return __builtin_amdgcn_rsqf(((q.x + q.y) + (q.z + q.w)) * kss_inv_n + io.kss_eps);
@@ -256,22 +272,26 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                 const int j = i * L / 4;
                 const int addr = ((i * 4 + g) * NCc + bcol - j * P) * 4;  // source lane, in bytes
 #pragma unroll
-                for (int c = 0; c < 4; ++c) bbuf[d][i][c] = __builtin_amdgcn_ds_bpermute(addr, src[j][c]);
+                for (int c = 0; c < 4; ++c) bbuf[d][0][i][c] = __builtin_amdgcn_ds_bpermute(addr, src[j][c]);
             }
         } else {
 #pragma unroll
-            for (int i = 0; i < 4; ++i) bbuf[d][i] = fbase[kb * fstride + i * 4 * NC];
+            for (int c = 0; c < NCT; ++c)
+#pragma unroll
+                for (int i = 0; i < 4; ++i) bbuf[d][c][i] = fbase[kb * fstride + i * 4 * NC + bcolv[c]];
         }
     };
-    auto compute = [&](int d, int kb, float ks = 1.f, int q = 0) {
-        f32x4* tot = tots[q];
+    // ks0 / ks1: the kKs block scale of the lane's token in column tile 0 / 1
+    auto compute = [&](int d, int kb, float ks0 = 1.f, int q = 0, float ks1 = 1.f) {
+        auto* tot = tots[q];
 #pragma unroll
         for (int r = 0; r < RT; ++r) {
-            f32x4 acc = {0.f, 0.f, 0.f, 0.f};
+            f32x4 acc[NCT];
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) acc[c] = f32x4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                Frag8 a, b;
-                b.i = bbuf[d][i];
+                Frag8 a;
                 if constexpr (kFp8) {
                     const i32x4 wv = wbuf[d][r][i >> 1];
                     const uint32_t d0 = static_cast<uint32_t>((i & 1) ? wv[2] : wv[0]);
@@ -281,18 +301,27 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                 } else {
                     a.i = wbuf[d][r][i];
                 }
-                acc = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc, 0, 0, 0);
+#pragma unroll
+                for (int c = 0; c < NCT; ++c) {
+                    Frag8 b;
+                    b.i = bbuf[d][c][i];
+                    acc[c] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[c], 0, 0, 0);
+                }
             }
-            if constexpr (kFp8 && kGuh)
-                tot[r] += (g < 2 ? sbuf[d][r] : sbuf2[d][r]) * acc;  // C rows 4g..4g+3: gate g < 2
-            else if constexpr (kFp8 && kKs)
-                tot[r] += (sbuf[d][r] * ks) * acc;
-            else if constexpr (kFp8)
-                tot[r] += sbuf[d][r] * acc;
-            else if constexpr (kKs)
-                tot[r] += ks * acc;
-            else
-                tot[r] += acc;
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) {
+                const float ks = c == 0 ? ks0 : ks1;
+                if constexpr (kFp8 && kGuh)
+                    tot[r][c] += (g < 2 ? sbuf[d][r] : sbuf2[d][r]) * acc[c];  // C rows 4g..4g+3: gate g < 2
+                else if constexpr (kFp8 && kKs)
+                    tot[r][c] += (sbuf[d][r] * ks) * acc[c];
+                else if constexpr (kFp8)
+                    tot[r][c] += sbuf[d][r] * acc[c];
+                else if constexpr (kKs)
+                    tot[r][c] += ks * acc[c];
+                else
+                    tot[r][c] += acc[c];
+            }
         }
     };
 
@@ -309,8 +338,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
                     const int kb = kb0 + q * KSPLIT;
                     if (q == 0 || kb < s_end) {
                         const float4 qs = block_sums(kb);
+                        const float4 qs1 = NCT > 1 ? block_sums(kb, NCT - 1) : qs;
                         load(0, kb, true);
-                        compute(0, kb, block_scale(qs), q);
+                        compute(0, kb, block_scale(qs), q, block_scale(qs1));
                     }
                 }
             }
@@ -354,7 +384,9 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
 #pragma unroll
     for (int q = 0; q < NP; ++q)
 #pragma unroll
-        for (int r = 0; r < RT; ++r) red[wave + q * KSPLIT][r][lane] = tots[q][r];
+        for (int r = 0; r < RT; ++r)
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) red[wave + q * KSPLIT][r][c][lane] = tots[q][r][c];
     reduce_ss();
     __syncthreads();
 
@@ -363,9 +395,12 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
     auto wg_value = [&](int r, int t, int row) {
         const int src_lane = (row >> 2) * 16;
         const int v = row & 3;
+        const int ch = t, cm = T + t;  // B columns of the token's hi and mid parts
         float s = 0.f;
 #pragma unroll
-        for (int w = 0; w < KP; ++w) s += red[w][r][src_lane + t][v] + red[w][r][src_lane + T + t][v];
+        for (int w = 0; w < KP; ++w)
+            s += red[w][r][NCT > 1 ? ch >> 4 : 0][src_lane + (ch & 15)][v] +
+                 red[w][r][NCT > 1 ? cm >> 4 : 0][src_lane + (cm & 15)][v];
         return s;
     };
 
@@ -472,14 +507,16 @@ __global__ __launch_bounds__(64 * KSPLIT) void gemm_frag_kernel(const uint8_t* _
         for (int r = 0; r < RT; ++r) {
             wbase[r] = W + static_cast<size_t>(xt) * n_kb * kTileBytes;
             sbase[r] = kFp8 ? tscale + static_cast<size_t>(xt) * n_kb : nullptr;
-            tot[r] = f32x4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+            for (int c = 0; c < NCT; ++c) tot[r][c] = f32x4{0.f, 0.f, 0.f, 0.f};
         }
         if (wave < per && kb < n_kb) {
             load(0, kb, true);
             compute(0, kb);
         }
         __syncthreads();  // the row epilogue above has read red
-        red[wave][0][lane] = tot[0];
+#pragma unroll
+        for (int c = 0; c < NCT; ++c) red[wave][0][c][lane] = tot[0][c];
         __syncthreads();
         if (static_cast<int>(threadIdx.x) < kTileRows * T) {
             const int row = threadIdx.x % kTileRows, t = threadIdx.x / kTileRows;
@@ -664,6 +701,17 @@ inline int rt_wide() {
     return rt;
 }
 
+// Row tiles per workgroup of the store and half-tile SwiGLU launches at T = 9..16
+// (RL_GEMM_RT16 = 2 or 4 overrides it for measurement)
+inline int rt_batch() {
+    static const int rt = [] {
+        const char* v = std::getenv("RL_GEMM_RT16");
+        const int r = v ? std::atoi(v) : 0;
+        return r == 2 || r == 4 ? r : 4;
+    }();
+    return rt;
+}
+
 // RL_ADDNORM16=0: the T = 1 residual add-norm launches keep 8 waves (A/B measurement)
 inline bool addnorm16_enabled() {
     static const bool on = [] {
@@ -726,8 +774,18 @@ void launch_gemm_cfg(const void* W, const float* tscale, const void* frag, float
             case 8: launch_gemm_spec<kFp8, RT, KS, kKs, 8, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S, frag_out, io, s); return;
             default: break;
             }
+            // T = 9..16 (batch steps of up to 16 rows): the 16-wave splits
+            if constexpr (KS == 16) {
+#define RL_T16(TN)                                                                                                      case TN:                                                                                                                launch_gemm_spec<kFp8, RT, KS, kKs, TN, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S,                                                        frag_out, io, s);                                                   return;
+                switch (T) {
+                    RL_T16(9) RL_T16(10) RL_T16(11) RL_T16(12) RL_T16(13) RL_T16(14) RL_T16(15) RL_T16(16)
+                default: break;
+                }
+#undef RL_T16
+            }
         }
     }
+    RL_REQUIRE(T <= 8, RL_ERR_UNSUPPORTED, "gemm: more than 8 rows need the batch work split");
     launch_gemm_tt<kFp8, RT, KS, D, kKs, 0, -1, -1, kGuh>(W, tscale, frag, Y, m, n_kb, T, epilogue, ldy, m_valid, S,
                                                          frag_out, io, s);
 }
@@ -740,7 +798,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
                  const NormIO* norm = nullptr) {
     const NormIO io = norm ? *norm : NormIO{};
     RL_REQUIRE(m > 0 && n > 0, RL_ERR_RANGE, "gemm: empty shape");
-    RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "gemm: T must be in 1..8");
+    RL_REQUIRE(T >= 1 && T <= 16, RL_ERR_RANGE, "gemm: T must be in 1..16");
     RL_REQUIRE(W && frag && (Y || frag_out), RL_ERR_RANGE, "gemm: null pointer");
     RL_REQUIRE(!frag_out || epilogue == kSwiGLU || epilogue == kSwiGLUH || epilogue == kAddNorm, RL_ERR_RANGE,
                "gemm: fragment output only with the SwiGLU / add-norm epilogues");
@@ -757,9 +815,14 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
         // vs 29.6 us for the whole-tile interleave at two tiles per workgroup)
         RL_REQUIRE(m % 16 == 0 && S == 1 && !io.kss && !io.xpart, RL_ERR_RANGE,
                    "gemm swiglu (half tiles): rows a multiple of 16, no split or block scale");
-        if (io.ss_in) RL_REQUIRE(16 >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
         const int rtw = T > 4 ? rt_wide() : 1;
-        if (rtw == 4)
+        if (T > 8 && rt_batch() == 4)
+            launch_gemm_cfg<kFp8, 4, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
+                                                         frag_out, io, s);
+        else if (T > 8)
+            launch_gemm_cfg<kFp8, 2, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
+                                                         frag_out, io, s);
+        else if (rtw == 4)
             launch_gemm_cfg<kFp8, 4, 16, 1, false, true>(W, tscale, frag, Y, m, n_kb, T, kSwiGLU, ldy, m_valid, S,
                                                          frag_out, io, s);
         else if (rtw == 2)
@@ -784,7 +847,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
         // 16-wave workgroup (16480 x 5120: 15.6 / 17.7 us vs 17.7 / 18.7 with two row
         // tiles per 8 waves), SwiGLU two (gate and up) per 16 waves (34816 x 5120:
         // 29.6 / 30.2 us vs 30.8 / 31.1)
-        if (epilogue == kStore || epilogue == kAdd) c = GemmCfg{T > 4 ? rt_wide() : 1, 16, 1};
+        if (epilogue == kStore || epilogue == kAdd) c = GemmCfg{T > 8 ? 2 : T > 4 ? rt_wide() : 1, 16, 1};
         if (epilogue == kSwiGLU) c = GemmCfg{2, 16, 1};
     }
     // BF16 stores (the lm_head: 248320 x 5120, 2.54 GB) take the same split: 370 / 360 us
@@ -792,7 +855,7 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     // (weights in HBM; every T uses this split, so rows of a verify or batch step
     // equal the T = 1 rows bit for bit)
     if (!kFp8 && bperm_enabled() && S == 1 && (epilogue == kStore || epilogue == kAdd))
-        c = GemmCfg{T > 4 ? rt_wide() : 1, 16, 1};
+        c = GemmCfg{T > 8 ? 2 : T > 4 ? rt_wide() : 1, 16, 1};
     if (g_force.rt) c = g_force;
     if (epilogue == kSwiGLU && c.rt == 1) c.rt = 2;
     // residual GEMMs (m = hidden: 160 groups): 8 waves measured faster than 16 there
@@ -803,8 +866,19 @@ void launch_gemm(const void* W, const float* tscale, const void* frag, float* Y,
     // T = 1 row equals the same row of a verify or batch step bit for bit.
     if (epilogue == kAddNorm && !g_force.rt)
         c = GemmCfg{2, kFp8 && bperm_enabled() && T == 1 && addnorm16_enabled() ? 16 : 8, kFp8 ? 1 : 2};
-    if (io.ss_in || epilogue == kAddNorm)
-        RL_REQUIRE(c.ks >= T, RL_ERR_RANGE, "gemm: folded RMSNorm needs a wave per token");
+    // 9..16 rows: the compile-time-T kernels with 16 waves at depth 1 (the same K split
+    // as T = 1, so a batch row equals the single-sequence row bit for bit).  The
+    // activation fragments of 16 tokens (8 KiB per column block) outweigh a row tile's
+    // weights (2 KiB), so stores take several row tiles per workgroup: at T = 16
+    // 34816 x 5120 SwiGLU 77.8 / 57.7 / 50.5 us with one / two / four, 14336 x 5120
+    // 26.6 / 21.0 us with two / four
+    if (T > 8) {
+        RL_REQUIRE(bperm_enabled() && !g_force.rt, RL_ERR_UNSUPPORTED,
+                   "gemm: more than 8 rows need the default work splits");
+        c = GemmCfg{epilogue == kStore || epilogue == kAdd ? rt_batch() : 2, 16, 1};
+    }
+    if (epilogue == kAddNorm)
+        RL_REQUIRE(c.rt * T * kTileRows <= 64 * c.ks, RL_ERR_RANGE, "gemm add-norm: a thread per output item");
     if (io.kss) {
         // folded gated norm (out_proj): the residual configuration only
         RL_REQUIRE(!io.ss_in && io.kss_n > 0 && S == 1, RL_ERR_RANGE, "gemm: bad block input scale");

@@ -233,12 +233,14 @@ def test_kquant_batch_decode_vs_oracle(gpu, orc, kinds, quant, B):
     ref.close()
 
 
-@pytest.mark.parametrize("kinds,quant,B", [([1, 1], M.Q_Q4_K, 6), ([0, 1], M.Q_Q6_K, 5), ([0, 0, 0, 1], None, 12)])
+@pytest.mark.parametrize("kinds,quant,B", [([1, 1], M.Q_Q4_K, 6), ([0, 1], M.Q_Q6_K, 5), ([0, 0, 0, 1], None, 12),
+                                           ([0, 0, 0, 1], None, 16), ([0, 1], None, 9)])
 def test_batch_slot_groups(gpu, kinds, quant, B):
-    """More slots than one batch step's rows (the K-quant GEMV takes 4, the FP8 GEMM
-    8): decode_tokens runs the slots in groups, one weight pass each, and every
-    slot's logits equal single-sequence decoding of its sequence bit for bit (the
-    reference allows up to min(ctx, 128) slots, cuda_engine.cu:20057-20062)."""
+    """More slots than one batch step's rows (the K-quant GEMV takes 4): decode_tokens
+    runs the slots in groups, one weight pass each; FP8 / BF16 steps take up to 16
+    rows in one pass.  Every slot's logits equal single-sequence decoding of its
+    sequence bit for bit (the reference allows up to min(ctx, 128) slots,
+    cuda_engine.cu:20057-20062)."""
     spec = mini_spec(n_layers=len(kinds), layer_kinds=kinds)
     if quant is None:
         W = M.random_weights(spec, seed=12, w_scale=(1e-3, 1e-2))

@@ -27,7 +27,7 @@ def test_e4m3_decode_bitexact(gpu, orc):
 
 
 @pytest.mark.parametrize("m,n", [(64, 512), (300, 1000), (17, 130), (1024, 5120)])
-@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 6, 7, 8])
+@pytest.mark.parametrize("T", [1, 2, 3, 4, 5, 6, 7, 8, 9, 12, 16])
 def test_gemm_fp8_vs_oracle(gpu, orc, m, n, T):
     r = synth.rng(100 + m + n + T)
     W = synth.fp8_weight(r, m, n)
@@ -40,7 +40,7 @@ def test_gemm_fp8_vs_oracle(gpu, orc, m, n, T):
         assert rel_l2(Y[t], Yo[t]) <= REL_L2, (m, n, T, t, rel_l2(Y[t], Yo[t]))
 
 
-@pytest.mark.parametrize("T", [4, 8])
+@pytest.mark.parametrize("T", [4, 8, 13, 16])
 def test_gemm_fp8_tokens_independent_of_T(gpu, T):
     """Token t's output is bit-identical whether it runs alone (T=1) or inside a
     T=4 verify or a batch of 8 rows: the greedy invariant needs T=4 == 4 x T=1
@@ -100,7 +100,8 @@ def test_gemm_fp8_large_activations(gpu, orc):
         assert rel_l2(Y[t], Yo[t]) <= REL_L2
 
 
-@pytest.mark.parametrize("m,n,T", [(96, 512, 1), (1000, 384, 4), (5120, 5120, 3), (700, 640, 8), (2048, 1024, 6)])
+@pytest.mark.parametrize("m,n,T", [(96, 512, 1), (1000, 384, 4), (5120, 5120, 3), (700, 640, 8), (2048, 1024, 6), (1500, 768, 16),
+                                   (300, 256, 11)])
 def test_gemm_bf16_vs_oracle(gpu, orc, m, n, T):
     r = synth.rng(200 + m)
     Wf = r.standard_normal((m, n)).astype(np.float32)
@@ -153,7 +154,7 @@ def test_gemm_fp8_split_k_partials(gpu, orc, T):
     assert np.any(P[1] != 0) and np.any(P[3] != 0)  # every slice did work
 
 
-@pytest.mark.parametrize("T", [1, 3, 7])
+@pytest.mark.parametrize("T", [1, 3, 7, 12])
 def test_gemm_fp8_swiglu_epilogue(gpu, orc, T):
     """Gate/up interleaved by 16-row tile, SwiGLU in the epilogue:
     h = silu(gate . x) * (up . x) (ops_fused.cpp:66-82, ops.cpp:607-609)."""
@@ -189,7 +190,8 @@ def _unpack_frag(raw, n, T):
 
 
 @pytest.mark.parametrize("T,block_scale,n", [(1, False, 1024), (4, False, 1024), (1, True, 1024), (4, True, 1024),
-                                               (2, True, 10240), (8, False, 1024), (6, True, 1024)])
+                                               (2, True, 10240), (8, False, 1024), (6, True, 1024), (16, False, 1024),
+                                               (11, True, 1024), (16, True, 10240)])
 def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale, n):
     """Residual GEMM fused with the next RMSNorm's data: x += W.a in place,
     fragments of x * (1 + gamma) for the next linear, and sum of x^2 per row group.
@@ -237,7 +239,7 @@ def test_gemm_fp8_add_norm_epilogue(gpu, orc, T, block_scale, n):
     assert np.all(np.abs(fr - xg) <= 2.0 ** -15 * np.abs(xg) + 1e-30)
 
 
-@pytest.mark.parametrize("T,I", [(1, 512), (3, 520), (4, 256), (6, 136), (8, 264)])
+@pytest.mark.parametrize("T,I", [(1, 512), (3, 520), (4, 256), (6, 136), (8, 264), (16, 512), (10, 136)])
 def test_gemm_fp8_swiglu_half_tiles(gpu, orc, T, I):
     """The engine's gate/up packing (rl_hip_pack_fp8_gate_up: tile k = gate rows
     8k..8k+7 then up rows 8k..8k+7, a block scale per half) with the SwiGLU epilogue
@@ -258,7 +260,7 @@ def test_gemm_fp8_swiglu_half_tiles(gpu, orc, T, I):
         assert rel_l2(Hh[t], want) <= REL_L2, (t, rel_l2(Hh[t], want))
 
 
-@pytest.mark.parametrize("T", [1, 2, 4, 5, 8])
+@pytest.mark.parametrize("T", [1, 2, 4, 5, 8, 10, 16])
 @pytest.mark.parametrize("epi", [0, 5])
 def test_gemm_fp8_folded_norm_input(gpu, orc, T, epi):
     """Store and half-tile SwiGLU launches that read the residual stream's sums of
