@@ -657,8 +657,9 @@ def main():
                     help="time only a prompt prefill of this many tokens (for kernel traces)")
     ap.add_argument("--configs-only", action="store_true",
                     help="run only the per-config kernel lines (configs 1-4), for kernel traces")
-    ap.add_argument("--batch-only", action="store_true",
-                    help="time only the batch-4 decode step (C5, 32K context per slot)")
+    ap.add_argument("--batch-only", type=int, nargs="?", const=4, default=0,
+                    help="time only the batch decode step of this many slots (default 4; C5, 32K context "
+                         "per slot)")
     ap.add_argument("--step-only", action="store_true",
                     help="time only the T=1 decode and T=4 verify steps (for kernel traces and A/B runs)")
     ap.add_argument("--copy-probe-mb", type=int, default=0,
@@ -715,13 +716,14 @@ def main():
         print(json.dumps(res))
         return
     if args.batch_only:
-        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=4)
+        B = args.batch_only
+        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=B)
         eng.synthetic_context(CTX)
-        eng.replicate_slot0(4)
-        eng.time_batch(4, args.warmup)
-        tb4 = eng.time_batch(4, args.steps) / args.steps
+        eng.replicate_slot0(B)
+        eng.time_batch(B, args.warmup)
+        tb = eng.time_batch(B, args.steps) / args.steps
         eng.close()
-        print(json.dumps({"batch4_step_ms": round(tb4, 4), "batch4_tok_s": round(4000.0 / tb4, 3)}))
+        print(json.dumps({f"batch{B}_step_ms": round(tb, 4), f"batch{B}_tok_s": round(1000.0 * B / tb, 3)}))
         return
     t0 = time.time()
     eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=1234, max_batch=4)
