@@ -268,6 +268,7 @@ static_assert(kCT >= 2 * kDK, "the q/k conv channels need a thread each");
 // the kCChunks threads of a column sum their rows' products (fixed DPP order)
 __device__ inline float column_sum(float v) { return kCChunks == 8 ? group8_sum(v) : group16_sum(v); }
 constexpr int kMaxAbSlices = 8;
+constexpr int kRing = 5;  // conv / record ring of the engine's T <= 4 steps
 
 struct GdnFusedArgs {
     GdnArgs g;
@@ -359,9 +360,31 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     const bool qk_lane = tid < 2 * kDK;  // thread tid < 256 owns q/k conv channel tid
     const int chan0 = chan_of(qk_lane ? tid : 0), chan1 = chan_of(2 * kDK + (has_v ? tid : 0));
     float win0[K], win1[K], w0[K], w1[K], xin0[kMaxT], xin1[kMaxT];
+    // With a ring of kRing slots the windows of every slot are requested at once and
+    // the current one picked when the slot index has arrived: no dependent memory
+    // round trip before the conv
+    const bool ring_all = cur && p.R == kRing;
     {
-        const float4 a0 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan0) * K);
-        const float4 a1 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan1) * K);
+        float4 a0, a1;
+        if (ring_all) {
+            float4 c0[kRing], c1[kRing];
+#pragma unroll
+            for (int q = 0; q < kRing; ++q) {
+                c0[q] = *reinterpret_cast<const float4*>(conv_base + q * p.conv_slot + static_cast<size_t>(chan0) * K);
+                c1[q] = *reinterpret_cast<const float4*>(conv_base + q * p.conv_slot + static_cast<size_t>(chan1) * K);
+            }
+            a0 = c0[0];
+            a1 = c1[0];
+#pragma unroll
+            for (int q = 1; q < kRing; ++q)
+                if (slot0 == q) {
+                    a0 = c0[q];
+                    a1 = c1[q];
+                }
+        } else {
+            a0 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan0) * K);
+            a1 = *reinterpret_cast<const float4*>(conv_in + static_cast<size_t>(chan1) * K);
+        }
         const float4 b0 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan0) * K);
         const float4 b1 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(chan1) * K);
         win0[0] = a0.x, win0[1] = a0.y, win0[2] = a0.z, win0[3] = a0.w;
@@ -419,7 +442,20 @@ __global__ __launch_bounds__(kCT) void gdn_fused_kernel(GdnFusedArgs a) {
     int* count = records ? a.rec.count + bs * a.batch.count_stride : nullptr;
     const int n_cons = records ? a.rec.n_cons[bs * a.batch.scal_stride] : 0;
     const int rbank = records ? ((slot0 - n_cons) % p.R + p.R) % p.R : 0;
-    const int n_rep = records ? min(min(n_cons, count[rbank * p.nv + h]), kMaxT) : 0;
+    int cnt = 0;
+    if (records && ring_all) {
+        // every bank's count requested together, the bank picked afterwards
+        int cq[kRing];
+#pragma unroll
+        for (int q = 0; q < kRing; ++q) cq[q] = count[q * p.nv + h];
+        cnt = cq[0];
+#pragma unroll
+        for (int q = 1; q < kRing; ++q)
+            if (rbank == q) cnt = cq[q];
+    } else if (records) {
+        cnt = count[rbank * p.nv + h];
+    }
+    const int n_rep = records ? min(min(n_cons, cnt), kMaxT) : 0;
     const size_t rec_t = static_cast<size_t>(p.nv) * kGdnRecFloats;  // token stride
     const size_t bank = static_cast<size_t>(a.rec.max_t) * rec_t;
     const float* rec_r = records ? rec_base + rbank * bank + static_cast<size_t>(h) * kGdnRecFloats : nullptr;
