@@ -530,6 +530,35 @@ class Engine {
         return ms;
     }
 
+    // Graph-replayed time of one layer's launches alone (layer = 0 .. n_layers - 1) or
+    // of the step's head and tail alone (layer = n_layers), T tokens: the layer runs
+    // on whatever its input buffers hold (bench: where a step's time goes under
+    // graph replay, which kernel traces cannot follow).
+    float time_layer(int layer, int T, int iters) {
+        RL_REQUIRE(layer >= 0 && layer <= c_.n_layers && iters >= 1 && T >= 1 && T <= tmax_, RL_ERR_RANGE,
+                   "time_layer: layer in 0..n_layers, T in 1..max_T");
+        RL_REQUIRE(fold_norm_ || kq_fold_, RL_ERR_UNSUPPORTED, "time_layer: folded-norm steps only");
+        struct Reset {
+            int& v;
+            ~Reset() { v = -1; }
+        } reset{only_layer_};
+        only_layer_ = layer;
+        hipEvent_t a, b;
+        RL_HIP(hipEventCreate(&a));
+        RL_HIP(hipEventCreate(&b));
+        const int key = kKeyLayer + layer * 16 + T;
+        launch_captured(key, [&] { step(T, T == 1 ? 1 : 0, false); });  // recorded outside the timing
+        RL_HIP(hipEventRecord(a, st_));
+        for (int i = 0; i < iters; ++i) launch_captured(key, [&] { step(T, T == 1 ? 1 : 0, false); });
+        RL_HIP(hipEventRecord(b, st_));
+        RL_HIP(hipEventSynchronize(b));
+        float ms = 0.f;
+        RL_HIP(hipEventElapsedTime(&ms, a, b));
+        (void)hipEventDestroy(a);
+        (void)hipEventDestroy(b);
+        return ms / static_cast<float>(iters);
+    }
+
     void* stream() const { return st_; }
 
     float time_batch(int B, int iters) {
@@ -538,7 +567,7 @@ class Engine {
         RL_HIP(hipEventCreate(&a));
         RL_HIP(hipEventCreate(&b));
         RL_HIP(hipEventRecord(a, st_));
-        for (int i = 0; i < iters; ++i) launch_captured(200 + B, [&] { batch_groups(B); });
+        for (int i = 0; i < iters; ++i) launch_captured(kKeyBatch + B, [&] { batch_groups(B); });
         RL_HIP(hipEventRecord(b, st_));
         RL_HIP(hipEventSynchronize(b));
         float ms = 0.f;
@@ -575,7 +604,7 @@ class Engine {
         for (int b = 0; b < B; ++b)
             RL_HIP(hipMemcpyAsync(scal_ + b * kScalars + kPos, host_in_ + kMaxSlots + b, sizeof(int), hipMemcpyHostToDevice,
                                   st_));
-        launch_captured(200 + B, [&] { batch_groups(B); });
+        launch_captured(kKeyBatch + B, [&] { batch_groups(B); });
         RL_HIP(hipMemcpyAsync(host_rb_ + kRbPreds, preds_, kMaxSlots * sizeof(int), hipMemcpyDeviceToHost, st_));
         RL_HIP(hipStreamSynchronize(st_));
         batch_rows_ = B;
@@ -696,6 +725,7 @@ class Engine {
 
     RlModelConfig c_;
     int ctx_ = 0, tmax_ = 4, R_ = 5;
+    int only_layer_ = -1;  // bench (time_layer): -1 the whole step, i layer i alone, n_layers head and tail
     int mb_ = 1;    // sequences (slots) for batch decode
     int tcap_ = 4;  // activation rows: max(tmax_, one slot group)
     // Batch slots: up to kMaxSlots; a batch step runs them in groups of at most
@@ -1599,15 +1629,19 @@ class Engine {
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
         float* x = xres_[0];
-        if (feed) copy_int(sc() + kNextTok, tok_, st_);
-        embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, T, st_);
-        rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_x_, H, T, eps, st_);
+        const bool ends = only_layer_ < 0 || only_layer_ >= c_.n_layers;  // head and tail of the step
+        if (ends) {
+            if (feed) copy_int(sc() + kNextTok, tok_, st_);
+            embed_rows(embed_, embed_kind_, tok_, x, H, c_.vocab, T, st_);
+            rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_x_, H, T, eps, st_);
+        }
         NormIO in;
         in.ss_in = ss_;
         in.groups_in = add_norm_groups(H);
         in.n_norm = H;
         in.eps = eps;
         for (int i = 0; i < c_.n_layers; ++i) {
+            if (only_layer_ >= 0 && i != only_layer_) continue;
             Layer& Ly = L_[i];
             const NormIO* io_in = i == 0 ? nullptr : &in;  // layer 0 reads normalised fragments
             NormIO out;
@@ -1659,6 +1693,7 @@ class Engine {
             out.gamma_out = i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_;
             gemm_on(Ly.down, frag_h_, x, H, H, T, kEpiAddNorm, frag_x_, &out);
         }
+        if (!ends) return;
         x_ = x;  // hidden after the layers (pre final norm), for the MTP history
         gemm_on(lm_head_, frag_x_, logits_, c_.vocab, c_.vocab, T, kEpiStore, nullptr, &in);
         argmax_rows(logits_, T, c_.vocab, preds_, nullptr, arg_ws_, st_);
@@ -1692,9 +1727,12 @@ class Engine {
         const int zdim = nv * dv, nq = c_.n_q, nkv = c_.n_kv, hd = c_.head_dim, I = c_.intermediate;
         const float eps = c_.rms_eps;
         float* x = xres_[0];
-        if (feed) copy_int(sc() + kNextTok, tok_, st_);
-        embed_rows(embed_, embed_kind_, tok_ + gb_, x, H, c_.vocab, T, st_);
-        rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_, H, T, eps, st_);
+        const bool ends = only_layer_ < 0 || only_layer_ >= c_.n_layers;  // head and tail of the step
+        if (ends) {
+            if (feed) copy_int(sc() + kNextTok, tok_, st_);
+            embed_rows(embed_, embed_kind_, tok_ + gb_, x, H, c_.vocab, T, st_);
+            rmsnorm_pack(x, H, L_[0].attn_norm, xn_, frag_, H, T, eps, st_);
+        }
         KqNorm kin;
         kin.ss_in = kq_ss_;
         kin.groups_in = kq_groups_;
@@ -1705,7 +1743,7 @@ class Engine {
         io.groups_in = kq_groups_;
         io.n_norm = H;
         io.eps = eps;
-        bool normalised = true;  // xn_ / frag_ hold the normalised rows (layer 0 only)
+        bool normalised = only_layer_ <= 0;  // xn_ / frag_ hold the normalised rows (layer 0 only)
         auto consume = [&](const Lin& L, float* Y, int ldy, int m_valid) {
             if (normalised)
                 linear(L, xn_, Y, ldy, m_valid, T, kEpiStore);
@@ -1831,6 +1869,7 @@ class Engine {
             }
             produce(Ly.down, h_, i + 1 < c_.n_layers ? L_[i + 1].attn_norm : final_norm_);
         }
+        if (!ends) return;
         consume(lm_head_, b_logits(), c_.vocab, c_.vocab);
         argmax_rows(b_logits(), T, c_.vocab, preds_ + gb_, nullptr, arg_ws_, st_);
         if (batch) {
@@ -1968,7 +2007,7 @@ class Engine {
     }
 
     void run_mtp(int n) {
-        launch_captured((mtp_mode_ == RL_MTP_LAYER ? 200 : 100) + n, [&] { mtp_body(n); });
+        launch_captured((mtp_mode_ == RL_MTP_LAYER ? kKeyMtpLayer : kKeyMtpStem) + n, [&] { mtp_body(n); });
     }
 
     // RL_HIP_GRAPHS=0 runs every step eagerly (same kernels, launched one by one):
@@ -1980,6 +2019,9 @@ class Engine {
         }();
         return on;
     }
+
+    // Graph keys: the T-token step is T; each other recording has its own range
+    static constexpr int kKeyMtpStem = 100, kKeyMtpLayer = 200, kKeyBatch = 300, kKeyLayer = 1000;
 
     template <class F>
     void launch_captured(int key, F body) {
@@ -2361,6 +2403,13 @@ int rl_hip_engine_prefill_eq_batch(RlEngine* e, const int32_t* ids, int T, int B
     return guard([&] {
         RL_ENGINE(e);
         e->e->prefill_eq_batch(ids, T, B);
+    });
+}
+int rl_hip_engine_time_layer(RlEngine* e, int layer, int T, int iters, float* ms) {
+    return guard([&] {
+        RL_ENGINE(e);
+        RL_REQUIRE(ms, RL_ERR_RANGE, "time_layer: bad arguments");
+        *ms = e->e->time_layer(layer, T, iters);
     });
 }
 int rl_hip_engine_time_batch(RlEngine* e, int B, int iters, float* ms) {

@@ -87,3 +87,51 @@ def test_mtp_layer_mode_needs_the_layer(gpu, orc):
         eng.set_mtp_mode(MTP_STEM)
     finally:
         eng.close()
+
+
+def test_mtp_layer_drafts_and_batch_steps_keep_their_own_graphs(gpu, orc):
+    """An engine with batch slots and the MTP decoder layer records a 3-draft call
+    and a 3-slot batch step as two different HIP graphs: each replays its own
+    kernels, in either order (drafts against the oracle, batch rows bit-identical
+    to single-sequence decoding)."""
+    spec = mini_spec()
+    W = M.random_weights(spec, seed=34, w_scale=(1e-3, 1e-2))
+    eng = Engine(spec, W, ctx=512, max_batch=4)
+    ref = Engine(spec, W, ctx=512)
+    om = OracleModel(spec, W, ctx=512)
+    prompts = [[1, 2, 3], [7, 7], [5, 9, 11, 2]]
+
+    def plain(p):
+        ref.prefill(p)
+        t0 = ref.greedy()
+        ref.decode_token(t0)
+        return t0, ref.copy_logits()
+
+    def batch_step():
+        eng.zero_slots(3)
+        toks, poss, want = [], [], []
+        for b, p in enumerate(prompts):
+            eng.prefill_slot(p, b)
+            t0, lg = plain(p)
+            toks.append(t0)
+            poss.append(len(p))
+            want.append(lg)
+        eng.decode_tokens(toks, poss)
+        rows = eng.copy_logits_n(3)
+        for b in range(3):
+            assert np.array_equal(rows[b], want[b]), b
+
+    def drafts():
+        g = run_prompt(eng, om, [4, 8, 15, 16])
+        assert eng.mtp_draft(g, 3).tolist() == om.mtp_draft(g, 3).tolist()
+
+    try:
+        eng.set_mtp_mode(MTP_LAYER)
+        om.set_mtp_mode(1)
+        drafts()
+        batch_step()
+        drafts()
+        batch_step()
+    finally:
+        eng.close()
+        ref.close()
