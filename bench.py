@@ -105,6 +105,28 @@ def measure_wide_batch(spec, K, W):
     return out
 
 
+def graph_breakdown(eng, spec, steps, iters=20):
+    """Where the graph-replayed step's time goes: one DeltaNet layer, one attention
+    layer (at the synthetic context), layer 0 (whose input is not a folded norm) and
+    the step's head and tail (embedding, first norm, lm_head, argmax, acceptance),
+    each recorded as a graph of its own launches and replayed `iters` times; their
+    sum over the step's layers against the step itself."""
+    kinds = spec.layer_kinds
+    d = next(i for i in range(1, len(kinds)) if kinds[i] == 0)
+    a = next(i for i in range(1, len(kinds)) if kinds[i] == 1)
+    n_d = sum(1 for k in kinds[1:] if k == 0)
+    n_a = sum(1 for k in kinds[1:] if k == 1)
+    out = {}
+    for T, step_ms in steps.items():
+        eng.time_layer(d, T, 3)
+        us = {name: eng.time_layer(i, T, iters) * 1e3
+              for name, i in (("delta_layer", d), ("attn_layer", a), ("layer0", 0), ("ends", spec.n_layers))}
+        total = us["layer0"] + n_d * us["delta_layer"] + n_a * us["attn_layer"] + us["ends"]
+        out[f"t{T}"] = {**{k + "_us": round(v, 2) for k, v in us.items()},
+                        "layers_sum_ms": round(total / 1e3, 4), "step_ms": round(step_ms, 4)}
+    return out
+
+
 def step_bytes(spec, T, ctx):
     """Algorithmic HBM bytes of one T-token step: every weight byte once, KV read
     once (+ the T new rows written), recurrent state read once and written once per
@@ -765,6 +787,7 @@ def main():
     eng.synthetic_context(CTX)
     eng.time_steps(1, W)
     t1 = eng.time_steps(1, K) / K
+    breakdown = graph_breakdown(eng, spec, {1: t1, 4: t4})
     eng.close()
     gguf = measure_gguf_step(spec, K, W)
     wide = measure_wide_batch(spec, K, W)
@@ -808,6 +831,7 @@ def main():
         "prefill_ms": round(pf_s * 1e3, 1),
         "prefill_tok_s": round(PF_TOKENS / pf_s, 1),
         "prefill_speedup_vs_verify_chunks": round((PF_TOKENS / pf_s) / (4000.0 / t4), 2),
+        "graph_breakdown": breakdown,
         "step_roofline": {"t1_bytes": b1["total"], "t1_GBps": round(b1["total"] / t1 / 1e6, 1),
                           "t1_frac": round(b1["total"] / t1 / 1e6 / PEAK_GBS, 4),
                           "t4_bytes": b4["total"], "t4_GBps": round(b4["total"] / t4 / 1e6, 1),

@@ -30,6 +30,12 @@ RlEngine* rl_hip_engine_create_synthetic(const RlModelConfig* cfg, uint64_t seed
 int rl_hip_engine_set_pos(RlEngine* e, int pos);
 int rl_hip_engine_synthetic_context(RlEngine* e, int n, uint64_t seed);
 int rl_hip_engine_time_steps(RlEngine* e, int T, int iters, int mtp_drafts, float* ms);
+/* Average graph-replayed time (ms) of one layer's launches alone (layer 0 ..
+ * n_layers-1) or of the step's head and tail alone (layer = n_layers: embedding,
+ * first norm, lm_head, argmax, acceptance), T tokens, on whatever the layer's input
+ * buffers hold; folded-norm engines only.  Where a step's time goes under graph
+ * replay, which kernel traces cannot follow.  No counterpart in the reference. */
+int rl_hip_engine_time_layer(RlEngine* e, int layer, int T, int iters, float* ms);
 
 RlEngine* rl_hip_engine_create_synthetic_batch(const RlModelConfig* cfg, uint64_t seed, int ctx, int max_T,
                                                int max_batch, int* status);

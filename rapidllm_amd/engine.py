@@ -139,6 +139,13 @@ class Engine:
         call("rl_hip_engine_time_steps", self.h, T, iters, mtp_drafts, C.byref(ms))
         return ms.value
 
+    def time_layer(self, layer: int, T: int, iters: int) -> float:
+        """Average graph-replayed ms of layer `layer`'s launches alone (n_layers: the
+        step's head and tail alone), T tokens (bench)."""
+        ms = C.c_float()
+        call("rl_hip_engine_time_layer", self.h, layer, T, iters, C.byref(ms))
+        return ms.value
+
     # ---- Session-level generate (session.cpp:687-829 semantics)
     def generate(self, prompt, max_new: int, spec_n: int = 0):
         """Greedy generation; spec_n > 0 uses MTP draft + verify at T = spec_n + 1.

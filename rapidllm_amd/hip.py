@@ -105,6 +105,7 @@ _SIGS = {
     "rl_hip_engine_set_pos": (_i, [_vp, _i]),
     "rl_hip_engine_synthetic_context": (_i, [_vp, _i, C.c_uint64]),
     "rl_hip_engine_time_steps": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
+    "rl_hip_engine_time_layer": (_i, [_vp, _i, _i, _i, C.POINTER(C.c_float)]),
     "rl_hip_engine_stream": (_vp, [_vp]),
     "rl_hip_engine_create_batch": (_vp, [_vp, _vp, _i, _i, _i, _i, C.POINTER(_i)]),
     "rl_hip_engine_create_synthetic_batch": (_vp, [_vp, C.c_uint64, _i, _i, _i, C.POINTER(_i)]),
