@@ -55,7 +55,7 @@ def measure_gguf_step(spec, K, W):
     eng.synthetic_context(CTX)
     eng.time_steps(4, W)
     t4 = eng.time_steps(4, K) / K
-    # prompt prefill through the chunked path (K-quant linears as BF16 hi + lo tiles)
+    # prompt prefill through the chunked path (K-quant linears as fp16 tiles, block-scaled)
     ids = np.random.default_rng(3).integers(0, spec.vocab, PF_TOKENS).astype(np.int32)
     eng.prefill(ids[:600])
     tp = time.perf_counter()

@@ -130,6 +130,19 @@ int rl_hip_gemm_bf16_prefill(const uint16_t* w_tiled, const uint16_t* w_lo_tiled
  * its top 16 bits (hi) and the top 16 bits of the remainder (lo). */
 int rl_hip_kquant_to_bf16x2(int type, const uint8_t* tiled, uint16_t* w_hi, uint16_t* w_lo, int m, int n,
                             void* stream);
+/* The K-quant prefill linears' form: a tiled Q4_K / Q6_K matrix as fp16 tiles in
+ * the BF16 tile layout (w16: 2 bytes per weight), each weight dequantised exactly,
+ * divided by its (16-row tile, 128-column block)'s power-of-two scale tile_scale
+ * [m/16][n/128] (which puts the block's largest |w| in [2^14, 2^15)) and rounded to
+ * fp16 (11 significant bits). */
+int rl_hip_kquant_to_f16(int type, const uint8_t* tiled, void* w16, float* tile_scale, int m, int n, void* stream);
+/* rl_hip_pack_act fragments (bf16 hi + mid) -> fp16 hi + lo fragments of
+ * x / xscale, xscale [n/128][T] a power of two per (128-column block, token). */
+int rl_hip_act_frag_to_f16(const void* frag, void* frag16, float* xscale, int n, int T, void* stream);
+/* Prompt prefill over fp16 tiles: Y[t][ldy] (=, +=, SwiGLU) sum over blocks of
+ * tile_scale * xscale * (W16 . x16) (two fp16 MFMAs per step, hi and lo of x). */
+int rl_hip_gemm_f16_prefill(const void* w16, const float* tile_scale, const void* frag16, const float* xscale,
+                            float* Y, int m, int n, int T, int epilogue, int ldy, void* stream);
 
 int rl_hip_gemm_fp8_frag(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                          int T, int accumulate, void* stream);

@@ -224,6 +224,12 @@ class Engine {
     float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr, *pf_xc_ = nullptr,
           *pf_gates_ = nullptr;
     void *pf_frag_ = nullptr, *pf_frag_h_ = nullptr, *pf_attn_ws_ = nullptr;
+    // K-quant prefill (fp16 form): the tiles' block scales, the input converted to
+    // fp16 hi + lo fragments and its block scales, and which fragments that input is
+    float* pf_ts_ = nullptr;
+    void* pf_frag16_ = nullptr;
+    float* pf_xs_ = nullptr;
+    const void* pf_f16_src_ = nullptr;
     size_t pf_attn_ws_bytes_ = 0;
     int* pf_pos_ = nullptr;
     uint16_t *pf_whi_ = nullptr, *pf_wlo_ = nullptr;  // a K-quant linear as BF16 hi + lo tiles
@@ -283,11 +289,30 @@ class Engine {
             gemm_prefill_any(0, L.w, nullptr, L.ts, frag, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
         } else if (L.kind == RL_Q_BF16) {
             gemm_prefill_any(1, L.w, nullptr, nullptr, frag, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
+        } else if (kq_f16()) {
+            // fp16 tiles with a power-of-two scale per block, the input fragments as
+            // fp16 hi + lo (converted once per input: the cache is cleared whenever a
+            // producer writes the fragments)
+            if (frag != pf_f16_src_) {
+                act_frag_to_f16(frag, pf_frag16_, pf_xs_, L.n, T, st_);
+                pf_f16_src_ = frag;
+            }
+            kq_to_f16(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, pf_whi_, pf_ts_, L.m, L.n, st_);
+            gemm_prefill_any(3, reinterpret_cast<const uint8_t*>(pf_whi_), nullptr, pf_ts_, pf_frag16_, Y, L.m, L.n, T,
+                             epi, ldy, m_valid, st_, pf_xs_);
         } else {
             kq_to_bf16x2(L.kind == RL_Q_Q4_K ? 4 : 6, L.w, pf_whi_, pf_wlo_, L.m, L.n, st_);
             gemm_prefill_any(2, reinterpret_cast<const uint8_t*>(pf_whi_), reinterpret_cast<const uint8_t*>(pf_wlo_),
                              nullptr, frag, Y, L.m, L.n, T, epi, ldy, m_valid, st_);
         }
+    }
+    // K-quant prefill linears as fp16 tiles (RL_PF_KQ16=0: the BF16 hi + lo tiles)
+    static bool kq_f16() {
+        static const bool on = [] {
+            const char* v = std::getenv("RL_PF_KQ16");
+            return !(v && v[0] == '0');
+        }();
+        return on;
     }
     void pf_parts(const std::vector<Lin>& parts, const std::vector<int>& offs, float* Y, int ldy, int T) {
         for (size_t k = 0; k < parts.size(); ++k) pf_linear(parts[k], pf_frag_, Y + offs[k], ldy, parts[k].m, T, kEpiStore);
@@ -318,9 +343,17 @@ class Engine {
         const size_t kqe = kq_prefill_elems();
         if (kqe) {
             pf_whi_ = pf_mem_->get_n<uint16_t>(kqe);
-            pf_wlo_ = pf_mem_->get_n<uint16_t>(kqe);
+            if (kq_f16()) {
+                const int wmax = std::max(wf, I);
+                pf_ts_ = pf_mem_->get_n<float>(kqe / 2048 + 1);  // one per 16 x 128 block
+                pf_frag16_ = pf_mem_->get(act_frag_bytes(wmax, C));
+                pf_xs_ = pf_mem_->get_n<float>(static_cast<size_t>((wmax + 127) / 128) * C);
+            } else {
+                pf_wlo_ = pf_mem_->get_n<uint16_t>(kqe);
+            }
             pf_u_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * I);
         }
+        pf_f16_src_ = nullptr;
         pf_cap_ = C;
     }
 
@@ -343,6 +376,7 @@ class Engine {
             for (int i = 0; i < c_.n_layers; ++i) {
                 Layer& Ly = L_[i];
                 rmsnorm_pack(pf_x_, H, Ly.attn_norm, nullptr, pf_frag_, H, T, eps, st_);
+                pf_f16_src_ = nullptr;
                 if (Ly.kind == RL_LAYER_DELTA) {
                     pf_parts(Ly.in_parts, Ly.in_offs, pf_y_, Ly.in_width, T);
                     float* ring = slot_conv(Ly.dslot);
@@ -351,6 +385,7 @@ class Engine {
                                 slot_S(Ly.dslot), pf_o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
                     gnorm_pack(pf_o_, pf_y_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, nullptr, pf_frag_, zdim, T,
                                1e-6f, st_);
+                    pf_f16_src_ = nullptr;
                     pf_linear(Ly.out_proj, pf_frag_, pf_x_, H, H, T, kEpiAdd);
                 } else {
                     pf_parts(Ly.qkv_parts, Ly.qkv_offs, pf_y_, Ly.qkv_width, T);
@@ -358,9 +393,11 @@ class Engine {
                                        ctx_, pf_pos_, T, nq, nkv, hd, c_.rotary_dim, c_.rope_theta, eps, pf_attn_ws_,
                                        pf_attn_ws_bytes_, pf_o_, st_);
                     pack_act(pf_o_, pf_frag_, nq * hd, T, st_);
+                    pf_f16_src_ = nullptr;
                     pf_linear(Ly.o_proj, pf_frag_, pf_x_, H, H, T, kEpiAdd);
                 }
                 rmsnorm_pack(pf_x_, H, Ly.ffn_norm, nullptr, pf_frag_, H, T, eps, st_);
+                pf_f16_src_ = nullptr;
                 if (Ly.gate_up.kind >= 0) {
                     pf_linear(Ly.gate_up, pf_frag_, pf_h_, I, I, T, Ly.gate_up.swiglu_epi());
                 } else if (Ly.gate_cat) {
@@ -371,6 +408,7 @@ class Engine {
                     swiglu(pf_h_, I, pf_u_, I, pf_h_, I, T, st_);
                 }
                 pack_act(pf_h_, pf_frag_h_, I, T, st_);
+                pf_f16_src_ = nullptr;
                 pf_linear(Ly.down, pf_frag_h_, pf_x_, H, H, T, kEpiAdd);
             }
             slot ^= 1;

@@ -58,9 +58,15 @@ int gemm_store_waves();
 // (interleaved gate/up tiles, m_valid = m/2 output rows).  frag: act fragments of T.
 // wk 0: FP8 tiles (ts); 1: BF16 tiles; 2: BF16 W + W_lo tiles (16 significant bits)
 void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float* ts, const void* frag, float* Y,
-                      int m, int n, int T, int epi, int ldy, int m_valid, hipStream_t s);
+                      int m, int n, int T, int epi, int ldy, int m_valid, hipStream_t s, const float* xscale = nullptr);
 // K-quant tiles (qt 4 / 6, m rows in 16-row tiles) -> BF16 tiles hi and lo
 void kq_to_bf16x2(int qt, const uint8_t* tiled, uint16_t* hi, uint16_t* lo, int m, int n, hipStream_t s);
+// K-quant tiles -> fp16 in the BF16 tile layout, one power-of-two scale per (16-row
+// tile, 128-column block) in tscale[m_tiles][n / 128]
+void kq_to_f16(int qt, const uint8_t* tiled, void* w16, float* tscale, int m, int n, hipStream_t s);
+// bf16 hi + mid activation fragments (T tokens, n columns) -> fp16 hi + lo fragments
+// of x / xscale[kb][t], xscale a power of two per (128-column block, token)
+void act_frag_to_f16(const void* frag, void* frag16, float* xscale, int n, int T, hipStream_t s);
 void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
                       int ldy, int m_valid, hipStream_t s);
 int device_cus();  // CUs of the current device

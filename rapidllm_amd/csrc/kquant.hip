@@ -712,26 +712,15 @@ __global__ void q6k_dequant_kernel(const uint8_t* __restrict__ src, float* __res
     }
 }
 
-// Tiled K-quant -> BF16 tiles hi + lo (the gemm.hip BF16 tile: 16 rows x 128
-// columns, unit (chunk q, lane (row, g)) = columns 32 g + 8 q .. + 8).  One thread
-// per (row tile, super-block, row, 8 columns): the eight weights dequantised with
-// the reference's operation order (q4k_dequant_kernel / q6k_dequant_kernel), each
-// split into its top 16 bits and the top 16 bits of the remainder.
+// Eight consecutive weights of row r16 of a K-quant tile row, columns c0 .. c0 + 7
+// of super-block tile `tile` (c0 a multiple of 8), dequantised with the reference's
+// operation order (q4k_dequant_kernel / q6k_dequant_kernel: separate products and
+// difference, no contraction).
 template <int QT>
-__global__ void kq_to_bf16x2_kernel(const uint8_t* __restrict__ tiled, uint16_t* __restrict__ hi,
-                                    uint16_t* __restrict__ lo, int m_tiles, int nsb) {
+__device__ inline void kq_dequant8(const uint8_t* __restrict__ tile, int r16, int c0, float (&w)[8]) {
 #pragma clang fp contract(off)
     using F = KFmt<QT>;
-    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rt, sb, u, r16)
-    if (idx >= static_cast<size_t>(m_tiles) * nsb * 32 * 16) return;
-    const int r16 = idx & 15;
-    const int u = (idx >> 4) & 31;  // 8-column group of the super-block
-    const int sb = static_cast<int>((idx >> 9) % nsb);
-    const int rt = static_cast<int>((idx >> 9) / nsb);
-    const uint8_t* tile = tiled + (static_cast<size_t>(rt) * nsb + sb) * F::kTileBytes;
     const uint8_t* hdr = tile + F::kHdr + 16 * r16;
-    const int c0 = 8 * u;  // first column within the super-block
-    float w[8];
     if constexpr (QT == 4) {
         const int g64 = c0 / 64, high = (c0 % 64) >= 32, l0 = c0 % 32;
         const uint8_t* qs = tile + (l0 / 16) * 1024 + 16 * (r16 + 16 * g64) + (l0 % 16);
@@ -760,6 +749,27 @@ __global__ void kq_to_bf16x2_kernel(const uint8_t* __restrict__ tiled, uint16_t*
             w[e] = __fmul_rn(a, static_cast<float>(v));
         }
     }
+}
+
+// Tiled K-quant -> BF16 tiles hi + lo (the gemm.hip BF16 tile: 16 rows x 128
+// columns, unit (chunk q, lane (row, g)) = columns 32 g + 8 q .. + 8).  One thread
+// per (row tile, super-block, row, 8 columns): the eight weights dequantised
+// (kq_dequant8), each split into its top 16 bits and the top 16 bits of the
+// remainder.
+template <int QT>
+__global__ void kq_to_bf16x2_kernel(const uint8_t* __restrict__ tiled, uint16_t* __restrict__ hi,
+                                    uint16_t* __restrict__ lo, int m_tiles, int nsb) {
+    using F = KFmt<QT>;
+    const size_t idx = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;  // (rt, sb, u, r16)
+    if (idx >= static_cast<size_t>(m_tiles) * nsb * 32 * 16) return;
+    const int r16 = idx & 15;
+    const int u = (idx >> 4) & 31;  // 8-column group of the super-block
+    const int sb = static_cast<int>((idx >> 9) % nsb);
+    const int rt = static_cast<int>((idx >> 9) / nsb);
+    const uint8_t* tile = tiled + (static_cast<size_t>(rt) * nsb + sb) * F::kTileBytes;
+    const int c0 = 8 * u;  // first column within the super-block
+    float w[8];
+    kq_dequant8<QT>(tile, r16, c0, w);
     // BF16 tile (rt, kb) and its unit for columns j .. j + 7 of the 128-column block
     const int kb = 2 * sb + c0 / 128, j = c0 % 128;
     const int g = j / 32, q = (j % 32) / 8;
@@ -772,6 +782,50 @@ __global__ void kq_to_bf16x2_kernel(const uint8_t* __restrict__ tiled, uint16_t*
     for (int e = 0; e < 8; ++e) split_bf16(w[e], H.h[e], L.h[e]);
     *reinterpret_cast<i32x4*>(hi + unit) = H.v;
     *reinterpret_cast<i32x4*>(lo + unit) = L.v;
+}
+
+// Power of two s with max / s in [2^14, 2^15) (1 for max = 0): values scaled by 1/s
+// keep fp16's full precision and range.
+__device__ inline float f16_block_scale(float mx) {
+    if (!(mx > 0.f)) return 1.f;
+    int e;
+    frexpf(mx, &e);  // mx = f * 2^e, f in [0.5, 1)
+    return ldexpf(1.f, e - 15);
+}
+
+// Tiled K-quant -> fp16 tiles in the BF16 tile layout, one power-of-two scale per
+// (16-row tile, 128-column block): workgroup = one (row tile, block), thread =
+// (row, 8 columns).  Each weight is dequantised exactly (kq_dequant8), divided by
+// the block's scale (exact) and rounded to fp16 (nearest even): 11 significant bits.
+template <int QT>
+__global__ __launch_bounds__(256) void kq_to_f16_kernel(const uint8_t* __restrict__ tiled, _Float16* __restrict__ w16,
+                                                        float* __restrict__ tscale, int nsb) {
+    using F = KFmt<QT>;
+    const int rt = blockIdx.x, kb = blockIdx.y, n_kb = 2 * nsb;
+    const int tid = threadIdx.x, r16 = tid & 15, u = tid >> 4;  // 8-column group u of the block
+    const int sb = kb >> 1, c0 = (kb & 1) * 128 + 8 * u;
+    const uint8_t* tile = tiled + (static_cast<size_t>(rt) * nsb + sb) * F::kTileBytes;
+    float w[8];
+    kq_dequant8<QT>(tile, r16, c0, w);
+    float mx = 0.f;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(w[e]));
+    mx = wave_max(mx);
+    __shared__ float wmax[4];
+    if ((tid & 63) == 0) wmax[tid >> 6] = mx;
+    __syncthreads();
+    const float s = f16_block_scale(fmaxf(fmaxf(wmax[0], wmax[1]), fmaxf(wmax[2], wmax[3])));
+    const float inv = 1.f / s;  // a power of two: exact
+    const int j = 8 * u, g = j / 32, q = (j % 32) / 8;
+    const size_t unit = (static_cast<size_t>(rt) * n_kb + kb) * 2048 + q * 512 + 8 * (r16 + 16 * g);
+    union {
+        _Float16 h[8];
+        i32x4 v;
+    } H;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) H.h[e] = static_cast<_Float16>(w[e] * inv);
+    *reinterpret_cast<i32x4*>(w16 + unit) = H.v;
+    if (tid == 0) tscale[static_cast<size_t>(rt) * n_kb + kb] = s;
 }
 
 size_t kq_tiled_bytes(int qt, int m, int n) {
@@ -869,6 +923,19 @@ void kq_to_bf16x2(int qt, const uint8_t* tiled, uint16_t* hi, uint16_t* lo, int 
     check_launch("kq_to_bf16x2_kernel");
 }
 
+
+void kq_to_f16(int qt, const uint8_t* tiled, void* w16, float* tscale, int m, int n, hipStream_t s) {
+    RL_REQUIRE((qt == 4 || qt == 6) && m > 0 && n > 0 && n % 256 == 0 && tiled && w16 && tscale, RL_ERR_RANGE,
+               "kquant_to_f16: Q4_K / Q6_K, n a multiple of 256");
+    const int m_tiles = (m + kTR - 1) / kTR, nsb = n / 256;
+    const dim3 grid(m_tiles, 2 * nsb);
+    _Float16* w = static_cast<_Float16*>(w16);
+    if (qt == 4)
+        hipLaunchKernelGGL(kq_to_f16_kernel<4>, grid, dim3(256), 0, s, tiled, w, tscale, nsb);
+    else
+        hipLaunchKernelGGL(kq_to_f16_kernel<6>, grid, dim3(256), 0, s, tiled, w, tscale, nsb);
+    check_launch("kq_to_f16_kernel");
+}
 
 size_t kq_workspace_bytes(int m, int n, int T) {
     // split-K tickets, then the partials of the split: S*T*m floats
@@ -1065,6 +1132,13 @@ int rl_hip_kquant_to_bf16x2(int type, const uint8_t* tiled, uint16_t* w_hi, uint
     return guard([&] {
         RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "kquant_to_bf16x2: Q4_K or Q6_K");
         rl::kq_to_bf16x2(type == RL_Q_Q4_K ? 4 : 6, tiled, w_hi, w_lo, m, n, S(stream));
+    });
+}
+
+int rl_hip_kquant_to_f16(int type, const uint8_t* tiled, void* w16, float* tile_scale, int m, int n, void* stream) {
+    return guard([&] {
+        RL_REQUIRE(type == RL_Q_Q4_K || type == RL_Q_Q6_K, RL_ERR_UNSUPPORTED, "kquant_to_f16: Q4_K or Q6_K");
+        rl::kq_to_f16(type == RL_Q_Q4_K ? 4 : 6, tiled, w16, tile_scale, m, n, S(stream));
     });
 }
 

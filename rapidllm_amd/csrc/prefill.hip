@@ -31,8 +31,11 @@ constexpr int kTileRows = 16;
 
 typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
 
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
 union Frag8 {
     bf16x8 v;
+    f16x8 h;
     uint32_t u[4];
     i32x4 i;
 };
@@ -52,17 +55,21 @@ __device__ inline float silu_f(float x) { return x / (1.f + __expf(-x)); }
 // [tile][kb][2]).
 // WK: the weight tiles.  0: block-FP8 (2 KiB tiles, tile scales).  1: BF16 (4 KiB
 // tiles of the decode GEMM's BF16 layout, no scales).  2: two BF16 matrices W_hi +
-// W_lo (a weight split into 16 significant bits, as the K-quant linears are
-// dequantised for prefill): three MFMAs per step, hi.x_hi + hi.x_mid + lo.x_hi.
-// RT row tiles per workgroup: 8 for FP8, 4 for BF16 (the same 16 KiB, or 32 KiB
-// for hi + lo, of weights staged per column block).
+// W_lo (a weight split into 16 significant bits): three MFMAs per step,
+// hi.x_hi + hi.x_mid + lo.x_hi.  3: fp16 tiles in the BF16 layout with one
+// power-of-two scale per (tile, column block) (the K-quant linears as dequantised
+// for prefill), activations as fp16 hi + lo fragments with one power-of-two scale
+// per (column block, token): two fp16 MFMAs per step.
+// RT row tiles per workgroup: 8 for FP8, 4 for BF16 and fp16 (the same 16 KiB of
+// weights staged per column block; 32 KiB for hi + lo).
 template <int EPI, int WK = 0>
 __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __restrict__ W,
                                                            const float* __restrict__ tscale,
                                                            const i32x4* __restrict__ frag, float* __restrict__ Y,
                                                            int m, int n_kb, int T, int ldy, int m_valid,
-                                                           const uint8_t* __restrict__ W_lo = nullptr) {
-    constexpr int kPfRT = WK == 0 ? 8 : 4;          // row tiles per workgroup
+                                                           const uint8_t* __restrict__ W_lo = nullptr,
+                                                           const float* __restrict__ xscale = nullptr) {
+    constexpr int kPfRT = WK == 0 ? 8 : 4;  // row tiles per workgroup (fp16 at 8: one wave per SIMD, slower)
     constexpr int kCh = WK == 0 ? 2 : 4;            // 16-B chunks per lane per tile
     constexpr int kTileB = WK == 0 ? 2048 : 4096;   // bytes per tile
     constexpr int kMat = WK == 2 ? 2 : 1;           // weight matrices staged
@@ -116,8 +123,14 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
     for (int kb = 0; kb < n_kb; ++kb) {
         const int buf = kb & 1;
         if (kb + 1 < n_kb) stage_load(kb + 1);
-        // activation fragments of this lane's token: 4 k-steps x (hi, mid)
+        // activation fragments of this lane's token: 4 k-steps x (hi, mid); WK 3: the
+        // fp16 hi / lo fragments and the token's block scale
         i32x4 bh[kPfNT][4], bm[kPfNT][4];
+        float xs[kPfNT];
+        if constexpr (WK == 3) {
+#pragma unroll
+            for (int nt = 0; nt < kPfNT; ++nt) xs[nt] = xscale[static_cast<size_t>(kb) * T + tokcv[nt]];
+        }
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt)
 #pragma unroll
@@ -144,10 +157,17 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
                 }
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) {
-                    b.i = bh[nt][i];
-                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
-                    b.i = bm[nt][i];
-                    acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
+                    if constexpr (WK == 3) {
+                        b.i = bh[nt][i];
+                        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, b.h, acc[nt], 0, 0, 0);
+                        b.i = bm[nt][i];
+                        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_f16(a.h, b.h, acc[nt], 0, 0, 0);
+                    } else {
+                        b.i = bh[nt][i];
+                        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
+                        b.i = bm[nt][i];
+                        acc[nt] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(a.v, b.v, acc[nt], 0, 0, 0);
+                    }
                 }
                 if constexpr (WK == 2) {
                     a.i = wl[buf][1][r][i][lane];
@@ -164,6 +184,10 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
                                           : tscale[static_cast<size_t>(rt) * n_kb + kb];
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += sc * acc[nt];
+            } else if constexpr (WK == 3) {
+                const float sc = tscale[static_cast<size_t>(rt) * n_kb + kb];
+#pragma unroll
+                for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += (sc * xs[nt]) * acc[nt];
             } else {
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += acc[nt];
@@ -218,15 +242,67 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
     }
 }
 
+
+// bf16 hi + mid activation fragments -> fp16 hi + lo fragments, one thread per
+// (128-column block kb, token t): x = hi + mid (exact, 16 significant bits), scaled
+// by a power of two xscale[kb][t] that puts the block's largest |x| in
+// [2^14, 2^15), then split into fp16 hi = rn(x / s) and lo = rn(x / s - hi), which
+// together hold every bit of x.  Same layout as the input (units (kb, i, g): hi in
+// column t, lo in column T + t).
+__global__ void act_frag_to_f16_kernel(const i32x4* __restrict__ frag, i32x4* __restrict__ out,
+                                       float* __restrict__ xscale, int n_kb, int T) {
+    const int idx = blockIdx.x * blockDim.x + threadIdx.x;
+    if (idx >= n_kb * T) return;
+    const int t = idx % T, kb = idx / T;
+    const size_t NC = 2 * static_cast<size_t>(T);
+    auto unit = [&](int gi) { return (static_cast<size_t>(kb) * 16 + gi) * NC + t; };
+    auto value = [&](const Frag8& h, const Frag8& md, int e) {
+        const uint32_t hb = (h.u[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        const uint32_t mb = (md.u[e >> 1] >> (16 * (e & 1))) & 0xffffu;
+        return __uint_as_float(hb << 16) + __uint_as_float(mb << 16);
+    };
+    float mx = 0.f;
+    for (int gi = 0; gi < 16; ++gi) {
+        Frag8 h, md;
+        h.i = frag[unit(gi)];
+        md.i = frag[unit(gi) + T];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) mx = fmaxf(mx, fabsf(value(h, md, e)));
+    }
+    float sc = 1.f;
+    if (mx > 0.f) {
+        int ex;
+        frexpf(mx, &ex);
+        sc = ldexpf(1.f, ex - 15);
+    }
+    const float inv = 1.f / sc;
+    for (int gi = 0; gi < 16; ++gi) {
+        Frag8 h, md, oh, ol;
+        h.i = frag[unit(gi)];
+        md.i = frag[unit(gi) + T];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            const float v = value(h, md, e) * inv;
+            const _Float16 vh = static_cast<_Float16>(v);
+            oh.h[e] = vh;
+            ol.h[e] = static_cast<_Float16>(v - static_cast<float>(vh));
+        }
+        out[unit(gi)] = oh.i;
+        out[unit(gi) + T] = ol.i;
+    }
+    xscale[static_cast<size_t>(kb) * T + t] = sc;
+}
+
 }  // namespace
 
 namespace rl {
 
 void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float* ts, const void* frag, float* Y,
-                      int m, int n, int T, int epi, int ldy, int m_valid, hipStream_t s) {
+                      int m, int n, int T, int epi, int ldy, int m_valid, hipStream_t s, const float* xscale) {
     RL_REQUIRE(m > 0 && n > 0 && T >= 1, RL_ERR_RANGE, "gemm_prefill: empty shape");
-    RL_REQUIRE(W && frag && Y && (wk != 0 || ts) && (wk != 2 || W_lo), RL_ERR_RANGE, "gemm_prefill: null pointer");
-    RL_REQUIRE(wk >= 0 && wk <= 2, RL_ERR_RANGE, "gemm_prefill: weight kind");
+    RL_REQUIRE(W && frag && Y && ((wk != 0 && wk != 3) || ts) && (wk != 2 || W_lo) && (wk != 3 || xscale),
+               RL_ERR_RANGE, "gemm_prefill: null pointer");
+    RL_REQUIRE(wk >= 0 && wk <= 3, RL_ERR_RANGE, "gemm_prefill: weight kind");
     RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU || epi == kEpiSwiGLUH, RL_ERR_RANGE,
                "gemm_prefill: epilogue must be store, add or swiglu");
     if (epi == kEpiSwiGLUH) RL_REQUIRE(m % 16 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows a multiple of 16");
@@ -240,14 +316,25 @@ void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float
 #define RL_PF(E, K)                                                                                                 \
     if (epi == E && wk == K) {                                                                                      \
         hipLaunchKernelGGL((gemm_prefill_kernel<E == kEpiSwiGLUH ? 5 : E, K>), grid, dim3(256), 0, s, W, ts, fr, Y, m, \
-                           n_kb, T, ldy, m_valid, W_lo);                                                            \
+                           n_kb, T, ldy, m_valid, W_lo, xscale);                                                    \
         check_launch("gemm_prefill_kernel");                                                                        \
         return;                                                                                                     \
     }
     RL_PF(kEpiStore, 0) RL_PF(kEpiAdd, 0) RL_PF(kEpiSwiGLU, 0) RL_PF(kEpiSwiGLUH, 0)
     RL_PF(kEpiStore, 1) RL_PF(kEpiAdd, 1) RL_PF(kEpiSwiGLU, 1) RL_PF(kEpiSwiGLUH, 1)
     RL_PF(kEpiStore, 2) RL_PF(kEpiAdd, 2) RL_PF(kEpiSwiGLU, 2) RL_PF(kEpiSwiGLUH, 2)
+    RL_PF(kEpiStore, 3) RL_PF(kEpiAdd, 3) RL_PF(kEpiSwiGLU, 3) RL_PF(kEpiSwiGLUH, 3)
 #undef RL_PF
+}
+
+void act_frag_to_f16(const void* frag, void* frag16, float* xscale, int n, int T, hipStream_t s) {
+    RL_REQUIRE(frag && frag16 && xscale && n > 0 && T >= 1 && frag != frag16, RL_ERR_RANGE,
+               "act_frag_to_f16: bad arguments");
+    const int n_kb = (n + 127) / 128;
+    const int total = n_kb * T;
+    hipLaunchKernelGGL(act_frag_to_f16_kernel, dim3((total + 255) / 256), dim3(256), 0, s,
+                       static_cast<const i32x4*>(frag), static_cast<i32x4*>(frag16), xscale, n_kb, T);
+    check_launch("act_frag_to_f16_kernel");
 }
 
 void gemm_fp8_prefill(const uint8_t* W, const float* ts, const void* frag, float* Y, int m, int n, int T, int epi,
@@ -274,6 +361,19 @@ int rl_hip_gemm_bf16_prefill(const uint16_t* w_tiled, const uint16_t* w_lo_tiled
         rl::gemm_prefill_any(w_lo_tiled ? 2 : 1, reinterpret_cast<const uint8_t*>(w_tiled),
                              reinterpret_cast<const uint8_t*>(w_lo_tiled), nullptr, frag, Y, m, n, T, epilogue,
                              ldy > 0 ? ldy : mv, mv, S(stream));
+    });
+}
+
+int rl_hip_act_frag_to_f16(const void* frag, void* frag16, float* xscale, int n, int T, void* stream) {
+    return guard([&] { rl::act_frag_to_f16(frag, frag16, xscale, n, T, S(stream)); });
+}
+
+int rl_hip_gemm_f16_prefill(const void* w16, const float* tile_scale, const void* frag16, const float* xscale,
+                            float* Y, int m, int n, int T, int epilogue, int ldy, void* stream) {
+    return guard([&] {
+        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
+        rl::gemm_prefill_any(3, static_cast<const uint8_t*>(w16), nullptr, tile_scale, frag16, Y, m, n, T, epilogue,
+                             ldy > 0 ? ldy : mv, mv, S(stream), xscale);
     });
 }
 

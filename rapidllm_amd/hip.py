@@ -135,6 +135,9 @@ _SIGS = {
     "rl_hip_gemm_fp8_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "rl_hip_gemm_bf16_prefill": (_i, [_vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "rl_hip_kquant_to_bf16x2": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_kquant_to_f16": (_i, [_i, _vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_act_frag_to_f16": (_i, [_vp, _vp, _vp, _i, _i, _vp]),
+    "rl_hip_gemm_f16_prefill": (_i, [_vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _vp]),
     "rl_hip_time_gemm_kquant": (_i, [_i, _vp, _i, _vp, _vp, _vp, _sz, _i, _i, _i, _i, _vp, C.POINTER(C.c_float)]),
     "rl_hip_time_gdn": (_i, [_vp, _i, _vp, _vp, _vp, _i, _vp, _vp, _vp, _vp, _vp, _vp, _i, _i, _i, _i, _i, _i, _i,
                              _i, _vp, C.POINTER(C.c_float)]),

@@ -239,6 +239,78 @@ def test_kquant_prefill_gemm_vs_oracle(gpu, orc, qt, m, n, T):
         assert rel_l2(got[t], want) <= REL_L2, (t, rel_l2(got[t], want))
 
 
+def _f16_to_f32(bits):
+    return np.asarray(bits, np.uint16).view(np.float16).astype(np.float32)
+
+
+@pytest.mark.parametrize("qt,m,n,T,epi", [(ops.Q4_K, 256, 1024, 70, 0), (ops.Q6_K, 160, 768, 130, 1),
+                                          (ops.Q4_K, 5120, 4096, 300, 0), (ops.Q6_K, 512, 1280, 64, 5)])
+def test_kquant_f16_prefill_gemm_vs_oracle(gpu, orc, qt, m, n, T, epi):
+    """The K-quant prefill linears' fp16 form: rl_hip_kquant_to_f16 stores each
+    weight of a (16-row tile, 128-column block) as rn16(w / s) with a power-of-two s
+    per block (checked against ops::dequant_q4_k / dequant_q6_k to fp16 rounding);
+    rl_hip_act_frag_to_f16 turns the bf16 hi + mid fragments into fp16 hi + lo of
+    x / xscale without losing a bit; the fp16 prefill GEMM (store, add, and SwiGLU
+    over half tiles) matches the oracle's K-quant GEMV per token."""
+    from rapidllm_amd.hip import DeviceBuffer, call
+    r = synth.rng(800 + m + T)
+    blocks = synth.q4k_blocks(r, m, n) if qt == ops.Q4_K else synth.q6k_blocks(r, m, n)
+    lin = ops.KQuantLinear(qt, blocks, m, n)
+    mt, nkb = (m + 15) // 16, n // 128
+    w16 = DeviceBuffer(mt * 16 * n * 2)
+    ts = DeviceBuffer(4 * mt * nkb)
+    call("rl_hip_kquant_to_f16", qt, lin.w.ptr, w16.ptr, ts.ptr, m, n, None)
+    deq = orc.dequant_q4_k if qt == ops.Q4_K else orc.dequant_q6_k
+    Wd = deq(np.ascontiguousarray(blocks.reshape(-1)), m * n).reshape(m, n)
+    h = _f16_to_f32(w16.numpy(np.uint16, (mt * 16 * n,)))
+    sc = ts.numpy(np.float32, (mt, nkb))
+    for rt in (0, mt - 1):
+        for kb in (0, nkb - 1):
+            blk = np.abs(Wd[16 * rt:16 * rt + 16, 128 * kb:128 * kb + 128])
+            s = sc[rt, kb]
+            mx = blk.max()
+            assert s > 0 and (mx == 0 or 2.0 ** 14 <= mx / s < 2.0 ** 15), (rt, kb, s, mx)
+            assert s == 2.0 ** np.round(np.log2(s))  # a power of two
+    for row in (0, 5, 15, 16 * (mt - 1) + 3):
+        for c in (0, 37, 128, n - 1):
+            rt, kb, j = row // 16, c // 128, c % 128
+            g, q, e = j // 32, (j % 32) // 8, j % 8
+            i = (rt * nkb + kb) * 2048 + q * 512 + 8 * (row % 16 + 16 * g) + e
+            w = np.float32(h[i]) * sc[rt, kb]
+            want = np.float32(Wd[row, c] / sc[rt, kb]).astype(np.float16).astype(np.float32) * sc[rt, kb]
+            assert w == want, (row, c, w, Wd[row, c])
+    X = (r.standard_normal((T, n)) * np.exp(r.uniform(-6, 6, (T, 1)))).astype(np.float32)
+    xd = DeviceBuffer.from_numpy(X)
+    frag = ops.act_frag_buffer(n, T)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
+    frag16 = ops.act_frag_buffer(n, T)
+    xs = DeviceBuffer(4 * nkb * T)
+    call("rl_hip_act_frag_to_f16", frag.ptr, frag16.ptr, xs.ptr, n, T, None)
+    # hi + lo (fp16) times the scale equals hi + mid (bf16) exactly, unit by unit
+    fb = frag.numpy(np.uint16, (frag.nbytes // 2,)).reshape(nkb * 16, 2 * T, 8)
+    f16 = frag16.numpy(np.uint16, (frag16.nbytes // 2,)).reshape(nkb * 16, 2 * T, 8)
+    xsv = xs.numpy(np.float32, (nkb, T))
+    for t in (0, T - 1):
+        bf = synth.bf16_to_f32(fb[:, t]) + synth.bf16_to_f32(fb[:, T + t])
+        hl = (_f16_to_f32(f16[:, t]).astype(np.float64) + _f16_to_f32(f16[:, T + t])) * \
+            np.repeat(xsv[:, t], 16)[:, None]
+        assert np.array_equal(bf.astype(np.float64), hl), t
+    mo = m // 2 if epi == 5 else m
+    Y0 = r.standard_normal((T, mo)).astype(np.float32)
+    yd = DeviceBuffer.from_numpy(Y0)
+    call("rl_hip_gemm_f16_prefill", w16.ptr, ts.ptr, frag16.ptr, xs.ptr, yd.ptr, m, n, T, epi, mo, None)
+    got = yd.numpy(np.float32, (T, mo))
+    gemv = orc.gemv_q4_k if qt == ops.Q4_K else orc.gemv_q6_k
+    for t in range(0, T, max(1, T // 7)):
+        y = gemv(np.ascontiguousarray(blocks.reshape(-1)), X[t], m, n, 8).astype(np.float64)
+        if epi == 5:  # half tiles: rows 16k .. 16k+7 gate, 16k+8 .. 16k+15 up of outputs 8k .. 8k+7
+            yt = y.reshape(-1, 2, 8)
+            want = (yt[:, 0] / (1.0 + np.exp(-yt[:, 0])) * yt[:, 1]).reshape(-1)
+        else:
+            want = y + (Y0[t] if epi == 1 else 0.0)
+        assert rel_l2(got[t], want) <= REL_L2, (t, rel_l2(got[t], want))
+
+
 @pytest.mark.parametrize("quant", ["q4_k", "q6_k"])
 def test_engine_kquant_chunked_prefill_matches_oracle(gpu, orc, monkeypatch, quant):
     """A GGUF-style model (K-quant layer linears, BF16 a / b rows, Q6_K lm_head)
