@@ -227,6 +227,10 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
  * conv_out (window after the last token; must not alias), S (transposed, as
  * rl_hip_gdn_decode) updated in place, o [T][nv*dv] raw recurrent output.  Workspace
  * rl_hip_gdn_prefill_workspace_bytes(T, ...).  dk 128, dv a multiple of 32, conv 4.
+ * With dk = dv = 128 the scan runs in chunks of 64 tokens (gated delta rule in WY
+ * form, fp32; the workspace then also holds the chunks' matrices, about 147 KB per
+ * head and chunk); other shapes, or RL_PF_GDN_CHUNK=0 in the environment, step the
+ * state token by token.  Both follow the same per-token recurrence to fp32 rounding.
  * Replaces the reference's prefill conv + scan (cuda_engine.cu:18338-18590;
  * CPU: per token ops::conv1d_update + delta_recurrent_step, ops.cpp:458-534). */
 size_t rl_hip_gdn_prefill_workspace_bytes(int T, int nk, int nv, int dk, int dv);

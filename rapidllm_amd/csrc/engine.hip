@@ -222,7 +222,7 @@ class Engine {
     static constexpr int kPfMinTokens = 16;
     int pf_cap_ = 0;
     float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr, *pf_xc_ = nullptr,
-          *pf_gates_ = nullptr;
+          *pf_gates_ = nullptr, *pf_gdn_ck_ = nullptr;
     void *pf_frag_ = nullptr, *pf_frag_h_ = nullptr, *pf_attn_ws_ = nullptr;
     // K-quant prefill (fp16 form): the tiles' block scales, the input converted to
     // fp16 hi + lo fragments and its block scales, and which fragments that input is
@@ -335,6 +335,10 @@ class Engine {
         pf_h_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * I);
         pf_xc_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * std::max(2 * c_.n_k_heads * c_.k_dim + c_.n_v_heads * c_.v_dim, 1));
         pf_gates_ = pf_mem_->get_n<float>(static_cast<size_t>(C) * std::max(c_.n_v_heads, 1) * 2);
+        {
+            const size_t ckf = gdn_prefill_chunked() ? gdn_prefill_chunk_floats(C, c_.n_v_heads, c_.k_dim, c_.v_dim) : 0;
+            pf_gdn_ck_ = ckf ? pf_mem_->get_n<float>(ckf) : nullptr;
+        }
         pf_frag_ = pf_mem_->get(act_frag_bytes(wf, C));
         pf_frag_h_ = pf_mem_->get(act_frag_bytes(I, C));
         pf_attn_ws_bytes_ = attn_prefill_workspace_bytes(std::max(c_.n_q, 1), C);
@@ -382,7 +386,8 @@ class Engine {
                     float* ring = slot_conv(Ly.dslot);
                     gdn_prefill(pf_y_, Ly.in_width, Ly.off_a, Ly.off_b, Ly.A_log, Ly.dt_bias, Ly.conv_w,
                                 ring + slot * conv_slot_, ring + (slot ^ 1) * conv_slot_, pf_xc_, pf_gates_,
-                                slot_S(Ly.dslot), pf_o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_);
+                                slot_S(Ly.dslot), pf_o_, T, nk, nv, c_.k_dim, dv, c_.conv_k, c_.v_tiled, st_,
+                                pf_gdn_ck_);
                     gnorm_pack(pf_o_, pf_y_ + Ly.off_z, Ly.in_width, Ly.gnorm, Ly.gnorm_n, nullptr, pf_frag_, zdim, T,
                                1e-6f, st_);
                     pf_f16_src_ = nullptr;

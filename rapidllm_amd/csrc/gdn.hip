@@ -19,6 +19,7 @@
 // State layout in HBM (transposed per head): St[h][j][i] = S[h][i][j], so each
 // thread's 8 values are 32 contiguous bytes and a wave reads 2 KiB contiguously.
 // Conv window layout is the reference's [channel][tap] (tap 0 oldest).
+#include <cstdlib>
 #include <algorithm>
 
 #include "internal.h"
@@ -835,6 +836,349 @@ __global__ __launch_bounds__(kPfCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
     for (int r = 0; r < kPfRows / 4; ++r) dp[r] = f32x4{S[4 * r], S[4 * r + 1], S[4 * r + 2], S[4 * r + 3]};
 }
 
+
+// ---- chunked prefill scan (gated delta rule in WY form over chunks of 64 tokens)
+// Within a chunk with cumulative log decays la_t = sum_{s<=t} log g_s, the per-token
+// recurrence (decay, delta rule, output) is the same as
+//   (I + A) X = diag(beta) [V | diag(gamma) K],  A[t][i] = beta_t G[t][i] k_t.k_i (i < t),
+//   X = [U~ | W~],  U = U~ - W~ S0,
+//   O = diag(gamma) Q S0 + (M o U),  M[t][i] = G[t][i] q_t.k_i (i <= t),
+//   S  = gamma_C S0 + K~^T U,         K~ = diag(gamma_C / gamma_i) K,
+// with gamma_t = exp(la_t), G[t][i] = exp(la_t - la_i) (never a division, so no
+// overflow however strong the decay).  gdn_pf_chunk_prep builds everything that
+// does not depend on S0 for all chunks at once (one workgroup per (v-head, chunk));
+// gdn_pf_chunk_scan then runs the chunks in order, one workgroup per (v-head,
+// 16 value columns), the state block in MFMA accumulators (fp32 16x16x4: exact
+// fp32 products, fp32 sums).
+constexpr int kCk = 64;          // tokens per chunk
+constexpr int kCkStride = kDK + 4;  // LDS row stride of q / k (floats)
+constexpr int kCkA = kCk + 4;       // LDS row stride of A
+constexpr int kCkCols = 16;         // value columns per scan workgroup
+// one (v-head, chunk) block of the workspace: U~ [64][128] | W~ [64][128] |
+// gamma Q [64][128] | K~^T [128][64] | M [64][64]
+constexpr size_t kCkFloats = 4 * static_cast<size_t>(kCk) * kDK + static_cast<size_t>(kCk) * kCk;
+
+__device__ inline f32x4 mfma_f32_4(float a, float b, f32x4 c) {
+    return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
+}
+
+// Tile pairs (t block, i block) of the 64 x 64 chunk matrices in 16 x 16 tiles:
+// the ten on or below the diagonal first, so that wave w's jobs w, w+4, w+8, w+12
+// hold two or three of them.
+__constant__ unsigned char kCkPairs[16][2] = {{0, 0}, {1, 0}, {1, 1}, {2, 0}, {2, 1}, {2, 2}, {3, 0}, {3, 1},
+                                              {3, 2}, {3, 3}, {0, 1}, {0, 2}, {0, 3}, {1, 2}, {1, 3}, {2, 3}};
+
+__global__ __launch_bounds__(256, 2) void gdn_pf_chunk_prep_kernel(GdnPfArgs p, float* ws, float* gc, int nch) {
+    const int h = blockIdx.x, c = blockIdx.y, tid = threadIdx.x;
+    const int w = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    const int t0 = c * kCk, n = min(kCk, p.T - t0);
+    const int rep = p.nv / p.nk;
+    const int src = p.v_tiled ? (h % p.nk) : (h / rep);
+    const int qdim = p.nk * kDK;
+    const float qscale = 1.f / sqrtf(static_cast<float>(kDK));
+    __shared__ __align__(16) float q_s[kCk][kCkStride];  // after the products: A [64][kCkA]
+    __shared__ __align__(16) float k_s[kCk][kCkStride];
+    __shared__ double la_s[kCk];
+    __shared__ float beta_s[kCk];
+    float(*a_s)[kCkA] = reinterpret_cast<float(*)[kCkA]>(&q_s[0][0]);
+    static_assert(kCk * kCkA <= kCk * kCkStride, "A fits in the q buffer");
+
+    float* blk = ws + (static_cast<size_t>(h) * nch + c) * kCkFloats;
+    float* ut = blk;
+    float* wt = ut + kCk * kDK;
+    float* qg = wt + kCk * kDK;
+    float* ktT = qg + kCk * kDK;
+    float* m = ktT + kDK * kCk;
+
+    // q and k of the chunk's tokens (zeros past the last token), gates
+    for (int u = tid; u < kCk * (2 * kDK / 4); u += 256) {
+        const int tt = u / (2 * kDK / 4), f = (u % (2 * kDK / 4)) * 4;
+        float4 v = make_float4(0.f, 0.f, 0.f, 0.f);
+        if (tt < n) {
+            const float* row = p.xc + static_cast<size_t>(t0 + tt) * p.conv_dim;
+            v = *reinterpret_cast<const float4*>(f < kDK ? row + src * kDK + f : row + qdim + src * kDK + (f - kDK));
+        }
+        *reinterpret_cast<float4*>(f < kDK ? &q_s[tt][f] : &k_s[tt][f - kDK]) = v;
+    }
+    // each thread's value column of V (threads 128 .. 255: the W~ columns, later)
+    float x[kCk];
+    const int col = tid;
+    if (col < kDK) {
+        const float* vp = p.xc + static_cast<size_t>(t0) * p.conv_dim + 2 * qdim + h * p.dv + col;
+#pragma unroll
+        for (int t = 0; t < kCk; ++t) x[t] = t < n ? vp[static_cast<size_t>(t) * p.conv_dim] : 0.f;
+    }
+    if (w == 0) {
+        // log of the decay the recurrence multiplies by (a decay that underflowed to
+        // 0 becomes exp(-150), itself 0 in fp32), summed over the chunk in double
+        float2 gb = make_float2(1.f, 0.f);
+        if (lane < n) gb = reinterpret_cast<const float2*>(p.gates)[static_cast<size_t>(t0 + lane) * p.nv + h];
+        double la = gb.x > 0.f ? static_cast<double>(fmaxf(logf(gb.x), -150.f)) : -150.0;
+#pragma unroll
+        for (int d = 1; d < 64; d <<= 1) {
+            const double o = __shfl_up(la, d);
+            if (lane >= d) la += o;
+        }
+        la_s[lane] = la;
+        beta_s[lane] = gb.y;
+    }
+    __syncthreads();
+    // L2 norms: two threads per vector (q of token v, or k of token v - 64)
+    {
+        const int v = tid >> 1, half = tid & 1;
+        float* xv = v < kCk ? &q_s[v][64 * half] : &k_s[v - kCk][64 * half];
+        float a4[4] = {0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < 64; ++i) a4[i & 3] = fmaf(xv[i], xv[i], a4[i & 3]);
+        float sum = (a4[0] + a4[1]) + (a4[2] + a4[3]);
+        sum += __shfl_xor(sum, 1);
+        const float inv = v < kCk ? 1.f / sqrtf(sum + 1e-6f) * qscale : 1.f / sqrtf(sum + 1e-6f);
+#pragma unroll
+        for (int i = 0; i < 64; ++i) xv[i] *= inv;
+    }
+    __syncthreads();
+    // gamma Q rows (q is not needed after the products below)
+    for (int u = tid; u < kCk * kDK / 4; u += 256) {
+        const int t = u / (kDK / 4), d = (u % (kDK / 4)) * 4;
+        const float gm = expf(static_cast<float>(la_s[t]));
+        const float4 qv = *reinterpret_cast<const float4*>(&q_s[t][d]);
+        *reinterpret_cast<float4*>(qg + t * kDK + d) = make_float4(gm * qv.x, gm * qv.y, gm * qv.z, gm * qv.w);
+    }
+    // K K^T and Q K^T by 16 x 16 tiles on MFMA; M to memory, A kept until q is free
+    f32x4 at[4];
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        const int job = w + 4 * jb;
+        const int tb = kCkPairs[job][0], ib = kCkPairs[job][1];
+        f32x4 kk = {0.f, 0.f, 0.f, 0.f}, qk = {0.f, 0.f, 0.f, 0.f};
+        if (job < 10) {
+#pragma unroll
+            for (int s = 0; s < kDK / 16; ++s) {
+                const float4 ka = *reinterpret_cast<const float4*>(&k_s[16 * tb + r][16 * s + 4 * g]);
+                const float4 qa = *reinterpret_cast<const float4*>(&q_s[16 * tb + r][16 * s + 4 * g]);
+                const float4 kb = *reinterpret_cast<const float4*>(&k_s[16 * ib + r][16 * s + 4 * g]);
+                kk = mfma_f32_4(ka.x, kb.x, kk);
+                qk = mfma_f32_4(qa.x, kb.x, qk);
+                kk = mfma_f32_4(ka.y, kb.y, kk);
+                qk = mfma_f32_4(qa.y, kb.y, qk);
+                kk = mfma_f32_4(ka.z, kb.z, kk);
+                qk = mfma_f32_4(qa.z, kb.z, qk);
+                kk = mfma_f32_4(ka.w, kb.w, kk);
+                qk = mfma_f32_4(qa.w, kb.w, qk);
+            }
+        }
+        const int i = 16 * ib + r;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 16 * tb + 4 * g + e;
+            const float G = i <= t ? expf(static_cast<float>(la_s[t] - la_s[i])) : 0.f;
+            at[jb][e] = i < t ? beta_s[t] * G * kk[e] : 0.f;
+            m[t * kCk + i] = G * qk[e];
+        }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int jb = 0; jb < 4; ++jb) {
+        const int job = w + 4 * jb;
+        const int tb = kCkPairs[job][0], ib = kCkPairs[job][1];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) a_s[16 * tb + 4 * g + e][16 * ib + r] = at[jb][e];
+    }
+    __syncthreads();
+
+    // forward substitution, one right-hand column per thread: V (U~) or gamma K (W~)
+    if (col >= kDK) {
+#pragma unroll
+        for (int t = 0; t < kCk; ++t) x[t] = expf(static_cast<float>(la_s[t])) * k_s[t][col - kDK];
+    }
+#pragma unroll
+    for (int t = 0; t < kCk; ++t) {
+        float s4[4] = {beta_s[t] * x[t], 0.f, 0.f, 0.f};
+#pragma unroll
+        for (int i = 0; i < t; ++i) s4[i & 3] = fmaf(-a_s[t][i], x[i], s4[i & 3]);
+        x[t] = (s4[0] + s4[1]) + (s4[2] + s4[3]);
+    }
+    {
+        float* dst = col < kDK ? ut + col : wt + (col - kDK);
+#pragma unroll
+        for (int t = 0; t < kCk; ++t) dst[t * kDK] = x[t];
+    }
+    // K~ transposed
+    for (int u = tid; u < kDK * kCk / 4; u += 256) {
+        const int d = u / (kCk / 4), t = (u % (kCk / 4)) * 4;
+        float v[4];
+#pragma unroll
+        for (int e = 0; e < 4; ++e)
+            v[e] = expf(static_cast<float>(la_s[n - 1] - la_s[t + e])) * k_s[t + e][d];
+        *reinterpret_cast<float4*>(ktT + d * kCk + t) = make_float4(v[0], v[1], v[2], v[3]);
+    }
+    if (tid == 0) gc[static_cast<size_t>(h) * nch + c] = expf(static_cast<float>(la_s[n - 1]));
+}
+
+
+// Barrier for LDS hand-offs only: waits for this wave's LDS traffic, not for its
+// global loads (a __syncthreads drains those too, which would stall the next
+// chunk's prefetch).
+__device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// A-operand registers of one chunk for one lane (row r = lane % 16, k group
+// g = lane / 16), in two sets loaded at different points of the previous chunk so
+// that at most three sets are live: first W~ and gamma Q rows of the wave's tokens
+// and U~ at the lane's four output rows, then the M row and K~^T rows of the
+// wave's two state tiles.
+struct CkOpsA {
+    float4 wa[kDK / 16], qa[kDK / 16];
+    float uu[4];
+};
+struct CkOpsB {
+    float4 ma[kCk / 16], ka[2][kCk / 16];
+    float gC;
+};
+
+// One workgroup per (v-head, 16 value columns), 4 waves.  Wave w owns token rows
+// 16w .. 16w+15 of U and O, and state rows 32w .. 32w+31 (two 16 x 16 MFMA tiles,
+// lane l holding rows 4(l/16) .. +3 of column l%16).  LDS holds the state block
+// and U transposed, the B operands every wave reads.  The next chunk's A operands
+// load while the current chunk computes.
+__global__ __launch_bounds__(256, 2) void gdn_pf_chunk_scan_kernel(GdnPfArgs p, const float* ws, const float* gc,
+                                                                int nch) {
+    const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
+    // consecutive workgroups take different heads, so the column blocks of one head
+    // (which read the same chunk data) share an XCD when nv is a multiple of 8
+    const int h = blockIdx.x % p.nv, j0 = (blockIdx.x / p.nv) * kCkCols;
+    __shared__ __align__(16) float st_s[kCkCols][kDK + 4];  // state block transposed: [column][key row]
+    __shared__ __align__(16) float ut_s[kCkCols][kCk + 4];  // U transposed: [column][token]
+    float* Sg = p.S + (static_cast<size_t>(h) * p.dv + j0 + r) * kDK;
+    const int row = 16 * w + r;
+    auto blk = [&](int c) { return ws + (static_cast<size_t>(h) * nch + c) * kCkFloats; };
+    auto load_a = [&](int c, CkOpsA& o) {
+        const float* ut = blk(c);
+        const float* wt = ut + kCk * kDK;
+        const float* qg = wt + kCk * kDK;
+#pragma unroll
+        for (int s = 0; s < kDK / 16; ++s) {
+            o.wa[s] = *reinterpret_cast<const float4*>(wt + row * kDK + 16 * s + 4 * g);
+            o.qa[s] = *reinterpret_cast<const float4*>(qg + row * kDK + 16 * s + 4 * g);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) o.uu[e] = ut[(16 * w + 4 * g + e) * kDK + j0 + r];
+    };
+    auto load_b = [&](int c, CkOpsB& o) {
+        const float* ktT = blk(c) + 3 * kCk * kDK;
+        const float* m = ktT + kDK * kCk;
+#pragma unroll
+        for (int s = 0; s < kCk / 16; ++s) {
+            o.ma[s] = *reinterpret_cast<const float4*>(m + row * kCk + 16 * s + 4 * g);
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt)
+                o.ka[tt][s] = *reinterpret_cast<const float4*>(ktT + (32 * w + 16 * tt + r) * kCk + 16 * s + 4 * g);
+        }
+        o.gC = gc[static_cast<size_t>(h) * nch + c];
+    };
+    f32x4 sreg[2];
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) {
+        const int i0 = 32 * w + 16 * tt + 4 * g;
+        sreg[tt] = *reinterpret_cast<const f32x4*>(Sg + i0);
+        *reinterpret_cast<f32x4*>(&st_s[r][i0]) = sreg[tt];
+    }
+    const size_t ldo = static_cast<size_t>(p.nv) * p.dv;
+    // chunk c from operands (ac, bc); loads chunk c + 1's into (an, bn) on the way
+    // (the last chunk reloads itself: no branch, nothing read out of bounds)
+    auto chunk = [&](int c, const CkOpsA& ac, const CkOpsB& bc, CkOpsA& an, CkOpsB& bn)
+        __attribute__((always_inline)) {
+        const int cn = min(c + 1, nch - 1);
+        load_b(cn, bn);
+        const int n = min(kCk, p.T - c * kCk);
+        // W~ S and gamma Q S for the wave's 16 tokens (K = 128 key rows); four
+        // accumulator chains (even / odd key blocks) keep the MFMA pipe busy
+        const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
+        f32x4 au[2] = {z4, z4}, ao[2] = {z4, z4};
+        float4 sb[kDK / 16];
+#pragma unroll
+        for (int s = 0; s < kDK / 16; ++s) sb[s] = *reinterpret_cast<const float4*>(&st_s[r][16 * s + 4 * g]);
+#pragma unroll
+        for (int s = 0; s < kDK / 16; ++s) {
+            const float4 wa = ac.wa[s], qa = ac.qa[s];
+            f32x4& u = au[s & 1];
+            f32x4& o = ao[s & 1];
+            u = mfma_f32_4(wa.x, sb[s].x, u);
+            o = mfma_f32_4(qa.x, sb[s].x, o);
+            u = mfma_f32_4(wa.y, sb[s].y, u);
+            o = mfma_f32_4(qa.y, sb[s].y, o);
+            u = mfma_f32_4(wa.z, sb[s].z, u);
+            o = mfma_f32_4(qa.z, sb[s].z, o);
+            u = mfma_f32_4(wa.w, sb[s].w, u);
+            o = mfma_f32_4(qa.w, sb[s].w, o);
+        }
+        // U = U~ - W~ S (rows 16w + 4g + e, column r)
+        {
+            f32x4 u;
+#pragma unroll
+            for (int e = 0; e < 4; ++e) u[e] = ac.uu[e] - (au[0][e] + au[1][e]);
+            *reinterpret_cast<f32x4*>(&ut_s[r][16 * w + 4 * g]) = u;
+        }
+        load_a(cn, an);
+        lds_barrier();
+        float4 ub[kCk / 16];
+#pragma unroll
+        for (int s = 0; s < kCk / 16; ++s) ub[s] = *reinterpret_cast<const float4*>(&ut_s[r][16 * s + 4 * g]);
+        // O += M U over tokens 0 .. 16w+15 (M is zero above the diagonal)
+#pragma unroll
+        for (int s = 0; s < kCk / 16; ++s) {
+            if (s > w) break;
+            const float4 ma = bc.ma[s];
+            f32x4& o = ao[s & 1];
+            o = mfma_f32_4(ma.x, ub[s].x, o);
+            o = mfma_f32_4(ma.y, ub[s].y, o);
+            o = mfma_f32_4(ma.z, ub[s].z, o);
+            o = mfma_f32_4(ma.w, ub[s].w, o);
+        }
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+            const int t = 16 * w + 4 * g + e;
+            if (t < n)
+                p.o[static_cast<size_t>(c * kCk + t) * ldo + static_cast<size_t>(h) * p.dv + j0 + r] =
+                    ao[0][e] + ao[1][e];
+        }
+        // S = gamma_C S + K~^T U, the two state tiles' chains interleaved
+        f32x4 acc[2] = {sreg[0] * bc.gC, sreg[1] * bc.gC};
+#pragma unroll
+        for (int s = 0; s < kCk / 16; ++s) {
+#pragma unroll
+            for (int q = 0; q < 4; ++q)
+#pragma unroll
+                for (int tt = 0; tt < 2; ++tt) {
+                    const float4 ka = bc.ka[tt][s];
+                    const float av = q == 0 ? ka.x : q == 1 ? ka.y : q == 2 ? ka.z : ka.w;
+                    const float bv = q == 0 ? ub[s].x : q == 1 ? ub[s].y : q == 2 ? ub[s].z : ub[s].w;
+                    acc[tt] = mfma_f32_4(av, bv, acc[tt]);
+                }
+        }
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            sreg[tt] = acc[tt];
+            *reinterpret_cast<f32x4*>(&st_s[r][32 * w + 16 * tt + 4 * g]) = acc[tt];
+        }
+        lds_barrier();
+    };
+    // two operand sets in turn (no register copies between chunks, which would
+    // wait for the prefetch)
+    CkOpsA a0, a1;
+    CkOpsB b0, b1;
+    load_a(0, a0);
+    load_b(0, b0);
+    lds_barrier();
+    int c = 0;
+    for (; c + 1 < nch; c += 2) {
+        chunk(c, a0, b0, a1, b1);
+        chunk(c + 1, a1, b1, a0, b0);
+    }
+    if (c < nch) chunk(c, a0, b0, a1, b1);
+#pragma unroll
+    for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<f32x4*>(Sg + 32 * w + 16 * tt + 4 * g) = sreg[tt];
+}
+
 }  // namespace
 
 namespace rl {
@@ -918,7 +1262,7 @@ void gdn_decode(const float* qkv, const float* a, const float* b, int ld_in, con
 
 void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
                  const float* conv_w, const float* conv_in, float* conv_out, float* xc, float* gates, float* S,
-                 float* o, int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s) {
+                 float* o, int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s, float* ck) {
     RL_REQUIRE(gdn_fused_supported(dk, dv, K), RL_ERR_UNSUPPORTED, "gdn_prefill: dk 128, dv a multiple of 32, conv 4");
     RL_REQUIRE(T >= 1 && nk > 0 && nv > 0 && nv % nk == 0, RL_ERR_RANGE, "gdn_prefill: bad shape");
     RL_REQUIRE(y && A_log && dt_bias && conv_w && conv_in && conv_out && xc && gates && S && o, RL_ERR_RANGE,
@@ -930,8 +1274,29 @@ void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_lo
     const size_t n = static_cast<size_t>(T) * (conv_dim + nv);
     hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p);
     check_launch("gdn_pf_conv_kernel");
+    if (ck && gdn_prefill_chunk_floats(T, nv, dk, dv) > 0) {
+        const int nch = (T + kCk - 1) / kCk;
+        float* gc = ck + static_cast<size_t>(nv) * nch * kCkFloats;
+        hipLaunchKernelGGL(gdn_pf_chunk_prep_kernel, dim3(nv, nch), dim3(256), 0, s, p, ck, gc, nch);
+        check_launch("gdn_pf_chunk_prep_kernel");
+        hipLaunchKernelGGL(gdn_pf_chunk_scan_kernel, dim3(nv * (dv / kCkCols)), dim3(256), 0, s, p,
+                           static_cast<const float*>(ck), static_cast<const float*>(gc), nch);
+        check_launch("gdn_pf_chunk_scan_kernel");
+        return;
+    }
     hipLaunchKernelGGL(gdn_pf_rec_kernel, dim3(nv * (dv / kCW)), dim3(kPfCT), 0, s, p);
     check_launch("gdn_pf_rec_kernel");
+}
+
+bool gdn_prefill_chunked() {
+    const char* env = std::getenv("RL_PF_GDN_CHUNK");  // measurement override, read per call
+    return !(env && env[0] == '0');
+}
+
+size_t gdn_prefill_chunk_floats(int T, int nv, int dk, int dv) {
+    if (dk != kDK || dv != kDK || T < 1 || nv < 1) return 0;
+    const size_t nch = static_cast<size_t>((T + kCk - 1) / kCk);
+    return static_cast<size_t>(nv) * nch * (kCkFloats + 1);
 }
 
 }  // namespace rl
@@ -954,7 +1319,8 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
 }
 
 size_t rl_hip_gdn_prefill_workspace_bytes(int T, int nk, int nv, int dk, int dv) {
-    return (static_cast<size_t>(T) * (2 * nk * dk + nv * dv) + static_cast<size_t>(T) * nv * 2) * sizeof(float) + 256;
+    return (static_cast<size_t>(T) * (2 * nk * dk + nv * dv) + static_cast<size_t>(T) * nv * 2 +
+            rl::gdn_prefill_chunk_floats(T, nv, dk, dv)) * sizeof(float) + 256;
 }
 
 int rl_hip_gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
@@ -966,8 +1332,9 @@ int rl_hip_gdn_prefill(const float* y, int ld, int off_a, int off_b, const float
                    RL_ERR_RANGE, "gdn_prefill: workspace too small");
         float* xc = static_cast<float*>(workspace);
         float* gates = xc + static_cast<size_t>(T) * (2 * nk * dk + nv * dv);
+        float* ck = gates + static_cast<size_t>(T) * nv * 2;
         rl::gdn_prefill(y, ld, off_a, off_b, A_log, dt_bias, conv_w, conv_in, conv_out, xc, gates, S_state, o, T, nk,
-                        nv, dk, dv, conv_k, v_tiled, S(stream));
+                        nv, dk, dv, conv_k, v_tiled, S(stream), rl::gdn_prefill_chunked() ? ck : nullptr);
     });
 }
 

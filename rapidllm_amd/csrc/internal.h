@@ -198,7 +198,14 @@ void gdn_decode_fused(const float* qkv, const float* a, const float* b, int ld_i
 // recurrent output; conv_out = window after the last token.
 void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_log, const float* dt_bias,
                  const float* conv_w, const float* conv_in, float* conv_out, float* xc, float* gates, float* S,
-                 float* o, int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s);
+                 float* o, int T, int nk, int nv, int dk, int dv, int K, int v_tiled, hipStream_t s,
+                 float* ck = nullptr);
+// ck (when not null and dk = dv = 128): gdn_prefill_chunk_floats(T, nv, dk, dv)
+// floats of scratch for the chunked scan; null, or other head sizes: the per-token
+// scan.  0 where the chunked scan does not apply.
+size_t gdn_prefill_chunk_floats(int T, int nv, int dk, int dv);
+// The chunked scan unless RL_PF_GDN_CHUNK=0.
+bool gdn_prefill_chunked();
 
 // attn.hip
 size_t attn_workspace_bytes(int nkv, int ctx);

@@ -199,6 +199,29 @@ def test_gdn_prefill_vs_oracle(gpu, orc, T, nk, nv, v_tiled):
     assert np.array_equal(conv, conv_ref)
 
 
+@pytest.mark.parametrize("T,decay", [(700, 0.5), (130, 6.0), (64, -3.0)])
+def test_gdn_prefill_chunked_vs_per_token(gpu, orc, monkeypatch, T, decay):
+    """The chunked scan (chunks of 64 tokens in WY form) and the per-token scan
+    (RL_PF_GDN_CHUNK=0) against the per-token oracle over several chunks and a
+    ragged last one: decay 6 makes A_log large enough that g underflows to 0 in
+    fp32 on some tokens (the chunk's log-decay sums must not turn into inf - inf),
+    decay -3 keeps g near 1 (little forgetting, the state carries over chunks)."""
+    from tests.test_gpu_layers import _gdn_case, _gdn_oracle
+    nk, nv = 2, 4
+    r = synth.rng(900 + T)
+    case = list(_gdn_case(r, T, nk, nv, False))
+    case[3] = (case[3] + decay).astype(np.float32)  # A_log
+    o_ref, S_ref, conv_ref = _gdn_oracle(orc, *case, nk, nv, False)
+    for mode in ("1", "0"):
+        monkeypatch.setenv("RL_PF_GDN_CHUNK", mode)
+        o, S, conv = ops.gdn_prefill(*case, nk, nv, False)
+        assert np.isfinite(o).all() and np.isfinite(S).all()
+        for t in range(T):
+            assert rel_l2(o[t], o_ref[t]) < 1e-3, (mode, t, rel_l2(o[t], o_ref[t]))
+        assert rel_l2(S, S_ref) < 1e-4, mode
+        assert np.array_equal(conv, conv_ref)
+
+
 @pytest.mark.parametrize("qt,m,n,T", [(ops.Q4_K, 256, 1024, 70), (ops.Q6_K, 160, 768, 130),
                                       (ops.Q4_K, 5120, 4096, 300)])
 def test_kquant_prefill_gemm_vs_oracle(gpu, orc, qt, m, n, T):
