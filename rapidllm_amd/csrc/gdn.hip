@@ -853,7 +853,6 @@ __global__ __launch_bounds__(kPfCT) void gdn_pf_rec_kernel(GdnPfArgs p) {
 constexpr int kCk = 64;          // tokens per chunk
 constexpr int kCkStride = kDK + 4;  // LDS row stride of q / k (floats)
 constexpr int kCkA = kCk + 4;       // LDS row stride of A
-constexpr int kCkCols = 16;         // value columns per scan workgroup
 // one (v-head, chunk) block of the workspace: U~ [64][128] | W~ [64][128] |
 // gamma Q [64][128] | K~^T [128][64] | M [64][64]
 constexpr size_t kCkFloats = 4 * static_cast<size_t>(kCk) * kDK + static_cast<size_t>(kCk) * kCk;
@@ -1024,34 +1023,37 @@ __device__ inline void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_b
 // A-operand registers of one chunk for one lane (row r = lane % 16, k group
 // g = lane / 16), in two sets loaded at different points of the previous chunk so
 // that at most three sets are live: first W~ and gamma Q rows of the wave's tokens
-// and U~ at the lane's four output rows, then the M row and K~^T rows of the
-// wave's two state tiles.
+// and U~ at the lane's four output rows of each column tile, then the M row and
+// K~^T rows of the wave's two state tiles.
+template <int NCT>
 struct CkOpsA {
     float4 wa[kDK / 16], qa[kDK / 16];
-    float uu[4];
+    float uu[NCT][4];
 };
 struct CkOpsB {
     float4 ma[kCk / 16], ka[2][kCk / 16];
     float gC;
 };
 
-// One workgroup per (v-head, 16 value columns), 4 waves.  Wave w owns token rows
-// 16w .. 16w+15 of U and O, and state rows 32w .. 32w+31 (two 16 x 16 MFMA tiles,
-// lane l holding rows 4(l/16) .. +3 of column l%16).  LDS holds the state block
-// and U transposed, the B operands every wave reads.  The next chunk's A operands
-// load while the current chunk computes.
-__global__ __launch_bounds__(256, 2) void gdn_pf_chunk_scan_kernel(GdnPfArgs p, const float* ws, const float* gc,
-                                                                int nch) {
+// One workgroup per (v-head, 16 NCT value columns), 4 waves.  Wave w owns token
+// rows 16w .. 16w+15 of U and O, and state rows 32w .. 32w+31 (two 16 x 16 MFMA
+// tiles per 16-column tile, lane l holding rows 4(l/16) .. +3 of column l%16);
+// each A operand feeds NCT MFMAs.  LDS holds the state block and U transposed,
+// the B operands every wave reads.  The next chunk's A operands load while the
+// current chunk computes.
+template <int NCT>
+__global__ __launch_bounds__(256, 3 - NCT) void gdn_pf_chunk_scan_kernel(GdnPfArgs p, const float* ws,
+                                                                         const float* gc, int nch) {
+    constexpr int NC = 16 * NCT;  // value columns per workgroup
     const int tid = threadIdx.x, w = tid >> 6, lane = tid & 63, r = lane & 15, g = lane >> 4;
     // consecutive workgroups take different heads, so the column blocks of one head
     // (which read the same chunk data) share an XCD when nv is a multiple of 8
-    const int h = blockIdx.x % p.nv, j0 = (blockIdx.x / p.nv) * kCkCols;
-    __shared__ __align__(16) float st_s[kCkCols][kDK + 4];  // state block transposed: [column][key row]
-    __shared__ __align__(16) float ut_s[kCkCols][kCk + 4];  // U transposed: [column][token]
-    float* Sg = p.S + (static_cast<size_t>(h) * p.dv + j0 + r) * kDK;
+    const int h = blockIdx.x % p.nv, j0 = (blockIdx.x / p.nv) * NC;
+    __shared__ __align__(16) float st_s[NC][kDK + 4];  // state block transposed: [column][key row]
+    __shared__ __align__(16) float ut_s[NC][kCk + 4];  // U transposed: [column][token]
     const int row = 16 * w + r;
     auto blk = [&](int c) { return ws + (static_cast<size_t>(h) * nch + c) * kCkFloats; };
-    auto load_a = [&](int c, CkOpsA& o) {
+    auto load_a = [&](int c, CkOpsA<NCT>& o) {
         const float* ut = blk(c);
         const float* wt = ut + kCk * kDK;
         const float* qg = wt + kCk * kDK;
@@ -1061,7 +1063,9 @@ __global__ __launch_bounds__(256, 2) void gdn_pf_chunk_scan_kernel(GdnPfArgs p, 
             o.qa[s] = *reinterpret_cast<const float4*>(qg + row * kDK + 16 * s + 4 * g);
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) o.uu[e] = ut[(16 * w + 4 * g + e) * kDK + j0 + r];
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) o.uu[ct][e] = ut[(16 * w + 4 * g + e) * kDK + j0 + 16 * ct + r];
     };
     auto load_b = [&](int c, CkOpsB& o) {
         const float* ktT = blk(c) + 3 * kCk * kDK;
@@ -1075,96 +1079,113 @@ __global__ __launch_bounds__(256, 2) void gdn_pf_chunk_scan_kernel(GdnPfArgs p, 
         }
         o.gC = gc[static_cast<size_t>(h) * nch + c];
     };
-    f32x4 sreg[2];
+    f32x4 sreg[NCT][2];
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) {
-        const int i0 = 32 * w + 16 * tt + 4 * g;
-        sreg[tt] = *reinterpret_cast<const f32x4*>(Sg + i0);
-        *reinterpret_cast<f32x4*>(&st_s[r][i0]) = sreg[tt];
-    }
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt) {
+            const int i0 = 32 * w + 16 * tt + 4 * g;
+            sreg[ct][tt] = *reinterpret_cast<const f32x4*>(p.S + (static_cast<size_t>(h) * p.dv + j0 + 16 * ct + r) *
+                                                                       kDK + i0);
+            *reinterpret_cast<f32x4*>(&st_s[16 * ct + r][i0]) = sreg[ct][tt];
+        }
     const size_t ldo = static_cast<size_t>(p.nv) * p.dv;
     // chunk c from operands (ac, bc); loads chunk c + 1's into (an, bn) on the way
     // (the last chunk reloads itself: no branch, nothing read out of bounds)
-    auto chunk = [&](int c, const CkOpsA& ac, const CkOpsB& bc, CkOpsA& an, CkOpsB& bn)
+    auto chunk = [&](int c, const CkOpsA<NCT>& ac, const CkOpsB& bc, CkOpsA<NCT>& an, CkOpsB& bn)
         __attribute__((always_inline)) {
         const int cn = min(c + 1, nch - 1);
         load_b(cn, bn);
         const int n = min(kCk, p.T - c * kCk);
-        // W~ S and gamma Q S for the wave's 16 tokens (K = 128 key rows); four
-        // accumulator chains (even / odd key blocks) keep the MFMA pipe busy
+        // W~ S and gamma Q S for the wave's 16 tokens (K = 128 key rows)
         const f32x4 z4 = {0.f, 0.f, 0.f, 0.f};
-        f32x4 au[2] = {z4, z4}, ao[2] = {z4, z4};
-        float4 sb[kDK / 16];
+        f32x4 au[NCT], ao[NCT];
 #pragma unroll
-        for (int s = 0; s < kDK / 16; ++s) sb[s] = *reinterpret_cast<const float4*>(&st_s[r][16 * s + 4 * g]);
+        for (int ct = 0; ct < NCT; ++ct) au[ct] = ao[ct] = z4;
 #pragma unroll
         for (int s = 0; s < kDK / 16; ++s) {
             const float4 wa = ac.wa[s], qa = ac.qa[s];
-            f32x4& u = au[s & 1];
-            f32x4& o = ao[s & 1];
-            u = mfma_f32_4(wa.x, sb[s].x, u);
-            o = mfma_f32_4(qa.x, sb[s].x, o);
-            u = mfma_f32_4(wa.y, sb[s].y, u);
-            o = mfma_f32_4(qa.y, sb[s].y, o);
-            u = mfma_f32_4(wa.z, sb[s].z, u);
-            o = mfma_f32_4(qa.z, sb[s].z, o);
-            u = mfma_f32_4(wa.w, sb[s].w, u);
-            o = mfma_f32_4(qa.w, sb[s].w, o);
+            float4 sb[NCT];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) sb[ct] = *reinterpret_cast<const float4*>(&st_s[16 * ct + r][16 * s + 4 * g]);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                au[ct] = mfma_f32_4(wa.x, sb[ct].x, au[ct]);
+                ao[ct] = mfma_f32_4(qa.x, sb[ct].x, ao[ct]);
+                au[ct] = mfma_f32_4(wa.y, sb[ct].y, au[ct]);
+                ao[ct] = mfma_f32_4(qa.y, sb[ct].y, ao[ct]);
+                au[ct] = mfma_f32_4(wa.z, sb[ct].z, au[ct]);
+                ao[ct] = mfma_f32_4(qa.z, sb[ct].z, ao[ct]);
+                au[ct] = mfma_f32_4(wa.w, sb[ct].w, au[ct]);
+                ao[ct] = mfma_f32_4(qa.w, sb[ct].w, ao[ct]);
+            }
         }
-        // U = U~ - W~ S (rows 16w + 4g + e, column r)
-        {
+        // U = U~ - W~ S (rows 16w + 4g + e, column 16 ct + r)
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) {
             f32x4 u;
 #pragma unroll
-            for (int e = 0; e < 4; ++e) u[e] = ac.uu[e] - (au[0][e] + au[1][e]);
-            *reinterpret_cast<f32x4*>(&ut_s[r][16 * w + 4 * g]) = u;
+            for (int e = 0; e < 4; ++e) u[e] = ac.uu[ct][e] - au[ct][e];
+            *reinterpret_cast<f32x4*>(&ut_s[16 * ct + r][16 * w + 4 * g]) = u;
         }
         load_a(cn, an);
         lds_barrier();
-        float4 ub[kCk / 16];
-#pragma unroll
-        for (int s = 0; s < kCk / 16; ++s) ub[s] = *reinterpret_cast<const float4*>(&ut_s[r][16 * s + 4 * g]);
         // O += M U over tokens 0 .. 16w+15 (M is zero above the diagonal)
 #pragma unroll
         for (int s = 0; s < kCk / 16; ++s) {
             if (s > w) break;
             const float4 ma = bc.ma[s];
-            f32x4& o = ao[s & 1];
-            o = mfma_f32_4(ma.x, ub[s].x, o);
-            o = mfma_f32_4(ma.y, ub[s].y, o);
-            o = mfma_f32_4(ma.z, ub[s].z, o);
-            o = mfma_f32_4(ma.w, ub[s].w, o);
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) {
+                const float4 ub = *reinterpret_cast<const float4*>(&ut_s[16 * ct + r][16 * s + 4 * g]);
+                ao[ct] = mfma_f32_4(ma.x, ub.x, ao[ct]);
+                ao[ct] = mfma_f32_4(ma.y, ub.y, ao[ct]);
+                ao[ct] = mfma_f32_4(ma.z, ub.z, ao[ct]);
+                ao[ct] = mfma_f32_4(ma.w, ub.w, ao[ct]);
+            }
         }
 #pragma unroll
-        for (int e = 0; e < 4; ++e) {
-            const int t = 16 * w + 4 * g + e;
-            if (t < n)
-                p.o[static_cast<size_t>(c * kCk + t) * ldo + static_cast<size_t>(h) * p.dv + j0 + r] =
-                    ao[0][e] + ao[1][e];
-        }
-        // S = gamma_C S + K~^T U, the two state tiles' chains interleaved
-        f32x4 acc[2] = {sreg[0] * bc.gC, sreg[1] * bc.gC};
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int e = 0; e < 4; ++e) {
+                const int t = 16 * w + 4 * g + e;
+                if (t < n)
+                    p.o[static_cast<size_t>(c * kCk + t) * ldo + static_cast<size_t>(h) * p.dv + j0 + 16 * ct + r] =
+                        ao[ct][e];
+            }
+        // S = gamma_C S + K~^T U (2 NCT independent accumulator chains)
+        f32x4 acc[NCT][2];
+#pragma unroll
+        for (int ct = 0; ct < NCT; ++ct) acc[ct][0] = sreg[ct][0] * bc.gC, acc[ct][1] = sreg[ct][1] * bc.gC;
 #pragma unroll
         for (int s = 0; s < kCk / 16; ++s) {
+            float4 ub[NCT];
+#pragma unroll
+            for (int ct = 0; ct < NCT; ++ct) ub[ct] = *reinterpret_cast<const float4*>(&ut_s[16 * ct + r][16 * s + 4 * g]);
 #pragma unroll
             for (int q = 0; q < 4; ++q)
 #pragma unroll
-                for (int tt = 0; tt < 2; ++tt) {
-                    const float4 ka = bc.ka[tt][s];
-                    const float av = q == 0 ? ka.x : q == 1 ? ka.y : q == 2 ? ka.z : ka.w;
-                    const float bv = q == 0 ? ub[s].x : q == 1 ? ub[s].y : q == 2 ? ub[s].z : ub[s].w;
-                    acc[tt] = mfma_f32_4(av, bv, acc[tt]);
-                }
+                for (int tt = 0; tt < 2; ++tt)
+#pragma unroll
+                    for (int ct = 0; ct < NCT; ++ct) {
+                        const float4 ka = bc.ka[tt][s];
+                        const float av = q == 0 ? ka.x : q == 1 ? ka.y : q == 2 ? ka.z : ka.w;
+                        const float bv = q == 0 ? ub[ct].x : q == 1 ? ub[ct].y : q == 2 ? ub[ct].z : ub[ct].w;
+                        acc[ct][tt] = mfma_f32_4(av, bv, acc[ct][tt]);
+                    }
         }
 #pragma unroll
-        for (int tt = 0; tt < 2; ++tt) {
-            sreg[tt] = acc[tt];
-            *reinterpret_cast<f32x4*>(&st_s[r][32 * w + 16 * tt + 4 * g]) = acc[tt];
-        }
+        for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+            for (int tt = 0; tt < 2; ++tt) {
+                sreg[ct][tt] = acc[ct][tt];
+                *reinterpret_cast<f32x4*>(&st_s[16 * ct + r][32 * w + 16 * tt + 4 * g]) = acc[ct][tt];
+            }
         lds_barrier();
     };
     // two operand sets in turn (no register copies between chunks, which would
     // wait for the prefetch)
-    CkOpsA a0, a1;
+    CkOpsA<NCT> a0, a1;
     CkOpsB b0, b1;
     load_a(0, a0);
     load_b(0, b0);
@@ -1176,7 +1197,11 @@ __global__ __launch_bounds__(256, 2) void gdn_pf_chunk_scan_kernel(GdnPfArgs p, 
     }
     if (c < nch) chunk(c, a0, b0, a1, b1);
 #pragma unroll
-    for (int tt = 0; tt < 2; ++tt) *reinterpret_cast<f32x4*>(Sg + 32 * w + 16 * tt + 4 * g) = sreg[tt];
+    for (int ct = 0; ct < NCT; ++ct)
+#pragma unroll
+        for (int tt = 0; tt < 2; ++tt)
+            *reinterpret_cast<f32x4*>(p.S + (static_cast<size_t>(h) * p.dv + j0 + 16 * ct + r) * kDK + 32 * w +
+                                      16 * tt + 4 * g) = sreg[ct][tt];
 }
 
 }  // namespace
@@ -1279,8 +1304,16 @@ void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_lo
         float* gc = ck + static_cast<size_t>(nv) * nch * kCkFloats;
         hipLaunchKernelGGL(gdn_pf_chunk_prep_kernel, dim3(nv, nch), dim3(256), 0, s, p, ck, gc, nch);
         check_launch("gdn_pf_chunk_prep_kernel");
-        hipLaunchKernelGGL(gdn_pf_chunk_scan_kernel, dim3(nv * (dv / kCkCols)), dim3(256), 0, s, p,
-                           static_cast<const float*>(ck), static_cast<const float*>(gc), nch);
+        static const int nct = [] {
+            const char* e = std::getenv("RL_PF_GDN_NCT");  // measurement override
+            return e && e[0] == '1' ? 1 : 2;
+        }();
+        if (nct == 2)
+            hipLaunchKernelGGL(gdn_pf_chunk_scan_kernel<2>, dim3(nv * (dv / 32)), dim3(256), 0, s, p,
+                               static_cast<const float*>(ck), static_cast<const float*>(gc), nch);
+        else
+            hipLaunchKernelGGL(gdn_pf_chunk_scan_kernel<1>, dim3(nv * (dv / 16)), dim3(256), 0, s, p,
+                               static_cast<const float*>(ck), static_cast<const float*>(gc), nch);
         check_launch("gdn_pf_chunk_scan_kernel");
         return;
     }
