@@ -112,8 +112,10 @@ int rl_hip_pack_act(const float* X, void* frag, int n, int T, void* stream);
 /* Prompt prefill: Y[t][ldy] (=, +=) W . x_t for T (any) tokens of rl_hip_pack_act
  * fragments, on the matrix cores (128 rows x 64 tokens per workgroup).  epilogue:
  * 0 store, 1 add, 2 SwiGLU over interleaved gate/up 16-row tiles (m/2 output rows),
- * 5 SwiGLU over the rl_hip_pack_fp8_gate_up half tiles (m/2 output rows).
- * ldy <= 0: m (m/2 for SwiGLU).  Replaces the reference's prefill linears
+ * 5 SwiGLU over the rl_hip_pack_fp8_gate_up half tiles (m/2 output rows), 6 the same
+ * written as rl_hip_pack_act fragments of the m/2 outputs (Y is then the fragment
+ * buffer, bit-identical to epilogue 5 followed by rl_hip_pack_act; m/2 a multiple of
+ * 128).  ldy <= 0: m (m/2 for SwiGLU).  Replaces the reference's prefill linears
  * (cuda_engine.cu:18338-18590 -> launch_linear for T > 8, :12008-12016). */
 int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                             int T, int epilogue, int ldy, void* stream);

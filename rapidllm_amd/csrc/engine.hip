@@ -403,16 +403,26 @@ class Engine {
                 }
                 rmsnorm_pack(pf_x_, H, Ly.ffn_norm, nullptr, pf_frag_, H, T, eps, st_);
                 pf_f16_src_ = nullptr;
-                if (Ly.gate_up.kind >= 0) {
+                // half-tile gate / up pairs write the down projection's input
+                // fragments directly when I fills whole 128-column blocks
+                const bool h_frag = I % 128 == 0;
+                float* hy = h_frag ? static_cast<float*>(pf_frag_h_) : pf_h_;
+                const int he = h_frag ? kEpiSwiGLUHFrag : kEpiSwiGLUH;
+                bool packed = false;
+                if (Ly.gate_up.kind >= 0 && Ly.gate_up.guh) {
+                    pf_linear(Ly.gate_up, pf_frag_, hy, I, I, T, he);
+                    packed = h_frag;
+                } else if (Ly.gate_up.kind >= 0) {
                     pf_linear(Ly.gate_up, pf_frag_, pf_h_, I, I, T, Ly.gate_up.swiglu_epi());
                 } else if (Ly.gate_cat) {
-                    pf_linear(Ly.gate, pf_frag_, pf_h_, I, I, T, kEpiSwiGLUH);
+                    pf_linear(Ly.gate, pf_frag_, hy, I, I, T, he);
+                    packed = h_frag;
                 } else {
                     pf_linear(Ly.gate, pf_frag_, pf_h_, I, I, T, kEpiStore);
                     pf_linear(Ly.up, pf_frag_, pf_u_, I, I, T, kEpiStore);
                     swiglu(pf_h_, I, pf_u_, I, pf_h_, I, T, st_);
                 }
-                pack_act(pf_h_, pf_frag_h_, I, T, st_);
+                if (!packed) pack_act(pf_h_, pf_frag_h_, I, T, st_);
                 pf_f16_src_ = nullptr;
                 pf_linear(Ly.down, pf_frag_h_, pf_x_, H, H, T, kEpiAdd);
             }

@@ -5,7 +5,17 @@
 
 namespace rl {
 
-enum GemmEpilogue { kEpiStore = 0, kEpiAdd = 1, kEpiSwiGLU = 2, kEpiPartial = 3, kEpiAddNorm = 4, kEpiSwiGLUH = 5 };
+enum GemmEpilogue {
+    kEpiStore = 0,
+    kEpiAdd = 1,
+    kEpiSwiGLU = 2,
+    kEpiPartial = 3,
+    kEpiAddNorm = 4,
+    kEpiSwiGLUH = 5,
+    // prefill only: SwiGLU over half tiles written straight as the next GEMM's bf16
+    // hi + mid input fragments (Y is the fragment buffer; outputs a multiple of 128)
+    kEpiSwiGLUHFrag = 6
+};
 
 // RMSNorm folded across a residual GEMM and the next linear (y = rmsnorm(x) * (1+g)
 // never materialised):

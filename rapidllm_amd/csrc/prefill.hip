@@ -180,7 +180,7 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
             }
             if constexpr (WK == 0) {
                 // C rows 4g..4g+3 of a half-tile matrix: gate (g < 2) or up scale
-                const float sc = EPI == 5 ? tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + (g >> 1)]
+                const float sc = (EPI == 5 || EPI == 6) ? tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + (g >> 1)]
                                           : tscale[static_cast<size_t>(rt) * n_kb + kb];
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += sc * acc[nt];
@@ -214,6 +214,24 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
                     const float up = __shfl_xor(tot[nt][r][v], 32, 64);
                     if (g < 2 && orow + v < m_valid) yrow[orow + v] = silu_f(tot[nt][r][v]) * up;
                 }
+            }
+        } else if constexpr (EPI == 6) {
+            // as 5; lanes g = 0 and 1 hold output rows 0..3 and 4..7 of the half tile,
+            // one 8-column fragment unit of the next GEMM's input, which lane g = 0
+            // writes (the same bf16 hi + mid split as pack_act)
+            i32x4* fo = reinterpret_cast<i32x4*>(Y);
+#pragma unroll
+            for (int r = 0; r < kPfRT; ++r) {
+                if (rt0 + r >= m_tiles) break;
+                float h8[8];
+#pragma unroll
+                for (int v = 0; v < 4; ++v) {
+                    const float up = __shfl_xor(tot[nt][r][v], 32, 64);
+                    h8[v] = silu_f(tot[nt][r][v]) * up;
+                }
+#pragma unroll
+                for (int v = 0; v < 4; ++v) h8[4 + v] = __shfl_xor(h8[v], 16, 64);
+                if (g == 0) write_frag8(fo, rt0 + r, tok, T, h8);
             }
         } else if constexpr (EPI == 2) {
 #pragma unroll
@@ -303,9 +321,13 @@ void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float
     RL_REQUIRE(W && frag && Y && ((wk != 0 && wk != 3) || ts) && (wk != 2 || W_lo) && (wk != 3 || xscale),
                RL_ERR_RANGE, "gemm_prefill: null pointer");
     RL_REQUIRE(wk >= 0 && wk <= 3, RL_ERR_RANGE, "gemm_prefill: weight kind");
-    RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU || epi == kEpiSwiGLUH, RL_ERR_RANGE,
-               "gemm_prefill: epilogue must be store, add or swiglu");
+    RL_REQUIRE(epi == kEpiStore || epi == kEpiAdd || epi == kEpiSwiGLU || epi == kEpiSwiGLUH ||
+                   epi == kEpiSwiGLUHFrag,
+               RL_ERR_RANGE, "gemm_prefill: epilogue must be store, add or swiglu");
     if (epi == kEpiSwiGLUH) RL_REQUIRE(m % 16 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows a multiple of 16");
+    if (epi == kEpiSwiGLUHFrag)
+        RL_REQUIRE(m % 256 == 0 && m_valid == m / 2, RL_ERR_RANGE,
+                   "gemm_prefill swiglu to fragments: outputs a multiple of 128");
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     if (epi == kEpiSwiGLU) RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows must be a multiple of 32");
     const int n_kb = (n + 127) / 128;
@@ -324,6 +346,7 @@ void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float
     RL_PF(kEpiStore, 1) RL_PF(kEpiAdd, 1) RL_PF(kEpiSwiGLU, 1) RL_PF(kEpiSwiGLUH, 1)
     RL_PF(kEpiStore, 2) RL_PF(kEpiAdd, 2) RL_PF(kEpiSwiGLU, 2) RL_PF(kEpiSwiGLUH, 2)
     RL_PF(kEpiStore, 3) RL_PF(kEpiAdd, 3) RL_PF(kEpiSwiGLU, 3) RL_PF(kEpiSwiGLUH, 3)
+    RL_PF(kEpiSwiGLUHFrag, 0) RL_PF(kEpiSwiGLUHFrag, 1) RL_PF(kEpiSwiGLUHFrag, 2) RL_PF(kEpiSwiGLUHFrag, 3)
 #undef RL_PF
 }
 
@@ -349,7 +372,7 @@ extern "C" {
 int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, const void* frag, float* Y, int m, int n,
                             int T, int epilogue, int ldy, void* stream) {
     return guard([&] {
-        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
+        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH || epilogue == kEpiSwiGLUHFrag ? m / 2 : m;
         rl::gemm_fp8_prefill(w_tiled, tile_scale, frag, Y, m, n, T, epilogue, ldy > 0 ? ldy : mv, mv, S(stream));
     });
 }
@@ -357,7 +380,7 @@ int rl_hip_gemm_fp8_prefill(const uint8_t* w_tiled, const float* tile_scale, con
 int rl_hip_gemm_bf16_prefill(const uint16_t* w_tiled, const uint16_t* w_lo_tiled, const void* frag, float* Y, int m,
                              int n, int T, int epilogue, int ldy, void* stream) {
     return guard([&] {
-        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
+        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH || epilogue == kEpiSwiGLUHFrag ? m / 2 : m;
         rl::gemm_prefill_any(w_lo_tiled ? 2 : 1, reinterpret_cast<const uint8_t*>(w_tiled),
                              reinterpret_cast<const uint8_t*>(w_lo_tiled), nullptr, frag, Y, m, n, T, epilogue,
                              ldy > 0 ? ldy : mv, mv, S(stream));
@@ -371,7 +394,7 @@ int rl_hip_act_frag_to_f16(const void* frag, void* frag16, float* xscale, int n,
 int rl_hip_gemm_f16_prefill(const void* w16, const float* tile_scale, const void* frag16, const float* xscale,
                             float* Y, int m, int n, int T, int epilogue, int ldy, void* stream) {
     return guard([&] {
-        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH ? m / 2 : m;
+        const int mv = epilogue == kEpiSwiGLU || epilogue == kEpiSwiGLUH || epilogue == kEpiSwiGLUHFrag ? m / 2 : m;
         rl::gemm_prefill_any(3, static_cast<const uint8_t*>(w16), nullptr, tile_scale, frag16, Y, m, n, T, epilogue,
                              ldy > 0 ? ldy : mv, mv, S(stream), xscale);
     });

@@ -48,6 +48,31 @@ def test_gemm_prefill_swiglu_half_tiles(gpu, orc, T, I):
         assert rel_l2(got[t], want[t]) <= REL_L2, (t, rel_l2(got[t], want[t]))
 
 
+@pytest.mark.parametrize("T,I", [(70, 256), (131, 384)])
+def test_gemm_prefill_swiglu_to_fragments(gpu, T, I):
+    """Epilogue 6 (SwiGLU half tiles written as the next GEMM's bf16 hi + mid
+    fragments) is byte-identical to epilogue 5 followed by rl_hip_pack_act."""
+    from rapidllm_amd.hip import DeviceBuffer, call
+    r = synth.rng(47 + I)
+    n = 512
+    lin = ops.Fp8GateUp(synth.fp8_weight(r, I, n), synth.fp8_scales(r, I, n), synth.fp8_weight(r, I, n),
+                        synth.fp8_scales(r, I, n))
+    X = r.standard_normal((T, n)).astype(np.float32)
+    xd = DeviceBuffer.from_numpy(X)
+    frag = ops.act_frag_buffer(n, T)
+    call("rl_hip_pack_act", xd.ptr, frag.ptr, n, T, None)
+    yd = DeviceBuffer(4 * T * I)
+    call("rl_hip_gemm_fp8_prefill", lin.w.ptr, lin.ts.ptr, frag.ptr, yd.ptr, 2 * I, n, T, 5, I, None)
+    want = ops.act_frag_buffer(I, T)
+    call("rl_hip_pack_act", yd.ptr, want.ptr, I, T, None)
+    got = ops.act_frag_buffer(I, T)
+    call("rl_hip_gemm_fp8_prefill", lin.w.ptr, lin.ts.ptr, frag.ptr, got.ptr, 2 * I, n, T, 6, I, None)
+    nb = (I // 128) * 16 * 2 * T * 16  # fragment units (block, i, g) x (hi, mid) x T x 16 B
+    a = got.numpy(np.uint8, (got.nbytes,))[:nb]
+    b = want.numpy(np.uint8, (want.nbytes,))[:nb]
+    assert np.array_equal(a, b)
+
+
 def test_gemm_prefill_add_and_swiglu(gpu, orc):
     r = synth.rng(41)
     T, n, I = 70, 768, 256
