@@ -224,7 +224,7 @@ int rl_hip_gdn_decode(const float* qkv, const float* a, const float* b, int ld_i
                       const float* S_in, float* S_out, float* o, int T, int nk, int nv, int dk, int dv, int conv_k,
                       int v_tiled, void* stream);
 
-/* Prompt prefill of T tokens (any T) for one DeltaNet layer, from the in_proj rows y
+/* Prompt prefill of T tokens (1..65535) for one DeltaNet layer, from the in_proj rows y
  * [T][ld] (qkv channels at 0, a at off_a, b at off_b): conv window conv_in ->
  * conv_out (window after the last token; must not alias), S (transposed, as
  * rl_hip_gdn_decode) updated in place, o [T][nv*dv] raw recurrent output.  Workspace

@@ -653,42 +653,60 @@ struct GdnPfArgs {
     int T, nk, nv, dv, conv_dim, v_tiled;
 };
 
-// One thread per (token, channel): the conv output of token t only needs the inputs
-// of tokens t-3 .. t (the window before the chunk for t < 3), so every token is
-// independent.  Threads of token T-1 also write the final window; threads past the
-// conv work form the gates of (t, head).
+// One thread per (channel, kPfConvTok consecutive tokens): the conv output of token t
+// only needs the inputs of tokens t-3 .. t (the window before the chunk for t < 3),
+// so token blocks are independent; within a block the 4-tap window slides in
+// registers (each input read once, the weights and incoming window once per block).
+// Grid (channel blocks, token blocks); the thread holding token T-1 also writes the
+// final window; threads past the conv channels form the gates of (t, head).
+constexpr int kPfConvTok = 16;
+
 __global__ __launch_bounds__(256) void gdn_pf_conv_kernel(GdnPfArgs p) {
-    const size_t i = static_cast<size_t>(blockIdx.x) * blockDim.x + threadIdx.x;
+    const int t0 = blockIdx.y * kPfConvTok, ch = blockIdx.x * blockDim.x + threadIdx.x;
+    const int nt = min(kPfConvTok, p.T - t0);
     constexpr int K = kConvK;
-    const size_t n_conv = static_cast<size_t>(p.T) * p.conv_dim;
-    if (i < n_conv) {
-        const int t = static_cast<int>(i / p.conv_dim), ch = static_cast<int>(i % p.conv_dim);
+    if (ch < p.conv_dim) {
         const float4 w4 = *reinterpret_cast<const float4*>(p.conv_w + static_cast<size_t>(ch) * K);
-        const float4 s4 = *reinterpret_cast<const float4*>(p.conv_in + static_cast<size_t>(ch) * K);
-        const float w[K] = {w4.x, w4.y, w4.z, w4.w};
-        const float st[K] = {s4.x, s4.y, s4.z, s4.w};
-        // window after token t: taps q = 0..3 hold inputs of tokens t-3+q
+        // window before token t0: inputs of tokens t0-4 .. t0-1 (taps of the incoming
+        // window for tokens before the chunk)
         float win[K];
+        {
+            const float4 s4 = *reinterpret_cast<const float4*>(p.conv_in + static_cast<size_t>(ch) * K);
+            const float st[K] = {s4.x, s4.y, s4.z, s4.w};
 #pragma unroll
-        for (int q = 0; q < K; ++q) {
-            const int tt = t - (K - 1) + q;
-            win[q] = tt >= 0 ? p.y[static_cast<size_t>(tt) * p.ld + ch] : st[q + t + 1];
+            for (int q = 0; q < K; ++q) {
+                const int tt = t0 - K + q;
+                win[q] = tt >= 0 ? p.y[static_cast<size_t>(tt) * p.ld + ch] : st[q];
+            }
         }
-        double acc = 0.0;
+        float in[kPfConvTok];
 #pragma unroll
-        for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
-        p.xc[i] = silu_f(static_cast<float>(acc));
-        if (t == p.T - 1)
-            *reinterpret_cast<float4*>(p.conv_out + static_cast<size_t>(ch) * K) =
-                make_float4(win[0], win[1], win[2], win[3]);
-    } else if (i < n_conv + static_cast<size_t>(p.T) * p.nv) {
-        const int k = static_cast<int>(i - n_conv);
-        const int t = k / p.nv, h = k % p.nv;
-        const float av = p.y[static_cast<size_t>(t) * p.ld + p.off_a + h];
-        const float bv = p.y[static_cast<size_t>(t) * p.ld + p.off_b + h];
-        const float g_log = -expf(p.A_log[h]) * softplus_f(av + p.dt_bias[h]);
-        p.gates[2 * static_cast<size_t>(k)] = expf(g_log);
-        p.gates[2 * static_cast<size_t>(k) + 1] = sigmoid_f(bv);
+        for (int j = 0; j < kPfConvTok; ++j) in[j] = j < nt ? p.y[static_cast<size_t>(t0 + j) * p.ld + ch] : 0.f;
+        const float w[K] = {w4.x, w4.y, w4.z, w4.w};
+#pragma unroll
+        for (int j = 0; j < kPfConvTok; ++j) {
+            if (j >= nt) break;
+            // window after token t0 + j: taps q hold inputs of tokens t0+j-3+q
+            win[0] = win[1], win[1] = win[2], win[2] = win[3], win[3] = in[j];
+            double acc = 0.0;
+#pragma unroll
+            for (int q = 0; q < K; ++q) acc += static_cast<double>(w[q]) * win[q];
+            p.xc[static_cast<size_t>(t0 + j) * p.conv_dim + ch] = silu_f(static_cast<float>(acc));
+            if (t0 + j == p.T - 1)
+                *reinterpret_cast<float4*>(p.conv_out + static_cast<size_t>(ch) * K) =
+                    make_float4(win[0], win[1], win[2], win[3]);
+        }
+    } else if (ch < p.conv_dim + p.nv) {
+        const int h = ch - p.conv_dim;
+        for (int j = 0; j < nt; ++j) {
+            const int t = t0 + j;
+            const size_t k = static_cast<size_t>(t) * p.nv + h;
+            const float av = p.y[static_cast<size_t>(t) * p.ld + p.off_a + h];
+            const float bv = p.y[static_cast<size_t>(t) * p.ld + p.off_b + h];
+            const float g_log = -expf(p.A_log[h]) * softplus_f(av + p.dt_bias[h]);
+            p.gates[2 * k] = expf(g_log);
+            p.gates[2 * k + 1] = sigmoid_f(bv);
+        }
     }
 }
 
@@ -1296,8 +1314,9 @@ void gdn_prefill(const float* y, int ld, int off_a, int off_b, const float* A_lo
     const int conv_dim = 2 * nk * dk + nv * dv;
     GdnPfArgs p{y, ld, off_a, off_b, A_log, dt_bias, conv_w, conv_in, conv_out, xc, gates, S, o,
                 T, nk, nv, dv, conv_dim, v_tiled};
-    const size_t n = static_cast<size_t>(T) * (conv_dim + nv);
-    hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3(static_cast<unsigned>((n + 255) / 256)), dim3(256), 0, s, p);
+    RL_REQUIRE(T <= 65535, RL_ERR_RANGE, "gdn_prefill: at most 65535 tokens per call");
+    hipLaunchKernelGGL(gdn_pf_conv_kernel, dim3((conv_dim + nv + 255) / 256, (T + kPfConvTok - 1) / kPfConvTok),
+                       dim3(256), 0, s, p);
     check_launch("gdn_pf_conv_kernel");
     if (ck && gdn_prefill_chunk_floats(T, nv, dk, dv) > 0) {
         const int nch = (T + kCk - 1) / kCk;

@@ -160,6 +160,46 @@ __global__ __launch_bounds__(64) void gnorm_pack_kernel(const float* __restrict_
     }
 }
 
+// The same for 128-wide heads with one gamma per head position: 16 lanes per head
+// (8 columns each, vector loads), 16 heads per 256-thread workgroup, grid
+// (heads / 16, T); the head's sum of squares in double over its 16 lanes.
+__global__ __launch_bounds__(256) void gnorm_pack128_kernel(const float* __restrict__ o, const float* __restrict__ z,
+                                                            int ld_z, const float* __restrict__ gamma,
+                                                            float* __restrict__ y, i32x4* __restrict__ frag, int n,
+                                                            int T, float eps) {
+    const int t = blockIdx.y, tid = threadIdx.x;
+    const int hh = blockIdx.x * 16 + (tid >> 4), u = tid & 15;
+    const bool ok = hh * 128 < n;  // whole 16-lane groups, so the shuffles below stay within valid groups
+    const int c0 = hh * 128 + 8 * u;
+    float ov[8], zv[8], gv[8];
+    double ss = 0.0;
+    if (ok) {
+        const float4* op = reinterpret_cast<const float4*>(o + static_cast<size_t>(t) * n + c0);
+        const float4* zp = reinterpret_cast<const float4*>(z + static_cast<size_t>(t) * ld_z + c0);
+        const float4 o0 = op[0], o1 = op[1], z0 = zp[0], z1 = zp[1];
+        ov[0] = o0.x, ov[1] = o0.y, ov[2] = o0.z, ov[3] = o0.w, ov[4] = o1.x, ov[5] = o1.y, ov[6] = o1.z, ov[7] = o1.w;
+        zv[0] = z0.x, zv[1] = z0.y, zv[2] = z0.z, zv[3] = z0.w, zv[4] = z1.x, zv[5] = z1.y, zv[6] = z1.z, zv[7] = z1.w;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+            gv[e] = gamma ? gamma[8 * u + e] : 1.f;
+            ss += static_cast<double>(ov[e]) * ov[e];
+        }
+    }
+#pragma unroll
+    for (int m = 1; m < 16; m <<= 1) ss += __shfl_xor(ss, m, 64);
+    if (!ok) return;
+    const float inv = 1.f / sqrtf(static_cast<float>(ss / 128) + eps);
+    float v[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = gv[e] * (ov[e] * inv) * silu_f(zv[e]);
+    if (y) {
+        float4* yp = reinterpret_cast<float4*>(y + static_cast<size_t>(t) * n + c0);
+        yp[0] = make_float4(v[0], v[1], v[2], v[3]);
+        yp[1] = make_float4(v[4], v[5], v[6], v[7]);
+    }
+    if (frag) write_frag8(frag, c0 >> 3, t, T, v);
+}
+
 // tokens[t] -> out[t][H]; kind: RL_Q_F32 / RL_Q_F16 / RL_Q_BF16 table [vocab][H].
 __global__ void embed_rows_kernel(const void* __restrict__ table, int kind, const int* __restrict__ tokens,
                                   float* __restrict__ out, int H, int vocab) {
@@ -235,6 +275,14 @@ void gnorm_pack(const float* o, const float* z, int ld_z, const float* gamma, in
     const int seg = per_head ? gamma_n : n;
     RL_REQUIRE(seg % 8 == 0 && T >= 1 && T <= 65535, RL_ERR_RANGE, "gnorm_pack: segment % 8 == 0, T in 1..65535");
     RL_REQUIRE(o && z && (y || frag), RL_ERR_RANGE, "gnorm_pack: null pointer");
+    const bool vec = reinterpret_cast<uintptr_t>(o) % 16 == 0 && reinterpret_cast<uintptr_t>(z) % 16 == 0 &&
+                     (!y || reinterpret_cast<uintptr_t>(y) % 16 == 0) && ld_z % 4 == 0;
+    if (per_head && seg == 128 && vec) {
+        hipLaunchKernelGGL(gnorm_pack128_kernel, dim3((n / 128 + 15) / 16, T), dim3(256), 0, s, o, z, ld_z, gamma, y,
+                           static_cast<i32x4*>(frag), n, T, eps);
+        check_launch("gnorm_pack128_kernel");
+        return;
+    }
     hipLaunchKernelGGL(gnorm_pack_kernel, dim3(n / seg, T), dim3(64), 0, s, o, z, ld_z, gamma, gamma_n,
                        per_head ? 1 : 0, y, static_cast<i32x4*>(frag), n, T, eps);
     check_launch("gnorm_pack_kernel");
