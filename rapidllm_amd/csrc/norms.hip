@@ -110,6 +110,59 @@ __global__ __launch_bounds__(kNormThreads) void residual_rmsnorm_kernel(const fl
     }
 }
 
+// RMSNorm + packing for many tokens (prefill): one wave per token, 4 tokens per
+// workgroup; lane l owns the 8-column units l, l + 64, ... (NU of them at most), all
+// loaded before the wave's double sum of squares (no LDS, no barrier).  Same
+// arithmetic per element as residual_rmsnorm_kernel without partials.
+template <int NU>
+__global__ __launch_bounds__(256) void rmsnorm_wave_kernel(const float* __restrict__ x, int ld_x,
+                                                           const float* __restrict__ gamma, float* __restrict__ y,
+                                                           i32x4* __restrict__ frag, int n, int T, float eps) {
+    const int t = blockIdx.x * 4 + (threadIdx.x >> 6), lane = threadIdx.x & 63;
+    if (t >= T) return;  // whole waves
+    const float* xt = x + static_cast<size_t>(t) * ld_x;
+    const int nu = n / 8;
+    const int units = ((n + kBlockCols - 1) / kBlockCols) * 16;
+    float v[NU][8];
+    double ss = 0.0;
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const int u = lane + 64 * k;
+        if (u < nu) {
+            const float4 a = reinterpret_cast<const float4*>(xt)[2 * u];
+            const float4 b = reinterpret_cast<const float4*>(xt)[2 * u + 1];
+            v[k][0] = a.x, v[k][1] = a.y, v[k][2] = a.z, v[k][3] = a.w;
+            v[k][4] = b.x, v[k][5] = b.y, v[k][6] = b.z, v[k][7] = b.w;
+        }
+    }
+#pragma unroll
+    for (int k = 0; k < NU; ++k)
+        if (lane + 64 * k < nu)
+#pragma unroll
+            for (int e = 0; e < 8; ++e) ss += static_cast<double>(v[k][e]) * v[k][e];
+    ss = wave_sum_d(ss);
+    const float inv = 1.f / sqrtf(static_cast<float>(ss / n) + eps);
+#pragma unroll
+    for (int k = 0; k < NU; ++k) {
+        const int u = lane + 64 * k;
+        if (u >= units) break;
+        float o[8];
+        if (u < nu) {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = v[k][e] * inv * (gamma ? 1.f + gamma[8 * u + e] : 1.f);
+            if (y) {
+                float4* yo = reinterpret_cast<float4*>(y + static_cast<size_t>(t) * n);
+                yo[2 * u] = make_float4(o[0], o[1], o[2], o[3]);
+                yo[2 * u + 1] = make_float4(o[4], o[5], o[6], o[7]);
+            }
+        } else {
+#pragma unroll
+            for (int e = 0; e < 8; ++e) o[e] = 0.f;
+        }
+        if (frag) write_frag8(frag, u, t, T, o);
+    }
+}
+
 // Gated RMSNorm + packing.  grid (segments, T), one wave per segment (a head when
 // per_head, else the whole vector).  seg % 8 == 0.
 __global__ __launch_bounds__(64) void gnorm_pack_kernel(const float* __restrict__ o, const float* __restrict__ z,
@@ -263,6 +316,24 @@ void rmsnorm_pack(const float* x, int ld_x, const float* gamma, float* y, void* 
     RL_REQUIRE(x && (y || frag), RL_ERR_RANGE, "rmsnorm_pack: null pointer");
     RL_REQUIRE(ld_x % 4 == 0, RL_ERR_RANGE, "rmsnorm_pack: row stride must be a multiple of 4");
     RL_REQUIRE(((n + kBlockCols - 1) / kBlockCols) * 16 <= kNormMaxUnits, RL_ERR_RANGE, "rmsnorm: n > 16384");
+    // prefill-sized T: one wave per token (the decode sizes keep the kernel below,
+    // so every decode step width uses the same summation order)
+    const int units = ((n + kBlockCols - 1) / kBlockCols) * 16;
+    const bool aligned = reinterpret_cast<uintptr_t>(x) % 16 == 0 && (!y || reinterpret_cast<uintptr_t>(y) % 16 == 0);
+    if (T >= 64 && aligned && units <= 64 * 12) {
+        const dim3 grid((T + 3) / 4);
+        if (units <= 64 * 4)
+            hipLaunchKernelGGL(rmsnorm_wave_kernel<4>, grid, dim3(256), 0, s, x, ld_x, gamma, y,
+                               static_cast<i32x4*>(frag), n, T, eps);
+        else if (units <= 64 * 8)
+            hipLaunchKernelGGL(rmsnorm_wave_kernel<8>, grid, dim3(256), 0, s, x, ld_x, gamma, y,
+                               static_cast<i32x4*>(frag), n, T, eps);
+        else
+            hipLaunchKernelGGL(rmsnorm_wave_kernel<12>, grid, dim3(256), 0, s, x, ld_x, gamma, y,
+                               static_cast<i32x4*>(frag), n, T, eps);
+        check_launch("rmsnorm_wave_kernel");
+        return;
+    }
     hipLaunchKernelGGL(residual_rmsnorm_kernel, dim3(T), dim3(kNormThreads), 0, s, x, ld_x, nullptr, 0, nullptr,
                        gamma, y, static_cast<i32x4*>(frag), n, T, eps);
     check_launch("residual_rmsnorm_kernel");
