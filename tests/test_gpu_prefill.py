@@ -247,6 +247,25 @@ def test_gdn_prefill_chunked_vs_per_token(gpu, orc, monkeypatch, T, decay):
         assert np.array_equal(conv, conv_ref)
 
 
+def test_gdn_prefill_chunked_full_shape(gpu, monkeypatch):
+    """At the 27B DeltaNet shape (16 k-heads, 48 v-heads) over a full 2048-token
+    prefill chunk, the chunked scan and the per-token scan (each pinned to the
+    per-token oracle at smaller sizes above) agree on every output row and on the
+    final state."""
+    from tests.test_gpu_layers import _gdn_case
+    T, nk, nv = 2048, 16, 48
+    case = _gdn_case(synth.rng(950), T, nk, nv, False)
+    monkeypatch.setenv("RL_PF_GDN_CHUNK", "1")
+    o1, S1, c1 = ops.gdn_prefill(*case, nk, nv, False)
+    monkeypatch.setenv("RL_PF_GDN_CHUNK", "0")
+    o0, S0, c0 = ops.gdn_prefill(*case, nk, nv, False)
+    assert np.isfinite(o1).all() and np.isfinite(S1).all()
+    err = np.linalg.norm(o1 - o0, axis=1) / np.maximum(np.linalg.norm(o0, axis=1), 1e-30)
+    assert err.max() < 1e-4, (int(err.argmax()), float(err.max()))
+    assert rel_l2(S1, S0) < 1e-5
+    assert np.array_equal(c1, c0)
+
+
 @pytest.mark.parametrize("qt,m,n,T", [(ops.Q4_K, 256, 1024, 70), (ops.Q6_K, 160, 768, 130),
                                       (ops.Q4_K, 5120, 4096, 300)])
 def test_kquant_prefill_gemm_vs_oracle(gpu, orc, qt, m, n, T):
