@@ -379,18 +379,19 @@ def test_kquant_f16_prefill_gemm_vs_oracle(gpu, orc, qt, m, n, T, epi):
         assert rel_l2(got[t], want) <= REL_L2, (t, rel_l2(got[t], want))
 
 
-@pytest.mark.parametrize("quant", ["q4_k", "q6_k"])
+@pytest.mark.parametrize("quant", ["q4_k", "q6_k", "bf16"])
 def test_engine_kquant_chunked_prefill_matches_oracle(gpu, orc, monkeypatch, quant):
-    """A GGUF-style model (K-quant layer linears, BF16 a / b rows, Q6_K lm_head)
-    prefills a 300-token prompt through the chunked path (two chunks of 256 + the
-    decode-step tail): logits and decoding continue as the oracle's."""
+    """A GGUF-style model (K-quant layer linears, BF16 a / b rows, Q6_K lm_head), or
+    a model with BF16 layer linears, prefills a 300-token prompt through the chunked
+    path (two chunks of 256 + the decode-step tail): logits and decoding continue as
+    the oracle's."""
     from oracle.oracle import OracleModel
     from rapidllm_amd import model as M
     from rapidllm_amd.engine import Engine
     from tests.test_gpu_engine import margin_ok, mini_spec
     spec = mini_spec()
-    W = M.random_weights(spec, seed=13, linear_quant=M.Q_Q4_K if quant == "q4_k" else M.Q_Q6_K,
-                         head_quant=M.Q_Q6_K)
+    lq = {"q4_k": M.Q_Q4_K, "q6_k": M.Q_Q6_K, "bf16": M.Q_BF16}[quant]
+    W = M.random_weights(spec, seed=13, linear_quant=lq, head_quant=M.Q_BF16 if quant == "bf16" else M.Q_Q6_K)
     monkeypatch.setenv("RL_PREFILL_CHUNK", "256")
     eng = Engine(spec, W, ctx=1024)
     orc_m = OracleModel(spec, W, ctx=1024)
