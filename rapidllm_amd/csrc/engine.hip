@@ -218,7 +218,7 @@ class Engine {
     // steps the committed state through it in registers (gdn_prefill; the conv
     // window ping-pongs between ring slots 0 and 1), attention is the causal prefill kernel (which
     // also writes the chunk's K/V).  RMSNorms are explicit (norm + pack kernels).
-    static constexpr int kPfChunk = 2048;
+    static constexpr int kPfChunk = 4096;
     static constexpr int kPfMinTokens = 16;
     int pf_cap_ = 0;
     float *pf_x_ = nullptr, *pf_y_ = nullptr, *pf_o_ = nullptr, *pf_h_ = nullptr, *pf_xc_ = nullptr,
