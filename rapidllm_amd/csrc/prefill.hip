@@ -87,20 +87,44 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
         tokcv[nt] = min(tokv[nt], T - 1);
     }
     const int NC = 2 * T;
+    // the input fragments as a buffer resource (gfx9 raw dword buffer; the host keeps
+    // them under 4 GiB) and the byte offset of the unit of (k-step i, lane group g,
+    // token) within a column block
+    const __amdgpu_buffer_rsrc_t frsrc = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<i32x4*>(frag), 0, static_cast<int>(static_cast<uint32_t>(n_kb) * 16u * 2u * T * 16u), 0x00020000);
+    uint32_t boff[kPfNT][4];
+#pragma unroll
+    for (int nt = 0; nt < kPfNT; ++nt)
+#pragma unroll
+        for (int i = 0; i < 4; ++i) boff[nt][i] = static_cast<uint32_t>((i * 4 + g) * NC + tokcv[nt]) * 16u;
 
     __shared__ i32x4 wl[2][kMat][kPfRT][kCh][64];  // [buffer][matrix][row tile][16-B chunk][lane]
 
-    // staging: unit u = (matrix, row tile, chunk, lane), kUnits per thread
+    // staging: unit u = (matrix, row tile, chunk, lane), kUnits per thread.  Every
+    // address is a uniform base for the column block plus a loop-invariant 32-bit
+    // lane offset (the host keeps weights and fragments under 4 GiB), so the loads
+    // take the scalar-base form with no 64-bit address arithmetic per iteration.
+    uint32_t woff[kUnits];
+#pragma unroll
+    for (int q = 0; q < kUnits; ++q) {
+        const int u = tid + 256 * q;
+        const int l = u & 63, c = (u >> 6) % kCh, r = (u / (64 * kCh)) % kPfRT;
+        const int rt = min(rt0 + r, m_tiles - 1);
+        woff[q] = static_cast<uint32_t>(rt) * static_cast<uint32_t>(n_kb * kTileB) + c * 1024 + 16 * l;
+    }
+    // weights as buffer resources too (non-temporal loads: aux bit 1)
+    const int wbytes = static_cast<int>(static_cast<uint32_t>(m_tiles) * static_cast<uint32_t>(n_kb * kTileB));
+    const __amdgpu_buffer_rsrc_t wrsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(W), 0, wbytes, 0x00020000);
+    const __amdgpu_buffer_rsrc_t wlrsrc =
+        __builtin_amdgcn_make_buffer_rsrc(const_cast<uint8_t*>(kMat > 1 ? W_lo : W), 0, wbytes, 0x00020000);
     i32x4 stg[kUnits];
     auto stage_load = [&](int kb) {
 #pragma unroll
         for (int q = 0; q < kUnits; ++q) {
-            const int u = tid + 256 * q;
-            const int l = u & 63, c = (u >> 6) % kCh, r = (u / (64 * kCh)) % kPfRT, mat = u / (64 * kCh * kPfRT);
-            const int rt = min(rt0 + r, m_tiles - 1);
-            const uint8_t* base = mat ? W_lo : W;
-            stg[q] = __builtin_nontemporal_load(reinterpret_cast<const i32x4*>(
-                base + (static_cast<size_t>(rt) * n_kb + kb) * kTileB + c * 1024 + 16 * l));
+            const int mat = (tid + 256 * q) / (64 * kCh * kPfRT);
+            stg[q] = __builtin_amdgcn_raw_buffer_load_b128(mat ? wlrsrc : wrsrc, static_cast<int>(woff[q]),
+                                                           kb * kTileB, 2);
         }
     };
     auto stage_store = [&](int buf) {
@@ -131,13 +155,15 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
 #pragma unroll
             for (int nt = 0; nt < kPfNT; ++nt) xs[nt] = xscale[static_cast<size_t>(kb) * T + tokcv[nt]];
         }
+        // buffer loads: the column block's offset as the scalar offset, the lane's
+        // as the vector offset (no per-load address arithmetic)
+        const int kbo = kb * 16 * NC * 16;
 #pragma unroll
         for (int nt = 0; nt < kPfNT; ++nt)
 #pragma unroll
             for (int i = 0; i < 4; ++i) {
-                const size_t u = (static_cast<size_t>(kb * 4 + i) * 4 + g) * NC + tokcv[nt];
-                bh[nt][i] = frag[u];
-                bm[nt][i] = frag[u + T];
+                bh[nt][i] = __builtin_amdgcn_raw_buffer_load_b128(frsrc, static_cast<int>(boff[nt][i]), kbo, 0);
+                bm[nt][i] = __builtin_amdgcn_raw_buffer_load_b128(frsrc, static_cast<int>(boff[nt][i]), kbo + 16 * T, 0);
             }
 #pragma unroll
         for (int r = 0; r < kPfRT; ++r) {
@@ -180,8 +206,14 @@ __global__ __launch_bounds__(256) void gemm_prefill_kernel(const uint8_t* __rest
             }
             if constexpr (WK == 0) {
                 // C rows 4g..4g+3 of a half-tile matrix: gate (g < 2) or up scale
-                const float sc = (EPI == 5 || EPI == 6) ? tscale[(static_cast<size_t>(rt) * n_kb + kb) * 2 + (g >> 1)]
-                                          : tscale[static_cast<size_t>(rt) * n_kb + kb];
+                // (rt, kb) is uniform: the scales are scalar loads; the lane picks its half's
+                float sc;
+                if constexpr (EPI == 5 || EPI == 6) {
+                    const float2 s2 = *reinterpret_cast<const float2*>(tscale + (static_cast<size_t>(rt) * n_kb + kb) * 2);
+                    sc = g >= 2 ? s2.y : s2.x;
+                } else {
+                    sc = tscale[static_cast<size_t>(rt) * n_kb + kb];
+                }
 #pragma unroll
                 for (int nt = 0; nt < kPfNT; ++nt) tot[nt][r] += sc * acc[nt];
             } else if constexpr (WK == 3) {
@@ -331,6 +363,10 @@ void gemm_prefill_any(int wk, const uint8_t* W, const uint8_t* W_lo, const float
     const int m_tiles = (m + kTileRows - 1) / kTileRows;
     if (epi == kEpiSwiGLU) RL_REQUIRE(m % 32 == 0, RL_ERR_RANGE, "gemm_prefill swiglu: rows must be a multiple of 32");
     const int n_kb = (n + 127) / 128;
+    // the kernel addresses weights and fragments with 32-bit offsets
+    RL_REQUIRE(static_cast<size_t>(m_tiles) * n_kb * (wk == 0 ? 2048 : 4096) < (size_t{1} << 32) &&
+                   static_cast<size_t>(n_kb) * 16 * 2 * T * 16 < (size_t{1} << 32),
+               RL_ERR_RANGE, "gemm_prefill: weights and input fragments must each stay under 4 GiB");
     const int rt = wk == 0 ? 8 : 4;
     const dim3 grid((m_tiles + rt - 1) / rt, (T + kPfTok - 1) / kPfTok);
     RL_REQUIRE(grid.y <= 65535, RL_ERR_RANGE, "gemm_prefill: too many tokens");
