@@ -36,19 +36,22 @@ PF_TOKENS = 4096
 def measure_gguf_step(spec, K, W):
     """The same C5 step with the layer linears and MTP fc as Q4_K super-blocks and a
     Q6_K lm_head (the tensor mix of a Q4_K_M GGUF; in_proj a/b BF16), random blocks
-    generated on the device: T=1 and T=4 step times, the batch-4 step (four
-    sequences at 32K context) and the weight bytes a T=1 step reads."""
+    generated on the device: T=1 and T=4 step times, the batch-4 and batch-8 steps
+    (sequences at 32K context, one weight pass each) and the weight bytes a T=1 step
+    reads."""
     from rapidllm_amd.engine import Engine
 
     os.environ["RL_SYNTH_LINEAR"] = "q4_k"
     try:
-        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321, max_batch=4)
+        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321, max_batch=8)
     finally:
         del os.environ["RL_SYNTH_LINEAR"]
     eng.synthetic_context(CTX)
-    eng.replicate_slot0(4)
+    eng.replicate_slot0(8)
     eng.time_batch(4, W)
     tb4 = eng.time_batch(4, K) / K
+    eng.time_batch(8, W)
+    tb8 = eng.time_batch(8, K) / K
     eng.synthetic_context(CTX)
     eng.time_steps(1, W)
     t1 = eng.time_steps(1, K) / K
@@ -81,6 +84,7 @@ def measure_gguf_step(spec, K, W):
             "t4_over_t1": round(t4 / t1, 4), "t1_bytes": int(total),
             "t1_GBps": round(total / t1 / 1e6, 1), "t1_frac": round(total / t1 / 1e6 / PEAK_GBS, 4),
             "batch4_step_ms": round(tb4, 4), "batch4_tok_s": round(4000.0 / tb4, 3),
+            "batch8_step_ms": round(tb8, 4), "batch8_tok_s": round(8000.0 / tb8, 3),
             "prefill_tokens": PF_TOKENS, "prefill_ms": round(pf_s * 1e3, 1),
             "prefill_tok_s": round(PF_TOKENS / pf_s, 1),
             "prefill_speedup_vs_verify_chunks": round((PF_TOKENS / pf_s) / (4000.0 / t4), 2)}
@@ -324,7 +328,7 @@ def measure_configs(spec, gemm_t1, gemm_t4, iters=30, rotate_bytes=768 << 20):
                                         "frac": frac(b, us)}
     del lin, copies, xd, frag, yd, ptrs
 
-    # C2: GGUF Q4_K / Q6_K GEMV, W [5120 x 17408], T = 1 (and T = 4)
+    # C2: GGUF Q4_K / Q6_K GEMV, W [5120 x 17408], T = 1 (and T = 4, 8)
     m, n = 5120, 17408
     for name, qt, gen, bb in (("q4_k", ops.Q4_K, synth.q4k_blocks, 144), ("q6_k", ops.Q6_K, synth.q6k_blocks, 210)):
         lin = ops.KQuantLinear(qt, gen(r, m, n), m, n)
@@ -334,7 +338,7 @@ def measure_configs(spec, gemm_t1, gemm_t4, iters=30, rotate_bytes=768 << 20):
             call("rl_hip_memcpy_d2d", c.ptr, lin.w.ptr, nb, s)
         ptrs = (C.c_void_p * len(copies))(*[c.ptr for c in copies])
         res = {}
-        for T in (1, 4):
+        for T in (1, 4, 8):
             xd = DeviceBuffer.from_numpy(r.standard_normal((T, n)).astype(np.float32))
             yd = DeviceBuffer(4 * T * m)
             ws = ops.kquant_workspace(m, n, T)

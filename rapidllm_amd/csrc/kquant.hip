@@ -1,4 +1,4 @@
-// kquant.hip -- GGUF Q4_K / Q6_K dequantisation and dequant-dot GEMV (T = 1..4).
+// kquant.hip -- GGUF Q4_K / Q6_K dequantisation and dequant-dot GEMV (T = 1..8).
 //
 // Dequant follows the reference CPU exactly (bit-exact, no FMA contraction):
 //   Q4_K (ops.cpp:245-284): w = (d * sc_j) * q - (dmin * m_j), each product rounded
@@ -136,6 +136,9 @@ __device__ inline i32x4 pack_i8x16(const int (&v)[16]) {
 // group's last ticket resets it, so every launch finds them zero.  Launches that
 // share one workspace must not overlap in time.
 inline size_t kq_ticket_bytes(int groups) { return (static_cast<size_t>(groups) * 64 + 255) / 256 * 256; }
+// Token groups of a launch: T <= 4 tokens in one, T = 5..8 in two groups of four
+// (each with its own tickets).
+inline int kq_token_groups(int T) { return (T + 3) / 4; }
 
 // Target of the pipeline's idle load slots (never written).
 constexpr int kKqDummyWindows = 64;
@@ -161,8 +164,9 @@ __host__ __device__ constexpr int kq_lds_bytes(int P, int nset, int T) {
 // holds row r at columns 32 g .. 32 g + 31 of each 128-column block (four 16-byte
 // chunks); waves take blocks w, w + 4, ...; lane groups summed by shuffles, waves
 // in order through LDS.
+// Tokens t0 .. t0 + tn - 1 of Tg (the launch's token group; T = 4 per group when Tg > 4).
 template <int T, int NRM>
-__device__ void kq_ab_rows(const KqNorm& nrm, const float* __restrict__ x, int n, int u) {
+__device__ void kq_ab_rows(const KqNorm& nrm, const float* __restrict__ x, int n, int u, int t0, int tn, int Tg) {
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, r16 = lane & 15;
@@ -182,7 +186,8 @@ __device__ void kq_ab_rows(const KqNorm& nrm, const float* __restrict__ x, int n
         for (int c4 = 0; c4 < 4; ++c4) w[c4] = *reinterpret_cast<const i32x4*>(tile + c4 * 1024 + 16 * lane);
 #pragma unroll
         for (int t = 0; t < T; ++t) {
-            const float4* xp = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + kb * 128 + 32 * g);
+            if (t >= tn) break;
+            const float4* xp = reinterpret_cast<const float4*>(x + static_cast<size_t>(t0 + t) * n + kb * 128 + 32 * g);
             float s0 = 0.f, s1 = 0.f;
 #pragma unroll
             for (int c4 = 0; c4 < 4; ++c4) {
@@ -202,9 +207,9 @@ __device__ void kq_ab_rows(const KqNorm& nrm, const float* __restrict__ x, int n
     if constexpr (NRM == 1) {
         // token w's 1/rms from the input's partial sums (groups in order, then a
         // fixed butterfly), as the K-quant rows
-        if (wave < T) {
+        if (wave < tn) {
             double ss = 0.0;
-            for (int gi = lane; gi < nrm.groups_in; gi += 64) ss += static_cast<double>(nrm.ss_in[gi * T + wave]);
+            for (int gi = lane; gi < nrm.groups_in; gi += 64) ss += static_cast<double>(nrm.ss_in[gi * Tg + t0 + wave]);
             ss = wave_sum_d(ss);
             if (lane == 0) inv_s[wave] = 1.f / sqrtf(static_cast<float>(ss / nrm.n_norm) + nrm.eps);
         }
@@ -216,13 +221,13 @@ __device__ void kq_ab_rows(const KqNorm& nrm, const float* __restrict__ x, int n
         if (g == 0) red[wave][t][r16] = acc[t];
     }
     __syncthreads();
-    if (static_cast<int>(threadIdx.x) < T * 16) {
+    if (static_cast<int>(threadIdx.x) < tn * 16) {
         const int t = threadIdx.x / 16, r = threadIdx.x % 16;
         const int row = rt * 16 + r;
         float v = ((red[0][t][r] + red[1][t][r]) + red[2][t][r]) + red[3][t][r];
         if constexpr (NRM == 1) v *= inv_s[t];
         (void)inv;
-        if (row < nrm.ab_rows) nrm.ab_out[(static_cast<size_t>(sl) * T + t) * nrm.ab_ld + row] = v;
+        if (row < nrm.ab_rows) nrm.ab_out[(static_cast<size_t>(sl) * Tg + t0 + t) * nrm.ab_ld + row] = v;
     }
 }
 
@@ -241,14 +246,24 @@ template <int QT, int T, int D, int RW, int NRM = 0>
 __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restrict__ W, const float* __restrict__ x,
                                                       float* __restrict__ Y, float* __restrict__ partial,
                                                       unsigned* __restrict__ tickets, int m, int n, int S,
-                                                      int accumulate, int ldy, KqNorm nrm) {
+                                                      int accumulate, int ldy, KqNorm nrm, int Tg, int nb) {
     using F = KFmt<QT>;
     constexpr int NSET = (T + 1) / 2;  // token sets of two (hi, mid, hi, mid columns)
+    // Token groups: Tg tokens (rows of x) in groups of T; the workgroups of one
+    // (row group, slice) for each group are blockIdx 8 apart, so they run on one XCD
+    // (workgroups go to the XCDs round-robin) and read the same weight tiles at about
+    // the same time: the second read hits that XCD's L2.  Each group runs the
+    // T-token kernel on its own rows: every token's sums are those of a launch with
+    // that token alone.  nb workgroups per group (kq_grid_x); the padding exits.
+    const int ngrp = (Tg + T - 1) / T;
+    const int tgi = (blockIdx.x / 8) % ngrp, bix = (blockIdx.x / (8 * ngrp)) * 8 + blockIdx.x % 8;
+    const int t0 = tgi * T, tn = min(T, Tg - t0);  // this workgroup's tokens t0 .. t0 + tn - 1
+    if (ngrp > 1 && bix >= nb) return;
     if constexpr (NRM < 2) {
         // extra workgroups past the K-quant ones: the BF16 rows (KqNorm::ab_w)
         const int ab_wgs = nrm.ab_w ? ((nrm.ab_rows + 15) / 16) * nrm.ab_slices : 0;
-        if (static_cast<int>(blockIdx.x) >= static_cast<int>(gridDim.x) - ab_wgs) {
-            kq_ab_rows<T, NRM>(nrm, x, n, blockIdx.x - (gridDim.x - ab_wgs));
+        if (bix >= nb - ab_wgs) {
+            kq_ab_rows<T, NRM>(nrm, x, n, bix - (nb - ab_wgs), t0, tn, Tg);
             return;
         }
     }
@@ -256,8 +271,8 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     const int lane = threadIdx.x & 63;
     const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
     const int g = lane >> 4, r16 = lane & 15;
-    const int rgp = blockIdx.x / S;
-    const int slice = blockIdx.x % S;
+    const int rgp = bix / S;
+    const int slice = bix % S;
     const int nsb = n / 256;
     const int per_slice = (nsb + S - 1) / S;
     const int s0 = min(nsb, slice * per_slice), s1 = min(nsb, s0 + per_slice);
@@ -280,7 +295,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     // queue every wave on one L2 channel).
     i32x4 buf[D][NL];
     uint32_t dbits[D];
-    const uint8_t* dummy = g_kq_dummy + ((blockIdx.x * RW + wave) % kKqDummyWindows) * 4096;
+    const uint8_t* dummy = g_kq_dummy + ((bix * RW + wave) % kKqDummyWindows) * 4096;
     auto load = [&](int d, int sb, bool live) {
         const uint8_t* tile = live ? tiles + static_cast<size_t>(sb) * F::kTileBytes : dummy;
 #pragma unroll
@@ -294,12 +309,12 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     // folded input RMSNorm: wave w < T holds token w's partial sums of squares
     // (group l + 64k in lane l), reduced in the epilogue
     float ssr[NRM == 1 ? kKqMaxSsPerLane : 1];
-    const bool ss_wave = NRM == 1 && wave < T;
+    const bool ss_wave = NRM == 1 && wave < tn;
     if constexpr (NRM == 1) {
 #pragma unroll
         for (int k = 0; k < kKqMaxSsPerLane; ++k) {
             const int gi = lane + 64 * k;
-            ssr[k] = ss_wave && gi < nrm.groups_in ? nrm.ss_in[static_cast<size_t>(gi) * T + wave] : 0.f;
+            ssr[k] = ss_wave && gi < nrm.groups_in ? nrm.ss_in[static_cast<size_t>(gi) * Tg + t0 + wave] : 0.f;
         }
     }
 
@@ -311,7 +326,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         if (threadIdx.x == 0) *zero16 = i32x4{0, 0, 0, 0};
         // items (token, sbl, r): the 16-value run r of the super-block; the two runs
         // of a 32-value block sit in adjacent lanes
-        const int items = T * P * 16;
+        const int items = tn * P * 16;
         // at most kPer items per thread: every item's x loads are issued before the
         // first item is processed (one memory round trip for the whole build)
         constexpr int kPer = (T * kKqMaxSlice * 16 + 64 * RW - 1) / (64 * RW);
@@ -326,11 +341,11 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
             if constexpr (NRM == 3) bs4[k] = make_float4(0.f, 0.f, 0.f, 0.f);
             if (it < items && sbl < nsl) {
                 const int col = (s0 + sbl) * 256 + 16 * r;
-                const float4* px = reinterpret_cast<const float4*>(x + static_cast<size_t>(t) * n + col);
+                const float4* px = reinterpret_cast<const float4*>(x + static_cast<size_t>(t0 + t) * n + col);
 #pragma unroll
                 for (int q = 0; q < 4; ++q) xv[k][q] = px[q];
                 if constexpr (NRM == 3)
-                    bs4[k] = *reinterpret_cast<const float4*>(nrm.bss + (static_cast<size_t>(col >> 7) * T + t) * 4);
+                    bs4[k] = *reinterpret_cast<const float4*>(nrm.bss + (static_cast<size_t>(col >> 7) * Tg + t0 + t) * 4);
             }
         }
         // the first weights are requested after the x loads and before the build:
@@ -525,22 +540,23 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     }
     const int te = g;  // this lane's token
     const int row = rt * kTR + r16;
-    const bool own = wave_live && te < T && row < m;
+    const bool own = wave_live && te < tn && row < m;
+    const int tw = t0 + te;  // the token's row of x / Y
     __shared__ int s_last;
     float v = tot[0];
 #pragma unroll
     for (int t = 1; t < T; ++t) v = te == t ? tot[t] : v;
     // the row's old value (accumulate) is requested now, so its round trip overlaps
     // the ticket and the partial loads
-    const float y_old = own && accumulate ? Y[static_cast<size_t>(te) * ldy + row] : 0.f;
+    const float y_old = own && accumulate ? Y[static_cast<size_t>(tw) * ldy + row] : 0.f;
     if (S > 1) {
         if (own)
-            __hip_atomic_store(partial + (static_cast<size_t>(slice) * T + te) * m + row, v, __ATOMIC_RELAXED,
+            __hip_atomic_store(partial + (static_cast<size_t>(slice) * Tg + tw) * m + row, v, __ATOMIC_RELAXED,
                                __HIP_MEMORY_SCOPE_AGENT);
         asm volatile("s_waitcnt vmcnt(0)" ::: "memory");  // partial stores complete before the ticket
         __syncthreads();
         if (threadIdx.x == 0) {
-            unsigned* tk = tickets + static_cast<size_t>(rgp) * 16;
+            unsigned* tk = tickets + (static_cast<size_t>(rgp) * ngrp + tgi) * 16;
             const unsigned old = __hip_atomic_fetch_add(tk, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
             const int last = old == static_cast<unsigned>(S - 1);
             if (last) __hip_atomic_store(tk, 0u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
@@ -556,7 +572,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
                 float pv[8];
 #pragma unroll
                 for (int j = 0; j < 8; ++j)
-                    pv[j] = q0 + j < S ? __hip_atomic_load(partial + (static_cast<size_t>(q0 + j) * T + te) * m + row,
+                    pv[j] = q0 + j < S ? __hip_atomic_load(partial + (static_cast<size_t>(q0 + j) * Tg + tw) * m + row,
                                                            __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT)
                                        : 0.f;
 #pragma unroll
@@ -581,18 +597,18 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         }
         __syncthreads();
     }
-    float y = NRM == 1 ? v * s_inv[te < T ? te : 0] : v;
+    float y = NRM == 1 ? v * s_inv[te < tn ? te : 0] : v;
     if (NRM < 2 && nrm.swiglu) {
         // gate / up half tiles: tile rows 8..15 are the up rows of rows 0..7, so
         // lane r16 < 8 pairs its gate value with lane r16 + 8's up value
         // (silu(g) * u, reference ops.cpp:607-609)
         const float u = __shfl_down(y, 8, 64);
-        if (own && r16 < 8) Y[static_cast<size_t>(te) * ldy + rt * 8 + r16] = y / (1.f + expf(-y)) * u;
+        if (own && r16 < 8) Y[static_cast<size_t>(tw) * ldy + rt * 8 + r16] = y / (1.f + expf(-y)) * u;
         return;
     }
     if (own) {
         y = accumulate ? y_old + y : y;
-        Y[static_cast<size_t>(te) * ldy + row] = y;
+        Y[static_cast<size_t>(tw) * ldy + row] = y;
     }
     if constexpr (NRM >= 2) {
         // residual add fused with the next RMSNorm's data: the row group's sum of
@@ -602,24 +618,24 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
         double sq = own ? static_cast<double>(y) * y : 0.0;
 #pragma unroll
         for (int o = 1; o < 16; o <<= 1) sq += __shfl_xor(sq, o, 64);
-        if (r16 == 0 && te < T) s_sq[wave][te] = sq;
+        if (r16 == 0 && te < tn) s_sq[wave][te] = sq;
         if (own) {
             const float xg = y * (1.f + nrm.gamma_out[row]);
-            nrm.xg_out[static_cast<size_t>(te) * m + row] = xg;
+            nrm.xg_out[static_cast<size_t>(tw) * m + row] = xg;
             if (nrm.frag_out) {
                 uint16_t* f16 = static_cast<uint16_t*>(nrm.frag_out);
                 uint16_t hi, mid;
                 split_bf16(xg, hi, mid);
-                const size_t u = frag_unit(row >> 3, te, T);
+                const size_t u = frag_unit(row >> 3, tw, Tg);
                 f16[u * 8 + (row & 7)] = hi;
-                f16[(u + T) * 8 + (row & 7)] = mid;
+                f16[(u + Tg) * 8 + (row & 7)] = mid;
             }
         }
         __syncthreads();
-        if (static_cast<int>(threadIdx.x) < T) {
+        if (static_cast<int>(threadIdx.x) < tn) {
             double sq = 0.0;
             for (int w = 0; w < RW; ++w) sq += s_sq[w][threadIdx.x];
-            nrm.ss_out[static_cast<size_t>(rgp) * T + threadIdx.x] = static_cast<float>(sq);
+            nrm.ss_out[static_cast<size_t>(rgp) * Tg + t0 + threadIdx.x] = static_cast<float>(sq);
         }
     }
 }
@@ -860,49 +876,55 @@ void kq_split(int m, int nsb, int& S) {
     S = std::min(S, nsb);
 }
 
+// T tokens per workgroup; Tg (> T only for T = 4) tokens in groups of T, one
+// workgroup per group for each (row group, slice).
 template <int QT, int T, int RW, int NRM>
 void launch_kq_rw(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int S,
-                  int accumulate, int ldy, hipStream_t s, const KqNorm& nrm) {
+                  int accumulate, int ldy, hipStream_t s, const KqNorm& nrm, int Tg) {
     const int groups = (m + kTR * RW - 1) / (kTR * RW);
     const int P = (n / 256 + S - 1) / S;
     const size_t lds = kq_lds_bytes<QT>(P, (T + 1) / 2, T);
     const int ab_wgs = nrm.ab_w ? ((nrm.ab_rows + 15) / 16) * nrm.ab_slices : 0;
-    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW, NRM>), dim3(groups * S + ab_wgs), dim3(64 * RW), lds, s, W,
-                       x, Y, partial, tickets, m, n, S, accumulate, ldy, nrm);
+    const int ngrp = (Tg + T - 1) / T;
+    const int nb = groups * S + ab_wgs;  // workgroups per token group
+    const int grid = ngrp == 1 ? nb : (nb + 7) / 8 * 8 * ngrp;
+    hipLaunchKernelGGL((kq_gemm_kernel<QT, T, kKqDepth, RW, NRM>), dim3(grid), dim3(64 * RW), lds, s, W, x, Y, partial,
+                       tickets, m, n, S, accumulate, ldy, nrm, Tg, nb);
 }
 
 template <int QT, int T>
 void launch_kq_t(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int S,
-                 int accumulate, int ldy, hipStream_t s, const KqNorm& nrm) {
+                 int accumulate, int ldy, hipStream_t s, const KqNorm& nrm, int Tg) {
     // the folded-norm variants use the default work split only
     if (nrm.ss_in) {
         RL_REQUIRE(kq_rw() == 4, RL_ERR_UNSUPPORTED, "kquant: folded RMSNorm needs four row tiles per workgroup");
-        launch_kq_rw<QT, T, 4, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+        launch_kq_rw<QT, T, 4, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg);
         return;
     }
     if (nrm.ss_out) {
         RL_REQUIRE(kq_rw() == 4, RL_ERR_UNSUPPORTED, "kquant: folded RMSNorm needs four row tiles per workgroup");
         if (nrm.bss)
-            launch_kq_rw<QT, T, 4, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+            launch_kq_rw<QT, T, 4, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg);
         else
-            launch_kq_rw<QT, T, 4, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm);
+            launch_kq_rw<QT, T, 4, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg);
         return;
     }
     switch (kq_rw()) {
-    case 1: launch_kq_rw<QT, T, 1, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
-    case 2: launch_kq_rw<QT, T, 2, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
-    default: launch_kq_rw<QT, T, 4, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    case 1: launch_kq_rw<QT, T, 1, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
+    case 2: launch_kq_rw<QT, T, 2, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
+    default: launch_kq_rw<QT, T, 4, 0>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
     }
 }
 
 template <int QT>
 void launch_kq(const uint8_t* W, const float* x, float* Y, float* partial, unsigned* tickets, int m, int n, int T, int S,
                int accumulate, int ldy, hipStream_t s, const KqNorm& nrm) {
+    const int Tg = T;
     switch (T) {
-    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
-    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
-    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
-    default: launch_kq_t<QT, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm); break;
+    case 1: launch_kq_t<QT, 1>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
+    case 2: launch_kq_t<QT, 2>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
+    case 3: launch_kq_t<QT, 3>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
+    default: launch_kq_t<QT, 4>(W, x, Y, partial, tickets, m, n, S, accumulate, ldy, s, nrm, Tg); break;
     }
 }
 
@@ -943,7 +965,7 @@ size_t kq_workspace_bytes(int m, int n, int T) {
     kq_split(m, n / 256, S);
     if (S == 1) return 256;
     const int groups = (m + kTR * kq_rw() - 1) / (kTR * kq_rw());
-    return kq_ticket_bytes(groups) + static_cast<size_t>(S) * T * m * 4;
+    return kq_ticket_bytes(groups * kq_token_groups(T)) + static_cast<size_t>(S) * T * m * 4;
 }
 
 // Y[T][m] (=, +=) W . x for Q4_K (qt=4) / Q6_K (qt=6) K-tiled weights.
@@ -967,14 +989,14 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     RL_REQUIRE(!nrm.swiglu || (!nrm.ss_out && !accumulate && m % kTR == 0 && ldy >= m / 2), RL_ERR_RANGE,
                "kquant: the SwiGLU output needs whole gate / up half tiles, no accumulate and no add-norm output");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
-    RL_REQUIRE(T >= 1 && T <= 4, RL_ERR_RANGE, "kquant: T must be in 1..4");
+    RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "kquant: T must be in 1..8 (groups of 4 above 4)");
     RL_REQUIRE(W && x && Y && ws, RL_ERR_RANGE, "kquant: null pointer");
     RL_REQUIRE(ws_bytes >= kq_workspace_bytes(m, n, T), RL_ERR_RANGE, "kquant: workspace too small");
     int S;
     kq_split(m, n / 256, S);
     const int groups = (m + kTR * kq_rw() - 1) / (kTR * kq_rw());
     unsigned* tickets = static_cast<unsigned*>(ws);
-    float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kq_ticket_bytes(groups));
+    float* partial = reinterpret_cast<float*>(static_cast<uint8_t*>(ws) + kq_ticket_bytes(groups * kq_token_groups(T)));
     if (qt == 4)
         launch_kq<4>(W, x, Y, partial, tickets, m, n, T, S, accumulate, ldy, s, nrm);
     else

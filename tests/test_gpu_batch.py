@@ -189,7 +189,8 @@ def test_batch_decode_vs_oracle(gpu, orc, B):
     eng.close()
 
 
-KQ_CASES = [([0, 0, 0, 1], M.Q_Q4_K, 2), ([0, 1], M.Q_Q6_K, 4), ([1, 1], M.Q_Q4_K, 3), ([0, 0], M.Q_Q4_K, 4)]
+KQ_CASES = [([0, 0, 0, 1], M.Q_Q4_K, 2), ([0, 1], M.Q_Q6_K, 4), ([1, 1], M.Q_Q4_K, 3), ([0, 0], M.Q_Q4_K, 4),
+            ([0, 0, 0, 1], M.Q_Q4_K, 8), ([0, 1], M.Q_Q6_K, 6)]
 
 
 @pytest.mark.parametrize("kinds,quant,B", KQ_CASES)
@@ -201,7 +202,7 @@ def test_kquant_batch_decode_vs_oracle(gpu, orc, kinds, quant, B):
     slices in a fixed order, whatever the row count)."""
     spec = mini_spec(n_layers=len(kinds), layer_kinds=kinds)
     W = M.random_weights(spec, seed=70 + B, linear_quant=quant, w_scale=(1e-3, 1e-2))
-    eng = Engine(spec, W, ctx=512, max_batch=4)
+    eng = Engine(spec, W, ctx=512, max_batch=max(4, B))
     ref = Engine(spec, W, ctx=512)
     rng = np.random.default_rng(80 + B)
     prompts = [[int(t) for t in rng.integers(0, spec.vocab, 2 + 3 * b)] for b in range(B)]
@@ -233,10 +234,11 @@ def test_kquant_batch_decode_vs_oracle(gpu, orc, kinds, quant, B):
     ref.close()
 
 
-@pytest.mark.parametrize("kinds,quant,B", [([1, 1], M.Q_Q4_K, 6), ([0, 1], M.Q_Q6_K, 5), ([0, 0, 0, 1], None, 12),
+@pytest.mark.parametrize("kinds,quant,B", [([1, 1], M.Q_Q4_K, 6), ([0, 1], M.Q_Q6_K, 5), ([1, 1], M.Q_Q4_K, 11),
+                                           ([0, 0, 0, 1], M.Q_Q4_K, 16), ([0, 0, 0, 1], None, 12),
                                            ([0, 0, 0, 1], None, 16), ([0, 1], None, 9)])
 def test_batch_slot_groups(gpu, kinds, quant, B):
-    """More slots than one batch step's rows (the K-quant GEMV takes 4): decode_tokens
+    """More slots than one batch step's rows (the K-quant GEMV takes 8): decode_tokens
     runs the slots in groups, one weight pass each; FP8 / BF16 steps take up to 16
     rows in one pass.  Every slot's logits equal single-sequence decoding of its
     sequence bit for bit (the reference allows up to min(ctx, 128) slots,

@@ -41,10 +41,10 @@ def test_dequant_bitexact(gpu, orc, kind):
 
 @pytest.mark.parametrize("kind", ["q4k", "q6k"])
 @pytest.mark.parametrize("m,n", [(64, 256), (100, 1024), (1000, 2048), (5120, 17408)])
-@pytest.mark.parametrize("T", [1, 2, 4])
+@pytest.mark.parametrize("T", [1, 2, 4, 8])
 def test_gemm_kquant_vs_oracle(gpu, orc, kind, m, n, T):
     if (m, n) == (5120, 17408) and T == 2:
-        pytest.skip("full shape covered at T=1 and T=4")
+        pytest.skip("full shape covered at T=1, 4 and 8")
     r = synth.rng(41 + m + T)
     blocks = _blocks(kind, r, m, n)
     X = r.standard_normal((T, n)).astype(np.float32)
@@ -56,20 +56,25 @@ def test_gemm_kquant_vs_oracle(gpu, orc, kind, m, n, T):
         assert rel_l2(Y[t], want) <= 1e-3, (kind, m, n, T, t, rel_l2(Y[t], want))
 
 
-def test_gemm_kquant_tokens_independent_of_T(gpu):
+@pytest.mark.parametrize("kind", ["q4k", "q6k"])
+def test_gemm_kquant_tokens_independent_of_T(gpu, kind):
+    """Every row of a T = 4, 6 or 8 launch equals the T = 1 launch of that row bit
+    for bit (one weight pass over two token groups of four changes no sum order)."""
     r = synth.rng(5)
     m, n = 512, 4096
-    blocks = synth.q4k_blocks(r, m, n)
-    X = r.standard_normal((4, n)).astype(np.float32)
-    lin = ops.KQuantLinear(ops.Q4_K, blocks, m, n)
-    Y4 = ops.kquant_linear_T(lin, X)
-    for t in range(4):
-        Y1 = ops.kquant_linear_T(lin, X[t:t + 1])[0]
-        assert np.array_equal(Y1.view(np.uint32), Y4[t].view(np.uint32))
+    blocks = _blocks(kind, r, m, n)
+    X = r.standard_normal((8, n)).astype(np.float32)
+    lin = ops.KQuantLinear(ops.Q4_K if kind == "q4k" else ops.Q6_K, blocks, m, n)
+    Y1 = [ops.kquant_linear_T(lin, X[t:t + 1])[0] for t in range(8)]
+    for T in (4, 6, 8):
+        YT = ops.kquant_linear_T(lin, X[:T])
+        for t in range(T):
+            assert np.array_equal(Y1[t].view(np.uint32), YT[t].view(np.uint32)), (T, t)
 
 
 @pytest.mark.parametrize("kind", ["q4k", "q6k"])
-@pytest.mark.parametrize("m,n,T", [(17, 256, 3), (200, 4096, 3), (300, 3072, 1)])
+@pytest.mark.parametrize("m,n,T", [(17, 256, 3), (200, 4096, 3), (300, 3072, 1), (17, 256, 5), (200, 4096, 7),
+                                   (300, 3072, 6)])
 def test_gemm_kquant_ragged_and_odd_T(gpu, orc, kind, m, n, T):
     """Row counts that leave a partial 16-row tile and a partial 4-tile workgroup,
     one super-block per row, three tokens (the second token set half empty)."""
@@ -186,7 +191,8 @@ def test_synthetic_q4_k_engine_spec_invariant(gpu, monkeypatch):
 
 
 @pytest.mark.parametrize("kind", ["q4k", "q6k"])
-@pytest.mark.parametrize("I,n,T", [(8, 256, 1), (200, 1024, 3), (1024, 2048, 4), (17408, 5120, 1), (17408, 5120, 4)])
+@pytest.mark.parametrize("I,n,T", [(8, 256, 1), (200, 1024, 3), (1024, 2048, 4), (200, 1024, 7), (17408, 5120, 1),
+                                   (17408, 5120, 4), (17408, 5120, 8)])
 def test_gemm_kquant_swiglu(gpu, orc, kind, I, n, T):
     """Gate / up half tiles with the SwiGLU write: against the oracle's two GEMVs
     and swiglu (<= 1e-3 relative L2), and against the same rows as one plain
