@@ -36,22 +36,24 @@ PF_TOKENS = 4096
 def measure_gguf_step(spec, K, W):
     """The same C5 step with the layer linears and MTP fc as Q4_K super-blocks and a
     Q6_K lm_head (the tensor mix of a Q4_K_M GGUF; in_proj a/b BF16), random blocks
-    generated on the device: T=1 and T=4 step times, the batch-4 and batch-8 steps
+    generated on the device: T=1 and T=4 step times, the batch-4, -8 and -16 steps
     (sequences at 32K context, one weight pass each) and the weight bytes a T=1 step
     reads."""
     from rapidllm_amd.engine import Engine
 
     os.environ["RL_SYNTH_LINEAR"] = "q4_k"
     try:
-        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321, max_batch=8)
+        eng = Engine(spec, None, ctx=CTX + 4096, max_T=4, seed=4321, max_batch=16)
     finally:
         del os.environ["RL_SYNTH_LINEAR"]
     eng.synthetic_context(CTX)
-    eng.replicate_slot0(8)
+    eng.replicate_slot0(16)
     eng.time_batch(4, W)
     tb4 = eng.time_batch(4, K) / K
     eng.time_batch(8, W)
     tb8 = eng.time_batch(8, K) / K
+    eng.time_batch(16, W)
+    tb16 = eng.time_batch(16, K) / K
     eng.synthetic_context(CTX)
     eng.time_steps(1, W)
     t1 = eng.time_steps(1, K) / K
@@ -85,6 +87,7 @@ def measure_gguf_step(spec, K, W):
             "t1_GBps": round(total / t1 / 1e6, 1), "t1_frac": round(total / t1 / 1e6 / PEAK_GBS, 4),
             "batch4_step_ms": round(tb4, 4), "batch4_tok_s": round(4000.0 / tb4, 3),
             "batch8_step_ms": round(tb8, 4), "batch8_tok_s": round(8000.0 / tb8, 3),
+            "batch16_step_ms": round(tb16, 4), "batch16_tok_s": round(16000.0 / tb16, 3),
             "prefill_tokens": PF_TOKENS, "prefill_ms": round(pf_s * 1e3, 1),
             "prefill_tok_s": round(PF_TOKENS / pf_s, 1),
             "prefill_speedup_vs_verify_chunks": round((PF_TOKENS / pf_s) / (4000.0 / t4), 2)}

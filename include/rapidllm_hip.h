@@ -162,7 +162,7 @@ int rl_hip_gemm_fp8(const uint8_t* w_tiled, const float* tile_scale, const float
  * and Device::launch("gemv_q4k" / "gemv_q6k", GemvKQuantParams) (params.h:7).
  * `type` is RL_Q_Q4_K or RL_Q_Q6_K.  Blocks are the GGUF bytes (144 B / 210 B per
  * 256 weights, rows contiguous); rl_hip_pack_kquant moves them (bytes only) into
- * the device layout.  X is fp32 [T][n], T in 1..8 (one weight pass for all T rows;
+ * the device layout.  X is fp32 [T][n], T in 1..16 (one weight pass for all T rows;
  * the noalloc variant below takes 1..4), n a multiple of 256.
  * rl_hip_dequant_kquant decodes row-major blocks bit-exactly like the reference.
  * workspace (rl_hip_kquant_workspace_bytes): split-K tickets then partial sums.
@@ -383,9 +383,7 @@ void* rl_hip_engine_stream(RlEngine* e);
  * at position poss[b] for slots 0 .. B-1 in one weight pass (B = 1: set_pos +
  * decode_token, as the reference); copy_logits_n / copy_greedy_n return its B rows.
  * prefill_slot runs the prefill on slot `slot` (copy_logits then has its last row).
- * max_batch <= 16.  FP8 / BF16 linears take all 16 rows in one weight pass; the
- * K-quant GEMV takes 8, so a K-quant step over more slots runs them in groups, one
- * weight pass each.  Needs the folded path: FP8 / BF16 linears (v_dim 128), or K-quant
+ * max_batch <= 16.  Every weight format takes all 16 rows in one weight pass.  Needs the folded path: FP8 / BF16 linears (v_dim 128), or K-quant
  * (Q4_K / Q6_K) linears with max_T <= 4; otherwise RL_ERR_UNSUPPORTED. */
 RlEngine* rl_hip_engine_create_batch(const RlModelConfig* cfg, const RlTensor* tensors, int n_tensors, int ctx,
                                      int max_T, int max_batch, int* status);

@@ -766,7 +766,7 @@ class Engine {
    private:
     static constexpr int kMaxSlots = 16;   // batch slots
     static constexpr int kGroupRows = 16;  // rows of one batch step (FP8 / BF16 linears)
-    static constexpr int kKqGroupRows = 8; // rows of one batch step (K-quant GEMV)
+    static constexpr int kKqGroupRows = 16; // rows of one batch step (K-quant GEMV)
     // device scalar block
     enum { kPos = 0, kSlot = 1, kNCons = 2, kNextTok = 3, kGenCount = 4, kScalars = 8 };
     // host readback block (ints): scalars, then preds, then toks
@@ -1113,7 +1113,7 @@ class Engine {
         // one committed S per layer plus R banks of per-token records with the fused
         // kernel, a ring of R states with the unfused one
         // batch decode runs the folded-norm steps with B rows: FP8/BF16 linears
-        // (step_batch) or K-quant linears (step_kq_folded, at most 8 rows), and with
+        // (step_batch) or K-quant linears (step_kq_folded, at most 16 rows), and with
         // DeltaNet layers the fused DeltaNet kernel over the slots' states
         RL_REQUIRE(mb_ == 1 || (fold_norm_ && (gdn_fused_norm_ || nd == 0)) ||
                        (kq_fold_ && tmax_ <= kKqGroupRows && (gdn_fused_ || nd == 0)),

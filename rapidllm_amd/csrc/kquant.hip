@@ -1,4 +1,4 @@
-// kquant.hip -- GGUF Q4_K / Q6_K dequantisation and dequant-dot GEMV (T = 1..8).
+// kquant.hip -- GGUF Q4_K / Q6_K dequantisation and dequant-dot GEMV (T = 1..16).
 //
 // Dequant follows the reference CPU exactly (bit-exact, no FMA contraction):
 //   Q4_K (ops.cpp:245-284): w = (d * sc_j) * q - (dmin * m_j), each product rounded
@@ -136,7 +136,7 @@ __device__ inline i32x4 pack_i8x16(const int (&v)[16]) {
 // group's last ticket resets it, so every launch finds them zero.  Launches that
 // share one workspace must not overlap in time.
 inline size_t kq_ticket_bytes(int groups) { return (static_cast<size_t>(groups) * 64 + 255) / 256 * 256; }
-// Token groups of a launch: T <= 4 tokens in one, T = 5..8 in two groups of four
+// Token groups of a launch: T <= 4 tokens in one, T = 5..16 in groups of four
 // (each with its own tickets).
 inline int kq_token_groups(int T) { return (T + 3) / 4; }
 
@@ -989,7 +989,7 @@ void kq_gemm(int qt, const uint8_t* W, const float* x, float* Y, void* ws, size_
     RL_REQUIRE(!nrm.swiglu || (!nrm.ss_out && !accumulate && m % kTR == 0 && ldy >= m / 2), RL_ERR_RANGE,
                "kquant: the SwiGLU output needs whole gate / up half tiles, no accumulate and no add-norm output");
     RL_REQUIRE(m > 0 && n > 0 && n % 256 == 0, RL_ERR_RANGE, "kquant: n must be a positive multiple of 256");
-    RL_REQUIRE(T >= 1 && T <= 8, RL_ERR_RANGE, "kquant: T must be in 1..8 (groups of 4 above 4)");
+    RL_REQUIRE(T >= 1 && T <= 16, RL_ERR_RANGE, "kquant: T must be in 1..16 (groups of 4 above 4)");
     RL_REQUIRE(W && x && Y && ws, RL_ERR_RANGE, "kquant: null pointer");
     RL_REQUIRE(ws_bytes >= kq_workspace_bytes(m, n, T), RL_ERR_RANGE, "kquant: workspace too small");
     int S;

@@ -41,10 +41,10 @@ def test_dequant_bitexact(gpu, orc, kind):
 
 @pytest.mark.parametrize("kind", ["q4k", "q6k"])
 @pytest.mark.parametrize("m,n", [(64, 256), (100, 1024), (1000, 2048), (5120, 17408)])
-@pytest.mark.parametrize("T", [1, 2, 4, 8])
+@pytest.mark.parametrize("T", [1, 2, 4, 8, 16])
 def test_gemm_kquant_vs_oracle(gpu, orc, kind, m, n, T):
     if (m, n) == (5120, 17408) and T == 2:
-        pytest.skip("full shape covered at T=1, 4 and 8")
+        pytest.skip("full shape covered at T=1, 4, 8 and 16")
     r = synth.rng(41 + m + T)
     blocks = _blocks(kind, r, m, n)
     X = r.standard_normal((T, n)).astype(np.float32)
@@ -58,15 +58,15 @@ def test_gemm_kquant_vs_oracle(gpu, orc, kind, m, n, T):
 
 @pytest.mark.parametrize("kind", ["q4k", "q6k"])
 def test_gemm_kquant_tokens_independent_of_T(gpu, kind):
-    """Every row of a T = 4, 6 or 8 launch equals the T = 1 launch of that row bit
-    for bit (one weight pass over two token groups of four changes no sum order)."""
+    """Every row of a T = 4, 6, 8, 13 or 16 launch equals the T = 1 launch of that row
+    bit for bit (one weight pass over token groups of four changes no sum order)."""
     r = synth.rng(5)
     m, n = 512, 4096
     blocks = _blocks(kind, r, m, n)
-    X = r.standard_normal((8, n)).astype(np.float32)
+    X = r.standard_normal((16, n)).astype(np.float32)
     lin = ops.KQuantLinear(ops.Q4_K if kind == "q4k" else ops.Q6_K, blocks, m, n)
-    Y1 = [ops.kquant_linear_T(lin, X[t:t + 1])[0] for t in range(8)]
-    for T in (4, 6, 8):
+    Y1 = [ops.kquant_linear_T(lin, X[t:t + 1])[0] for t in range(16)]
+    for T in (4, 6, 8, 13, 16):
         YT = ops.kquant_linear_T(lin, X[:T])
         for t in range(T):
             assert np.array_equal(Y1[t].view(np.uint32), YT[t].view(np.uint32)), (T, t)
