@@ -329,12 +329,14 @@ __global__ __launch_bounds__(256) void attn_part_kernel(AttnArgs p) {
     }
 }
 
-// grid (G*T pairs, nkv, slots * hd/64), 256 threads = 4 chunk groups x 64 dims.
+// grid (G*T pairs, nkv, slots * hd/64), 1024 threads = 16 chunk groups x 64 dims
+// (at 32K context each thread's chunk loop is 8 loads, issued together).
 // Chunk weights w_c = exp(m_c - M) are computed once into LDS; each thread sums
-// its chunk group's O_c[d] * w_c, the 4 groups are added in a fixed order.
+// its chunk group's O_c[d] * w_c, the 16 groups are added in a fixed order.
 constexpr int kMaxChunksLds = 4096;  // 1M positions
 
-__global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
+constexpr int kCombG = 16;  // chunk groups (waves) per workgroup
+__global__ __launch_bounds__(64 * kCombG) void attn_comb_kernel(AttnArgs p) {
     const int k = blockIdx.x, kv = blockIdx.y;
     const int dz = blockIdx.z % (kHD / 64);
     to_slot(p, blockIdx.z / (kHD / 64));
@@ -346,18 +348,20 @@ __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
     const int nch = (L + kChunk - 1) / kChunk;
     const size_t base = static_cast<size_t>(kv) * p.max_chunks;
     __shared__ float w_s[kMaxChunksLds];
-    __shared__ float red[4][64];
-    __shared__ float sh[8];
+    __shared__ float red[kCombG][64];
+    __shared__ float sh[2 * kCombG];
     // chunk max
     float mx = -INFINITY;
-    for (int c = tid; c < nch; c += 256) mx = fmaxf(mx, p.part_m[(base + c) * kMaxPairs + k]);
+    for (int c = tid; c < nch; c += 64 * kCombG) mx = fmaxf(mx, p.part_m[(base + c) * kMaxPairs + k]);
     mx = wave_max(mx);
     if ((tid & 63) == 0) sh[tid >> 6] = mx;
     __syncthreads();
-    const float M = fmaxf(fmaxf(sh[0], sh[1]), fmaxf(sh[2], sh[3]));
+    float M = sh[0];
+#pragma unroll
+    for (int w = 1; w < kCombG; ++w) M = fmaxf(M, sh[w]);
     // weights and the softmax denominator
     float ls = 0.f;
-    for (int c = tid; c < nch; c += 256) {
+    for (int c = tid; c < nch; c += 64 * kCombG) {
         const float m = p.part_m[(base + c) * kMaxPairs + k];
         const float w = m == -INFINITY ? 0.f : expf(m - M);
         w_s[c] = w;
@@ -365,19 +369,24 @@ __global__ __launch_bounds__(256) void attn_comb_kernel(AttnArgs p) {
     }
     ls = wave_sum(ls);
     __syncthreads();
-    if ((tid & 63) == 0) sh[4 + (tid >> 6)] = ls;
+    if ((tid & 63) == 0) sh[kCombG + (tid >> 6)] = ls;
     __syncthreads();
-    const float Ls = (sh[4] + sh[5]) + (sh[6] + sh[7]);
+    float Ls = 0.f;
+#pragma unroll
+    for (int w = 0; w < kCombG; ++w) Ls += sh[kCombG + w];  // fixed order
     // weighted sum of the chunk outputs for dim d over chunks c = q (mod 4)
     float acc = 0.f;
     const float* po = p.part_o + (base * kMaxPairs + k) * kHD + d;
     const size_t cstride = static_cast<size_t>(kMaxPairs) * kHD;
 #pragma unroll 8
-    for (int c = q; c < nch; c += 4) acc += po[c * cstride] * w_s[c];
+    for (int c = q; c < nch; c += kCombG) acc += po[c * cstride] * w_s[c];
     red[q][dl] = acc;
     __syncthreads();
     if (q != 0) return;
-    const float o = ((red[0][dl] + red[1][dl]) + (red[2][dl] + red[3][dl])) / Ls;
+    float os = 0.f;
+#pragma unroll
+    for (int w = 0; w < kCombG; ++w) os += red[w][dl];  // fixed order
+    const float o = os / Ls;
     const float gate = p.Y[static_cast<size_t>(t) * p.ld_y + static_cast<size_t>(h) * 2 * kHD + kHD + d];
     const float val = o * sigmoid_f(gate);
     const int n = p.nq * kHD;
@@ -704,7 +713,7 @@ void attn_decode_layer(const float* Y, int ld_y, const float* q_norm, const floa
     else
         hipLaunchKernelGGL(attn_part_kernel<2>, dim3(chunks * nkv * nb), dim3(256), 0, s, p);
     check_launch("attn_part_kernel");
-    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv, (kHD / 64) * nb), dim3(256), 0, s, p);
+    hipLaunchKernelGGL(attn_comb_kernel, dim3(G * T, nkv, (kHD / 64) * nb), dim3(64 * kCombG), 0, s, p);
     check_launch("attn_comb_kernel");
 }
 
