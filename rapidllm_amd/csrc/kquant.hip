@@ -254,7 +254,7 @@ __global__ __launch_bounds__(64 * RW) void kq_gemm_kernel(const uint8_t* __restr
     // (workgroups go to the XCDs round-robin) and read the same weight tiles at about
     // the same time: the second read hits that XCD's L2.  Each group runs the
     // T-token kernel on its own rows: every token's sums are those of a launch with
-    // that token alone.  nb workgroups per group (kq_grid_x); the padding exits.
+    // that token alone.  nb workgroups per group (launch_kq_rw); the padding exits.
     const int ngrp = (Tg + T - 1) / T;
     const int tgi = (blockIdx.x / 8) % ngrp, bix = (blockIdx.x / (8 * ngrp)) * 8 + blockIdx.x % 8;
     const int t0 = tgi * T, tn = min(T, Tg - t0);  // this workgroup's tokens t0 .. t0 + tn - 1
